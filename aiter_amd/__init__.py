@@ -1,0 +1,33 @@
+"""aiter_amd: MI355X (gfx950) blockscale fused-MoE, a drop-in for
+aiter.fused_moe's FP8 block-scale path.
+
+    from aiter_amd import fused_moe, QuantType, ActivationType
+    out = fused_moe(x, w1, w2, topk_weight, topk_ids,
+                    quant_type=QuantType.per_128x128, w1_scale=s1, w2_scale=s2)
+
+The compute runs in libaiter_amd.so (HIP kernels behind a C ABI, see
+include/aiter_amd.h); build it with ``python -m aiter_amd.build``.
+"""
+from .enums import ActivationType, QuantType, dtypes, quant_remap
+from .fused_moe import (
+    BLOCK_SIZE_M,
+    default_block_m,
+    fused_moe,
+    fused_moe_,
+    fused_moe_fake,
+    get_inter_dim,
+    moe_sorting,
+    moe_stage1_fp8_blockscale,
+    moe_stage2_fp8_blockscale,
+    sorted_capacity,
+)
+from .quant import dynamic_per_token_scaled_quant, per_group_quant_hip, quant_weight_per_128x128
+from .shuffle import shuffle_weight, unshuffle_weight
+
+__all__ = [
+    "ActivationType", "QuantType", "dtypes", "quant_remap", "BLOCK_SIZE_M", "default_block_m",
+    "fused_moe", "fused_moe_", "fused_moe_fake", "get_inter_dim", "moe_sorting",
+    "moe_stage1_fp8_blockscale", "moe_stage2_fp8_blockscale", "sorted_capacity",
+    "dynamic_per_token_scaled_quant", "per_group_quant_hip", "quant_weight_per_128x128",
+    "shuffle_weight", "unshuffle_weight",
+]

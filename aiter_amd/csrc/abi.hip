@@ -1,0 +1,338 @@
+// extern "C" boundary of libaiter_amd.so: argument validation, the
+// thread-local error bridge, workspace layout of the fused entry point, and
+// dispatch to the kernel launchers.  Declarations and the reference
+// interface each entry point replaces are in include/aiter_amd.h.
+#include "../../include/aiter_amd.h"
+
+#include <algorithm>
+#include <string>
+
+#include "common.h"
+
+namespace aiter_amd {
+
+static thread_local std::string g_last_error;
+
+void set_last_error(const std::string& msg) { g_last_error = msg; }
+
+// launchers (moe_sort.hip, quant.hip, moe_gemm_fp8bs.hip)
+int64_t sort_workspace_bytes(int64_t rows, int64_t topk, int64_t E);
+void launch_moe_sort(const int32_t*, const float*, const int32_t*, const int32_t*, int32_t*,
+                     float*, int32_t*, int32_t*, void*, int64_t, int64_t, int64_t, int64_t,
+                     int64_t, void*, int64_t, hipStream_t);
+void launch_per_group_quant_fp8(const void*, int, void*, float*, int64_t, int64_t, int,
+                                const int32_t*, int64_t, hipStream_t);
+void launch_acc_to_out(const float*, void*, int, const int32_t*, int64_t, int64_t, hipStream_t);
+void launch_moe_stage1_fp8bs(const uint8_t*, const float*, int64_t, int64_t, const uint8_t*,
+                             const float*, const int32_t*, const int32_t*, const int32_t*,
+                             uint8_t*, float*, int64_t, int64_t, int64_t, int64_t, int64_t,
+                             int64_t, int64_t, int, hipStream_t);
+void launch_moe_stage2_fp8bs(const uint8_t*, const float*, const uint8_t*, const float*,
+                             const int32_t*, const float*, const int32_t*, const int32_t*,
+                             float*, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t,
+                             int64_t, int, hipStream_t);
+
+namespace {
+
+constexpr int64_t kMaxTokens = (1ll << 24) - 1;  // token id field of sorted_ids
+constexpr int64_t kMaxTopk = 32;                 // slot bitmask width in sorting
+constexpr int64_t kMaxExperts = 4096;
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+void check_ptr(const void* p, const char* name) {
+    AMD_CHECK(p != nullptr, std::string(name) + " is NULL");
+    AMD_CHECK(aligned16(p), std::string(name) + " is not 16-byte aligned");
+}
+
+int64_t sorted_capacity_for(int64_t tokens, int64_t topk, int64_t E, int64_t bm) {
+    return tokens * topk + E * bm - topk;
+}
+
+void check_block_m_gemm(int64_t bm) {
+    AMD_CHECK(bm == 16 || bm == 32 || bm == 64,
+              "block_m must be 16, 32 or 64 for the fp8 blockscale GEMMs, got " +
+                  std::to_string(bm));
+}
+
+void check_dims(int64_t model_dim, int64_t inter_dim) {
+    AMD_CHECK(model_dim > 0 && model_dim % 128 == 0,
+              "model_dim must be a positive multiple of 128, got " + std::to_string(model_dim));
+    AMD_CHECK(inter_dim > 0 && inter_dim % 128 == 0,
+              "inter_dim must be a positive multiple of 128, got " + std::to_string(inter_dim));
+}
+
+void check_topk_experts(int64_t tokens, int64_t topk, int64_t E) {
+    AMD_CHECK(tokens >= 0 && tokens <= kMaxTokens,
+              "tokens must be in [0, 2^24), got " + std::to_string(tokens));
+    AMD_CHECK(topk >= 1 && topk <= kMaxTopk,
+              "topk must be in [1, 32], got " + std::to_string(topk));
+    AMD_CHECK(E >= 1 && E <= kMaxExperts,
+              "num_experts must be in [1, 4096], got " + std::to_string(E));
+    // the padded-length bound tokens*topk + E*block - topk assumes topk <= E
+    AMD_CHECK(topk <= E, "topk must not exceed num_experts");
+}
+
+struct FusedLayout {
+    int64_t cap, blocks;
+    int64_t off_sorted_ids, off_sorted_w, off_sorted_eids, off_num_valid, off_sort_ws;
+    int64_t off_a1, off_a1_scale, off_a2, off_a2_scale, off_acc, total;
+    int64_t sort_ws_bytes;
+};
+
+int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
+
+FusedLayout fused_layout(int64_t T, int64_t H, int64_t I, int64_t E_sort, int64_t k,
+                         int64_t bm) {
+    FusedLayout L;
+    L.cap = sorted_capacity_for(T, k, E_sort, bm);
+    L.blocks = ceil_div(L.cap, bm);
+    L.sort_ws_bytes = sort_workspace_bytes(T, k, E_sort);
+    int64_t o = 0;
+    L.off_sorted_ids = o;  o = align256(o + L.cap * 4);
+    L.off_sorted_w = o;    o = align256(o + L.cap * 4);
+    L.off_sorted_eids = o; o = align256(o + L.blocks * 4);
+    L.off_num_valid = o;   o = align256(o + 8);
+    L.off_sort_ws = o;     o = align256(o + L.sort_ws_bytes);
+    L.off_a1 = o;          o = align256(o + T * H);
+    L.off_a1_scale = o;    o = align256(o + T * (H / 128) * 4);
+    L.off_a2 = o;          o = align256(o + T * k * I);
+    L.off_a2_scale = o;    o = align256(o + T * k * (I / 128) * 4);
+    L.off_acc = o;         o = align256(o + T * H * 4);
+    L.total = o;
+    return L;
+}
+
+int64_t default_block_m(int64_t tokens, int64_t topk, int64_t E) {
+    const int64_t avg = E > 0 ? tokens * topk / E : 0;
+    if (avg <= 8) return 16;
+    if (avg <= 48) return 32;
+    return 64;
+}
+
+}  // namespace
+}  // namespace aiter_amd
+
+using namespace aiter_amd;
+
+extern "C" {
+
+int aiter_amd_abi_version(void) { return AITER_AMD_ABI_VERSION; }
+
+const char* aiter_amd_get_last_error(void) { return g_last_error.c_str(); }
+
+void aiter_amd_clear_last_error(void) { g_last_error.clear(); }
+
+int64_t aiter_amd_moe_sorting_workspace_bytes(int64_t tokens, int64_t topk, int64_t num_experts) {
+    if (tokens < 0 || topk < 1 || num_experts < 1) return 0;
+    return sort_workspace_bytes(tokens, topk, num_experts);
+}
+
+int64_t aiter_amd_default_block_m(int64_t tokens, int64_t topk, int64_t num_experts) {
+    return default_block_m(tokens, topk, num_experts);
+}
+
+int aiter_amd_moe_sorting_fwd(const int32_t* topk_ids, const float* topk_weights, int64_t tokens,
+                              int64_t topk, int32_t* sorted_ids, float* sorted_weights,
+                              int32_t* sorted_expert_ids, int32_t* num_valid_ids,
+                              int64_t sorted_capacity, int64_t blocks_capacity, void* moe_buf,
+                              int64_t moe_buf_row_bytes, int64_t num_experts, int64_t block_size,
+                              const int32_t* expert_mask, const int32_t* num_local_tokens,
+                              int64_t dispatch_policy, void* workspace, int64_t workspace_bytes,
+                              void* stream) {
+    (void)dispatch_policy;
+    return safe_call([&] {
+        check_topk_experts(tokens, topk, num_experts);
+        AMD_CHECK(block_size >= 1 && block_size <= 256,
+                  "block_size must be in [1, 256], got " + std::to_string(block_size));
+        AMD_CHECK(topk_ids && topk_weights && sorted_ids && sorted_weights && sorted_expert_ids &&
+                      num_valid_ids,
+                  "a required pointer is NULL");
+        const int64_t cap = sorted_capacity_for(tokens, topk, num_experts, block_size);
+        AMD_CHECK(sorted_capacity >= cap, "sorted_ids capacity " +
+                                              std::to_string(sorted_capacity) + " < required " +
+                                              std::to_string(cap));
+        AMD_CHECK(blocks_capacity >= ceil_div(cap, block_size),
+                  "sorted_expert_ids capacity too small");
+        if (moe_buf) {
+            AMD_CHECK(aligned16(moe_buf), "moe_buf is not 16-byte aligned");
+            AMD_CHECK(moe_buf_row_bytes > 0 && moe_buf_row_bytes % 16 == 0,
+                      "moe_buf row bytes must be a positive multiple of 16");
+        }
+        const int64_t need = sort_workspace_bytes(tokens, topk, num_experts);
+        AMD_CHECK(need == 0 || (workspace && workspace_bytes >= need),
+                  "sorting workspace of " + std::to_string(need) + " bytes required");
+        launch_moe_sort(topk_ids, topk_weights, expert_mask, num_local_tokens, sorted_ids,
+                        sorted_weights, sorted_expert_ids, num_valid_ids, moe_buf,
+                        moe_buf_row_bytes, tokens, topk, num_experts, block_size, workspace,
+                        workspace_bytes, (hipStream_t)stream);
+    });
+}
+
+int aiter_amd_dynamic_per_group_quant_fp8(const void* input, int input_dtype, int64_t rows,
+                                          int64_t cols, int64_t group_size, void* out,
+                                          float* scales, int transpose_scale,
+                                          const int32_t* num_rows, int64_t num_rows_factor,
+                                          void* stream) {
+    return safe_call([&] {
+        AMD_CHECK(group_size == 128, "only group_size 128 is supported, got " +
+                                         std::to_string(group_size));
+        AMD_CHECK(input_dtype == DT_BF16 || input_dtype == DT_FP16,
+                  "input dtype must be bf16 or fp16");
+        AMD_CHECK(rows >= 0 && cols > 0 && cols % 128 == 0,
+                  "cols must be a positive multiple of 128");
+        AMD_CHECK(num_rows_factor >= 1, "num_rows_factor must be >= 1");
+        if (rows == 0) return;
+        check_ptr(input, "input");
+        check_ptr(out, "out");
+        AMD_CHECK(scales != nullptr, "scales is NULL");
+        launch_per_group_quant_fp8(input, input_dtype, out, scales, rows, cols, transpose_scale,
+                                   num_rows, num_rows_factor, (hipStream_t)stream);
+    });
+}
+
+int aiter_amd_moe_stage1_fp8_blockscale(const void* a1, const float* a1_scale,
+                                        int64_t a1_scale_transposed, const void* w1,
+                                        const float* w1_scale, const int32_t* sorted_ids,
+                                        const int32_t* sorted_expert_ids,
+                                        const int32_t* num_valid_ids, void* a2, float* a2_scale,
+                                        int64_t tokens, int64_t model_dim, int64_t inter_dim,
+                                        int64_t num_experts, int64_t topk, int64_t block_m,
+                                        int64_t max_m_blocks, int64_t activation,
+                                        int64_t w_shuffled, void* stream) {
+    return safe_call([&] {
+        check_dims(model_dim, inter_dim);
+        check_topk_experts(tokens, topk, num_experts);
+        check_block_m_gemm(block_m);
+        AMD_CHECK(activation == 0, "only ActivationType.Silu (0) is supported, got " +
+                                       std::to_string(activation));
+        AMD_CHECK(max_m_blocks >= 0, "max_m_blocks must be >= 0");
+        if (tokens == 0 || max_m_blocks == 0) return;
+        check_ptr(a1, "a1");
+        check_ptr(w1, "w1");
+        check_ptr(a2, "a2");
+        AMD_CHECK(a1_scale && w1_scale && a2_scale && sorted_ids && sorted_expert_ids &&
+                      num_valid_ids,
+                  "a required pointer is NULL");
+        const int64_t KB = model_dim / 128;
+        const int64_t sa_row = a1_scale_transposed ? 1 : KB;
+        const int64_t sa_kb = a1_scale_transposed ? tokens : 1;
+        launch_moe_stage1_fp8bs((const uint8_t*)a1, a1_scale, sa_row, sa_kb, (const uint8_t*)w1,
+                                w1_scale, sorted_ids, sorted_expert_ids, num_valid_ids,
+                                (uint8_t*)a2, a2_scale, tokens, model_dim, inter_dim, num_experts,
+                                topk, block_m, max_m_blocks, (int)(w_shuffled != 0),
+                                (hipStream_t)stream);
+    });
+}
+
+int aiter_amd_moe_stage2_fp8_blockscale(const void* a2, const float* a2_scale, const void* w2,
+                                        const float* w2_scale, const int32_t* sorted_ids,
+                                        const float* sorted_weights,
+                                        const int32_t* sorted_expert_ids,
+                                        const int32_t* num_valid_ids, float* out_acc,
+                                        int64_t tokens, int64_t model_dim, int64_t inter_dim,
+                                        int64_t num_experts, int64_t topk, int64_t block_m,
+                                        int64_t max_m_blocks, int64_t w_shuffled, void* stream) {
+    return safe_call([&] {
+        check_dims(model_dim, inter_dim);
+        check_topk_experts(tokens, topk, num_experts);
+        check_block_m_gemm(block_m);
+        AMD_CHECK(max_m_blocks >= 0, "max_m_blocks must be >= 0");
+        if (tokens == 0 || max_m_blocks == 0) return;
+        check_ptr(a2, "a2");
+        check_ptr(w2, "w2");
+        check_ptr(out_acc, "out_acc");
+        AMD_CHECK(a2_scale && w2_scale && sorted_ids && sorted_weights && sorted_expert_ids &&
+                      num_valid_ids,
+                  "a required pointer is NULL");
+        launch_moe_stage2_fp8bs((const uint8_t*)a2, a2_scale, (const uint8_t*)w2, w2_scale,
+                                sorted_ids, sorted_weights, sorted_expert_ids, num_valid_ids,
+                                out_acc, tokens * topk, inter_dim, model_dim, num_experts, topk,
+                                block_m, max_m_blocks, (int)(w_shuffled != 0),
+                                (hipStream_t)stream);
+    });
+}
+
+int aiter_amd_moe_acc_to_out(const float* acc, void* out, int out_dtype,
+                             const int32_t* num_valid_ids, int64_t tokens, int64_t model_dim,
+                             void* stream) {
+    return safe_call([&] {
+        AMD_CHECK(out_dtype == DT_BF16 || out_dtype == DT_FP16, "out dtype must be bf16 or fp16");
+        AMD_CHECK(model_dim > 0 && model_dim % 8 == 0, "model_dim must be a multiple of 8");
+        AMD_CHECK(tokens >= 0, "tokens must be >= 0");
+        if (tokens == 0) return;
+        check_ptr(acc, "acc");
+        check_ptr(out, "out");
+        launch_acc_to_out(acc, out, out_dtype, num_valid_ids, tokens, model_dim,
+                          (hipStream_t)stream);
+    });
+}
+
+int64_t aiter_amd_fused_moe_workspace_bytes(int64_t tokens, int64_t model_dim, int64_t inter_dim,
+                                            int64_t num_experts, int64_t topk, int64_t block_m) {
+    if (tokens < 0 || model_dim <= 0 || inter_dim <= 0 || num_experts < 1 || topk < 1)
+        return -1;
+    if (block_m <= 0) block_m = default_block_m(tokens, topk, num_experts);
+    return fused_layout(tokens, model_dim, inter_dim, num_experts, topk, block_m).total;
+}
+
+int aiter_amd_fused_moe_fp8_blockscale(const void* hidden_states, int hidden_dtype,
+                                       const void* w1, const float* w1_scale, const void* w2,
+                                       const float* w2_scale, const float* topk_weights,
+                                       const int32_t* topk_ids, const int32_t* expert_mask,
+                                       const int32_t* num_local_tokens, void* out, int out_dtype,
+                                       int64_t tokens, int64_t model_dim, int64_t inter_dim,
+                                       int64_t num_experts, int64_t global_experts, int64_t topk,
+                                       int64_t block_m, int64_t w_shuffled, void* workspace,
+                                       int64_t workspace_bytes, void* stream) {
+    return safe_call([&] {
+        check_dims(model_dim, inter_dim);
+        check_topk_experts(tokens, topk, num_experts);
+        AMD_CHECK(hidden_dtype == DT_BF16 || hidden_dtype == DT_FP16,
+                  "hidden_states dtype must be bf16 or fp16");
+        AMD_CHECK(out_dtype == DT_BF16 || out_dtype == DT_FP16, "out dtype must be bf16 or fp16");
+        const int64_t E_sort = expert_mask ? global_experts : num_experts;
+        AMD_CHECK(E_sort >= num_experts && E_sort <= kMaxExperts,
+                  "global_experts must be in [num_experts, 4096]");
+        if (block_m <= 0) block_m = default_block_m(tokens, topk, num_experts);
+        check_block_m_gemm(block_m);
+        if (tokens == 0) return;
+        check_ptr(hidden_states, "hidden_states");
+        check_ptr(w1, "w1");
+        check_ptr(w2, "w2");
+        check_ptr(out, "out");
+        AMD_CHECK(w1_scale && w2_scale && topk_weights && topk_ids,
+                  "a required pointer is NULL");
+        const FusedLayout L = fused_layout(tokens, model_dim, inter_dim, E_sort, topk, block_m);
+        check_ptr(workspace, "workspace");
+        AMD_CHECK(workspace_bytes >= L.total, "workspace of " + std::to_string(L.total) +
+                                                  " bytes required, got " +
+                                                  std::to_string(workspace_bytes));
+        uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
+        int32_t* sorted_ids = reinterpret_cast<int32_t*>(ws + L.off_sorted_ids);
+        float* sorted_w = reinterpret_cast<float*>(ws + L.off_sorted_w);
+        int32_t* sorted_eids = reinterpret_cast<int32_t*>(ws + L.off_sorted_eids);
+        int32_t* num_valid = reinterpret_cast<int32_t*>(ws + L.off_num_valid);
+        uint8_t* a1 = ws + L.off_a1;
+        float* a1_scale = reinterpret_cast<float*>(ws + L.off_a1_scale);
+        uint8_t* a2 = ws + L.off_a2;
+        float* a2_scale = reinterpret_cast<float*>(ws + L.off_a2_scale);
+        float* acc = reinterpret_cast<float*>(ws + L.off_acc);
+        hipStream_t s = (hipStream_t)stream;
+        launch_moe_sort(topk_ids, topk_weights, expert_mask, num_local_tokens, sorted_ids,
+                        sorted_w, sorted_eids, num_valid, acc, model_dim * 4, tokens, topk,
+                        E_sort, block_m, ws + L.off_sort_ws, L.sort_ws_bytes, s);
+        launch_per_group_quant_fp8(hidden_states, hidden_dtype, a1, a1_scale, tokens, model_dim,
+                                   0, num_local_tokens, 1, s);
+        const int sh = (int)(w_shuffled != 0);
+        launch_moe_stage1_fp8bs(a1, a1_scale, model_dim / 128, 1, (const uint8_t*)w1, w1_scale,
+                                sorted_ids, sorted_eids, num_valid, a2, a2_scale, tokens,
+                                model_dim, inter_dim, num_experts, topk, block_m, L.blocks, sh, s);
+        launch_moe_stage2_fp8bs(a2, a2_scale, (const uint8_t*)w2, w2_scale, sorted_ids, sorted_w,
+                                sorted_eids, num_valid, acc, tokens * topk, inter_dim, model_dim,
+                                num_experts, topk, block_m, L.blocks, sh, s);
+        launch_acc_to_out(acc, out, out_dtype, num_valid, tokens, model_dim, s);
+    });
+}
+
+}  // extern "C"

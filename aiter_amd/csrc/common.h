@@ -1,0 +1,137 @@
+// Shared helpers for the aiter_amd fused-MoE library (gfx950 / CDNA4 only).
+//
+// Error handling follows the reference's ctypes bridge
+// (csrc/include/aiter_ctypes_error.h:60-147): every extern "C" entry point
+// returns 0 on success and -1 on failure, and the failure text is kept in a
+// thread-local string that aiter_amd_get_last_error() returns.  No C++
+// exception ever crosses the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <stdexcept>
+#include <string>
+
+namespace aiter_amd {
+
+// ---------------------------------------------------------------- errors ---
+void set_last_error(const std::string& msg);
+
+struct AbiError : public std::runtime_error {
+    explicit AbiError(const std::string& m) : std::runtime_error(m) {}
+};
+
+#define AMD_CHECK(cond, msg)                                                   \
+    do {                                                                       \
+        if (!(cond)) {                                                         \
+            throw ::aiter_amd::AbiError(std::string(__func__) + ": " + (msg)); \
+        }                                                                      \
+    } while (0)
+
+#define AMD_HIP_CHECK(expr)                                                    \
+    do {                                                                       \
+        hipError_t _e = (expr);                                                \
+        if (_e != hipSuccess) {                                                \
+            throw ::aiter_amd::AbiError(std::string(#expr) + " failed: " +     \
+                                        hipGetErrorString(_e));                \
+        }                                                                      \
+    } while (0)
+
+// Runs `fn` and converts any exception into the thread-local error + -1.
+template <typename F>
+inline int safe_call(F&& fn) {
+    try {
+        fn();
+        return 0;
+    } catch (const std::exception& e) {
+        set_last_error(e.what());
+        return -1;
+    } catch (...) {
+        set_last_error("unknown C++ exception");
+        return -1;
+    }
+}
+
+// dtype codes: identical to AiterDtype (csrc/include/aiter_enum.h:27-43).
+enum DtypeCode : int {
+    DT_FP8 = 0,
+    DT_FP8_E8M0 = 1,
+    DT_FP16 = 2,
+    DT_BF16 = 3,
+    DT_FP32 = 4,
+    DT_FP4X2 = 6,
+    DT_I32 = 8,
+};
+
+// ------------------------------------------------------- device helpers ---
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// 1/448 rounded to fp32, the e4m3fn maximum's reciprocal.  The reference
+// kernel multiplies amax by this constant (quant_kernels.cu:67-69,98-100).
+constexpr float kInvFp8Max = (float)(1.0 / 448.0);
+constexpr float kFp8Max = 448.0f;
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
+    return __uint_as_float(((uint32_t)b) << 16);
+}
+
+__device__ __forceinline__ float fp16_bits_to_f32(uint16_t b) {
+    return (float)__builtin_bit_cast(_Float16, b);
+}
+
+// fp32 -> bf16, round to nearest even (inputs here are finite).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+    uint32_t u = __float_as_uint(f);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ uint16_t f32_to_fp16_bits(float f) {
+    return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+__device__ __forceinline__ float bf16_round(float f) {
+    return bf16_bits_to_f32(f32_to_bf16_bits(f));
+}
+
+// Two fp32 -> two e4m3fn bytes (low 16 bits of the result), saturated to
+// +-448 first and then converted round-to-nearest-even by the hardware
+// converter.
+__device__ __forceinline__ uint32_t f32x2_to_fp8x2(float a, float b) {
+    a = __builtin_fminf(__builtin_fmaxf(a, -kFp8Max), kFp8Max);
+    b = __builtin_fminf(__builtin_fmaxf(b, -kFp8Max), kFp8Max);
+    return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false) & 0xFFFFu;
+}
+
+__device__ __forceinline__ uint32_t f32x4_to_fp8x4(float a, float b, float c, float d) {
+    return f32x2_to_fp8x2(a, b) | (f32x2_to_fp8x2(c, d) << 16);
+}
+
+// One 16x16x128 fp8 x fp8 MFMA with fresh (zero) accumulator.  Scale
+// operands of zero select the unscaled gfx950 instruction
+// v_mfma_f32_16x16x128_f8f6f4.
+__device__ __forceinline__ v4f mfma16x16x128_fp8(const v8i& a, const v8i& b) {
+    v4f z = {0.f, 0.f, 0.f, 0.f};
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, z, 0, 0, 0, 0, 0, 0);
+}
+
+template <typename T>
+__device__ __forceinline__ T warp_max_16(T v) {
+    // max over the 16 lanes that share lane/16 (xor over lane bits 0..3)
+    v = __builtin_fmaxf(v, __shfl_xor(v, 1, 64));
+    v = __builtin_fmaxf(v, __shfl_xor(v, 2, 64));
+    v = __builtin_fmaxf(v, __shfl_xor(v, 4, 64));
+    v = __builtin_fmaxf(v, __shfl_xor(v, 8, 64));
+    return v;
+}
+
+__device__ __forceinline__ float silu_f32(float x) {
+    return x / (1.0f + __expf(-x));
+}
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace aiter_amd

@@ -1,0 +1,392 @@
+// MoE token sorting: bucket every (token, slot) routing pair into per-expert
+// segments padded to a multiple of the GEMM M-block (block_m).
+//
+// Output contract (bit-exact with the reference's sorting kernels,
+// csrc/include/moe_sorting_opus.h:266-352 for the encoding and the worked
+// example, 724-1059 one-shot, 2612-3130 multi-phase; closed form
+// op_tests/test_moe_sorting.py:15-70):
+//   * experts are laid out in ascending id order; an expert with no pair, or
+//     one switched off by expert_mask, gets no segment;
+//   * a segment holds the expert's pairs ordered by (token, slot) and is
+//     padded to ceil(count/block_m)*block_m entries;
+//   * sorted_ids[i] = (slot << 24) | token, sorted_weights[i] = w[token, slot];
+//     padding entries are (topk << 24) | tokens with weight 0;
+//   * sorted_expert_ids[b] = expert id of M-block b (the local id, i.e. the
+//     exclusive prefix sum of expert_mask, when a mask is given);
+//   * num_valid_ids = {total padded length, tokens};
+//   * entries past num_valid_ids[0] are not written;
+//   * ids outside [0, num_experts) are ignored;
+//   * the optional zero buffer (the fp32 accumulator of the down GEMM) is
+//     cleared for `tokens` rows, as the reference clears moe_buf.
+//
+// MI355X design (not the reference's LDS mesh + lane-group walk): tokens are
+// cut into chunks of `ct` tokens.  Each chunk builds an LDS bitmap
+// table[token][expert] of slot masks (a byte per cell for topk <= 8, a u32
+// up to topk 32, so duplicates of an expert inside one token's top-k are all
+// kept, in slot order), counts per
+// expert, and a single-block scan turns the per-chunk counts into absolute
+// write positions.  Small batches (one chunk) run the whole thing in one
+// block of one launch; the other blocks of that launch clear the
+// accumulator.
+#include "common.h"
+
+namespace aiter_amd {
+
+constexpr int kSortThreads = 256;
+
+struct SortParams {
+    const int32_t* topk_ids;    // [rows, topk]
+    const float* topk_w;        // [rows, topk]
+    const int32_t* expert_mask; // [E] or null
+    const int32_t* local_tokens;// [1] device scalar or null
+    int32_t* sorted_ids;
+    float* sorted_w;
+    int32_t* sorted_eids;
+    int32_t* num_valid;         // [2]
+    int32_t* ws;                // counts [num_chunks][E] then starts [E]
+    void* zero_buf;             // cleared for `tokens` rows (may be null)
+    int64_t zero_row_bytes;     // multiple of 16
+    int rows;
+    int topk;
+    int E;
+    int bm;
+    int ct;
+    int cell_bytes;             // 1 when topk <= 8 (u8 slot masks), else 4
+    int num_chunks;
+    int sort_blocks;            // blocks of the launch doing sorting work
+};
+
+__host__ __device__ inline int table_words(int ct, int E, int cell_bytes) {
+    return (ct * E * cell_bytes + 3) / 4;
+}
+
+__device__ __forceinline__ int sort_tokens(const SortParams& p) {
+    int t = p.local_tokens ? p.local_tokens[0] : p.rows;
+    return min(max(t, 0), p.rows);
+}
+
+// Clear the accumulator rows [0, tokens) with 16-byte stores; run by the
+// blocks of a launch that are not sorting.
+__device__ void zero_rows(const SortParams& p, int tokens, int block, int nblocks) {
+    if (!p.zero_buf || nblocks <= 0) return;
+    int64_t n16 = (int64_t)tokens * p.zero_row_bytes / 16;
+    v4i z = {0, 0, 0, 0};
+    v4i* dst = reinterpret_cast<v4i*>(p.zero_buf);
+    for (int64_t i = (int64_t)block * kSortThreads + threadIdx.x; i < n16;
+         i += (int64_t)nblocks * kSortThreads)
+        dst[i] = z;
+}
+
+// Slot-mask cell (token tl, expert e) of the chunk table.  Cells are one
+// byte when topk <= 8 and one u32 otherwise; byte cells are set with a u32
+// atomicOr on the aligned word that holds them.
+__device__ __forceinline__ uint32_t table_cell(const SortParams& p, const uint32_t* table, int tl,
+                                               int e) {
+    const int i = tl * p.E + e;
+    if (p.cell_bytes == 1) return reinterpret_cast<const uint8_t*>(table)[i];
+    return table[i];
+}
+
+// Fill table[ct][E] with slot bitmasks of chunk c.
+__device__ void build_table(const SortParams& p, uint32_t* table, int c, int tokens) {
+    const int nwords = (p.ct * p.E * p.cell_bytes + 3) / 4;
+    for (int i = threadIdx.x; i < nwords; i += kSortThreads) table[i] = 0u;
+    __syncthreads();
+    const int t0 = c * p.ct;
+    const int npairs = p.ct * p.topk;
+    for (int i = threadIdx.x; i < npairs; i += kSortThreads) {
+        int tl = i / p.topk;
+        int j = i - tl * p.topk;
+        int t = t0 + tl;
+        if (t < tokens) {
+            int e = p.topk_ids[(int64_t)t * p.topk + j];
+            if (e >= 0 && e < p.E) {
+                const int cell = tl * p.E + e;
+                if (p.cell_bytes == 1)
+                    atomicOr(&table[cell >> 2], (1u << j) << (8 * (cell & 3)));
+                else
+                    atomicOr(&table[cell], 1u << j);
+            }
+        }
+    }
+    __syncthreads();
+}
+
+__device__ __forceinline__ int chunk_rows(const SortParams& p, int c, int tokens) {
+    return max(0, min(p.ct, tokens - c * p.ct));
+}
+
+__device__ __forceinline__ int expert_enabled(const SortParams& p, int e) {
+    return p.expert_mask ? (p.expert_mask[e] != 0) : 1;
+}
+
+__device__ __forceinline__ int wave_incl_scan(int v) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        int n = __shfl_up(v, off, 64);
+        if (lane >= off) v += n;
+    }
+    return v;
+}
+
+// Block-wide exclusive scan of one int per thread; returns the block total
+// through *total.  `scratch` holds kSortThreads/64 ints of LDS.
+__device__ int block_excl_scan(int v, int* scratch, int* total) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    int incl = wave_incl_scan(v);
+    if (lane == 63) scratch[wave] = incl;
+    __syncthreads();
+    int pre = 0, tot = 0;
+#pragma unroll
+    for (int w = 0; w < kSortThreads / 64; ++w) {
+        int s = scratch[w];
+        if (w < wave) pre += s;
+        tot += s;
+    }
+    __syncthreads();
+    *total = tot;
+    return pre + incl - v;
+}
+
+// Given per-expert pair counts in s_total, lay out segments: s_start (padded
+// start offset) and s_local (local expert id); write sorted_expert_ids, the
+// padding entries and num_valid_ids.
+__device__ void finalize_segments(const SortParams& p, const int* s_total, int* s_start,
+                                  int* s_local, int* scratch, int tokens) {
+    const int E = p.E;
+    const int bm = p.bm;
+    const int ept = (E + kSortThreads - 1) / kSortThreads;
+    const int base = threadIdx.x * ept;
+    int psum = 0, msum = 0;
+    for (int i = 0; i < ept; ++i) {
+        int e = base + i;
+        if (e < E) {
+            int en = expert_enabled(p, e);
+            int cnt = s_total[e];
+            psum += en ? ((cnt + bm - 1) / bm) * bm : 0;
+            msum += p.expert_mask ? p.expert_mask[e] : 1;
+        }
+    }
+    int ptot, mtot;
+    int ppre = block_excl_scan(psum, scratch, &ptot);
+    int mpre = block_excl_scan(msum, scratch, &mtot);
+    for (int i = 0; i < ept; ++i) {
+        int e = base + i;
+        if (e < E) {
+            int en = expert_enabled(p, e);
+            int cnt = s_total[e];
+            s_start[e] = ppre;
+            s_local[e] = mpre;
+            ppre += en ? ((cnt + bm - 1) / bm) * bm : 0;
+            mpre += p.expert_mask ? p.expert_mask[e] : 1;
+        }
+    }
+    if (threadIdx.x == 0) {
+        p.num_valid[0] = ptot;
+        p.num_valid[1] = tokens;
+    }
+    __syncthreads();
+    const int32_t pad_id = (int32_t)(((uint32_t)(p.topk & 0xFF) << 24) | ((uint32_t)tokens & 0xFFFFFFu));
+    for (int e = threadIdx.x; e < E; e += kSortThreads) {
+        if (!expert_enabled(p, e)) continue;
+        int cnt = s_total[e];
+        if (cnt == 0) continue;
+        int start = s_start[e];
+        int padded = ((cnt + bm - 1) / bm) * bm;
+        int eid = p.expert_mask ? s_local[e] : e;
+        for (int b = start / bm; b < (start + padded) / bm; ++b) p.sorted_eids[b] = eid;
+        for (int i = start + cnt; i < start + padded; ++i) {
+            p.sorted_ids[i] = pad_id;
+            p.sorted_w[i] = 0.0f;
+        }
+    }
+}
+
+// Emit the pairs of chunk c for every expert, starting at pos0[e].
+__device__ void scatter_chunk(const SortParams& p, const uint32_t* table, int c, int tokens,
+                              const int* s_pos_base, const int32_t* g_off) {
+    const int E = p.E;
+    const int t0 = c * p.ct;
+    const int nrows = chunk_rows(p, c, tokens);
+    for (int e = threadIdx.x; e < E; e += kSortThreads) {
+        if (!expert_enabled(p, e)) continue;
+        int pos = s_pos_base[e] + (g_off ? g_off[(int64_t)c * E + e] : 0);
+        for (int tl = 0; tl < nrows; ++tl) {
+            uint32_t m = table_cell(p, table, tl, e);
+            while (m) {
+                int j = __ffs(m) - 1;
+                m &= m - 1u;
+                int t = t0 + tl;
+                p.sorted_ids[pos] = (int32_t)(((uint32_t)j << 24) | (uint32_t)t);
+                p.sorted_w[pos] = p.topk_w[(int64_t)t * p.topk + j];
+                ++pos;
+            }
+        }
+    }
+}
+
+// LDS layout of the sorting kernels: table[ct*E] | s_total[E] | s_start[E] |
+// s_local[E] | scratch[kSortThreads/64]
+__global__ __launch_bounds__(kSortThreads) void moe_sort_oneshot_kernel(SortParams p) {
+    extern __shared__ uint32_t smem[];
+    const int tokens = sort_tokens(p);
+    if ((int)blockIdx.x >= p.sort_blocks) {
+        zero_rows(p, tokens, blockIdx.x - p.sort_blocks, gridDim.x - p.sort_blocks);
+        return;
+    }
+    uint32_t* table = smem;
+    int* s_total = reinterpret_cast<int*>(smem + table_words(p.ct, p.E, p.cell_bytes));
+    int* s_start = s_total + p.E;
+    int* s_local = s_start + p.E;
+    int* scratch = s_local + p.E;
+    build_table(p, table, 0, tokens);
+    const int nrows = chunk_rows(p, 0, tokens);
+    for (int e = threadIdx.x; e < p.E; e += kSortThreads) {
+        int cnt = 0;
+        for (int tl = 0; tl < nrows; ++tl) cnt += __popc(table_cell(p, table, tl, e));
+        s_total[e] = cnt;
+    }
+    __syncthreads();
+    finalize_segments(p, s_total, s_start, s_local, scratch, tokens);
+    __syncthreads();
+    scatter_chunk(p, table, 0, tokens, s_start, nullptr);
+}
+
+__global__ __launch_bounds__(kSortThreads) void moe_sort_count_kernel(SortParams p) {
+    extern __shared__ uint32_t smem[];
+    const int tokens = sort_tokens(p);
+    if ((int)blockIdx.x >= p.sort_blocks) {
+        zero_rows(p, tokens, blockIdx.x - p.sort_blocks, gridDim.x - p.sort_blocks);
+        return;
+    }
+    const int c = blockIdx.x;
+    build_table(p, smem, c, tokens);
+    const int nrows = chunk_rows(p, c, tokens);
+    for (int e = threadIdx.x; e < p.E; e += kSortThreads) {
+        int cnt = 0;
+        for (int tl = 0; tl < nrows; ++tl) cnt += __popc(table_cell(p, smem, tl, e));
+        p.ws[(int64_t)c * p.E + e] = cnt;
+    }
+}
+
+// One block: per-expert prefix over chunks (counts become chunk offsets in
+// place), then the segment layout.
+__global__ __launch_bounds__(kSortThreads) void moe_sort_scan_kernel(SortParams p) {
+    extern __shared__ uint32_t smem[];
+    const int tokens = sort_tokens(p);
+    int* s_total = reinterpret_cast<int*>(smem);
+    int* s_start = s_total + p.E;
+    int* s_local = s_start + p.E;
+    int* scratch = s_local + p.E;
+    const int E = p.E;
+    for (int e = threadIdx.x; e < E; e += kSortThreads) {
+        int run = 0;
+        int c = 0;
+        for (; c + 4 <= p.num_chunks; c += 4) {
+            int v0 = p.ws[(int64_t)(c + 0) * E + e];
+            int v1 = p.ws[(int64_t)(c + 1) * E + e];
+            int v2 = p.ws[(int64_t)(c + 2) * E + e];
+            int v3 = p.ws[(int64_t)(c + 3) * E + e];
+            p.ws[(int64_t)(c + 0) * E + e] = run;
+            p.ws[(int64_t)(c + 1) * E + e] = run + v0;
+            p.ws[(int64_t)(c + 2) * E + e] = run + v0 + v1;
+            p.ws[(int64_t)(c + 3) * E + e] = run + v0 + v1 + v2;
+            run += v0 + v1 + v2 + v3;
+        }
+        for (; c < p.num_chunks; ++c) {
+            int v = p.ws[(int64_t)c * E + e];
+            p.ws[(int64_t)c * E + e] = run;
+            run += v;
+        }
+        s_total[e] = run;
+    }
+    __syncthreads();
+    finalize_segments(p, s_total, s_start, s_local, scratch, tokens);
+    int32_t* g_start = p.ws + (int64_t)p.num_chunks * E;
+    for (int e = threadIdx.x; e < E; e += kSortThreads) g_start[e] = s_start[e];
+}
+
+__global__ __launch_bounds__(kSortThreads) void moe_sort_scatter_kernel(SortParams p) {
+    extern __shared__ uint32_t smem[];
+    const int tokens = sort_tokens(p);
+    const int c = blockIdx.x;
+    if (c * p.ct >= tokens) return;
+    build_table(p, smem, c, tokens);
+    const int32_t* g_start = p.ws + (int64_t)p.num_chunks * p.E;
+    int* s_base = reinterpret_cast<int*>(smem + table_words(p.ct, p.E, p.cell_bytes));
+    for (int e = threadIdx.x; e < p.E; e += kSortThreads) s_base[e] = g_start[e];
+    __syncthreads();
+    scatter_chunk(p, smem, c, tokens, s_base, p.ws);
+}
+
+// ---------------------------------------------------------------- host ---
+// Tokens per chunk: the largest power of two <= 256 whose slot-mask table
+// fits in 48 KB of LDS (so table + scan arrays stay within 64 KB).
+static int sort_chunk_tokens(int E, int topk) {
+    const int cell = topk <= 8 ? 1 : 4;
+    int ct = 256;
+    while (ct > 1 && (int64_t)ct * E * cell > 48 * 1024) ct >>= 1;
+    return ct;
+}
+
+int64_t sort_workspace_bytes(int64_t rows, int64_t topk, int64_t E) {
+    int ct = sort_chunk_tokens((int)E, (int)topk);
+    int64_t chunks = ceil_div(rows > 0 ? rows : 1, ct);
+    if (chunks <= 1) return 0;
+    return (chunks * E + E) * 4;
+}
+
+void launch_moe_sort(const int32_t* topk_ids, const float* topk_w, const int32_t* expert_mask,
+                     const int32_t* local_tokens, int32_t* sorted_ids, float* sorted_w,
+                     int32_t* sorted_eids, int32_t* num_valid, void* zero_buf,
+                     int64_t zero_row_bytes, int64_t rows, int64_t topk, int64_t E, int64_t bm,
+                     void* ws, int64_t ws_bytes, hipStream_t stream) {
+    SortParams p;
+    p.topk_ids = topk_ids;
+    p.topk_w = topk_w;
+    p.expert_mask = expert_mask;
+    p.local_tokens = local_tokens;
+    p.sorted_ids = sorted_ids;
+    p.sorted_w = sorted_w;
+    p.sorted_eids = sorted_eids;
+    p.num_valid = num_valid;
+    p.zero_buf = zero_buf;
+    p.zero_row_bytes = zero_row_bytes;
+    p.rows = (int)rows;
+    p.topk = (int)topk;
+    p.E = (int)E;
+    p.bm = (int)bm;
+    p.ct = sort_chunk_tokens((int)E, (int)topk);
+    p.cell_bytes = topk <= 8 ? 1 : 4;
+    p.num_chunks = (int)ceil_div(rows > 0 ? rows : 1, p.ct);
+    p.ws = reinterpret_cast<int32_t*>(ws);
+
+    // zero blocks: about one 16-byte store per thread per 4 iterations
+    int zero_blocks = 0;
+    if (zero_buf && rows > 0) {
+        int64_t n16 = rows * zero_row_bytes / 16;
+        zero_blocks = (int)std::min<int64_t>(ceil_div(n16, (int64_t)kSortThreads * 4), 2048);
+        if (zero_blocks < 1) zero_blocks = 1;
+    }
+    const size_t scan_lds = (size_t)(3 * E + kSortThreads / 64) * 4;
+    const size_t table_lds = (size_t)table_words(p.ct, (int)E, p.cell_bytes) * 4;
+    if (p.num_chunks == 1) {
+        p.sort_blocks = 1;
+        hipLaunchKernelGGL(moe_sort_oneshot_kernel, dim3(1 + zero_blocks), dim3(kSortThreads),
+                           table_lds + scan_lds, stream, p);
+    } else {
+        AMD_CHECK(ws != nullptr && ws_bytes >= sort_workspace_bytes(rows, topk, E),
+                  "sorting workspace too small");
+        p.sort_blocks = p.num_chunks;
+        hipLaunchKernelGGL(moe_sort_count_kernel, dim3(p.num_chunks + zero_blocks),
+                           dim3(kSortThreads), table_lds, stream, p);
+        hipLaunchKernelGGL(moe_sort_scan_kernel, dim3(1), dim3(kSortThreads), scan_lds, stream, p);
+        hipLaunchKernelGGL(moe_sort_scatter_kernel, dim3(p.num_chunks), dim3(kSortThreads),
+                           table_lds + (size_t)E * 4, stream, p);
+    }
+    AMD_HIP_CHECK(hipGetLastError());
+}
+
+}  // namespace aiter_amd

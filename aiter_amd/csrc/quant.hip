@@ -1,0 +1,142 @@
+// Per-token-group (1 x 128) dynamic FP8 e4m3fn quantisation of activations,
+// and the fp32 -> bf16/fp16 conversion that finishes the down GEMM.
+//
+// Quantisation semantics follow the reference HIP kernel
+// (csrc/kernels/quant_kernels.cu:16-133, host 710-757):
+//   amax  = max(1e-10, max |x|) over the 128-element group
+//   scale = amax * fp32(1/448)
+//   q     = e4m3fn_rne(clamp(x * fp32(1/scale), -448, 448))
+// The scale is stored row-major [rows, cols/128], or transposed
+// [cols/128, rows] when transpose_scale is set (quant_kernels.cu:118-121).
+// When num_rows is given (a device scalar), only *num_rows * num_rows_factor
+// rows are processed (quant_kernels.cu:32-35).
+//
+// MI355X layout: 16 lanes x 8 elements (one 16-byte load each) cover a
+// group; a 256-thread block quantises 16 groups; the group amax is a 4-step
+// xor-shuffle inside the 16-lane quarter of the wave.
+#include "common.h"
+
+namespace aiter_amd {
+
+constexpr int kQuantThreads = 256;
+
+template <bool kBf16>
+__global__ __launch_bounds__(kQuantThreads) void per_group_quant_fp8_kernel(
+    const uint16_t* __restrict__ x, uint8_t* __restrict__ q, float* __restrict__ scale,
+    int64_t rows, int cols, int transpose_scale, const int32_t* __restrict__ num_rows,
+    int num_rows_factor) {
+    int64_t rows_eff = rows;
+    if (num_rows) {
+        int64_t r = (int64_t)num_rows[0] * num_rows_factor;
+        rows_eff = r < 0 ? 0 : (r < rows ? r : rows);
+    }
+    const int G = cols / 128;
+    const int64_t g = (int64_t)blockIdx.x * (kQuantThreads / 16) + (threadIdx.x >> 4);
+    const int sub = threadIdx.x & 15;
+    const int64_t row = g / G;
+    const int gc = (int)(g - row * G);
+    const bool active = row < rows_eff;
+    const int64_t off = row * cols + (int64_t)gc * 128 + sub * 8;
+
+    float v[8];
+    float amax = 1e-10f;
+    if (active) {
+        v4i raw = *reinterpret_cast<const v4i*>(x + off);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            uint32_t w = (uint32_t)raw[i];
+            if (kBf16) {
+                v[2 * i] = bf16_bits_to_f32((uint16_t)(w & 0xFFFFu));
+                v[2 * i + 1] = bf16_bits_to_f32((uint16_t)(w >> 16));
+            } else {
+                v[2 * i] = fp16_bits_to_f32((uint16_t)(w & 0xFFFFu));
+                v[2 * i + 1] = fp16_bits_to_f32((uint16_t)(w >> 16));
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[i]));
+    }
+    amax = warp_max_16(amax);
+    if (!active) return;
+    const float s = amax * kInvFp8Max;
+    const float inv = 1.0f / s;
+    uint32_t lo = f32x4_to_fp8x4(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv);
+    uint32_t hi = f32x4_to_fp8x4(v[4] * inv, v[5] * inv, v[6] * inv, v[7] * inv);
+    uint2 packed;
+    packed.x = lo;
+    packed.y = hi;
+    *reinterpret_cast<uint2*>(q + off) = packed;
+    if (sub == 0) {
+        if (transpose_scale)
+            scale[(int64_t)gc * rows_eff + row] = s;
+        else
+            scale[row * G + gc] = s;
+    }
+}
+
+void launch_per_group_quant_fp8(const void* x, int x_dtype, void* q, float* scale, int64_t rows,
+                                int64_t cols, int transpose_scale, const int32_t* num_rows,
+                                int64_t num_rows_factor, hipStream_t stream) {
+    const int64_t groups = rows * (cols / 128);
+    if (groups == 0) return;
+    const int64_t blocks = ceil_div(groups, kQuantThreads / 16);
+    AMD_CHECK(blocks < (1ll << 31), "too many rows");
+    if (x_dtype == DT_BF16)
+        hipLaunchKernelGGL(per_group_quant_fp8_kernel<true>, dim3((unsigned)blocks),
+                           dim3(kQuantThreads), 0, stream, (const uint16_t*)x, (uint8_t*)q, scale,
+                           rows, (int)cols, transpose_scale, num_rows, (int)num_rows_factor);
+    else
+        hipLaunchKernelGGL(per_group_quant_fp8_kernel<false>, dim3((unsigned)blocks),
+                           dim3(kQuantThreads), 0, stream, (const uint16_t*)x, (uint8_t*)q, scale,
+                           rows, (int)cols, transpose_scale, num_rows, (int)num_rows_factor);
+    AMD_HIP_CHECK(hipGetLastError());
+}
+
+// ------------------------------------------- fp32 accumulator -> output ---
+// out[r, :] = round(acc[r, :]) for r < tokens (tokens = *num_valid[1]);
+// 8 elements per thread.
+template <bool kBf16>
+__global__ __launch_bounds__(256) void acc_to_out_kernel(const float* __restrict__ acc,
+                                                         uint16_t* __restrict__ out,
+                                                         const int32_t* __restrict__ num_valid,
+                                                         int64_t rows, int cols) {
+    int64_t tokens = num_valid ? (int64_t)num_valid[1] : rows;
+    tokens = tokens < rows ? tokens : rows;
+    const int64_t n8 = tokens * cols / 8;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n8;
+         i += (int64_t)gridDim.x * 256) {
+        const v4f a = *reinterpret_cast<const v4f*>(acc + i * 8);
+        const v4f b = *reinterpret_cast<const v4f*>(acc + i * 8 + 4);
+        uint32_t w[4];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            float x0 = a[2 * j], x1 = a[2 * j + 1];
+            float y0 = b[2 * j], y1 = b[2 * j + 1];
+            if (kBf16) {
+                w[j] = f32_to_bf16_bits(x0) | ((uint32_t)f32_to_bf16_bits(x1) << 16);
+                w[2 + j] = f32_to_bf16_bits(y0) | ((uint32_t)f32_to_bf16_bits(y1) << 16);
+            } else {
+                w[j] = f32_to_fp16_bits(x0) | ((uint32_t)f32_to_fp16_bits(x1) << 16);
+                w[2 + j] = f32_to_fp16_bits(y0) | ((uint32_t)f32_to_fp16_bits(y1) << 16);
+            }
+        }
+        v4i o = {(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+        *reinterpret_cast<v4i*>(out + i * 8) = o;
+    }
+}
+
+void launch_acc_to_out(const float* acc, void* out, int out_dtype, const int32_t* num_valid,
+                       int64_t rows, int64_t cols, hipStream_t stream) {
+    const int64_t n8 = rows * cols / 8;
+    if (n8 == 0) return;
+    const int blocks = (int)std::min<int64_t>(ceil_div(n8, 256), 8192);
+    if (out_dtype == DT_BF16)
+        hipLaunchKernelGGL(acc_to_out_kernel<true>, dim3(blocks), dim3(256), 0, stream, acc,
+                           (uint16_t*)out, num_valid, rows, (int)cols);
+    else
+        hipLaunchKernelGGL(acc_to_out_kernel<false>, dim3(blocks), dim3(256), 0, stream, acc,
+                           (uint16_t*)out, num_valid, rows, (int)cols);
+    AMD_HIP_CHECK(hipGetLastError());
+}
+
+}  // namespace aiter_amd

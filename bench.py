@@ -1,0 +1,296 @@
+"""Benchmark of the MI355X blockscale fused-MoE layer (one GPU).
+
+Default workload (BASELINE.json metric, first leg): the MiMo-style prefill
+layer, E=256, top-8, hidden 4096, inter 2048, T=8192 tokens with
+Zipf(1.1)-skewed routing, fp8 e4m3fn 128x128 weight scales, 1x128 activation
+scales, bf16 in/out.  A step is one aiter_amd.fused_moe call (sorting,
+activation quant, stage 1, stage 2, output conversion) on inputs resident
+in HBM.  The decode leg (T=32, uniform softmax routing) is reported under
+"decode".  Prints one JSON line.
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload prefill8192|decode32]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_FP8_FLOPS = 5.0e15   # MI355X dense fp8 MFMA
+PEAK_HBM_BPS = 8.0e12     # MI355X HBM3E
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--workload", default="prefill8192",
+                   choices=["prefill8192", "prefill2048", "decode32", "decode1", "decode128",
+                            "ep4096"])
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-decode", action="store_true")
+    p.add_argument("--kernel-iters", type=int, default=10)
+    return p.parse_args()
+
+
+def make_cfg(name):
+    from aiter_amd import workloads as W
+
+    if name.startswith("prefill"):
+        return W.mimo_prefill(int(name[len("prefill"):]))
+    if name.startswith("decode"):
+        return W.mimo_decode(int(name[len("decode"):]))
+    return W.mimo_ep_share(int(name[len("ep"):]))
+
+
+class Layer:
+    """Inputs of one MoE layer resident on the GPU."""
+
+    def __init__(self, cfg, dev):
+        import torch
+
+        from aiter_amd import workloads as W
+
+        self.cfg = cfg
+        self.dev = dev
+        self.w = W.make_weights(cfg, device=dev, shuffle=True)
+        self.x = W.make_hidden(cfg, device=dev)
+        self.tw, self.ids = W.make_routing(cfg, device=dev)
+        self.mask = W.make_expert_mask(cfg, device=dev)
+        ids = self.ids
+        if self.mask is not None:
+            local = self.mask.bool()[ids.long()]
+            self.pairs = int(local.sum().item())
+            self.distinct = int(torch.unique(ids[local]).numel())
+        else:
+            self.pairs = ids.numel()
+            self.distinct = int(torch.unique(ids).numel())
+        torch.cuda.synchronize()
+
+    def run(self):
+        import aiter_amd as A
+
+        return A.fused_moe(self.x, self.w["w1"], self.w["w2"], self.tw, self.ids,
+                           expert_mask=self.mask, quant_type=A.QuantType.per_128x128,
+                           w1_scale=self.w["w1_scale"], w2_scale=self.w["w2_scale"])
+
+
+def time_steps(fn, steps, warmup):
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    s = torch.cuda.Event(enable_timing=True)
+    e = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    s.record()
+    for _ in range(steps):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return s.elapsed_time(e) / steps, wall
+
+
+def stage_kernel_times(layer, iters):
+    """Average device time of each stage's kernel, measured with HIP events
+    on torch's current stream (the stream the kernels are launched on)."""
+    import torch
+
+    import aiter_amd as A
+
+    cfg = layer.cfg
+    bm = A.default_block_m(cfg.tokens, cfg.topk, cfg.local_experts or cfg.experts)
+    E_sort = cfg.experts
+    sid, sw, se, nv, acc = A.moe_sorting(layer.ids, layer.tw, E_sort, cfg.model_dim,
+                                         torch.float32, bm, layer.mask)
+    a1, a1s = A.per_group_quant_hip(layer.x)
+    a2, a2s = A.moe_stage1_fp8_blockscale(a1, a1s, layer.w["w1"], layer.w["w1_scale"], sid, se,
+                                          nv, cfg.topk, bm, True)
+    torch.cuda.synchronize()
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(iters):
+            fn()
+        e.record()
+        torch.cuda.synchronize()
+        return s.elapsed_time(e) / iters * 1e-3
+
+    t1 = timed(lambda: A.moe_stage1_fp8_blockscale(a1, a1s, layer.w["w1"], layer.w["w1_scale"],
+                                                   sid, se, nv, cfg.topk, bm, True))
+    t2 = timed(lambda: A.moe_stage2_fp8_blockscale(a2, a2s, layer.w["w2"], layer.w["w2_scale"],
+                                                   sid, sw, se, nv, acc, bm, True))
+    tq = timed(lambda: A.per_group_quant_hip(layer.x))
+    ts = timed(lambda: A.moe_sorting(layer.ids, layer.tw, E_sort, cfg.model_dim, torch.float32,
+                                     bm, layer.mask))
+    return {"stage1_s": t1, "stage2_s": t2, "act_quant_s": tq, "sorting_s": ts, "block_m": bm}
+
+
+def stage1_work(layer):
+    cfg = layer.cfg
+    H, I, P, D, T = cfg.model_dim, cfg.inter_dim, layer.pairs, layer.distinct, cfg.tokens
+    flops = 2.0 * P * (2 * I) * H
+    w_bytes = D * (2 * I * H + 4 * (2 * I // 128) * (H // 128))
+    act_bytes = T * H + T * (H // 128) * 4 + P * I + P * (I // 128) * 4 + P * 4
+    return flops, float(w_bytes + act_bytes)
+
+
+def roofline(flops, bytes_, seconds):
+    t_mfma = flops / PEAK_FP8_FLOPS
+    t_hbm = bytes_ / PEAK_HBM_BPS
+    if t_hbm >= t_mfma:
+        ach = bytes_ / seconds / 1e9
+        return {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_BPS / 1e9,
+                "unit": "GB/s", "frac": round(ach / (PEAK_HBM_BPS / 1e9), 4), "traffic": None,
+                "mfma_frac": round(flops / seconds / PEAK_FP8_FLOPS, 4)}
+    ach = flops / seconds / 1e12
+    return {"bound": "mfma", "achieved": round(ach, 1), "peak": PEAK_FP8_FLOPS / 1e12,
+            "unit": "TFLOP/s", "frac": round(ach / (PEAK_FP8_FLOPS / 1e12), 4), "traffic": None,
+            "hbm_frac": round(bytes_ / seconds / PEAK_HBM_BPS, 4)}
+
+
+def cpu_baseline(layer, budget_s=12.0):
+    """Oracle (numpy 'port' of the reference torch path) timed on this host on
+    a bounded sample of the same workload: a seeded random sample of the
+    touched experts, each processed for all of its routed pairs (dequant of
+    its weights, stage-1 GEMM, SiLU*up, requant, stage-2 GEMM).  The full
+    layer time is extrapolated as D * (mean dequant time per expert) +
+    P * (mean GEMM time per pair)."""
+    import numpy as np
+    import torch
+
+    from oracle import moe_ref as R
+
+    cfg = layer.cfg
+    ids = layer.ids.cpu().numpy()
+    tw = layer.tw.cpu().numpy()
+    x = layer.x.float().cpu().numpy()
+    if layer.mask is not None:
+        ids = R.local_expert_ids(ids, layer.mask.cpu().numpy())
+    experts = np.unique(ids[ids >= 0])
+    rng = np.random.default_rng(0)
+    rng.shuffle(experts)
+    from aiter_amd.shuffle import unshuffle_weight
+
+    t_deq = t_gemm = 0.0
+    n_exp = n_pairs = 0
+    t_start = time.perf_counter()
+    a1q, a1s = R.quant_1x128_kernel(x)
+    a1 = R.dequant_1x128(a1q, a1s)
+    t_quant = time.perf_counter() - t_start
+    I = cfg.inter_dim
+    for e in experts:
+        w1q = unshuffle_weight(layer.w["w1"][e:e + 1]).view(torch.uint8).cpu().numpy()
+        w2q = unshuffle_weight(layer.w["w2"][e:e + 1]).view(torch.uint8).cpu().numpy()
+        s1 = layer.w["w1_scale"][e:e + 1].cpu().numpy()
+        s2 = layer.w["w2_scale"][e:e + 1].cpu().numpy()
+        t0 = time.perf_counter()
+        w1 = R.dequant_weight_128x128(w1q, s1)[0]
+        w2 = R.dequant_weight_128x128(w2q, s2)[0]
+        t1 = time.perf_counter()
+        tok, slot = np.nonzero(ids == e)
+        y = a1[tok] @ w1.T
+        h = R.bf16_round(R.silu(y[:, :I]) * y[:, I:])
+        hq, hs = R.quant_1x128_kernel(h)
+        o = (R.dequant_1x128(hq, hs) @ w2.T) * tw[tok, slot][:, None]
+        t2 = time.perf_counter()
+        t_deq += t1 - t0
+        t_gemm += t2 - t1
+        n_exp += 1
+        n_pairs += tok.size
+        if time.perf_counter() - t_start > budget_s and n_exp >= 2:
+            break
+    full = t_quant + len(experts) * (t_deq / n_exp) + layer.pairs * (t_gemm / max(n_pairs, 1))
+    threads = torch.get_num_threads()
+    try:
+        import numpy.__config__  # noqa: F401
+        cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    except Exception:  # pragma: no cover
+        cores = threads
+    return {
+        "value": round(cfg.tokens / full, 2), "unit": "tokens/s", "cores": cores,
+        "kind": "port",
+        "sample": (f"numpy oracle on {n_exp} of {len(experts)} touched experts "
+                   f"({n_pairs} of {layer.pairs} routed pairs) of the same T={cfg.tokens} "
+                   f"layer; full-layer time extrapolated as D*dequant/expert + P*gemm/pair "
+                   f"= {full:.2f} s"),
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on exactly one GPU; --gpus N>1 is not "
+                                   "supported (see DESIGN.md: how the path would shard)"}))
+        sys.exit(2)
+    import torch
+
+    dev = torch.device("cuda:0")
+    cfg = make_cfg(args.workload)
+    layer = Layer(cfg, dev)
+    ms, wall = time_steps(layer.run, args.steps, args.warmup)
+    layer_s = ms * 1e-3
+    flops_layer = 2.0 * layer.pairs * 3 * cfg.inter_dim * cfg.model_dim
+    from aiter_amd import workloads as W
+
+    bytes_layer = W.layer_bytes(cfg, layer.distinct)
+    kt = stage_kernel_times(layer, args.kernel_iters)
+    f1, b1 = stage1_work(layer)
+    line = {
+        "metric": "MoE-layer tokens/s (MiMo-style FP8 blockscale layer, T=%d)" % cfg.tokens,
+        "value": round(cfg.tokens / layer_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8",
+        "data": "synthetic (seeded N(0,0.02) weights -> fp8 128x128, N(0,1) bf16 activations)",
+        "config": {"workload": cfg.name, "tokens": cfg.tokens, "model_dim": cfg.model_dim,
+                   "inter_dim": cfg.inter_dim, "experts": cfg.experts, "topk": cfg.topk,
+                   "routing": cfg.routing, "local_experts": cfg.local_experts,
+                   "block_m": kt["block_m"], "distinct_experts": layer.distinct},
+        "layer": {"tflops": round(flops_layer / layer_s / 1e12, 2),
+                  "fp8_peak_frac": round(flops_layer / layer_s / PEAK_FP8_FLOPS, 4),
+                  "hbm_gbps": round(bytes_layer / layer_s / 1e9, 1),
+                  "hbm_peak_frac": round(bytes_layer / layer_s / PEAK_HBM_BPS, 4),
+                  "alg_flops": flops_layer, "alg_bytes": bytes_layer,
+                  "wall_s_timed_region": round(wall, 4)},
+        "kernels_us": {k: round(v * 1e6, 1) for k, v in kt.items() if k.endswith("_s")},
+        "roofline": dict(roofline(f1, b1, kt["stage1_s"]), kernel="moe_gemm_fp8bs stage 1"),
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(layer)
+    if not args.no_decode and not args.workload.startswith("decode"):
+        dcfg = make_cfg("decode32")
+        del layer
+        torch.cuda.empty_cache()
+        dl = Layer(dcfg, dev)
+        dms, _ = time_steps(dl.run, max(args.steps, 20), args.warmup)
+        db = W.layer_bytes(dcfg, dl.distinct)
+        line["decode"] = {"workload": dcfg.name, "ms_per_step": round(dms, 4),
+                          "tokens_per_s": round(dcfg.tokens / (dms * 1e-3), 1),
+                          "hbm_gbps": round(db / (dms * 1e-3) / 1e9, 1),
+                          "hbm_peak_frac": round(db / (dms * 1e-3) / PEAK_HBM_BPS, 4),
+                          "distinct_experts": dl.distinct}
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

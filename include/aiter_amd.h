@@ -1,0 +1,147 @@
+/*
+ * aiter_amd — C ABI of the MI355X (gfx950) blockscale fused-MoE library.
+ *
+ * Conventions (mirroring the reference's ctypes bridge,
+ * csrc/include/aiter_ctypes_error.h:60-147 and aiter/jit/core.py:1105-1363):
+ *   - every compute entry point returns 0 on success, -1 on failure; the
+ *     failure text is read with aiter_amd_get_last_error() (per thread);
+ *   - every buffer is caller-owned device memory passed as a plain pointer;
+ *     the library never allocates or frees device memory;
+ *   - `stream` is a hipStream_t (torch's current stream in the Python layer)
+ *     and is always the last argument; no entry point synchronises the host;
+ *   - all argument validation happens before any device work, so invalid
+ *     calls fail without touching the GPU;
+ *   - dtype codes are AiterDtype values (csrc/include/aiter_enum.h:27-43):
+ *     fp8 = 0, fp16 = 2, bf16 = 3, fp32 = 4.
+ * fp8 means OCP e4m3fn (torch.float8_e4m3fn), the gfx950 fp8 format.
+ */
+#ifndef AITER_AMD_H
+#define AITER_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define AITER_AMD_ABI_VERSION 1
+
+/* Replaces aiter_ctypes_abi_version (aiter_ctypes_error.h:120-147). */
+int aiter_amd_abi_version(void);
+/* Replaces aiter_get_last_error / aiter_clear_last_error
+ * (aiter_ctypes_error.h:60-118, read by aiter/jit/core.py:1341-1355). */
+const char* aiter_amd_get_last_error(void);
+void aiter_amd_clear_last_error(void);
+
+/* Bytes of device workspace aiter_amd_moe_sorting_fwd needs for `tokens`
+ * rows of topk_ids (0 when the one-launch path is taken).  Plays the role
+ * of moe_sorting_get_workspace_size (csrc/include/moe_sorting_opus.h:1351-1379). */
+int64_t aiter_amd_moe_sorting_workspace_bytes(int64_t tokens, int64_t topk,
+                                              int64_t num_experts);
+
+/* Replaces moe_sorting_fwd (csrc/py_itfs_ck/moe_sorting_kernels.cu:10-70)
+ * and moe_sorting_opus_fwd (csrc/py_itfs_cu/moe_sorting_opus_kernels.cu:31-92).
+ *   topk_ids [tokens, topk] i32, topk_weights [tokens, topk] f32
+ *   sorted_ids / sorted_weights: capacity >= tokens*topk + E*block_size - topk
+ *   sorted_expert_ids: capacity >= ceil(that / block_size); num_valid_ids [2]
+ *   moe_buf: optional, cleared for the first `tokens` (or *num_local_tokens)
+ *   rows of moe_buf_row_bytes bytes (a multiple of 16)
+ *   expert_mask [num_experts] i32 or NULL; num_local_tokens: device i32[1] or NULL
+ *   dispatch_policy is accepted for interface parity and ignored (every
+ *   policy yields the same output). */
+int aiter_amd_moe_sorting_fwd(const int32_t* topk_ids, const float* topk_weights,
+                              int64_t tokens, int64_t topk, int32_t* sorted_ids,
+                              float* sorted_weights, int32_t* sorted_expert_ids,
+                              int32_t* num_valid_ids, int64_t sorted_capacity,
+                              int64_t blocks_capacity, void* moe_buf,
+                              int64_t moe_buf_row_bytes, int64_t num_experts,
+                              int64_t block_size, const int32_t* expert_mask,
+                              const int32_t* num_local_tokens, int64_t dispatch_policy,
+                              void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Replaces dynamic_per_token_scaled_quant for 1x128 groups
+ * (csrc/kernels/quant_kernels.cu:710-757, kernel 16-133), as called by
+ * per_group_quant_hip (aiter/ops/quant.py:260-292).
+ *   input [rows, cols] bf16/fp16 -> out [rows, cols] fp8, scales f32
+ *   [rows, cols/128] (or [cols/128, rows] when transpose_scale != 0).
+ *   group_size must be 128; num_rows: device i32[1] or NULL. */
+int aiter_amd_dynamic_per_group_quant_fp8(const void* input, int input_dtype, int64_t rows,
+                                          int64_t cols, int64_t group_size, void* out,
+                                          float* scales, int transpose_scale,
+                                          const int32_t* num_rows, int64_t num_rows_factor,
+                                          void* stream);
+
+/* Replaces ck_moe_stage1 with per_1x128 fp8 (gemm_moe_ck2stages.cu:46-116)
+ * plus the a2 requant (aiter/fused_moe.py:1306-1314); the fused fp8-out
+ * form matches moe_stage1_g1u1 blockscale (asm_moe_2stage.cu:148-280).
+ *   a1 [tokens, model_dim] fp8, a1_scale f32 [tokens, model_dim/128]
+ *   (or [model_dim/128, tokens] when a1_scale_transposed != 0)
+ *   w1 [E, 2*inter_dim, model_dim] fp8, w1_scale [E, 2*inter_dim/128, model_dim/128]
+ *   a2 [tokens, topk, inter_dim] fp8, a2_scale [tokens, topk, inter_dim/128]
+ *   activation must be 0 (Silu); w_shuffled: 1 for the (16,16) layout.
+ *   block_m in {16, 32, 64}; max_m_blocks = capacity of sorted_expert_ids. */
+int aiter_amd_moe_stage1_fp8_blockscale(const void* a1, const float* a1_scale,
+                                        int64_t a1_scale_transposed, const void* w1,
+                                        const float* w1_scale, const int32_t* sorted_ids,
+                                        const int32_t* sorted_expert_ids,
+                                        const int32_t* num_valid_ids, void* a2, float* a2_scale,
+                                        int64_t tokens, int64_t model_dim, int64_t inter_dim,
+                                        int64_t num_experts, int64_t topk, int64_t block_m,
+                                        int64_t max_m_blocks, int64_t activation,
+                                        int64_t w_shuffled, void* stream);
+
+/* Replaces ck_moe_stage2 with per_1x128 fp8 (gemm_moe_ck2stages.cu:118-181).
+ *   a2 [tokens, topk, inter_dim] fp8 + a2_scale [tokens, topk, inter_dim/128]
+ *   w2 [E, model_dim, inter_dim] fp8, w2_scale [E, model_dim/128, inter_dim/128]
+ *   out_acc [tokens, model_dim] f32 accumulates sorted_weight * row (it must
+ *   be zeroed first, e.g. by aiter_amd_moe_sorting_fwd's moe_buf). */
+int aiter_amd_moe_stage2_fp8_blockscale(const void* a2, const float* a2_scale, const void* w2,
+                                        const float* w2_scale, const int32_t* sorted_ids,
+                                        const float* sorted_weights,
+                                        const int32_t* sorted_expert_ids,
+                                        const int32_t* num_valid_ids, float* out_acc,
+                                        int64_t tokens, int64_t model_dim, int64_t inter_dim,
+                                        int64_t num_experts, int64_t topk, int64_t block_m,
+                                        int64_t max_m_blocks, int64_t w_shuffled, void* stream);
+
+/* Converts the stage-2 f32 accumulator into moe_buf (bf16 or fp16) for the
+ * first num_valid_ids[1] rows.  The reference accumulates into moe_buf
+ * directly (gemm_moe_ck2stages.cu:118-181); this is the finishing pass of the
+ * f32-accumulating design. */
+int aiter_amd_moe_acc_to_out(const float* acc, void* out, int out_dtype,
+                             const int32_t* num_valid_ids, int64_t tokens, int64_t model_dim,
+                             void* stream);
+
+/* Bytes of workspace for aiter_amd_fused_moe_fp8_blockscale. */
+int64_t aiter_amd_fused_moe_workspace_bytes(int64_t tokens, int64_t model_dim,
+                                            int64_t inter_dim, int64_t num_experts,
+                                            int64_t topk, int64_t block_m);
+
+/* The whole 2-stage FP8 blockscale MoE in one call; replaces the sequence
+ * of fused_moe_ -> moe_sorting -> fused_moe_2stages (aiter/fused_moe.py:
+ * 205-364, 27-103, 1103-1334) for quant_type per_1x128 / per_128x128.
+ *   hidden_states [tokens, model_dim] bf16/fp16 (hidden_dtype)
+ *   w1/w2/w1_scale/w2_scale as for the stage calls; topk_ids/topk_weights
+ *   [tokens, topk]; expert_mask [global_experts] or NULL (then
+ *   global_experts == num_experts); num_local_tokens device i32[1] or NULL.
+ *   out [tokens, model_dim] in out_dtype (bf16/fp16).
+ *   block_m = 0 picks the default for the token count. */
+int aiter_amd_fused_moe_fp8_blockscale(const void* hidden_states, int hidden_dtype,
+                                       const void* w1, const float* w1_scale, const void* w2,
+                                       const float* w2_scale, const float* topk_weights,
+                                       const int32_t* topk_ids, const int32_t* expert_mask,
+                                       const int32_t* num_local_tokens, void* out,
+                                       int out_dtype, int64_t tokens, int64_t model_dim,
+                                       int64_t inter_dim, int64_t num_experts,
+                                       int64_t global_experts, int64_t topk, int64_t block_m,
+                                       int64_t w_shuffled, void* workspace,
+                                       int64_t workspace_bytes, void* stream);
+
+/* Default M-block (sorted rows per GEMM tile) for a token count. */
+int64_t aiter_amd_default_block_m(int64_t tokens, int64_t topk, int64_t num_experts);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AITER_AMD_H */

@@ -1,0 +1,162 @@
+"""C-ABI checks that need no GPU: the library loads, exports every symbol
+include/aiter_amd.h declares, reports its ABI version, and rejects invalid
+arguments (before any device work) with -1 and a readable last error --
+the reference's ctypes error bridge (csrc/include/aiter_ctypes_error.h:
+60-147).  Also host-side logic of the Python layer.
+"""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from aiter_amd import _abi
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def _declared_symbols():
+    text = (ROOT / "include" / "aiter_amd.h").read_text()
+    return sorted(set(re.findall(r"\b(aiter_amd_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _abi.load()
+
+
+def test_header_and_binding_agree():
+    assert _declared_symbols() == sorted(_abi.EXPORTED)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in _declared_symbols():
+        assert hasattr(lib, name), name
+
+
+def test_abi_version(lib):
+    assert lib.aiter_amd_abi_version() == 1
+
+
+def _expect_error(name, *args, match):
+    with pytest.raises(RuntimeError, match=match):
+        _abi.call(name, *args)
+
+
+def test_sorting_validation_errors(lib):
+    # topk out of range, block_size out of range, capacity too small, NULL
+    _expect_error("aiter_amd_moe_sorting_fwd", 1, 1, 4, 0, 1, 1, 1, 1, 100, 10, None, 0, 8, 32,
+                  None, None, 0, None, 0, None, match="topk must be")
+    _expect_error("aiter_amd_moe_sorting_fwd", 1, 1, 4, 2, 1, 1, 1, 1, 100, 10, None, 0, 8, 0,
+                  None, None, 0, None, 0, None, match="block_size")
+    _expect_error("aiter_amd_moe_sorting_fwd", 1, 1, 4, 2, 1, 1, 1, 1, 10, 10, None, 0, 8, 32,
+                  None, None, 0, None, 0, None, match="capacity")
+    _expect_error("aiter_amd_moe_sorting_fwd", None, 1, 4, 2, 1, 1, 1, 1, 1000, 100, None, 0, 8,
+                  32, None, None, 0, None, 0, None, match="NULL")
+    _expect_error("aiter_amd_moe_sorting_fwd", 16, 16, 4, 2, 16, 16, 16, 16, 1000, 100, 16, 24,
+                  8, 32, None, None, 0, None, 0, None, match="multiple of 16")
+    # large token counts need a workspace
+    need = lib.aiter_amd_moe_sorting_workspace_bytes(100000, 8, 256)
+    assert need > 0 and lib.aiter_amd_moe_sorting_workspace_bytes(8, 8, 256) == 0
+    _expect_error("aiter_amd_moe_sorting_fwd", 16, 16, 100000, 8, 16, 16, 16, 16, 10**7, 10**6,
+                  None, 0, 256, 32, None, None, 0, None, 0, None, match="workspace")
+
+
+def test_quant_validation_errors():
+    _expect_error("aiter_amd_dynamic_per_group_quant_fp8", 16, 3, 4, 256, 64, 16, 16, 0, None, 1,
+                  None, match="group_size 128")
+    _expect_error("aiter_amd_dynamic_per_group_quant_fp8", 16, 4, 4, 256, 128, 16, 16, 0, None, 1,
+                  None, match="bf16 or fp16")
+    _expect_error("aiter_amd_dynamic_per_group_quant_fp8", 16, 3, 4, 200, 128, 16, 16, 0, None, 1,
+                  None, match="multiple of 128")
+    _expect_error("aiter_amd_dynamic_per_group_quant_fp8", 8, 3, 4, 256, 128, 16, 16, 0, None, 1,
+                  None, match="aligned")
+
+
+def test_stage_validation_errors():
+    args = [16, 16, 0, 16, 16, 16, 16, 16, 16, 16]
+    _expect_error("aiter_amd_moe_stage1_fp8_blockscale", *args, 4, 4096, 2000, 8, 2, 32, 10, 0, 1,
+                  None, match="inter_dim must be")
+    _expect_error("aiter_amd_moe_stage1_fp8_blockscale", *args, 4, 4096, 2048, 8, 2, 128, 10, 0,
+                  1, None, match="block_m must be 16, 32 or 64")
+    _expect_error("aiter_amd_moe_stage1_fp8_blockscale", *args, 4, 4096, 2048, 8, 2, 32, 10, 1, 1,
+                  None, match="Silu")
+    _expect_error("aiter_amd_moe_stage2_fp8_blockscale", 16, 16, 16, 16, 16, 16, 16, 16, 16, 4,
+                  4096, 2048, 8, 40, 32, 10, 1, None, match="topk must be")
+    _expect_error("aiter_amd_moe_acc_to_out", 16, 16, 4, 16, 4, 64, None, match="bf16 or fp16")
+
+
+def test_fused_validation_errors(lib):
+    base = [16, 3, 16, 16, 16, 16, 16, 16, None, None, 16, 3]
+    _expect_error("aiter_amd_fused_moe_fp8_blockscale", *base, 4, 4096, 2048, 8, 8, 2, 0, 1, 16,
+                  10, None, match="workspace of")
+    masked = [16, 3, 16, 16, 16, 16, 16, 16, 16, None, 16, 3]    # expert_mask given
+    _expect_error("aiter_amd_fused_moe_fp8_blockscale", *masked, 4, 4096, 2048, 8, 4, 2, 0, 1,
+                  16, 10**9, None, match="global_experts")
+    ws = lib.aiter_amd_fused_moe_workspace_bytes(8192, 4096, 2048, 256, 8, 64)
+    # sorted ids/weights + a1 + a2 + f32 accumulator dominate
+    assert ws > 8192 * 4096 * (1 + 4) + 8192 * 8 * 2048
+
+
+def test_default_block_m(lib):
+    assert lib.aiter_amd_default_block_m(1, 8, 256) == 16
+    assert lib.aiter_amd_default_block_m(32, 8, 256) == 16
+    assert lib.aiter_amd_default_block_m(8192, 8, 256) == 64
+
+
+def test_python_layer_rejects_unsupported_modes():
+    from aiter_amd import ActivationType, QuantType, fused_moe
+
+    x = torch.zeros(4, 256, dtype=torch.bfloat16)
+    w1 = torch.zeros(2, 256, 256, dtype=torch.float8_e4m3fn)
+    w2 = torch.zeros(2, 256, 128, dtype=torch.float8_e4m3fn)
+    ids = torch.zeros(4, 1, dtype=torch.int32)
+    tw = torch.ones(4, 1)
+    s1 = torch.ones(2, 2, 2)
+    s2 = torch.ones(2, 2, 1)
+    with pytest.raises(NotImplementedError, match="quant_type"):
+        fused_moe(x, w1, w2, tw, ids, quant_type=QuantType.No)
+    with pytest.raises(NotImplementedError, match="activation"):
+        fused_moe(x, w1, w2, tw, ids, quant_type=QuantType.per_128x128,
+                  activation=ActivationType.Gelu, w1_scale=s1, w2_scale=s2)
+    with pytest.raises(NotImplementedError, match="doweight_stage1"):
+        fused_moe(x, w1, w2, tw, ids, quant_type=QuantType.per_128x128, doweight_stage1=True,
+                  w1_scale=s1, w2_scale=s2)
+    with pytest.raises(ValueError, match="w1_scale"):
+        fused_moe(x, w1, w2, tw, ids, quant_type=QuantType.per_128x128)
+
+
+def test_enum_values_match_reference():
+    from aiter_amd import ActivationType, QuantType
+
+    # csrc/include/aiter_enum.h:7-26
+    assert [ActivationType.No, ActivationType.Silu, ActivationType.Gelu,
+            ActivationType.Swiglu] == [-1, 0, 1, 2]
+    assert QuantType.per_1x128 == 4 and QuantType.per_128x128 == 5 and QuantType.per_1x32 == 3
+
+
+def test_shuffle_roundtrip_and_layout():
+    import numpy as np
+
+    from aiter_amd import shuffle_weight, unshuffle_weight
+    from oracle import moe_ref as R
+
+    w = torch.randint(0, 255, (3, 64, 256), dtype=torch.uint8)
+    sh = shuffle_weight(w)
+    assert sh.is_shuffled
+    assert np.array_equal(sh.numpy(), R.shuffle_16x16(w.numpy()))
+    assert torch.equal(unshuffle_weight(sh), w)
+
+
+def test_weight_quant_matches_oracle():
+    import numpy as np
+
+    from aiter_amd import quant_weight_per_128x128
+    from oracle import moe_ref as R
+
+    w = torch.randn(2, 256, 384) * 0.02
+    q, s = quant_weight_per_128x128(w)
+    qo, so = R.quant_weight_128x128(w.numpy())
+    assert np.array_equal(q.view(torch.uint8).numpy(), qo)
+    assert np.array_equal(s.numpy(), so)

@@ -1,0 +1,248 @@
+"""Pins of the CPU oracle (oracle/moe_ref.py) -- CPU only.
+
+Every oracle function is checked here against something it does not
+share code with: torch's own fp8/bf16 conversions, the reference's worked
+sorting example (csrc/include/moe_sorting_opus.h:277-339), an independent
+argsort statement of sorting, closed forms (the group maximum quantises to
+exactly 448; E=1,k=1 is a dense block-scale GEMM) and fp64 brute force on
+tiny inputs.  Each check is chosen so a plausible slip (dropped scale, wrong
+slot/token order, swapped gate/up, transposed weight) fails it.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe_ref as R
+
+
+# ------------------------------------------------------------------ fp8 ---
+def test_fp8_lut_matches_torch():
+    codes = torch.arange(256, dtype=torch.int32).to(torch.uint8)
+    tv = codes.view(torch.float8_e4m3fn).float().numpy()
+    nan = np.isnan(tv)
+    assert (nan == np.isnan(R.FP8_LUT)).all()
+    assert np.array_equal(tv[~nan], R.FP8_LUT[~nan])
+    assert R.FP8_LUT[0x7E] == 448.0 and R.FP8_LUT[0x01] == 2.0 ** -9
+
+
+def test_fp8_encode_matches_torch_random_and_midpoints():
+    rng = np.random.default_rng(1)
+    x = np.concatenate([
+        rng.standard_normal(200000).astype(np.float32) * 50,
+        rng.standard_normal(20000).astype(np.float32) * 1e-3,     # subnormal range
+    ])
+    vals = R.FP8_LUT[:0x7F].astype(np.float64)
+    mids = ((vals[1:] + vals[:-1]) / 2).astype(np.float32)         # exact ties
+    x = np.concatenate([x, mids, -mids, np.float32([0.0, -0.0, 448.0, -448.0])])
+    x = np.clip(x, -448, 448)
+    got = R.fp8_encode_rne_sat(x)
+    ref = torch.from_numpy(x).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(got, ref)
+
+
+def test_fp8_encode_saturates():
+    got = R.fp8_encode_rne_sat(np.float32([1e6, -1e6, 464.0, 470.0]))
+    assert list(got) == [0x7E, 0xFE, 0x7E, 0x7E]
+
+
+def test_bf16_round_matches_torch():
+    x = np.random.default_rng(2).standard_normal(100000).astype(np.float32) * 1e3
+    ref = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(R.bf16_round(x), ref)
+
+
+# ------------------------------------------------------------ act quant ---
+def test_quant_1x128_group_max_hits_448():
+    x = R.bf16_round(np.random.default_rng(3).standard_normal((37, 512)).astype(np.float32))
+    q, s = R.quant_1x128_kernel(x)
+    g = x.reshape(37, 4, 128)
+    idx = np.abs(g).argmax(-1)
+    qmax = np.take_along_axis(R.fp8_decode(q).reshape(37, 4, 128), idx[..., None], -1)[..., 0]
+    assert np.all(np.abs(qmax) == 448.0)
+    np.testing.assert_array_equal(s, (np.abs(g).max(-1) * np.float32(1 / 448)).astype(np.float32))
+
+
+def test_quant_1x128_close_to_torch_pertoken_quant():
+    x = R.bf16_round(np.random.default_rng(4).standard_normal((64, 1024)).astype(np.float32))
+    qk, sk = R.quant_1x128_kernel(x)
+    qt, st = R.pertoken_quant_torch_semantics(x)
+    # scales: x*(1/448) vs x/448 differ by at most one ulp
+    assert np.all(np.abs(sk.view(np.int32) - st.view(np.int32)) <= 1)
+    # codes: identical except one-step flips where x/s lands on an fp8 tie
+    # (bf16 inputs make exact ties common; x*(1/s) and x/s break them apart)
+    diff = np.abs(qk.astype(np.int32) - qt.astype(np.int32))
+    assert diff.max() <= 1 and (diff != 0).mean() < 1e-2
+    # torch reference of the same pertoken_quant
+    xt = torch.from_numpy(x).view(64, 8, 128)
+    amax = xt.abs().amax(-1, keepdim=True)
+    sc = amax / 448.0
+    qref = (xt / sc).to(torch.float8_e4m3fn).view(torch.uint8).numpy().reshape(64, 1024)
+    assert np.array_equal(qt, qref)
+
+
+def test_quant_zero_group_and_dequant_error_bound():
+    x = np.zeros((2, 256), np.float32)
+    x[1, 128:] = np.linspace(-3, 3, 128)
+    q, s = R.quant_1x128_kernel(x)
+    assert np.all(R.fp8_decode(q[0]) == 0) and s[0, 0] == np.float32(1e-10) * np.float32(1 / 448)
+    d = R.dequant_1x128(q, s)
+    # e4m3 has 3 mantissa bits: relative error <= 2^-4 for normals
+    nz = np.abs(x) > 448 * 2 ** -6 * s.repeat(128, axis=1)
+    assert np.all(np.abs(d - x)[nz] <= np.abs(x)[nz] * 2 ** -4 + 1e-12)
+
+
+def test_weight_quant_128x128_matches_torch_pertoken():
+    w = np.random.default_rng(5).standard_normal((2, 256, 384)).astype(np.float32) * 0.02
+    w[1, :128, :128] = 0.0
+    q, s = R.quant_weight_128x128(w)
+    assert s.shape == (2, 2, 3) and s[1, 0, 0] == 1.0
+    wt = torch.from_numpy(w).view(2, 2, 128, 3, 128).permute(0, 1, 3, 2, 4)
+    amax = wt.abs().amax((-1, -2), keepdim=True)
+    sc = amax / 448.0
+    sc[sc == 0] = 1
+    qt = (wt / sc).to(torch.float8_e4m3fn).permute(0, 1, 3, 2, 4).reshape(2, 256, 384)
+    assert np.array_equal(q, qt.view(torch.uint8).numpy())
+    np.testing.assert_array_equal(s, sc.view(2, 2, 3).numpy())
+
+
+def test_shuffle_matches_definition():
+    w = np.arange(2 * 32 * 64, dtype=np.int64).reshape(2, 32, 64) % 251
+    sh = R.shuffle_16x16(w.astype(np.uint8))
+    # element (e, n, k) lands at [e][n//16][k//32][(k%32)//16][n%16][k%16]
+    for (e, n, k) in [(0, 0, 0), (1, 17, 45), (0, 31, 63), (1, 5, 16)]:
+        flat = ((((n // 16) * 2 + k // 32) * 2 + (k % 32) // 16) * 16 + n % 16) * 16 + k % 16
+        assert sh[e].reshape(-1)[flat] == w[e, n, k]
+
+
+# -------------------------------------------------------------- sorting ---
+def _header_example():
+    # csrc/include/moe_sorting_opus.h:277-339 (E=6, topk=3, block 4, 5 tokens)
+    ids = np.array([[0, 3, 5], [2, 3, 5], [1, 3, 5], [1, 2, 3], [1, 3, 5]], np.int32)
+    w = np.arange(15, dtype=np.float32).reshape(5, 3) + 1
+    return ids, w
+
+
+def test_sorting_reference_worked_example():
+    ids, w = _header_example()
+    sid, sw, se, nv = R.moe_sorting_ref(ids, w, 6, 4)
+    assert list(se) == [0, 1, 2, 3, 3, 5] and list(nv) == [24, 5]
+    tok = (sid & 0xFFFFFF).tolist()
+    assert tok == [0, 5, 5, 5, 2, 3, 4, 5, 1, 3, 5, 5, 0, 1, 2, 3, 4, 5, 5, 5, 0, 1, 2, 4]
+    slot = (sid >> 24).tolist()
+    assert slot[:4] == [0, 3, 3, 3] and slot[12:17] == [1, 1, 1, 2, 1]
+    assert sw[0] == 1 and sw[4] == w[2, 0] and np.all(sw[1:4] == 0)
+    # masked variant: experts 1 and 4 are off -> local ids [0, 1, 2, 2, 3], total 20
+    sid, sw, se, nv = R.moe_sorting_ref(ids, w, 6, 4, expert_mask=np.array([1, 0, 1, 1, 0, 1]))
+    assert list(se) == [0, 1, 2, 2, 3] and list(nv) == [20, 5]
+
+
+@pytest.mark.parametrize("T,E,k,bm,masked,local", [
+    (1, 32, 5, 32, False, None), (31, 32, 5, 16, True, None), (128, 256, 8, 32, False, None),
+    (300, 256, 8, 64, True, 250), (64, 8, 2, 16, False, None), (7, 257, 9, 32, False, 5),
+])
+def test_sorting_two_statements_agree(T, E, k, bm, masked, local):
+    rng = np.random.default_rng(T * 131 + E)
+    ids = np.stack([rng.permutation(E)[:k] for _ in range(T)]).astype(np.int32)
+    w = rng.random((T, k), dtype=np.float32)
+    mask = rng.integers(0, 2, E) if masked else None
+    a = R.moe_sorting_ref(ids, w, E, bm, mask, local)
+    b = R.moe_sorting_argsort(ids, w, E, bm, mask, local)
+    for x, y in zip(a, b):
+        assert np.array_equal(x, y)
+    sid, sw, se, nv = a
+    # invariants: segments are block multiples, every local pair once
+    assert nv[0] % bm == 0 and se.size == nv[0] // bm
+    tokens = T if local is None else local
+    real = sid[(sid & 0xFFFFFF) < tokens]
+    enabled = np.ones(E, bool) if mask is None else mask.astype(bool)
+    expect = sum(int(enabled[e]) for e in ids[:tokens].reshape(-1))
+    assert real.size == expect == np.unique(real).size
+
+
+def test_sorting_duplicates_and_out_of_range_ids():
+    ids = np.array([[1, 1, 9], [0, -1, 1]], np.int32)
+    w = np.array([[0.1, 0.2, 0.3], [0.4, 0.5, 0.6]], np.float32)
+    sid, sw, se, nv = R.moe_sorting_ref(ids, w, 4, 4)
+    assert list(nv) == [8, 2] and list(se) == [0, 1]
+    assert sid[4:7].tolist() == [0, 1 << 24, (2 << 24) | 1]
+    b = R.moe_sorting_argsort(ids, w, 4, 4)
+    assert np.array_equal(sid, b[0]) and np.array_equal(sw, b[1])
+
+
+# --------------------------------------------------------- stage oracles ---
+def _brute_force_layer(x, w1d, w2d, ids_local, topk_w):
+    """fp64 loops over (token, slot): independent of the vectorised oracle."""
+    T, H = x.shape
+    E, N1, _ = w1d.shape
+    I = N1 // 2
+    out = np.zeros((T, H))
+    hs = np.zeros((T, ids_local.shape[1], I))
+    for t in range(T):
+        for j in range(ids_local.shape[1]):
+            e = ids_local[t, j]
+            if e < 0:
+                continue
+            y = w1d[e].astype(np.float64) @ x[t].astype(np.float64)
+            h = y[:I] / (1 + np.exp(-y[:I])) * y[I:]
+            hs[t, j] = h
+            out[t] += topk_w[t, j] * (w2d[e].astype(np.float64) @ h)
+    return hs, out
+
+
+def test_stage_oracles_vs_fp64_brute_force():
+    rng = np.random.default_rng(6)
+    T, H, I, E, k = 9, 256, 128, 4, 2
+    x = R.bf16_round(rng.standard_normal((T, H)).astype(np.float32))
+    w1d = rng.standard_normal((E, 2 * I, H)).astype(np.float32) * 0.05
+    w2d = rng.standard_normal((E, H, I)).astype(np.float32) * 0.05
+    ids = np.stack([rng.permutation(E)[:k] for _ in range(T)])
+    tw = rng.random((T, k)).astype(np.float32)
+    h = R.moe_stage1_ref(x, w1d, ids)
+    out = R.moe_stage2_ref(h, w2d, ids, tw)
+    hb, ob = _brute_force_layer(x, w1d, w2d, ids, tw)
+    np.testing.assert_allclose(h, hb, rtol=1e-2, atol=1e-3)
+    # stage 2 fed with the same h in fp64
+    _, ob2 = _brute_force_layer(x, w1d, w2d, ids, tw)
+    mx, rms = R.normalized_errors(ob2, out)
+    assert mx < 1e-2 and rms < 3e-3
+    # a swapped gate/up or a transposed weight is caught
+    w1_swapped = np.concatenate([w1d[:, I:], w1d[:, :I]], axis=1)
+    assert R.normalized_errors(hb, R.moe_stage1_ref(x, w1_swapped, ids))[0] > 0.1
+
+
+def test_stage1_e1_k1_is_dense_blockscale_gemm():
+    rng = np.random.default_rng(7)
+    T, H, I = 5, 384, 128
+    w = rng.standard_normal((1, 2 * I, H)).astype(np.float32) * 0.03
+    wq, ws = R.quant_weight_128x128(w)
+    x = R.bf16_round(rng.standard_normal((T, H)).astype(np.float32))
+    aq, as_ = R.quant_1x128_kernel(x)
+    ids = np.zeros((T, 1), np.int64)
+    h = R.moe_stage1_ref(R.dequant_1x128(aq, as_), R.dequant_weight_128x128(wq, ws), ids)
+    # dense: sum over K blocks of (a_q . w_q) * a_s * w_s, in float64
+    A = R.fp8_decode(aq).astype(np.float64)
+    W = R.fp8_decode(wq[0]).astype(np.float64)
+    y = np.zeros((T, 2 * I))
+    for kb in range(H // 128):
+        sl = slice(kb * 128, kb * 128 + 128)
+        y += (A[:, sl] @ W[:, sl].T) * as_[:, kb:kb + 1] * np.repeat(ws[0][:, kb], 128)[None]
+    hd = y[:, :I] / (1 + np.exp(-y[:, :I])) * y[:, I:]
+    np.testing.assert_allclose(h[:, 0], hd, rtol=8e-3, atol=1e-4)
+
+
+def test_expert_mask_local_ids():
+    ids = np.array([[0, 3], [5, 2]])
+    mask = np.array([1, 0, 1, 1, 0, 1])
+    assert R.local_expert_ids(ids, mask).tolist() == [[0, 2], [3, 1]]
+    ids = np.array([[1, 4]])
+    assert R.local_expert_ids(ids, mask).tolist() == [[-1, -1]]
+
+
+def test_normalized_errors_known_values():
+    ref = np.array([1.0, -2.0, 0.5, 0.0])
+    got = np.array([1.0, -2.0, 0.5, 0.02])
+    mx, rms = R.normalized_errors(ref, got)
+    refn = ref / 2
+    rms_ref = np.sqrt((refn ** 2).mean())
+    assert np.isclose(mx, 0.01 / rms_ref)
+    assert np.isclose(rms, np.sqrt(((0.01 / rms_ref) ** 2) / 4))
