@@ -36,6 +36,9 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-decode", action="store_true")
     p.add_argument("--kernel-iters", type=int, default=10)
+    p.add_argument("--kernel-only", choices=["stage1", "stage2"], default=None,
+                   help="profiling mode: run a 256 MiB device copy (counter calibration) "
+                        "then only this kernel --steps times")
     return p.parse_args()
 
 
@@ -143,6 +146,37 @@ def stage_kernel_times(layer, iters):
     return {"stage1_s": t1, "stage2_s": t2, "act_quant_s": tq, "sorting_s": ts, "block_m": bm}
 
 
+def kernel_only(layer, which, steps):
+    """Profiling mode for rocprofv3 counter runs: a plain 256 MiB copy
+    (known bytes, for scaling FETCH_SIZE / WRITE_SIZE) and then one stage
+    kernel alone."""
+    import torch
+
+    import aiter_amd as A
+
+    src = torch.empty(256 << 20, dtype=torch.uint8, device=layer.dev).fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    cfg = layer.cfg
+    bm = A.default_block_m(cfg.tokens, cfg.topk, cfg.local_experts or cfg.experts)
+    sid, sw, se, nv, acc = A.moe_sorting(layer.ids, layer.tw, cfg.experts, cfg.model_dim,
+                                         torch.float32, bm, layer.mask)
+    a1, a1s = A.per_group_quant_hip(layer.x)
+    a2, a2s = A.moe_stage1_fp8_blockscale(a1, a1s, layer.w["w1"], layer.w["w1_scale"], sid, se,
+                                          nv, cfg.topk, bm, True)
+    torch.cuda.synchronize()
+    for _ in range(steps):
+        if which == "stage1":
+            A.moe_stage1_fp8_blockscale(a1, a1s, layer.w["w1"], layer.w["w1_scale"], sid, se, nv,
+                                        cfg.topk, bm, True)
+        else:
+            A.moe_stage2_fp8_blockscale(a2, a2s, layer.w["w2"], layer.w["w2_scale"], sid, sw, se,
+                                        nv, acc, bm, True)
+    torch.cuda.synchronize()
+    log(f"kernel-only {which}: {steps} launches done")
+
+
 def stage1_work(layer):
     cfg = layer.cfg
     H, I, P, D, T = cfg.model_dim, cfg.inter_dim, layer.pairs, layer.distinct, cfg.tokens
@@ -246,6 +280,9 @@ def main():
     cfg = make_cfg(args.workload)
     log(f"building {cfg.name} inputs")
     layer = Layer(cfg, dev)
+    if args.kernel_only:
+        kernel_only(layer, args.kernel_only, args.steps)
+        return
     log(f"timing {args.steps} steps after {args.warmup} warmup")
     ms, wall = time_steps(layer.run, args.steps, args.warmup)
     log(f"layer {ms:.3f} ms/step; timing kernels")
