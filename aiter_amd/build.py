@@ -27,6 +27,8 @@ HIPCC_FLAGS = [
     "-Wno-unused-function",
     # packed fp32 VALU ops stay off (only ordinary scalar fp32 code is emitted)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results straight into VGPRs: the block-scale FMA reads them there
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 
 

@@ -31,6 +31,45 @@ void launch_moe_stage2_fp8bs(const uint8_t*, const float*, const uint8_t*, const
                              const int32_t*, const float*, const int32_t*, const int32_t*,
                              float*, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t,
                              int64_t, int, hipStream_t);
+// moe_gemm_fp8bs_v2.hip (64/128-row M-blocks)
+bool v2_supported(int64_t block_m, int64_t K);
+void launch_moe_stage1_fp8bs_v2(const uint8_t*, const float*, int64_t, int64_t, const uint8_t*,
+                                const float*, const int32_t*, const int32_t*, const int32_t*,
+                                uint8_t*, float*, int64_t, int64_t, int64_t, int64_t, int64_t,
+                                int64_t, int64_t, int, hipStream_t);
+void launch_moe_stage2_fp8bs_v2(const uint8_t*, const float*, const uint8_t*, const float*,
+                                const int32_t*, const float*, const int32_t*, const int32_t*,
+                                float*, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t,
+                                int64_t, int, hipStream_t);
+
+// Kernel choice per shape: M-blocks of 64/128 rows with K a multiple of 256
+// (and, for stage 2, 256-column output tiles) take the large-tile
+// direct-to-LDS kernels; 16/32-row blocks (decode) the streaming kernels.
+static void stage1_dispatch(const uint8_t* a, const float* sa, int64_t sa_row, int64_t sa_kb,
+                            const uint8_t* w1, const float* w1s, const int32_t* sid,
+                            const int32_t* seid, const int32_t* nv, uint8_t* a2, float* a2s,
+                            int64_t a_rows, int64_t K, int64_t I, int64_t E, int64_t topk,
+                            int64_t bm, int64_t mblocks, int sh, hipStream_t s) {
+    if (v2_supported(bm, K))
+        launch_moe_stage1_fp8bs_v2(a, sa, sa_row, sa_kb, w1, w1s, sid, seid, nv, a2, a2s, a_rows,
+                                   K, I, E, topk, bm, mblocks, sh, s);
+    else
+        launch_moe_stage1_fp8bs(a, sa, sa_row, sa_kb, w1, w1s, sid, seid, nv, a2, a2s, a_rows, K,
+                                I, E, topk, bm, mblocks, sh, s);
+}
+
+static void stage2_dispatch(const uint8_t* a2, const float* a2s, const uint8_t* w2,
+                            const float* w2s, const int32_t* sid, const float* sw,
+                            const int32_t* seid, const int32_t* nv, float* acc, int64_t a_rows,
+                            int64_t I, int64_t H, int64_t E, int64_t topk, int64_t bm,
+                            int64_t mblocks, int sh, hipStream_t s) {
+    if (v2_supported(bm, I) && H % 256 == 0)
+        launch_moe_stage2_fp8bs_v2(a2, a2s, w2, w2s, sid, sw, seid, nv, acc, a_rows, I, H, E, topk,
+                                   bm, mblocks, sh, s);
+    else
+        launch_moe_stage2_fp8bs(a2, a2s, w2, w2s, sid, sw, seid, nv, acc, a_rows, I, H, E, topk, bm,
+                                mblocks, sh, s);
+}
 
 namespace {
 
@@ -49,10 +88,14 @@ int64_t sorted_capacity_for(int64_t tokens, int64_t topk, int64_t E, int64_t bm)
     return tokens * topk + E * bm - topk;
 }
 
-void check_block_m_gemm(int64_t bm) {
-    AMD_CHECK(bm == 16 || bm == 32 || bm == 64,
-              "block_m must be 16, 32 or 64 for the fp8 blockscale GEMMs, got " +
+void check_block_m_gemm(int64_t bm, int64_t model_dim, int64_t inter_dim) {
+    AMD_CHECK(bm == 16 || bm == 32 || bm == 64 || bm == 128,
+              "block_m must be 16, 32, 64 or 128 for the fp8 blockscale GEMMs, got " +
                   std::to_string(bm));
+    if (bm == 128)
+        AMD_CHECK(v2_supported(bm, model_dim) && v2_supported(bm, inter_dim) &&
+                      model_dim % 256 == 0,
+                  "block_m 128 needs model_dim a multiple of 256 and model_dim, inter_dim <= 8192");
 }
 
 void check_dims(int64_t model_dim, int64_t inter_dim) {
@@ -103,10 +146,15 @@ FusedLayout fused_layout(int64_t T, int64_t H, int64_t I, int64_t E_sort, int64_
     return L;
 }
 
-int64_t default_block_m(int64_t tokens, int64_t topk, int64_t E) {
+int64_t default_block_m(int64_t tokens, int64_t topk, int64_t E, int64_t model_dim,
+                        int64_t inter_dim) {
     const int64_t avg = E > 0 ? tokens * topk / E : 0;
     if (avg <= 8) return 16;
     if (avg <= 48) return 32;
+    // 128-row tiles halve the B (weight) re-reads; worth it once padding is a small fraction
+    if (avg >= 128 && v2_supported(128, model_dim) && v2_supported(128, inter_dim) &&
+        model_dim % 256 == 0)
+        return 128;
     return 64;
 }
 
@@ -128,8 +176,9 @@ int64_t aiter_amd_moe_sorting_workspace_bytes(int64_t tokens, int64_t topk, int6
     return sort_workspace_bytes(tokens, topk, num_experts);
 }
 
-int64_t aiter_amd_default_block_m(int64_t tokens, int64_t topk, int64_t num_experts) {
-    return default_block_m(tokens, topk, num_experts);
+int64_t aiter_amd_default_block_m(int64_t tokens, int64_t topk, int64_t num_experts,
+                                  int64_t model_dim, int64_t inter_dim) {
+    return default_block_m(tokens, topk, num_experts, model_dim, inter_dim);
 }
 
 int aiter_amd_moe_sorting_fwd(const int32_t* topk_ids, const float* topk_weights, int64_t tokens,
@@ -203,7 +252,7 @@ int aiter_amd_moe_stage1_fp8_blockscale(const void* a1, const float* a1_scale,
     return safe_call([&] {
         check_dims(model_dim, inter_dim);
         check_topk_experts(tokens, topk, num_experts);
-        check_block_m_gemm(block_m);
+        check_block_m_gemm(block_m, model_dim, inter_dim);
         AMD_CHECK(activation == 0, "only ActivationType.Silu (0) is supported, got " +
                                        std::to_string(activation));
         AMD_CHECK(max_m_blocks >= 0, "max_m_blocks must be >= 0");
@@ -217,11 +266,10 @@ int aiter_amd_moe_stage1_fp8_blockscale(const void* a1, const float* a1_scale,
         const int64_t KB = model_dim / 128;
         const int64_t sa_row = a1_scale_transposed ? 1 : KB;
         const int64_t sa_kb = a1_scale_transposed ? tokens : 1;
-        launch_moe_stage1_fp8bs((const uint8_t*)a1, a1_scale, sa_row, sa_kb, (const uint8_t*)w1,
-                                w1_scale, sorted_ids, sorted_expert_ids, num_valid_ids,
-                                (uint8_t*)a2, a2_scale, tokens, model_dim, inter_dim, num_experts,
-                                topk, block_m, max_m_blocks, (int)(w_shuffled != 0),
-                                (hipStream_t)stream);
+        stage1_dispatch((const uint8_t*)a1, a1_scale, sa_row, sa_kb, (const uint8_t*)w1, w1_scale,
+                        sorted_ids, sorted_expert_ids, num_valid_ids, (uint8_t*)a2, a2_scale,
+                        tokens, model_dim, inter_dim, num_experts, topk, block_m, max_m_blocks,
+                        (int)(w_shuffled != 0), (hipStream_t)stream);
     });
 }
 
@@ -236,7 +284,7 @@ int aiter_amd_moe_stage2_fp8_blockscale(const void* a2, const float* a2_scale, c
     return safe_call([&] {
         check_dims(model_dim, inter_dim);
         check_topk_experts(tokens, topk, num_experts);
-        check_block_m_gemm(block_m);
+        check_block_m_gemm(block_m, model_dim, inter_dim);
         AMD_CHECK(max_m_blocks >= 0, "max_m_blocks must be >= 0");
         if (tokens == 0 || max_m_blocks == 0) return;
         check_ptr(a2, "a2");
@@ -245,11 +293,10 @@ int aiter_amd_moe_stage2_fp8_blockscale(const void* a2, const float* a2_scale, c
         AMD_CHECK(a2_scale && w2_scale && sorted_ids && sorted_weights && sorted_expert_ids &&
                       num_valid_ids,
                   "a required pointer is NULL");
-        launch_moe_stage2_fp8bs((const uint8_t*)a2, a2_scale, (const uint8_t*)w2, w2_scale,
-                                sorted_ids, sorted_weights, sorted_expert_ids, num_valid_ids,
-                                out_acc, tokens * topk, inter_dim, model_dim, num_experts, topk,
-                                block_m, max_m_blocks, (int)(w_shuffled != 0),
-                                (hipStream_t)stream);
+        stage2_dispatch((const uint8_t*)a2, a2_scale, (const uint8_t*)w2, w2_scale, sorted_ids,
+                        sorted_weights, sorted_expert_ids, num_valid_ids, out_acc, tokens * topk,
+                        inter_dim, model_dim, num_experts, topk, block_m, max_m_blocks,
+                        (int)(w_shuffled != 0), (hipStream_t)stream);
     });
 }
 
@@ -272,7 +319,7 @@ int64_t aiter_amd_fused_moe_workspace_bytes(int64_t tokens, int64_t model_dim, i
                                             int64_t num_experts, int64_t topk, int64_t block_m) {
     if (tokens < 0 || model_dim <= 0 || inter_dim <= 0 || num_experts < 1 || topk < 1)
         return -1;
-    if (block_m <= 0) block_m = default_block_m(tokens, topk, num_experts);
+    if (block_m <= 0) block_m = default_block_m(tokens, topk, num_experts, model_dim, inter_dim);
     return fused_layout(tokens, model_dim, inter_dim, num_experts, topk, block_m).total;
 }
 
@@ -294,8 +341,8 @@ int aiter_amd_fused_moe_fp8_blockscale(const void* hidden_states, int hidden_dty
         const int64_t E_sort = expert_mask ? global_experts : num_experts;
         AMD_CHECK(E_sort >= num_experts && E_sort <= kMaxExperts,
                   "global_experts must be in [num_experts, 4096]");
-        if (block_m <= 0) block_m = default_block_m(tokens, topk, num_experts);
-        check_block_m_gemm(block_m);
+        if (block_m <= 0) block_m = default_block_m(tokens, topk, num_experts, model_dim, inter_dim);
+        check_block_m_gemm(block_m, model_dim, inter_dim);
         if (tokens == 0) return;
         check_ptr(hidden_states, "hidden_states");
         check_ptr(w1, "w1");
@@ -325,12 +372,12 @@ int aiter_amd_fused_moe_fp8_blockscale(const void* hidden_states, int hidden_dty
         launch_per_group_quant_fp8(hidden_states, hidden_dtype, a1, a1_scale, tokens, model_dim,
                                    0, num_local_tokens, 1, s);
         const int sh = (int)(w_shuffled != 0);
-        launch_moe_stage1_fp8bs(a1, a1_scale, model_dim / 128, 1, (const uint8_t*)w1, w1_scale,
-                                sorted_ids, sorted_eids, num_valid, a2, a2_scale, tokens,
-                                model_dim, inter_dim, num_experts, topk, block_m, L.blocks, sh, s);
-        launch_moe_stage2_fp8bs(a2, a2_scale, (const uint8_t*)w2, w2_scale, sorted_ids, sorted_w,
-                                sorted_eids, num_valid, acc, tokens * topk, inter_dim, model_dim,
-                                num_experts, topk, block_m, L.blocks, sh, s);
+        stage1_dispatch(a1, a1_scale, model_dim / 128, 1, (const uint8_t*)w1, w1_scale, sorted_ids,
+                        sorted_eids, num_valid, a2, a2_scale, tokens, model_dim, inter_dim,
+                        num_experts, topk, block_m, L.blocks, sh, s);
+        stage2_dispatch(a2, a2_scale, (const uint8_t*)w2, w2_scale, sorted_ids, sorted_w,
+                        sorted_eids, num_valid, acc, tokens * topk, inter_dim, model_dim,
+                        num_experts, topk, block_m, L.blocks, sh, s);
         launch_acc_to_out(acc, out, out_dtype, num_valid, tokens, model_dim, s);
     });
 }

@@ -1,0 +1,527 @@
+// Prefill-shaped FP8 block-scale MoE GEMMs for gfx950: large tiles,
+// direct-to-LDS loads, a 3-stage K pipeline, XCD-aware tile order.
+//
+// Same contract as moe_gemm_fp8bs.hip (stage 1: gate+up GEMM, SiLU*up,
+// bf16 rounding and 1x128 fp8 requant; stage 2: down GEMM, routing weight,
+// f32 atomic accumulate), for M-blocks of 64 or 128 sorted rows.
+//
+// Workgroup: 512 threads = 2 (M) x 4 (N) wave64s, two waves per SIMD so the
+// block-scale FMAs of one wave run beside the other wave's MFMAs; tile BM
+// rows x 256 weight rows (stage 1: 128 gate + the matching 128 up rows =
+// 128 outputs; stage 2: 256 outputs); each wave owns (BM/2) x 64 weight
+// columns, i.e. 4 16-wide MFMA column tiles (stage 1: 2 gate + the 2
+// matching up tiles), so a 128-K step costs the wave BM/32 * 4
+// v_mfma_f32_16x16x128_f8f6f4 against (BM/2 + 64) * 128 bytes of LDS reads.
+//
+// K pipeline: every operand of a K step -- the A rows (gathered by token),
+// the B tile and the A scales -- is fetched with buffer_load ... lds
+// straight into one of NS LDS stage buffers, NS-1 steps ahead of the step
+// being computed.  Each step begins with s_waitcnt vmcnt(<loads of the
+// steps still in flight>) and a barrier, issues the loads of step k+NS-1
+// into the buffer step k-1 used, then computes step k.
+// LDS layouts are fragment-major: an MFMA operand fragment (one row or
+// column, 32 consecutive K bytes of quarter kq) sits in one 32-byte slot
+// and the 16 lanes of a quarter read one 512-byte span, as two 16-byte
+// reads.  Within each slot the two 16-byte halves are swapped for rows
+// with h0(r) = ((r >> 2) ^ (r >> 3)) & 1, so each 16-byte read of 8 or 16
+// consecutive lanes covers distinct banks.
+//   A tile: [kq 4][row BM][32 B];  B tile: 16 groups of 16 weight rows,
+//   each [kq 4][row 16][32 B] (the (16,16) shuffled 2 KB block with the two
+//   16-byte halves of a row brought together).  The DMA lane -> global
+//   address map does the reordering.
+// Tile order: the grid is 1-D; workgroup L runs on XCD L % 8 and each XCD
+// owns n_tiles/8 column tiles for every M-block, so the weight slice of an
+// expert stays in that XCD's L2 across the expert's consecutive M-blocks.
+#include "common.h"
+
+namespace aiter_amd {
+
+namespace v2 {
+
+constexpr int kThreads = 512;
+constexpr int kWaves = kThreads / 64;
+constexpr int kBK = 128;
+constexpr int kBRows = 256;                  // weight rows per tile
+constexpr int kBBytes = kBRows * kBK;        // 32 KB
+constexpr int kStages = 3;
+
+typedef __attribute__((address_space(3))) void* lds_void_t;
+
+struct Args {
+    const uint8_t* a;
+    const float* a_scale;
+    int64_t sa_row;      // a_scale element strides (row, K block)
+    int64_t sa_kb;
+    int64_t sa_bytes;    // extent of a_scale in bytes
+    const uint8_t* w;
+    const float* w_scale;
+    const int32_t* sorted_ids;
+    const float* sorted_w;
+    const int32_t* sorted_eids;
+    const int32_t* num_valid;
+    uint8_t* a2;
+    float* a2_scale;
+    float* acc;
+    int K;
+    int N;           // weight rows per expert
+    int inter;
+    int topk;
+    int E;
+    int64_t a_rows;
+    int n_tiles;     // column tiles (grid = n_tiles * m_blocks)
+    int m_blocks;
+};
+
+// Buffer resource (base, byte size) for the LDS-DMA loads: word1 carries
+// the high address bits with stride 0; word3 is the raw-buffer config of
+// gfx9-class parts.
+struct Rsrc {
+    v4i w;
+};
+
+__device__ __forceinline__ Rsrc make_rsrc(const void* base, uint32_t bytes) {
+    const uint64_t p = reinterpret_cast<uint64_t>(base);
+    Rsrc r;
+    r.w = v4i{(int)(uint32_t)p, (int)(uint32_t)((p >> 32) & 0xFFFFu), (int)bytes, 0x00020000};
+    return r;
+}
+
+// Which 16-byte half of row r's 32-byte fragment slot holds K bytes 0-15.
+__device__ __forceinline__ int frag_swap(int r) { return ((r >> 2) ^ (r >> 3)) & 1; }
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)reinterpret_cast<uintptr_t>((lds_void_t)(void*)p);
+}
+
+// buffer_load_dword{x4} ... lds: each lane's 4 or 16 bytes at r + voff +
+// soff go to LDS at lds + lane * {4,16}.  Issued from inline asm, so the
+// compiler's wait-count pass does not see them (it would drain the whole
+// prefetch before every LDS read); the kernel waits for them itself with
+// an explicit s_waitcnt vmcnt(N) and issues no other vector loads in the
+// pipeline.  m0 holds the LDS base; nothing the compiler emits in this
+// kernel reads m0.
+__device__ __forceinline__ void dma16(const Rsrc& r, uint32_t voff, uint32_t soff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+                 :
+                 : "v"(voff), "s"(r.w), "s"(soff), "s"(lds)
+                 : "memory");
+}
+
+__device__ __forceinline__ void dma4(const Rsrc& r, uint32_t voff, uint32_t soff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dword %0, %1, %2 offen lds"
+                 :
+                 : "v"(voff), "s"(r.w), "s"(soff), "s"(lds)
+                 : "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <int BM>
+struct Tile {
+    static constexpr int NRT = BM / 32;                 // 16-row MFMA tiles per wave
+    static constexpr int A_BYTES = BM * kBK;
+    static constexpr int A_INSTR = BM * kBK / 1024 / kWaves;  // 1 KB DMA instructions per wave
+    static constexpr int B_INSTR = kBBytes / 1024 / kWaves;   // = 4 per wave
+    static constexpr int LOADS = A_INSTR + B_INSTR + 1; // DMA instructions per wave per step
+    static_assert(BM == 64 || BM == 128, "v2 tiles are 64 or 128 rows");
+    static_assert(A_INSTR >= 1, "every wave issues at least one A chunk");
+};
+
+template <int BM, int STAGE, bool SHUFFLED>
+__global__ __launch_bounds__(kThreads, 1) void moe_gemm_fp8bs_v2_kernel(Args g) {
+    using T = Tile<BM>;
+    constexpr int NRT = T::NRT;
+    constexpr int A_INSTR = T::A_INSTR;
+    constexpr int B_INSTR = T::B_INSTR;
+
+    __shared__ __attribute__((aligned(1024))) uint8_t s_a[kStages][T::A_BYTES];
+    __shared__ __attribute__((aligned(1024))) uint8_t s_b[kStages][kBBytes];
+    __shared__ __attribute__((aligned(16))) float s_sa[kStages][kThreads];
+    __shared__ int32_t s_arow[BM];
+    __shared__ int64_t s_orow[BM];
+    __shared__ float s_w[BM];
+    __shared__ float s_amax[4][BM];
+    __shared__ float s_sw[2][64];    // weight scales of the tile's two 128-row blocks per K block
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wv = tid >> 6;
+    const int wvu = __builtin_amdgcn_readfirstlane(wv);   // wave-uniform copy (scalar)
+    const int wm = wv >> 2;     // 0..1: row half
+    const int wn = wv & 3;      // 0..3: 64-column quarter of the weight tile
+    const int lr = lane & 15;
+    const int lq = lane >> 4;
+
+    // ---- XCD-aware tile order ----
+    const int L = blockIdx.x;
+    int nt, mb;
+    if ((g.n_tiles & 7) == 0) {
+        const int per = g.n_tiles >> 3;
+        const int xcd = L & 7;
+        const int idx = L >> 3;
+        nt = xcd * per + idx % per;
+        mb = idx / per;
+    } else {
+        nt = L % g.n_tiles;
+        mb = L / g.n_tiles;
+    }
+    if (mb >= g.m_blocks) return;
+    const int nvalid = g.num_valid[0];
+    if (mb * BM >= nvalid) return;
+    const int tokens = g.num_valid[1];
+    const int e = g.sorted_eids[mb];
+    if (e < 0 || e >= g.E) return;
+    const int n0 = STAGE == 1 ? nt * 128 : nt * 256;
+
+    for (int r = tid; r < BM; r += kThreads) {
+        const uint32_t id = (uint32_t)g.sorted_ids[mb * BM + r];
+        const int t = (int)(id & 0xFFFFFFu);
+        const int s = (int)(id >> 24);
+        const bool valid = t < tokens && s < g.topk;
+        const int64_t pair = (int64_t)t * g.topk + s;
+        int64_t arow = -1, orow = -1;
+        if (valid) {
+            arow = STAGE == 1 ? (int64_t)t : pair;
+            orow = STAGE == 1 ? pair : (int64_t)t;
+            if (arow >= g.a_rows) arow = orow = -1;
+        }
+        s_arow[r] = (int32_t)arow;
+        s_orow[r] = orow;
+        s_w[r] = STAGE == 2 && valid ? g.sorted_w[mb * BM + r] : 0.0f;
+    }
+
+    const int K = g.K;
+    const int KB = K / kBK;
+    const uint8_t* we = g.w + (int64_t)e * g.N * K;
+    const float* wse = g.w_scale + (int64_t)e * (g.N / 128) * KB;
+
+    // weight-scale block rows of the tile: stage 1 gate / up, stage 2 the two
+    // 128-column halves
+    const int nb0 = n0 / 128;
+    const int nb1 = STAGE == 1 ? (g.inter + n0) / 128 : n0 / 128 + 1;
+    for (int i = tid; i < 2 * KB; i += kThreads)
+        s_sw[i / KB][i % KB] = wse[(i < KB ? nb0 : nb1) * KB + (i % KB)];
+    const int swsel0 = STAGE == 1 ? 0 : (wn >> 1);
+    const int swsel1 = STAGE == 1 ? 1 : (wn >> 1);
+    __syncthreads();
+
+    // ---- per-lane DMA sources (byte offsets; the K step goes in soffset) ----
+    uint32_t a_off[A_INSTR];
+#pragma unroll
+    for (int i = 0; i < A_INSTR; ++i) {   // 1 KB chunk c: rows r0..r0+31 of quarter kq
+        const int c = wvu * A_INSTR + i;
+        const int kq = c / (BM / 32);
+        const int row = (c % (BM / 32)) * 32 + (lane >> 1);
+        const int h = (lane & 1) ^ frag_swap(row);
+        int arow = s_arow[row];
+        if (arow < 0) arow = 0;           // pad rows: any valid row, result unused
+        a_off[i] = (uint32_t)arow * (uint32_t)K + (uint32_t)(kq * 32 + h * 16);
+    }
+    uint32_t b_off[B_INSTR];
+#pragma unroll
+    for (int i = 0; i < B_INSTR; ++i) {   // 1 KB chunk: half of a 16-row group, slot kq*32+rr*2+h
+        const int chunk = wvu * B_INSTR + i;   // 32 chunks of 1 KB
+        const int grp = chunk >> 1;
+        const int slot = (chunk & 1) * 64 + lane;
+        const int kq = slot >> 5, rr = (slot >> 1) & 15, h = (slot & 1) ^ frag_swap(rr);
+        int row0;
+        if (STAGE == 1)
+            row0 = grp < 8 ? n0 + 16 * grp : g.inter + n0 + 16 * (grp - 8);
+        else
+            row0 = n0 + 16 * grp;
+        if (SHUFFLED)   // (16,16) layout: [K/32][h][row 16][16 B] per 16-row group
+            b_off[i] = (uint32_t)row0 * (uint32_t)K + (uint32_t)(kq * 512 + h * 256 + rr * 16);
+        else
+            b_off[i] = (uint32_t)(row0 + rr) * (uint32_t)K + (uint32_t)(kq * 32 + h * 16);
+    }
+    uint32_t sa_off;                      // lane's scale: row tid (rows >= BM re-read row 0)
+    {
+        int arow = tid < BM ? s_arow[tid] : 0;
+        if (arow < 0) arow = 0;
+        sa_off = (uint32_t)((int64_t)arow * g.sa_row * 4);
+    }
+    const Rsrc ra = make_rsrc(g.a, (uint32_t)(g.a_rows * K));
+    const Rsrc rb = make_rsrc(we, (uint32_t)((int64_t)g.N * K));
+    const Rsrc rs = make_rsrc(g.a_scale, (uint32_t)g.sa_bytes);
+    const uint32_t sa_kb_bytes = (uint32_t)(g.sa_kb * 4);
+
+    auto issue = [&](int kb, int stage) {
+        kb = kb < KB ? kb : KB - 1;       // past the end: repeat the last step (keeps counts uniform)
+        const uint32_t aoff = (uint32_t)kb * kBK;
+#pragma unroll
+        for (int i = 0; i < A_INSTR; ++i)
+            dma16(ra, a_off[i], aoff, lds_addr(&s_a[stage][(wvu * A_INSTR + i) * 1024]));
+        const uint32_t boff = SHUFFLED ? (uint32_t)kb * 2048u : (uint32_t)kb * kBK;
+#pragma unroll
+        for (int i = 0; i < B_INSTR; ++i)
+            dma16(rb, b_off[i], boff, lds_addr(&s_b[stage][(wvu * B_INSTR + i) * 1024]));
+        dma4(rs, sa_off, (uint32_t)kb * sa_kb_bytes, lds_addr(&s_sa[stage][wvu * 64]));
+    };
+
+    v4f acc[NRT][4];
+#pragma unroll
+    for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct) acc[rt][ct] = v4f{0.f, 0.f, 0.f, 0.f};
+    const int row_base = wm * (BM / 2);
+    const int h0 = frag_swap(lr);
+
+    // One K step of the wave's (BM/2) x 128 tile, software-pipelined across
+    // column tiles: the NRT MFMAs of tile c+1 go into the other of two
+    // temporary sets while the VALU folds tile c's results into the
+    // accumulators (acc += blk * a_scale * w_scale), so the MFMA pipe never
+    // waits for the block-scale FMAs.  The combined scales of the half
+    // (gate / up, or the wave's stage-2 block) are recomputed per half.
+    auto compute = [&](int kb, int stage) {
+        const uint8_t* sa_src = &s_a[stage][0];
+        const uint8_t* sb_src = &s_b[stage][0];
+        // fragment = K bytes 0-15 from half h0, 16-31 from half h0^1 (h0 depends
+        // only on lr: row_base and rt*16 are multiples of 16)
+        auto frag = [&](const uint8_t* slot) {
+            const v4i lo = *reinterpret_cast<const v4i*>(slot + h0 * 16);
+            const v4i hi = *reinterpret_cast<const v4i*>(slot + (h0 ^ 1) * 16);
+            return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        };
+        v8i afrag[NRT];
+#pragma unroll
+        for (int rt = 0; rt < NRT; ++rt) {
+            const int row = row_base + rt * 16 + lr;
+            afrag[rt] = frag(sa_src + lq * (BM * 32) + row * 32);
+        }
+        // column tile ct (0..3) -> 16-row weight group: stage 1 tiles 0,1 are gate
+        // rows, 2,3 the matching up rows; stage 2 four consecutive groups
+        auto bfrag_at = [&](int ct) {
+            int grp;
+            if (STAGE == 1)
+                grp = ct < 2 ? wn * 2 + ct : 8 + wn * 2 + (ct - 2);
+            else
+                grp = wn * 4 + ct;
+            return frag(sb_src + grp * 2048 + lq * 512 + lr * 32);
+        };
+        float sc[NRT][4];
+        auto load_scales = [&](int half) {
+            const float sw = s_sw[half == 0 ? swsel0 : swsel1][kb];
+#pragma unroll
+            for (int rt = 0; rt < NRT; ++rt) {
+                const v4f s4 = *reinterpret_cast<const v4f*>(&s_sa[stage][row_base + rt * 16 + 4 * lq]);
+#pragma unroll
+                for (int v = 0; v < 4; ++v) sc[rt][v] = s4[v] * sw;
+            }
+        };
+        v4f blk[2][NRT];
+        v8i bfrag = bfrag_at(0);
+#pragma unroll
+        for (int rt = 0; rt < NRT; ++rt) blk[0][rt] = mfma16x16x128_fp8(afrag[rt], bfrag);
+        load_scales(0);
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct) {
+            const int cur = ct & 1;
+            if (ct + 1 < 4) {
+                bfrag = bfrag_at(ct + 1);
+#pragma unroll
+                for (int rt = 0; rt < NRT; ++rt)
+                    blk[cur ^ 1][rt] = mfma16x16x128_fp8(afrag[rt], bfrag);
+            }
+#pragma unroll
+            for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc[rt][ct][v] += blk[cur][rt][v] * sc[rt][v];
+            if (ct == 1 && STAGE == 1) load_scales(1);
+#pragma unroll
+            for (int i = 0; i < NRT; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // VALU
+            }
+        }
+    };
+
+    // ---- pipeline: the prologue fills two stages; step k waits for its own
+    // loads (the next step's may stay in flight), syncs, refills the stage
+    // step k-1 used, computes.  One loop body with a rotating stage index
+    // keeps the accumulators in fixed registers. ----
+    issue(0, 0);
+    issue(1, 1);
+    int cs = 0;                           // stage buffer of step kb
+    for (int kb = 0; kb < KB; ++kb) {
+        wait_vm<T::LOADS>();
+        __syncthreads();
+        const int ls = cs == 0 ? kStages - 1 : cs - 1;   // buffer step kb-1 used
+        issue(kb + kStages - 1, ls);
+        compute(kb, cs);
+        cs = cs == kStages - 1 ? 0 : cs + 1;
+    }
+    wait_vm<0>();
+    __syncthreads();
+
+    if (STAGE == 2) {
+#pragma unroll
+        for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int row = row_base + rt * 16 + 4 * lq + v;
+                const int64_t t = s_orow[row];
+                if (t < 0) continue;
+                const float wgt = s_w[row];
+                float* dst = g.acc + t * g.N + n0 + wn * 64 + lr;
+#pragma unroll
+                for (int ct = 0; ct < 4; ++ct) unsafeAtomicAdd(dst + ct * 16, acc[rt][ct][v] * wgt);
+            }
+        return;
+    }
+
+    // ---- stage 1 epilogue: silu(gate)*up -> bf16 -> 1x128 fp8 requant ----
+    // wave wn holds output columns wn*32 + j*16 + lr (j = 0, 1) of the tile's 128
+    float h[NRT][2][4];
+#pragma unroll
+    for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+                h[rt][j][v] = bf16_round(silu_f32(acc[rt][j][v]) * acc[rt][2 + j][v]);
+#pragma unroll
+    for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            float m = __builtin_fmaxf(__builtin_fabsf(h[rt][0][v]), __builtin_fabsf(h[rt][1][v]));
+            m = warp_max_16(m);
+            if (lr == 0) s_amax[wn][row_base + rt * 16 + 4 * lq + v] = m;
+        }
+    __syncthreads();
+    auto row_amax = [&](int row) {
+        const float m = __builtin_fmaxf(__builtin_fmaxf(s_amax[0][row], s_amax[1][row]),
+                                        __builtin_fmaxf(s_amax[2][row], s_amax[3][row]));
+        return __builtin_fmaxf(m, 1e-10f);
+    };
+    uint8_t* s_q = &s_a[0][0];  // [BM][128] fp8 staging (the pipeline is drained)
+#pragma unroll
+    for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int row = row_base + rt * 16 + 4 * lq + v;
+            const float inv = 1.0f / (row_amax(row) * kInvFp8Max);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const uint32_t b = f32x2_to_fp8x2(h[rt][j][v] * inv, 0.0f) & 0xFFu;
+                s_q[row * kBK + wn * 32 + j * 16 + lr] = (uint8_t)b;
+            }
+        }
+    __syncthreads();
+    const int I = g.inter;
+    for (int q = tid; q < BM * 8; q += kThreads) {
+        const int row = q >> 3, part = q & 7;
+        const int64_t orow = s_orow[row];
+        if (orow < 0) continue;
+        *reinterpret_cast<v4i*>(g.a2 + orow * I + n0 + part * 16) =
+            *reinterpret_cast<const v4i*>(s_q + row * kBK + part * 16);
+        if (part == 0) g.a2_scale[orow * (I / 128) + n0 / 128] = row_amax(row) * kInvFp8Max;
+    }
+}
+
+template <int STAGE, bool SHUFFLED>
+static void launch_bm(int bm, int grid, Args& a, hipStream_t stream) {
+    if (bm == 64)
+        hipLaunchKernelGGL((moe_gemm_fp8bs_v2_kernel<64, STAGE, SHUFFLED>), dim3(grid),
+                           dim3(kThreads), 0, stream, a);
+    else if (bm == 128)
+        hipLaunchKernelGGL((moe_gemm_fp8bs_v2_kernel<128, STAGE, SHUFFLED>), dim3(grid),
+                           dim3(kThreads), 0, stream, a);
+    else
+        AMD_CHECK(false, "v2 GEMM block_m must be 64 or 128");
+}
+
+static int64_t scale_bytes(int64_t rows, int64_t KB, int64_t sa_row, int64_t sa_kb) {
+    return ((rows - 1) * sa_row + (KB - 1) * sa_kb + 1) * 4;
+}
+
+}  // namespace v2
+
+bool v2_supported(int64_t block_m, int64_t K) {
+    return (block_m == 64 || block_m == 128) && K > 0 && K % 128 == 0 && K / 128 <= 64;
+}
+
+void launch_moe_stage1_fp8bs_v2(const uint8_t* a, const float* a_scale, int64_t sa_row,
+                                int64_t sa_kb, const uint8_t* w1, const float* w1_scale,
+                                const int32_t* sorted_ids, const int32_t* sorted_eids,
+                                const int32_t* num_valid, uint8_t* a2, float* a2_scale,
+                                int64_t a_rows, int64_t K, int64_t inter, int64_t E, int64_t topk,
+                                int64_t block_m, int64_t max_m_blocks, int shuffled,
+                                hipStream_t stream) {
+    v2::Args g{};
+    g.a = a;
+    g.a_scale = a_scale;
+    g.sa_row = sa_row;
+    g.sa_kb = sa_kb;
+    g.sa_bytes = v2::scale_bytes(a_rows, K / 128, sa_row, sa_kb);
+    g.w = w1;
+    g.w_scale = w1_scale;
+    g.sorted_ids = sorted_ids;
+    g.sorted_eids = sorted_eids;
+    g.num_valid = num_valid;
+    g.a2 = a2;
+    g.a2_scale = a2_scale;
+    g.K = (int)K;
+    g.N = (int)(2 * inter);
+    g.inter = (int)inter;
+    g.topk = (int)topk;
+    g.E = (int)E;
+    g.a_rows = a_rows;
+    g.n_tiles = (int)(inter / 128);
+    g.m_blocks = (int)max_m_blocks;
+    AMD_CHECK(a_rows * K < (1ll << 32) && 2 * inter * K < (1ll << 32) &&
+                  g.sa_bytes < (1ll << 32),
+              "v2 GEMM needs 32-bit buffer offsets");
+    const int64_t grid = (int64_t)g.n_tiles * max_m_blocks;
+    if (grid == 0) return;
+    if (shuffled)
+        v2::launch_bm<1, true>((int)block_m, (int)grid, g, stream);
+    else
+        v2::launch_bm<1, false>((int)block_m, (int)grid, g, stream);
+    AMD_HIP_CHECK(hipGetLastError());
+}
+
+void launch_moe_stage2_fp8bs_v2(const uint8_t* a2, const float* a2_scale, const uint8_t* w2,
+                                const float* w2_scale, const int32_t* sorted_ids,
+                                const float* sorted_w, const int32_t* sorted_eids,
+                                const int32_t* num_valid, float* acc, int64_t a_rows,
+                                int64_t inter, int64_t hidden, int64_t E, int64_t topk,
+                                int64_t block_m, int64_t max_m_blocks, int shuffled,
+                                hipStream_t stream) {
+    v2::Args g{};
+    g.a = a2;
+    g.a_scale = a2_scale;
+    g.sa_row = inter / 128;
+    g.sa_kb = 1;
+    g.sa_bytes = v2::scale_bytes(a_rows, inter / 128, g.sa_row, g.sa_kb);
+    g.w = w2;
+    g.w_scale = w2_scale;
+    g.sorted_ids = sorted_ids;
+    g.sorted_w = sorted_w;
+    g.sorted_eids = sorted_eids;
+    g.num_valid = num_valid;
+    g.acc = acc;
+    g.K = (int)inter;
+    g.N = (int)hidden;
+    g.inter = (int)inter;
+    g.topk = (int)topk;
+    g.E = (int)E;
+    g.a_rows = a_rows;
+    g.n_tiles = (int)(hidden / 256);
+    g.m_blocks = (int)max_m_blocks;
+    AMD_CHECK(a_rows * inter < (1ll << 32) && hidden * inter < (1ll << 32) &&
+                  g.sa_bytes < (1ll << 32),
+              "v2 GEMM needs 32-bit buffer offsets");
+    const int64_t grid = (int64_t)g.n_tiles * max_m_blocks;
+    if (grid == 0) return;
+    if (shuffled)
+        v2::launch_bm<2, true>((int)block_m, (int)grid, g, stream);
+    else
+        v2::launch_bm<2, false>((int)block_m, (int)grid, g, stream);
+    AMD_HIP_CHECK(hipGetLastError());
+}
+
+}  // namespace aiter_amd

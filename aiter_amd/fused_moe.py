@@ -95,8 +95,10 @@ def get_inter_dim(w1_shape, w2_shape):
     return E, model_dim, inter_dim
 
 
-def default_block_m(tokens: int, topk: int, num_experts: int) -> int:
-    return _abi.query("aiter_amd_default_block_m", tokens, topk, num_experts)
+def default_block_m(tokens: int, topk: int, num_experts: int, model_dim: int = 0,
+                    inter_dim: int = 0) -> int:
+    """M-block for a layer; model_dim/inter_dim 0 rule out 128-row tiles."""
+    return _abi.query("aiter_amd_default_block_m", tokens, topk, num_experts, model_dim, inter_dim)
 
 
 def fused_moe(
@@ -199,7 +201,7 @@ def fused_moe_(hidden_states, w1, w2, topk_weight, topk_ids, expert_mask=None,
         raise ValueError("w1 and w2 must both be shuffled or both be plain")
     global_E = expert_mask.numel() if expert_mask is not None else E
     block_m = int(block_size_M) if block_size_M not in (None, -1) else default_block_m(
-        M, topk, E)
+        M, topk, E, model_dim, inter_dim)
     device = topk_ids.device
     topk_ids = topk_ids.to(torch.int32).contiguous()
     topk_weight = topk_weight.to(torch.float32).contiguous()

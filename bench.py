@@ -36,6 +36,7 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-decode", action="store_true")
     p.add_argument("--kernel-iters", type=int, default=10)
+    p.add_argument("--block-m", type=int, default=0, help="override the M-block (0 = default)")
     p.add_argument("--kernel-only", choices=["stage1", "stage2"], default=None,
                    help="profiling mode: run a 256 MiB device copy (counter calibration) "
                         "then only this kernel --steps times")
@@ -59,12 +60,13 @@ def make_cfg(name):
 class Layer:
     """Inputs of one MoE layer resident on the GPU."""
 
-    def __init__(self, cfg, dev):
+    def __init__(self, cfg, dev, block_m=0):
         import torch
 
         from aiter_amd import workloads as W
 
         self.cfg = cfg
+        self.block_m = block_m
         self.dev = dev
         self.w = W.make_weights(cfg, device=dev, shuffle=True)
         self.x = W.make_hidden(cfg, device=dev)
@@ -85,7 +87,8 @@ class Layer:
 
         return A.fused_moe(self.x, self.w["w1"], self.w["w2"], self.tw, self.ids,
                            expert_mask=self.mask, quant_type=A.QuantType.per_128x128,
-                           w1_scale=self.w["w1_scale"], w2_scale=self.w["w2_scale"])
+                           w1_scale=self.w["w1_scale"], w2_scale=self.w["w2_scale"],
+                           block_size_M=self.block_m or None)
 
 
 def time_steps(fn, steps, warmup):
@@ -115,7 +118,8 @@ def stage_kernel_times(layer, iters):
     import aiter_amd as A
 
     cfg = layer.cfg
-    bm = A.default_block_m(cfg.tokens, cfg.topk, cfg.local_experts or cfg.experts)
+    bm = layer.block_m or A.default_block_m(cfg.tokens, cfg.topk, cfg.local_experts or cfg.experts,
+                                          cfg.model_dim, cfg.inter_dim)
     E_sort = cfg.experts
     sid, sw, se, nv, acc = A.moe_sorting(layer.ids, layer.tw, E_sort, cfg.model_dim,
                                          torch.float32, bm, layer.mask)
@@ -159,7 +163,8 @@ def kernel_only(layer, which, steps):
     for _ in range(3):
         dst.copy_(src)
     cfg = layer.cfg
-    bm = A.default_block_m(cfg.tokens, cfg.topk, cfg.local_experts or cfg.experts)
+    bm = layer.block_m or A.default_block_m(cfg.tokens, cfg.topk, cfg.local_experts or cfg.experts,
+                                          cfg.model_dim, cfg.inter_dim)
     sid, sw, se, nv, acc = A.moe_sorting(layer.ids, layer.tw, cfg.experts, cfg.model_dim,
                                          torch.float32, bm, layer.mask)
     a1, a1s = A.per_group_quant_hip(layer.x)
@@ -279,7 +284,7 @@ def main():
     dev = torch.device("cuda:0")
     cfg = make_cfg(args.workload)
     log(f"building {cfg.name} inputs")
-    layer = Layer(cfg, dev)
+    layer = Layer(cfg, dev, args.block_m)
     if args.kernel_only:
         kernel_only(layer, args.kernel_only, args.steps)
         return

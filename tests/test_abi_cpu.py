@@ -78,8 +78,10 @@ def test_stage_validation_errors():
     args = [16, 16, 0, 16, 16, 16, 16, 16, 16, 16]
     _expect_error("aiter_amd_moe_stage1_fp8_blockscale", *args, 4, 4096, 2000, 8, 2, 32, 10, 0, 1,
                   None, match="inter_dim must be")
-    _expect_error("aiter_amd_moe_stage1_fp8_blockscale", *args, 4, 4096, 2048, 8, 2, 128, 10, 0,
-                  1, None, match="block_m must be 16, 32 or 64")
+    _expect_error("aiter_amd_moe_stage1_fp8_blockscale", *args, 4, 4096, 2048, 8, 2, 256, 10, 0,
+                  1, None, match="block_m must be 16, 32, 64 or 128")
+    _expect_error("aiter_amd_moe_stage1_fp8_blockscale", *args, 4, 4224, 1152, 8, 2, 128, 10, 0,
+                  1, None, match="block_m 128 needs")
     _expect_error("aiter_amd_moe_stage1_fp8_blockscale", *args, 4, 4096, 2048, 8, 2, 32, 10, 1, 1,
                   None, match="Silu")
     _expect_error("aiter_amd_moe_stage2_fp8_blockscale", 16, 16, 16, 16, 16, 16, 16, 16, 16, 4,
@@ -100,9 +102,14 @@ def test_fused_validation_errors(lib):
 
 
 def test_default_block_m(lib):
-    assert lib.aiter_amd_default_block_m(1, 8, 256) == 16
-    assert lib.aiter_amd_default_block_m(32, 8, 256) == 16
-    assert lib.aiter_amd_default_block_m(8192, 8, 256) == 64
+    assert lib.aiter_amd_default_block_m(1, 8, 256, 4096, 2048) == 16
+    assert lib.aiter_amd_default_block_m(32, 8, 256, 4096, 2048) == 16
+    assert lib.aiter_amd_default_block_m(1024, 8, 256, 4096, 2048) == 32
+    assert lib.aiter_amd_default_block_m(2048, 8, 256, 4096, 2048) == 64
+    assert lib.aiter_amd_default_block_m(8192, 8, 256, 4096, 2048) == 128
+    # 128-row tiles need model_dim % 256 == 0 and dims <= 8192
+    assert lib.aiter_amd_default_block_m(8192, 8, 256, 4224, 2048) == 64
+    assert lib.aiter_amd_default_block_m(8192, 8, 256, 0, 0) == 64
 
 
 def test_python_layer_rejects_unsupported_modes():

@@ -137,7 +137,7 @@ def _check(ref_out, got, tag):
 
 
 @pytest.mark.parametrize("shuffle", [True, False])
-@pytest.mark.parametrize("bm", [16, 32, 64])
+@pytest.mark.parametrize("bm", [16, 32, 64, 128])
 def test_fused_moe_config_a(cuda_device, shuffle, bm):
     cfg = W.CONFIG_A
     dev, ref = _make_layer(cfg, cuda_device, shuffle)
