@@ -1,5 +1,6 @@
 """aiter_amd: MI355X (gfx950) blockscale fused-MoE, a drop-in for
-aiter.fused_moe's FP8 block-scale path.
+aiter.fused_moe's FP8 block-scale path and its A8W4 (fp8 activations x MXFP4
+weights, quant_type=per_1x32) variant.
 
     from aiter_amd import fused_moe, QuantType, ActivationType
     out = fused_moe(x, w1, w2, topk_weight, topk_ids,
@@ -17,17 +18,27 @@ from .fused_moe import (
     fused_moe_fake,
     get_inter_dim,
     moe_sorting,
+    moe_stage1_a8w4,
     moe_stage1_fp8_blockscale,
+    moe_stage2_a8w4,
     moe_stage2_fp8_blockscale,
     sorted_capacity,
 )
-from .quant import dynamic_per_token_scaled_quant, per_group_quant_hip, quant_weight_per_128x128
+from .quant import (
+    dynamic_per_token_scaled_quant,
+    e8m0_to_f32,
+    f32_to_e8m0,
+    per_1x32_f4_quant,
+    per_group_quant_hip,
+    quant_weight_per_128x128,
+)
 from .shuffle import shuffle_weight, unshuffle_weight
 
 __all__ = [
     "ActivationType", "QuantType", "dtypes", "quant_remap", "BLOCK_SIZE_M", "default_block_m",
     "fused_moe", "fused_moe_", "fused_moe_fake", "get_inter_dim", "moe_sorting",
-    "moe_stage1_fp8_blockscale", "moe_stage2_fp8_blockscale", "sorted_capacity",
-    "dynamic_per_token_scaled_quant", "per_group_quant_hip", "quant_weight_per_128x128",
+    "moe_stage1_fp8_blockscale", "moe_stage2_fp8_blockscale", "moe_stage1_a8w4",
+    "moe_stage2_a8w4", "sorted_capacity", "dynamic_per_token_scaled_quant", "per_group_quant_hip",
+    "quant_weight_per_128x128", "per_1x32_f4_quant", "f32_to_e8m0", "e8m0_to_f32",
     "shuffle_weight", "unshuffle_weight",
 ]

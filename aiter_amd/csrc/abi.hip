@@ -23,52 +23,62 @@ void launch_moe_sort(const int32_t*, const float*, const int32_t*, const int32_t
 void launch_per_group_quant_fp8(const void*, int, void*, float*, int64_t, int64_t, int,
                                 const int32_t*, int64_t, hipStream_t);
 void launch_acc_to_out(const float*, void*, int, const int32_t*, int64_t, int64_t, hipStream_t);
+// The GEMM launchers take the weight scales either as fp32 128x128 blocks
+// (FP8 weights) or, when the e8m0 pointer is non-null, as e8m0 bytes per
+// 1x32 K block (MXFP4 weights, A8W4).
 void launch_moe_stage1_fp8bs(const uint8_t*, const float*, int64_t, int64_t, const uint8_t*,
-                             const float*, const int32_t*, const int32_t*, const int32_t*,
-                             uint8_t*, float*, int64_t, int64_t, int64_t, int64_t, int64_t,
-                             int64_t, int64_t, int, hipStream_t);
+                             const float*, const uint8_t*, const int32_t*, const int32_t*,
+                             const int32_t*, uint8_t*, float*, int64_t, int64_t, int64_t, int64_t,
+                             int64_t, int64_t, int64_t, int, hipStream_t);
 void launch_moe_stage2_fp8bs(const uint8_t*, const float*, const uint8_t*, const float*,
-                             const int32_t*, const float*, const int32_t*, const int32_t*,
-                             float*, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t,
-                             int64_t, int, hipStream_t);
+                             const uint8_t*, const int32_t*, const float*, const int32_t*,
+                             const int32_t*, float*, int64_t, int64_t, int64_t, int64_t, int64_t,
+                             int64_t, int64_t, int, hipStream_t);
 // moe_gemm_fp8bs_v2.hip (64/128-row M-blocks)
 bool v2_supported(int64_t block_m, int64_t K);
 void launch_moe_stage1_fp8bs_v2(const uint8_t*, const float*, int64_t, int64_t, const uint8_t*,
-                                const float*, const int32_t*, const int32_t*, const int32_t*,
-                                uint8_t*, float*, int64_t, int64_t, int64_t, int64_t, int64_t,
-                                int64_t, int64_t, int, hipStream_t);
+                                const float*, const uint8_t*, const int32_t*, const int32_t*,
+                                const int32_t*, uint8_t*, float*, int64_t, int64_t, int64_t,
+                                int64_t, int64_t, int64_t, int64_t, int, hipStream_t);
 void launch_moe_stage2_fp8bs_v2(const uint8_t*, const float*, const uint8_t*, const float*,
-                                const int32_t*, const float*, const int32_t*, const int32_t*,
-                                float*, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t,
-                                int64_t, int, hipStream_t);
+                                const uint8_t*, const int32_t*, const float*, const int32_t*,
+                                const int32_t*, float*, int64_t, int64_t, int64_t, int64_t,
+                                int64_t, int64_t, int64_t, int, hipStream_t);
+
+// Weight scales of one layer: fp32 128x128 blocks (fp8 weights) or e8m0
+// bytes per 1x32 K block (MXFP4 weights); exactly one is set.
+struct WScale {
+    const float* f32;
+    const uint8_t* e8m0;
+};
 
 // Kernel choice per shape: M-blocks of 64/128 rows with K a multiple of 256
 // (and, for stage 2, 256-column output tiles) take the large-tile
 // direct-to-LDS kernels; 16/32-row blocks (decode) the streaming kernels.
 static void stage1_dispatch(const uint8_t* a, const float* sa, int64_t sa_row, int64_t sa_kb,
-                            const uint8_t* w1, const float* w1s, const int32_t* sid,
+                            const uint8_t* w1, WScale w1s, const int32_t* sid,
                             const int32_t* seid, const int32_t* nv, uint8_t* a2, float* a2s,
                             int64_t a_rows, int64_t K, int64_t I, int64_t E, int64_t topk,
                             int64_t bm, int64_t mblocks, int sh, hipStream_t s) {
     if (v2_supported(bm, K))
-        launch_moe_stage1_fp8bs_v2(a, sa, sa_row, sa_kb, w1, w1s, sid, seid, nv, a2, a2s, a_rows,
-                                   K, I, E, topk, bm, mblocks, sh, s);
+        launch_moe_stage1_fp8bs_v2(a, sa, sa_row, sa_kb, w1, w1s.f32, w1s.e8m0, sid, seid, nv, a2,
+                                   a2s, a_rows, K, I, E, topk, bm, mblocks, sh, s);
     else
-        launch_moe_stage1_fp8bs(a, sa, sa_row, sa_kb, w1, w1s, sid, seid, nv, a2, a2s, a_rows, K,
-                                I, E, topk, bm, mblocks, sh, s);
+        launch_moe_stage1_fp8bs(a, sa, sa_row, sa_kb, w1, w1s.f32, w1s.e8m0, sid, seid, nv, a2,
+                                a2s, a_rows, K, I, E, topk, bm, mblocks, sh, s);
 }
 
 static void stage2_dispatch(const uint8_t* a2, const float* a2s, const uint8_t* w2,
-                            const float* w2s, const int32_t* sid, const float* sw,
+                            WScale w2s, const int32_t* sid, const float* sw,
                             const int32_t* seid, const int32_t* nv, float* acc, int64_t a_rows,
                             int64_t I, int64_t H, int64_t E, int64_t topk, int64_t bm,
                             int64_t mblocks, int sh, hipStream_t s) {
     if (v2_supported(bm, I) && H % 256 == 0)
-        launch_moe_stage2_fp8bs_v2(a2, a2s, w2, w2s, sid, sw, seid, nv, acc, a_rows, I, H, E, topk,
-                                   bm, mblocks, sh, s);
+        launch_moe_stage2_fp8bs_v2(a2, a2s, w2, w2s.f32, w2s.e8m0, sid, sw, seid, nv, acc, a_rows,
+                                   I, H, E, topk, bm, mblocks, sh, s);
     else
-        launch_moe_stage2_fp8bs(a2, a2s, w2, w2s, sid, sw, seid, nv, acc, a_rows, I, H, E, topk, bm,
-                                mblocks, sh, s);
+        launch_moe_stage2_fp8bs(a2, a2s, w2, w2s.f32, w2s.e8m0, sid, sw, seid, nv, acc, a_rows, I,
+                                H, E, topk, bm, mblocks, sh, s);
 }
 
 namespace {
@@ -156,6 +166,114 @@ int64_t default_block_m(int64_t tokens, int64_t topk, int64_t E, int64_t model_d
         model_dim % 256 == 0)
         return 128;
     return 64;
+}
+
+void check_e8m0(const uint8_t* p, const char* name) {
+    AMD_CHECK(p != nullptr, std::string(name) + " is NULL");
+    AMD_CHECK((reinterpret_cast<uintptr_t>(p) & 3u) == 0,
+              std::string(name) + " is not 4-byte aligned");
+}
+
+void stage1_entry(const void* a1, const float* a1_scale, int64_t a1_scale_transposed,
+                  const void* w1, WScale w1s, const int32_t* sorted_ids,
+                  const int32_t* sorted_expert_ids, const int32_t* num_valid_ids, void* a2,
+                  float* a2_scale, int64_t tokens, int64_t model_dim, int64_t inter_dim,
+                  int64_t num_experts, int64_t topk, int64_t block_m, int64_t max_m_blocks,
+                  int64_t activation, int64_t w_shuffled, void* stream) {
+    check_dims(model_dim, inter_dim);
+    check_topk_experts(tokens, topk, num_experts);
+    check_block_m_gemm(block_m, model_dim, inter_dim);
+    AMD_CHECK(activation == 0, "only ActivationType.Silu (0) is supported, got " +
+                                   std::to_string(activation));
+    AMD_CHECK(max_m_blocks >= 0, "max_m_blocks must be >= 0");
+    if (tokens == 0 || max_m_blocks == 0) return;
+    check_ptr(a1, "a1");
+    check_ptr(w1, "w1");
+    check_ptr(a2, "a2");
+    AMD_CHECK(a1_scale && a2_scale && sorted_ids && sorted_expert_ids && num_valid_ids,
+              "a required pointer is NULL");
+    const int64_t KB = model_dim / 128;
+    const int64_t sa_row = a1_scale_transposed ? 1 : KB;
+    const int64_t sa_kb = a1_scale_transposed ? tokens : 1;
+    stage1_dispatch((const uint8_t*)a1, a1_scale, sa_row, sa_kb, (const uint8_t*)w1, w1s,
+                    sorted_ids, sorted_expert_ids, num_valid_ids, (uint8_t*)a2, a2_scale, tokens,
+                    model_dim, inter_dim, num_experts, topk, block_m, max_m_blocks,
+                    (int)(w_shuffled != 0), (hipStream_t)stream);
+}
+
+void stage2_entry(const void* a2, const float* a2_scale, const void* w2, WScale w2s,
+                  const int32_t* sorted_ids, const float* sorted_weights,
+                  const int32_t* sorted_expert_ids, const int32_t* num_valid_ids, float* out_acc,
+                  int64_t tokens, int64_t model_dim, int64_t inter_dim, int64_t num_experts,
+                  int64_t topk, int64_t block_m, int64_t max_m_blocks, int64_t w_shuffled,
+                  void* stream) {
+    check_dims(model_dim, inter_dim);
+    check_topk_experts(tokens, topk, num_experts);
+    check_block_m_gemm(block_m, model_dim, inter_dim);
+    AMD_CHECK(max_m_blocks >= 0, "max_m_blocks must be >= 0");
+    if (tokens == 0 || max_m_blocks == 0) return;
+    check_ptr(a2, "a2");
+    check_ptr(w2, "w2");
+    check_ptr(out_acc, "out_acc");
+    AMD_CHECK(a2_scale && sorted_ids && sorted_weights && sorted_expert_ids && num_valid_ids,
+              "a required pointer is NULL");
+    stage2_dispatch((const uint8_t*)a2, a2_scale, (const uint8_t*)w2, w2s, sorted_ids,
+                    sorted_weights, sorted_expert_ids, num_valid_ids, out_acc, tokens * topk,
+                    inter_dim, model_dim, num_experts, topk, block_m, max_m_blocks,
+                    (int)(w_shuffled != 0), (hipStream_t)stream);
+}
+
+void fused_entry(const void* hidden_states, int hidden_dtype, const void* w1, WScale w1s,
+                 const void* w2, WScale w2s, const float* topk_weights, const int32_t* topk_ids,
+                 const int32_t* expert_mask, const int32_t* num_local_tokens, void* out,
+                 int out_dtype, int64_t tokens, int64_t model_dim, int64_t inter_dim,
+                 int64_t num_experts, int64_t global_experts, int64_t topk, int64_t block_m,
+                 int64_t w_shuffled, void* workspace, int64_t workspace_bytes, void* stream) {
+    check_dims(model_dim, inter_dim);
+    check_topk_experts(tokens, topk, num_experts);
+    AMD_CHECK(hidden_dtype == DT_BF16 || hidden_dtype == DT_FP16,
+              "hidden_states dtype must be bf16 or fp16");
+    AMD_CHECK(out_dtype == DT_BF16 || out_dtype == DT_FP16, "out dtype must be bf16 or fp16");
+    const int64_t E_sort = expert_mask ? global_experts : num_experts;
+    AMD_CHECK(E_sort >= num_experts && E_sort <= kMaxExperts,
+              "global_experts must be in [num_experts, 4096]");
+    if (block_m <= 0) block_m = default_block_m(tokens, topk, num_experts, model_dim, inter_dim);
+    check_block_m_gemm(block_m, model_dim, inter_dim);
+    if (tokens == 0) return;
+    check_ptr(hidden_states, "hidden_states");
+    check_ptr(w1, "w1");
+    check_ptr(w2, "w2");
+    check_ptr(out, "out");
+    AMD_CHECK(topk_weights && topk_ids, "a required pointer is NULL");
+    const FusedLayout L = fused_layout(tokens, model_dim, inter_dim, E_sort, topk, block_m);
+    check_ptr(workspace, "workspace");
+    AMD_CHECK(workspace_bytes >= L.total, "workspace of " + std::to_string(L.total) +
+                                              " bytes required, got " +
+                                              std::to_string(workspace_bytes));
+    uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
+    int32_t* sorted_ids = reinterpret_cast<int32_t*>(ws + L.off_sorted_ids);
+    float* sorted_w = reinterpret_cast<float*>(ws + L.off_sorted_w);
+    int32_t* sorted_eids = reinterpret_cast<int32_t*>(ws + L.off_sorted_eids);
+    int32_t* num_valid = reinterpret_cast<int32_t*>(ws + L.off_num_valid);
+    uint8_t* a1 = ws + L.off_a1;
+    float* a1_scale = reinterpret_cast<float*>(ws + L.off_a1_scale);
+    uint8_t* a2 = ws + L.off_a2;
+    float* a2_scale = reinterpret_cast<float*>(ws + L.off_a2_scale);
+    float* acc = reinterpret_cast<float*>(ws + L.off_acc);
+    hipStream_t s = (hipStream_t)stream;
+    launch_moe_sort(topk_ids, topk_weights, expert_mask, num_local_tokens, sorted_ids, sorted_w,
+                    sorted_eids, num_valid, acc, model_dim * 4, tokens, topk, E_sort, block_m,
+                    ws + L.off_sort_ws, L.sort_ws_bytes, s);
+    launch_per_group_quant_fp8(hidden_states, hidden_dtype, a1, a1_scale, tokens, model_dim, 0,
+                               num_local_tokens, 1, s);
+    const int sh = (int)(w_shuffled != 0);
+    stage1_dispatch(a1, a1_scale, model_dim / 128, 1, (const uint8_t*)w1, w1s, sorted_ids,
+                    sorted_eids, num_valid, a2, a2_scale, tokens, model_dim, inter_dim,
+                    num_experts, topk, block_m, L.blocks, sh, s);
+    stage2_dispatch(a2, a2_scale, (const uint8_t*)w2, w2s, sorted_ids, sorted_w, sorted_eids,
+                    num_valid, acc, tokens * topk, inter_dim, model_dim, num_experts, topk,
+                    block_m, L.blocks, sh, s);
+    launch_acc_to_out(acc, out, out_dtype, num_valid, tokens, model_dim, s);
 }
 
 }  // namespace
@@ -250,26 +368,26 @@ int aiter_amd_moe_stage1_fp8_blockscale(const void* a1, const float* a1_scale,
                                         int64_t max_m_blocks, int64_t activation,
                                         int64_t w_shuffled, void* stream) {
     return safe_call([&] {
-        check_dims(model_dim, inter_dim);
-        check_topk_experts(tokens, topk, num_experts);
-        check_block_m_gemm(block_m, model_dim, inter_dim);
-        AMD_CHECK(activation == 0, "only ActivationType.Silu (0) is supported, got " +
-                                       std::to_string(activation));
-        AMD_CHECK(max_m_blocks >= 0, "max_m_blocks must be >= 0");
-        if (tokens == 0 || max_m_blocks == 0) return;
-        check_ptr(a1, "a1");
-        check_ptr(w1, "w1");
-        check_ptr(a2, "a2");
-        AMD_CHECK(a1_scale && w1_scale && a2_scale && sorted_ids && sorted_expert_ids &&
-                      num_valid_ids,
-                  "a required pointer is NULL");
-        const int64_t KB = model_dim / 128;
-        const int64_t sa_row = a1_scale_transposed ? 1 : KB;
-        const int64_t sa_kb = a1_scale_transposed ? tokens : 1;
-        stage1_dispatch((const uint8_t*)a1, a1_scale, sa_row, sa_kb, (const uint8_t*)w1, w1_scale,
-                        sorted_ids, sorted_expert_ids, num_valid_ids, (uint8_t*)a2, a2_scale,
-                        tokens, model_dim, inter_dim, num_experts, topk, block_m, max_m_blocks,
-                        (int)(w_shuffled != 0), (hipStream_t)stream);
+        AMD_CHECK(w1_scale != nullptr, "w1_scale is NULL");
+        stage1_entry(a1, a1_scale, a1_scale_transposed, w1, WScale{w1_scale, nullptr}, sorted_ids,
+                     sorted_expert_ids, num_valid_ids, a2, a2_scale, tokens, model_dim, inter_dim,
+                     num_experts, topk, block_m, max_m_blocks, activation, w_shuffled, stream);
+    });
+}
+
+int aiter_amd_moe_stage1_a8w4(const void* a1, const float* a1_scale, int64_t a1_scale_transposed,
+                              const void* w1, const uint8_t* w1_scale,
+                              const int32_t* sorted_ids, const int32_t* sorted_expert_ids,
+                              const int32_t* num_valid_ids, void* a2, float* a2_scale,
+                              int64_t tokens, int64_t model_dim, int64_t inter_dim,
+                              int64_t num_experts, int64_t topk, int64_t block_m,
+                              int64_t max_m_blocks, int64_t activation, int64_t w_shuffled,
+                              void* stream) {
+    return safe_call([&] {
+        check_e8m0(w1_scale, "w1_scale");
+        stage1_entry(a1, a1_scale, a1_scale_transposed, w1, WScale{nullptr, w1_scale}, sorted_ids,
+                     sorted_expert_ids, num_valid_ids, a2, a2_scale, tokens, model_dim, inter_dim,
+                     num_experts, topk, block_m, max_m_blocks, activation, w_shuffled, stream);
     });
 }
 
@@ -282,21 +400,25 @@ int aiter_amd_moe_stage2_fp8_blockscale(const void* a2, const float* a2_scale, c
                                         int64_t num_experts, int64_t topk, int64_t block_m,
                                         int64_t max_m_blocks, int64_t w_shuffled, void* stream) {
     return safe_call([&] {
-        check_dims(model_dim, inter_dim);
-        check_topk_experts(tokens, topk, num_experts);
-        check_block_m_gemm(block_m, model_dim, inter_dim);
-        AMD_CHECK(max_m_blocks >= 0, "max_m_blocks must be >= 0");
-        if (tokens == 0 || max_m_blocks == 0) return;
-        check_ptr(a2, "a2");
-        check_ptr(w2, "w2");
-        check_ptr(out_acc, "out_acc");
-        AMD_CHECK(a2_scale && w2_scale && sorted_ids && sorted_weights && sorted_expert_ids &&
-                      num_valid_ids,
-                  "a required pointer is NULL");
-        stage2_dispatch((const uint8_t*)a2, a2_scale, (const uint8_t*)w2, w2_scale, sorted_ids,
-                        sorted_weights, sorted_expert_ids, num_valid_ids, out_acc, tokens * topk,
-                        inter_dim, model_dim, num_experts, topk, block_m, max_m_blocks,
-                        (int)(w_shuffled != 0), (hipStream_t)stream);
+        AMD_CHECK(w2_scale != nullptr, "w2_scale is NULL");
+        stage2_entry(a2, a2_scale, w2, WScale{w2_scale, nullptr}, sorted_ids, sorted_weights,
+                     sorted_expert_ids, num_valid_ids, out_acc, tokens, model_dim, inter_dim,
+                     num_experts, topk, block_m, max_m_blocks, w_shuffled, stream);
+    });
+}
+
+int aiter_amd_moe_stage2_a8w4(const void* a2, const float* a2_scale, const void* w2,
+                              const uint8_t* w2_scale, const int32_t* sorted_ids,
+                              const float* sorted_weights, const int32_t* sorted_expert_ids,
+                              const int32_t* num_valid_ids, float* out_acc, int64_t tokens,
+                              int64_t model_dim, int64_t inter_dim, int64_t num_experts,
+                              int64_t topk, int64_t block_m, int64_t max_m_blocks,
+                              int64_t w_shuffled, void* stream) {
+    return safe_call([&] {
+        check_e8m0(w2_scale, "w2_scale");
+        stage2_entry(a2, a2_scale, w2, WScale{nullptr, w2_scale}, sorted_ids, sorted_weights,
+                     sorted_expert_ids, num_valid_ids, out_acc, tokens, model_dim, inter_dim,
+                     num_experts, topk, block_m, max_m_blocks, w_shuffled, stream);
     });
 }
 
@@ -333,52 +455,29 @@ int aiter_amd_fused_moe_fp8_blockscale(const void* hidden_states, int hidden_dty
                                        int64_t block_m, int64_t w_shuffled, void* workspace,
                                        int64_t workspace_bytes, void* stream) {
     return safe_call([&] {
-        check_dims(model_dim, inter_dim);
-        check_topk_experts(tokens, topk, num_experts);
-        AMD_CHECK(hidden_dtype == DT_BF16 || hidden_dtype == DT_FP16,
-                  "hidden_states dtype must be bf16 or fp16");
-        AMD_CHECK(out_dtype == DT_BF16 || out_dtype == DT_FP16, "out dtype must be bf16 or fp16");
-        const int64_t E_sort = expert_mask ? global_experts : num_experts;
-        AMD_CHECK(E_sort >= num_experts && E_sort <= kMaxExperts,
-                  "global_experts must be in [num_experts, 4096]");
-        if (block_m <= 0) block_m = default_block_m(tokens, topk, num_experts, model_dim, inter_dim);
-        check_block_m_gemm(block_m, model_dim, inter_dim);
-        if (tokens == 0) return;
-        check_ptr(hidden_states, "hidden_states");
-        check_ptr(w1, "w1");
-        check_ptr(w2, "w2");
-        check_ptr(out, "out");
-        AMD_CHECK(w1_scale && w2_scale && topk_weights && topk_ids,
-                  "a required pointer is NULL");
-        const FusedLayout L = fused_layout(tokens, model_dim, inter_dim, E_sort, topk, block_m);
-        check_ptr(workspace, "workspace");
-        AMD_CHECK(workspace_bytes >= L.total, "workspace of " + std::to_string(L.total) +
-                                                  " bytes required, got " +
-                                                  std::to_string(workspace_bytes));
-        uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
-        int32_t* sorted_ids = reinterpret_cast<int32_t*>(ws + L.off_sorted_ids);
-        float* sorted_w = reinterpret_cast<float*>(ws + L.off_sorted_w);
-        int32_t* sorted_eids = reinterpret_cast<int32_t*>(ws + L.off_sorted_eids);
-        int32_t* num_valid = reinterpret_cast<int32_t*>(ws + L.off_num_valid);
-        uint8_t* a1 = ws + L.off_a1;
-        float* a1_scale = reinterpret_cast<float*>(ws + L.off_a1_scale);
-        uint8_t* a2 = ws + L.off_a2;
-        float* a2_scale = reinterpret_cast<float*>(ws + L.off_a2_scale);
-        float* acc = reinterpret_cast<float*>(ws + L.off_acc);
-        hipStream_t s = (hipStream_t)stream;
-        launch_moe_sort(topk_ids, topk_weights, expert_mask, num_local_tokens, sorted_ids,
-                        sorted_w, sorted_eids, num_valid, acc, model_dim * 4, tokens, topk,
-                        E_sort, block_m, ws + L.off_sort_ws, L.sort_ws_bytes, s);
-        launch_per_group_quant_fp8(hidden_states, hidden_dtype, a1, a1_scale, tokens, model_dim,
-                                   0, num_local_tokens, 1, s);
-        const int sh = (int)(w_shuffled != 0);
-        stage1_dispatch(a1, a1_scale, model_dim / 128, 1, (const uint8_t*)w1, w1_scale, sorted_ids,
-                        sorted_eids, num_valid, a2, a2_scale, tokens, model_dim, inter_dim,
-                        num_experts, topk, block_m, L.blocks, sh, s);
-        stage2_dispatch(a2, a2_scale, (const uint8_t*)w2, w2_scale, sorted_ids, sorted_w,
-                        sorted_eids, num_valid, acc, tokens * topk, inter_dim, model_dim,
-                        num_experts, topk, block_m, L.blocks, sh, s);
-        launch_acc_to_out(acc, out, out_dtype, num_valid, tokens, model_dim, s);
+        AMD_CHECK(w1_scale && w2_scale, "a required pointer is NULL");
+        fused_entry(hidden_states, hidden_dtype, w1, WScale{w1_scale, nullptr}, w2,
+                    WScale{w2_scale, nullptr}, topk_weights, topk_ids, expert_mask,
+                    num_local_tokens, out, out_dtype, tokens, model_dim, inter_dim, num_experts,
+                    global_experts, topk, block_m, w_shuffled, workspace, workspace_bytes, stream);
+    });
+}
+
+int aiter_amd_fused_moe_a8w4(const void* hidden_states, int hidden_dtype, const void* w1,
+                             const uint8_t* w1_scale, const void* w2, const uint8_t* w2_scale,
+                             const float* topk_weights, const int32_t* topk_ids,
+                             const int32_t* expert_mask, const int32_t* num_local_tokens,
+                             void* out, int out_dtype, int64_t tokens, int64_t model_dim,
+                             int64_t inter_dim, int64_t num_experts, int64_t global_experts,
+                             int64_t topk, int64_t block_m, int64_t w_shuffled, void* workspace,
+                             int64_t workspace_bytes, void* stream) {
+    return safe_call([&] {
+        check_e8m0(w1_scale, "w1_scale");
+        check_e8m0(w2_scale, "w2_scale");
+        fused_entry(hidden_states, hidden_dtype, w1, WScale{nullptr, w1_scale}, w2,
+                    WScale{nullptr, w2_scale}, topk_weights, topk_ids, expert_mask,
+                    num_local_tokens, out, out_dtype, tokens, model_dim, inter_dim, num_experts,
+                    global_experts, topk, block_m, w_shuffled, workspace, workspace_bytes, stream);
     });
 }
 

@@ -118,6 +118,18 @@ __device__ __forceinline__ v4f mfma16x16x128_fp8(const v8i& a, const v8i& b) {
     return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, z, 0, 0, 0, 0, 0, 0);
 }
 
+// One 16x16x128 MFMA of fp8 e4m3 A against fp4 e2m1 B (two values per byte,
+// even K in the low nibble) with an e8m0 scale per B lane taken from byte 0 of
+// b_scale; the A scale is 127 = 1.0.  Only the low 4 dwords of b are used.
+// K order of this operand pairing (measured on gfx950): the B lane of group
+// q = lane/16 holds K 32q..32q+31 in nibble order -- one MX block, which its
+// scale byte covers -- and the matching A lane must hold K 16q..16q+15 in
+// bytes 0-15 and K 64+16q..64+16q+15 in bytes 16-31 of its 32-byte fragment.
+__device__ __forceinline__ v4f mfma16x16x128_fp8_fp4(const v8i& a, const v8i& b, int b_scale) {
+    v4f z = {0.f, 0.f, 0.f, 0.f};
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, z, 0, 4, 0, 127, 0, b_scale);
+}
+
 template <typename T>
 __device__ __forceinline__ T warp_max_16(T v) {
     // max over the 16 lanes that share lane/16 (xor over lane bits 0..3)

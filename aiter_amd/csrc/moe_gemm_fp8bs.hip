@@ -30,6 +30,16 @@
 // copied verbatim into LDS, 2 KB per 16-row group per K block, and an MFMA
 // B fragment is two conflict-free 16-byte LDS reads.  Plain row-major
 // [E, N, K] weights are rearranged into the same LDS layout while staging.
+//
+// A8W4 (W4 = true): the weights are MXFP4 -- packed e2m1 [E, N, K/2] bytes
+// (shuffled on the byte view the same way, or row-major) with e8m0 scales
+// [E, N, K/32] (the layout torch_moe_stage1/2 read in their per_1x32
+// branch, aiter/fused_moe.py:1539-1553, 1635-1649).  A 16-row group's K
+// block is 1 KB and lane l's B fragment is its 16 bytes at l*16 (MX block
+// l/16 of row l%16); the lane's e8m0 byte goes into the scaled MFMA, so the
+// dequant FMA only applies the activation scale.  The A fragment takes K
+// bytes 16q..16q+15 and 64+16q..64+16q+15 (q = lane/16), the K pairing of
+// the fp8 x fp4 MFMA (see mfma16x16x128_fp8_fp4).
 #include "common.h"
 
 namespace aiter_amd {
@@ -44,7 +54,8 @@ struct GemmArgs {
     int64_t sa_row;
     int64_t sa_kb;
     const uint8_t* w;           // [E, N, K] fp8 (shuffled or row-major)
-    const float* w_scale;       // [E, N/128, K/128]
+    const float* w_scale;       // [E, N/128, K/128] (fp8 weights)
+    const uint8_t* w_scale8;    // [E, N, K/32] e8m0 (MXFP4 weights)
     const int32_t* sorted_ids;
     const float* sorted_w;
     const int32_t* sorted_eids;
@@ -60,17 +71,18 @@ struct GemmArgs {
     int64_t a_rows;
 };
 
-template <int BM, int STAGE, bool SHUFFLED>
+template <int BM, int STAGE, bool SHUFFLED, bool W4>
 __global__ __launch_bounds__(kGemmThreads) void moe_gemm_fp8bs_kernel(GemmArgs g) {
     constexpr int NGRP = STAGE == 1 ? 16 : 8;           // 16-row weight groups per tile
     constexpr int NCT = STAGE == 1 ? 4 : 2;             // 16-col MFMA tiles per wave
     constexpr int NRT = BM / 16;                        // 16-row MFMA tiles
+    constexpr int GB = W4 ? 1024 : 2048;                // bytes per 16-row group per K block
     constexpr int A_PIECES = (BM * 8 + kGemmThreads - 1) / kGemmThreads;
-    constexpr int B_PIECES = NGRP * 128 / kGemmThreads; // 16-byte pieces per thread
+    constexpr int B_PIECES = NGRP * (GB / 16) / kGemmThreads; // 16-byte pieces per thread
     static_assert(BM % 16 == 0 && BM <= 64, "BM must be 16, 32 or 64");
 
     __shared__ __attribute__((aligned(16))) uint8_t s_a[BM * kAStride];
-    __shared__ __attribute__((aligned(16))) uint8_t s_b[NGRP * 2048];
+    __shared__ __attribute__((aligned(16))) uint8_t s_b[NGRP * GB];
     __shared__ float s_sa[BM];
     __shared__ int64_t s_arow[BM];   // activation row (or -1)
     __shared__ int64_t s_orow[BM];   // output row (or -1)
@@ -111,8 +123,9 @@ __global__ __launch_bounds__(kGemmThreads) void moe_gemm_fp8bs_kernel(GemmArgs g
 
     const int K = g.K;
     const int KB = K / kBK;
-    const uint8_t* we = g.w + (int64_t)e * g.N * K;
-    const float* wse = g.w_scale + (int64_t)e * (g.N / 128) * KB;
+    const int KBY = W4 ? K / 2 : K;                     // weight bytes per row
+    const uint8_t* we = g.w + (int64_t)e * g.N * KBY;
+    const float* wse = W4 ? nullptr : g.w_scale + (int64_t)e * (g.N / 128) * KB;
 
     // Per-thread staging descriptors (fixed across K blocks).
     const uint8_t* a_src[A_PIECES];
@@ -134,7 +147,21 @@ __global__ __launch_bounds__(kGemmThreads) void moe_gemm_fp8bs_kernel(GemmArgs g
 #pragma unroll
     for (int i = 0; i < B_PIECES; ++i) {
         const int q = tid + i * kGemmThreads;
-        if (SHUFFLED) {
+        if (W4) {
+            // group grp's K block: 16 rows x 64 B; LDS holds it lane-linear
+            // (MX block j of row r at j*256 + r*16), which is also the shuffled
+            // byte layout of the block
+            const int grp = q >> 6, within = q & 63;
+            const int r = within & 15, j = within >> 4;
+            int row0;
+            if (STAGE == 1)
+                row0 = grp < 8 ? n0 + 16 * grp : g.inter + n0 + 16 * (grp - 8);
+            else
+                row0 = n0 + 16 * grp;
+            b_src[i] = SHUFFLED ? (int64_t)row0 * KBY + within * 16
+                                : (int64_t)(row0 + r) * KBY + j * 16;
+            b_dst[i] = q * 16;
+        } else if (SHUFFLED) {
             const int grp = q >> 7, within = q & 127;
             int row0;
             if (STAGE == 1)
@@ -156,8 +183,27 @@ __global__ __launch_bounds__(kGemmThreads) void moe_gemm_fp8bs_kernel(GemmArgs g
     }
     const int64_t sa_self = tid < BM ? s_arow[tid] : -1;
 
+    // column tile ct of this wave -> 16-row weight group
+    auto group_of = [&](int ct) {
+        if (STAGE == 1) return ct < 2 ? 2 * wv + ct : 8 + 2 * wv + (ct - 2);
+        return 2 * wv + ct;
+    };
+    // A8W4: lane's e8m0 scale row (the weight row of its column) per column tile
+    const uint8_t* bs_row[NCT];
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) {
+        bs_row[ct] = nullptr;
+        if (W4) {
+            const int grp = group_of(ct);
+            const int row = STAGE == 1 ? (grp < 8 ? n0 + 16 * grp : g.inter + n0 + 16 * (grp - 8))
+                                       : n0 + 16 * grp;
+            bs_row[ct] = g.w_scale8 + ((int64_t)e * g.N + row + lr) * (K / 32);
+        }
+    }
+
     v4i ra[A_PIECES];
     v4i rb[B_PIECES];
+    uint32_t rbs[NCT];
     float rsa = 0.0f;
     auto load_kb = [&](int kb) {
 #pragma unroll
@@ -167,8 +213,14 @@ __global__ __launch_bounds__(kGemmThreads) void moe_gemm_fp8bs_kernel(GemmArgs g
         }
 #pragma unroll
         for (int i = 0; i < B_PIECES; ++i) {
-            const int64_t off = SHUFFLED ? b_src[i] + (int64_t)kb * 2048 : b_src[i] + kb * kBK;
+            const int64_t off = W4 ? b_src[i] + (int64_t)kb * (SHUFFLED ? 1024 : 64)
+                                   : (SHUFFLED ? b_src[i] + (int64_t)kb * 2048 : b_src[i] + kb * kBK);
             rb[i] = *reinterpret_cast<const v4i*>(we + off);
+        }
+        if (W4) {
+#pragma unroll
+            for (int ct = 0; ct < NCT; ++ct)
+                rbs[ct] = *reinterpret_cast<const uint32_t*>(bs_row[ct] + kb * 4);
         }
         rsa = sa_self >= 0 ? g.a_scale[sa_self * g.sa_row + kb * g.sa_kb] : 0.0f;
     };
@@ -191,40 +243,46 @@ __global__ __launch_bounds__(kGemmThreads) void moe_gemm_fp8bs_kernel(GemmArgs g
 #pragma unroll
         for (int i = 0; i < B_PIECES; ++i) *reinterpret_cast<v4i*>(s_b + b_dst[i]) = rb[i];
         if (tid < BM) s_sa[tid] = rsa;
+        int bsc[NCT];                   // this step's e8m0 byte per column tile (A8W4)
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct) bsc[ct] = W4 ? (int)(rbs[ct] >> (8 * lq)) : 0;
         __syncthreads();
         if (kb + 1 < KB) load_kb(kb + 1);
 
-        const float sw0 = wse[nb0 * KB + kb];
-        const float sw1 = STAGE == 1 ? wse[nb1 * KB + kb] : 0.0f;
+        const float sw0 = W4 ? 1.0f : wse[nb0 * KB + kb];
+        const float sw1 = !W4 && STAGE == 1 ? wse[nb1 * KB + kb] : 1.0f;
 
         v8i bfrag[NCT];
 #pragma unroll
         for (int ct = 0; ct < NCT; ++ct) {
-            int grp;
-            if (STAGE == 1)
-                grp = ct < 2 ? 2 * wv + ct : 8 + 2 * wv + (ct - 2);
-            else
-                grp = 2 * wv + ct;
-            const uint8_t* p = s_b + grp * 2048 + lq * 512 + lr * 16;
-            const v4i lo = *reinterpret_cast<const v4i*>(p);
-            const v4i hi = *reinterpret_cast<const v4i*>(p + 256);
-            bfrag[ct] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            const int grp = group_of(ct);
+            if (W4) {
+                const v4i lo = *reinterpret_cast<const v4i*>(s_b + grp * 1024 + lane * 16);
+                bfrag[ct] = v8i{lo[0], lo[1], lo[2], lo[3], 0, 0, 0, 0};
+            } else {
+                const uint8_t* p = s_b + grp * 2048 + lq * 512 + lr * 16;
+                const v4i lo = *reinterpret_cast<const v4i*>(p);
+                const v4i hi = *reinterpret_cast<const v4i*>(p + 256);
+                bfrag[ct] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            }
         }
 #pragma unroll
         for (int rt = 0; rt < NRT; ++rt) {
-            const uint8_t* p = s_a + (rt * 16 + lr) * kAStride + lq * 32;
-            const v4i lo = *reinterpret_cast<const v4i*>(p);
-            const v4i hi = *reinterpret_cast<const v4i*>(p + 16);
+            const uint8_t* p = s_a + (rt * 16 + lr) * kAStride;
+            const v4i lo = *reinterpret_cast<const v4i*>(p + (W4 ? lq * 16 : lq * 32));
+            const v4i hi = *reinterpret_cast<const v4i*>(p + (W4 ? 64 + lq * 16 : lq * 32 + 16));
             const v8i afrag = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
             float sa[4];
 #pragma unroll
             for (int v = 0; v < 4; ++v) sa[v] = s_sa[rt * 16 + 4 * lq + v];
 #pragma unroll
             for (int ct = 0; ct < NCT; ++ct) {
-                const v4f blk = mfma16x16x128_fp8(afrag, bfrag[ct]);
+                const v4f blk = W4 ? mfma16x16x128_fp8_fp4(afrag, bfrag[ct], bsc[ct])
+                                   : mfma16x16x128_fp8(afrag, bfrag[ct]);
                 const float sw = (STAGE == 1 && ct >= 2) ? sw1 : sw0;
 #pragma unroll
-                for (int v = 0; v < 4; ++v) acc[rt][ct][v] += blk[v] * (sa[v] * sw);
+                for (int v = 0; v < 4; ++v)
+                    acc[rt][ct][v] += W4 ? blk[v] * sa[v] : blk[v] * (sa[v] * sw);
             }
         }
         __syncthreads();
@@ -299,19 +357,19 @@ __global__ __launch_bounds__(kGemmThreads) void moe_gemm_fp8bs_kernel(GemmArgs g
     }
 }
 
-template <int STAGE, bool SHUFFLED>
+template <int STAGE, bool SHUFFLED, bool W4>
 static void launch_gemm_bm(int bm, dim3 grid, GemmArgs& g, hipStream_t stream) {
     switch (bm) {
         case 16:
-            hipLaunchKernelGGL((moe_gemm_fp8bs_kernel<16, STAGE, SHUFFLED>), grid,
+            hipLaunchKernelGGL((moe_gemm_fp8bs_kernel<16, STAGE, SHUFFLED, W4>), grid,
                                dim3(kGemmThreads), 0, stream, g);
             break;
         case 32:
-            hipLaunchKernelGGL((moe_gemm_fp8bs_kernel<32, STAGE, SHUFFLED>), grid,
+            hipLaunchKernelGGL((moe_gemm_fp8bs_kernel<32, STAGE, SHUFFLED, W4>), grid,
                                dim3(kGemmThreads), 0, stream, g);
             break;
         case 64:
-            hipLaunchKernelGGL((moe_gemm_fp8bs_kernel<64, STAGE, SHUFFLED>), grid,
+            hipLaunchKernelGGL((moe_gemm_fp8bs_kernel<64, STAGE, SHUFFLED, W4>), grid,
                                dim3(kGemmThreads), 0, stream, g);
             break;
         default:
@@ -319,8 +377,25 @@ static void launch_gemm_bm(int bm, dim3 grid, GemmArgs& g, hipStream_t stream) {
     }
 }
 
+template <int STAGE>
+static void launch_gemm(int bm, dim3 grid, GemmArgs& g, int shuffled, bool w4,
+                        hipStream_t stream) {
+    if (w4) {
+        if (shuffled)
+            launch_gemm_bm<STAGE, true, true>(bm, grid, g, stream);
+        else
+            launch_gemm_bm<STAGE, false, true>(bm, grid, g, stream);
+    } else {
+        if (shuffled)
+            launch_gemm_bm<STAGE, true, false>(bm, grid, g, stream);
+        else
+            launch_gemm_bm<STAGE, false, false>(bm, grid, g, stream);
+    }
+}
+
 void launch_moe_stage1_fp8bs(const uint8_t* a, const float* a_scale, int64_t sa_row,
                              int64_t sa_kb, const uint8_t* w1, const float* w1_scale,
+                             const uint8_t* w1_scale_e8m0,
                              const int32_t* sorted_ids, const int32_t* sorted_eids,
                              const int32_t* num_valid, uint8_t* a2, float* a2_scale,
                              int64_t a_rows, int64_t K, int64_t inter, int64_t E, int64_t topk,
@@ -333,6 +408,7 @@ void launch_moe_stage1_fp8bs(const uint8_t* a, const float* a_scale, int64_t sa_
     g.sa_kb = sa_kb;
     g.w = w1;
     g.w_scale = w1_scale;
+    g.w_scale8 = w1_scale_e8m0;
     g.sorted_ids = sorted_ids;
     g.sorted_w = nullptr;
     g.sorted_eids = sorted_eids;
@@ -348,15 +424,13 @@ void launch_moe_stage1_fp8bs(const uint8_t* a, const float* a_scale, int64_t sa_
     g.a_rows = a_rows;
     if (max_m_blocks == 0) return;
     dim3 grid((unsigned)(inter / 128), (unsigned)max_m_blocks);
-    if (shuffled)
-        launch_gemm_bm<1, true>((int)block_m, grid, g, stream);
-    else
-        launch_gemm_bm<1, false>((int)block_m, grid, g, stream);
+    launch_gemm<1>((int)block_m, grid, g, shuffled, w1_scale_e8m0 != nullptr, stream);
     AMD_HIP_CHECK(hipGetLastError());
 }
 
 void launch_moe_stage2_fp8bs(const uint8_t* a2, const float* a2_scale, const uint8_t* w2,
-                             const float* w2_scale, const int32_t* sorted_ids,
+                             const float* w2_scale, const uint8_t* w2_scale_e8m0,
+                             const int32_t* sorted_ids,
                              const float* sorted_w, const int32_t* sorted_eids,
                              const int32_t* num_valid, float* acc, int64_t a_rows, int64_t inter,
                              int64_t hidden, int64_t E, int64_t topk, int64_t block_m,
@@ -368,6 +442,7 @@ void launch_moe_stage2_fp8bs(const uint8_t* a2, const float* a2_scale, const uin
     g.sa_kb = 1;
     g.w = w2;
     g.w_scale = w2_scale;
+    g.w_scale8 = w2_scale_e8m0;
     g.sorted_ids = sorted_ids;
     g.sorted_w = sorted_w;
     g.sorted_eids = sorted_eids;
@@ -383,10 +458,7 @@ void launch_moe_stage2_fp8bs(const uint8_t* a2, const float* a2_scale, const uin
     g.a_rows = a_rows;
     if (max_m_blocks == 0) return;
     dim3 grid((unsigned)(hidden / 128), (unsigned)max_m_blocks);
-    if (shuffled)
-        launch_gemm_bm<2, true>((int)block_m, grid, g, stream);
-    else
-        launch_gemm_bm<2, false>((int)block_m, grid, g, stream);
+    launch_gemm<2>((int)block_m, grid, g, shuffled, w2_scale_e8m0 != nullptr, stream);
     AMD_HIP_CHECK(hipGetLastError());
 }
 

@@ -32,6 +32,14 @@
 // Tile order: the grid is 1-D; workgroup L runs on XCD L % 8 and each XCD
 // owns n_tiles/8 column tiles for every M-block, so the weight slice of an
 // expert stays in that XCD's L2 across the expert's consecutive M-blocks.
+//
+// A8W4 (W4 = true): MXFP4 weights (packed e2m1 [E, N, K/2], e8m0 scales
+// [E, N, K/32]).  A 16-row group's K step is 1 KB, kept lane-linear in LDS
+// (lane l's B fragment = MX block l/16 of row l%16 at l*16, conflict-free);
+// the e8m0 dwords of the tile's 256 weight rows (4 MX blocks per K step)
+// ride in the scale DMA next to the activation scales, and each lane's byte
+// goes into the scaled MFMA.  The A slots then hold K bytes 16q..16q+15 and
+// 64+16q..64+16q+15 (the fp8 x fp4 K pairing, see mfma16x16x128_fp8_fp4).
 #include "common.h"
 
 namespace aiter_amd {
@@ -42,7 +50,6 @@ constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / 64;
 constexpr int kBK = 128;
 constexpr int kBRows = 256;                  // weight rows per tile
-constexpr int kBBytes = kBRows * kBK;        // 32 KB
 constexpr int kStages = 3;
 
 typedef __attribute__((address_space(3))) void* lds_void_t;
@@ -54,7 +61,8 @@ struct Args {
     int64_t sa_kb;
     int64_t sa_bytes;    // extent of a_scale in bytes
     const uint8_t* w;
-    const float* w_scale;
+    const float* w_scale;        // [E, N/128, K/128] (fp8 weights)
+    const uint8_t* w_scale8;     // [E, N, K/32] e8m0 (MXFP4 weights)
     const int32_t* sorted_ids;
     const float* sorted_w;
     const int32_t* sorted_eids;
@@ -120,26 +128,32 @@ __device__ __forceinline__ void wait_vm() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-template <int BM>
+template <int BM, bool W4>
 struct Tile {
     static constexpr int NRT = BM / 32;                 // 16-row MFMA tiles per wave
     static constexpr int A_BYTES = BM * kBK;
+    static constexpr int GB = W4 ? 1024 : 2048;         // bytes per 16-row group per K step
+    static constexpr int B_BYTES = 16 * GB;             // 256 weight rows
     static constexpr int A_INSTR = BM * kBK / 1024 / kWaves;  // 1 KB DMA instructions per wave
-    static constexpr int B_INSTR = kBBytes / 1024 / kWaves;   // = 4 per wave
+    static constexpr int B_INSTR = B_BYTES / 1024 / kWaves;   // 4 (fp8) or 2 (fp4) per wave
     static constexpr int LOADS = A_INSTR + B_INSTR + 1; // DMA instructions per wave per step
+    static constexpr int SA_WAVES = BM / 64;            // waves whose scale DMA carries a_scale
     static_assert(BM == 64 || BM == 128, "v2 tiles are 64 or 128 rows");
     static_assert(A_INSTR >= 1, "every wave issues at least one A chunk");
+    static_assert(!W4 || SA_WAVES + 4 <= kWaves, "room for the 256 e8m0 rows");
 };
 
-template <int BM, int STAGE, bool SHUFFLED>
+template <int BM, int STAGE, bool SHUFFLED, bool W4>
 __global__ __launch_bounds__(kThreads, 1) void moe_gemm_fp8bs_v2_kernel(Args g) {
-    using T = Tile<BM>;
+    using T = Tile<BM, W4>;
     constexpr int NRT = T::NRT;
     constexpr int A_INSTR = T::A_INSTR;
     constexpr int B_INSTR = T::B_INSTR;
-
+    constexpr int GB = T::GB;
     __shared__ __attribute__((aligned(1024))) uint8_t s_a[kStages][T::A_BYTES];
-    __shared__ __attribute__((aligned(1024))) uint8_t s_b[kStages][kBBytes];
+    __shared__ __attribute__((aligned(1024))) uint8_t s_b[kStages][T::B_BYTES];
+    // per stage: a_scale of row r at [r]; A8W4: e8m0 dword (4 MX blocks) of tile
+    // weight row j at [BM + j]
     __shared__ __attribute__((aligned(16))) float s_sa[kStages][kThreads];
     __shared__ int32_t s_arow[BM];
     __shared__ int64_t s_orow[BM];
@@ -196,15 +210,18 @@ __global__ __launch_bounds__(kThreads, 1) void moe_gemm_fp8bs_v2_kernel(Args g) 
 
     const int K = g.K;
     const int KB = K / kBK;
-    const uint8_t* we = g.w + (int64_t)e * g.N * K;
-    const float* wse = g.w_scale + (int64_t)e * (g.N / 128) * KB;
+    const int KBY = W4 ? K / 2 : K;                      // weight bytes per row
+    const uint8_t* we = g.w + (int64_t)e * g.N * KBY;
 
     // weight-scale block rows of the tile: stage 1 gate / up, stage 2 the two
     // 128-column halves
-    const int nb0 = n0 / 128;
-    const int nb1 = STAGE == 1 ? (g.inter + n0) / 128 : n0 / 128 + 1;
-    for (int i = tid; i < 2 * KB; i += kThreads)
-        s_sw[i / KB][i % KB] = wse[(i < KB ? nb0 : nb1) * KB + (i % KB)];
+    if (!W4) {
+        const float* wse = g.w_scale + (int64_t)e * (g.N / 128) * KB;
+        const int nb0 = n0 / 128;
+        const int nb1 = STAGE == 1 ? (g.inter + n0) / 128 : n0 / 128 + 1;
+        for (int i = tid; i < 2 * KB; i += kThreads)
+            s_sw[i / KB][i % KB] = wse[(i < KB ? nb0 : nb1) * KB + (i % KB)];
+    }
     const int swsel0 = STAGE == 1 ? 0 : (wn >> 1);
     const int swsel1 = STAGE == 1 ? 1 : (wn >> 1);
     __syncthreads();
@@ -219,12 +236,22 @@ __global__ __launch_bounds__(kThreads, 1) void moe_gemm_fp8bs_v2_kernel(Args g) 
         const int h = (lane & 1) ^ frag_swap(row);
         int arow = s_arow[row];
         if (arow < 0) arow = 0;           // pad rows: any valid row, result unused
-        a_off[i] = (uint32_t)arow * (uint32_t)K + (uint32_t)(kq * 32 + h * 16);
+        a_off[i] = (uint32_t)arow * (uint32_t)K +
+                   (uint32_t)(W4 ? kq * 16 + h * 64 : kq * 32 + h * 16);
     }
     uint32_t b_off[B_INSTR];
 #pragma unroll
     for (int i = 0; i < B_INSTR; ++i) {   // 1 KB chunk: half of a 16-row group, slot kq*32+rr*2+h
-        const int chunk = wvu * B_INSTR + i;   // 32 chunks of 1 KB
+        const int chunk = wvu * B_INSTR + i;   // 32 (fp8) or 16 (fp4) chunks of 1 KB
+        if (W4) {                              // chunk = group; lane-linear MX blocks
+            const int grp = chunk;
+            const int row0 = STAGE == 1 ? (grp < 8 ? n0 + 16 * grp : g.inter + n0 + 16 * (grp - 8))
+                                        : n0 + 16 * grp;
+            b_off[i] = SHUFFLED ? (uint32_t)row0 * (uint32_t)KBY + (uint32_t)(lane * 16)
+                                : (uint32_t)(row0 + (lane & 15)) * (uint32_t)KBY +
+                                      (uint32_t)((lane >> 4) * 16);
+            continue;
+        }
         const int grp = chunk >> 1;
         const int slot = (chunk & 1) * 64 + lane;
         const int kq = slot >> 5, rr = (slot >> 1) & 15, h = (slot & 1) ^ frag_swap(rr);
@@ -245,9 +272,19 @@ __global__ __launch_bounds__(kThreads, 1) void moe_gemm_fp8bs_v2_kernel(Args g) 
         sa_off = (uint32_t)((int64_t)arow * g.sa_row * 4);
     }
     const Rsrc ra = make_rsrc(g.a, (uint32_t)(g.a_rows * K));
-    const Rsrc rb = make_rsrc(we, (uint32_t)((int64_t)g.N * K));
-    const Rsrc rs = make_rsrc(g.a_scale, (uint32_t)g.sa_bytes);
-    const uint32_t sa_kb_bytes = (uint32_t)(g.sa_kb * 4);
+    const Rsrc rb = make_rsrc(we, (uint32_t)((int64_t)g.N * KBY));
+    Rsrc rs = make_rsrc(g.a_scale, (uint32_t)g.sa_bytes);
+    uint32_t sa_kb_bytes = (uint32_t)(g.sa_kb * 4);
+    // A8W4: waves SA_WAVES..SA_WAVES+3 fetch the e8m0 dwords of tile rows
+    // j = (wave - SA_WAVES) * 64 + lane instead of activation scales
+    if (W4 && wvu >= T::SA_WAVES && wvu < T::SA_WAVES + 4) {
+        const int j = (wvu - T::SA_WAVES) * 64 + lane;
+        const int row = STAGE == 1 ? (j < 128 ? n0 + j : g.inter + n0 + (j - 128)) : n0 + j;
+        const int KS = K / 32;                           // e8m0 bytes per weight row
+        rs = make_rsrc(g.w_scale8 + (int64_t)e * g.N * KS, (uint32_t)(g.N * KS));
+        sa_off = (uint32_t)(row * KS);
+        sa_kb_bytes = 4;
+    }
 
     auto issue = [&](int kb, int stage) {
         kb = kb < KB ? kb : KB - 1;       // past the end: repeat the last step (keeps counts uniform)
@@ -255,7 +292,7 @@ __global__ __launch_bounds__(kThreads, 1) void moe_gemm_fp8bs_v2_kernel(Args g) 
 #pragma unroll
         for (int i = 0; i < A_INSTR; ++i)
             dma16(ra, a_off[i], aoff, lds_addr(&s_a[stage][(wvu * A_INSTR + i) * 1024]));
-        const uint32_t boff = SHUFFLED ? (uint32_t)kb * 2048u : (uint32_t)kb * kBK;
+        const uint32_t boff = (uint32_t)kb * (SHUFFLED ? (uint32_t)GB : (uint32_t)GB / 16u);
 #pragma unroll
         for (int i = 0; i < B_INSTR; ++i)
             dma16(rb, b_off[i], boff, lds_addr(&s_b[stage][(wvu * B_INSTR + i) * 1024]));
@@ -294,43 +331,57 @@ __global__ __launch_bounds__(kThreads, 1) void moe_gemm_fp8bs_v2_kernel(Args g) 
         }
         // column tile ct (0..3) -> 16-row weight group: stage 1 tiles 0,1 are gate
         // rows, 2,3 the matching up rows; stage 2 four consecutive groups
+        auto group_of = [&](int ct) {
+            if (STAGE == 1) return ct < 2 ? wn * 2 + ct : 8 + wn * 2 + (ct - 2);
+            return wn * 4 + ct;
+        };
         auto bfrag_at = [&](int ct) {
-            int grp;
-            if (STAGE == 1)
-                grp = ct < 2 ? wn * 2 + ct : 8 + wn * 2 + (ct - 2);
-            else
-                grp = wn * 4 + ct;
+            const int grp = group_of(ct);
+            if (W4) {
+                const v4i lo = *reinterpret_cast<const v4i*>(sb_src + grp * 1024 + lane * 16);
+                return v8i{lo[0], lo[1], lo[2], lo[3], 0, 0, 0, 0};
+            }
             return frag(sb_src + grp * 2048 + lq * 512 + lr * 32);
+        };
+        // A8W4: the lane's e8m0 byte (MX block lq of its weight row) for tile ct
+        const uint8_t* s_bs = reinterpret_cast<const uint8_t*>(&s_sa[stage][BM]);
+        auto bscale_at = [&](int ct) {
+            return W4 ? (int)s_bs[(group_of(ct) * 16 + lr) * 4 + lq] : 0;
+        };
+        auto mfma = [&](const v8i& a, const v8i& b, int bs) {
+            return W4 ? mfma16x16x128_fp8_fp4(a, b, bs) : mfma16x16x128_fp8(a, b);
         };
         float sc[NRT][4];
         auto load_scales = [&](int half) {
-            const float sw = s_sw[half == 0 ? swsel0 : swsel1][kb];
+            const float sw = W4 ? 1.0f : s_sw[half == 0 ? swsel0 : swsel1][kb];
 #pragma unroll
             for (int rt = 0; rt < NRT; ++rt) {
                 const v4f s4 = *reinterpret_cast<const v4f*>(&s_sa[stage][row_base + rt * 16 + 4 * lq]);
 #pragma unroll
-                for (int v = 0; v < 4; ++v) sc[rt][v] = s4[v] * sw;
+                for (int v = 0; v < 4; ++v) sc[rt][v] = W4 ? s4[v] : s4[v] * sw;
             }
         };
         v4f blk[2][NRT];
         v8i bfrag = bfrag_at(0);
+        int bs = bscale_at(0);
 #pragma unroll
-        for (int rt = 0; rt < NRT; ++rt) blk[0][rt] = mfma16x16x128_fp8(afrag[rt], bfrag);
+        for (int rt = 0; rt < NRT; ++rt) blk[0][rt] = mfma(afrag[rt], bfrag, bs);
         load_scales(0);
 #pragma unroll
         for (int ct = 0; ct < 4; ++ct) {
             const int cur = ct & 1;
             if (ct + 1 < 4) {
                 bfrag = bfrag_at(ct + 1);
+                bs = bscale_at(ct + 1);
 #pragma unroll
                 for (int rt = 0; rt < NRT; ++rt)
-                    blk[cur ^ 1][rt] = mfma16x16x128_fp8(afrag[rt], bfrag);
+                    blk[cur ^ 1][rt] = mfma(afrag[rt], bfrag, bs);
             }
 #pragma unroll
             for (int rt = 0; rt < NRT; ++rt)
 #pragma unroll
                 for (int v = 0; v < 4; ++v) acc[rt][ct][v] += blk[cur][rt][v] * sc[rt][v];
-            if (ct == 1 && STAGE == 1) load_scales(1);
+            if (ct == 1 && STAGE == 1 && !W4) load_scales(1);
 #pragma unroll
             for (int i = 0; i < NRT; ++i) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
@@ -422,16 +473,31 @@ __global__ __launch_bounds__(kThreads, 1) void moe_gemm_fp8bs_v2_kernel(Args g) 
     }
 }
 
-template <int STAGE, bool SHUFFLED>
+template <int STAGE, bool SHUFFLED, bool W4>
 static void launch_bm(int bm, int grid, Args& a, hipStream_t stream) {
     if (bm == 64)
-        hipLaunchKernelGGL((moe_gemm_fp8bs_v2_kernel<64, STAGE, SHUFFLED>), dim3(grid),
+        hipLaunchKernelGGL((moe_gemm_fp8bs_v2_kernel<64, STAGE, SHUFFLED, W4>), dim3(grid),
                            dim3(kThreads), 0, stream, a);
     else if (bm == 128)
-        hipLaunchKernelGGL((moe_gemm_fp8bs_v2_kernel<128, STAGE, SHUFFLED>), dim3(grid),
+        hipLaunchKernelGGL((moe_gemm_fp8bs_v2_kernel<128, STAGE, SHUFFLED, W4>), dim3(grid),
                            dim3(kThreads), 0, stream, a);
     else
         AMD_CHECK(false, "v2 GEMM block_m must be 64 or 128");
+}
+
+template <int STAGE>
+static void launch(int bm, int grid, Args& a, int shuffled, bool w4, hipStream_t stream) {
+    if (w4) {
+        if (shuffled)
+            launch_bm<STAGE, true, true>(bm, grid, a, stream);
+        else
+            launch_bm<STAGE, false, true>(bm, grid, a, stream);
+    } else {
+        if (shuffled)
+            launch_bm<STAGE, true, false>(bm, grid, a, stream);
+        else
+            launch_bm<STAGE, false, false>(bm, grid, a, stream);
+    }
 }
 
 static int64_t scale_bytes(int64_t rows, int64_t KB, int64_t sa_row, int64_t sa_kb) {
@@ -446,7 +512,7 @@ bool v2_supported(int64_t block_m, int64_t K) {
 
 void launch_moe_stage1_fp8bs_v2(const uint8_t* a, const float* a_scale, int64_t sa_row,
                                 int64_t sa_kb, const uint8_t* w1, const float* w1_scale,
-                                const int32_t* sorted_ids, const int32_t* sorted_eids,
+                                const uint8_t* w1_scale_e8m0, const int32_t* sorted_ids, const int32_t* sorted_eids,
                                 const int32_t* num_valid, uint8_t* a2, float* a2_scale,
                                 int64_t a_rows, int64_t K, int64_t inter, int64_t E, int64_t topk,
                                 int64_t block_m, int64_t max_m_blocks, int shuffled,
@@ -459,6 +525,7 @@ void launch_moe_stage1_fp8bs_v2(const uint8_t* a, const float* a_scale, int64_t 
     g.sa_bytes = v2::scale_bytes(a_rows, K / 128, sa_row, sa_kb);
     g.w = w1;
     g.w_scale = w1_scale;
+    g.w_scale8 = w1_scale_e8m0;
     g.sorted_ids = sorted_ids;
     g.sorted_eids = sorted_eids;
     g.num_valid = num_valid;
@@ -477,15 +544,13 @@ void launch_moe_stage1_fp8bs_v2(const uint8_t* a, const float* a_scale, int64_t 
               "v2 GEMM needs 32-bit buffer offsets");
     const int64_t grid = (int64_t)g.n_tiles * max_m_blocks;
     if (grid == 0) return;
-    if (shuffled)
-        v2::launch_bm<1, true>((int)block_m, (int)grid, g, stream);
-    else
-        v2::launch_bm<1, false>((int)block_m, (int)grid, g, stream);
+    v2::launch<1>((int)block_m, (int)grid, g, shuffled, w1_scale_e8m0 != nullptr, stream);
     AMD_HIP_CHECK(hipGetLastError());
 }
 
 void launch_moe_stage2_fp8bs_v2(const uint8_t* a2, const float* a2_scale, const uint8_t* w2,
-                                const float* w2_scale, const int32_t* sorted_ids,
+                                const float* w2_scale, const uint8_t* w2_scale_e8m0,
+                                const int32_t* sorted_ids,
                                 const float* sorted_w, const int32_t* sorted_eids,
                                 const int32_t* num_valid, float* acc, int64_t a_rows,
                                 int64_t inter, int64_t hidden, int64_t E, int64_t topk,
@@ -499,6 +564,7 @@ void launch_moe_stage2_fp8bs_v2(const uint8_t* a2, const float* a2_scale, const 
     g.sa_bytes = v2::scale_bytes(a_rows, inter / 128, g.sa_row, g.sa_kb);
     g.w = w2;
     g.w_scale = w2_scale;
+    g.w_scale8 = w2_scale_e8m0;
     g.sorted_ids = sorted_ids;
     g.sorted_w = sorted_w;
     g.sorted_eids = sorted_eids;
@@ -517,10 +583,7 @@ void launch_moe_stage2_fp8bs_v2(const uint8_t* a2, const float* a2_scale, const 
               "v2 GEMM needs 32-bit buffer offsets");
     const int64_t grid = (int64_t)g.n_tiles * max_m_blocks;
     if (grid == 0) return;
-    if (shuffled)
-        v2::launch_bm<2, true>((int)block_m, (int)grid, g, stream);
-    else
-        v2::launch_bm<2, false>((int)block_m, (int)grid, g, stream);
+    v2::launch<2>((int)block_m, (int)grid, g, shuffled, w2_scale_e8m0 != nullptr, stream);
     AMD_HIP_CHECK(hipGetLastError());
 }
 

@@ -89,9 +89,12 @@ def moe_sorting(
 
 @functools.lru_cache(maxsize=2048)
 def get_inter_dim(w1_shape, w2_shape):
-    """(E, model_dim, inter_dim) from the weight shapes (fused_moe.py:108-115)."""
+    """(E, model_dim, inter_dim) from the weight shapes (fused_moe.py:108-115);
+    packed fp4 weights hold two K values per byte, which the model_dim /
+    w1.shape[-1] factor undoes."""
     E, _, model_dim = w1_shape
     E, model_dim, inter_dim = w2_shape
+    inter_dim *= model_dim // w1_shape[-1]
     return E, model_dim, inter_dim
 
 
@@ -154,24 +157,35 @@ def _out_dtype(hidden_states, dtype):
     return hidden_states.dtype if hidden_states.dtype in (dtypes.bf16, dtypes.fp16) else dtypes.bf16
 
 
+_FP4_DTYPES = (torch.uint8, dtypes.fp4x2)
+_E8M0_DTYPES = (torch.uint8, dtypes.fp8_e8m0)
+
+
 def _check_supported(hidden_states, w1, w2, activation, quant_type, doweight_stage1, w1_scale,
                      w2_scale, a1_scale, hidden_pad, intermediate_pad, bias1, bias2, out_dtype):
-    if quant_type != QuantType.per_1x128:
+    if quant_type not in (QuantType.per_1x128, QuantType.per_1x32):
         raise NotImplementedError(
-            f"quant_type {quant_type!r}: only per_128x128 / per_1x128 fp8 blockscale is "
-            "implemented")
+            f"quant_type {quant_type!r}: only per_128x128 / per_1x128 fp8 blockscale and "
+            "per_1x32 MXFP4 weights (A8W4) are implemented")
     if activation != ActivationType.Silu:
         raise NotImplementedError(f"activation {activation!r}: only Silu is implemented")
     if doweight_stage1:
         raise NotImplementedError("doweight_stage1=True is not implemented")
     if hidden_pad or intermediate_pad or bias1 is not None or bias2 is not None:
         raise NotImplementedError("hidden_pad / intermediate_pad / bias are not implemented")
-    if w1.dtype != dtypes.fp8 or w2.dtype != dtypes.fp8:
-        raise ValueError(f"w1/w2 must be {dtypes.fp8}, got {w1.dtype}/{w2.dtype}")
     if w1_scale is None or w2_scale is None:
-        raise ValueError("w1_scale and w2_scale are required for blockscale fp8")
-    if w1_scale.dtype != dtypes.fp32 or w2_scale.dtype != dtypes.fp32:
-        raise ValueError("w1_scale / w2_scale must be float32")
+        raise ValueError("w1_scale and w2_scale are required")
+    if quant_type == QuantType.per_1x32:
+        if w1.dtype not in _FP4_DTYPES or w2.dtype not in _FP4_DTYPES:
+            raise ValueError(f"per_1x32 needs packed fp4x2 (or uint8) w1/w2, got "
+                             f"{w1.dtype}/{w2.dtype}")
+        if w1_scale.dtype not in _E8M0_DTYPES or w2_scale.dtype not in _E8M0_DTYPES:
+            raise ValueError("per_1x32 w1_scale / w2_scale must be e8m0 (or uint8)")
+    else:
+        if w1.dtype != dtypes.fp8 or w2.dtype != dtypes.fp8:
+            raise ValueError(f"w1/w2 must be {dtypes.fp8}, got {w1.dtype}/{w2.dtype}")
+        if w1_scale.dtype != dtypes.fp32 or w2_scale.dtype != dtypes.fp32:
+            raise ValueError("w1_scale / w2_scale must be float32")
     if out_dtype not in (dtypes.bf16, dtypes.fp16):
         raise ValueError(f"Fused_moe unsupported out dtype: {out_dtype}")
     if hidden_states.dtype == dtypes.fp8 and a1_scale is None:
@@ -186,7 +200,9 @@ def fused_moe_(hidden_states, w1, w2, topk_weight, topk_ids, expert_mask=None,
                a2_scale=None, block_size_M=-1, num_local_tokens=None,
                moe_sorting_dispatch_policy=0, dtype=None, hidden_pad=0, intermediate_pad=0,
                bias1=None, bias2=None):
-    """Body of the drop-in (fused_moe.py:205-364) for the fp8 blockscale path."""
+    """Body of the drop-in (fused_moe.py:205-364) for the fp8 blockscale path
+    and, with quant_type per_1x32 and packed fp4 weights, the A8W4 path (fp8
+    1x128 activations x MXFP4 weights)."""
     activation = ActivationType(activation)
     quant_type = quant_remap.get(QuantType(quant_type), QuantType(quant_type))
     M, topk = topk_ids.shape
@@ -196,6 +212,13 @@ def fused_moe_(hidden_states, w1, w2, topk_weight, topk_ids, expert_mask=None,
     out_dtype = _out_dtype(hidden_states, dtype)
     _check_supported(hidden_states, w1, w2, activation, quant_type, doweight_stage1, w1_scale,
                      w2_scale, a1_scale, hidden_pad, intermediate_pad, bias1, bias2, out_dtype)
+    a8w4 = quant_type == QuantType.per_1x32
+    if a8w4:
+        exp1 = (E, 2 * inter_dim, model_dim // 32)
+        exp2 = (E, model_dim, inter_dim // 32)
+        if tuple(w1_scale.shape) != exp1 or tuple(w2_scale.shape) != exp2:
+            raise ValueError(f"e8m0 scales must be {exp1} / {exp2}, got "
+                             f"{tuple(w1_scale.shape)} / {tuple(w2_scale.shape)}")
     shuffled = bool(getattr(w1, "is_shuffled", False))
     if bool(getattr(w2, "is_shuffled", False)) != shuffled:
         raise ValueError("w1 and w2 must both be shuffled or both be plain")
@@ -207,6 +230,9 @@ def fused_moe_(hidden_states, w1, w2, topk_weight, topk_ids, expert_mask=None,
     topk_weight = topk_weight.to(torch.float32).contiguous()
     w1c, w2c = w1.contiguous(), w2.contiguous()
     w1s, w2s = w1_scale.contiguous(), w2_scale.contiguous()
+    if a8w4:   # byte views; the kernels read packed e2m1 and e8m0 bytes
+        w1c, w2c = w1c.view(torch.uint8), w2c.view(torch.uint8)
+        w1s, w2s = w1s.view(torch.uint8), w2s.view(torch.uint8)
     mask = expert_mask.to(torch.int32).contiguous() if expert_mask is not None else None
     out = torch.empty((M, model_dim), dtype=out_dtype, device=device)
     if M == 0:
@@ -220,7 +246,7 @@ def fused_moe_(hidden_states, w1, w2, topk_weight, topk_ids, expert_mask=None,
                               global_E, topk, block_m)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
         _abi.call(
-            "aiter_amd_fused_moe_fp8_blockscale",
+            "aiter_amd_fused_moe_a8w4" if a8w4 else "aiter_amd_fused_moe_fp8_blockscale",
             x.data_ptr(), AITER_DTYPE[x.dtype], w1c.data_ptr(), w1s.data_ptr(), w2c.data_ptr(),
             w2s.data_ptr(), topk_weight.data_ptr(), topk_ids.data_ptr(), _ptr(mask),
             _ptr(num_local_tokens), out.data_ptr(), AITER_DTYPE[out_dtype], M, model_dim,
@@ -231,14 +257,31 @@ def fused_moe_(hidden_states, w1, w2, topk_weight, topk_ids, expert_mask=None,
     sorted_ids, sorted_w, sorted_eids, num_valid, acc = moe_sorting(
         topk_ids, topk_weight, global_E, model_dim, dtypes.fp32, block_m, mask,
         num_local_tokens, moe_sorting_dispatch_policy)
-    a2, a2s = moe_stage1_fp8_blockscale(hidden_states.contiguous(), a1_scale.contiguous(), w1c,
-                                        w1s, sorted_ids, sorted_eids, num_valid, topk, block_m,
-                                        shuffled)
-    moe_stage2_fp8_blockscale(a2, a2s, w2c, w2s, sorted_ids, sorted_w, sorted_eids, num_valid,
-                              acc, block_m, shuffled)
+    st1 = moe_stage1_a8w4 if a8w4 else moe_stage1_fp8_blockscale
+    st2 = moe_stage2_a8w4 if a8w4 else moe_stage2_fp8_blockscale
+    a2, a2s = st1(hidden_states.contiguous(), a1_scale.contiguous(), w1c, w1s, sorted_ids,
+                  sorted_eids, num_valid, topk, block_m, shuffled)
+    st2(a2, a2s, w2c, w2s, sorted_ids, sorted_w, sorted_eids, num_valid, acc, block_m, shuffled)
     _abi.call("aiter_amd_moe_acc_to_out", acc.data_ptr(), out.data_ptr(), AITER_DTYPE[out_dtype],
               num_valid.data_ptr(), M, model_dim, stream)
     return out
+
+
+def _stage1(entry, a1, a1_scale, w1, w1_scale, sorted_ids, sorted_expert_ids, num_valid_ids,
+            topk, block_m, shuffled, a1_scale_transposed):
+    T, H = a1.shape
+    E, N1, _ = w1.shape
+    inter = N1 // 2
+    a2 = torch.empty((T, topk, inter), dtype=dtypes.fp8, device=a1.device)
+    a2s = torch.empty((T, topk, inter // 128), dtype=dtypes.fp32, device=a1.device)
+    _abi.call(
+        entry,
+        a1.data_ptr(), a1_scale.data_ptr(), int(bool(a1_scale_transposed)), w1.data_ptr(),
+        w1_scale.data_ptr(), sorted_ids.data_ptr(), sorted_expert_ids.data_ptr(),
+        num_valid_ids.data_ptr(), a2.data_ptr(), a2s.data_ptr(), T, H, inter, E, topk,
+        int(block_m), sorted_expert_ids.numel(), int(ActivationType.Silu), int(bool(shuffled)),
+        _stream(a1.device))
+    return a2, a2s
 
 
 def moe_stage1_fp8_blockscale(a1, a1_scale, w1, w1_scale, sorted_ids, sorted_expert_ids,
@@ -248,38 +291,52 @@ def moe_stage1_fp8_blockscale(a1, a1_scale, w1, w1_scale, sorted_ids, sorted_exp
     Returns (a2 fp8 [T, topk, I], a2_scale f32 [T, topk, I/128]) -- the pair
     the reference builds from ck_moe_stage1 + quant (fused_moe.py:1297-1314).
     """
-    T, H = a1.shape
-    E, N1, _ = w1.shape
-    inter = N1 // 2
-    a2 = torch.empty((T, topk, inter), dtype=dtypes.fp8, device=a1.device)
-    a2s = torch.empty((T, topk, inter // 128), dtype=dtypes.fp32, device=a1.device)
-    _abi.call(
-        "aiter_amd_moe_stage1_fp8_blockscale",
-        a1.data_ptr(), a1_scale.data_ptr(), int(bool(a1_scale_transposed)), w1.data_ptr(),
-        w1_scale.data_ptr(), sorted_ids.data_ptr(), sorted_expert_ids.data_ptr(),
-        num_valid_ids.data_ptr(), a2.data_ptr(), a2s.data_ptr(), T, H, inter, E, topk,
-        int(block_m), sorted_expert_ids.numel(), int(ActivationType.Silu), int(bool(shuffled)),
-        _stream(a1.device))
-    return a2, a2s
+    return _stage1("aiter_amd_moe_stage1_fp8_blockscale", a1, a1_scale, w1, w1_scale,
+                   sorted_ids, sorted_expert_ids, num_valid_ids, topk, block_m, shuffled,
+                   a1_scale_transposed)
 
 
-def moe_stage2_fp8_blockscale(a2, a2_scale, w2, w2_scale, sorted_ids, sorted_weights,
-                              sorted_expert_ids, num_valid_ids, out_acc, block_m, shuffled):
-    """Stage 2: out_acc[t] += w * (a2 . w2^T) with block-scale dequant (f32 accumulate)."""
+def moe_stage1_a8w4(a1, a1_scale, w1, w1_scale, sorted_ids, sorted_expert_ids, num_valid_ids,
+                    topk, block_m, shuffled, a1_scale_transposed=False):
+    """A8W4 stage 1: fp8 1x128 activations x MXFP4 w1 (packed uint8 [E, 2I, H/2],
+    e8m0 uint8 [E, 2I, H/32]); same outputs as moe_stage1_fp8_blockscale."""
+    return _stage1("aiter_amd_moe_stage1_a8w4", a1, a1_scale, w1.view(torch.uint8),
+                   w1_scale.view(torch.uint8), sorted_ids, sorted_expert_ids, num_valid_ids,
+                   topk, block_m, shuffled, a1_scale_transposed)
+
+
+def _stage2(entry, a2, a2_scale, w2, w2_scale, sorted_ids, sorted_weights, sorted_expert_ids,
+            num_valid_ids, out_acc, block_m, shuffled):
     T, topk, inter = a2.shape
     E, H, _ = w2.shape
     if out_acc.dtype != dtypes.fp32:
         raise ValueError("out_acc must be float32")
     _abi.call(
-        "aiter_amd_moe_stage2_fp8_blockscale",
+        entry,
         a2.data_ptr(), a2_scale.data_ptr(), w2.data_ptr(), w2_scale.data_ptr(),
         sorted_ids.data_ptr(), sorted_weights.data_ptr(), sorted_expert_ids.data_ptr(),
         num_valid_ids.data_ptr(), out_acc.data_ptr(), T, H, inter, E, topk, int(block_m),
         sorted_expert_ids.numel(), int(bool(shuffled)), _stream(a2.device))
 
 
+def moe_stage2_fp8_blockscale(a2, a2_scale, w2, w2_scale, sorted_ids, sorted_weights,
+                              sorted_expert_ids, num_valid_ids, out_acc, block_m, shuffled):
+    """Stage 2: out_acc[t] += w * (a2 . w2^T) with block-scale dequant (f32 accumulate)."""
+    _stage2("aiter_amd_moe_stage2_fp8_blockscale", a2, a2_scale, w2, w2_scale, sorted_ids,
+            sorted_weights, sorted_expert_ids, num_valid_ids, out_acc, block_m, shuffled)
+
+
+def moe_stage2_a8w4(a2, a2_scale, w2, w2_scale, sorted_ids, sorted_weights, sorted_expert_ids,
+                    num_valid_ids, out_acc, block_m, shuffled):
+    """A8W4 stage 2: MXFP4 w2 (packed uint8 [E, H, I/2], e8m0 uint8 [E, H, I/32])."""
+    _stage2("aiter_amd_moe_stage2_a8w4", a2, a2_scale, w2.view(torch.uint8),
+            w2_scale.view(torch.uint8), sorted_ids, sorted_weights, sorted_expert_ids,
+            num_valid_ids, out_acc, block_m, shuffled)
+
+
 __all__ = [
     "BLOCK_SIZE_M", "fused_moe", "fused_moe_", "fused_moe_fake", "moe_sorting",
-    "moe_stage1_fp8_blockscale", "moe_stage2_fp8_blockscale", "per_group_quant_hip",
+    "moe_stage1_fp8_blockscale", "moe_stage2_fp8_blockscale", "moe_stage1_a8w4",
+    "moe_stage2_a8w4", "per_group_quant_hip",
     "get_inter_dim", "default_block_m", "sorted_capacity",
 ]

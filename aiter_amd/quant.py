@@ -102,3 +102,68 @@ def quant_weight_per_128x128(w: torch.Tensor, quant_dtype: torch.dtype = dtypes.
     q = (blk / scale).to(quant_dtype)
     q = q.permute(0, 1, 3, 2, 4).contiguous().view(E, N, K)
     return q, scale.view(E, N // 128, K // 128).contiguous()
+
+
+# ------------------------------------------------------------------ MXFP4 ---
+# Weight preparation for the A8W4 path (run once at load time, like
+# quant_weight_per_128x128).  OCP MX FP4: e2m1 values, two per byte with the
+# even element in the low nibble, one e8m0 scale per 32 consecutive K.
+
+
+def f32_to_e8m0(x: torch.Tensor) -> torch.Tensor:
+    """fp32 -> e8m0 byte as aiter/utility/fp4_utils.py:49-58: the biased
+    exponent, plus one when mantissa bit 22 is set and a lower bit is set or
+    the value is normal (1.5*2^e and above round to 2^(e+1))."""
+    u = x.float().contiguous().view(torch.int32)
+    exp = (u >> 23) & 0xFF
+    up = ((u & 0x400000) != 0) & (((u & 0x200000) != 0) | ((u & 0x1FFFFF) != 0) | (exp > 0))
+    e = (exp + up.to(torch.int32)) & 0xFF
+    e = torch.where(exp == 0xFF, torch.full_like(e, 0xFF), e)
+    return e.to(torch.uint8)
+
+
+def e8m0_to_f32(e: torch.Tensor) -> torch.Tensor:
+    """e8m0 byte -> 2^(e-127) (aiter/utility/fp4_utils.py:61-69; 0 -> 2^-127)."""
+    ei = e.view(torch.uint8).to(torch.int32)
+    bits = ei << 23
+    bits = torch.where(ei == 0, torch.full_like(bits, 0x00400000), bits)
+    bits = torch.where(ei == 0xFF, torch.full_like(bits, 0x7F800001), bits)
+    return bits.view(torch.float32)
+
+
+def f32_to_e2m1(y: torch.Tensor) -> torch.Tensor:
+    """fp32 -> e2m1 code (uint8 0..15): round to nearest even, |y| >= 6
+    saturates, sign kept -- the saturating conversion of
+    aiter/utility/fp4_utils.py:120-235.  Below 1.0 the value is rounded on
+    the 0.5 grid by adding 2^22 in fp32; above, the exponent is rebased
+    (bias 127 -> 1) and the 22 dropped mantissa bits are rounded half-even."""
+    u = y.float().contiguous().view(torch.int32)
+    sign = (u >> 31) & 1
+    a = (u & 0x7FFFFFFF).view(torch.float32)
+    denorm = (a + 2.0 ** 22).view(torch.int32) - (149 << 23)
+    ua = a.view(torch.int32)
+    normal = (ua + ((1 - 127) << 23) + ((1 << 21) - 1) + ((ua >> 22) & 1)) >> 22
+    code = torch.where(a >= 6.0, torch.full_like(ua, 7), torch.where(a < 1.0, denorm, normal))
+    return ((code & 7) | (sign << 3)).to(torch.uint8)
+
+
+def per_1x32_f4_quant(x: torch.Tensor, scale=None, quant_dtype=dtypes.fp4x2,
+                      shuffle: bool = False):
+    """MXFP4 quant of [..., K] (aiter/ops/quant.py:75-105): per 32-element
+    block, scale = e8m0(amax / 4), values e2m1(x / 2^(scale-127)).
+    Returns (packed [..., K/2] as fp4x2, scales [..., K/32] as e8m0)."""
+    if scale is not None:
+        raise ValueError("unsupported: static MXFP4 scale")
+    if quant_dtype != dtypes.fp4x2:
+        raise NotImplementedError(f"quant_dtype {quant_dtype} is not supported (fp4x2 only)")
+    if shuffle:
+        raise NotImplementedError("e8m0 scale shuffling is not used by these kernels")
+    shape = x.shape
+    K = shape[-1]
+    if K % 32:
+        raise ValueError(f"last dim {K} must be a multiple of 32")
+    b = x.float().reshape(-1, K // 32, 32)
+    e = f32_to_e8m0(b.abs().amax(dim=-1) / 4.0)
+    codes = f32_to_e2m1(b / e8m0_to_f32(e).unsqueeze(-1)).reshape(*shape)
+    packed = (codes[..., 0::2] | (codes[..., 1::2] << 4)).contiguous()
+    return packed.view(dtypes.fp4x2), e.reshape(*shape[:-1], K // 32).view(dtypes.fp8_e8m0)

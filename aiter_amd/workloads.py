@@ -8,7 +8,8 @@ scores + top-k + renormalise for the expert-parallel share
 (aiter/ops/topk.py:116-157); a Zipf(s) popularity prior added to the logits
 (log p_e, p_e ~ rank^-s over a seeded expert permutation) for skewed
 prefill.  Weights are N(0, 0.02), quantised to fp8 e4m3fn with 128x128
-block scales and, optionally, pre-shuffled to the (16,16) layout.
+block scales (or, for A8W4, to MXFP4 with e8m0 1x32 scales) and,
+optionally, pre-shuffled to the (16,16) layout.
 """
 from __future__ import annotations
 
@@ -17,7 +18,7 @@ from typing import Optional
 
 import torch
 
-from .quant import quant_weight_per_128x128
+from .quant import per_1x32_f4_quant, quant_weight_per_128x128
 from .shuffle import shuffle_weight
 
 
@@ -33,6 +34,7 @@ class MoEConfig:
     zipf_s: float = 1.1
     local_experts: Optional[int] = None  # EP share: experts held by this GPU
     seed: int = 0
+    weights: str = "fp8"            # fp8 (128x128 blockscale) | mxfp4 (A8W4)
     extra: dict = field(default_factory=dict)
 
 
@@ -47,6 +49,14 @@ def mimo_decode(tokens: int, seed: int = 1) -> MoEConfig:
 
 def mimo_prefill(tokens: int, seed: int = 5) -> MoEConfig:
     return MoEConfig(f"mimo_prefill_T{tokens}", tokens, routing="zipf", seed=seed, **MIMO)
+
+
+def mimo_a8w4(tokens: int, seed: Optional[int] = None) -> MoEConfig:
+    """A8W4 layer: uniform routing, seeds 6 / 7 / 8 for T = 32 / 1024 / 8192."""
+    if seed is None:
+        seed = {32: 6, 1024: 7, 8192: 8}.get(tokens, 6)
+    return MoEConfig(f"mimo_a8w4_T{tokens}", tokens, routing="softmax", seed=seed,
+                     weights="mxfp4", **MIMO)
 
 
 def mimo_ep_share(tokens: int = 4096, seed: int = 9) -> MoEConfig:
@@ -92,16 +102,39 @@ def make_expert_mask(cfg: MoEConfig, device="cpu"):
 
 
 def make_weights(cfg: MoEConfig, device="cpu", shuffle: bool = True, chunk: int = 8):
-    """fp8 weights + fp32 128x128 scales for the experts held locally.
+    """Quantised weights for the experts held locally.
 
-    Returns dict(w1, w1_scale, w2, w2_scale) with w1 [E, 2I, H], w2 [E, H, I]
-    (optionally shuffled, carrying is_shuffled).  Generated `chunk` experts
-    at a time on `device` with a per-chunk seeded generator, so large
-    layers never hold their fp32 weights at once.
+    fp8 (cfg.weights == "fp8"): dict(w1, w1_scale, w2, w2_scale) with w1
+    [E, 2I, H], w2 [E, H, I] fp8 and fp32 128x128 scales.  mxfp4: w1
+    [E, 2I, H/2], w2 [E, H, I/2] packed e2m1 (uint8) and e8m0 scales (uint8)
+    [E, 2I, H/32], [E, H, I/32].  Weights are optionally shuffled (carrying
+    is_shuffled).  Generated `chunk` experts at a time on `device` with a
+    per-chunk seeded generator, so large layers never hold their fp32
+    weights at once; the fp32 draws are the same for both formats.
     """
     E = cfg.local_experts or cfg.experts
     H, I = cfg.model_dim, cfg.inter_dim
     dev = torch.device(device)
+    if cfg.weights == "mxfp4":
+        w1 = torch.empty(E, 2 * I, H // 2, dtype=torch.uint8, device=dev)
+        w2 = torch.empty(E, H, I // 2, dtype=torch.uint8, device=dev)
+        s1 = torch.empty(E, 2 * I, H // 32, dtype=torch.uint8, device=dev)
+        s2 = torch.empty(E, H, I // 32, dtype=torch.uint8, device=dev)
+        for c0 in range(0, E, chunk):
+            c1 = min(E, c0 + chunk)
+            g = torch.Generator(device=dev).manual_seed(cfg.seed * 104729 + c0)
+            f1 = torch.randn(c1 - c0, 2 * I, H, generator=g, device=dev) * 0.02
+            q1, sc1 = per_1x32_f4_quant(f1)
+            del f1
+            f2 = torch.randn(c1 - c0, H, I, generator=g, device=dev) * 0.02
+            q2, sc2 = per_1x32_f4_quant(f2)
+            del f2
+            w1[c0:c1], s1[c0:c1] = q1.view(torch.uint8), sc1.view(torch.uint8)
+            w2[c0:c1], s2[c0:c1] = q2.view(torch.uint8), sc2.view(torch.uint8)
+        if shuffle:
+            w1 = shuffle_weight(w1)
+            w2 = shuffle_weight(w2)
+        return {"w1": w1, "w1_scale": s1, "w2": w2, "w2_scale": s2}
     w1 = torch.empty(E, 2 * I, H, dtype=torch.float8_e4m3fn, device=dev)
     w2 = torch.empty(E, H, I, dtype=torch.float8_e4m3fn, device=dev)
     s1 = torch.empty(E, 2 * I // 128, H // 128, dtype=torch.float32, device=dev)
@@ -134,9 +167,19 @@ def expert_bytes_fp8(cfg: MoEConfig) -> int:
     return 2 * I * H + H * I + 4 * ((2 * I // 128) * (H // 128) + (H // 128) * (I // 128))
 
 
+def expert_bytes_a8w4(cfg: MoEConfig) -> int:
+    """Packed e2m1 weights + e8m0 1x32 scales of one expert."""
+    H, I = cfg.model_dim, cfg.inter_dim
+    return (2 * I * H + H * I) // 2 + (2 * I * H + H * I) // 32
+
+
+def expert_bytes(cfg: MoEConfig) -> int:
+    return expert_bytes_a8w4(cfg) if cfg.weights == "mxfp4" else expert_bytes_fp8(cfg)
+
+
 def layer_bytes(cfg: MoEConfig, distinct_experts: int, tokens: Optional[int] = None) -> float:
     """Algorithmic HBM bytes: touched experts' weights + x (bf16) + out (bf16)
     + routing ids/weights (4 B each per slot)."""
     T = cfg.tokens if tokens is None else tokens
-    return float(distinct_experts * expert_bytes_fp8(cfg) +
+    return float(distinct_experts * expert_bytes(cfg) +
                  T * (cfg.model_dim * 2 + cfg.model_dim * 2 + 8 * cfg.topk))

@@ -79,7 +79,7 @@ int aiter_amd_dynamic_per_group_quant_fp8(const void* input, int input_dtype, in
  *   w1 [E, 2*inter_dim, model_dim] fp8, w1_scale [E, 2*inter_dim/128, model_dim/128]
  *   a2 [tokens, topk, inter_dim] fp8, a2_scale [tokens, topk, inter_dim/128]
  *   activation must be 0 (Silu); w_shuffled: 1 for the (16,16) layout.
- *   block_m in {16, 32, 64}; max_m_blocks = capacity of sorted_expert_ids. */
+ *   block_m in {16, 32, 64, 128}; max_m_blocks = capacity of sorted_expert_ids. */
 int aiter_amd_moe_stage1_fp8_blockscale(const void* a1, const float* a1_scale,
                                         int64_t a1_scale_transposed, const void* w1,
                                         const float* w1_scale, const int32_t* sorted_ids,
@@ -104,6 +104,37 @@ int aiter_amd_moe_stage2_fp8_blockscale(const void* a2, const float* a2_scale, c
                                         int64_t num_experts, int64_t topk, int64_t block_m,
                                         int64_t max_m_blocks, int64_t w_shuffled, void* stream);
 
+/* A8W4 stage 1: fp8 1x128 activations x MXFP4 weights.  Replaces the per_1x32
+ * fp4x2-weight stage 1 (cktile_moe_stage1, aiter/ops/moe_op.py:343-464 ->
+ * csrc/ck_tile_gemm_moe_2stages/moe_cktile2stages.cu:316-345), with the
+ * activations quantised 1x128 as for aiter_amd_moe_stage1_fp8_blockscale
+ * (the reference's fp8-activation A8W4 branch casts them with unit e8m0
+ * scales, aiter/fused_moe.py:1167-1177).
+ *   w1 [E, 2*inter_dim, model_dim/2] packed e2m1 (even K in the low nibble),
+ *   row-major or (16,16)-shuffled on the byte view (w_shuffled);
+ *   w1_scale [E, 2*inter_dim, model_dim/32] e8m0 bytes (4-byte aligned).
+ *   Everything else as aiter_amd_moe_stage1_fp8_blockscale. */
+int aiter_amd_moe_stage1_a8w4(const void* a1, const float* a1_scale, int64_t a1_scale_transposed,
+                              const void* w1, const uint8_t* w1_scale,
+                              const int32_t* sorted_ids, const int32_t* sorted_expert_ids,
+                              const int32_t* num_valid_ids, void* a2, float* a2_scale,
+                              int64_t tokens, int64_t model_dim, int64_t inter_dim,
+                              int64_t num_experts, int64_t topk, int64_t block_m,
+                              int64_t max_m_blocks, int64_t activation, int64_t w_shuffled,
+                              void* stream);
+
+/* A8W4 stage 2: replaces the per_1x32 fp4x2-weight stage 2 (cktile_moe_stage2,
+ * aiter/ops/moe_op.py:343-464 -> moe_cktile2stages.cu:444-475).
+ *   w2 [E, model_dim, inter_dim/2] packed e2m1, w2_scale [E, model_dim, inter_dim/32]
+ *   e8m0 bytes; everything else as aiter_amd_moe_stage2_fp8_blockscale. */
+int aiter_amd_moe_stage2_a8w4(const void* a2, const float* a2_scale, const void* w2,
+                              const uint8_t* w2_scale, const int32_t* sorted_ids,
+                              const float* sorted_weights, const int32_t* sorted_expert_ids,
+                              const int32_t* num_valid_ids, float* out_acc, int64_t tokens,
+                              int64_t model_dim, int64_t inter_dim, int64_t num_experts,
+                              int64_t topk, int64_t block_m, int64_t max_m_blocks,
+                              int64_t w_shuffled, void* stream);
+
 /* Converts the stage-2 f32 accumulator into moe_buf (bf16 or fp16) for the
  * first num_valid_ids[1] rows.  The reference accumulates into moe_buf
  * directly (gemm_moe_ck2stages.cu:118-181); this is the finishing pass of the
@@ -112,7 +143,8 @@ int aiter_amd_moe_acc_to_out(const float* acc, void* out, int out_dtype,
                              const int32_t* num_valid_ids, int64_t tokens, int64_t model_dim,
                              void* stream);
 
-/* Bytes of workspace for aiter_amd_fused_moe_fp8_blockscale. */
+/* Bytes of workspace for aiter_amd_fused_moe_fp8_blockscale and
+ * aiter_amd_fused_moe_a8w4. */
 int64_t aiter_amd_fused_moe_workspace_bytes(int64_t tokens, int64_t model_dim,
                                             int64_t inter_dim, int64_t num_experts,
                                             int64_t topk, int64_t block_m);
@@ -136,6 +168,19 @@ int aiter_amd_fused_moe_fp8_blockscale(const void* hidden_states, int hidden_dty
                                        int64_t global_experts, int64_t topk, int64_t block_m,
                                        int64_t w_shuffled, void* workspace,
                                        int64_t workspace_bytes, void* stream);
+
+/* The whole 2-stage A8W4 MoE in one call: fused_moe_ with quant_type per_1x32
+ * and fp4x2 weights (aiter/fused_moe.py:255-275, 1103-1334), fp8 1x128
+ * activations.  Arguments as aiter_amd_fused_moe_fp8_blockscale with the
+ * weights and e8m0 scales of aiter_amd_moe_stage{1,2}_a8w4. */
+int aiter_amd_fused_moe_a8w4(const void* hidden_states, int hidden_dtype, const void* w1,
+                             const uint8_t* w1_scale, const void* w2, const uint8_t* w2_scale,
+                             const float* topk_weights, const int32_t* topk_ids,
+                             const int32_t* expert_mask, const int32_t* num_local_tokens,
+                             void* out, int out_dtype, int64_t tokens, int64_t model_dim,
+                             int64_t inter_dim, int64_t num_experts, int64_t global_experts,
+                             int64_t topk, int64_t block_m, int64_t w_shuffled, void* workspace,
+                             int64_t workspace_bytes, void* stream);
 
 /* Default M-block (sorted rows per GEMM tile) for a token count: 16 / 32 / 64 by the average
  * rows per expert, 128 once experts average >= 128 rows and the dims allow 128-row tiles.

@@ -136,6 +136,105 @@ def shuffle_16x16(w: np.ndarray) -> np.ndarray:
         w.reshape(E, N // 16, 16, K // 32, 2, 16).transpose(0, 1, 3, 4, 2, 5)).reshape(E, N, K)
 
 
+# --------------------------------------------------------------- mxfp4 ---
+# OCP MX FP4: e2m1 elements (1 sign, 2 exponent bits with bias 1, 1 mantissa
+# bit; values 0, 0.5, 1, 1.5, 2, 3, 4, 6), two per byte with the even element
+# in the low nibble (aiter/utility/fp4_utils.py:19-46 unpack, 100-105 pack),
+# and one e8m0 scale 2^(e-127) per 32 consecutive K elements.
+FP4_LUT = np.array([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0,
+                    -0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0], dtype=np.float32)
+FP4_MAX = 6.0
+
+
+def fp4_encode_rne_sat(x: np.ndarray) -> np.ndarray:
+    """fp32 -> e2m1 code (uint8 0..15), round to nearest even, magnitudes
+    >= 6 saturate to 6, sign kept.  Bit-level statement of the reference's
+    _f32_to_floatx_unpacked with ebits=2, mbits=1
+    (aiter/utility/fp4_utils.py:120-235): values below the smallest normal
+    (1.0) are rounded on the 0.5 grid by adding 2^22 in fp32; normal values
+    get their exponent rebased and the dropped 22 mantissa bits rounded
+    half-to-even."""
+    x = np.asarray(x, dtype=np.float32)
+    u = x.view(np.uint32).astype(np.int64)
+    sign = (u >> 31) & 1
+    a = (u & 0x7FFFFFFF).astype(np.uint32).view(np.float32)
+    # denormal branch: a + 2^22 rounds a to a multiple of 0.5 (fp32 ulp there)
+    denorm = ((a + np.float32(2.0 ** 22)).view(np.uint32).astype(np.int64)
+              - (149 << 23))
+    # normal branch: rebase exponent (127 -> 1), round the 22 dropped bits RNE
+    ua = a.view(np.uint32).astype(np.int64)
+    odd = (ua >> 22) & 1
+    normal = (ua + ((1 - 127) << 23) + ((1 << 21) - 1) + odd) >> 22
+    code = np.where(a >= np.float32(FP4_MAX), 7,
+                    np.where(a < np.float32(1.0), denorm, normal))
+    return ((code & 7) | (sign << 3)).astype(np.uint8)
+
+
+def fp4_pack(codes: np.ndarray) -> np.ndarray:
+    """[..., K] e2m1 codes -> [..., K/2] bytes, even element in the low nibble."""
+    c = np.asarray(codes, dtype=np.uint8)
+    return (c[..., 0::2] | (c[..., 1::2] << 4)).astype(np.uint8)
+
+
+def fp4_unpack(packed: np.ndarray) -> np.ndarray:
+    b = np.asarray(packed, dtype=np.uint8)
+    out = np.empty(b.shape[:-1] + (b.shape[-1] * 2,), dtype=np.uint8)
+    out[..., 0::2] = b & 0xF
+    out[..., 1::2] = b >> 4
+    return out
+
+
+def mxfp4_decode(packed: np.ndarray) -> np.ndarray:
+    return FP4_LUT[fp4_unpack(packed)]
+
+
+def f32_to_e8m0(x: np.ndarray) -> np.ndarray:
+    """fp32 -> e8m0 exponent byte (aiter/utility/fp4_utils.py:49-58): the
+    biased exponent of x, plus one when mantissa bit 22 is set and either a
+    lower mantissa bit is set or x is normal (so 1.5*2^e and above go to
+    2^(e+1)); NaN/inf exponents stay 0xFF."""
+    u = np.asarray(x, dtype=np.float32).view(np.uint32).astype(np.int64)
+    exp = (u >> 23) & 0xFF
+    up = ((u & 0x400000) != 0) & (((u & 0x200000) != 0) | ((u & 0x1FFFFF) != 0) | (exp > 0))
+    out = (exp + up.astype(np.int64)) & 0xFF
+    return np.where(exp == 0xFF, 0xFF, out).astype(np.uint8)
+
+
+def e8m0_to_f32(e: np.ndarray) -> np.ndarray:
+    """e8m0 byte -> 2^(e-127) (aiter/utility/fp4_utils.py:61-69): 0 is
+    2^-127 (fp32 subnormal 0x00400000), 0xFF is NaN."""
+    e = np.asarray(e, dtype=np.uint8).astype(np.uint32)
+    bits = e << 23
+    bits = np.where(e == 0, np.uint32(0x00400000), bits)
+    bits = np.where(e == 0xFF, np.uint32(0x7F800001), bits)
+    return bits.astype(np.uint32).view(np.float32)
+
+
+def quant_weight_mxfp4(w: np.ndarray):
+    """per_1x32_f4_quant (aiter/ops/quant.py:75-105) of [..., K]:
+    per 32-element block, scale = e8m0(amax / 4) (4 = 2^floor(log2 6)),
+    codes = e2m1(x / 2^(scale-127)).  Returns (packed u8 [..., K/2],
+    scale u8 [..., K/32])."""
+    w = np.asarray(w, dtype=np.float32)
+    lead, K = w.shape[:-1], w.shape[-1]
+    b = w.reshape(-1, K // 32, 32)
+    amax = np.abs(b).max(axis=-1).astype(np.float32)
+    e = f32_to_e8m0((amax / np.float32(4.0)).astype(np.float32))
+    y = (b / e8m0_to_f32(e)[..., None]).astype(np.float32)
+    codes = fp4_encode_rne_sat(y).reshape(*lead, K)
+    return fp4_pack(codes), e.reshape(*lead, K // 32)
+
+
+def dequant_weight_mxfp4(packed: np.ndarray, scale: np.ndarray) -> np.ndarray:
+    """[..., K/2] packed e2m1 + [..., K/32] e8m0 -> fp32 [..., K]
+    (torch_moe_stage1's per_1x32 weight branch, aiter/fused_moe.py:1504-1553)."""
+    v = mxfp4_decode(packed)
+    K = v.shape[-1]
+    s = e8m0_to_f32(scale)
+    return (v.reshape(*v.shape[:-1], K // 32, 32) * s[..., None]).reshape(v.shape).astype(
+        np.float32)
+
+
 # ------------------------------------------------------------- sorting ---
 def moe_sorting_ref(topk_ids: np.ndarray, topk_w: np.ndarray, num_experts: int,
                     block_size: int, expert_mask=None, num_local_tokens=None):
@@ -264,14 +363,20 @@ def moe_stage2_ref(a2: np.ndarray, w2: np.ndarray, topk_ids_local: np.ndarray,
 
 
 def fused_moe_ref(x_bf16: np.ndarray, w1q, w1s, w2q, w2s, topk_ids, topk_w,
-                  expert_mask=None, num_local_tokens=None, act_quant="kernel"):
+                  expert_mask=None, num_local_tokens=None, act_quant="kernel",
+                  weight_format="fp8_128x128"):
     """The whole 2-stage FP8 blockscale layer as the reference's fused_moe
     computes it (aiter/fused_moe.py:1103-1334 with the oracles of
     op_tests/test_moe_2stage.py:187-231): 1x128 quant of x, stage 1 with
     fp32 dequant, bf16, 1x128 requant, stage 2, bf16.
     act_quant='kernel' uses the HIP kernel's quant arithmetic (what
     fused_moe runs), 'torch' the test's pertoken_quant.
+    weight_format='mxfp4' is the A8W4 layer: the same 1x128 fp8 activations
+    with packed e2m1 weights [E, N, K/2] and e8m0 scales [E, N, K/32]
+    dequantised as in torch_moe_stage1/2's per_1x32 weight branch
+    (aiter/fused_moe.py:1539-1553, 1635-1649).
     Returns dict with out [T, H] (fp32 of bf16 values) and intermediates."""
+    deq = dequant_weight_mxfp4 if weight_format == "mxfp4" else dequant_weight_128x128
     q = quant_1x128_kernel if act_quant == "kernel" else pertoken_quant_torch_semantics
     x = np.asarray(x_bf16, dtype=np.float32)
     T, H = x.shape
@@ -280,13 +385,13 @@ def fused_moe_ref(x_bf16: np.ndarray, w1q, w1s, w2q, w2s, topk_ids, topk_w,
     ids_local = np.where(np.arange(T)[:, None] < tokens, ids_local, -1)
     a1q, a1s = q(x)
     a1 = dequant_1x128(a1q, a1s)
-    w1 = dequant_weight_128x128(w1q, w1s)
+    w1 = deq(w1q, w1s)
     h = moe_stage1_ref(a1, w1, ids_local)
     topk = h.shape[1]
     inter = h.shape[2]
     a2q, a2s = q(h.reshape(T * topk, inter))
     a2 = dequant_1x128(a2q, a2s).reshape(T, topk, inter)
-    w2 = dequant_weight_128x128(w2q, w2s)
+    w2 = deq(w2q, w2s)
     out = moe_stage2_ref(a2, w2, ids_local, topk_w)
     return {"out": out, "a1q": a1q, "a1s": a1s, "h": h, "a2q": a2q.reshape(T, topk, inter),
             "a2s": a2s.reshape(T, topk, inter // 128), "ids_local": ids_local}

@@ -8,10 +8,13 @@ import ctypes
 import re
 from pathlib import Path
 
+import numpy as np
 import pytest
 import torch
 
+import aiter_amd as A
 from aiter_amd import _abi
+from oracle import moe_ref as R
 
 ROOT = Path(__file__).resolve().parents[1]
 
@@ -167,3 +170,52 @@ def test_weight_quant_matches_oracle():
     qo, so = R.quant_weight_128x128(w.numpy())
     assert np.array_equal(q.view(torch.uint8).numpy(), qo)
     assert np.array_equal(s.numpy(), so)
+
+
+def test_torch_mxfp4_quant_matches_oracle():
+    g = torch.Generator().manual_seed(5)
+    w = torch.randn(3, 64, 256, generator=g) * 0.02
+    w[0, 0, :32] = 0.0
+    w[1, 2, 64:96] *= 1e4
+    w[2, 5, 7] = -0.0
+    p, s = A.per_1x32_f4_quant(w)
+    assert p.dtype == A.dtypes.fp4x2 and s.dtype == A.dtypes.fp8_e8m0
+    rp, rs = R.quant_weight_mxfp4(w.numpy())
+    np.testing.assert_array_equal(p.view(torch.uint8).numpy(), rp)
+    np.testing.assert_array_equal(s.view(torch.uint8).numpy(), rs)
+    e = torch.arange(1, 255, dtype=torch.uint8)
+    np.testing.assert_array_equal(A.e8m0_to_f32(e).numpy(), R.e8m0_to_f32(e.numpy()))
+
+
+def test_a8w4_validation_errors():
+    args = [16, 16, 0, 16]
+    tail = [16, 16, 16, 16, 16, 4, 4096, 2048, 8, 2, 32, 10, 0, 1, None]
+    _expect_error("aiter_amd_moe_stage1_a8w4", *args, None, *tail, match="w1_scale is NULL")
+    _expect_error("aiter_amd_moe_stage1_a8w4", *args, 18, *tail, match="4-byte aligned")
+    _expect_error("aiter_amd_moe_stage2_a8w4", 16, 16, 16, None, 16, 16, 16, 16, 16, 4, 4096,
+                  2048, 8, 2, 32, 10, 1, None, match="w2_scale is NULL")
+    base = [16, 3, 16, 16, 16, None, 16, 16, None, None, 16, 3]
+    _expect_error("aiter_amd_fused_moe_a8w4", *base, 4, 4096, 2048, 8, 8, 2, 0, 1, 16, 10,
+                  None, match="w2_scale is NULL")
+
+
+def test_python_layer_a8w4_checks():
+    from aiter_amd import QuantType, fused_moe
+
+    x = torch.zeros(4, 256, dtype=torch.bfloat16)
+    ids = torch.zeros(4, 1, dtype=torch.int32)
+    tw = torch.ones(4, 1)
+    w1 = torch.zeros(2, 256, 128, dtype=torch.uint8)    # [E, 2I, H/2]
+    w2 = torch.zeros(2, 256, 64, dtype=torch.uint8)     # [E, H, I/2]
+    s1 = torch.zeros(2, 256, 8, dtype=torch.uint8)
+    s2 = torch.zeros(2, 256, 4, dtype=torch.uint8)
+    assert A.get_inter_dim(w1.shape, w2.shape) == (2, 256, 128)
+    with pytest.raises(ValueError, match="e8m0 scales must be"):
+        fused_moe(x, w1, w2, tw, ids, quant_type=QuantType.per_1x32, w1_scale=s1[..., :4],
+                  w2_scale=s2)
+    with pytest.raises(ValueError, match="per_1x32 needs packed fp4x2"):
+        fused_moe(x, w1.view(torch.float8_e4m3fn), w2.view(torch.float8_e4m3fn), tw, ids,
+                  quant_type=QuantType.per_1x32, w1_scale=s1, w2_scale=s2)
+    with pytest.raises(ValueError, match="e8m0"):
+        fused_moe(x, w1, w2, tw, ids, quant_type=QuantType.per_1x32, w1_scale=s1.float(),
+                  w2_scale=s2)

@@ -1,0 +1,164 @@
+"""GPU parity of the A8W4 path (fp8 1x128 activations x MXFP4 weights,
+quant_type per_1x32) against the CPU oracle, through the C ABI.
+
+Same bar as the FP8 blockscale path: the oracle is the reference's
+torch_moe_stage1/2 with the per_1x32 weight dequant
+(aiter/fused_moe.py:1539-1553, 1635-1649) and 1x128 activation quant;
+outputs agree within max-rel <= 2e-2, RMS-rel <= 4e-3
+(op_tests/triton_tests/moe/test_moe_gemm_a8w4.py:104-160).
+"""
+import dataclasses
+
+import numpy as np
+import pytest
+import torch
+
+import aiter_amd as A
+from aiter_amd import workloads as W
+from oracle import moe_ref as R
+
+pytestmark = pytest.mark.gpu
+
+MAXTOL, RMSTOL = R.MAXTOL, R.RMSTOL
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+def _a8w4(cfg):
+    return dataclasses.replace(cfg, weights="mxfp4")
+
+
+def _make_layer(cfg, device, shuffle):
+    wts = W.make_weights(cfg, device="cpu", shuffle=False)
+    x = W.make_hidden(cfg)
+    tw, ids = W.make_routing(cfg)
+    mask = W.make_expert_mask(cfg)
+    ref = R.fused_moe_ref(x.float().numpy(), wts["w1"].numpy(), wts["w1_scale"].numpy(),
+                          wts["w2"].numpy(), wts["w2_scale"].numpy(), ids.numpy(), tw.numpy(),
+                          None if mask is None else mask.numpy(), weight_format="mxfp4")
+    w1, w2 = wts["w1"], wts["w2"]
+    if shuffle:
+        w1, w2 = A.shuffle_weight(w1), A.shuffle_weight(w2)
+    dev = dict(x=x.to(device), w1=w1.to(device), w2=w2.to(device),
+               s1=wts["w1_scale"].to(device), s2=wts["w2_scale"].to(device), tw=tw.to(device),
+               ids=ids.to(device), mask=None if mask is None else mask.to(device))
+    if shuffle:
+        dev["w1"].is_shuffled = True
+        dev["w2"].is_shuffled = True
+    return dev, ref
+
+
+def _run(dev, **kw):
+    return A.fused_moe(dev["x"], dev["w1"], dev["w2"], dev["tw"], dev["ids"],
+                       expert_mask=dev["mask"], quant_type=A.QuantType.per_1x32,
+                       w1_scale=dev["s1"], w2_scale=dev["s2"], **kw)
+
+
+def _check(ref_out, got, tag):
+    mx, rms = R.normalized_errors(ref_out, got)
+    print(f"[{tag}] max-rel {mx:.3e} rms-rel {rms:.3e}", flush=True)
+    assert mx <= MAXTOL and rms <= RMSTOL, (mx, rms)
+
+
+@pytest.mark.parametrize("shuffle", [True, False])
+@pytest.mark.parametrize("bm", [16, 32, 64, 128])
+def test_a8w4_config_a(cuda_device, shuffle, bm):
+    cfg = _a8w4(W.CONFIG_A)
+    dev, ref = _make_layer(cfg, cuda_device, shuffle)
+    out = _run(dev, block_size_M=bm)
+    assert out.dtype == torch.bfloat16 and out.shape == (cfg.tokens, cfg.model_dim)
+    _check(ref["out"], _np(out.float()), f"A8W4 A shuffle={shuffle} bm={bm}")
+
+
+def test_a8w4_torch_dtypes_match_byte_views(cuda_device):
+    """fp4x2 / e8m0 tensors and their uint8 views give the same bits."""
+    cfg = _a8w4(W.CONFIG_A)
+    dev, _ = _make_layer(cfg, cuda_device, True)
+    out_u8 = _run(dev)
+    typed = dict(dev)
+    typed["w1"] = dev["w1"].view(A.dtypes.fp4x2)
+    typed["w2"] = dev["w2"].view(A.dtypes.fp4x2)
+    typed["w1"].is_shuffled = typed["w2"].is_shuffled = True
+    typed["s1"] = dev["s1"].view(A.dtypes.fp8_e8m0)
+    typed["s2"] = dev["s2"].view(A.dtypes.fp8_e8m0)
+    out_typed = _run(typed)
+    # same kernels, same inputs: equal up to the f32 atomic order of stage 2
+    mx, rms = R.normalized_errors(_np(out_u8.float()), _np(out_typed.float()))
+    assert mx <= 1e-2 and rms <= 1e-3
+
+
+@pytest.mark.parametrize("bm", [64, 128])
+def test_a8w4_prefill_shape(cuda_device, bm):
+    """Large M-blocks (the direct-to-LDS kernels) with K > 1 pipeline depth."""
+    cfg = W.MoEConfig("a8w4_prefill", 512, 1024, 512, 8, 2, seed=11, weights="mxfp4")
+    dev, ref = _make_layer(cfg, cuda_device, True)
+    _check(ref["out"], _np(_run(dev, block_size_M=bm).float()), f"A8W4 T=512 bm={bm}")
+
+
+def test_a8w4_fp8_input_path(cuda_device):
+    cfg = _a8w4(W.CONFIG_A)
+    dev, ref = _make_layer(cfg, cuda_device, True)
+    a1, a1s = A.per_group_quant_hip(dev["x"])
+    out = A.fused_moe(a1, dev["w1"], dev["w2"], dev["tw"], dev["ids"],
+                      quant_type=A.QuantType.per_1x32, w1_scale=dev["s1"], w2_scale=dev["s2"],
+                      a1_scale=a1s, dtype=torch.bfloat16)
+    _check(ref["out"], _np(out.float()), "A8W4 fp8 input")
+
+
+def test_a8w4_ep_share_small(cuda_device):
+    cfg = W.MoEConfig("a8w4_ep", 96, 512, 512, 16, 4, routing="sigmoid", local_experts=4,
+                      seed=3, weights="mxfp4")
+    dev, ref = _make_layer(cfg, cuda_device, False)
+    out = _run(dev)
+    _check(ref["out"], _np(out.float()), "A8W4 EP small")
+    none_local = (ref["ids_local"] < 0).all(axis=1)
+    assert none_local.any()
+    assert torch.count_nonzero(out[torch.from_numpy(none_local).to(cuda_device)]).item() == 0
+
+
+# ------------------------------------------- full MiMo shape (decode) ---
+def _deq_mxfp4(wp, sc):
+    """[N, K/2] packed e2m1 + [N, K/32] e8m0 -> fp32 [N, K] on the GPU."""
+    lut = torch.tensor(R.FP4_LUT, device=wp.device)
+    N = wp.shape[0]
+    v = torch.stack([lut[(wp & 15).long()], lut[(wp >> 4).long()]], dim=-1).view(N, -1)
+    s = torch.exp2(sc.float() - 127.0)
+    return (v.view(N, -1, 32) * s[..., None]).view(N, -1)
+
+
+def _torch_ref_gpu(x, w1, s1, w2, s2, ids, tw, inter):
+    """Plain torch fp32 reference on the GPU: kernel-semantics 1x128 quant of
+    x and h, MXFP4 dequant of the touched experts' weights."""
+    T, H = x.shape
+
+    def q1x128(v):
+        g = v.float().view(v.shape[0], -1, 128)
+        amax = g.abs().amax(-1, keepdim=True).clamp_min(1e-10)
+        sc = amax * np.float32(1 / 448)
+        q = (g * (1.0 / sc)).clamp(-448, 448).to(torch.float8_e4m3fn).float()
+        return (q * sc).view_as(v)
+
+    a1 = q1x128(x)
+    out = torch.zeros(T, H, device=x.device)
+    for e in torch.unique(ids).tolist():
+        tok, slot = torch.nonzero(ids == e, as_tuple=True)
+        y = a1[tok] @ _deq_mxfp4(w1[e], s1[e]).T
+        h = (torch.nn.functional.silu(y[:, :inter]) * y[:, inter:]).to(torch.bfloat16)
+        a2 = q1x128(h)
+        out.index_add_(0, tok, (a2 @ _deq_mxfp4(w2[e], s2[e]).T) * tw[tok, slot][:, None])
+    return out.to(torch.bfloat16).float()
+
+
+def test_a8w4_mimo_decode_T32(cuda_device):
+    cfg = W.mimo_a8w4(32)
+    wts = W.make_weights(cfg, device=cuda_device, shuffle=False)
+    x = W.make_hidden(cfg, device=cuda_device)
+    tw, ids = W.make_routing(cfg, device=cuda_device)
+    ref = _torch_ref_gpu(x, wts["w1"], wts["w1_scale"], wts["w2"], wts["w2_scale"], ids, tw,
+                         cfg.inter_dim)
+    w1s, w2s = A.shuffle_weight(wts["w1"]), A.shuffle_weight(wts["w2"])
+    out = A.fused_moe(x, w1s, w2s, tw, ids, quant_type=A.QuantType.per_1x32,
+                      w1_scale=wts["w1_scale"], w2_scale=wts["w2_scale"])
+    _check(_np(ref), _np(out.float()), "A8W4 MiMo T=32")

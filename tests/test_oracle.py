@@ -246,3 +246,113 @@ def test_normalized_errors_known_values():
     rms_ref = np.sqrt((refn ** 2).mean())
     assert np.isclose(mx, 0.01 / rms_ref)
     assert np.isclose(rms, np.sqrt(((0.01 / rms_ref) ** 2) / 4))
+
+
+# ------------------------------------------------------------------ mxfp4 ---
+def _e2m1_from_fields(c: int) -> float:
+    s = -1.0 if c & 8 else 1.0
+    e, m = (c >> 1) & 3, c & 1
+    return s * (m * 0.5 if e == 0 else 2.0 ** (e - 1) * (1 + m / 2))
+
+
+def test_fp4_lut_is_e2m1():
+    for c in range(16):
+        v = _e2m1_from_fields(c)
+        assert R.FP4_LUT[c] == v and np.signbit(R.FP4_LUT[c]) == bool(c & 8)
+
+
+def _fp4_brute_force(x):
+    mags = np.array([_e2m1_from_fields(c) for c in range(8)])
+    out = []
+    for v in np.asarray(x, np.float32).astype(np.float64):
+        a = min(abs(v), 6.0)
+        d = np.abs(mags - a)
+        best = np.flatnonzero(d == d.min())
+        code = best[0] if len(best) == 1 else [b for b in best if b % 2 == 0][0]
+        out.append(code | (8 if np.signbit(v) else 0))
+    return np.array(out, np.uint8)
+
+
+def test_fp4_encode_matches_brute_force_nearest_even():
+    mags = np.array([_e2m1_from_fields(c) for c in range(8)])
+    mids = (mags[1:] + mags[:-1]) / 2
+    x = np.concatenate([np.linspace(-9, 9, 4001), mags, -mags, mids, -mids,
+                        np.nextafter(mids.astype(np.float32), np.float32(0)),
+                        np.nextafter(mids.astype(np.float32), np.float32(9)),
+                        [0.0, -0.0, 1e-30, -1e-30, 5.999, 6.0, 6.5, 1e30, -1e30]]).astype(np.float32)
+    np.testing.assert_array_equal(R.fp4_encode_rne_sat(x), _fp4_brute_force(x))
+    # ties go to the even code: 0.25->0, 0.75->1.0, 1.25->1.0, 1.75->2, 2.5->2, 3.5->4, 5->4
+    t = np.array([0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0], np.float32)
+    assert R.FP4_LUT[R.fp4_encode_rne_sat(t)].tolist() == [0.0, 1.0, 1.0, 2.0, 2.0, 4.0, 4.0]
+
+
+def test_fp4_pack_nibble_order():
+    assert R.fp4_pack(np.array([1, 2, 15, 0], np.uint8)).tolist() == [0x21, 0x0F]
+    assert R.mxfp4_decode(np.array([0x21], np.uint8)).tolist() == [0.5, 1.0]
+    c = np.random.default_rng(0).integers(0, 16, (3, 64)).astype(np.uint8)
+    np.testing.assert_array_equal(R.fp4_unpack(R.fp4_pack(c)), c)
+
+
+def test_e8m0_rounding_bracket_and_known_values():
+    known = {1.0: 127, 1.4999: 127, 1.5: 128, 2.0: 128, 2.99: 128, 3.0: 129, 0.75: 127,
+             0.5: 126, 0.7: 126, 2.0 ** -100: 27}
+    for x, e in known.items():
+        assert int(R.f32_to_e8m0(np.float32(x))) == e, x
+    rng = np.random.default_rng(1)
+    x = np.exp2(rng.uniform(-100, 100, 20000)).astype(np.float32)
+    s = R.e8m0_to_f32(R.f32_to_e8m0(x)).astype(np.float64)
+    r = x.astype(np.float64) / s
+    assert (r >= 0.75).all() and (r < 1.5).all()
+    k = np.arange(-126, 128)
+    np.testing.assert_array_equal(R.e8m0_to_f32(R.f32_to_e8m0(np.exp2(k).astype(np.float32))),
+                                  np.exp2(k).astype(np.float32))
+    assert R.e8m0_to_f32(np.uint8(0)) == np.float32(2.0 ** -127)
+    assert np.isnan(R.e8m0_to_f32(np.uint8(255)))
+
+
+def test_mxfp4_weight_quant_bounds():
+    rng = np.random.default_rng(2)
+    w = (rng.standard_normal((2, 48, 256)) * 0.02).astype(np.float32)
+    w[0, 0, :32] = 0.0                                  # all-zero block
+    packed, sc = R.quant_weight_mxfp4(w)
+    assert packed.shape == (2, 48, 128) and sc.shape == (2, 48, 8)
+    dq = R.dequant_weight_mxfp4(packed, sc)
+    s = R.e8m0_to_f32(sc).astype(np.float64)
+    blocks = w.reshape(2, 48, 8, 32).astype(np.float64)
+    amax = np.abs(blocks).max(-1)
+    nz = amax > 0
+    # scale = e8m0(amax/4) => amax / s in [3, 6): the block max never saturates
+    ratio = amax[nz] / s[nz]
+    assert (ratio >= 3).all() and (ratio < 6).all()
+    # each element is the nearest e2m1 value of w/s: error <= half the grid step
+    y = np.abs(blocks) / s[..., None]
+    step = np.where(y < 2, 0.5, np.where(y < 4, 1.0, 2.0))
+    err = np.abs(dq.reshape(blocks.shape) - blocks)
+    assert (err <= step * s[..., None] / 2 + 1e-12).all()
+    np.testing.assert_array_equal(R.fp4_unpack(packed).reshape(blocks.shape),
+                                  _fp4_brute_force((blocks / s[..., None]).ravel()).reshape(
+                                      blocks.shape))
+    assert (dq[0, 0, :32] == 0).all()
+
+
+def test_a8w4_layer_oracle_vs_fp64_brute_force():
+    rng = np.random.default_rng(3)
+    T, H, I, E, k = 5, 256, 128, 3, 2
+    x = R.bf16_round(rng.standard_normal((T, H)).astype(np.float32))
+    w1p, w1s = R.quant_weight_mxfp4((rng.standard_normal((E, 2 * I, H)) * 0.05).astype(np.float32))
+    w2p, w2s = R.quant_weight_mxfp4((rng.standard_normal((E, H, I)) * 0.05).astype(np.float32))
+    ids = np.array([[0, 2], [1, 0], [2, 1], [0, 1], [2, 0]])
+    tw = rng.uniform(0.1, 1, (T, k)).astype(np.float32)
+    ref = R.fused_moe_ref(x, w1p, w1s, w2p, w2s, ids, tw, weight_format="mxfp4")
+    # fp64 brute force on the same quantised operands
+    aq, as_ = R.quant_1x128_kernel(x)
+    a = R.fp8_decode(aq).astype(np.float64) * np.repeat(as_, 128, axis=1)
+    W1 = np.stack([np.array([[R.FP4_LUT[(w1p[e, n, kk // 2] >> (4 * (kk % 2))) & 15]
+                              * 2.0 ** (int(w1s[e, n, kk // 32]) - 127) for kk in range(H)]
+                             for n in range(2 * I)]) for e in range(E)])
+    h = np.zeros((T, k, I))
+    for t in range(T):
+        for j in range(k):
+            y = W1[ids[t, j]] @ a[t]
+            h[t, j] = y[:I] / (1 + np.exp(-y[:I])) * y[I:]
+    np.testing.assert_allclose(ref["h"], h, rtol=1e-2, atol=1e-3 * np.abs(h).max())
