@@ -45,6 +45,17 @@ void launch_moe_stage2_fp8bs_v2(const uint8_t*, const float*, const uint8_t*, co
                                 const int32_t*, float*, int64_t, int64_t, int64_t, int64_t,
                                 int64_t, int64_t, int64_t, int, hipStream_t);
 
+// moe_gemm_stream.hip (16/32-row M-blocks, weights streamed into registers)
+bool stream_supported(int64_t block_m, int64_t K);
+void launch_moe_stage1_stream(const uint8_t*, const float*, int64_t, int64_t, const uint8_t*,
+                              const float*, const uint8_t*, const int32_t*, const int32_t*,
+                              const int32_t*, uint8_t*, float*, int64_t, int64_t, int64_t,
+                              int64_t, int64_t, int64_t, int64_t, int, hipStream_t);
+void launch_moe_stage2_stream(const uint8_t*, const float*, const uint8_t*, const float*,
+                              const uint8_t*, const int32_t*, const float*, const int32_t*,
+                              const int32_t*, float*, int64_t, int64_t, int64_t, int64_t,
+                              int64_t, int64_t, int64_t, int, hipStream_t);
+
 // Weight scales of one layer: fp32 128x128 blocks (fp8 weights) or e8m0
 // bytes per 1x32 K block (MXFP4 weights); exactly one is set.
 struct WScale {
@@ -52,15 +63,20 @@ struct WScale {
     const uint8_t* e8m0;
 };
 
-// Kernel choice per shape: M-blocks of 64/128 rows with K a multiple of 256
-// (and, for stage 2, 256-column output tiles) take the large-tile
-// direct-to-LDS kernels; 16/32-row blocks (decode) the streaming kernels.
+// Kernel choice per shape: 16/32-row M-blocks (decode-sized layers) take the
+// register-streaming kernels, 64/128-row M-blocks the large-tile
+// direct-to-LDS kernels (stage 2 of both needs 256-column output tiles,
+// model_dim % 256 == 0); other shapes the general kernels of
+// moe_gemm_fp8bs.hip.
 static void stage1_dispatch(const uint8_t* a, const float* sa, int64_t sa_row, int64_t sa_kb,
                             const uint8_t* w1, WScale w1s, const int32_t* sid,
                             const int32_t* seid, const int32_t* nv, uint8_t* a2, float* a2s,
                             int64_t a_rows, int64_t K, int64_t I, int64_t E, int64_t topk,
                             int64_t bm, int64_t mblocks, int sh, hipStream_t s) {
-    if (v2_supported(bm, K))
+    if (stream_supported(bm, K))
+        launch_moe_stage1_stream(a, sa, sa_row, sa_kb, w1, w1s.f32, w1s.e8m0, sid, seid, nv, a2,
+                                 a2s, a_rows, K, I, E, topk, bm, mblocks, sh, s);
+    else if (v2_supported(bm, K))
         launch_moe_stage1_fp8bs_v2(a, sa, sa_row, sa_kb, w1, w1s.f32, w1s.e8m0, sid, seid, nv, a2,
                                    a2s, a_rows, K, I, E, topk, bm, mblocks, sh, s);
     else
@@ -73,7 +89,10 @@ static void stage2_dispatch(const uint8_t* a2, const float* a2s, const uint8_t* 
                             const int32_t* seid, const int32_t* nv, float* acc, int64_t a_rows,
                             int64_t I, int64_t H, int64_t E, int64_t topk, int64_t bm,
                             int64_t mblocks, int sh, hipStream_t s) {
-    if (v2_supported(bm, I) && H % 256 == 0)
+    if (stream_supported(bm, I) && H % 256 == 0)
+        launch_moe_stage2_stream(a2, a2s, w2, w2s.f32, w2s.e8m0, sid, sw, seid, nv, acc, a_rows,
+                                 I, H, E, topk, bm, mblocks, sh, s);
+    else if (v2_supported(bm, I) && H % 256 == 0)
         launch_moe_stage2_fp8bs_v2(a2, a2s, w2, w2s.f32, w2s.e8m0, sid, sw, seid, nv, acc, a_rows,
                                    I, H, E, topk, bm, mblocks, sh, s);
     else
@@ -158,11 +177,13 @@ FusedLayout fused_layout(int64_t T, int64_t H, int64_t I, int64_t E_sort, int64_
 
 int64_t default_block_m(int64_t tokens, int64_t topk, int64_t E, int64_t model_dim,
                         int64_t inter_dim) {
+    // measured on MI355X (MiMo shape, FP8 and A8W4): 16-row blocks while experts
+    // average <= 8 rows, 32 up to ~20, then 64; 128-row tiles halve the weight
+    // re-reads once experts average >= 64 rows
     const int64_t avg = E > 0 ? tokens * topk / E : 0;
     if (avg <= 8) return 16;
-    if (avg <= 48) return 32;
-    // 128-row tiles halve the B (weight) re-reads; worth it once padding is a small fraction
-    if (avg >= 128 && v2_supported(128, model_dim) && v2_supported(128, inter_dim) &&
+    if (avg <= 20) return 32;
+    if (avg >= 64 && v2_supported(128, model_dim) && v2_supported(128, inter_dim) &&
         model_dim % 256 == 0)
         return 128;
     return 64;

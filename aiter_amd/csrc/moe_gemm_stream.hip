@@ -1,0 +1,417 @@
+// Decode-shaped MoE gather-GEMMs for gfx950: the weights stream from HBM
+// straight into MFMA operand registers, D K-steps in flight per wave.
+//
+// Same contract as moe_gemm_fp8bs.hip (stage 1: gate+up GEMM, SiLU*up, bf16
+// rounding, fused 1x128 fp8 requant; stage 2: down GEMM, routing weight,
+// fp32 atomic accumulate; FP8 128x128 blockscale or MXFP4 weights), for
+// M-blocks of 16 or 32 sorted rows -- the token counts where a layer is a
+// pass over the touched experts' weights and the MFMA work is small.
+//
+// Why registers and not LDS: at decode sizes the kernel is bound by how many
+// weight bytes each CU keeps in flight.  LDS (160 KB per CU) caps a staged
+// pipeline near 128 KB; the register file holds far more.  Every lane loads
+// exactly its own MFMA fragments: in the (16,16)-shuffled layout a 16-row
+// group's K block is [K/32][2][16 rows][16 B], so lane (q = lane/16,
+// r = lane%16) takes the 16-byte pieces at q*512 + r*16 and +256 (fp8; for
+// packed fp4 the block is 1 KB and lane l's piece sits at l*16); row-major
+// weights give the same fragments as contiguous pieces of row r.  Nothing is
+// shared between waves, so there is no barrier in the K loop.
+//
+// Workgroup: 256 threads = 4 waves; one M-block (BM rows) x 256 weight rows
+// (stage 1: 128 gate rows + the matching 128 up rows = 128 outputs; stage 2:
+// 256 outputs).  Wave w owns 4 16-row weight groups (stage 1: gate rows
+// 32w..32w+31 and the same up rows), so each K step is BM/16 * 4 MFMAs.
+// The K loop is unrolled by D with D operand buffers: step k computes from
+// buffer k % D and then refills it with step k + D, so D steps of loads are
+// always outstanding and the compiler's wait counts target the oldest.
+// Weight loads are non-temporal: each weight byte is used by one workgroup
+// once, so it should not displace the activations and scales in the caches.
+#include "common.h"
+
+namespace aiter_amd {
+
+namespace stream {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = 4;
+constexpr int kNCT = 4;      // 16-row weight groups (MFMA column tiles) per wave
+constexpr int kMaxKB = 64;   // K <= 8192
+
+struct Args {
+    const uint8_t* a;          // activation rows, fp8 [a_rows, K]
+    const float* a_scale;      // a_scale[row*sa_row + kb*sa_kb]
+    int64_t sa_row;
+    int64_t sa_kb;
+    const uint8_t* w;          // fp8 [E, N, K] or packed e2m1 [E, N, K/2]
+    const float* w_scale;      // [E, N/128, K/128] (fp8 weights)
+    const uint8_t* w_scale8;   // [E, N, K/32] e8m0 (MXFP4 weights)
+    const int32_t* sorted_ids;
+    const float* sorted_w;
+    const int32_t* sorted_eids;
+    const int32_t* num_valid;
+    uint8_t* a2;
+    float* a2_scale;
+    float* acc;
+    int K;
+    int N;                     // weight rows per expert
+    int inter;
+    int topk;
+    int E;
+    int64_t a_rows;
+};
+
+// One K step of one wave's operands.
+template <int NRT, bool W4>
+struct Step {
+    v4i a[NRT][2];
+    v4i b[kNCT][W4 ? 1 : 2];
+    int bs[kNCT];              // e8m0 byte per column tile (A8W4)
+};
+
+template <int BM, int STAGE, bool SHUFFLED, bool W4, int D>
+__global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
+    constexpr int NRT = BM / 16;
+    static_assert(BM == 16 || BM == 32, "stream tiles are 16 or 32 rows");
+    __shared__ __attribute__((aligned(16))) float s_sa[kMaxKB * BM];   // [kb][row]
+    __shared__ float s_sw[2][kMaxKB];
+    __shared__ int32_t s_arow[BM];
+    __shared__ int64_t s_orow[BM];
+    __shared__ float s_w[BM];
+    __shared__ float s_amax[kWaves][BM];
+    __shared__ __attribute__((aligned(16))) uint8_t s_q[STAGE == 1 ? BM * 144 : 16];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wv = tid >> 6;
+    const int lr = lane & 15;
+    const int lq = lane >> 4;
+
+    const int mb = blockIdx.y;
+    const int nvalid = g.num_valid[0];
+    if (mb * BM >= nvalid) return;
+    const int tokens = g.num_valid[1];
+    const int e = g.sorted_eids[mb];
+    if (e < 0 || e >= g.E) return;
+    const int n0 = blockIdx.x * (STAGE == 1 ? 128 : 256);
+
+    for (int r = tid; r < BM; r += kThreads) {
+        const uint32_t id = (uint32_t)g.sorted_ids[mb * BM + r];
+        const int t = (int)(id & 0xFFFFFFu);
+        const int s = (int)(id >> 24);
+        const bool valid = t < tokens && s < g.topk;
+        const int64_t pair = (int64_t)t * g.topk + s;
+        int64_t arow = -1, orow = -1;
+        if (valid) {
+            arow = STAGE == 1 ? (int64_t)t : pair;
+            orow = STAGE == 1 ? pair : (int64_t)t;
+            if (arow >= g.a_rows) arow = orow = -1;
+        }
+        s_arow[r] = (int32_t)arow;
+        s_orow[r] = orow;
+        s_w[r] = STAGE == 2 && valid ? g.sorted_w[mb * BM + r] : 0.0f;
+    }
+    __syncthreads();
+
+    const int K = g.K;
+    const int KB = K / 128;
+    const int KBY = W4 ? K / 2 : K;
+    // activation scales of the block's rows, [kb][row]; weight-scale blocks
+    // of the tile (stage 1: gate / up; stage 2: the two 128-column halves)
+    for (int i = tid; i < BM * KB; i += kThreads) {
+        const int r = i % BM, kb = i / BM;
+        const int arow = s_arow[r];
+        s_sa[kb * BM + r] = arow >= 0 ? g.a_scale[arow * g.sa_row + kb * g.sa_kb] : 0.0f;
+    }
+    if (!W4) {
+        const float* wse = g.w_scale + (int64_t)e * (g.N / 128) * KB;
+        const int nb0 = n0 / 128;
+        const int nb1 = STAGE == 1 ? (g.inter + n0) / 128 : n0 / 128 + 1;
+        for (int i = tid; i < 2 * KB; i += kThreads)
+            s_sw[i / KB][i % KB] = wse[(i < KB ? nb0 : nb1) * KB + (i % KB)];
+    }
+    __syncthreads();
+
+    // ---- per-lane operand sources (K step 0) ----
+    const uint8_t* we = g.w + (int64_t)e * g.N * KBY;
+    const uint8_t* bsrc[kNCT];
+    const uint8_t* bssrc[kNCT];
+#pragma unroll
+    for (int ct = 0; ct < kNCT; ++ct) {
+        int row0;
+        if (STAGE == 1)
+            row0 = ct < 2 ? n0 + 32 * wv + 16 * ct : g.inter + n0 + 32 * wv + 16 * (ct - 2);
+        else
+            row0 = n0 + 64 * wv + 16 * ct;
+        if (W4)
+            bsrc[ct] = SHUFFLED ? we + (int64_t)row0 * KBY + lane * 16
+                                : we + (int64_t)(row0 + lr) * KBY + lq * 16;
+        else
+            bsrc[ct] = SHUFFLED ? we + (int64_t)row0 * K + lq * 512 + lr * 16
+                                : we + (int64_t)(row0 + lr) * K + lq * 32;
+        bssrc[ct] = W4 ? g.w_scale8 + ((int64_t)e * g.N + row0 + lr) * (K / 32) + lq : nullptr;
+    }
+    constexpr int BSTEP = W4 ? (SHUFFLED ? 1024 : 64) : (SHUFFLED ? 2048 : 128);
+    constexpr int BHI = SHUFFLED ? 256 : 16;       // fp8: offset of the fragment's second half
+    constexpr int AHI = W4 ? 64 : 16;              // second half of the A fragment
+    const uint8_t* asrc[NRT];
+#pragma unroll
+    for (int rt = 0; rt < NRT; ++rt) {
+        int arow = s_arow[rt * 16 + lr];
+        if (arow < 0) arow = 0;                    // pad rows: any valid row, result unused
+        asrc[rt] = g.a + (int64_t)arow * K + (W4 ? lq * 16 : lq * 32);
+    }
+
+    using S = Step<NRT, W4>;
+    auto load = [&](S& s, int kb) {
+#pragma unroll
+        for (int ct = 0; ct < kNCT; ++ct) {
+            const uint8_t* p = bsrc[ct] + (int64_t)kb * BSTEP;
+            s.b[ct][0] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(p));
+            if (!W4)
+                s.b[ct][W4 ? 0 : 1] =
+                    __builtin_nontemporal_load(reinterpret_cast<const v4i*>(p + BHI));
+            if (W4) s.bs[ct] = bssrc[ct][kb * 4];
+        }
+#pragma unroll
+        for (int rt = 0; rt < NRT; ++rt) {
+            const uint8_t* p = asrc[rt] + kb * 128;
+            s.a[rt][0] = *reinterpret_cast<const v4i*>(p);
+            s.a[rt][1] = *reinterpret_cast<const v4i*>(p + AHI);
+        }
+    };
+
+    v4f acc[NRT][kNCT];
+#pragma unroll
+    for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < kNCT; ++ct) acc[rt][ct] = v4f{0.f, 0.f, 0.f, 0.f};
+
+    auto compute = [&](const S& s, int kb) {
+        // stage 1: tiles 0,1 gate (scale block 0), 2,3 up (block 1); stage 2:
+        // the wave's 64 columns lie in 128-column block wv/2
+        const float sw0 = W4 ? 1.0f : s_sw[STAGE == 1 ? 0 : (wv >> 1)][kb];
+        const float sw1 = W4 ? 1.0f : s_sw[STAGE == 1 ? 1 : (wv >> 1)][kb];
+#pragma unroll
+        for (int rt = 0; rt < NRT; ++rt) {
+            const v4f sa = *reinterpret_cast<const v4f*>(&s_sa[kb * BM + rt * 16 + 4 * lq]);
+            const v8i af = v8i{s.a[rt][0][0], s.a[rt][0][1], s.a[rt][0][2], s.a[rt][0][3],
+                               s.a[rt][1][0], s.a[rt][1][1], s.a[rt][1][2], s.a[rt][1][3]};
+#pragma unroll
+            for (int ct = 0; ct < kNCT; ++ct) {
+                v4f blk;
+                if (W4) {
+                    const v8i bf = v8i{s.b[ct][0][0], s.b[ct][0][1], s.b[ct][0][2],
+                                       s.b[ct][0][3], 0, 0, 0, 0};
+                    blk = mfma16x16x128_fp8_fp4(af, bf, s.bs[ct]);
+                } else {
+                    const v8i bf = v8i{s.b[ct][0][0], s.b[ct][0][1], s.b[ct][0][2],
+                                       s.b[ct][0][3], s.b[ct][W4 ? 0 : 1][0],
+                                       s.b[ct][W4 ? 0 : 1][1], s.b[ct][W4 ? 0 : 1][2],
+                                       s.b[ct][W4 ? 0 : 1][3]};
+                    blk = mfma16x16x128_fp8(af, bf);
+                }
+                const float sw = ct < 2 ? sw0 : sw1;
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+                    acc[rt][ct][v] += W4 ? blk[v] * sa[v] : blk[v] * (sa[v] * sw);
+            }
+        }
+    };
+
+    // ---- K loop: D steps in flight ----
+    S buf[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) load(buf[d], d);
+    for (int kb0 = 0; kb0 < KB - D; kb0 += D) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            compute(buf[d], kb0 + d);
+            load(buf[d], kb0 + d + D);
+        }
+    }
+#pragma unroll
+    for (int d = 0; d < D; ++d) compute(buf[d], KB - D + d);
+
+    if (STAGE == 2) {
+#pragma unroll
+        for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int row = rt * 16 + 4 * lq + v;
+                const int64_t t = s_orow[row];
+                if (t < 0) continue;
+                const float wgt = s_w[row];
+                float* dst = g.acc + t * g.N + n0 + 64 * wv + lr;
+#pragma unroll
+                for (int ct = 0; ct < kNCT; ++ct) unsafeAtomicAdd(dst + 16 * ct, acc[rt][ct][v] * wgt);
+            }
+        return;
+    }
+
+    // ---- stage 1 epilogue: silu(gate)*up -> bf16 -> 1x128 fp8 requant ----
+    // wave wv holds output columns 32*wv + 16*j + lr (j = 0, 1) of the tile's 128
+    float h[NRT][2][4];
+#pragma unroll
+    for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+                h[rt][j][v] = bf16_round(silu_f32(acc[rt][j][v]) * acc[rt][2 + j][v]);
+#pragma unroll
+    for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            float m = __builtin_fmaxf(__builtin_fabsf(h[rt][0][v]), __builtin_fabsf(h[rt][1][v]));
+            m = warp_max_16(m);
+            if (lr == 0) s_amax[wv][rt * 16 + 4 * lq + v] = m;
+        }
+    __syncthreads();
+    auto row_amax = [&](int row) {
+        const float m = __builtin_fmaxf(__builtin_fmaxf(s_amax[0][row], s_amax[1][row]),
+                                        __builtin_fmaxf(s_amax[2][row], s_amax[3][row]));
+        return __builtin_fmaxf(m, 1e-10f);
+    };
+#pragma unroll
+    for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int row = rt * 16 + 4 * lq + v;
+            const float inv = 1.0f / (row_amax(row) * kInvFp8Max);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const uint32_t b = f32x2_to_fp8x2(h[rt][j][v] * inv, 0.0f) & 0xFFu;
+                s_q[row * 144 + 32 * wv + 16 * j + lr] = (uint8_t)b;
+            }
+        }
+    __syncthreads();
+    const int I = g.inter;
+    for (int q = tid; q < BM * 8; q += kThreads) {
+        const int row = q >> 3, part = q & 7;
+        const int64_t orow = s_orow[row];
+        if (orow < 0) continue;
+        *reinterpret_cast<v4i*>(g.a2 + orow * I + n0 + part * 16) =
+            *reinterpret_cast<const v4i*>(s_q + row * 144 + part * 16);
+        if (part == 0) g.a2_scale[orow * (I / 128) + n0 / 128] = row_amax(row) * kInvFp8Max;
+    }
+}
+
+// K steps in flight: as many as divide the K-step count, up to the depth
+// the registers of the tile allow.
+template <int BM>
+constexpr int max_depth() { return BM == 16 ? 4 : 2; }
+
+template <int BM, int STAGE, bool SHUFFLED, bool W4>
+static void launch_depth(int KB, dim3 grid, const Args& a, hipStream_t s) {
+    constexpr int DM = max_depth<BM>();
+    if (DM >= 4 && KB % 4 == 0)
+        hipLaunchKernelGGL((moe_gemm_stream_kernel<BM, STAGE, SHUFFLED, W4, DM >= 4 ? 4 : 2>),
+                           grid, dim3(kThreads), 0, s, a);
+    else if (KB % 2 == 0)
+        hipLaunchKernelGGL((moe_gemm_stream_kernel<BM, STAGE, SHUFFLED, W4, 2>), grid,
+                           dim3(kThreads), 0, s, a);
+    else
+        hipLaunchKernelGGL((moe_gemm_stream_kernel<BM, STAGE, SHUFFLED, W4, 1>), grid,
+                           dim3(kThreads), 0, s, a);
+}
+
+template <int STAGE, bool SHUFFLED, bool W4>
+static void launch_bm(int bm, int KB, dim3 grid, const Args& a, hipStream_t s) {
+    if (bm == 16)
+        launch_depth<16, STAGE, SHUFFLED, W4>(KB, grid, a, s);
+    else if (bm == 32)
+        launch_depth<32, STAGE, SHUFFLED, W4>(KB, grid, a, s);
+    else
+        AMD_CHECK(false, "streaming GEMM block_m must be 16 or 32");
+}
+
+template <int STAGE>
+static void launch(int bm, int KB, dim3 grid, const Args& a, int shuffled, hipStream_t s) {
+    const bool w4 = a.w_scale8 != nullptr;
+    if (w4) {
+        if (shuffled)
+            launch_bm<STAGE, true, true>(bm, KB, grid, a, s);
+        else
+            launch_bm<STAGE, false, true>(bm, KB, grid, a, s);
+    } else {
+        if (shuffled)
+            launch_bm<STAGE, true, false>(bm, KB, grid, a, s);
+        else
+            launch_bm<STAGE, false, false>(bm, KB, grid, a, s);
+    }
+}
+
+}  // namespace stream
+
+// 16/32-row M-blocks, K a multiple of 128 up to 8192; stage 2 also needs
+// 256-column output tiles (model_dim % 256 == 0).
+bool stream_supported(int64_t block_m, int64_t K) {
+    return (block_m == 16 || block_m == 32) && K > 0 && K % 128 == 0 &&
+           K / 128 <= stream::kMaxKB;
+}
+
+void launch_moe_stage1_stream(const uint8_t* a, const float* a_scale, int64_t sa_row,
+                              int64_t sa_kb, const uint8_t* w1, const float* w1_scale,
+                              const uint8_t* w1_scale_e8m0, const int32_t* sorted_ids,
+                              const int32_t* sorted_eids, const int32_t* num_valid, uint8_t* a2,
+                              float* a2_scale, int64_t a_rows, int64_t K, int64_t inter,
+                              int64_t E, int64_t topk, int64_t block_m, int64_t max_m_blocks,
+                              int shuffled, hipStream_t stream) {
+    stream::Args g{};
+    g.a = a;
+    g.a_scale = a_scale;
+    g.sa_row = sa_row;
+    g.sa_kb = sa_kb;
+    g.w = w1;
+    g.w_scale = w1_scale;
+    g.w_scale8 = w1_scale_e8m0;
+    g.sorted_ids = sorted_ids;
+    g.sorted_eids = sorted_eids;
+    g.num_valid = num_valid;
+    g.a2 = a2;
+    g.a2_scale = a2_scale;
+    g.K = (int)K;
+    g.N = (int)(2 * inter);
+    g.inter = (int)inter;
+    g.topk = (int)topk;
+    g.E = (int)E;
+    g.a_rows = a_rows;
+    if (max_m_blocks == 0) return;
+    const dim3 grid((unsigned)(inter / 128), (unsigned)max_m_blocks);
+    stream::launch<1>((int)block_m, (int)(K / 128), grid, g, shuffled, stream);
+    AMD_HIP_CHECK(hipGetLastError());
+}
+
+void launch_moe_stage2_stream(const uint8_t* a2, const float* a2_scale, const uint8_t* w2,
+                              const float* w2_scale, const uint8_t* w2_scale_e8m0,
+                              const int32_t* sorted_ids, const float* sorted_w,
+                              const int32_t* sorted_eids, const int32_t* num_valid, float* acc,
+                              int64_t a_rows, int64_t inter, int64_t hidden, int64_t E,
+                              int64_t topk, int64_t block_m, int64_t max_m_blocks, int shuffled,
+                              hipStream_t stream) {
+    stream::Args g{};
+    g.a = a2;
+    g.a_scale = a2_scale;
+    g.sa_row = inter / 128;
+    g.sa_kb = 1;
+    g.w = w2;
+    g.w_scale = w2_scale;
+    g.w_scale8 = w2_scale_e8m0;
+    g.sorted_ids = sorted_ids;
+    g.sorted_w = sorted_w;
+    g.sorted_eids = sorted_eids;
+    g.num_valid = num_valid;
+    g.acc = acc;
+    g.K = (int)inter;
+    g.N = (int)hidden;
+    g.inter = (int)inter;
+    g.topk = (int)topk;
+    g.E = (int)E;
+    g.a_rows = a_rows;
+    if (max_m_blocks == 0) return;
+    const dim3 grid((unsigned)(hidden / 256), (unsigned)max_m_blocks);
+    stream::launch<2>((int)block_m, (int)(inter / 128), grid, g, shuffled, stream);
+    AMD_HIP_CHECK(hipGetLastError());
+}
+
+}  // namespace aiter_amd

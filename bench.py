@@ -6,9 +6,12 @@ Zipf(1.1)-skewed routing, fp8 e4m3fn 128x128 weight scales, 1x128 activation
 scales, bf16 in/out.  A step is one aiter_amd.fused_moe call (sorting,
 activation quant, stage 1, stage 2, output conversion) on inputs resident
 in HBM.  The decode leg (T=32, uniform softmax routing) is reported under
-"decode".  Prints one JSON line.
+"decode"; the other single-GPU configurations -- A8W4 (fp8 activations x
+MXFP4 weights) at T=32/1024/8192 and the expert-parallel share (32 of 256
+experts, T=4096) -- under "legs".  Prints one JSON line.
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload prefill8192|decode32]
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload prefill8192|decode32|...]
+                  [--legs a8w4_32,a8w4_1024,a8w4_8192,ep4096|none]
 """
 from __future__ import annotations
 
@@ -25,14 +28,24 @@ PEAK_FP8_FLOPS = 5.0e15   # MI355X dense fp8 MFMA
 PEAK_HBM_BPS = 8.0e12     # MI355X HBM3E
 
 
+def _workload(name):
+    import re
+
+    if not re.fullmatch(r"(prefill|decode|a8w4_|ep)[1-9][0-9]*", name):
+        raise argparse.ArgumentTypeError(f"unknown workload {name!r}")
+    return name
+
+
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
-    p.add_argument("--workload", default="prefill8192",
-                   choices=["prefill8192", "prefill2048", "decode32", "decode1", "decode128",
-                            "ep4096"])
+    p.add_argument("--workload", default="prefill8192", type=_workload,
+                   help="prefill<T> | decode<T> | a8w4_<T> | ep<T> (e.g. prefill8192, "
+                        "decode32, a8w4_1024, ep4096)")
+    p.add_argument("--legs", default="a8w4_32,a8w4_1024,a8w4_8192,ep4096",
+                   help="comma-separated extra workloads reported under 'legs' ('none': skip)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-decode", action="store_true")
     p.add_argument("--kernel-iters", type=int, default=10)
@@ -54,6 +67,8 @@ def make_cfg(name):
         return W.mimo_prefill(int(name[len("prefill"):]))
     if name.startswith("decode"):
         return W.mimo_decode(int(name[len("decode"):]))
+    if name.startswith("a8w4_"):
+        return W.mimo_a8w4(int(name[len("a8w4_"):]))
     return W.mimo_ep_share(int(name[len("ep"):]))
 
 
@@ -82,13 +97,34 @@ class Layer:
             self.distinct = int(torch.unique(ids).numel())
         torch.cuda.synchronize()
 
+    @property
+    def a8w4(self):
+        return self.cfg.weights == "mxfp4"
+
     def run(self):
         import aiter_amd as A
 
+        qt = A.QuantType.per_1x32 if self.a8w4 else A.QuantType.per_128x128
         return A.fused_moe(self.x, self.w["w1"], self.w["w2"], self.tw, self.ids,
-                           expert_mask=self.mask, quant_type=A.QuantType.per_128x128,
+                           expert_mask=self.mask, quant_type=qt,
                            w1_scale=self.w["w1_scale"], w2_scale=self.w["w2_scale"],
                            block_size_M=self.block_m or None)
+
+    def stages(self):
+        """(stage-1 fn, stage-2 fn) of this layer's weight format."""
+        import aiter_amd as A
+
+        if self.a8w4:
+            return A.moe_stage1_a8w4, A.moe_stage2_a8w4
+        return A.moe_stage1_fp8_blockscale, A.moe_stage2_fp8_blockscale
+
+    def block_m_used(self):
+        import aiter_amd as A
+
+        cfg = self.cfg
+        return self.block_m or A.default_block_m(cfg.tokens, cfg.topk,
+                                                 cfg.local_experts or cfg.experts,
+                                                 cfg.model_dim, cfg.inter_dim)
 
 
 def time_steps(fn, steps, warmup):
@@ -118,14 +154,13 @@ def stage_kernel_times(layer, iters):
     import aiter_amd as A
 
     cfg = layer.cfg
-    bm = layer.block_m or A.default_block_m(cfg.tokens, cfg.topk, cfg.local_experts or cfg.experts,
-                                          cfg.model_dim, cfg.inter_dim)
+    bm = layer.block_m_used()
+    st1, st2 = layer.stages()
     E_sort = cfg.experts
     sid, sw, se, nv, acc = A.moe_sorting(layer.ids, layer.tw, E_sort, cfg.model_dim,
                                          torch.float32, bm, layer.mask)
     a1, a1s = A.per_group_quant_hip(layer.x)
-    a2, a2s = A.moe_stage1_fp8_blockscale(a1, a1s, layer.w["w1"], layer.w["w1_scale"], sid, se,
-                                          nv, cfg.topk, bm, True)
+    a2, a2s = st1(a1, a1s, layer.w["w1"], layer.w["w1_scale"], sid, se, nv, cfg.topk, bm, True)
     torch.cuda.synchronize()
 
     def timed(fn):
@@ -140,10 +175,10 @@ def stage_kernel_times(layer, iters):
         torch.cuda.synchronize()
         return s.elapsed_time(e) / iters * 1e-3
 
-    t1 = timed(lambda: A.moe_stage1_fp8_blockscale(a1, a1s, layer.w["w1"], layer.w["w1_scale"],
-                                                   sid, se, nv, cfg.topk, bm, True))
-    t2 = timed(lambda: A.moe_stage2_fp8_blockscale(a2, a2s, layer.w["w2"], layer.w["w2_scale"],
-                                                   sid, sw, se, nv, acc, bm, True))
+    t1 = timed(lambda: st1(a1, a1s, layer.w["w1"], layer.w["w1_scale"], sid, se, nv, cfg.topk,
+                           bm, True))
+    t2 = timed(lambda: st2(a2, a2s, layer.w["w2"], layer.w["w2_scale"], sid, sw, se, nv, acc,
+                           bm, True))
     tq = timed(lambda: A.per_group_quant_hip(layer.x))
     ts = timed(lambda: A.moe_sorting(layer.ids, layer.tw, E_sort, cfg.model_dim, torch.float32,
                                      bm, layer.mask))
@@ -163,30 +198,33 @@ def kernel_only(layer, which, steps):
     for _ in range(3):
         dst.copy_(src)
     cfg = layer.cfg
-    bm = layer.block_m or A.default_block_m(cfg.tokens, cfg.topk, cfg.local_experts or cfg.experts,
-                                          cfg.model_dim, cfg.inter_dim)
+    bm = layer.block_m_used()
+    st1, st2 = layer.stages()
     sid, sw, se, nv, acc = A.moe_sorting(layer.ids, layer.tw, cfg.experts, cfg.model_dim,
                                          torch.float32, bm, layer.mask)
     a1, a1s = A.per_group_quant_hip(layer.x)
-    a2, a2s = A.moe_stage1_fp8_blockscale(a1, a1s, layer.w["w1"], layer.w["w1_scale"], sid, se,
-                                          nv, cfg.topk, bm, True)
+    a2, a2s = st1(a1, a1s, layer.w["w1"], layer.w["w1_scale"], sid, se, nv, cfg.topk, bm, True)
     torch.cuda.synchronize()
     for _ in range(steps):
         if which == "stage1":
-            A.moe_stage1_fp8_blockscale(a1, a1s, layer.w["w1"], layer.w["w1_scale"], sid, se, nv,
-                                        cfg.topk, bm, True)
+            st1(a1, a1s, layer.w["w1"], layer.w["w1_scale"], sid, se, nv, cfg.topk, bm, True)
         else:
-            A.moe_stage2_fp8_blockscale(a2, a2s, layer.w["w2"], layer.w["w2_scale"], sid, sw, se,
-                                        nv, acc, bm, True)
+            st2(a2, a2s, layer.w["w2"], layer.w["w2_scale"], sid, sw, se, nv, acc, bm, True)
     torch.cuda.synchronize()
     log(f"kernel-only {which}: {steps} launches done")
 
 
 def stage1_work(layer):
+    """Algorithmic FLOPs and HBM bytes of one stage-1 launch: P routed pairs x
+    2I x H MACs; bytes = the D touched experts' w1 (+ scales), x in fp8 + its
+    scales, a2 out in fp8 + scales, and the sorted ids."""
     cfg = layer.cfg
     H, I, P, D, T = cfg.model_dim, cfg.inter_dim, layer.pairs, layer.distinct, cfg.tokens
     flops = 2.0 * P * (2 * I) * H
-    w_bytes = D * (2 * I * H + 4 * (2 * I // 128) * (H // 128))
+    if layer.a8w4:
+        w_bytes = D * (2 * I * H // 2 + 2 * I * H // 32)
+    else:
+        w_bytes = D * (2 * I * H + 4 * (2 * I // 128) * (H // 128))
     act_bytes = T * H + T * (H // 128) * 4 + P * I + P * (I // 128) * 4 + P * 4
     return flops, float(w_bytes + act_bytes)
 
@@ -228,6 +266,11 @@ def cpu_baseline(layer, budget_s=12.0):
     rng.shuffle(experts)
     from aiter_amd.shuffle import unshuffle_weight
 
+    def deq(w, s):
+        if layer.a8w4:
+            return R.dequant_weight_mxfp4(w, s)[0]
+        return R.dequant_weight_128x128(w, s)[0]
+
     t_deq = t_gemm = 0.0
     n_exp = n_pairs = 0
     t_start = time.perf_counter()
@@ -241,8 +284,8 @@ def cpu_baseline(layer, budget_s=12.0):
         s1 = layer.w["w1_scale"][e:e + 1].cpu().numpy()
         s2 = layer.w["w2_scale"][e:e + 1].cpu().numpy()
         t0 = time.perf_counter()
-        w1 = R.dequant_weight_128x128(w1q, s1)[0]
-        w2 = R.dequant_weight_128x128(w2q, s2)[0]
+        w1 = deq(w1q, s1)
+        w2 = deq(w2q, s2)
         t1 = time.perf_counter()
         tok, slot = np.nonzero(ids == e)
         y = a1[tok] @ w1.T
@@ -273,6 +316,37 @@ def cpu_baseline(layer, budget_s=12.0):
     }
 
 
+def leg(name, args, dev):
+    """One extra workload: layer time, throughput, roofline fractions and
+    per-stage kernel times."""
+    import torch
+
+    from aiter_amd import workloads as W
+
+    cfg = make_cfg(name)
+    log(f"leg {cfg.name}")
+    lay = Layer(cfg, dev)
+    ms, _ = time_steps(lay.run, max(args.steps, 20), args.warmup)
+    sec = ms * 1e-3
+    flops = 2.0 * lay.pairs * 3 * cfg.inter_dim * cfg.model_dim
+    byts = W.layer_bytes(cfg, lay.distinct)
+    kt = stage_kernel_times(lay, args.kernel_iters)
+    f1, b1 = stage1_work(lay)
+    out = {"workload": cfg.name, "weights": cfg.weights, "tokens": cfg.tokens,
+           "ms_per_step": round(ms, 4), "tokens_per_s": round(cfg.tokens / sec, 1),
+           "tflops": round(flops / sec / 1e12, 2),
+           "fp8_peak_frac": round(flops / sec / PEAK_FP8_FLOPS, 4),
+           "hbm_gbps": round(byts / sec / 1e9, 1),
+           "hbm_peak_frac": round(byts / sec / PEAK_HBM_BPS, 4),
+           "routed_pairs": lay.pairs, "distinct_experts": lay.distinct,
+           "block_m": kt["block_m"],
+           "kernels_us": {k: round(v * 1e6, 1) for k, v in kt.items() if k.endswith("_s")},
+           "stage1_roofline": roofline(f1, b1, kt["stage1_s"])}
+    del lay
+    torch.cuda.empty_cache()
+    return out
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -298,8 +372,9 @@ def main():
     bytes_layer = W.layer_bytes(cfg, layer.distinct)
     kt = stage_kernel_times(layer, args.kernel_iters)
     f1, b1 = stage1_work(layer)
+    fmt = "A8W4 (fp8 x MXFP4)" if layer.a8w4 else "FP8 blockscale"
     line = {
-        "metric": "MoE-layer tokens/s (MiMo-style FP8 blockscale layer, T=%d)" % cfg.tokens,
+        "metric": "MoE-layer tokens/s (MiMo-style %s layer, T=%d)" % (fmt, cfg.tokens),
         "value": round(cfg.tokens / layer_s, 1),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -310,7 +385,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp8",
-        "data": "synthetic (seeded N(0,0.02) weights -> fp8 128x128, N(0,1) bf16 activations)",
+        "data": ("synthetic (seeded N(0,0.02) weights -> %s, N(0,1) bf16 activations)"
+                 % ("MXFP4 e2m1 + e8m0 1x32" if layer.a8w4 else "fp8 128x128")),
         "config": {"workload": cfg.name, "tokens": cfg.tokens, "model_dim": cfg.model_dim,
                    "inter_dim": cfg.inter_dim, "experts": cfg.experts, "topk": cfg.topk,
                    "routing": cfg.routing, "local_experts": cfg.local_experts,
@@ -324,6 +400,7 @@ def main():
         "kernels_us": {k: round(v * 1e6, 1) for k, v in kt.items() if k.endswith("_s")},
         "roofline": dict(roofline(f1, b1, kt["stage1_s"]), kernel="moe_gemm_fp8bs stage 1"),
     }
+    legs = [] if args.legs in ("", "none") else [x for x in args.legs.split(",") if x]
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle sample)")
         line["cpu_baseline"] = cpu_baseline(layer)
@@ -340,6 +417,19 @@ def main():
                           "hbm_gbps": round(db / (dms * 1e-3) / 1e9, 1),
                           "hbm_peak_frac": round(db / (dms * 1e-3) / PEAK_HBM_BPS, 4),
                           "distinct_experts": dl.distinct}
+        del dl
+        torch.cuda.empty_cache()
+    if legs:
+        if "layer" in locals():
+            del layer
+            torch.cuda.empty_cache()
+        line["legs"] = {}
+        for name in legs:
+            try:
+                line["legs"][name] = leg(name, args, dev)
+            except Exception as exc:  # keep the headline line even if a leg fails
+                line["legs"][name] = {"error": f"{type(exc).__name__}: {exc}"}
+                log(f"leg {name} failed: {exc}")
     print(json.dumps(line), flush=True)
 
 

@@ -183,7 +183,8 @@ int aiter_amd_fused_moe_a8w4(const void* hidden_states, int hidden_dtype, const 
                              int64_t workspace_bytes, void* stream);
 
 /* Default M-block (sorted rows per GEMM tile) for a token count: 16 / 32 / 64 by the average
- * rows per expert, 128 once experts average >= 128 rows and the dims allow 128-row tiles.
+ * rows per expert (<= 8, <= 20, else), 128 once experts average >= 64 rows and the dims allow
+ * 128-row tiles.
  * Plays the part of the block_m choice in aiter's get_2stage_cfgs (aiter/fused_moe.py:830-905). */
 int64_t aiter_amd_default_block_m(int64_t tokens, int64_t topk, int64_t num_experts,
                                   int64_t model_dim, int64_t inter_dim);

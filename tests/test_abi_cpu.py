@@ -107,8 +107,9 @@ def test_fused_validation_errors(lib):
 def test_default_block_m(lib):
     assert lib.aiter_amd_default_block_m(1, 8, 256, 4096, 2048) == 16
     assert lib.aiter_amd_default_block_m(32, 8, 256, 4096, 2048) == 16
-    assert lib.aiter_amd_default_block_m(1024, 8, 256, 4096, 2048) == 32
-    assert lib.aiter_amd_default_block_m(2048, 8, 256, 4096, 2048) == 64
+    assert lib.aiter_amd_default_block_m(512, 8, 256, 4096, 2048) == 32
+    assert lib.aiter_amd_default_block_m(1024, 8, 256, 4096, 2048) == 64
+    assert lib.aiter_amd_default_block_m(2048, 8, 256, 4096, 2048) == 128
     assert lib.aiter_amd_default_block_m(8192, 8, 256, 4096, 2048) == 128
     # 128-row tiles need model_dim % 256 == 0 and dims <= 8192
     assert lib.aiter_amd_default_block_m(8192, 8, 256, 4224, 2048) == 64

@@ -162,3 +162,10 @@ def test_a8w4_mimo_decode_T32(cuda_device):
     out = A.fused_moe(x, w1s, w2s, tw, ids, quant_type=A.QuantType.per_1x32,
                       w1_scale=wts["w1_scale"], w2_scale=wts["w2_scale"])
     _check(_np(ref), _np(out.float()), "A8W4 MiMo T=32")
+
+
+@pytest.mark.parametrize("bm", [16, 32, 64])
+def test_a8w4_odd_model_dim(cuda_device, bm):
+    cfg = W.MoEConfig("a8w4_odd_h", 48, 384, 256, 6, 2, seed=8, weights="mxfp4")
+    dev, ref = _make_layer(cfg, cuda_device, False)
+    _check(ref["out"], _np(_run(dev, block_size_M=bm).float()), f"A8W4 H=384 bm={bm}")

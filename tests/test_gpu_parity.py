@@ -271,3 +271,12 @@ def test_fused_moe_mimo_decode(cuda_device, T):
                        w1_scale=wts["w1_scale"], w2_scale=wts["w2_scale"])
     mx, rms = R.normalized_errors(_np(out.float()) * 2, _np(out2.float()))
     assert mx <= 1e-2 and rms <= 1e-3
+
+
+@pytest.mark.parametrize("bm", [16, 32, 64])
+def test_fused_moe_odd_model_dim(cuda_device, bm):
+    """model_dim 384 (3 K blocks; stage 2 cannot use 256-column tiles, so it
+    takes the general kernels) with every small block size."""
+    cfg = W.MoEConfig("odd_h", 48, 384, 256, 6, 2, seed=8)
+    dev, ref = _make_layer(cfg, cuda_device, True)
+    _check(ref["out"], _np(_run(dev, block_size_M=bm).float()), f"H=384 bm={bm}")
