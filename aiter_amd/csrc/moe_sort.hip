@@ -23,11 +23,13 @@
 // cut into chunks of `ct` tokens.  Each chunk builds an LDS bitmap
 // table[token][expert] of slot masks (a byte per cell for topk <= 8, a u32
 // up to topk 32, so duplicates of an expert inside one token's top-k are all
-// kept, in slot order), counts per
-// expert, and a single-block scan turns the per-chunk counts into absolute
-// write positions.  Small batches (one chunk) run the whole thing in one
-// block of one launch; the other blocks of that launch clear the
-// accumulator.
+// kept, in slot order) and stages its routing weights in LDS.  Small batches
+// (one chunk) run the whole sort in one block of one launch; the other
+// blocks of that launch clear the accumulator.  Larger batches take two
+// launches: per-chunk expert counts (plus the clearing), then one block per
+// chunk that sums the counts of the chunks before it (and of all chunks,
+// for the segment layout) and writes its pairs -- the prefix is recomputed
+// by every block in parallel instead of by a serial scan launch.
 #include "common.h"
 
 namespace aiter_amd {
@@ -43,7 +45,7 @@ struct SortParams {
     float* sorted_w;
     int32_t* sorted_eids;
     int32_t* num_valid;         // [2]
-    int32_t* ws;                // counts [num_chunks][E] then starts [E]
+    int32_t* ws;                // per-chunk expert counts [num_chunks][E]
     void* zero_buf;             // cleared for `tokens` rows (may be null)
     int64_t zero_row_bytes;     // multiple of 16
     int rows;
@@ -87,18 +89,27 @@ __device__ __forceinline__ uint32_t table_cell(const SortParams& p, const uint32
     return table[i];
 }
 
-// Fill table[ct][E] with slot bitmasks of chunk c.
-__device__ void build_table(const SortParams& p, uint32_t* table, int c, int tokens) {
-    const int nwords = (p.ct * p.E * p.cell_bytes + 3) / 4;
+__device__ __forceinline__ int chunk_rows(const SortParams& p, int c, int tokens) {
+    return max(0, min(p.ct, tokens - c * p.ct));
+}
+
+// Fill table[rows][E] with slot bitmasks of chunk c (only the chunk's rows
+// are cleared and used) and, when s_wt is given, stage the chunk's routing
+// weights there as [row][slot].
+__device__ void build_table(const SortParams& p, uint32_t* table, int c, int tokens,
+                            float* s_wt) {
+    const int nrows = chunk_rows(p, c, tokens);
+    const int nwords = (nrows * p.E * p.cell_bytes + 3) / 4;
     for (int i = threadIdx.x; i < nwords; i += kSortThreads) table[i] = 0u;
     __syncthreads();
     const int t0 = c * p.ct;
-    const int npairs = p.ct * p.topk;
+    const int npairs = nrows * p.topk;
     for (int i = threadIdx.x; i < npairs; i += kSortThreads) {
         int tl = i / p.topk;
         int j = i - tl * p.topk;
         int t = t0 + tl;
-        if (t < tokens) {
+        if (s_wt) s_wt[i] = p.topk_w[(int64_t)t0 * p.topk + i];
+        {
             int e = p.topk_ids[(int64_t)t * p.topk + j];
             if (e >= 0 && e < p.E) {
                 const int cell = tl * p.E + e;
@@ -110,10 +121,6 @@ __device__ void build_table(const SortParams& p, uint32_t* table, int c, int tok
         }
     }
     __syncthreads();
-}
-
-__device__ __forceinline__ int chunk_rows(const SortParams& p, int c, int tokens) {
-    return max(0, min(p.ct, tokens - c * p.ct));
 }
 
 __device__ __forceinline__ int expert_enabled(const SortParams& p, int e) {
@@ -154,7 +161,7 @@ __device__ int block_excl_scan(int v, int* scratch, int* total) {
 // start offset) and s_local (local expert id); write sorted_expert_ids, the
 // padding entries and num_valid_ids.
 __device__ void finalize_segments(const SortParams& p, const int* s_total, int* s_start,
-                                  int* s_local, int* scratch, int tokens) {
+                                  int* s_local, int* scratch, int tokens, bool write) {
     const int E = p.E;
     const int bm = p.bm;
     const int ept = (E + kSortThreads - 1) / kSortThreads;
@@ -183,11 +190,12 @@ __device__ void finalize_segments(const SortParams& p, const int* s_total, int* 
             mpre += p.expert_mask ? p.expert_mask[e] : 1;
         }
     }
-    if (threadIdx.x == 0) {
+    if (threadIdx.x == 0 && write) {
         p.num_valid[0] = ptot;
         p.num_valid[1] = tokens;
     }
     __syncthreads();
+    if (!write) return;
     const int32_t pad_id = (int32_t)(((uint32_t)(p.topk & 0xFF) << 24) | ((uint32_t)tokens & 0xFFFFFFu));
     for (int e = threadIdx.x; e < E; e += kSortThreads) {
         if (!expert_enabled(p, e)) continue;
@@ -204,31 +212,53 @@ __device__ void finalize_segments(const SortParams& p, const int* s_total, int* 
     }
 }
 
-// Emit the pairs of chunk c for every expert, starting at pos0[e].
+// Emit the pairs of chunk c for every expert, starting at s_pos[e]; the
+// routing weights come from the chunk's LDS copy s_wt.
 __device__ void scatter_chunk(const SortParams& p, const uint32_t* table, int c, int tokens,
-                              const int* s_pos_base, const int32_t* g_off) {
+                              const int* s_pos, const float* s_wt) {
     const int E = p.E;
     const int t0 = c * p.ct;
     const int nrows = chunk_rows(p, c, tokens);
     for (int e = threadIdx.x; e < E; e += kSortThreads) {
         if (!expert_enabled(p, e)) continue;
-        int pos = s_pos_base[e] + (g_off ? g_off[(int64_t)c * E + e] : 0);
+        int pos = s_pos[e];
         for (int tl = 0; tl < nrows; ++tl) {
             uint32_t m = table_cell(p, table, tl, e);
             while (m) {
                 int j = __ffs(m) - 1;
                 m &= m - 1u;
-                int t = t0 + tl;
-                p.sorted_ids[pos] = (int32_t)(((uint32_t)j << 24) | (uint32_t)t);
-                p.sorted_w[pos] = p.topk_w[(int64_t)t * p.topk + j];
+                p.sorted_ids[pos] = (int32_t)(((uint32_t)j << 24) | (uint32_t)(t0 + tl));
+                p.sorted_w[pos] = s_wt[tl * p.topk + j];
                 ++pos;
             }
         }
     }
 }
 
-// LDS layout of the sorting kernels: table[ct*E] | s_total[E] | s_start[E] |
-// s_local[E] | scratch[kSortThreads/64]
+// LDS layout of the sorting kernels: table[ct*E] | s_wt[ct*topk] | s_total[E] |
+// s_start[E] | s_local[E] | s_pos[E] | scratch[kSortThreads/64]
+struct SortLds {
+    uint32_t* table;
+    float* s_wt;
+    int* s_total;
+    int* s_start;
+    int* s_local;
+    int* s_pos;
+    int* scratch;
+};
+
+__device__ SortLds carve_lds(const SortParams& p, uint32_t* smem) {
+    SortLds L;
+    L.table = smem;
+    L.s_wt = reinterpret_cast<float*>(smem + table_words(p.ct, p.E, p.cell_bytes));
+    L.s_total = reinterpret_cast<int*>(L.s_wt + p.ct * p.topk);
+    L.s_start = L.s_total + p.E;
+    L.s_local = L.s_start + p.E;
+    L.s_pos = L.s_local + p.E;
+    L.scratch = L.s_pos + p.E;
+    return L;
+}
+
 __global__ __launch_bounds__(kSortThreads) void moe_sort_oneshot_kernel(SortParams p) {
     extern __shared__ uint32_t smem[];
     const int tokens = sort_tokens(p);
@@ -236,22 +266,18 @@ __global__ __launch_bounds__(kSortThreads) void moe_sort_oneshot_kernel(SortPara
         zero_rows(p, tokens, blockIdx.x - p.sort_blocks, gridDim.x - p.sort_blocks);
         return;
     }
-    uint32_t* table = smem;
-    int* s_total = reinterpret_cast<int*>(smem + table_words(p.ct, p.E, p.cell_bytes));
-    int* s_start = s_total + p.E;
-    int* s_local = s_start + p.E;
-    int* scratch = s_local + p.E;
-    build_table(p, table, 0, tokens);
+    const SortLds L = carve_lds(p, smem);
+    build_table(p, L.table, 0, tokens, L.s_wt);
     const int nrows = chunk_rows(p, 0, tokens);
     for (int e = threadIdx.x; e < p.E; e += kSortThreads) {
         int cnt = 0;
-        for (int tl = 0; tl < nrows; ++tl) cnt += __popc(table_cell(p, table, tl, e));
-        s_total[e] = cnt;
+        for (int tl = 0; tl < nrows; ++tl) cnt += __popc(table_cell(p, L.table, tl, e));
+        L.s_total[e] = cnt;
     }
     __syncthreads();
-    finalize_segments(p, s_total, s_start, s_local, scratch, tokens);
+    finalize_segments(p, L.s_total, L.s_start, L.s_local, L.scratch, tokens, true);
     __syncthreads();
-    scatter_chunk(p, table, 0, tokens, s_start, nullptr);
+    scatter_chunk(p, L.table, 0, tokens, L.s_start, L.s_wt);
 }
 
 __global__ __launch_bounds__(kSortThreads) void moe_sort_count_kernel(SortParams p) {
@@ -262,7 +288,7 @@ __global__ __launch_bounds__(kSortThreads) void moe_sort_count_kernel(SortParams
         return;
     }
     const int c = blockIdx.x;
-    build_table(p, smem, c, tokens);
+    build_table(p, smem, c, tokens, nullptr);
     const int nrows = chunk_rows(p, c, tokens);
     for (int e = threadIdx.x; e < p.E; e += kSortThreads) {
         int cnt = 0;
@@ -271,54 +297,43 @@ __global__ __launch_bounds__(kSortThreads) void moe_sort_count_kernel(SortParams
     }
 }
 
-// One block: per-expert prefix over chunks (counts become chunk offsets in
-// place), then the segment layout.
-__global__ __launch_bounds__(kSortThreads) void moe_sort_scan_kernel(SortParams p) {
-    extern __shared__ uint32_t smem[];
-    const int tokens = sort_tokens(p);
-    int* s_total = reinterpret_cast<int*>(smem);
-    int* s_start = s_total + p.E;
-    int* s_local = s_start + p.E;
-    int* scratch = s_local + p.E;
-    const int E = p.E;
-    for (int e = threadIdx.x; e < E; e += kSortThreads) {
-        int run = 0;
-        int c = 0;
-        for (; c + 4 <= p.num_chunks; c += 4) {
-            int v0 = p.ws[(int64_t)(c + 0) * E + e];
-            int v1 = p.ws[(int64_t)(c + 1) * E + e];
-            int v2 = p.ws[(int64_t)(c + 2) * E + e];
-            int v3 = p.ws[(int64_t)(c + 3) * E + e];
-            p.ws[(int64_t)(c + 0) * E + e] = run;
-            p.ws[(int64_t)(c + 1) * E + e] = run + v0;
-            p.ws[(int64_t)(c + 2) * E + e] = run + v0 + v1;
-            p.ws[(int64_t)(c + 3) * E + e] = run + v0 + v1 + v2;
-            run += v0 + v1 + v2 + v3;
-        }
-        for (; c < p.num_chunks; ++c) {
-            int v = p.ws[(int64_t)c * E + e];
-            p.ws[(int64_t)c * E + e] = run;
-            run += v;
-        }
-        s_total[e] = run;
-    }
-    __syncthreads();
-    finalize_segments(p, s_total, s_start, s_local, scratch, tokens);
-    int32_t* g_start = p.ws + (int64_t)p.num_chunks * E;
-    for (int e = threadIdx.x; e < E; e += kSortThreads) g_start[e] = s_start[e];
-}
-
+// Block c: per expert, the pairs of chunks before c (its write offset inside
+// the expert's segment) and of all chunks (the segment layout, which every
+// block derives identically); block 0 also writes the padding, the
+// sorted_expert_ids and num_valid_ids.  Then the chunk's pairs.
 __global__ __launch_bounds__(kSortThreads) void moe_sort_scatter_kernel(SortParams p) {
     extern __shared__ uint32_t smem[];
     const int tokens = sort_tokens(p);
     const int c = blockIdx.x;
-    if (c * p.ct >= tokens) return;
-    build_table(p, smem, c, tokens);
-    const int32_t* g_start = p.ws + (int64_t)p.num_chunks * p.E;
-    int* s_base = reinterpret_cast<int*>(smem + table_words(p.ct, p.E, p.cell_bytes));
-    for (int e = threadIdx.x; e < p.E; e += kSortThreads) s_base[e] = g_start[e];
+    const SortLds L = carve_lds(p, smem);
+    const int E = p.E;
+    for (int e = threadIdx.x; e < E; e += kSortThreads) {
+        int before = 0, total = 0;
+        int k = 0;
+        for (; k + 8 <= p.num_chunks; k += 8) {   // 8 independent loads in flight
+            int v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = p.ws[(int64_t)(k + u) * E + e];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                before += k + u < c ? v[u] : 0;
+                total += v[u];
+            }
+        }
+        for (; k < p.num_chunks; ++k) {
+            const int v = p.ws[(int64_t)k * E + e];
+            before += k < c ? v : 0;
+            total += v;
+        }
+        L.s_total[e] = total;
+        L.s_pos[e] = before;
+    }
     __syncthreads();
-    scatter_chunk(p, smem, c, tokens, s_base, p.ws);
+    finalize_segments(p, L.s_total, L.s_start, L.s_local, L.scratch, tokens, c == 0);
+    for (int e = threadIdx.x; e < E; e += kSortThreads) L.s_pos[e] += L.s_start[e];
+    if (c * p.ct >= tokens) return;
+    build_table(p, L.table, c, tokens, L.s_wt);   // its barriers also publish s_pos
+    scatter_chunk(p, L.table, c, tokens, L.s_pos, L.s_wt);
 }
 
 // ---------------------------------------------------------------- host ---
@@ -335,7 +350,7 @@ int64_t sort_workspace_bytes(int64_t rows, int64_t topk, int64_t E) {
     int ct = sort_chunk_tokens((int)E, (int)topk);
     int64_t chunks = ceil_div(rows > 0 ? rows : 1, ct);
     if (chunks <= 1) return 0;
-    return (chunks * E + E) * 4;
+    return chunks * E * 4;
 }
 
 void launch_moe_sort(const int32_t* topk_ids, const float* topk_w, const int32_t* expert_mask,
@@ -370,21 +385,21 @@ void launch_moe_sort(const int32_t* topk_ids, const float* topk_w, const int32_t
         zero_blocks = (int)std::min<int64_t>(ceil_div(n16, (int64_t)kSortThreads * 4), 2048);
         if (zero_blocks < 1) zero_blocks = 1;
     }
-    const size_t scan_lds = (size_t)(3 * E + kSortThreads / 64) * 4;
     const size_t table_lds = (size_t)table_words(p.ct, (int)E, p.cell_bytes) * 4;
+    const size_t full_lds =
+        table_lds + (size_t)p.ct * p.topk * 4 + (size_t)(4 * E + kSortThreads / 64) * 4;
     if (p.num_chunks == 1) {
         p.sort_blocks = 1;
         hipLaunchKernelGGL(moe_sort_oneshot_kernel, dim3(1 + zero_blocks), dim3(kSortThreads),
-                           table_lds + scan_lds, stream, p);
+                           full_lds, stream, p);
     } else {
         AMD_CHECK(ws != nullptr && ws_bytes >= sort_workspace_bytes(rows, topk, E),
                   "sorting workspace too small");
         p.sort_blocks = p.num_chunks;
         hipLaunchKernelGGL(moe_sort_count_kernel, dim3(p.num_chunks + zero_blocks),
                            dim3(kSortThreads), table_lds, stream, p);
-        hipLaunchKernelGGL(moe_sort_scan_kernel, dim3(1), dim3(kSortThreads), scan_lds, stream, p);
         hipLaunchKernelGGL(moe_sort_scatter_kernel, dim3(p.num_chunks), dim3(kSortThreads),
-                           table_lds + (size_t)E * 4, stream, p);
+                           full_lds, stream, p);
     }
     AMD_HIP_CHECK(hipGetLastError());
 }
