@@ -229,6 +229,20 @@ def stage1_work(layer):
     return flops, float(w_bytes + act_bytes)
 
 
+def measured_traffic(workload, kernel="stage1"):
+    """HBM bytes per launch of a stage kernel from the committed rocprofv3
+    FETCH_SIZE + WRITE_SIZE summary (profiles/traffic_<workload>_<stage>.md,
+    each counter scaled by what it reads for a 256 MiB copy), or None."""
+    import re
+
+    path = os.path.join(ROOT, "profiles", f"traffic_{workload}_{kernel}.md")
+    try:
+        m = re.search(r"^traffic_bytes_per_launch: (\d+)$", open(path).read(), re.M)
+    except OSError:
+        return None
+    return int(m.group(1)) if m else None
+
+
 def roofline(flops, bytes_, seconds):
     t_mfma = flops / PEAK_FP8_FLOPS
     t_hbm = bytes_ / PEAK_HBM_BPS
@@ -398,7 +412,9 @@ def main():
                   "alg_flops": flops_layer, "alg_bytes": bytes_layer,
                   "wall_s_timed_region": round(wall, 4)},
         "kernels_us": {k: round(v * 1e6, 1) for k, v in kt.items() if k.endswith("_s")},
-        "roofline": dict(roofline(f1, b1, kt["stage1_s"]), kernel="moe_gemm_fp8bs stage 1"),
+        "roofline": dict(roofline(f1, b1, kt["stage1_s"]), kernel="stage-1 gather-GEMM",
+                         traffic=measured_traffic(args.workload),
+                         alg_bytes=round(b1)),
     }
     legs = [] if args.legs in ("", "none") else [x for x in args.legs.split(",") if x]
     if not args.no_cpu_baseline:
