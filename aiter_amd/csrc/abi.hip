@@ -56,6 +56,17 @@ void launch_moe_stage2_stream(const uint8_t*, const float*, const uint8_t*, cons
                               const int32_t*, float*, int64_t, int64_t, int64_t, int64_t,
                               int64_t, int64_t, int64_t, int, hipStream_t);
 
+// moe_gemm_prefill.hip (64/128-row M-blocks, weight fragments in registers)
+bool prefill_supported(int64_t block_m, int64_t K);
+void launch_moe_stage1_prefill(const uint8_t*, const float*, int64_t, int64_t, const uint8_t*,
+                               const float*, const uint8_t*, const int32_t*, const int32_t*,
+                               const int32_t*, uint8_t*, float*, int64_t, int64_t, int64_t,
+                               int64_t, int64_t, int64_t, int64_t, int, hipStream_t);
+void launch_moe_stage2_prefill(const uint8_t*, const float*, const uint8_t*, const float*,
+                               const uint8_t*, const int32_t*, const float*, const int32_t*,
+                               const int32_t*, float*, int64_t, int64_t, int64_t, int64_t,
+                               int64_t, int64_t, int64_t, int, hipStream_t);
+
 // Weight scales of one layer: fp32 128x128 blocks (fp8 weights) or e8m0
 // bytes per 1x32 K block (MXFP4 weights); exactly one is set.
 struct WScale {
@@ -63,10 +74,12 @@ struct WScale {
     const uint8_t* e8m0;
 };
 
-// Kernel choice per shape: 16/32-row M-blocks (decode-sized layers) take the
-// register-streaming kernels, 64/128-row M-blocks the large-tile
-// direct-to-LDS kernels (stage 2 of both needs 256-column output tiles,
-// model_dim % 256 == 0); other shapes the general kernels of
+// Kernel choice per shape (measured on MI355X): 16/32-row M-blocks
+// (decode-sized layers) take the register-streaming kernels; 64/128-row
+// M-blocks take, for FP8 weights, the register-B prefill kernels and, for
+// MXFP4 weights (half the weight bytes per K step), the direct-to-LDS
+// kernels.  Stage 2 of all of them needs 256-column output tiles
+// (model_dim % 256 == 0); other shapes take the general kernels of
 // moe_gemm_fp8bs.hip.
 static void stage1_dispatch(const uint8_t* a, const float* sa, int64_t sa_row, int64_t sa_kb,
                             const uint8_t* w1, WScale w1s, const int32_t* sid,
@@ -76,6 +89,9 @@ static void stage1_dispatch(const uint8_t* a, const float* sa, int64_t sa_row, i
     if (stream_supported(bm, K))
         launch_moe_stage1_stream(a, sa, sa_row, sa_kb, w1, w1s.f32, w1s.e8m0, sid, seid, nv, a2,
                                  a2s, a_rows, K, I, E, topk, bm, mblocks, sh, s);
+    else if (prefill_supported(bm, K) && !w1s.e8m0)
+        launch_moe_stage1_prefill(a, sa, sa_row, sa_kb, w1, w1s.f32, w1s.e8m0, sid, seid, nv, a2,
+                                  a2s, a_rows, K, I, E, topk, bm, mblocks, sh, s);
     else if (v2_supported(bm, K))
         launch_moe_stage1_fp8bs_v2(a, sa, sa_row, sa_kb, w1, w1s.f32, w1s.e8m0, sid, seid, nv, a2,
                                    a2s, a_rows, K, I, E, topk, bm, mblocks, sh, s);
@@ -92,6 +108,9 @@ static void stage2_dispatch(const uint8_t* a2, const float* a2s, const uint8_t* 
     if (stream_supported(bm, I) && H % 256 == 0)
         launch_moe_stage2_stream(a2, a2s, w2, w2s.f32, w2s.e8m0, sid, sw, seid, nv, acc, a_rows,
                                  I, H, E, topk, bm, mblocks, sh, s);
+    else if (prefill_supported(bm, I) && H % 256 == 0 && !w2s.e8m0)
+        launch_moe_stage2_prefill(a2, a2s, w2, w2s.f32, w2s.e8m0, sid, sw, seid, nv, acc, a_rows,
+                                  I, H, E, topk, bm, mblocks, sh, s);
     else if (v2_supported(bm, I) && H % 256 == 0)
         launch_moe_stage2_fp8bs_v2(a2, a2s, w2, w2s.f32, w2s.e8m0, sid, sw, seid, nv, acc, a_rows,
                                    I, H, E, topk, bm, mblocks, sh, s);
