@@ -71,16 +71,24 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, int64_t
                                              0x00020000);
 }
 
-// One K step of a wave's B operand.
-template <bool W4>
+// Waves along M in the 8-wave workgroup (template WM): 2 -> 2 x 4 waves of
+// (BM/2) x 64 (the two M-waves of a SIMD load the same weight fragments, the
+// second from L1); 1 -> each wave owns all BM rows and 32 weight rows (no
+// weight fragment is loaded twice, every wave reads all A rows from LDS).
+// Measured on MI355X: 2 x 4 for stage 1 (K = 4096), 1 x 8 for stage 2.
+
+// One K step of a wave's B operand (NCT 16-row weight groups).
+template <bool W4, int NCT>
 struct BStep {
-    v4i b[4][W4 ? 1 : 2];
-    int bs[4];
+    v4i b[NCT][W4 ? 1 : 2];
+    int bs[NCT];
 };
 
-template <int BM, int STAGE, bool SHUFFLED, bool W4, int D>
+template <int BM, int STAGE, bool SHUFFLED, bool W4, int D, int kWM>
 __global__ __launch_bounds__(kThreads, 1) void moe_gemm_prefill_kernel(Args g) {
-    constexpr int NRT = BM / 32;                         // 16-row MFMA tiles per wave
+    constexpr int WN = kWaves / kWM;                     // waves along N
+    constexpr int NCT = 16 / WN;                         // 16-row weight groups per wave
+    constexpr int NRT = BM / 16 / kWM;                   // 16-row MFMA tiles per wave
     constexpr int A_BYTES = BM * 128;
     constexpr int A_PT = A_BYTES / 16 / kThreads;        // 16-byte A pieces per thread
     constexpr int NH = W4 ? 1 : 2;                       // scale products per (row, kb)
@@ -91,13 +99,13 @@ __global__ __launch_bounds__(kThreads, 1) void moe_gemm_prefill_kernel(Args g) {
     __shared__ int32_t s_arow[BM];
     __shared__ int64_t s_orow[BM];
     __shared__ float s_w[BM];
-    __shared__ float s_amax[4][BM];
+    __shared__ float s_amax[WN][BM];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wv = tid >> 6;
-    const int wm = wv >> 2;
-    const int wn = wv & 3;
+    const int wm = wv / WN;
+    const int wn = wv % WN;
     const int lr = lane & 15;
     const int lq = lane >> 4;
 
@@ -186,14 +194,16 @@ __global__ __launch_bounds__(kThreads, 1) void moe_gemm_prefill_kernel(Args g) {
     const __amdgpu_buffer_rsrc_t rb = rsrc(g.w + (int64_t)e * g.N * KBY, (int64_t)g.N * KBY);
     const __amdgpu_buffer_rsrc_t rbs =
         rsrc(W4 ? g.w_scale8 + (int64_t)e * g.N * KS : g.w, W4 ? (int64_t)g.N * KS : 0);
-    uint32_t boff[4], bsoff[4];
+    uint32_t boff[NCT], bsoff[NCT];
 #pragma unroll
-    for (int ct = 0; ct < 4; ++ct) {
+    for (int ct = 0; ct < NCT; ++ct) {
+        // stage 1: the wave's gate tiles (ct < NCT/2) and the matching up tiles
         int row0;
         if (STAGE == 1)
-            row0 = ct < 2 ? n0 + 32 * wn + 16 * ct : g.inter + n0 + 32 * wn + 16 * (ct - 2);
+            row0 = ct < NCT / 2 ? n0 + 16 * (wn * (NCT / 2) + ct)
+                                : g.inter + n0 + 16 * (wn * (NCT / 2) + ct - NCT / 2);
         else
-            row0 = n0 + 64 * wn + 16 * ct;
+            row0 = n0 + 16 * (wn * NCT + ct);
         if (W4)
             boff[ct] = SHUFFLED ? (uint32_t)(row0 * KBY + lane * 16)
                                 : (uint32_t)((row0 + lr) * KBY + lq * 16);
@@ -205,10 +215,10 @@ __global__ __launch_bounds__(kThreads, 1) void moe_gemm_prefill_kernel(Args g) {
     constexpr int BSTEP = W4 ? (SHUFFLED ? 1024 : 64) : (SHUFFLED ? 2048 : 128);
     constexpr int BHI = SHUFFLED ? 256 : 16;
 
-    using BS = BStep<W4>;
+    using BS = BStep<W4, NCT>;
     auto load_b = [&](BS& s, int kb) {
 #pragma unroll
-        for (int ct = 0; ct < 4; ++ct) {
+        for (int ct = 0; ct < NCT; ++ct) {
             s.b[ct][0] = __builtin_amdgcn_raw_buffer_load_b128(rb, boff[ct], kb * BSTEP, 0);
             if (!W4)
                 s.b[ct][W4 ? 0 : 1] =
@@ -231,12 +241,12 @@ __global__ __launch_bounds__(kThreads, 1) void moe_gemm_prefill_kernel(Args g) {
             *reinterpret_cast<v4i*>(&s_a[buf][a_dst[j]]) = areg[buf][j];
     };
 
-    v4f acc[NRT][4];
+    v4f acc[NRT][NCT];
 #pragma unroll
     for (int rt = 0; rt < NRT; ++rt)
 #pragma unroll
-        for (int ct = 0; ct < 4; ++ct) acc[rt][ct] = v4f{0.f, 0.f, 0.f, 0.f};
-    const int row_base = wm * (BM / 2);
+        for (int ct = 0; ct < NCT; ++ct) acc[rt][ct] = v4f{0.f, 0.f, 0.f, 0.f};
+    const int row_base = wm * (BM / kWM);
     const int h0 = frag_swap(lr);
 
     // One K step: NRT x 4 MFMAs, row tile by row tile (the B fragments stay
@@ -265,14 +275,15 @@ __global__ __launch_bounds__(kThreads, 1) void moe_gemm_prefill_kernel(Args g) {
         };
         // scale half of column tile ct: stage 1 gate (tiles 0,1) / up (2,3);
         // stage 2 the wave's 128-column block
-        const int hsel0 = W4 ? 0 : (STAGE == 1 ? 0 : (wn >> 1));
-        const int hsel1 = W4 ? 0 : (STAGE == 1 ? 1 : (wn >> 1));
+        const int hblk = (wn * NCT * 16) / 128;           // stage 2: the wave's 128-column block
+        const int hsel0 = W4 ? 0 : (STAGE == 1 ? 0 : hblk);
+        const int hsel1 = W4 ? 0 : (STAGE == 1 ? 1 : hblk);
         const float* sc_row = &s_sc[kb * NH * BM + row_base + 4 * lq];
-        v4f blk[2][4];
+        v4f blk[2][NCT];
         {
             const v8i a0 = afrag(0);
 #pragma unroll
-            for (int ct = 0; ct < 4; ++ct) blk[0][ct] = mfma(a0, ct);
+            for (int ct = 0; ct < NCT; ++ct) blk[0][ct] = mfma(a0, ct);
         }
 #pragma unroll
         for (int rt = 0; rt < NRT; ++rt) {
@@ -280,17 +291,17 @@ __global__ __launch_bounds__(kThreads, 1) void moe_gemm_prefill_kernel(Args g) {
             if (rt + 1 < NRT) {
                 const v8i an = afrag(rt + 1);
 #pragma unroll
-                for (int ct = 0; ct < 4; ++ct) blk[cur ^ 1][ct] = mfma(an, ct);
+                for (int ct = 0; ct < NCT; ++ct) blk[cur ^ 1][ct] = mfma(an, ct);
             }
             const v4f s0 = *reinterpret_cast<const v4f*>(sc_row + hsel0 * BM + rt * 16);
             const v4f s1 = *reinterpret_cast<const v4f*>(sc_row + hsel1 * BM + rt * 16);
 #pragma unroll
-            for (int ct = 0; ct < 4; ++ct)
+            for (int ct = 0; ct < NCT; ++ct)
 #pragma unroll
                 for (int v = 0; v < 4; ++v)
-                    acc[rt][ct][v] += blk[cur][ct][v] * (ct < 2 ? s0[v] : s1[v]);
+                    acc[rt][ct][v] += blk[cur][ct][v] * (ct < NCT / 2 ? s0[v] : s1[v]);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < NCT; ++i) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
                 __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // VALU
             }
@@ -337,35 +348,40 @@ __global__ __launch_bounds__(kThreads, 1) void moe_gemm_prefill_kernel(Args g) {
                 const int64_t t = s_orow[row];
                 if (t < 0) continue;
                 const float wgt = s_w[row];
-                float* dst = g.acc + t * g.N + n0 + wn * 64 + lr;
+                float* dst = g.acc + t * g.N + n0 + wn * NCT * 16 + lr;
 #pragma unroll
-                for (int ct = 0; ct < 4; ++ct) unsafeAtomicAdd(dst + ct * 16, acc[rt][ct][v] * wgt);
+                for (int ct = 0; ct < NCT; ++ct)
+                    unsafeAtomicAdd(dst + ct * 16, acc[rt][ct][v] * wgt);
             }
         return;
     }
 
     // ---- stage 1 epilogue: silu(gate)*up -> bf16 -> 1x128 fp8 requant ----
-    // wave wn holds output columns wn*32 + j*16 + lr (j = 0, 1) of the tile's 128
-    float h[NRT][2][4];
+    // wave wn holds output columns wn*NH1*16 + j*16 + lr (j < NH1) of the tile's 128
+    constexpr int NH1 = NCT / 2;
+    float h[NRT][NH1][4];
 #pragma unroll
     for (int rt = 0; rt < NRT; ++rt)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < NH1; ++j)
 #pragma unroll
             for (int v = 0; v < 4; ++v)
-                h[rt][j][v] = bf16_round(silu_f32(acc[rt][j][v]) * acc[rt][2 + j][v]);
+                h[rt][j][v] = bf16_round(silu_f32(acc[rt][j][v]) * acc[rt][NH1 + j][v]);
 #pragma unroll
     for (int rt = 0; rt < NRT; ++rt)
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-            float m = __builtin_fmaxf(__builtin_fabsf(h[rt][0][v]), __builtin_fabsf(h[rt][1][v]));
+            float m = 0.0f;
+#pragma unroll
+            for (int j = 0; j < NH1; ++j) m = __builtin_fmaxf(m, __builtin_fabsf(h[rt][j][v]));
             m = warp_max_16(m);
             if (lr == 0) s_amax[wn][row_base + rt * 16 + 4 * lq + v] = m;
         }
     __syncthreads();
     auto row_amax = [&](int row) {
-        const float m = __builtin_fmaxf(__builtin_fmaxf(s_amax[0][row], s_amax[1][row]),
-                                        __builtin_fmaxf(s_amax[2][row], s_amax[3][row]));
+        float m = s_amax[0][row];
+#pragma unroll
+        for (int w = 1; w < WN; ++w) m = __builtin_fmaxf(m, s_amax[w][row]);
         return __builtin_fmaxf(m, 1e-10f);
     };
     uint8_t* s_q = &s_a[0][0];  // [BM][128] fp8 staging (the K loop is done)
@@ -376,9 +392,9 @@ __global__ __launch_bounds__(kThreads, 1) void moe_gemm_prefill_kernel(Args g) {
             const int row = row_base + rt * 16 + 4 * lq + v;
             const float inv = 1.0f / (row_amax(row) * kInvFp8Max);
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
+            for (int j = 0; j < NH1; ++j) {
                 const uint32_t b = f32x2_to_fp8x2(h[rt][j][v] * inv, 0.0f) & 0xFFu;
-                s_q[row * 128 + wn * 32 + j * 16 + lr] = (uint8_t)b;
+                s_q[row * 128 + wn * NH1 * 16 + j * 16 + lr] = (uint8_t)b;
             }
         }
     __syncthreads();
@@ -395,11 +411,16 @@ __global__ __launch_bounds__(kThreads, 1) void moe_gemm_prefill_kernel(Args g) {
 
 template <int BM, int STAGE, bool SHUFFLED, bool W4>
 static void launch_depth(int KB, int grid, const Args& a, hipStream_t s) {
-    if (KB % 2 == 0)
-        hipLaunchKernelGGL((moe_gemm_prefill_kernel<BM, STAGE, SHUFFLED, W4, 2>), dim3(grid),
+    constexpr int WM = STAGE == 1 ? 2 : 1;
+    constexpr int DM = STAGE == 1 ? 2 : 4;      // the 1 x 8 tile has registers for 4 steps
+    if (DM >= 4 && KB % 4 == 0)
+        hipLaunchKernelGGL((moe_gemm_prefill_kernel<BM, STAGE, SHUFFLED, W4, DM >= 4 ? 4 : 2, WM>),
+                           dim3(grid), dim3(kThreads), 0, s, a);
+    else if (KB % 2 == 0)
+        hipLaunchKernelGGL((moe_gemm_prefill_kernel<BM, STAGE, SHUFFLED, W4, 2, WM>), dim3(grid),
                            dim3(kThreads), 0, s, a);
     else
-        hipLaunchKernelGGL((moe_gemm_prefill_kernel<BM, STAGE, SHUFFLED, W4, 1>), dim3(grid),
+        hipLaunchKernelGGL((moe_gemm_prefill_kernel<BM, STAGE, SHUFFLED, W4, 1, WM>), dim3(grid),
                            dim3(kThreads), 0, s, a);
 }
 
