@@ -78,7 +78,8 @@ struct WScale {
 // (decode-sized layers) take the register-streaming kernels; 64/128-row
 // M-blocks take, for FP8 weights, the register-B prefill kernels and, for
 // MXFP4 weights (half the weight bytes per K step), the direct-to-LDS
-// kernels.  Stage 2 of all of them needs 256-column output tiles
+// kernels -- except stage 2 at 128 rows, where the register-B kernel's 1 x 8
+// tile is faster for both.  Stage 2 of all of them needs 256-column output tiles
 // (model_dim % 256 == 0); other shapes take the general kernels of
 // moe_gemm_fp8bs.hip.
 static void stage1_dispatch(const uint8_t* a, const float* sa, int64_t sa_row, int64_t sa_kb,
@@ -108,7 +109,7 @@ static void stage2_dispatch(const uint8_t* a2, const float* a2s, const uint8_t* 
     if (stream_supported(bm, I) && H % 256 == 0)
         launch_moe_stage2_stream(a2, a2s, w2, w2s.f32, w2s.e8m0, sid, sw, seid, nv, acc, a_rows,
                                  I, H, E, topk, bm, mblocks, sh, s);
-    else if (prefill_supported(bm, I) && H % 256 == 0 && !w2s.e8m0)
+    else if (prefill_supported(bm, I) && H % 256 == 0 && (!w2s.e8m0 || bm == 128))
         launch_moe_stage2_prefill(a2, a2s, w2, w2s.f32, w2s.e8m0, sid, sw, seid, nv, acc, a_rows,
                                   I, H, E, topk, bm, mblocks, sh, s);
     else if (v2_supported(bm, I) && H % 256 == 0)
