@@ -1,0 +1,133 @@
+"""Full-size parity checks split at the stage boundary (GPU, torch fp32).
+
+At MiMo's dimensions a stage-1 accumulation in another fp32 order moves a
+few SiLU*up values across a bf16 rounding boundary, and their fp8 1x128
+requant then differs by one e4m3 ulp (32/448 of the group amax at the top
+binade). The product of two Gaussians behind SiLU*up is heavy-tailed, so
+one such flip on a dominant element shifts an output by a few per cent:
+the end-to-end max-rel bar of the small cases is then a statement about
+torch's accumulation order, not about the kernel. These checks pin each
+stage to what it can be held to instead:
+
+* stage 1 against torch's stage 1 (same fp8 activations): every 1x128
+  scale within one bf16 ulp of amax/448, every dequantised a2 element
+  within one top-binade e4m3 ulp of its group, and at most 1% of the fp8
+  codes different;
+* stage 2 on the kernel's own a2 against torch's fp32 product: the strict
+  normalised bar (max-rel <= 2e-2, RMS-rel <= 4e-3,
+  op_tests/triton_tests/moe/test_moe_gemm_a8w4.py:104-160);
+* end to end against torch's chain: the reference's own bar for this
+  layer, allclose(rtol=atol=0.05) on at least 95% of the outputs
+  (op_tests/test_moe_blockscale.py:288 via aiter/test_common.py:399-430),
+  plus RMS-rel <= 4e-3.
+"""
+import numpy as np
+import torch
+
+import aiter_amd as A
+from aiter_amd import workloads as W
+from oracle import moe_ref as R
+
+E4M3_TOP_ULP = 32.0 / 448.0
+BF16_ULP = 2.0 ** -7
+
+
+def deq_fp8_128x128(wq, sc):
+    N, K = wq.shape
+    return (wq.float().view(N // 128, 128, K // 128, 128) *
+            sc.view(N // 128, 1, K // 128, 1)).view(N, K)
+
+
+def deq_mxfp4(wp, sc):
+    """[N, K/2] packed e2m1 + [N, K/32] e8m0 -> fp32 [N, K]."""
+    lut = torch.tensor(R.FP4_LUT, device=wp.device)
+    N = wp.shape[0]
+    v = torch.stack([lut[(wp & 15).long()], lut[(wp >> 4).long()]], dim=-1).view(N, -1)
+    s = torch.exp2(sc.float() - 127.0)
+    return (v.view(N, -1, 32) * s[..., None]).view(N, -1)
+
+
+def q1x128(v):
+    """Kernel-semantics fp8 1x128 quant: (codes, scales) of a [rows, K] tensor."""
+    g = v.float().view(v.shape[0], -1, 128)
+    amax = g.abs().amax(-1, keepdim=True).clamp_min(1e-10)
+    sc = amax * np.float32(1 / 448)
+    q = (g * (1.0 / sc)).clamp(-448, 448).to(torch.float8_e4m3fn)
+    return q.view(v.shape[0], -1), sc.view(v.shape[0], -1)
+
+
+def deq1x128(q, sc):
+    rows = q.shape[0]
+    return (q.float().view(rows, -1, 128) * sc.view(rows, -1, 1)).view(rows, -1)
+
+
+def stagewise_check(cfg, device, block_ms, log=print):
+    mx4 = cfg.weights == "mxfp4"
+    deq = deq_mxfp4 if mx4 else deq_fp8_128x128
+    qt = A.QuantType.per_1x32 if mx4 else A.QuantType.per_128x128
+    stage1 = A.moe_stage1_a8w4 if mx4 else A.moe_stage1_fp8_blockscale
+    stage2 = A.moe_stage2_a8w4 if mx4 else A.moe_stage2_fp8_blockscale
+    T, H, I, E, k = cfg.tokens, cfg.model_dim, cfg.inter_dim, cfg.experts, cfg.topk
+
+    wts = W.make_weights(cfg, device=device, shuffle=False)
+    x = W.make_hidden(cfg, device=device)
+    tw, ids = W.make_routing(cfg, device=device)
+    w1, s1, w2, s2 = wts["w1"], wts["w1_scale"], wts["w2"], wts["w2_scale"]
+    w1s, w2s = A.shuffle_weight(w1), A.shuffle_weight(w2)
+    experts = torch.unique(ids).tolist()
+    routes = {e: torch.nonzero(ids == e, as_tuple=True) for e in experts}
+
+    # the fp8 activation quant is bit-exact with the oracle (its own tests);
+    # both stage-1 paths start from the kernel's a1
+    a1, a1s = A.per_group_quant_hip(x)
+    a1d = deq1x128(a1, a1s)
+    y = torch.empty(T, k, 2 * I, device=device)
+    for e in experts:
+        tok, slot = routes[e]
+        y[tok, slot] = a1d[tok] @ deq(w1[e], s1[e]).T
+    h = (torch.nn.functional.silu(y[..., :I]) * y[..., I:]).to(torch.bfloat16)
+    del y
+    q_ref, sc_ref = q1x128(h.view(T * k, I))
+    del h
+    a2_ref = deq1x128(q_ref, sc_ref)
+
+    def stage2_torch(a2d):
+        out = torch.zeros(T, H, device=device)
+        for e in experts:
+            tok, slot = routes[e]
+            rows = tok * k + slot
+            out.index_add_(0, tok, (a2d[rows] @ deq(w2[e], s2[e]).T) * tw[tok, slot][:, None])
+        return out
+
+    chain_ref = stage2_torch(a2_ref)
+    for bm in block_ms:
+        tag = f"{cfg.name} bm={bm}"
+        sid, sw, se, nv, _ = A.moe_sorting(ids, tw, E, H, torch.bfloat16, bm)
+        a2, a2s = stage1(a1, a1s, w1s, s1, sid, se, nv, k, bm, True)
+        a2s = a2s.view(T * k, -1)
+        a2 = a2.view(T * k, I)
+        srel = ((a2s - sc_ref).abs() / sc_ref).max().item()
+        a2d = deq1x128(a2, a2s)
+        err = ((a2d - a2_ref).abs().view(T * k, -1, 128) /
+               (sc_ref.view(T * k, -1, 1) * 448)).max().item()
+        codes = (a2.view(torch.uint8) != q_ref.view(torch.uint8)).float().mean().item()
+        log(f"[{tag}] stage 1: scale rel {srel:.2e}, element err/amax {err:.4f}, "
+            f"codes differing {codes:.3%}")
+        assert srel <= BF16_ULP * (1 + 1e-6), srel
+        assert err <= E4M3_TOP_ULP * (1 + 2 * BF16_ULP), err
+        assert codes <= 0.01, codes
+
+        acc = torch.zeros(T, H, dtype=torch.float32, device=device)
+        stage2(a2.view(T, k, I), a2s.view(T, k, -1), w2s, s2, sid, sw, se, nv, acc, bm, True)
+        mx, rms = R.normalized_errors(stage2_torch(a2d).cpu().numpy(), acc.cpu().numpy())
+        log(f"[{tag}] stage 2 on the kernel's a2: max-rel {mx:.2e} rms-rel {rms:.2e}")
+        assert mx <= R.MAXTOL and rms <= R.RMSTOL, (mx, rms)
+
+        out = A.fused_moe(x, w1s, w2s, tw, ids, quant_type=qt, w1_scale=s1, w2_scale=s2,
+                          block_size_M=bm).float()
+        ref = chain_ref.to(torch.bfloat16).float()
+        far = (~torch.isclose(out, ref, rtol=0.05, atol=0.05)).float().mean().item()
+        mx, rms = R.normalized_errors(ref.cpu().numpy(), out.cpu().numpy())
+        log(f"[{tag}] end to end: outside allclose(0.05) {far:.4%}, "
+            f"max-rel {mx:.2e} rms-rel {rms:.2e}")
+        assert far <= 0.05 and rms <= R.RMSTOL, (far, rms)

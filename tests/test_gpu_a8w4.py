@@ -17,6 +17,8 @@ import aiter_amd as A
 from aiter_amd import workloads as W
 from oracle import moe_ref as R
 
+import _fullshape
+
 pytestmark = pytest.mark.gpu
 
 MAXTOL, RMSTOL = R.MAXTOL, R.RMSTOL
@@ -169,3 +171,23 @@ def test_a8w4_odd_model_dim(cuda_device, bm):
     cfg = W.MoEConfig("a8w4_odd_h", 48, 384, 256, 6, 2, seed=8, weights="mxfp4")
     dev, ref = _make_layer(cfg, cuda_device, False)
     _check(ref["out"], _np(_run(dev, block_size_M=bm).float()), f"A8W4 H=384 bm={bm}")
+
+
+def test_a8w4_num_local_tokens(cuda_device):
+    cfg = W.MoEConfig("a8w4_local", 80, 512, 512, 8, 2, seed=4, weights="mxfp4")
+    dev, _ = _make_layer(cfg, cuda_device, True)
+    loc = torch.tensor([50], dtype=torch.int32, device=cuda_device)
+    out = _run(dev, num_local_tokens=loc)
+    wts = W.make_weights(cfg, device="cpu", shuffle=False)
+    ref = R.fused_moe_ref(dev["x"].float().cpu().numpy(), wts["w1"].numpy(),
+                          wts["w1_scale"].numpy(), wts["w2"].numpy(), wts["w2_scale"].numpy(),
+                          _np(dev["ids"]), _np(dev["tw"]), num_local_tokens=50,
+                          weight_format="mxfp4")
+    _check(ref["out"][:50], _np(out.float())[:50], "A8W4 num_local_tokens")
+
+
+@pytest.mark.parametrize("T,block_ms", [(1024, (64, 128)), (8192, (128,))])
+def test_a8w4_mimo_stagewise(cuda_device, T, block_ms):
+    """Full MiMo dims for the A8W4 mid-size and prefill configs, checked per
+    stage (64 is the direct-to-LDS kernels, 128 the prefill stage 2)."""
+    _fullshape.stagewise_check(W.mimo_a8w4(T), cuda_device, block_ms)

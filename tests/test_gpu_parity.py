@@ -13,6 +13,8 @@ import aiter_amd as A
 from aiter_amd import workloads as W
 from oracle import moe_ref as R
 
+import _fullshape
+
 pytestmark = pytest.mark.gpu
 
 MAXTOL, RMSTOL = R.MAXTOL, R.RMSTOL
@@ -38,6 +40,7 @@ SORT_CASES = [
     (2048, 256, 8, 64, False, None), (8192, 256, 8, 64, False, None),
     (8192, 256, 8, 32, True, None), (300, 256, 8, 32, False, 250), (33, 4096, 1, 16, False, None),
     (4096, 256, 8, 64, False, 4000), (163840, 32, 5, 32, False, None),
+    (37, 32, 16, 16, False, None), (600, 64, 16, 32, True, None), (45, 1, 1, 64, False, None),
 ]
 
 
@@ -280,3 +283,33 @@ def test_fused_moe_odd_model_dim(cuda_device, bm):
     cfg = W.MoEConfig("odd_h", 48, 384, 256, 6, 2, seed=8)
     dev, ref = _make_layer(cfg, cuda_device, True)
     _check(ref["out"], _np(_run(dev, block_size_M=bm).float()), f"H=384 bm={bm}")
+
+
+# ------------------------------------------- full MiMo shape (prefill) ---
+@pytest.mark.parametrize("T,block_ms", [(2048, (128, 64, 32)), (8192, (128,))])
+def test_fused_moe_mimo_prefill_stagewise(cuda_device, T, block_ms):
+    """Full MiMo dims with Zipf routing (128 is the default block_m: the
+    register-B prefill kernels at K = 4096 / 2048), checked per stage."""
+    cfg = W.mimo_prefill(T)
+    assert A.default_block_m(cfg.tokens, cfg.topk, cfg.experts, cfg.model_dim,
+                             cfg.inter_dim) == 128
+    _fullshape.stagewise_check(cfg, cuda_device, block_ms)
+
+
+# --------------------------------------------------------- edge cases ---
+def test_fused_moe_empty_batch(cuda_device):
+    cfg = W.CONFIG_A
+    dev, _ = _make_layer(cfg, cuda_device, True)
+    out = A.fused_moe(dev["x"][:0], dev["w1"], dev["w2"], dev["tw"][:0], dev["ids"][:0],
+                      quant_type=A.QuantType.per_128x128, w1_scale=dev["s1"], w2_scale=dev["s2"])
+    assert out.shape == (0, cfg.model_dim) and out.dtype == torch.bfloat16
+
+
+@pytest.mark.parametrize("T,E,k,seed", [(37, 32, 16, 12), (45, 1, 1, 13), (1, 8, 8, 14)])
+def test_fused_moe_topk_and_expert_extremes(cuda_device, T, E, k, seed):
+    """topk 16 (32-bit slot masks in sorting), a single expert with top-1
+    (a dense block-scale GEMM), and topk == E with one token, on every
+    block size. Sixteen summed slots make the end-to-end error sensitive to
+    one-ulp fp8 requant flips, so the layer is checked per stage."""
+    cfg = W.MoEConfig("extreme", T, 512, 512, E, k, seed=seed)
+    _fullshape.stagewise_check(cfg, cuda_device, (16, 32, 64, 128))
