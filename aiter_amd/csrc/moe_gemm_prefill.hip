@@ -6,35 +6,37 @@
 // fp32 atomic accumulate; FP8 128x128 blockscale or MXFP4 weights).
 //
 // What bounds this shape on MI355X, measured: LDS reads run at ~128 B/clk
-// per CU, so a 2x4-wave tile that reads both operands from LDS spends as
-// long reading LDS as the MFMAs take; and VALU issue barely overlaps MFMA --
-// 16x16x128 fp8 MFMAs with the 4 fp32 FMAs per MFMA that the per-128-K
-// block scales need reach ~65% of peak with two waves per SIMD.  So:
+// per CU, so a tile that reads both operands from LDS spends as long reading
+// LDS as the MFMAs take; and VALU issue barely overlaps MFMA -- 16x16x128
+// fp8 MFMAs with the 4 fp32 FMAs per MFMA that the per-128-K block scales
+// need reach ~65% of peak with two waves per SIMD.  So:
 //   * B (weights) never touches LDS: every lane loads its own MFMA
 //     fragments from global memory (the (16,16) layout puts them in 16-byte
-//     pieces), D K-steps ahead in registers.  The two M-waves that share a
-//     weight group issue the same addresses back to back, so the second
-//     read hits the CU's L1.
-//   * A (token rows, gathered) is loaded to registers one step ahead and
-//     written to one of two LDS stages, fragment-major with a per-row swap
-//     of the 16-byte halves ((r>>2 ^ r>>3) & 1) so 16-byte reads are
-//     conflict-free; one barrier per K step.
+//     pieces), D K-steps ahead in registers.
+//   * A (token rows, gathered) is loaded to registers two steps ahead and
+//     written to one of two LDS stages one step ahead, fragment-major with a
+//     per-row swap of the 16-byte halves ((r>>2 ^ r>>3) & 1) so 16-byte
+//     reads are conflict-free; one barrier per K step.
 //   * The products a_scale[row, kb] * w_scale[block, kb] of the whole K
 //     range are computed once per workgroup into LDS, so the K loop's VALU
-//     work is the 4 FMAs per MFMA and little else.
-// Workgroup: 512 threads = 2 (M) x 4 (N) waves, two per SIMD; tile BM rows
-// x 256 weight rows (stage 1: 128 gate rows + the matching 128 up rows = 128
-// outputs; stage 2: 256 outputs); each wave (BM/2) x 64.  Tile order is
-// XCD-aware: workgroup L runs on XCD L % 8, and each XCD owns n_tiles/8
-// column tiles of every M-block so an expert's weight slice stays in its L2.
+//     work is the 4 FMAs per MFMA and little else; each wave folds row tile
+//     r while the MFMAs of row tile r+1 run.
+// Workgroup: 256 threads = 4 waves along N, two workgroups per CU (one wave
+// of each per SIMD), so one workgroup's prologue and epilogue run under the
+// other's K loop.  Stage 1: 64 rows (half a 128-row sorted block) x 256
+// weight rows (128 gate + the matching 128 up rows = one 1x128 quant group
+// per row); stage 2: 128 (or 64) rows x 128 output columns.  A tile whose
+// rows are all padding exits at once.  Tile order is XCD-aware: workgroup L
+// runs on XCD L % 8, and each XCD owns n_tiles/8 column tiles of every
+// M-block so an expert's weight slice stays in its L2.
 #include "common.h"
 
 namespace aiter_amd {
 
 namespace pf {
 
-constexpr int kThreads = 512;
-constexpr int kWaves = 8;
+constexpr int kThreads = 256;
+constexpr int kWaves = 4;
 constexpr int kMaxKB = 64;     // K <= 8192
 
 struct Args {
@@ -59,7 +61,8 @@ struct Args {
     int E;
     int64_t a_rows;
     int n_tiles;
-    int m_blocks;
+    int m_tiles;               // sorted M-blocks x workgroups per M-block
+    int block_m;               // rows per sorted M-block (BM or 2 BM)
 };
 
 __device__ __forceinline__ int frag_swap(int r) { return ((r >> 2) ^ (r >> 3)) & 1; }
@@ -71,11 +74,55 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, int64_t
                                              0x00020000);
 }
 
-// Waves along M in the 8-wave workgroup (template WM): 2 -> 2 x 4 waves of
-// (BM/2) x 64 (the two M-waves of a SIMD load the same weight fragments, the
-// second from L1); 1 -> each wave owns all BM rows and 32 weight rows (no
-// weight fragment is loaded twice, every wave reads all A rows from LDS).
-// Measured on MI355X: 2 x 4 for stage 1 (K = 4096), 1 x 8 for stage 2.
+// a_scale[row, kb] * w_scale[block h, kb] for row r, K blocks q, q + RP, ...
+// (RP = threads per row) into s_sc[kb][h][row]; NJ covers the K range. The
+// loads (clamped addresses, no branches) and the products are separate calls
+// so the caller can issue other loads in between.
+template <int N>
+struct IntC {
+    static constexpr int value = N;
+};
+
+template <bool W4, int NJ>
+struct ScaleRegs {
+    float av[NJ];
+    float b0[W4 ? 1 : NJ];
+    float b1[W4 ? 1 : NJ];
+};
+
+template <int BM, int NH, bool W4, int NJ>
+__device__ __forceinline__ void scale_load(ScaleRegs<W4, NJ>& sr, const float* sa, int64_t sa_kb,
+                                           const float* w0, const float* w1, int KB, int q) {
+    constexpr int RP = kThreads / BM;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        const int kb = q + j * RP;
+        const int kc = kb < KB ? kb : KB - 1;
+        sr.av[j] = sa[(int64_t)kc * sa_kb];
+        if (!W4) {
+            sr.b0[j] = w0[kc];
+            if (NH == 2) sr.b1[j] = w1[kc];
+        }
+    }
+}
+
+template <int BM, int NH, bool W4, int NJ>
+__device__ __forceinline__ void scale_store(const ScaleRegs<W4, NJ>& sr, float* s_sc, int KB,
+                                            int r, int q, bool valid) {
+    constexpr int RP = kThreads / BM;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        const int kb = q + j * RP;
+        if (kb < KB) {
+            const float v = valid ? sr.av[j] : 0.0f;
+            s_sc[(kb * NH) * BM + r] = W4 ? v : v * sr.b0[j];
+            if (!W4 && NH == 2) s_sc[(kb * NH + 1) * BM + r] = v * sr.b1[j];
+        }
+    }
+}
+
+// Waves along M (template kWM): 1 -> every wave owns all BM rows; 2 -> 2 x 2
+// waves of BM/2 rows (the two M-waves load the same weight fragments).
 
 // One K step of a wave's B operand (NCT 16-row weight groups).
 template <bool W4, int NCT>
@@ -85,13 +132,18 @@ struct BStep {
 };
 
 template <int BM, int STAGE, bool SHUFFLED, bool W4, int D, int kWM>
-__global__ __launch_bounds__(kThreads, 1) void moe_gemm_prefill_kernel(Args g) {
+__global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
     constexpr int WN = kWaves / kWM;                     // waves along N
-    constexpr int NCT = 16 / WN;                         // 16-row weight groups per wave
+    // 16-row weight groups per wave: stage 1 256 weight rows (128 gate + the
+    // matching 128 up rows) per workgroup, stage 2 128
+    constexpr int NCT = STAGE == 1 ? 16 / WN : 8 / WN;
+    constexpr int NW = 16 * NCT * WN;                    // weight rows per workgroup
     constexpr int NRT = BM / 16 / kWM;                   // 16-row MFMA tiles per wave
     constexpr int A_BYTES = BM * 128;
     constexpr int A_PT = A_BYTES / 16 / kThreads;        // 16-byte A pieces per thread
-    constexpr int NH = W4 ? 1 : 2;                       // scale products per (row, kb)
+    // scale products per (row, kb): stage 1 gate / up blocks; stage 2 the
+    // workgroup's 128-column weight-scale blocks
+    constexpr int NH = W4 ? 1 : (STAGE == 1 ? 2 : NW / 128);
     static_assert(BM == 64 || BM == 128, "prefill tiles are 64 or 128 rows");
     static_assert(A_PT >= 1, "one A piece per thread at least");
     __shared__ __attribute__((aligned(1024))) uint8_t s_a[2][A_BYTES];
@@ -111,26 +163,30 @@ __global__ __launch_bounds__(kThreads, 1) void moe_gemm_prefill_kernel(Args g) {
 
     // ---- XCD-aware tile order ----
     const int L = blockIdx.x;
-    int nt, mb;
+    int nt, mt;
     if ((g.n_tiles & 7) == 0) {
         const int per = g.n_tiles >> 3;
         const int idx = L >> 3;
         nt = (L & 7) * per + idx % per;
-        mb = idx / per;
+        mt = idx / per;
     } else {
         nt = L % g.n_tiles;
-        mb = L / g.n_tiles;
+        mt = L / g.n_tiles;
     }
-    if (mb >= g.m_blocks) return;
+    if (mt >= g.m_tiles) return;
+    const int subs = g.block_m / BM;                     // workgroups per sorted M-block
+    const int mb = mt / subs;
+    const int srow0 = mb * g.block_m + (mt % subs) * BM; // first sorted row of the tile
     const int nvalid = g.num_valid[0];
-    if (mb * BM >= nvalid) return;
+    if (srow0 >= nvalid) return;
     const int tokens = g.num_valid[1];
     const int e = g.sorted_eids[mb];
     if (e < 0 || e >= g.E) return;
-    const int n0 = STAGE == 1 ? nt * 128 : nt * 256;
+    const int n0 = STAGE == 1 ? nt * 128 : nt * NW;
 
+    int any_valid = 0;
     for (int r = tid; r < BM; r += kThreads) {
-        const uint32_t id = (uint32_t)g.sorted_ids[mb * BM + r];
+        const uint32_t id = (uint32_t)g.sorted_ids[srow0 + r];
         const int t = (int)(id & 0xFFFFFFu);
         const int s = (int)(id >> 24);
         const bool valid = t < tokens && s < g.topk;
@@ -143,32 +199,16 @@ __global__ __launch_bounds__(kThreads, 1) void moe_gemm_prefill_kernel(Args g) {
         }
         s_arow[r] = (int32_t)arow;
         s_orow[r] = orow;
-        s_w[r] = STAGE == 2 && valid ? g.sorted_w[mb * BM + r] : 0.0f;
+        s_w[r] = STAGE == 2 && valid ? g.sorted_w[srow0 + r] : 0.0f;
+        any_valid |= (int)valid;
     }
-    __syncthreads();
+    // a tile whose rows are all padding (the end of an expert's last
+    // M-block) has nothing to compute
+    if (__syncthreads_or(any_valid) == 0) return;
 
     const int K = g.K;
     const int KB = K / 128;
     const int KBY = W4 ? K / 2 : K;
-
-    // ---- scale products of the whole K range: [kb][h][row] ----
-    // fp8: h = 0 / 1 are stage 1's gate / up blocks or stage 2's two
-    // 128-column blocks; A8W4: the activation scale only (the weight scale
-    // goes into the MFMA)
-    {
-        const float* wse = W4 ? nullptr : g.w_scale + (int64_t)e * (g.N / 128) * KB;
-        const int nb0 = n0 / 128;
-        const int nb1 = STAGE == 1 ? (g.inter + n0) / 128 : n0 / 128 + 1;
-        for (int i = tid; i < KB * NH * BM; i += kThreads) {
-            const int r = i % BM;
-            const int h = (i / BM) % NH;
-            const int kb = i / (NH * BM);
-            const int arow = s_arow[r];
-            float v = arow >= 0 ? g.a_scale[arow * g.sa_row + kb * g.sa_kb] : 0.0f;
-            if (!W4) v *= wse[(h == 0 ? nb0 : nb1) * KB + kb];
-            s_sc[i] = v;
-        }
-    }
 
     // ---- A staging: piece p = tid + j*512 -> 1 KB chunk c = p/64 (rows
     // 32*(c % (BM/32)) .. +31 of K quarter kq = c / (BM/32)), position l = p%64
@@ -248,12 +288,24 @@ __global__ __launch_bounds__(kThreads, 1) void moe_gemm_prefill_kernel(Args g) {
         for (int ct = 0; ct < NCT; ++ct) acc[rt][ct] = v4f{0.f, 0.f, 0.f, 0.f};
     const int row_base = wm * (BM / kWM);
     const int h0 = frag_swap(lr);
+    // row tiles of this wave that hold a routed row (sorting pads each
+    // expert's last block at its end): the MFMAs and FMAs of the others
+    // are skipped, their accumulators stay 0 and their rows are not stored
+    int nact = 0;
+#pragma unroll
+    for (int rt = 0; rt < NRT; ++rt)
+        if (__builtin_amdgcn_ballot_w64(s_arow[row_base + rt * 16 + lr] >= 0) != 0) nact = rt + 1;
+    nact = __builtin_amdgcn_readfirstlane(nact);
 
-    // One K step: NRT x 4 MFMAs, row tile by row tile (the B fragments stay
-    // in registers for the whole step, so only two A fragments are live);
-    // the MFMAs of row tile r+1 are issued into the other of two result sets
-    // while the FMAs fold tile r.
-    auto compute = [&](const BS& bsv, int kb, int stage) {
+    // One K step: nact x NCT MFMAs, row tile by row tile (the B fragments
+    // stay in registers for the whole step). Region r of the step issues the
+    // MFMAs of row tile r+1 into one of two result sets, prefetches the next
+    // A fragment and scale products from LDS, and folds row tile r's results
+    // (issued one region earlier) into the accumulators. The regions are
+    // fenced so the scheduler cannot pair an FMA with the MFMA that feeds it
+    // (which serialises a wave on MFMA latency).
+    auto compute = [&](const BS& bsv, int kb, int stage, auto na) {
+        constexpr int NA = decltype(na)::value;
         const uint8_t* sa_src = &s_a[stage][0];
         auto afrag = [&](int rt) {
             const uint8_t* slot = sa_src + lq * (BM * 32) + (row_base + rt * 16 + lr) * 32;
@@ -273,71 +325,128 @@ __global__ __launch_bounds__(kThreads, 1) void moe_gemm_prefill_kernel(Args g) {
             return W4 ? mfma16x16x128_fp8_fp4(a, bfrag(ct), bsv.bs[ct])
                       : mfma16x16x128_fp8(a, bfrag(ct));
         };
-        // scale half of column tile ct: stage 1 gate (tiles 0,1) / up (2,3);
+        // scale half of column tile ct: stage 1 gate (ct < NCT/2) / up;
         // stage 2 the wave's 128-column block
-        const int hblk = (wn * NCT * 16) / 128;           // stage 2: the wave's 128-column block
+        const int hblk = (wn * NCT * 16) / 128;
         const int hsel0 = W4 ? 0 : (STAGE == 1 ? 0 : hblk);
         const int hsel1 = W4 ? 0 : (STAGE == 1 ? 1 : hblk);
         const float* sc_row = &s_sc[kb * NH * BM + row_base + 4 * lq];
-        v4f blk[2][NCT];
-        {
-            const v8i a0 = afrag(0);
-#pragma unroll
-            for (int ct = 0; ct < NCT; ++ct) blk[0][ct] = mfma(a0, ct);
-        }
-#pragma unroll
-        for (int rt = 0; rt < NRT; ++rt) {
-            const int cur = rt & 1;
-            if (rt + 1 < NRT) {
-                const v8i an = afrag(rt + 1);
-#pragma unroll
-                for (int ct = 0; ct < NCT; ++ct) blk[cur ^ 1][ct] = mfma(an, ct);
-            }
-            const v4f s0 = *reinterpret_cast<const v4f*>(sc_row + hsel0 * BM + rt * 16);
-            const v4f s1 = *reinterpret_cast<const v4f*>(sc_row + hsel1 * BM + rt * 16);
+        auto scales = [&](int rt, v4f& s0, v4f& s1) {
+            s0 = *reinterpret_cast<const v4f*>(sc_row + hsel0 * BM + rt * 16);
+            s1 = *reinterpret_cast<const v4f*>(sc_row + hsel1 * BM + rt * 16);
+        };
+        auto fold = [&](const v4f (&b)[NCT], int rt, const v4f& s0, const v4f& s1) {
 #pragma unroll
             for (int ct = 0; ct < NCT; ++ct)
 #pragma unroll
                 for (int v = 0; v < 4; ++v)
-                    acc[rt][ct][v] += blk[cur][ct][v] * (ct < NCT / 2 ? s0[v] : s1[v]);
+                    acc[rt][ct][v] += b[ct][v] * (ct < NCT / 2 ? s0[v] : s1[v]);
+        };
+        v4f blk[2][NCT];
+        v8i an;
+        v4f s0, s1;
+        if (NA > 0) {
+            an = afrag(0);
 #pragma unroll
-            for (int i = 0; i < NCT; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-                __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // VALU
+            for (int ct = 0; ct < NCT; ++ct) blk[0][ct] = mfma(an, ct);
+            if (NRT > 1) an = afrag(1);
+            scales(0, s0, s1);
+        }
+#pragma unroll
+        for (int rt = 0; rt < NRT; ++rt) {
+            const int cur = rt & 1;
+            __builtin_amdgcn_sched_barrier(0);
+            if (rt + 1 < NA) {
+                v4f n0, n1;
+#pragma unroll
+                for (int ct = 0; ct < NCT; ++ct) blk[cur ^ 1][ct] = mfma(an, ct);
+                if (rt + 2 < NRT) an = afrag(rt + 2);
+                scales(rt + 1, n0, n1);
+                fold(blk[cur], rt, s0, s1);
+#pragma unroll
+                for (int i = 0; i < NCT; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // VALU
+                }
+                s0 = n0;
+                s1 = n1;
+            } else if (rt < NA) {
+                fold(blk[cur], rt, s0, s1);
             }
         }
+        __builtin_amdgcn_sched_barrier(0);
     };
 
     // ---- K loop: B D steps ahead in registers; A two steps ahead in
     // registers and double-buffered in LDS; one barrier per step ----
     BS bbuf[D];
+    // ---- preheader: the loads of the K loop's virtual steps -3 .. -1 in the
+    // loop's own order (step j loads A(j+3), then B(j+D)), so the wait
+    // counts at the loop head are the steady-state ones; the scale loads go
+    // first (oldest) and their products are stored once they land ----
+    // scale products of the whole K range, [kb][h][row]: fp8 h = 0 / 1 are
+    // stage 1's gate / up blocks or stage 2's two 128-column blocks; A8W4 the
+    // activation scale only (the weight scale goes into the MFMA)
+    const int sr_r = tid % BM, sr_q = tid / BM;
+    const int sr_arow = s_arow[sr_r];
+    const float* sr_a = g.a_scale + (int64_t)(sr_arow < 0 ? 0 : sr_arow) * g.sa_row;
+    const float* sr_w = W4 ? g.a_scale : g.w_scale + (int64_t)e * (g.N / 128) * KB;
+    const float* sr_w0 = sr_w + (n0 / 128) * KB;
+    // second block (NH == 2 only): stage 1's up rows, stage 2's next 128 columns
+    const float* sr_w1 = sr_w + (STAGE == 1 ? (g.inter + n0) / 128 : n0 / 128 + NH - 1) * KB;
+    auto last = [&](int m) { return m < KB ? m : KB - 1; };
+    auto preheader = [&](auto nj) {
+        constexpr int NJ = decltype(nj)::value;
+        ScaleRegs<W4, NJ> sr;
+        scale_load<BM, NH, W4, NJ>(sr, sr_a, g.sa_kb, sr_w0, sr_w1, KB, sr_q);
 #pragma unroll
-    for (int d = 0; d < D; ++d) load_b(bbuf[d], d);
-    load_a(0, 0);
-    store_a(0);
-    load_a(1, KB > 1 ? 1 : 0);
-    load_a(0, KB > 2 ? 2 : KB - 1);
+        for (int m = 0; m < D - 3; ++m) load_b(bbuf[m], last(m));
+        load_a(0, 0);                                           // step -3
+        if constexpr (D >= 3) load_b(bbuf[D - 3], last(D - 3));
+        load_a(1, last(1));                                     // step -2
+        if constexpr (D >= 2) load_b(bbuf[D - 2], last(D - 2));
+        scale_store<BM, NH, W4, NJ>(sr, s_sc, KB, sr_r, sr_q, sr_arow >= 0);
+        store_a(0);                                             // step -1
+        load_a(0, last(2));
+        load_b(bbuf[D - 1], last(D - 1));
+    };
+    constexpr int RP = kThreads / BM;
+    if (KB <= 16)
+        preheader(IntC<16 / RP>{});
+    else if (KB <= 32)
+        preheader(IntC<32 / RP>{});
+    else
+        preheader(IntC<kMaxKB / RP>{});
     __syncthreads();                      // stage 0 and the scale products
-    for (int kb0 = 0; kb0 < KB; kb0 += D) {
+    auto kloop = [&](auto na) {
+        for (int kb0 = 0; kb0 < KB; kb0 += D) {
 #pragma unroll
-        for (int d = 0; d < D; ++d) {
-            const int k = kb0 + d;
-            // Everything in the step is unconditional so the loop is one basic
-            // block and the compiler's wait counts stay exact: past the end the
-            // loads re-read the last step (L2 hits) and the store fills the
-            // stage that step k does not read.
-            store_a((k + 1) & 1);
-            load_a((k + 1) & 1, k + 3 < KB ? k + 3 : KB - 1);
-            // issue the A loads before the step's math (a full step to land)
-            __builtin_amdgcn_sched_barrier(0);
-            compute(bbuf[d], k, k & 1);
-            load_b(bbuf[d], k + D < KB ? k + D : KB - 1);
-            __syncthreads();
-            // keep the scheduler from interleaving the unrolled steps (their
-            // operand sets would all be live at once)
-            __builtin_amdgcn_sched_barrier(0);
+            for (int d = 0; d < D; ++d) {
+                const int k = kb0 + d;
+                // Everything in the step is unconditional so the loop is one basic
+                // block and the compiler's wait counts stay exact: past the end the
+                // loads re-read the last step (L2 hits) and the store fills the
+                // stage that step k does not read.
+                store_a((k + 1) & 1);
+                load_a((k + 1) & 1, k + 3 < KB ? k + 3 : KB - 1);
+                // issue the A loads before the step's math (a full step to land)
+                __builtin_amdgcn_sched_barrier(0);
+                compute(bbuf[d], k, k & 1, na);
+                load_b(bbuf[d], k + D < KB ? k + D : KB - 1);
+                __syncthreads();
+                // keep the scheduler from interleaving the unrolled steps (their
+                // operand sets would all be live at once)
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
-    }
+    };
+    // a wave whose rows are all padding runs a copy of the K loop without
+    // math (it still stages A and meets every barrier); more copies, one
+    // per active row-tile count, push the kernel past 256 registers
+    if (kWM > 1 && nact == 0)
+        kloop(IntC<0>{});
+    else
+        kloop(IntC<NRT>{});
 
     if (STAGE == 2) {
 #pragma unroll
@@ -411,8 +520,11 @@ __global__ __launch_bounds__(kThreads, 1) void moe_gemm_prefill_kernel(Args g) {
 
 template <int BM, int STAGE, bool SHUFFLED, bool W4>
 static void launch_depth(int KB, int grid, const Args& a, hipStream_t s) {
-    constexpr int WM = STAGE == 1 ? 2 : 1;
-    constexpr int DM = STAGE == 1 ? 2 : 4;      // the 1 x 8 tile has registers for 4 steps
+    // 1 x 4 waves: stage 1 64 rows x 64 weight rows per wave, B two steps
+    // ahead; stage 2 BM rows x 32 columns, B four steps ahead (measured on
+    // MI355X against 2 x 2 waves for stage 2: 1230 vs 1282 us at T=8192)
+    constexpr int WM = 1;
+    constexpr int DM = STAGE == 1 ? 2 : 4;
     if (DM >= 4 && KB % 4 == 0)
         hipLaunchKernelGGL((moe_gemm_prefill_kernel<BM, STAGE, SHUFFLED, W4, DM >= 4 ? 4 : 2, WM>),
                            dim3(grid), dim3(kThreads), 0, s, a);
@@ -424,14 +536,20 @@ static void launch_depth(int KB, int grid, const Args& a, hipStream_t s) {
                            dim3(kThreads), 0, s, a);
 }
 
+// Rows per workgroup: stage 1 always 64 (a 128-row sorted block is two
+// workgroups); stage 2 the sorted block size.
+template <int STAGE>
+constexpr int wg_rows(int block_m) { return STAGE == 1 ? 64 : block_m; }
+
 template <int STAGE, bool SHUFFLED, bool W4>
 static void launch_bm(int bm, int KB, int grid, const Args& a, hipStream_t s) {
-    if (bm == 64)
+    AMD_CHECK(bm == 64 || bm == 128, "prefill GEMM block_m must be 64 or 128");
+    if constexpr (STAGE == 1)
         launch_depth<64, STAGE, SHUFFLED, W4>(KB, grid, a, s);
-    else if (bm == 128)
-        launch_depth<128, STAGE, SHUFFLED, W4>(KB, grid, a, s);
+    else if (bm == 64)
+        launch_depth<64, STAGE, SHUFFLED, W4>(KB, grid, a, s);
     else
-        AMD_CHECK(false, "prefill GEMM block_m must be 64 or 128");
+        launch_depth<128, STAGE, SHUFFLED, W4>(KB, grid, a, s);
 }
 
 template <int STAGE>
@@ -484,8 +602,9 @@ void launch_moe_stage1_prefill(const uint8_t* a, const float* a_scale, int64_t s
     g.E = (int)E;
     g.a_rows = a_rows;
     g.n_tiles = (int)(inter / 128);
-    g.m_blocks = (int)max_m_blocks;
-    const int64_t grid = (int64_t)g.n_tiles * max_m_blocks;
+    g.block_m = (int)block_m;
+    g.m_tiles = (int)(max_m_blocks * (block_m / pf::wg_rows<1>((int)block_m)));
+    const int64_t grid = (int64_t)g.n_tiles * g.m_tiles;
     if (grid == 0) return;
     pf::launch<1>((int)block_m, (int)(K / 128), (int)grid, g, shuffled, stream);
     AMD_HIP_CHECK(hipGetLastError());
@@ -517,9 +636,10 @@ void launch_moe_stage2_prefill(const uint8_t* a2, const float* a2_scale, const u
     g.topk = (int)topk;
     g.E = (int)E;
     g.a_rows = a_rows;
-    g.n_tiles = (int)(hidden / 256);
-    g.m_blocks = (int)max_m_blocks;
-    const int64_t grid = (int64_t)g.n_tiles * max_m_blocks;
+    g.n_tiles = (int)(hidden / 128);
+    g.block_m = (int)block_m;
+    g.m_tiles = (int)(max_m_blocks * (block_m / pf::wg_rows<2>((int)block_m)));
+    const int64_t grid = (int64_t)g.n_tiles * g.m_tiles;
     if (grid == 0) return;
     pf::launch<2>((int)block_m, (int)(inter / 128), (int)grid, g, shuffled, stream);
     AMD_HIP_CHECK(hipGetLastError());
