@@ -139,6 +139,11 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
     constexpr int NCT = STAGE == 1 ? 16 / WN : 8 / WN;
     constexpr int NW = 16 * NCT * WN;                    // weight rows per workgroup
     constexpr int NRT = BM / 16 / kWM;                   // 16-row MFMA tiles per wave
+    // FP8 stage 1 computes the transposed tile (weights as the MFMA's A
+    // operand): a lane then holds one token row and four consecutive output
+    // columns, so its activation scale is one value per row tile and its
+    // fp8 outputs pack into one dword
+    constexpr bool TR = STAGE == 1 && !W4;
     constexpr int A_BYTES = BM * 128;
     constexpr int A_PT = A_BYTES / 16 / kThreads;        // 16-byte A pieces per thread
     // scale products per (row, kb): stage 1 gate / up blocks; stage 2 the
@@ -322,6 +327,7 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
                        bsv.b[ct][W4 ? 0 : 1][2], bsv.b[ct][W4 ? 0 : 1][3]};
         };
         auto mfma = [&](const v8i& a, int ct) {
+            if constexpr (TR) return mfma16x16x128_fp8(bfrag(ct), a);
             return W4 ? mfma16x16x128_fp8_fp4(a, bfrag(ct), bsv.bs[ct])
                       : mfma16x16x128_fp8(a, bfrag(ct));
         };
@@ -330,8 +336,15 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
         const int hblk = (wn * NCT * 16) / 128;
         const int hsel0 = W4 ? 0 : (STAGE == 1 ? 0 : hblk);
         const int hsel1 = W4 ? 0 : (STAGE == 1 ? 1 : hblk);
-        const float* sc_row = &s_sc[kb * NH * BM + row_base + 4 * lq];
+        const float* sc_row = &s_sc[kb * NH * BM + row_base + (TR ? lr : 4 * lq)];
         auto scales = [&](int rt, v4f& s0, v4f& s1) {
+            if constexpr (TR) {
+                const float x0 = sc_row[hsel0 * BM + rt * 16];
+                const float x1 = sc_row[hsel1 * BM + rt * 16];
+                s0 = v4f{x0, x0, x0, x0};
+                s1 = v4f{x1, x1, x1, x1};
+                return;
+            }
             s0 = *reinterpret_cast<const v4f*>(sc_row + hsel0 * BM + rt * 16);
             s1 = *reinterpret_cast<const v4f*>(sc_row + hsel1 * BM + rt * 16);
         };
@@ -466,8 +479,11 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
     }
 
     // ---- stage 1 epilogue: silu(gate)*up -> bf16 -> 1x128 fp8 requant ----
-    // wave wn holds output columns wn*NH1*16 + j*16 + lr (j < NH1) of the tile's 128
+    // wave wn holds output columns wn*NH1*16 + j*16 + (TR ? 4*lq + v : lr)
+    // (j < NH1) of the tile's 128, for rows row_base + rt*16 + (TR ? lr :
+    // 4*lq + v)
     constexpr int NH1 = NCT / 2;
+    constexpr int QP = 144;     // s_q row pitch: 16-byte aligned, conflict-free dword stores
     float h[NRT][NH1][4];
 #pragma unroll
     for (int rt = 0; rt < NRT; ++rt)
@@ -476,16 +492,30 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
 #pragma unroll
             for (int v = 0; v < 4; ++v)
                 h[rt][j][v] = bf16_round(silu_f32(acc[rt][j][v]) * acc[rt][NH1 + j][v]);
+    if constexpr (TR) {
 #pragma unroll
-    for (int rt = 0; rt < NRT; ++rt)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
+        for (int rt = 0; rt < NRT; ++rt) {
             float m = 0.0f;
 #pragma unroll
-            for (int j = 0; j < NH1; ++j) m = __builtin_fmaxf(m, __builtin_fabsf(h[rt][j][v]));
-            m = warp_max_16(m);
-            if (lr == 0) s_amax[wn][row_base + rt * 16 + 4 * lq + v] = m;
+            for (int j = 0; j < NH1; ++j)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) m = __builtin_fmaxf(m, __builtin_fabsf(h[rt][j][v]));
+            m = __builtin_fmaxf(m, __shfl_xor(m, 16, 64));
+            m = __builtin_fmaxf(m, __shfl_xor(m, 32, 64));
+            if (lq == 0) s_amax[wn][row_base + rt * 16 + lr] = m;
         }
+    } else {
+#pragma unroll
+        for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                float m = 0.0f;
+#pragma unroll
+                for (int j = 0; j < NH1; ++j) m = __builtin_fmaxf(m, __builtin_fabsf(h[rt][j][v]));
+                m = warp_max_16(m);
+                if (lr == 0) s_amax[wn][row_base + rt * 16 + 4 * lq + v] = m;
+            }
+    }
     __syncthreads();
     auto row_amax = [&](int row) {
         float m = s_amax[0][row];
@@ -493,19 +523,33 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
         for (int w = 1; w < WN; ++w) m = __builtin_fmaxf(m, s_amax[w][row]);
         return __builtin_fmaxf(m, 1e-10f);
     };
-    uint8_t* s_q = &s_a[0][0];  // [BM][128] fp8 staging (the K loop is done)
+    uint8_t* s_q = &s_a[0][0];  // [BM][QP] fp8 staging over both A stages (the K loop is done)
+    static_assert(BM * QP <= 2 * A_BYTES, "fp8 staging fits the A stages");
+    if constexpr (TR) {
 #pragma unroll
-    for (int rt = 0; rt < NRT; ++rt)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const int row = row_base + rt * 16 + 4 * lq + v;
+        for (int rt = 0; rt < NRT; ++rt) {
+            const int row = row_base + rt * 16 + lr;
             const float inv = 1.0f / (row_amax(row) * kInvFp8Max);
 #pragma unroll
-            for (int j = 0; j < NH1; ++j) {
-                const uint32_t b = f32x2_to_fp8x2(h[rt][j][v] * inv, 0.0f) & 0xFFu;
-                s_q[row * 128 + wn * NH1 * 16 + j * 16 + lr] = (uint8_t)b;
-            }
+            for (int j = 0; j < NH1; ++j)
+                *reinterpret_cast<uint32_t*>(&s_q[row * QP + wn * NH1 * 16 + j * 16 + 4 * lq]) =
+                    f32x4_to_fp8x4(h[rt][j][0] * inv, h[rt][j][1] * inv, h[rt][j][2] * inv,
+                                   h[rt][j][3] * inv);
         }
+    } else {
+#pragma unroll
+        for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int row = row_base + rt * 16 + 4 * lq + v;
+                const float inv = 1.0f / (row_amax(row) * kInvFp8Max);
+#pragma unroll
+                for (int j = 0; j < NH1; ++j) {
+                    const uint32_t b = f32x2_to_fp8x2(h[rt][j][v] * inv, 0.0f) & 0xFFu;
+                    s_q[row * QP + wn * NH1 * 16 + j * 16 + lr] = (uint8_t)b;
+                }
+            }
+    }
     __syncthreads();
     const int I = g.inter;
     for (int q = tid; q < BM * 8; q += kThreads) {
@@ -513,7 +557,7 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
         const int64_t orow = s_orow[row];
         if (orow < 0) continue;
         *reinterpret_cast<v4i*>(g.a2 + orow * I + n0 + part * 16) =
-            *reinterpret_cast<const v4i*>(s_q + row * 128 + part * 16);
+            *reinterpret_cast<const v4i*>(s_q + row * QP + part * 16);
         if (part == 0) g.a2_scale[orow * (I / 128) + n0 / 128] = row_amax(row) * kInvFp8Max;
     }
 }
