@@ -33,6 +33,14 @@ from .quant import (
     quant_weight_per_128x128,
 )
 from .shuffle import shuffle_weight, unshuffle_weight
+from .topk import (
+    biased_grouped_topk,
+    biased_grouped_topk_hip,
+    fused_topk,
+    grouped_topk,
+    topk_sigmoid,
+    topk_softmax,
+)
 
 __all__ = [
     "ActivationType", "QuantType", "dtypes", "quant_remap", "BLOCK_SIZE_M", "default_block_m",
@@ -40,5 +48,6 @@ __all__ = [
     "moe_stage1_fp8_blockscale", "moe_stage2_fp8_blockscale", "moe_stage1_a8w4",
     "moe_stage2_a8w4", "sorted_capacity", "dynamic_per_token_scaled_quant", "per_group_quant_hip",
     "quant_weight_per_128x128", "per_1x32_f4_quant", "f32_to_e8m0", "e8m0_to_f32",
-    "shuffle_weight", "unshuffle_weight",
+    "shuffle_weight", "unshuffle_weight", "topk_softmax", "topk_sigmoid", "grouped_topk",
+    "biased_grouped_topk", "biased_grouped_topk_hip", "fused_topk",
 ]

@@ -30,6 +30,14 @@ _SIGNATURES = {
     "aiter_amd_clear_last_error": (None, []),
     "aiter_amd_moe_sorting_workspace_bytes": (c_i64, [c_i64, c_i64, c_i64]),
     "aiter_amd_default_block_m": (c_i64, [c_i64, c_i64, c_i64, c_i64, c_i64]),
+    "aiter_amd_topk_softmax": (
+        c_int, [c_vp, c_int, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_int, c_vp]),
+    "aiter_amd_topk_sigmoid": (
+        c_int, [c_vp, c_int, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp]),
+    "aiter_amd_grouped_topk": (
+        c_int,
+        [c_vp, c_int, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, c_int, c_int, ctypes.c_float, c_vp,
+         c_i64, c_vp, c_i64, c_vp]),
     "aiter_amd_moe_sorting_fwd": (
         c_int,
         [c_vp, c_vp, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_vp, c_i64, c_i64,

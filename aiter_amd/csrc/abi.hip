@@ -56,6 +56,13 @@ void launch_moe_stage2_stream(const uint8_t*, const float*, const uint8_t*, cons
                               const int32_t*, float*, int64_t, int64_t, int64_t, int64_t,
                               int64_t, int64_t, int64_t, int, hipStream_t);
 
+// moe_route.hip (router top-k)
+bool route_supported(int64_t E, int64_t k);
+void launch_moe_route(const void* gating, int dtype, int64_t M, int64_t E, int64_t k, int mode,
+                      int need_renorm, int softmax_scores, int64_t n_group, int64_t topk_group,
+                      float scaling, const float* bias, float* w, int64_t ws, int32_t* ids,
+                      int64_t is, int32_t* tei, hipStream_t stream);
+
 // moe_gemm_prefill.hip (64/128-row M-blocks, weight fragments in registers)
 bool prefill_supported(int64_t block_m, int64_t K);
 void launch_moe_stage1_prefill(const uint8_t*, const float*, int64_t, int64_t, const uint8_t*,
@@ -519,6 +526,76 @@ int aiter_amd_fused_moe_a8w4(const void* hidden_states, int hidden_dtype, const 
                     WScale{nullptr, w2_scale}, topk_weights, topk_ids, expert_mask,
                     num_local_tokens, out, out_dtype, tokens, model_dim, inter_dim, num_experts,
                     global_experts, topk, block_m, w_shuffled, workspace, workspace_bytes, stream);
+    });
+}
+
+static void check_route(const void* gating, int dtype, int64_t tokens, int64_t E, int64_t topk,
+                        const float* w, int64_t ws, const int32_t* ids, int64_t is) {
+    AMD_CHECK(dtype == DT_FP32 || dtype == DT_BF16 || dtype == DT_FP16,
+              "gating dtype must be fp32, bf16 or fp16");
+    AMD_CHECK(tokens >= 0, "tokens must be >= 0");
+    AMD_CHECK(route_supported(E, topk), "need 1 <= topk <= min(num_experts, 32) and "
+                                        "num_experts <= 1024, got topk " + std::to_string(topk) +
+                                        ", num_experts " + std::to_string(E));
+    AMD_CHECK(ws >= topk && is >= topk, "output row strides must be >= topk");
+    if (tokens == 0) return;
+    AMD_CHECK(gating && w && ids, "a required pointer is NULL");
+}
+
+int aiter_amd_topk_softmax(const void* gating, int gating_dtype, int64_t tokens,
+                           int64_t num_experts, int64_t topk, float* topk_weights,
+                           int64_t weights_stride, int32_t* topk_ids, int64_t ids_stride,
+                           int32_t* token_expert_indices, int need_renorm, void* stream) {
+    return safe_call([&] {
+        check_route(gating, gating_dtype, tokens, num_experts, topk, topk_weights,
+                    weights_stride, topk_ids, ids_stride);
+        if (tokens == 0) return;
+        launch_moe_route(gating, gating_dtype, tokens, num_experts, topk, 0, need_renorm != 0, 0,
+                         1, 1, 1.0f, nullptr, topk_weights, weights_stride, topk_ids, ids_stride,
+                         token_expert_indices, (hipStream_t)stream);
+    });
+}
+
+int aiter_amd_topk_sigmoid(const void* gating, int gating_dtype, int64_t tokens,
+                           int64_t num_experts, int64_t topk, float* topk_weights,
+                           int64_t weights_stride, int32_t* topk_ids, int64_t ids_stride,
+                           void* stream) {
+    return safe_call([&] {
+        check_route(gating, gating_dtype, tokens, num_experts, topk, topk_weights,
+                    weights_stride, topk_ids, ids_stride);
+        if (tokens == 0) return;
+        launch_moe_route(gating, gating_dtype, tokens, num_experts, topk, 1, 0, 0, 1, 1, 1.0f,
+                         nullptr, topk_weights, weights_stride, topk_ids, ids_stride, nullptr,
+                         (hipStream_t)stream);
+    });
+}
+
+int aiter_amd_grouped_topk(const void* gating, int gating_dtype, const float* correction_bias,
+                           int64_t tokens, int64_t num_experts, int64_t topk,
+                           int64_t num_expert_group, int64_t topk_group, int need_renorm,
+                           int is_softmax, float routed_scaling_factor, float* topk_weights,
+                           int64_t weights_stride, int32_t* topk_ids, int64_t ids_stride,
+                           void* stream) {
+    return safe_call([&] {
+        check_route(gating, gating_dtype, tokens, num_experts, topk, topk_weights,
+                    weights_stride, topk_ids, ids_stride);
+        AMD_CHECK(num_expert_group >= 1 && num_expert_group <= 32 &&
+                      num_experts % num_expert_group == 0,
+                  "num_expert_group must divide num_experts and be <= 32");
+        AMD_CHECK(topk_group >= 1 && topk_group <= num_expert_group,
+                  "topk_group must be in [1, num_expert_group]");
+        const int64_t per = num_experts / num_expert_group;
+        AMD_CHECK(topk <= topk_group * per, "topk exceeds the experts of the kept groups");
+        if (correction_bias) {
+            AMD_CHECK(!is_softmax, "biased grouped top-k uses sigmoid scores");
+            AMD_CHECK(per >= 2, "biased grouped top-k needs >= 2 experts per group");
+        }
+        if (tokens == 0) return;
+        launch_moe_route(gating, gating_dtype, tokens, num_experts, topk,
+                         correction_bias ? 3 : 2, need_renorm != 0, is_softmax != 0,
+                         num_expert_group, topk_group, routed_scaling_factor, correction_bias,
+                         topk_weights, weights_stride, topk_ids, ids_stride, nullptr,
+                         (hipStream_t)stream);
     });
 }
 

@@ -24,6 +24,7 @@ import torch
 from . import _abi
 from .enums import AITER_DTYPE, ActivationType, QuantType, dtypes, quant_remap
 from .quant import per_group_quant_hip
+from .topk import fused_topk  # noqa: F401  (aiter.fused_moe.fused_topk)
 
 BLOCK_SIZE_M = 32
 

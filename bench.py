@@ -44,8 +44,9 @@ def parse():
     p.add_argument("--workload", default="prefill8192", type=_workload,
                    help="prefill<T> | decode<T> | a8w4_<T> | ep<T> (e.g. prefill8192, "
                         "decode32, a8w4_1024, ep4096)")
-    p.add_argument("--legs", default="a8w4_32,a8w4_1024,a8w4_8192,ep4096",
-                   help="comma-separated extra workloads reported under 'legs' ('none': skip)")
+    p.add_argument("--legs", default="a8w4_32,a8w4_1024,a8w4_8192,ep4096,route_32,route_8192",
+                   help="comma-separated extra workloads reported under 'legs' ('none': "
+                        "skip); route_<T> times the router top-k kernels at T tokens")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-decode", action="store_true")
     p.add_argument("--kernel-iters", type=int, default=10)
@@ -330,9 +331,40 @@ def cpu_baseline(layer, budget_s=12.0):
     }
 
 
+def route_leg(name, args, dev):
+    """The router step before the layer (moe_route.hip) at T tokens: MiMo's
+    softmax top-8 of 256 experts (bf16 logits) and the DeepSeek-V3-shaped
+    biased grouped top-8 (8 groups, 4 kept). HBM-bound: algorithmic bytes =
+    T*E*2 read + T*k*8 written."""
+    import torch
+
+    import aiter_amd as A
+
+    T = int(name.split("_")[1])
+    E, k = 256, 8
+    g = torch.Generator().manual_seed(T)
+    x = (torch.randn(T, E, generator=g) * 2).to(torch.bfloat16).to(dev)
+    bias = (torch.randn(E, generator=g) * 0.3).to(dev)
+    w = torch.empty(T, k, dtype=torch.float32, device=dev)
+    ids = torch.empty(T, k, dtype=torch.int32, device=dev)
+    iters = max(args.steps, 50)
+    byts = T * E * 2 + T * k * 8
+    out = {"workload": name, "tokens": T, "experts": E, "topk": k, "alg_bytes": byts}
+    for tag, fn in (("softmax_topk", lambda: A.topk_softmax(w, ids, None, x, True)),
+                    ("biased_grouped_topk",
+                     lambda: A.biased_grouped_topk(x, bias, w, ids, 8, 4, True, 2.5))):
+        ms, _ = time_steps(fn, iters, args.warmup)
+        sec = ms * 1e-3
+        out[tag] = {"us": round(ms * 1e3, 2), "hbm_gbps": round(byts / sec / 1e9, 1),
+                    "hbm_peak_frac": round(byts / sec / PEAK_HBM_BPS, 4)}
+    return out
+
+
 def leg(name, args, dev):
     """One extra workload: layer time, throughput, roofline fractions and
     per-stage kernel times."""
+    if name.startswith("route_"):
+        return route_leg(name, args, dev)
     import torch
 
     from aiter_amd import workloads as W

@@ -182,6 +182,49 @@ int aiter_amd_fused_moe_a8w4(const void* hidden_states, int hidden_dtype, const 
                              int64_t topk, int64_t block_m, int64_t w_shuffled, void* workspace,
                              int64_t workspace_bytes, void* stream);
 
+/* ---- routing: top-k experts per token from the router logits ----
+ * gating [tokens, num_experts] fp32/bf16/fp16 (dtype code as above),
+ * contiguous; outputs topk_weights f32 and topk_ids i32 with row strides
+ * weights_stride / ids_stride (elements, >= topk). num_experts <= 1024,
+ * topk <= 32. Ties rank the lower expert (group) index first; rows come out
+ * in rank order. */
+
+/* Replaces topk_softmax / topk_softmax_asm (aiter/ops/moe_op.py:15-36;
+ * csrc/kernels/topk_softmax_kernels.cu:380-500), as called by fused_topk
+ * (aiter/fused_moe.py:1853-1923): experts ranked by logit, weight
+ * exp(x - rowmax) / (sum over the topk if need_renorm, else over the row).
+ * token_expert_indices [tokens, topk] i32 (= rank * tokens + row) or NULL. */
+int aiter_amd_topk_softmax(const void* gating, int gating_dtype, int64_t tokens,
+                           int64_t num_experts, int64_t topk, float* topk_weights,
+                           int64_t weights_stride, int32_t* topk_ids, int64_t ids_stride,
+                           int32_t* token_expert_indices, int need_renorm, void* stream);
+
+/* Replaces topk_sigmoid (aiter/ops/moe_op.py:39-42; semantics
+ * op_tests/test_moe_topk_sigmoid.py:28-32): experts ranked by logit, weight
+ * sigmoid(logit). */
+int aiter_amd_topk_sigmoid(const void* gating, int gating_dtype, int64_t tokens,
+                           int64_t num_experts, int64_t topk, float* topk_weights,
+                           int64_t weights_stride, int32_t* topk_ids, int64_t ids_stride,
+                           void* stream);
+
+/* Replaces grouped_topk (aiter/ops/topk.py:28-38, torch semantics 163-197)
+ * when correction_bias is NULL, and biased_grouped_topk
+ * (aiter/ops/topk.py:15-25,90-160) when it is an f32 [num_experts] array.
+ *   grouped: scores = softmax (is_softmax != 0) or sigmoid of the logits;
+ *     a group's score is its best expert score;
+ *   biased: scores = sigmoid; choice = score + bias; a group's score is the
+ *     sum of its two best choices (is_softmax must be 0).
+ * The topk_group best groups are kept and their experts ranked by choice
+ * (grouped: score); weight = score * routed_scaling_factor / (sum of the
+ * topk scores if need_renorm, else 1). num_expert_group <= 32 divides
+ * num_experts; topk_group <= num_expert_group; topk <= the experts kept. */
+int aiter_amd_grouped_topk(const void* gating, int gating_dtype, const float* correction_bias,
+                           int64_t tokens, int64_t num_experts, int64_t topk,
+                           int64_t num_expert_group, int64_t topk_group, int need_renorm,
+                           int is_softmax, float routed_scaling_factor, float* topk_weights,
+                           int64_t weights_stride, int32_t* topk_ids, int64_t ids_stride,
+                           void* stream);
+
 /* Default M-block (sorted rows per GEMM tile) for a token count: 16 / 32 / 64 by the average
  * rows per expert (<= 8, <= 20, else), 128 once experts average >= 64 rows and the dims allow
  * 128-row tiles.

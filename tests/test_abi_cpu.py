@@ -220,3 +220,29 @@ def test_python_layer_a8w4_checks():
     with pytest.raises(ValueError, match="e8m0"):
         fused_moe(x, w1, w2, tw, ids, quant_type=QuantType.per_1x32, w1_scale=s1.float(),
                   w2_scale=s2)
+
+
+def test_routing_validation_errors(lib):
+    # topk_softmax: topk > 32, E > 1024, strides < topk, bad dtype, NULL
+    _expect_error("aiter_amd_topk_softmax", 16, 4, 8, 256, 33, 16, 33, 16, 33, None, 1, None,
+                  match="topk")
+    _expect_error("aiter_amd_topk_softmax", 16, 4, 8, 2048, 8, 16, 8, 16, 8, None, 1, None,
+                  match="num_experts <= 1024")
+    _expect_error("aiter_amd_topk_softmax", 16, 4, 8, 256, 8, 16, 4, 16, 8, None, 1, None,
+                  match="strides")
+    _expect_error("aiter_amd_topk_softmax", 16, 0, 8, 256, 8, 16, 8, 16, 8, None, 1, None,
+                  match="dtype")
+    _expect_error("aiter_amd_topk_sigmoid", None, 4, 8, 256, 8, 16, 8, 16, 8, None,
+                  match="NULL")
+    # grouped: groups must divide E, topk_group <= groups, topk <= kept experts,
+    # biased needs sigmoid scores
+    _expect_error("aiter_amd_grouped_topk", 16, 4, None, 8, 256, 8, 7, 4, 1, 1, 1.0, 16, 8, 16,
+                  8, None, match="divide")
+    _expect_error("aiter_amd_grouped_topk", 16, 4, None, 8, 256, 8, 8, 9, 1, 1, 1.0, 16, 8, 16,
+                  8, None, match="topk_group")
+    _expect_error("aiter_amd_grouped_topk", 16, 4, None, 8, 256, 9, 32, 1, 1, 1, 1.0, 16, 9, 16,
+                  9, None, match="kept groups")
+    _expect_error("aiter_amd_grouped_topk", 16, 4, 16, 8, 256, 8, 8, 4, 1, 1, 1.0, 16, 8, 16, 8,
+                  None, match="sigmoid")
+    # zero tokens is a no-op
+    _abi.call("aiter_amd_topk_softmax", None, 4, 0, 256, 8, None, 8, None, 8, None, 1, None)

@@ -356,3 +356,94 @@ def test_a8w4_layer_oracle_vs_fp64_brute_force():
             y = W1[ids[t, j]] @ a[t]
             h[t, j] = y[:I] / (1 + np.exp(-y[:I])) * y[I:]
     np.testing.assert_allclose(ref["h"], h, rtol=1e-2, atol=1e-3 * np.abs(h).max())
+
+
+# -------------------------------------------------------------- routing ---
+from oracle import route_ref as RR  # noqa: E402
+from scipy import special  # noqa: E402
+
+
+def _brute_rank(row, k):
+    return sorted(range(len(row)), key=lambda e: (-float(row[e]), e))[:k]
+
+
+@pytest.mark.parametrize("E,k", [(8, 1), (8, 3), (13, 5), (64, 8)])
+def test_route_topk_softmax_oracle_vs_brute_force(E, k):
+    rng = np.random.default_rng(E * 10 + k)
+    # small-integer logits: many exact ties, which must go to the lower index
+    x = rng.integers(-3, 3, size=(40, E)).astype(np.float32)
+    x[0] = 1.0                                   # a row of equal logits
+    for renorm in (True, False):
+        w, ids, tei = RR.topk_softmax_ref(x, k, renorm)
+        for r in range(x.shape[0]):
+            ref = _brute_rank(x[r], k)
+            assert ids[r].tolist() == ref
+            p = special.softmax(x[r].astype(np.float64))[ref]
+            if renorm:
+                p = p / p.sum()
+            np.testing.assert_allclose(w[r], p, rtol=2e-6, atol=0)
+        assert ids[0].tolist() == list(range(k))
+        assert np.array_equal(tei, np.arange(k)[None, :] * x.shape[0] + np.arange(x.shape[0])[:, None])
+
+
+def test_route_topk_sigmoid_oracle():
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((30, 128)).astype(np.float32) * 3
+    w, ids = RR.topk_sigmoid_ref(x, 4)
+    for r in range(30):
+        ref = _brute_rank(x[r], 4)
+        assert ids[r].tolist() == ref
+        np.testing.assert_allclose(w[r], special.expit(x[r, ref].astype(np.float64)), rtol=2e-6)
+
+
+def _grouped_brute(x, k, n_group, topk_group, renorm, softmax, scaling, bias):
+    """Per-row python loops in fp64 (the structure of aiter/ops/topk.py:127-197)."""
+    xs = x.astype(np.float64)
+    s = special.softmax(xs) if (softmax and bias is None) else special.expit(xs)
+    E = len(xs)
+    G = E // n_group
+    c = s if bias is None else s + bias.astype(np.float64)
+    gsc = []
+    for g in range(n_group):
+        vals = sorted(c[g * G:(g + 1) * G], reverse=True)
+        gsc.append(vals[0] if bias is None else vals[0] + vals[1])
+    groups = sorted(range(n_group), key=lambda g: (-gsc[g], g))[:topk_group]
+    cand = [e for e in range(E) if e // G in groups]
+    ids = sorted(cand, key=lambda e: (-c[e], e))[:k]
+    w = np.array([s[e] for e in ids])
+    w = w * scaling / w.sum() if renorm else w * scaling
+    return ids, w
+
+
+@pytest.mark.parametrize("E,n_group,topk_group,k,biased", [
+    (256, 8, 4, 8, False), (256, 8, 4, 8, True), (64, 4, 2, 4, False), (64, 4, 2, 6, True),
+    (48, 3, 1, 5, False)])
+def test_route_grouped_oracle_vs_brute_force(E, n_group, topk_group, k, biased):
+    rng = np.random.default_rng(E + k)
+    x = rng.standard_normal((25, E)).astype(np.float32) * 2
+    bias = (rng.standard_normal(E) * 0.3).astype(np.float32) if biased else None
+    for renorm, softmax, scaling in ((True, True, 1.0), (False, False, 2.5), (True, False, 1.5)):
+        if biased and softmax:
+            continue
+        w, ids = RR.grouped_topk_ref(x, k, n_group, topk_group, renorm, softmax, scaling, bias)
+        for r in range(x.shape[0]):
+            ref_ids, ref_w = _grouped_brute(x[r], k, n_group, topk_group, renorm, softmax,
+                                            scaling, bias)
+            assert ids[r].tolist() == ref_ids
+            np.testing.assert_allclose(w[r], ref_w, rtol=5e-6)
+
+
+def test_route_grouped_reduces_to_plain_topk():
+    """One group kept out of one: grouped softmax top-k ranks like the plain
+    softmax top-k (softmax is monotone); biased with zero bias ranks like
+    the sigmoid top-k and returns its weights."""
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((20, 96)).astype(np.float32)
+    w1, ids1 = RR.grouped_topk_ref(x, 6, 1, 1, True, True, 1.0)
+    w0, ids0, _ = RR.topk_softmax_ref(x, 6, True)
+    assert np.array_equal(ids1, ids0)
+    np.testing.assert_allclose(w1, w0, rtol=3e-6)
+    w2, ids2 = RR.grouped_topk_ref(x, 6, 1, 1, False, False, 1.0, np.zeros(96, np.float32))
+    w3, ids3 = RR.topk_sigmoid_ref(x, 6)
+    assert np.array_equal(ids2, ids3)
+    np.testing.assert_allclose(w2, w3, rtol=1e-6)
