@@ -23,7 +23,7 @@ import torch
 
 from . import _abi
 from .enums import AITER_DTYPE, ActivationType, QuantType, dtypes, quant_remap
-from .quant import per_group_quant_hip
+from .quant import e8m0_unshuffle, per_group_quant_hip
 from .topk import fused_topk  # noqa: F401  (aiter.fused_moe.fused_topk)
 
 BLOCK_SIZE_M = 32
@@ -162,6 +162,33 @@ _FP4_DTYPES = (torch.uint8, dtypes.fp4x2)
 _E8M0_DTYPES = (torch.uint8, dtypes.fp8_e8m0)
 
 
+def e8m0_rowmajor(scale: torch.Tensor, E: int, N: int, KS: int) -> torch.Tensor:
+    """The kernels' MXFP4 scale layout, row-major e8m0 bytes [E, N, KS], from
+    either form a caller may hold:
+    * [E, N, KS] (per_1x32_f4_quant of [E, N, K]) is used as it is;
+    * a 2-D [ceil(E*N/256)*256, ceil(KS/8)*8] array is the reference's
+      e8m0_shuffle layout, the form its fused kernels take
+      (op_tests/test_moe_2stage.py:166-184, aiter/utility/fp4_utils.py:72-92).
+      It is un-shuffled once and the result cached on the tensor, keyed by
+      the tensor's version counter (an in-place update converts again)."""
+    if scale.dim() == 3:
+        if tuple(scale.shape) != (E, N, KS):
+            raise ValueError(f"e8m0 scales must be {(E, N, KS)}, got {tuple(scale.shape)}")
+        return scale
+    if scale.dim() != 2:
+        raise ValueError(f"e8m0 scales must be 3-D [E, N, K/32] or the 2-D e8m0_shuffle layout, "
+                         f"got {tuple(scale.shape)}")
+    shp = ((E * N + 255) // 256 * 256, (KS + 7) // 8 * 8)
+    if tuple(scale.shape) != shp:
+        raise ValueError(f"e8m0_shuffle scales must be {shp}, got {tuple(scale.shape)}")
+    cached = getattr(scale, "_aiter_amd_rowmajor", None)
+    if cached is not None and cached[0] == scale._version:
+        return cached[1]
+    rm = e8m0_unshuffle(scale.view(torch.uint8), E * N, KS).view(E, N, KS)
+    scale._aiter_amd_rowmajor = (scale._version, rm)
+    return rm
+
+
 def _check_supported(hidden_states, w1, w2, activation, quant_type, doweight_stage1, w1_scale,
                      w2_scale, a1_scale, hidden_pad, intermediate_pad, bias1, bias2, out_dtype):
     if quant_type not in (QuantType.per_1x128, QuantType.per_1x32):
@@ -215,11 +242,8 @@ def fused_moe_(hidden_states, w1, w2, topk_weight, topk_ids, expert_mask=None,
                      w2_scale, a1_scale, hidden_pad, intermediate_pad, bias1, bias2, out_dtype)
     a8w4 = quant_type == QuantType.per_1x32
     if a8w4:
-        exp1 = (E, 2 * inter_dim, model_dim // 32)
-        exp2 = (E, model_dim, inter_dim // 32)
-        if tuple(w1_scale.shape) != exp1 or tuple(w2_scale.shape) != exp2:
-            raise ValueError(f"e8m0 scales must be {exp1} / {exp2}, got "
-                             f"{tuple(w1_scale.shape)} / {tuple(w2_scale.shape)}")
+        w1_scale = e8m0_rowmajor(w1_scale, E, 2 * inter_dim, model_dim // 32)
+        w2_scale = e8m0_rowmajor(w2_scale, E, model_dim, inter_dim // 32)
     shuffled = bool(getattr(w1, "is_shuffled", False))
     if bool(getattr(w2, "is_shuffled", False)) != shuffled:
         raise ValueError("w1 and w2 must both be shuffled or both be plain")
@@ -300,7 +324,10 @@ def moe_stage1_fp8_blockscale(a1, a1_scale, w1, w1_scale, sorted_ids, sorted_exp
 def moe_stage1_a8w4(a1, a1_scale, w1, w1_scale, sorted_ids, sorted_expert_ids, num_valid_ids,
                     topk, block_m, shuffled, a1_scale_transposed=False):
     """A8W4 stage 1: fp8 1x128 activations x MXFP4 w1 (packed uint8 [E, 2I, H/2],
-    e8m0 uint8 [E, 2I, H/32]); same outputs as moe_stage1_fp8_blockscale."""
+    e8m0 [E, 2I, H/32] or its 2-D e8m0_shuffle layout); same outputs as
+    moe_stage1_fp8_blockscale."""
+    E, N1 = w1.shape[0], w1.shape[1]
+    w1_scale = e8m0_rowmajor(w1_scale, E, N1, a1.shape[1] // 32)
     return _stage1("aiter_amd_moe_stage1_a8w4", a1, a1_scale, w1.view(torch.uint8),
                    w1_scale.view(torch.uint8), sorted_ids, sorted_expert_ids, num_valid_ids,
                    topk, block_m, shuffled, a1_scale_transposed)
@@ -329,14 +356,16 @@ def moe_stage2_fp8_blockscale(a2, a2_scale, w2, w2_scale, sorted_ids, sorted_wei
 
 def moe_stage2_a8w4(a2, a2_scale, w2, w2_scale, sorted_ids, sorted_weights, sorted_expert_ids,
                     num_valid_ids, out_acc, block_m, shuffled):
-    """A8W4 stage 2: MXFP4 w2 (packed uint8 [E, H, I/2], e8m0 uint8 [E, H, I/32])."""
+    """A8W4 stage 2: MXFP4 w2 (packed uint8 [E, H, I/2], e8m0 [E, H, I/32] or its
+    2-D e8m0_shuffle layout)."""
+    w2_scale = e8m0_rowmajor(w2_scale, w2.shape[0], w2.shape[1], a2.shape[-1] // 32)
     _stage2("aiter_amd_moe_stage2_a8w4", a2, a2_scale, w2.view(torch.uint8),
             w2_scale.view(torch.uint8), sorted_ids, sorted_weights, sorted_expert_ids,
             num_valid_ids, out_acc, block_m, shuffled)
 
 
 __all__ = [
-    "BLOCK_SIZE_M", "fused_moe", "fused_moe_", "fused_moe_fake", "moe_sorting",
+    "BLOCK_SIZE_M", "fused_moe", "fused_moe_", "fused_moe_fake", "moe_sorting", "e8m0_rowmajor",
     "moe_stage1_fp8_blockscale", "moe_stage2_fp8_blockscale", "moe_stage1_a8w4",
     "moe_stage2_a8w4", "per_group_quant_hip",
     "get_inter_dim", "default_block_m", "sorted_capacity",

@@ -151,13 +151,12 @@ def per_1x32_f4_quant(x: torch.Tensor, scale=None, quant_dtype=dtypes.fp4x2,
                       shuffle: bool = False):
     """MXFP4 quant of [..., K] (aiter/ops/quant.py:75-105): per 32-element
     block, scale = e8m0(amax / 4), values e2m1(x / 2^(scale-127)).
-    Returns (packed [..., K/2] as fp4x2, scales [..., K/32] as e8m0)."""
+    Returns (packed [..., K/2] as fp4x2, scales [..., K/32] as e8m0); with
+    shuffle, the scales are the reference's 2-D e8m0_shuffle layout."""
     if scale is not None:
         raise ValueError("unsupported: static MXFP4 scale")
     if quant_dtype != dtypes.fp4x2:
         raise NotImplementedError(f"quant_dtype {quant_dtype} is not supported (fp4x2 only)")
-    if shuffle:
-        raise NotImplementedError("e8m0 scale shuffling is not used by these kernels")
     shape = x.shape
     K = shape[-1]
     if K % 32:
@@ -166,4 +165,32 @@ def per_1x32_f4_quant(x: torch.Tensor, scale=None, quant_dtype=dtypes.fp4x2,
     e = f32_to_e8m0(b.abs().amax(dim=-1) / 4.0)
     codes = f32_to_e2m1(b / e8m0_to_f32(e).unsqueeze(-1)).reshape(*shape)
     packed = (codes[..., 0::2] | (codes[..., 1::2] << 4)).contiguous()
+    if shuffle:   # the reference's 2-D scale, then e8m0_shuffle (aiter/ops/quant.py:101-105)
+        return packed.view(dtypes.fp4x2), e8m0_shuffle(e.reshape(-1, K // 32)).view(dtypes.fp8_e8m0)
     return packed.view(dtypes.fp4x2), e.reshape(*shape[:-1], K // 32).view(dtypes.fp8_e8m0)
+
+
+def e8m0_shuffle(scale: torch.Tensor) -> torch.Tensor:
+    """The reference's MXFP4 scale layout for its fused kernels
+    (aiter/utility/fp4_utils.py:72-92): a 2-D [m, n] byte array, padded to
+    [ceil(m/256)*256, ceil(n/8)*8], viewed as (m/32, 2, 16, n/8, 2, 4) and
+    permuted to (0, 3, 5, 2, 4, 1). fp32 scales pass through."""
+    if scale is None or scale.dtype == torch.float32:
+        return scale
+    if scale.dim() != 2:
+        raise ValueError("scale must be a 2D tensor")
+    m, n = scale.shape
+    sm, sn = (m + 255) // 256 * 256, (n + 7) // 8 * 8
+    pad = torch.empty((sm, sn), dtype=scale.dtype, device=scale.device)
+    pad[:m, :n] = scale
+    return (pad.view(sm // 32, 2, 16, sn // 8, 2, 4).permute(0, 3, 5, 2, 4, 1)
+            .contiguous().view(sm, sn))
+
+
+def e8m0_unshuffle(scale: torch.Tensor, rows: int, cols: int) -> torch.Tensor:
+    """Inverse of e8m0_shuffle: the row-major [rows, cols] scales."""
+    sm, sn = scale.shape
+    if sm % 256 or sn % 8 or rows > sm or cols > sn:
+        raise ValueError(f"[{sm}, {sn}] is not an e8m0_shuffle layout of [{rows}, {cols}]")
+    return (scale.view(sm // 32, sn // 8, 4, 16, 2, 2).permute(0, 5, 3, 1, 4, 2)
+            .contiguous().view(sm, sn)[:rows, :cols].contiguous())

@@ -417,3 +417,22 @@ def normalized_errors(ref: np.ndarray, got: np.ndarray):
 
 MAXTOL = 2e-2
 RMSTOL = 4e-3
+
+
+# ------------------------------------------------------- e8m0 shuffle ---
+def e8m0_shuffle_ref(scale: np.ndarray) -> np.ndarray:
+    """e8m0_shuffle (aiter/utility/fp4_utils.py:72-92) as an index formula:
+    the byte of row m = 32a + 16b + c, column n = 8d + 4e + f of the padded
+    [sm, sn] array lands at ((((a*(sn/8) + d)*4 + f)*16 + c)*2 + e)*2 + b."""
+    m, n = scale.shape
+    sm, sn = (m + 255) // 256 * 256, (n + 7) // 8 * 8
+    out = np.zeros(sm * sn, dtype=scale.dtype)
+    filled = np.zeros(sm * sn, dtype=bool)
+    for r in range(m):
+        a, b, c = r >> 5, (r >> 4) & 1, r & 15
+        for col in range(n):
+            d, e, f = col >> 3, (col >> 2) & 1, col & 3
+            off = ((((a * (sn // 8) + d) * 4 + f) * 16 + c) * 2 + e) * 2 + b
+            out[off] = scale[r, col]
+            filled[off] = True
+    return out.reshape(sm, sn), filled.reshape(sm, sn)

@@ -246,3 +246,31 @@ def test_routing_validation_errors(lib):
                   None, match="sigmoid")
     # zero tokens is a no-op
     _abi.call("aiter_amd_topk_softmax", None, 4, 0, 256, 8, None, 8, None, 8, None, 1, None)
+
+
+def test_e8m0_shuffle_layout_and_loader():
+    """e8m0_shuffle is the reference's index permutation (pinned by the
+    oracle's index formula); fused_moe's loader turns it back into the
+    kernels' row-major [E, N, K/32] and caches the result on the tensor."""
+    from aiter_amd.fused_moe import e8m0_rowmajor
+    rng = np.random.default_rng(5)
+    for m, n in [(300, 13), (512, 64), (1024, 128)]:
+        x = rng.integers(0, 255, (m, n)).astype(np.uint8)
+        ref, filled = R.e8m0_shuffle_ref(x)
+        got = A.e8m0_shuffle(torch.from_numpy(x)).numpy()
+        assert got.shape == ref.shape and np.array_equal(got[filled], ref[filled])
+        assert np.array_equal(A.e8m0_unshuffle(torch.from_numpy(got), m, n).numpy(), x)
+    # per_1x32_f4_quant(shuffle=True) == e8m0_shuffle of the 2-D scales
+    w = torch.randn(4, 64, 256) * 0.05
+    p, s3 = A.per_1x32_f4_quant(w)
+    p2, s2 = A.per_1x32_f4_quant(w, shuffle=True)
+    assert torch.equal(p.view(torch.uint8), p2.view(torch.uint8))
+    assert torch.equal(s2.view(torch.uint8), A.e8m0_shuffle(s3.view(torch.uint8).reshape(-1, 8)))
+    rm = e8m0_rowmajor(s2, 4, 64, 8)
+    assert torch.equal(rm.view(torch.uint8), s3.view(torch.uint8))
+    assert e8m0_rowmajor(s2, 4, 64, 8) is rm               # cached
+    s2.view(torch.uint8)[0, 0] ^= 1                        # an in-place update converts again
+    assert e8m0_rowmajor(s2, 4, 64, 8) is not rm
+    assert e8m0_rowmajor(s3, 4, 64, 8) is s3                # 3-D scales pass through
+    with pytest.raises(ValueError, match="e8m0_shuffle scales must be"):
+        e8m0_rowmajor(torch.zeros(100, 8, dtype=torch.uint8), 4, 64, 8)

@@ -191,3 +191,21 @@ def test_a8w4_mimo_stagewise(cuda_device, T, block_ms):
     """Full MiMo dims for the A8W4 mid-size and prefill configs, checked per
     stage (64 is the direct-to-LDS kernels, 128 the prefill stage 2)."""
     _fullshape.stagewise_check(W.mimo_a8w4(T), cuda_device, block_ms)
+
+
+@pytest.mark.parametrize("bm", [16, 64, 128])
+def test_a8w4_reference_scale_layout(cuda_device, bm):
+    """The reference hands its fused kernels e8m0_shuffle'd 2-D scales
+    (op_tests/test_moe_2stage.py:166-184): the same layer as row-major
+    [E, N, K/32] scales, and the same stage-wise results."""
+    cfg = _a8w4(W.CONFIG_A)
+    dev, ref = _make_layer(cfg, cuda_device, True)
+    out_rm = _run(dev, block_size_M=bm)
+    s1 = A.e8m0_shuffle(dev["s1"].view(torch.uint8).reshape(-1, dev["s1"].shape[-1]))
+    s2 = A.e8m0_shuffle(dev["s2"].view(torch.uint8).reshape(-1, dev["s2"].shape[-1]))
+    sh = dict(dev, s1=s1.view(A.dtypes.fp8_e8m0), s2=s2.view(A.dtypes.fp8_e8m0))
+    out_sh = _run(sh, block_size_M=bm)
+    # the same kernel inputs: equal up to fp32 atomic order (one bf16 rounding)
+    mx, _ = R.normalized_errors(_np(out_rm.float()), _np(out_sh.float()))
+    assert mx <= 1e-2, mx
+    _check(ref["out"], _np(out_sh.float()), f"A8W4 e8m0_shuffle scales bm={bm}")
