@@ -22,6 +22,7 @@ from .fused_moe import (
     moe_stage1_fp8_blockscale,
     moe_stage2_a8w4,
     moe_stage2_fp8_blockscale,
+    select_block_m,
     sorted_capacity,
 )
 from .quant import (
@@ -48,7 +49,7 @@ __all__ = [
     "ActivationType", "QuantType", "dtypes", "quant_remap", "BLOCK_SIZE_M", "default_block_m",
     "fused_moe", "fused_moe_", "fused_moe_fake", "get_inter_dim", "moe_sorting",
     "moe_stage1_fp8_blockscale", "moe_stage2_fp8_blockscale", "moe_stage1_a8w4",
-    "moe_stage2_a8w4", "sorted_capacity", "dynamic_per_token_scaled_quant", "per_group_quant_hip",
+    "moe_stage2_a8w4", "select_block_m", "sorted_capacity", "dynamic_per_token_scaled_quant", "per_group_quant_hip",
     "quant_weight_per_128x128", "per_1x32_f4_quant", "f32_to_e8m0", "e8m0_to_f32", "e8m0_shuffle",
     "e8m0_unshuffle",
     "shuffle_weight", "unshuffle_weight", "topk_softmax", "topk_sigmoid", "grouped_topk",

@@ -25,12 +25,18 @@ from . import _abi
 from .enums import AITER_DTYPE, ActivationType, QuantType, dtypes, quant_remap
 from .quant import e8m0_unshuffle, per_group_quant_hip
 from .topk import fused_topk  # noqa: F401  (aiter.fused_moe.fused_topk)
+from .tune import tuned_block_m
 
 BLOCK_SIZE_M = 32
 
 
 def _stream(dev: torch.device) -> int:
     return torch.cuda.current_stream(dev).cuda_stream
+
+
+@functools.lru_cache(maxsize=16)
+def _cu_num(dev: torch.device) -> int:
+    return torch.cuda.get_device_properties(dev).multi_processor_count
 
 
 def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
@@ -162,6 +168,16 @@ _FP4_DTYPES = (torch.uint8, dtypes.fp4x2)
 _E8M0_DTYPES = (torch.uint8, dtypes.fp8_e8m0)
 
 
+def select_block_m(tokens: int, topk: int, num_experts: int, model_dim: int, inter_dim: int,
+                   a8w4: bool, device: torch.device) -> int:
+    """fused_moe's block_m when the caller gives none: the tuned table
+    (aiter_amd/tune.py, the get_2stage_cfgs lookup of aiter/fused_moe.py:719-1100),
+    else the heuristic default_block_m."""
+    tuned = tuned_block_m(_cu_num(device), tokens, model_dim, inter_dim, num_experts, topk,
+                          "per_1x32" if a8w4 else "per_1x128", "fp4x2" if a8w4 else "fp8")
+    return tuned or default_block_m(tokens, topk, num_experts, model_dim, inter_dim)
+
+
 def e8m0_rowmajor(scale: torch.Tensor, E: int, N: int, KS: int) -> torch.Tensor:
     """The kernels' MXFP4 scale layout, row-major e8m0 bytes [E, N, KS], from
     either form a caller may hold:
@@ -248,8 +264,10 @@ def fused_moe_(hidden_states, w1, w2, topk_weight, topk_ids, expert_mask=None,
     if bool(getattr(w2, "is_shuffled", False)) != shuffled:
         raise ValueError("w1 and w2 must both be shuffled or both be plain")
     global_E = expert_mask.numel() if expert_mask is not None else E
-    block_m = int(block_size_M) if block_size_M not in (None, -1) else default_block_m(
-        M, topk, E, model_dim, inter_dim)
+    if block_size_M not in (None, -1):
+        block_m = int(block_size_M)
+    else:
+        block_m = select_block_m(M, topk, E, model_dim, inter_dim, a8w4, topk_ids.device)
     device = topk_ids.device
     topk_ids = topk_ids.to(torch.int32).contiguous()
     topk_weight = topk_weight.to(torch.float32).contiguous()
@@ -366,6 +384,7 @@ def moe_stage2_a8w4(a2, a2_scale, w2, w2_scale, sorted_ids, sorted_weights, sort
 
 __all__ = [
     "BLOCK_SIZE_M", "fused_moe", "fused_moe_", "fused_moe_fake", "moe_sorting", "e8m0_rowmajor",
+    "select_block_m",
     "moe_stage1_fp8_blockscale", "moe_stage2_fp8_blockscale", "moe_stage1_a8w4",
     "moe_stage2_a8w4", "per_group_quant_hip",
     "get_inter_dim", "default_block_m", "sorted_capacity",

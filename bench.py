@@ -123,9 +123,9 @@ class Layer:
         import aiter_amd as A
 
         cfg = self.cfg
-        return self.block_m or A.default_block_m(cfg.tokens, cfg.topk,
-                                                 cfg.local_experts or cfg.experts,
-                                                 cfg.model_dim, cfg.inter_dim)
+        return self.block_m or A.select_block_m(
+            cfg.tokens, cfg.topk, cfg.local_experts or cfg.experts, cfg.model_dim,
+            cfg.inter_dim, self.a8w4, self.dev)
 
 
 def time_steps(fn, steps, warmup):

@@ -274,3 +274,18 @@ def test_e8m0_shuffle_layout_and_loader():
     assert e8m0_rowmajor(s3, 4, 64, 8) is s3                # 3-D scales pass through
     with pytest.raises(ValueError, match="e8m0_shuffle scales must be"):
         e8m0_rowmajor(torch.zeros(100, 8, dtype=torch.uint8), 4, 64, 8)
+
+
+def test_tuned_dispatch_table():
+    """The committed block_m table (aiter_amd/tune.py) answers for the MiMo
+    shapes it was swept on and buckets token counts like get_padded_M."""
+    from aiter_amd import tune as T
+    assert [T.padded_tokens(m) for m in (1, 3, 32, 33, 40000)] == [1, 4, 32, 64, 32768]
+    bm = {t: T.tuned_block_m(256, t, 4096, 2048, 256, 8, "per_1x128", "fp8")
+          for t in (1, 32, 8192)}
+    assert all(b in (16, 32, 64, 128) for b in bm.values()), bm
+    assert T.tuned_block_m(256, 20, 4096, 2048, 256, 8, "per_1x128", "fp8") == \
+        T.tuned_block_m(256, 32, 4096, 2048, 256, 8, "per_1x128", "fp8")
+    assert T.tuned_block_m(256, 32, 4096, 2048, 256, 8, "per_1x32", "fp4x2") in (16, 32, 64, 128)
+    assert T.tuned_block_m(304, 32, 4096, 2048, 256, 8, "per_1x128", "fp8") is None
+    assert T.tuned_block_m(256, 32, 1024, 512, 8, 2, "per_1x128", "fp8") is None
