@@ -66,6 +66,7 @@ enum DtypeCode : int {
 
 // ------------------------------------------------------- device helpers ---
 typedef int v8i __attribute__((ext_vector_type(8)));
+typedef int v2i __attribute__((ext_vector_type(2)));
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 

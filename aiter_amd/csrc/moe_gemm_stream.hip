@@ -65,7 +65,6 @@ template <int NRT, bool W4>
 struct Step {
     v4i a[NRT][2];
     v4i b[kNCT][W4 ? 1 : 2];
-    int bs[kNCT];              // e8m0 byte per column tile (A8W4)
 };
 
 template <int BM, int STAGE, bool SHUFFLED, bool W4, int D>
@@ -148,7 +147,8 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
         else
             bsrc[ct] = SHUFFLED ? we + (int64_t)row0 * K + lq * 512 + lr * 16
                                 : we + (int64_t)(row0 + lr) * K + lq * 32;
-        bssrc[ct] = W4 ? g.w_scale8 + ((int64_t)e * g.N + row0 + lr) * (K / 32) + lq : nullptr;
+        // A8W4: the e8m0 bytes of the lane's weight row (all four lane quarters)
+        bssrc[ct] = W4 ? g.w_scale8 + ((int64_t)e * g.N + row0 + lr) * (K / 32) : nullptr;
     }
     constexpr int BSTEP = W4 ? (SHUFFLED ? 1024 : 64) : (SHUFFLED ? 2048 : 128);
     constexpr int BHI = SHUFFLED ? 256 : 16;       // fp8: offset of the fragment's second half
@@ -170,7 +170,6 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
             if (!W4)
                 s.b[ct][W4 ? 0 : 1] =
                     __builtin_nontemporal_load(reinterpret_cast<const v4i*>(p + BHI));
-            if (W4) s.bs[ct] = bssrc[ct][kb * 4];
         }
 #pragma unroll
         for (int rt = 0; rt < NRT; ++rt) {
@@ -186,7 +185,26 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
 #pragma unroll
         for (int ct = 0; ct < kNCT; ++ct) acc[rt][ct] = v4f{0.f, 0.f, 0.f, 0.f};
 
-    auto compute = [&](const S& s, int kb) {
+    // A8W4 scales of a group of D steps in one load: k-groups 4*kb .. 4*(kb+D)-1
+    // of the row (the row and kb*4 are multiples of 4*D bytes, as D divides
+    // K/128); step d's byte for this lane is byte lq of dword d
+    auto load_sg = [&](int (&dst)[kNCT][D], int kb) {
+#pragma unroll
+        for (int ct = 0; ct < kNCT; ++ct) {
+            const uint8_t* p = bssrc[ct] + kb * 4;
+            if constexpr (D == 4) {
+                const v4i v = *reinterpret_cast<const v4i*>(p);
+                dst[ct][0] = v[0], dst[ct][1] = v[1], dst[ct][2] = v[2], dst[ct][3] = v[3];
+            } else if constexpr (D == 2) {
+                const v2i v = *reinterpret_cast<const v2i*>(p);
+                dst[ct][0] = v[0], dst[ct][1] = v[1];
+            } else {
+                dst[ct][0] = *reinterpret_cast<const int*>(p);
+            }
+        }
+    };
+
+    auto compute = [&](const S& s, int kb, const int (&sg)[kNCT][D], int d) {
         // stage 1: tiles 0,1 gate (scale block 0), 2,3 up (block 1); stage 2:
         // the wave's 64 columns lie in 128-column block wv/2
         const float sw0 = W4 ? 1.0f : s_sw[STAGE == 1 ? 0 : (wv >> 1)][kb];
@@ -202,7 +220,7 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
                 if (W4) {
                     const v8i bf = v8i{s.b[ct][0][0], s.b[ct][0][1], s.b[ct][0][2],
                                        s.b[ct][0][3], 0, 0, 0, 0};
-                    blk = mfma16x16x128_fp8_fp4(af, bf, s.bs[ct]);
+                    blk = mfma16x16x128_fp8_fp4(af, bf, sg[ct][d] >> (8 * lq));
                 } else {
                     const v8i bf = v8i{s.b[ct][0][0], s.b[ct][0][1], s.b[ct][0][2],
                                        s.b[ct][0][3], s.b[ct][W4 ? 0 : 1][0],
@@ -220,17 +238,26 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
 
     // ---- K loop: D steps in flight ----
     S buf[D];
+    int sgc[kNCT][D], sgn[kNCT][D];            // A8W4 scales: current / next group
+    if (W4) load_sg(sgc, 0);
 #pragma unroll
     for (int d = 0; d < D; ++d) load(buf[d], d);
     for (int kb0 = 0; kb0 < KB - D; kb0 += D) {
+        if (W4) load_sg(sgn, kb0 + D);
 #pragma unroll
         for (int d = 0; d < D; ++d) {
-            compute(buf[d], kb0 + d);
+            compute(buf[d], kb0 + d, sgc, d);
             load(buf[d], kb0 + d + D);
+        }
+        if (W4) {
+#pragma unroll
+            for (int ct = 0; ct < kNCT; ++ct)
+#pragma unroll
+                for (int d = 0; d < D; ++d) sgc[ct][d] = sgn[ct][d];
         }
     }
 #pragma unroll
-    for (int d = 0; d < D; ++d) compute(buf[d], KB - D + d);
+    for (int d = 0; d < D; ++d) compute(buf[d], KB - D + d, sgc, d);
 
     if (STAGE == 2) {
 #pragma unroll
