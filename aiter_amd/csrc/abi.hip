@@ -56,6 +56,11 @@ void launch_moe_stage2_stream(const uint8_t*, const float*, const uint8_t*, cons
                               const int32_t*, float*, int64_t, int64_t, int64_t, int64_t,
                               int64_t, int64_t, int64_t, int, hipStream_t);
 
+// quant.hip: per-pair bf16 rows -> output
+void launch_slot_sum(const uint16_t* part, const int32_t* topk_ids, const int32_t* mask,
+                     int64_t num_experts, const int32_t* num_valid, void* out, int out_dtype,
+                     int64_t rows, int64_t topk, int64_t cols, hipStream_t stream);
+
 // moe_route.hip (router top-k)
 bool route_supported(int64_t E, int64_t k);
 void launch_moe_route(const void* gating, int dtype, int64_t M, int64_t E, int64_t k, int mode,
@@ -71,8 +76,8 @@ void launch_moe_stage1_prefill(const uint8_t*, const float*, int64_t, int64_t, c
                                int64_t, int64_t, int64_t, int64_t, int, hipStream_t);
 void launch_moe_stage2_prefill(const uint8_t*, const float*, const uint8_t*, const float*,
                                const uint8_t*, const int32_t*, const float*, const int32_t*,
-                               const int32_t*, float*, int64_t, int64_t, int64_t, int64_t,
-                               int64_t, int64_t, int64_t, int, hipStream_t);
+                               const int32_t*, float*, uint16_t*, int64_t, int64_t, int64_t,
+                               int64_t, int64_t, int64_t, int64_t, int, hipStream_t);
 
 // Weight scales of one layer: fp32 128x128 blocks (fp8 weights) or e8m0
 // bytes per 1x32 K block (MXFP4 weights); exactly one is set.
@@ -108,17 +113,27 @@ static void stage1_dispatch(const uint8_t* a, const float* sa, int64_t sa_row, i
                                 a2s, a_rows, K, I, E, topk, bm, mblocks, sh, s);
 }
 
+// Stage 2 runs on the prefill kernel for this shape (the only stage-2
+// kernel that can also write per-pair bf16 rows instead of accumulating).
+static bool stage2_on_prefill(int64_t bm, int64_t I, int64_t H, WScale w2s) {
+    return !(stream_supported(bm, I) && H % 256 == 0) && prefill_supported(bm, I) &&
+           H % 256 == 0 && (!w2s.e8m0 || bm == 128);
+}
+
+// acc: fp32 [tokens, H] accumulated atomically; part (prefill kernel only):
+// bf16 [pairs, H] rows written once each, acc unused.
 static void stage2_dispatch(const uint8_t* a2, const float* a2s, const uint8_t* w2,
                             WScale w2s, const int32_t* sid, const float* sw,
                             const int32_t* seid, const int32_t* nv, float* acc, int64_t a_rows,
                             int64_t I, int64_t H, int64_t E, int64_t topk, int64_t bm,
-                            int64_t mblocks, int sh, hipStream_t s) {
+                            int64_t mblocks, int sh, hipStream_t s, uint16_t* part = nullptr) {
+    AMD_CHECK(!part || stage2_on_prefill(bm, I, H, w2s), "per-pair rows need the prefill kernel");
     if (stream_supported(bm, I) && H % 256 == 0)
         launch_moe_stage2_stream(a2, a2s, w2, w2s.f32, w2s.e8m0, sid, sw, seid, nv, acc, a_rows,
                                  I, H, E, topk, bm, mblocks, sh, s);
     else if (prefill_supported(bm, I) && H % 256 == 0 && (!w2s.e8m0 || bm == 128))
-        launch_moe_stage2_prefill(a2, a2s, w2, w2s.f32, w2s.e8m0, sid, sw, seid, nv, acc, a_rows,
-                                  I, H, E, topk, bm, mblocks, sh, s);
+        launch_moe_stage2_prefill(a2, a2s, w2, w2s.f32, w2s.e8m0, sid, sw, seid, nv, acc, part,
+                                  a_rows, I, H, E, topk, bm, mblocks, sh, s);
     else if (v2_supported(bm, I) && H % 256 == 0)
         launch_moe_stage2_fp8bs_v2(a2, a2s, w2, w2s.f32, w2s.e8m0, sid, sw, seid, nv, acc, a_rows,
                                    I, H, E, topk, bm, mblocks, sh, s);
@@ -197,7 +212,9 @@ FusedLayout fused_layout(int64_t T, int64_t H, int64_t I, int64_t E_sort, int64_
     L.off_a1_scale = o;    o = align256(o + T * (H / 128) * 4);
     L.off_a2 = o;          o = align256(o + T * k * I);
     L.off_a2_scale = o;    o = align256(o + T * k * (I / 128) * 4);
-    L.off_acc = o;         o = align256(o + T * H * 4);
+    // fp32 accumulator [T, H], or per-pair bf16 rows [T*k, H] when stage 2
+    // runs on the prefill kernel: room for either
+    L.off_acc = o;         o = align256(o + std::max(T * H * 4, T * k * H * 2));
     L.total = o;
     return L;
 }
@@ -308,10 +325,14 @@ void fused_entry(const void* hidden_states, int hidden_dtype, const void* w1, WS
     uint8_t* a2 = ws + L.off_a2;
     float* a2_scale = reinterpret_cast<float*>(ws + L.off_a2_scale);
     float* acc = reinterpret_cast<float*>(ws + L.off_acc);
+    // stage 2 on the prefill kernel writes each pair's weighted row once (bf16)
+    // and one pass sums a token's slots: no fp32 atomics, no accumulator to clear
+    uint16_t* part = stage2_on_prefill(block_m, inter_dim, model_dim, w2s)
+                         ? reinterpret_cast<uint16_t*>(ws + L.off_acc) : nullptr;
     hipStream_t s = (hipStream_t)stream;
     launch_moe_sort(topk_ids, topk_weights, expert_mask, num_local_tokens, sorted_ids, sorted_w,
-                    sorted_eids, num_valid, acc, model_dim * 4, tokens, topk, E_sort, block_m,
-                    ws + L.off_sort_ws, L.sort_ws_bytes, s);
+                    sorted_eids, num_valid, part ? nullptr : acc, model_dim * 4, tokens, topk,
+                    E_sort, block_m, ws + L.off_sort_ws, L.sort_ws_bytes, s);
     launch_per_group_quant_fp8(hidden_states, hidden_dtype, a1, a1_scale, tokens, model_dim, 0,
                                num_local_tokens, 1, s);
     const int sh = (int)(w_shuffled != 0);
@@ -319,9 +340,13 @@ void fused_entry(const void* hidden_states, int hidden_dtype, const void* w1, WS
                     sorted_eids, num_valid, a2, a2_scale, tokens, model_dim, inter_dim,
                     num_experts, topk, block_m, L.blocks, sh, s);
     stage2_dispatch(a2, a2_scale, (const uint8_t*)w2, w2s, sorted_ids, sorted_w, sorted_eids,
-                    num_valid, acc, tokens * topk, inter_dim, model_dim, num_experts, topk,
-                    block_m, L.blocks, sh, s);
-    launch_acc_to_out(acc, out, out_dtype, num_valid, tokens, model_dim, s);
+                    num_valid, part ? nullptr : acc, tokens * topk, inter_dim, model_dim,
+                    num_experts, topk, block_m, L.blocks, sh, s, part);
+    if (part)
+        launch_slot_sum(part, topk_ids, expert_mask, E_sort, num_valid, out, out_dtype, tokens,
+                        topk, model_dim, s);
+    else
+        launch_acc_to_out(acc, out, out_dtype, num_valid, tokens, model_dim, s);
 }
 
 }  // namespace

@@ -54,6 +54,7 @@ struct Args {
     uint8_t* a2;
     float* a2_scale;
     float* acc;
+    uint16_t* part;            // stage 2: bf16 rows [pairs, N] instead of acc (or NULL)
     int K;
     int N;                     // weight rows per expert
     int inter;
@@ -462,6 +463,32 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
         kloop(IntC<NRT>{});
 
     if (STAGE == 2) {
+        if (g.part) {
+            // the pair's weighted row, rounded once to bf16, staged through LDS
+            // and stored as whole 16-byte pieces at part[pair, n0 ..]
+            static_assert(STAGE != 2 || BM * NW * 2 <= 2 * A_BYTES, "bf16 staging fits the A stages");
+            uint16_t* s_p = reinterpret_cast<uint16_t*>(&s_a[0][0]);   // [BM][NW]
+#pragma unroll
+            for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int row = row_base + rt * 16 + 4 * lq + v;
+                    const float wgt = s_w[row];
+#pragma unroll
+                    for (int ct = 0; ct < NCT; ++ct)
+                        s_p[row * NW + wn * NCT * 16 + ct * 16 + lr] =
+                            f32_to_bf16_bits(acc[rt][ct][v] * wgt);
+                }
+            __syncthreads();
+            for (int q = tid; q < BM * (NW / 8); q += kThreads) {
+                const int row = q / (NW / 8), piece = q % (NW / 8);
+                const int64_t pair = s_arow[row];
+                if (pair < 0) continue;
+                *reinterpret_cast<v4i*>(g.part + pair * g.N + n0 + piece * 8) =
+                    *reinterpret_cast<const v4i*>(s_p + row * NW + piece * 8);
+            }
+            return;
+        }
 #pragma unroll
         for (int rt = 0; rt < NRT; ++rt)
 #pragma unroll
@@ -658,9 +685,9 @@ void launch_moe_stage2_prefill(const uint8_t* a2, const float* a2_scale, const u
                                const float* w2_scale, const uint8_t* w2_scale_e8m0,
                                const int32_t* sorted_ids, const float* sorted_w,
                                const int32_t* sorted_eids, const int32_t* num_valid, float* acc,
-                               int64_t a_rows, int64_t inter, int64_t hidden, int64_t E,
-                               int64_t topk, int64_t block_m, int64_t max_m_blocks, int shuffled,
-                               hipStream_t stream) {
+                               uint16_t* part, int64_t a_rows, int64_t inter, int64_t hidden,
+                               int64_t E, int64_t topk, int64_t block_m, int64_t max_m_blocks,
+                               int shuffled, hipStream_t stream) {
     pf::Args g{};
     g.a = a2;
     g.a_scale = a2_scale;
@@ -674,6 +701,7 @@ void launch_moe_stage2_prefill(const uint8_t* a2, const float* a2_scale, const u
     g.sorted_eids = sorted_eids;
     g.num_valid = num_valid;
     g.acc = acc;
+    g.part = part;
     g.K = (int)inter;
     g.N = (int)hidden;
     g.inter = (int)inter;

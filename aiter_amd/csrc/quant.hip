@@ -139,4 +139,63 @@ void launch_acc_to_out(const float* acc, void* out, int out_dtype, const int32_t
     AMD_HIP_CHECK(hipGetLastError());
 }
 
+// ------------------------------------ per-pair bf16 rows -> output ---
+// out[t, :] = round(sum over the token's routed slots j of part[t*topk + j, :])
+// for t < tokens (= *num_valid[1]), summed in fp32 in slot order. A slot is
+// routed when sorting kept its pair: expert id in [0, num_experts) and, with
+// an expert mask, mask[id] != 0. 8 elements per thread.
+template <bool kBf16>
+__global__ __launch_bounds__(256) void slot_sum_kernel(const uint16_t* __restrict__ part,
+                                                       const int32_t* __restrict__ topk_ids,
+                                                       const int32_t* __restrict__ mask,
+                                                       int num_experts,
+                                                       const int32_t* __restrict__ num_valid,
+                                                       uint16_t* __restrict__ out, int64_t rows,
+                                                       int topk, int cols) {
+    int64_t tokens = (int64_t)num_valid[1];
+    tokens = tokens < rows ? tokens : rows;
+    const int c8 = cols / 8;
+    const int64_t n8 = tokens * c8;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n8;
+         i += (int64_t)gridDim.x * 256) {
+        const int64_t t = i / c8;
+        const int64_t col = (i % c8) * 8;
+        float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < topk; ++j) {
+            const int id = topk_ids[t * topk + j];
+            if (id < 0 || id >= num_experts || (mask && mask[id] == 0)) continue;
+            const v4i v = *reinterpret_cast<const v4i*>(part + (t * topk + j) * cols + col);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                a[2 * e] += bf16_bits_to_f32((uint16_t)((uint32_t)v[e] & 0xFFFFu));
+                a[2 * e + 1] += bf16_bits_to_f32((uint16_t)((uint32_t)v[e] >> 16));
+            }
+        }
+        uint32_t w[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            w[e] = kBf16 ? f32_to_bf16_bits(a[2 * e]) | ((uint32_t)f32_to_bf16_bits(a[2 * e + 1]) << 16)
+                         : f32_to_fp16_bits(a[2 * e]) | ((uint32_t)f32_to_fp16_bits(a[2 * e + 1]) << 16);
+        v4i o = {(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+        *reinterpret_cast<v4i*>(out + t * cols + col) = o;
+    }
+}
+
+void launch_slot_sum(const uint16_t* part, const int32_t* topk_ids, const int32_t* mask,
+                     int64_t num_experts, const int32_t* num_valid, void* out, int out_dtype,
+                     int64_t rows, int64_t topk, int64_t cols, hipStream_t stream) {
+    const int64_t n8 = rows * cols / 8;
+    if (n8 == 0) return;
+    const int blocks = (int)std::min<int64_t>(ceil_div(n8, 256), 16384);
+    if (out_dtype == DT_BF16)
+        hipLaunchKernelGGL(slot_sum_kernel<true>, dim3(blocks), dim3(256), 0, stream, part,
+                           topk_ids, mask, (int)num_experts, num_valid, (uint16_t*)out, rows,
+                           (int)topk, (int)cols);
+    else
+        hipLaunchKernelGGL(slot_sum_kernel<false>, dim3(blocks), dim3(256), 0, stream, part,
+                           topk_ids, mask, (int)num_experts, num_valid, (uint16_t*)out, rows,
+                           (int)topk, (int)cols);
+    AMD_HIP_CHECK(hipGetLastError());
+}
+
 }  // namespace aiter_amd

@@ -191,24 +191,28 @@ def test_fused_moe_fp8_input_path(cuda_device):
     _check(ref["out"], _np(out.float()), "fp8 input")
 
 
-def test_fused_moe_ep_share_small(cuda_device):
+@pytest.mark.parametrize("bm", [None, 64, 128])
+def test_fused_moe_ep_share_small(cuda_device, bm):
     """expert_mask: 4 local experts of 16 (sigmoid routing); tokens with no
-    local expert give zero rows (op_tests/test_moe_ep.py:117-126)."""
+    local expert give zero rows (op_tests/test_moe_ep.py:117-126). bm 64/128
+    run stage 2 on the prefill kernel (per-pair rows summed over the local
+    slots only)."""
     cfg = W.MoEConfig("ep_small", 96, 512, 512, 16, 4, routing="sigmoid", local_experts=4,
                       seed=3)
     dev, ref = _make_layer(cfg, cuda_device, True)
-    out = _run(dev)
+    out = _run(dev, block_size_M=bm)
     _check(ref["out"], _np(out.float()), "EP small")
     none_local = (ref["ids_local"] < 0).all(axis=1)
     assert none_local.any()
     assert torch.count_nonzero(out[torch.from_numpy(none_local).to(cuda_device)]).item() == 0
 
 
-def test_fused_moe_num_local_tokens(cuda_device):
+@pytest.mark.parametrize("bm", [None, 64, 128])
+def test_fused_moe_num_local_tokens(cuda_device, bm):
     cfg = W.MoEConfig("local_tok", 80, 512, 512, 8, 2, seed=4)
     dev, _ = _make_layer(cfg, cuda_device, True)
     loc = torch.tensor([50], dtype=torch.int32, device=cuda_device)
-    out = _run(dev, num_local_tokens=loc)
+    out = _run(dev, num_local_tokens=loc, block_size_M=bm)
     wts = W.make_weights(cfg, device="cpu", shuffle=False)
     ref = R.fused_moe_ref(dev["x"].float().cpu().numpy(), wts["w1"].view(torch.uint8).numpy(),
                           wts["w1_scale"].numpy(), wts["w2"].view(torch.uint8).numpy(),
@@ -217,11 +221,12 @@ def test_fused_moe_num_local_tokens(cuda_device):
     _check(ref["out"][:50], _np(out.float())[:50], "num_local_tokens")
 
 
-def test_fused_moe_fp16_io(cuda_device):
+@pytest.mark.parametrize("bm", [None, 128])
+def test_fused_moe_fp16_io(cuda_device, bm):
     cfg = W.MoEConfig("fp16", 40, 512, 512, 8, 2, seed=6)
     dev, ref = _make_layer(cfg, cuda_device, True)
     dev["x"] = dev["x"].to(torch.float16)
-    out = _run(dev)
+    out = _run(dev, block_size_M=bm)
     assert out.dtype == torch.float16
     _check(ref["out"], _np(out.float()), "fp16")
 
