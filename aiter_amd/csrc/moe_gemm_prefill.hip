@@ -28,7 +28,12 @@
 // per row); stage 2: 128 (or 64) rows x 128 output columns.  A tile whose
 // rows are all padding exits at once.  Tile order is XCD-aware: workgroup L
 // runs on XCD L % 8, and each XCD owns n_tiles/8 column tiles of every
-// M-block so an expert's weight slice stays in its L2.
+// M-block so an expert's weight slice stays in its L2.  A workgroup may walk
+// ntw consecutive column tiles of its M-block in one pipelined K loop (setup
+// paid once; the next tile's first loads are in flight during a tile's
+// epilogue).
+#include <cstdlib>
+
 #include "common.h"
 
 namespace aiter_amd {
@@ -64,6 +69,7 @@ struct Args {
     int n_tiles;
     int m_tiles;               // sorted M-blocks x workgroups per M-block
     int block_m;               // rows per sorted M-block (BM or 2 BM)
+    int ntw;                   // column tiles per workgroup, walked in one pipelined K loop
 };
 
 __device__ __forceinline__ int frag_swap(int r) { return ((r >> 2) ^ (r >> 3)) & 1; }
@@ -75,10 +81,13 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, int64_t
                                              0x00020000);
 }
 
-// a_scale[row, kb] * w_scale[block h, kb] for row r, K blocks q, q + RP, ...
-// (RP = threads per row) into s_sc[kb][h][row]; NJ covers the K range. The
-// loads (clamped addresses, no branches) and the products are separate calls
-// so the caller can issue other loads in between.
+// a_scale[row, kb] * w_scale[block h, kb] for row r, steps c = q, q + RP, ...
+// (RP = threads per row) into s_sc[c][h][row]. Step c is K block c % KB of
+// the workgroup's column tile c / KB, whose weight-scale blocks follow the
+// first tile's at a stride of KB, so w0 / w1 are indexed by c itself; NJ
+// covers the KBT steps of all tiles. The loads (clamped addresses, no
+// branches) and the products are separate calls so the caller can issue
+// other loads in between.
 template <int N>
 struct IntC {
     static constexpr int value = N;
@@ -93,31 +102,36 @@ struct ScaleRegs {
 
 template <int BM, int NH, bool W4, int NJ>
 __device__ __forceinline__ void scale_load(ScaleRegs<W4, NJ>& sr, const float* sa, int64_t sa_kb,
-                                           const float* w0, const float* w1, int KB, int q) {
+                                           const float* w0, const float* w1, int KB, int KBT,
+                                           int q) {
     constexpr int RP = kThreads / BM;
+    // c % KB by a float reciprocal: c < 64 and KB <= 64, so the quotient of
+    // (c + 1/2) / KB is at least 1/128 from an integer and rounds exactly
+    const float rkb = 1.0f / (float)KB;
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
-        const int kb = q + j * RP;
-        const int kc = kb < KB ? kb : KB - 1;
+        const int c = q + j * RP;
+        const int cc = c < KBT ? c : KBT - 1;
+        const int kc = cc - KB * (int)(((float)cc + 0.5f) * rkb);
         sr.av[j] = sa[(int64_t)kc * sa_kb];
         if (!W4) {
-            sr.b0[j] = w0[kc];
-            if (NH == 2) sr.b1[j] = w1[kc];
+            sr.b0[j] = w0[cc];
+            if (NH == 2) sr.b1[j] = w1[cc];
         }
     }
 }
 
 template <int BM, int NH, bool W4, int NJ>
-__device__ __forceinline__ void scale_store(const ScaleRegs<W4, NJ>& sr, float* s_sc, int KB,
+__device__ __forceinline__ void scale_store(const ScaleRegs<W4, NJ>& sr, float* s_sc, int KBT,
                                             int r, int q, bool valid) {
     constexpr int RP = kThreads / BM;
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
-        const int kb = q + j * RP;
-        if (kb < KB) {
+        const int c = q + j * RP;
+        if (c < KBT) {
             const float v = valid ? sr.av[j] : 0.0f;
-            s_sc[(kb * NH) * BM + r] = W4 ? v : v * sr.b0[j];
-            if (!W4 && NH == 2) s_sc[(kb * NH + 1) * BM + r] = v * sr.b1[j];
+            s_sc[(c * NH) * BM + r] = W4 ? v : v * sr.b0[j];
+            if (!W4 && NH == 2) s_sc[(c * NH + 1) * BM + r] = v * sr.b1[j];
         }
     }
 }
@@ -150,10 +164,15 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
     // scale products per (row, kb): stage 1 gate / up blocks; stage 2 the
     // workgroup's 128-column weight-scale blocks
     constexpr int NH = W4 ? 1 : (STAGE == 1 ? 2 : NW / 128);
+    // weight rows one column tile advances: stage 1 128 gate (and 128 up)
+    // rows, stage 2 the tile's NW output columns
+    constexpr int TROWS = STAGE == 1 ? 128 : NW;
+    constexpr int QP = 144;     // stage-1 fp8 staging row pitch: 16-byte aligned, conflict-free
     static_assert(BM == 64 || BM == 128, "prefill tiles are 64 or 128 rows");
     static_assert(A_PT >= 1, "one A piece per thread at least");
     __shared__ __attribute__((aligned(1024))) uint8_t s_a[2][A_BYTES];
-    __shared__ __attribute__((aligned(16))) float s_sc[kMaxKB * NH * BM];   // [kb][h][row]
+    __shared__ __attribute__((aligned(16))) float s_sc[kMaxKB * NH * BM];   // [step][h][row]
+    __shared__ __attribute__((aligned(16))) uint8_t s_q[STAGE == 1 ? BM * QP : 16];
     __shared__ int32_t s_arow[BM];
     __shared__ int64_t s_orow[BM];
     __shared__ float s_w[BM];
@@ -167,17 +186,20 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
     const int lr = lane & 15;
     const int lq = lane >> 4;
 
-    // ---- XCD-aware tile order ----
+    // ---- XCD-aware tile order: the grid's columns are groups of ntw
+    // column tiles ----
     const int L = blockIdx.x;
+    const int ntw = g.ntw;
+    const int ng = g.n_tiles / ntw;
     int nt, mt;
-    if ((g.n_tiles & 7) == 0) {
-        const int per = g.n_tiles >> 3;
+    if ((ng & 7) == 0) {
+        const int per = ng >> 3;
         const int idx = L >> 3;
         nt = (L & 7) * per + idx % per;
         mt = idx / per;
     } else {
-        nt = L % g.n_tiles;
-        mt = L / g.n_tiles;
+        nt = L % ng;
+        mt = L / ng;
     }
     if (mt >= g.m_tiles) return;
     const int subs = g.block_m / BM;                     // workgroups per sorted M-block
@@ -188,7 +210,7 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
     const int tokens = g.num_valid[1];
     const int e = g.sorted_eids[mb];
     if (e < 0 || e >= g.E) return;
-    const int n0 = STAGE == 1 ? nt * 128 : nt * NW;
+    const int n0 = nt * ntw * TROWS;                     // first column of the first tile
 
     int any_valid = 0;
     for (int r = tid; r < BM; r += kThreads) {
@@ -262,15 +284,17 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
     constexpr int BHI = SHUFFLED ? 256 : 16;
 
     using BS = BStep<W4, NCT>;
-    auto load_b = [&](BS& s, int kb) {
+    // B of K block kb of column tile jt (wave-uniform offsets)
+    auto load_b = [&](BS& s, int kb, int jt) {
+        const int so = __builtin_amdgcn_readfirstlane(kb * BSTEP + jt * (TROWS * KBY));
+        const int sso = __builtin_amdgcn_readfirstlane(kb * 4 + jt * (TROWS * KS));
 #pragma unroll
         for (int ct = 0; ct < NCT; ++ct) {
-            s.b[ct][0] = __builtin_amdgcn_raw_buffer_load_b128(rb, boff[ct], kb * BSTEP, 0);
+            s.b[ct][0] = __builtin_amdgcn_raw_buffer_load_b128(rb, boff[ct], so, 0);
             if (!W4)
                 s.b[ct][W4 ? 0 : 1] =
-                    __builtin_amdgcn_raw_buffer_load_b128(rb, boff[ct] + BHI, kb * BSTEP, 0);
-            s.bs[ct] = W4 ? (int)__builtin_amdgcn_raw_buffer_load_b8(rbs, bsoff[ct], kb * 4, 0)
-                          : 0;
+                    __builtin_amdgcn_raw_buffer_load_b128(rb, boff[ct] + BHI, so, 0);
+            s.bs[ct] = W4 ? (int)__builtin_amdgcn_raw_buffer_load_b8(rbs, bsoff[ct], sso, 0) : 0;
         }
     };
     // A of step k is staged in areg[k & 1]: loaded two steps ahead, stored
@@ -310,7 +334,7 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
     // (issued one region earlier) into the accumulators. The regions are
     // fenced so the scheduler cannot pair an FMA with the MFMA that feeds it
     // (which serialises a wave on MFMA latency).
-    auto compute = [&](const BS& bsv, int kb, int stage, auto na) {
+    auto compute = [&](const BS& bsv, int st, int stage, auto na) {
         constexpr int NA = decltype(na)::value;
         const uint8_t* sa_src = &s_a[stage][0];
         auto afrag = [&](int rt) {
@@ -337,7 +361,7 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
         const int hblk = (wn * NCT * 16) / 128;
         const int hsel0 = W4 ? 0 : (STAGE == 1 ? 0 : hblk);
         const int hsel1 = W4 ? 0 : (STAGE == 1 ? 1 : hblk);
-        const float* sc_row = &s_sc[kb * NH * BM + row_base + (TR ? lr : 4 * lq)];
+        const float* sc_row = &s_sc[st * NH * BM + row_base + (TR ? lr : 4 * lq)];
         auto scales = [&](int rt, v4f& s0, v4f& s1) {
             if constexpr (TR) {
                 const float x0 = sc_row[hsel0 * BM + rt * 16];
@@ -391,14 +415,18 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
         __builtin_amdgcn_sched_barrier(0);
     };
 
-    // ---- K loop: B D steps ahead in registers; A two steps ahead in
-    // registers and double-buffered in LDS; one barrier per step ----
+    // ---- K loop over the workgroup's ntw column tiles (KBT steps): B D
+    // steps ahead in registers; A two steps ahead in registers and
+    // double-buffered in LDS; one barrier per step. Step s is K block s % KB
+    // of column tile s / KB; A depends on the K block only, so the loads of
+    // the next tile's first steps are in flight while a tile's epilogue runs
+    const int KBT = KB * ntw;
     BS bbuf[D];
     // ---- preheader: the loads of the K loop's virtual steps -3 .. -1 in the
     // loop's own order (step j loads A(j+3), then B(j+D)), so the wait
     // counts at the loop head are the steady-state ones; the scale loads go
     // first (oldest) and their products are stored once they land ----
-    // scale products of the whole K range, [kb][h][row]: fp8 h = 0 / 1 are
+    // scale products of all steps, [step][h][row]: fp8 h = 0 / 1 are
     // stage 1's gate / up blocks or stage 2's two 128-column blocks; A8W4 the
     // activation scale only (the weight scale goes into the MFMA)
     const int sr_r = tid % BM, sr_q = tid / BM;
@@ -412,45 +440,215 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
     auto preheader = [&](auto nj) {
         constexpr int NJ = decltype(nj)::value;
         ScaleRegs<W4, NJ> sr;
-        scale_load<BM, NH, W4, NJ>(sr, sr_a, g.sa_kb, sr_w0, sr_w1, KB, sr_q);
+        scale_load<BM, NH, W4, NJ>(sr, sr_a, g.sa_kb, sr_w0, sr_w1, KB, KBT, sr_q);
 #pragma unroll
-        for (int m = 0; m < D - 3; ++m) load_b(bbuf[m], last(m));
+        for (int m = 0; m < D - 3; ++m) load_b(bbuf[m], last(m), 0);
         load_a(0, 0);                                           // step -3
-        if constexpr (D >= 3) load_b(bbuf[D - 3], last(D - 3));
+        if constexpr (D >= 3) load_b(bbuf[D - 3], last(D - 3), 0);
         load_a(1, last(1));                                     // step -2
-        if constexpr (D >= 2) load_b(bbuf[D - 2], last(D - 2));
-        scale_store<BM, NH, W4, NJ>(sr, s_sc, KB, sr_r, sr_q, sr_arow >= 0);
+        if constexpr (D >= 2) load_b(bbuf[D - 2], last(D - 2), 0);
+        scale_store<BM, NH, W4, NJ>(sr, s_sc, KBT, sr_r, sr_q, sr_arow >= 0);
         store_a(0);                                             // step -1
         load_a(0, last(2));
-        load_b(bbuf[D - 1], last(D - 1));
+        load_b(bbuf[D - 1], last(D - 1), 0);
     };
     constexpr int RP = kThreads / BM;
-    if (KB <= 16)
+    if (KBT <= 16)
         preheader(IntC<16 / RP>{});
-    else if (KB <= 32)
+    else if (KBT <= 32)
         preheader(IntC<32 / RP>{});
     else
         preheader(IntC<kMaxKB / RP>{});
     __syncthreads();                      // stage 0 and the scale products
+
+    // ---- epilogue of column tile jt; stage stg of s_a holds no live A ----
+    auto epilogue = [&](int jt, int stg) {
+        if constexpr (STAGE == 2) {
+            const int nc = n0 + jt * TROWS;
+            if (g.part) {
+                // the pair's weighted row, rounded once to bf16, staged through
+                // the free A stage half the rows at a time and stored as whole
+                // 16-byte pieces at part[pair, nc ..]
+                static_assert(STAGE != 2 || (BM / 2) * NW * 2 <= A_BYTES,
+                              "half a tile of bf16 rows fits one A stage");
+                uint16_t* s_p = reinterpret_cast<uint16_t*>(&s_a[stg][0]);   // [BM/2][NW]
+#pragma unroll
+                for (int hf = 0; hf < 2; ++hf) {
+#pragma unroll
+                    for (int rt = 0; rt < NRT; ++rt) {
+                        if ((row_base + rt * 16) / (BM / 2) != hf) continue;
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) {
+                            const int row = row_base + rt * 16 + 4 * lq + v;
+                            const float wgt = s_w[row];
+                            const int lrow = row - hf * (BM / 2);
+#pragma unroll
+                            for (int ct = 0; ct < NCT; ++ct)
+                                s_p[lrow * NW + wn * NCT * 16 + ct * 16 + lr] =
+                                    f32_to_bf16_bits(acc[rt][ct][v] * wgt);
+                        }
+                    }
+                    __syncthreads();
+                    for (int q = tid; q < (BM / 2) * (NW / 8); q += kThreads) {
+                        const int lrow = q / (NW / 8), piece = q % (NW / 8);
+                        const int64_t pair = s_arow[lrow + hf * (BM / 2)];
+                        if (pair < 0) continue;
+                        *reinterpret_cast<v4i*>(g.part + pair * g.N + nc + piece * 8) =
+                            *reinterpret_cast<const v4i*>(s_p + lrow * NW + piece * 8);
+                    }
+                    __syncthreads();
+                }
+            } else {
+#pragma unroll
+                for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        const int row = row_base + rt * 16 + 4 * lq + v;
+                        const int64_t t = s_orow[row];
+                        if (t < 0) continue;
+                        const float wgt = s_w[row];
+                        float* dst = g.acc + t * g.N + nc + wn * NCT * 16 + lr;
+#pragma unroll
+                        for (int ct = 0; ct < NCT; ++ct)
+                            unsafeAtomicAdd(dst + ct * 16, acc[rt][ct][v] * wgt);
+                    }
+            }
+            return;
+        } else {
+        // ---- stage 1: silu(gate)*up -> bf16 -> 1x128 fp8 requant ----
+        // wave wn holds output columns wn*NH1*16 + j*16 + (TR ? 4*lq + v : lr)
+        // (j < NH1) of the tile's 128, for rows row_base + rt*16 + (TR ? lr :
+        // 4*lq + v)
+        constexpr int NH1 = NCT / 2;
+        const int nc = n0 + jt * TROWS;
+        float h[NRT][NH1][4];
+#pragma unroll
+        for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+            for (int j = 0; j < NH1; ++j)
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+                    h[rt][j][v] = bf16_round(silu_f32(acc[rt][j][v]) * acc[rt][NH1 + j][v]);
+        if constexpr (TR) {
+#pragma unroll
+            for (int rt = 0; rt < NRT; ++rt) {
+                float m = 0.0f;
+#pragma unroll
+                for (int j = 0; j < NH1; ++j)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v)
+                        m = __builtin_fmaxf(m, __builtin_fabsf(h[rt][j][v]));
+                m = __builtin_fmaxf(m, __shfl_xor(m, 16, 64));
+                m = __builtin_fmaxf(m, __shfl_xor(m, 32, 64));
+                if (lq == 0) s_amax[wn][row_base + rt * 16 + lr] = m;
+            }
+        } else {
+#pragma unroll
+            for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    float m = 0.0f;
+#pragma unroll
+                    for (int j = 0; j < NH1; ++j)
+                        m = __builtin_fmaxf(m, __builtin_fabsf(h[rt][j][v]));
+                    m = warp_max_16(m);
+                    if (lr == 0) s_amax[wn][row_base + rt * 16 + 4 * lq + v] = m;
+                }
+        }
+        __syncthreads();
+        auto row_amax = [&](int row) {
+            float m = s_amax[0][row];
+#pragma unroll
+            for (int w = 1; w < WN; ++w) m = __builtin_fmaxf(m, s_amax[w][row]);
+            return __builtin_fmaxf(m, 1e-10f);
+        };
+        if constexpr (TR) {
+#pragma unroll
+            for (int rt = 0; rt < NRT; ++rt) {
+                const int row = row_base + rt * 16 + lr;
+                const float inv = 1.0f / (row_amax(row) * kInvFp8Max);
+#pragma unroll
+                for (int j = 0; j < NH1; ++j)
+                    *reinterpret_cast<uint32_t*>(&s_q[row * QP + wn * NH1 * 16 + j * 16 + 4 * lq]) =
+                        f32x4_to_fp8x4(h[rt][j][0] * inv, h[rt][j][1] * inv, h[rt][j][2] * inv,
+                                       h[rt][j][3] * inv);
+            }
+        } else {
+#pragma unroll
+            for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int row = row_base + rt * 16 + 4 * lq + v;
+                    const float inv = 1.0f / (row_amax(row) * kInvFp8Max);
+#pragma unroll
+                    for (int j = 0; j < NH1; ++j) {
+                        const uint32_t b = f32x2_to_fp8x2(h[rt][j][v] * inv, 0.0f) & 0xFFu;
+                        s_q[row * QP + wn * NH1 * 16 + j * 16 + lr] = (uint8_t)b;
+                    }
+                }
+        }
+        __syncthreads();
+        const int I = g.inter;
+        for (int q = tid; q < BM * 8; q += kThreads) {
+            const int row = q >> 3, part = q & 7;
+            const int64_t orow = s_orow[row];
+            if (orow < 0) continue;
+            *reinterpret_cast<v4i*>(g.a2 + orow * I + nc + part * 16) =
+                *reinterpret_cast<const v4i*>(s_q + row * QP + part * 16);
+            if (part == 0) g.a2_scale[orow * (I / 128) + nc / 128] = row_amax(row) * kInvFp8Max;
+        }
+        // s_q and s_amax are next written by the following tile's epilogue,
+        // after that tile's K steps and their barriers
+        }
+    };
+
     auto kloop = [&](auto na) {
-        for (int kb0 = 0; kb0 < KB; kb0 += D) {
+        int kbl = 0, jt = 0;             // K block and column tile of step kb0
+        for (int kb0 = 0; kb0 < KBT; kb0 += D) {
 #pragma unroll
             for (int d = 0; d < D; ++d) {
                 const int k = kb0 + d;
-                // Everything in the step is unconditional so the loop is one basic
-                // block and the compiler's wait counts stay exact: past the end the
-                // loads re-read the last step (L2 hits) and the store fills the
-                // stage that step k does not read.
+                // Every load and store in the step is unconditional: past the
+                // end A loads wrap to the first K blocks and B loads re-read the
+                // last step (L2 hits), and the store fills the stage that step k
+                // does not read.
+                // A of step k + 3: K block kbl + d + 3 <= KB + 2, wrapped (KB >= 1)
+                int ka = kbl + d + 3;
+                ka = ka >= KB ? ka - KB : ka;
+                ka = ka >= KB ? ka - KB : ka;
+                ka = ka >= KB ? ka - KB : ka;
                 store_a((k + 1) & 1);
-                load_a((k + 1) & 1, k + 3 < KB ? k + 3 : KB - 1);
+                load_a((k + 1) & 1, ka);
                 // issue the A loads before the step's math (a full step to land)
                 __builtin_amdgcn_sched_barrier(0);
                 compute(bbuf[d], k, k & 1, na);
-                load_b(bbuf[d], k + D < KB ? k + D : KB - 1);
+                // B of step k + D: this column tile or the next (D divides KB)
+                int kn = kbl + d + D, jn = jt;
+                if (kn >= KB) {
+                    kn -= KB;
+                    ++jn;
+                }
+                if (jn >= ntw) {
+                    kn = KB - 1;
+                    jn = ntw - 1;
+                }
+                load_b(bbuf[d], kn, jn);
                 __syncthreads();
                 // keep the scheduler from interleaving the unrolled steps (their
                 // operand sets would all be live at once)
                 __builtin_amdgcn_sched_barrier(0);
+            }
+            kbl += D;
+            if (kbl == KB) {
+                // the tile's last step read A stage (kb0 + D - 1) & 1, which the
+                // next step refills only after the epilogue's last barrier
+                epilogue(jt, (kb0 + D - 1) & 1);
+#pragma unroll
+                for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+                    for (int ct = 0; ct < NCT; ++ct) acc[rt][ct] = v4f{0.f, 0.f, 0.f, 0.f};
+                kbl = 0;
+                ++jt;
             }
         }
     };
@@ -461,132 +659,6 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
         kloop(IntC<0>{});
     else
         kloop(IntC<NRT>{});
-
-    if (STAGE == 2) {
-        if (g.part) {
-            // the pair's weighted row, rounded once to bf16, staged through LDS
-            // and stored as whole 16-byte pieces at part[pair, n0 ..]
-            static_assert(STAGE != 2 || BM * NW * 2 <= 2 * A_BYTES, "bf16 staging fits the A stages");
-            uint16_t* s_p = reinterpret_cast<uint16_t*>(&s_a[0][0]);   // [BM][NW]
-#pragma unroll
-            for (int rt = 0; rt < NRT; ++rt)
-#pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    const int row = row_base + rt * 16 + 4 * lq + v;
-                    const float wgt = s_w[row];
-#pragma unroll
-                    for (int ct = 0; ct < NCT; ++ct)
-                        s_p[row * NW + wn * NCT * 16 + ct * 16 + lr] =
-                            f32_to_bf16_bits(acc[rt][ct][v] * wgt);
-                }
-            __syncthreads();
-            for (int q = tid; q < BM * (NW / 8); q += kThreads) {
-                const int row = q / (NW / 8), piece = q % (NW / 8);
-                const int64_t pair = s_arow[row];
-                if (pair < 0) continue;
-                *reinterpret_cast<v4i*>(g.part + pair * g.N + n0 + piece * 8) =
-                    *reinterpret_cast<const v4i*>(s_p + row * NW + piece * 8);
-            }
-            return;
-        }
-#pragma unroll
-        for (int rt = 0; rt < NRT; ++rt)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const int row = row_base + rt * 16 + 4 * lq + v;
-                const int64_t t = s_orow[row];
-                if (t < 0) continue;
-                const float wgt = s_w[row];
-                float* dst = g.acc + t * g.N + n0 + wn * NCT * 16 + lr;
-#pragma unroll
-                for (int ct = 0; ct < NCT; ++ct)
-                    unsafeAtomicAdd(dst + ct * 16, acc[rt][ct][v] * wgt);
-            }
-        return;
-    }
-
-    // ---- stage 1 epilogue: silu(gate)*up -> bf16 -> 1x128 fp8 requant ----
-    // wave wn holds output columns wn*NH1*16 + j*16 + (TR ? 4*lq + v : lr)
-    // (j < NH1) of the tile's 128, for rows row_base + rt*16 + (TR ? lr :
-    // 4*lq + v)
-    constexpr int NH1 = NCT / 2;
-    constexpr int QP = 144;     // s_q row pitch: 16-byte aligned, conflict-free dword stores
-    float h[NRT][NH1][4];
-#pragma unroll
-    for (int rt = 0; rt < NRT; ++rt)
-#pragma unroll
-        for (int j = 0; j < NH1; ++j)
-#pragma unroll
-            for (int v = 0; v < 4; ++v)
-                h[rt][j][v] = bf16_round(silu_f32(acc[rt][j][v]) * acc[rt][NH1 + j][v]);
-    if constexpr (TR) {
-#pragma unroll
-        for (int rt = 0; rt < NRT; ++rt) {
-            float m = 0.0f;
-#pragma unroll
-            for (int j = 0; j < NH1; ++j)
-#pragma unroll
-                for (int v = 0; v < 4; ++v) m = __builtin_fmaxf(m, __builtin_fabsf(h[rt][j][v]));
-            m = __builtin_fmaxf(m, __shfl_xor(m, 16, 64));
-            m = __builtin_fmaxf(m, __shfl_xor(m, 32, 64));
-            if (lq == 0) s_amax[wn][row_base + rt * 16 + lr] = m;
-        }
-    } else {
-#pragma unroll
-        for (int rt = 0; rt < NRT; ++rt)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                float m = 0.0f;
-#pragma unroll
-                for (int j = 0; j < NH1; ++j) m = __builtin_fmaxf(m, __builtin_fabsf(h[rt][j][v]));
-                m = warp_max_16(m);
-                if (lr == 0) s_amax[wn][row_base + rt * 16 + 4 * lq + v] = m;
-            }
-    }
-    __syncthreads();
-    auto row_amax = [&](int row) {
-        float m = s_amax[0][row];
-#pragma unroll
-        for (int w = 1; w < WN; ++w) m = __builtin_fmaxf(m, s_amax[w][row]);
-        return __builtin_fmaxf(m, 1e-10f);
-    };
-    uint8_t* s_q = &s_a[0][0];  // [BM][QP] fp8 staging over both A stages (the K loop is done)
-    static_assert(BM * QP <= 2 * A_BYTES, "fp8 staging fits the A stages");
-    if constexpr (TR) {
-#pragma unroll
-        for (int rt = 0; rt < NRT; ++rt) {
-            const int row = row_base + rt * 16 + lr;
-            const float inv = 1.0f / (row_amax(row) * kInvFp8Max);
-#pragma unroll
-            for (int j = 0; j < NH1; ++j)
-                *reinterpret_cast<uint32_t*>(&s_q[row * QP + wn * NH1 * 16 + j * 16 + 4 * lq]) =
-                    f32x4_to_fp8x4(h[rt][j][0] * inv, h[rt][j][1] * inv, h[rt][j][2] * inv,
-                                   h[rt][j][3] * inv);
-        }
-    } else {
-#pragma unroll
-        for (int rt = 0; rt < NRT; ++rt)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const int row = row_base + rt * 16 + 4 * lq + v;
-                const float inv = 1.0f / (row_amax(row) * kInvFp8Max);
-#pragma unroll
-                for (int j = 0; j < NH1; ++j) {
-                    const uint32_t b = f32x2_to_fp8x2(h[rt][j][v] * inv, 0.0f) & 0xFFu;
-                    s_q[row * QP + wn * NH1 * 16 + j * 16 + lr] = (uint8_t)b;
-                }
-            }
-    }
-    __syncthreads();
-    const int I = g.inter;
-    for (int q = tid; q < BM * 8; q += kThreads) {
-        const int row = q >> 3, part = q & 7;
-        const int64_t orow = s_orow[row];
-        if (orow < 0) continue;
-        *reinterpret_cast<v4i*>(g.a2 + orow * I + n0 + part * 16) =
-            *reinterpret_cast<const v4i*>(s_q + row * QP + part * 16);
-        if (part == 0) g.a2_scale[orow * (I / 128) + n0 / 128] = row_amax(row) * kInvFp8Max;
-    }
 }
 
 template <int BM, int STAGE, bool SHUFFLED, bool W4>
@@ -639,6 +711,31 @@ static void launch(int bm, int KB, int grid, const Args& a, int shuffled, hipStr
     }
 }
 
+// Column tiles per workgroup. Walking two amortises a tile's setup chain
+// (sorted ids, then A rows and scales) and lets the next tile's first loads
+// land while the epilogue runs, but the tiles that share an M-block's A rows
+// then run one after another instead of side by side on one XCD, so A is
+// fetched into L2 once per tile. Measured on MI355X at T=8192 (MiMo dims):
+// stage 1 1735 -> 1783 us at two tiles; stage 2 1237 -> 1192 us at two,
+// 1223 us at four; with fewer than ~16 rounds of workgroups the longer tail
+// costs more (EP share T=4096: stage 2 116 -> 120 us). So stage 2 walks two
+// tiles on large grids, stage 1 none. AITER_AMD_PF_NTW1 / AITER_AMD_PF_NTW2
+// force a count (tests use them; any divisor of n_tiles with ntw * KB <=
+// kMaxKB).
+static int pick_ntw(int stage, int n_tiles, int KB, int64_t pairs, int rows) {
+    if (const char* env = getenv(stage == 1 ? "AITER_AMD_PF_NTW1" : "AITER_AMD_PF_NTW2")) {
+        const int c = atoi(env);
+        if (c >= 1 && n_tiles % c == 0 && c * KB <= kMaxKB) return c;
+    }
+    constexpr int64_t kSlots = 512;   // 256 CUs x 2 workgroups
+    constexpr int64_t kMinRounds = 16;
+    const int64_t wgs = (pairs + rows - 1) / rows * n_tiles;
+    if (stage == 2 && n_tiles % 2 == 0 && (n_tiles / 2) % 8 == 0 && 2 * KB <= kMaxKB &&
+        wgs / 2 >= kMinRounds * kSlots)
+        return 2;
+    return 1;
+}
+
 }  // namespace pf
 
 bool prefill_supported(int64_t block_m, int64_t K) {
@@ -675,7 +772,8 @@ void launch_moe_stage1_prefill(const uint8_t* a, const float* a_scale, int64_t s
     g.n_tiles = (int)(inter / 128);
     g.block_m = (int)block_m;
     g.m_tiles = (int)(max_m_blocks * (block_m / pf::wg_rows<1>((int)block_m)));
-    const int64_t grid = (int64_t)g.n_tiles * g.m_tiles;
+    g.ntw = pf::pick_ntw(1, g.n_tiles, (int)(K / 128), a_rows * topk, 64);
+    const int64_t grid = (int64_t)(g.n_tiles / g.ntw) * g.m_tiles;
     if (grid == 0) return;
     pf::launch<1>((int)block_m, (int)(K / 128), (int)grid, g, shuffled, stream);
     AMD_HIP_CHECK(hipGetLastError());
@@ -711,7 +809,8 @@ void launch_moe_stage2_prefill(const uint8_t* a2, const float* a2_scale, const u
     g.n_tiles = (int)(hidden / 128);
     g.block_m = (int)block_m;
     g.m_tiles = (int)(max_m_blocks * (block_m / pf::wg_rows<2>((int)block_m)));
-    const int64_t grid = (int64_t)g.n_tiles * g.m_tiles;
+    g.ntw = pf::pick_ntw(2, g.n_tiles, (int)(inter / 128), a_rows, (int)block_m);
+    const int64_t grid = (int64_t)(g.n_tiles / g.ntw) * g.m_tiles;
     if (grid == 0) return;
     pf::launch<2>((int)block_m, (int)(inter / 128), (int)grid, g, shuffled, stream);
     AMD_HIP_CHECK(hipGetLastError());

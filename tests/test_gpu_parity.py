@@ -301,6 +301,45 @@ def test_fused_moe_mimo_prefill_stagewise(cuda_device, T, block_ms):
     _fullshape.stagewise_check(cfg, cuda_device, block_ms)
 
 
+@pytest.mark.parametrize("weights,bm", [("fp8", 64), ("fp8", 128), ("mxfp4", 128)])
+@pytest.mark.parametrize("ntw", [2, 4])
+def test_prefill_column_walk_bit_exact(cuda_device, monkeypatch, weights, bm, ntw):
+    """A prefill workgroup that walks ntw column tiles in one pipelined K loop
+    (AITER_AMD_PF_NTW1/2 force the count) computes every tile as a
+    one-tile workgroup does: stage 1's a2 and the layer's output (per-pair
+    rows summed in slot order) are bitwise equal. Stage 1 has 8 column tiles
+    and stage 2 16, so both the XCD order (8 column groups) and the plain
+    order are walked."""
+    cfg = W.MoEConfig("walk", 300, 2048, 1024, 16, 4, seed=21, weights=weights)
+    wts = W.make_weights(cfg, device=cuda_device, shuffle=True)
+    x = W.make_hidden(cfg, device=cuda_device)
+    tw, ids = W.make_routing(cfg, device=cuda_device)
+    qt = A.QuantType.per_1x32 if weights == "mxfp4" else A.QuantType.per_128x128
+
+    def layer(c):
+        monkeypatch.setenv("AITER_AMD_PF_NTW1", str(c))
+        monkeypatch.setenv("AITER_AMD_PF_NTW2", str(c))
+        out = A.fused_moe(x, wts["w1"], wts["w2"], tw, ids, quant_type=qt,
+                          w1_scale=wts["w1_scale"], w2_scale=wts["w2_scale"], block_size_M=bm)
+        a2 = None
+        if weights == "fp8":
+            a1, a1s = A.per_group_quant_hip(x)
+            sid, sw, se, nv, _ = A.moe_sorting(ids, tw, cfg.experts, cfg.model_dim,
+                                                torch.bfloat16, bm)
+            a2, a2s = A.moe_stage1_fp8_blockscale(a1, a1s, wts["w1"], wts["w1_scale"], sid, se,
+                                                  nv, cfg.topk, bm, True)
+            a2 = (a2.view(torch.uint8).clone(), a2s.clone())
+        torch.cuda.synchronize()
+        return out, a2
+
+    out1, a21 = layer(1)
+    outc, a2c = layer(ntw)
+    if a21 is not None:
+        assert torch.equal(a21[0], a2c[0]) and torch.equal(a21[1], a2c[1])
+    assert torch.equal(out1, outc), (out1.float() - outc.float()).abs().max().item()
+    assert torch.count_nonzero(out1).item() > 0
+
+
 # --------------------------------------------------------- edge cases ---
 def test_fused_moe_empty_batch(cuda_device):
     cfg = W.CONFIG_A
