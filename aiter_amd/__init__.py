@@ -35,7 +35,8 @@ from .quant import (
     per_group_quant_hip,
     quant_weight_per_128x128,
 )
-from .shuffle import shuffle_weight, unshuffle_weight
+from .shuffle import (shuffle_scale_a16w4, shuffle_weight, shuffle_weight_a16w4,
+                      unshuffle_scale_a16w4, unshuffle_weight, unshuffle_weight_a16w4)
 from .topk import (
     biased_grouped_topk,
     biased_grouped_topk_hip,
@@ -52,6 +53,7 @@ __all__ = [
     "moe_stage2_a8w4", "select_block_m", "sorted_capacity", "dynamic_per_token_scaled_quant", "per_group_quant_hip",
     "quant_weight_per_128x128", "per_1x32_f4_quant", "f32_to_e8m0", "e8m0_to_f32", "e8m0_shuffle",
     "e8m0_unshuffle",
-    "shuffle_weight", "unshuffle_weight", "topk_softmax", "topk_sigmoid", "grouped_topk",
+    "shuffle_weight", "unshuffle_weight", "shuffle_weight_a16w4", "unshuffle_weight_a16w4",
+    "shuffle_scale_a16w4", "unshuffle_scale_a16w4", "topk_softmax", "topk_sigmoid", "grouped_topk",
     "biased_grouped_topk", "biased_grouped_topk_hip", "fused_topk",
 ]

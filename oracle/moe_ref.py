@@ -436,3 +436,52 @@ def e8m0_shuffle_ref(scale: np.ndarray) -> np.ndarray:
             out[off] = scale[r, col]
             filled[off] = True
     return out.reshape(sm, sn), filled.reshape(sm, sn)
+
+
+# ------------------------------------------------------ a16w4 layouts ---
+def a16w4_weight_ref(w: np.ndarray, nlane: int, gate_up: bool) -> np.ndarray:
+    """shuffle_weight_a16w4 (aiter/ops/shuffle.py:51-81) as an index formula:
+    byte (e, n, k) with KLane = 64 / nlane, KPack = 16, n = half*N/2 +
+    n0*nlane + nl (gate_up) or n0*nlane + nl, k = (k0*KLane + kl)*16 + kp
+    lands at ((((n0*H + half)*K0 + k0)*KLane + kl)*nlane + nl)*16 + kp of its
+    expert, H = 2 with gate_up, else 1 (half = 0)."""
+    E, N, Kp = w.shape
+    klane = 64 // nlane
+    h = N // 2 if gate_up else N
+    H = 2 if gate_up else 1
+    K0 = Kp // (klane * 16)
+    out = np.empty_like(w).reshape(E, -1)
+    for n in range(N):
+        half, r = (n // h, n % h)
+        n0, nl = r // nlane, r % nlane
+        for k in range(Kp):
+            k0, rem = k // (klane * 16), k % (klane * 16)
+            kl, kp = rem // 16, rem % 16
+            off = ((((n0 * H + half) * K0 + k0) * klane + kl) * nlane + nl) * 16 + kp
+            out[:, off] = w[:, n, k]
+    return out.reshape(w.shape)
+
+
+def a16w4_scale_ref(s: np.ndarray, experts: int, gate_up: bool) -> np.ndarray:
+    """shuffle_scale_a16w4 (aiter/ops/shuffle.py:84-113) as an index formula:
+    byte (e, n, k) of the [E*N, K/32] array, n = np*N/2 + n1*16 + nl
+    (gate_up) or n1*32 + np*16 + nl, k = (k1*2 + kk)*4 + kl, lands at
+    ((((n1*K1 + k1)*4 + kl)*16 + nl)*2 + kk)*2 + np of its expert."""
+    n_all, k_ = s.shape
+    N = n_all // experts
+    K1 = k_ // 8
+    src = s.reshape(experts, N, k_)
+    out = np.empty((experts, N * k_), dtype=s.dtype)
+    for n in range(N):
+        if gate_up:
+            np_, r = n // (N // 2), n % (N // 2)
+            n1, nl = r // 16, r % 16
+        else:
+            n1, r = n // 32, n % 32
+            np_, nl = r // 16, r % 16
+        for k in range(k_):
+            k1, r2 = k // 8, k % 8
+            kk, kl = r2 // 4, r2 % 4
+            off = ((((n1 * K1 + k1) * 4 + kl) * 16 + nl) * 2 + kk) * 2 + np_
+            out[:, off] = src[:, n, k]
+    return out.reshape(n_all, k_)

@@ -276,6 +276,35 @@ def test_e8m0_shuffle_layout_and_loader():
         e8m0_rowmajor(torch.zeros(100, 8, dtype=torch.uint8), 4, 64, 8)
 
 
+@pytest.mark.parametrize("nlane", [16, 32])
+@pytest.mark.parametrize("gate_up", [True, False])
+def test_a16w4_layouts_convert_to_row_major(nlane, gate_up):
+    """The reference's a16w4 weight and scale layouts (its Swiglu fp4 kernels'
+    inputs): the view/permute implementation matches the oracle's explicit
+    index formula, the unshuffle functions invert it, and an A8W4 checkpoint
+    packed that way comes back as the row-major weights and [E, N, K/32]
+    scales fused_moe reads."""
+    rng = np.random.default_rng(nlane + gate_up)
+    E, N, K = 3, 128, 512
+    w = rng.integers(0, 256, (E, N, K // 2)).astype(np.uint8)
+    s = rng.integers(100, 140, (E * N, K // 32)).astype(np.uint8)
+    wt, st = torch.from_numpy(w), torch.from_numpy(s)
+    ws = A.shuffle_weight_a16w4(wt, nlane, gate_up)
+    ss = A.shuffle_scale_a16w4(st, E, gate_up)
+    assert np.array_equal(ws.numpy(), R.a16w4_weight_ref(w, nlane, gate_up))
+    assert np.array_equal(ss.numpy(), R.a16w4_scale_ref(s, E, gate_up))
+    assert not np.array_equal(ws.numpy(), w) and not np.array_equal(ss.numpy(), s)
+    assert torch.equal(A.unshuffle_weight_a16w4(ws, nlane, gate_up), wt)
+    assert torch.equal(A.unshuffle_scale_a16w4(ss, E, gate_up), st)
+    # typed tensors keep their dtype
+    wf = wt.view(torch.float8_e4m3fn)
+    assert A.shuffle_weight_a16w4(wf, nlane, gate_up).dtype == torch.float8_e4m3fn
+    with pytest.raises(ValueError, match="does not tile"):
+        A.shuffle_weight_a16w4(wt[:, :, :100], nlane, gate_up)
+    with pytest.raises(ValueError, match="N % 32"):
+        A.shuffle_scale_a16w4(st[: E * 16], E, gate_up)
+
+
 def test_tuned_dispatch_table():
     """The committed block_m table (aiter_amd/tune.py) answers for the MiMo
     shapes it was swept on and buckets token counts like get_padded_M."""
