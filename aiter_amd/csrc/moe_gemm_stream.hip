@@ -26,6 +26,9 @@
 // always outstanding and the compiler's wait counts target the oldest.
 // Weight loads are non-temporal: each weight byte is used by one workgroup
 // once, so it should not displace the activations and scales in the caches.
+#include <algorithm>
+#include <cstdlib>
+
 #include "common.h"
 
 namespace aiter_amd {
@@ -58,6 +61,7 @@ struct Args {
     int topk;
     int E;
     int64_t a_rows;
+    int ntw;                   // stage 2: 256-column groups per workgroup, one K loop
 };
 
 // One K step of one wave's operands.
@@ -72,7 +76,9 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
     constexpr int NRT = BM / 16;
     static_assert(BM == 16 || BM == 32, "stream tiles are 16 or 32 rows");
     __shared__ __attribute__((aligned(16))) float s_sa[kMaxKB * BM];   // [kb][row]
-    __shared__ float s_sw[2][kMaxKB];
+    // weight-scale blocks [block][kb]: stage 1 gate / up (row stride kMaxKB),
+    // stage 2 the 2 * ntw 128-column blocks (row stride KB)
+    __shared__ float s_sw[2 * kMaxKB];
     __shared__ int32_t s_arow[BM];
     __shared__ int64_t s_orow[BM];
     __shared__ float s_w[BM];
@@ -91,7 +97,10 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
     const int tokens = g.num_valid[1];
     const int e = g.sorted_eids[mb];
     if (e < 0 || e >= g.E) return;
-    const int n0 = blockIdx.x * (STAGE == 1 ? 128 : 256);
+    // stage 2 may walk ntw consecutive 256-column groups in one K loop (steps
+    // s = jt * KB + kb); stage 1 always has one tile
+    const int ntw = STAGE == 2 ? g.ntw : 1;
+    const int n0 = blockIdx.x * (STAGE == 1 ? 128 : 256 * ntw);
 
     for (int r = tid; r < BM; r += kThreads) {
         const uint32_t id = (uint32_t)g.sorted_ids[mb * BM + r];
@@ -122,11 +131,15 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
         s_sa[kb * BM + r] = arow >= 0 ? g.a_scale[arow * g.sa_row + kb * g.sa_kb] : 0.0f;
     }
     if (!W4) {
+        // stage 1: blocks gate, up; stage 2: the 2 * ntw 128-column blocks
         const float* wse = g.w_scale + (int64_t)e * (g.N / 128) * KB;
         const int nb0 = n0 / 128;
         const int nb1 = STAGE == 1 ? (g.inter + n0) / 128 : n0 / 128 + 1;
-        for (int i = tid; i < 2 * KB; i += kThreads)
-            s_sw[i / KB][i % KB] = wse[(i < KB ? nb0 : nb1) * KB + (i % KB)];
+        for (int i = tid; i < 2 * ntw * KB; i += kThreads) {
+            const int blk = i / KB;
+            s_sw[blk * (STAGE == 1 ? kMaxKB : KB) + i % KB] =
+                wse[(STAGE == 1 ? (blk == 0 ? nb0 : nb1) : nb0 + blk) * KB + (i % KB)];
+        }
     }
     __syncthreads();
 
@@ -162,10 +175,11 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
     }
 
     using S = Step<NRT, W4>;
-    auto load = [&](S& s, int kb) {
+    // operands of K block kb of column group jt
+    auto load = [&](S& s, int kb, int jt) {
 #pragma unroll
         for (int ct = 0; ct < kNCT; ++ct) {
-            const uint8_t* p = bsrc[ct] + (int64_t)kb * BSTEP;
+            const uint8_t* p = bsrc[ct] + (int64_t)kb * BSTEP + (int64_t)jt * 256 * KBY;
             s.b[ct][0] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(p));
             if (!W4)
                 s.b[ct][W4 ? 0 : 1] =
@@ -188,10 +202,10 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
     // A8W4 scales of a group of D steps in one load: k-groups 4*kb .. 4*(kb+D)-1
     // of the row (the row and kb*4 are multiples of 4*D bytes, as D divides
     // K/128); step d's byte for this lane is byte lq of dword d
-    auto load_sg = [&](int (&dst)[kNCT][D], int kb) {
+    auto load_sg = [&](int (&dst)[kNCT][D], int kb, int jt) {
 #pragma unroll
         for (int ct = 0; ct < kNCT; ++ct) {
-            const uint8_t* p = bssrc[ct] + kb * 4;
+            const uint8_t* p = bssrc[ct] + kb * 4 + (int64_t)jt * 256 * (K / 32);
             if constexpr (D == 4) {
                 const v4i v = *reinterpret_cast<const v4i*>(p);
                 dst[ct][0] = v[0], dst[ct][1] = v[1], dst[ct][2] = v[2], dst[ct][3] = v[3];
@@ -204,11 +218,12 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
         }
     };
 
-    auto compute = [&](const S& s, int kb, const int (&sg)[kNCT][D], int d) {
+    auto compute = [&](const S& s, int kb, int jt, const int (&sg)[kNCT][D], int d) {
         // stage 1: tiles 0,1 gate (scale block 0), 2,3 up (block 1); stage 2:
-        // the wave's 64 columns lie in 128-column block wv/2
-        const float sw0 = W4 ? 1.0f : s_sw[STAGE == 1 ? 0 : (wv >> 1)][kb];
-        const float sw1 = W4 ? 1.0f : s_sw[STAGE == 1 ? 1 : (wv >> 1)][kb];
+        // the wave's 64 columns lie in 128-column block wv/2 of group jt
+        const float sw0 = W4 ? 1.0f : STAGE == 1 ? s_sw[kb] : s_sw[(2 * jt + (wv >> 1)) * KB + kb];
+        const float sw1 =
+            W4 ? 1.0f : STAGE == 1 ? s_sw[kMaxKB + kb] : s_sw[(2 * jt + (wv >> 1)) * KB + kb];
 #pragma unroll
         for (int rt = 0; rt < NRT; ++rt) {
             const v4f sa = *reinterpret_cast<const v4f*>(&s_sa[kb * BM + rt * 16 + 4 * lq]);
@@ -236,30 +251,8 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
         }
     };
 
-    // ---- K loop: D steps in flight ----
-    S buf[D];
-    int sgc[kNCT][D], sgn[kNCT][D];            // A8W4 scales: current / next group
-    if (W4) load_sg(sgc, 0);
-#pragma unroll
-    for (int d = 0; d < D; ++d) load(buf[d], d);
-    for (int kb0 = 0; kb0 < KB - D; kb0 += D) {
-        if (W4) load_sg(sgn, kb0 + D);
-#pragma unroll
-        for (int d = 0; d < D; ++d) {
-            compute(buf[d], kb0 + d, sgc, d);
-            load(buf[d], kb0 + d + D);
-        }
-        if (W4) {
-#pragma unroll
-            for (int ct = 0; ct < kNCT; ++ct)
-#pragma unroll
-                for (int d = 0; d < D; ++d) sgc[ct][d] = sgn[ct][d];
-        }
-    }
-#pragma unroll
-    for (int d = 0; d < D; ++d) compute(buf[d], KB - D + d, sgc, d);
-
-    if (STAGE == 2) {
+    // ---- stage 2 epilogue of column group jt: weighted fp32 atomics ----
+    auto epilogue2 = [&](int jt) {
 #pragma unroll
         for (int rt = 0; rt < NRT; ++rt)
 #pragma unroll
@@ -268,10 +261,71 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
                 const int64_t t = s_orow[row];
                 if (t < 0) continue;
                 const float wgt = s_w[row];
-                float* dst = g.acc + t * g.N + n0 + 64 * wv + lr;
+                float* dst = g.acc + t * g.N + n0 + jt * 256 + 64 * wv + lr;
 #pragma unroll
                 for (int ct = 0; ct < kNCT; ++ct) unsafeAtomicAdd(dst + 16 * ct, acc[rt][ct][v] * wgt);
             }
+    };
+
+    S buf[D];
+    int sgc[kNCT][D], sgn[kNCT][D];            // A8W4 scales: current / next group
+    if (W4) load_sg(sgc, 0, 0);
+#pragma unroll
+    for (int d = 0; d < D; ++d) load(buf[d], d, 0);
+    auto next_scales = [&]() {
+        if (W4) {
+#pragma unroll
+            for (int ct = 0; ct < kNCT; ++ct)
+#pragma unroll
+                for (int d = 0; d < D; ++d) sgc[ct][d] = sgn[ct][d];
+        }
+    };
+    if constexpr (STAGE == 1) {
+        // ---- K loop: D steps in flight ----
+        for (int kb0 = 0; kb0 < KB - D; kb0 += D) {
+            if (W4) load_sg(sgn, kb0 + D, 0);
+#pragma unroll
+            for (int d = 0; d < D; ++d) {
+                compute(buf[d], kb0 + d, 0, sgc, d);
+                load(buf[d], kb0 + d + D, 0);
+            }
+            next_scales();
+        }
+#pragma unroll
+        for (int d = 0; d < D; ++d) compute(buf[d], KB - D + d, 0, sgc, d);
+    } else {
+        // ---- K loop over ntw * KB steps: D steps in flight; a group's last
+        // steps are followed by its epilogue while the next group's first D
+        // steps load (D divides KB) ----
+        const int KBT = KB * ntw;
+        int kbl = 0, jt = 0;                   // K block and column group of step kb0
+        for (int kb0 = 0; kb0 < KBT - D; kb0 += D) {
+            // K block and group of step kb0 + D
+            int kbn = kbl + D, jn = jt;
+            if (kbn == KB) {
+                kbn = 0;
+                ++jn;
+            }
+            if (W4) load_sg(sgn, kbn, jn);
+#pragma unroll
+            for (int d = 0; d < D; ++d) {
+                compute(buf[d], kbl + d, jt, sgc, d);
+                load(buf[d], kbn + d, jn);
+            }
+            next_scales();
+            if (jn != jt) {
+                epilogue2(jt);
+#pragma unroll
+                for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+                    for (int ct = 0; ct < kNCT; ++ct) acc[rt][ct] = v4f{0.f, 0.f, 0.f, 0.f};
+            }
+            kbl = kbn;
+            jt = jn;
+        }
+#pragma unroll
+        for (int d = 0; d < D; ++d) compute(buf[d], kbl + d, jt, sgc, d);
+        epilogue2(jt);
         return;
     }
 
@@ -368,6 +422,30 @@ static void launch(int bm, int KB, dim3 grid, const Args& a, int shuffled, hipSt
     }
 }
 
+// Stage 2's 256-column groups per workgroup. A stage-2 workgroup streams
+// 256 x K weight bytes per group (MiMo dims: 512 KB fp8, 256 KB fp4, against
+// a stage-1 workgroup's 1 MB / 512 KB), so its setup and epilogue weigh more;
+// walking groups in one K loop, up to ~1 MB of weights per workgroup, evens
+// that out while the grid stays large enough to keep every CU streaming.
+// Measured on MI355X (stage 2, MiMo dims): fp8 T=32 231 -> 213 us at two
+// groups, T=128 378 -> 351 us; fp4 T=32 128 -> 124 us at four; T=1 15 ->
+// 24 us at two (64 workgroups), hence the grid floor. est_blocks: the
+// expected M-blocks (at decode sizes one per touched expert).
+// AITER_AMD_ST_NTW2 forces a count (tests use it).
+static int pick_ntw2(int64_t groups, int64_t KB, int64_t KBY, int64_t est_blocks) {
+    if (const char* env = getenv("AITER_AMD_ST_NTW2")) {
+        const int c = atoi(env);
+        if (c >= 1 && groups % c == 0 && c * KB <= kMaxKB) return c;
+    }
+    constexpr int64_t kMinWgs = 1024;             // 256 CUs x 2 workgroups x 2 rounds
+    constexpr int64_t kTargetBytes = 1 << 20;     // weight bytes per workgroup
+    for (int64_t c = std::max<int64_t>(1, kTargetBytes / (256 * KBY)); c > 1; c /= 2) {
+        if (groups % c == 0 && c * KB <= kMaxKB && est_blocks * groups / c >= kMinWgs)
+            return (int)c;
+    }
+    return 1;
+}
+
 }  // namespace stream
 
 // 16/32-row M-blocks, K a multiple of 128 up to 8192; stage 2 also needs
@@ -436,7 +514,9 @@ void launch_moe_stage2_stream(const uint8_t* a2, const float* a2_scale, const ui
     g.E = (int)E;
     g.a_rows = a_rows;
     if (max_m_blocks == 0) return;
-    const dim3 grid((unsigned)(hidden / 256), (unsigned)max_m_blocks);
+    g.ntw = stream::pick_ntw2(hidden / 256, inter / 128, w2_scale_e8m0 ? inter / 2 : inter,
+                              std::min<int64_t>(a_rows, E));
+    const dim3 grid((unsigned)(hidden / 256 / g.ntw), (unsigned)max_m_blocks);
     stream::launch<2>((int)block_m, (int)(inter / 128), grid, g, shuffled, stream);
     AMD_HIP_CHECK(hipGetLastError());
 }

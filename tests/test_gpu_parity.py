@@ -340,6 +340,46 @@ def test_prefill_column_walk_bit_exact(cuda_device, monkeypatch, weights, bm, nt
     assert torch.count_nonzero(out1).item() > 0
 
 
+@pytest.mark.parametrize("weights", ["fp8", "mxfp4"])
+@pytest.mark.parametrize("bm", [16, 32])
+@pytest.mark.parametrize("ntw", [2, 4])
+def test_stream_stage2_column_walk(cuda_device, monkeypatch, weights, bm, ntw):
+    """The decode kernel's stage 2 walking ntw 256-column groups per workgroup
+    (AITER_AMD_ST_NTW2 forces the count). With one slot per token every
+    output element gets exactly one atomic add, so the accumulator is
+    bitwise equal to the one-group walk's; with top-4 the two differ only by
+    the order of the fp32 atomic adds (the one-group path itself is checked
+    against the oracle by the layer tests)."""
+    st1 = A.moe_stage1_a8w4 if weights == "mxfp4" else A.moe_stage1_fp8_blockscale
+    st2 = A.moe_stage2_a8w4 if weights == "mxfp4" else A.moe_stage2_fp8_blockscale
+    for k, seed in ((1, 31), (4, 32)):
+        cfg = W.MoEConfig("swalk", 40, 2048, 1024, 8, k, seed=seed, weights=weights)
+        wts = W.make_weights(cfg, device=cuda_device, shuffle=True)
+        x = W.make_hidden(cfg, device=cuda_device)
+        tw, ids = W.make_routing(cfg, device=cuda_device)
+        a1, a1s = A.per_group_quant_hip(x)
+        sid, sw, se, nv, _ = A.moe_sorting(ids, tw, cfg.experts, cfg.model_dim, torch.float32,
+                                            bm)
+        a2, a2s = st1(a1, a1s, wts["w1"], wts["w1_scale"], sid, se, nv, k, bm, True)
+
+        def stage2(c):
+            monkeypatch.setenv("AITER_AMD_ST_NTW2", str(c))
+            acc = torch.zeros(cfg.tokens, cfg.model_dim, dtype=torch.float32,
+                              device=cuda_device)
+            st2(a2, a2s, wts["w2"], wts["w2_scale"], sid, sw, se, nv, acc, bm, True)
+            torch.cuda.synchronize()
+            return acc
+
+        acc1, accc = stage2(1), stage2(ntw)
+        assert torch.count_nonzero(acc1).item() > 0
+        if k == 1:
+            assert torch.equal(acc1, accc)
+        else:
+            # four fp32 terms summed in another order: a few ulps of the largest
+            tol = 4 * 2.0 ** -23 * acc1.abs().max().item()
+            assert (acc1 - accc).abs().max().item() <= tol
+
+
 # --------------------------------------------------------- edge cases ---
 def test_fused_moe_empty_batch(cuda_device):
     cfg = W.CONFIG_A
