@@ -77,7 +77,7 @@ void launch_moe_stage1_prefill(const uint8_t*, const float*, int64_t, int64_t, c
 void launch_moe_stage2_prefill(const uint8_t*, const float*, const uint8_t*, const float*,
                                const uint8_t*, const int32_t*, const float*, const int32_t*,
                                const int32_t*, float*, uint16_t*, int64_t, int64_t, int64_t,
-                               int64_t, int64_t, int64_t, int64_t, int, hipStream_t);
+                               int64_t, int64_t, int64_t, int64_t, int, hipStream_t, int64_t);
 
 // Weight scales of one layer: fp32 128x128 blocks (fp8 weights) or e8m0
 // bytes per 1x32 K block (MXFP4 weights); exactly one is set.
@@ -122,18 +122,22 @@ static bool stage2_on_prefill(int64_t bm, int64_t I, int64_t H, WScale w2s) {
 
 // acc: fp32 [tokens, H] accumulated atomically; part (prefill kernel only):
 // bf16 [pairs, H] rows written once each, acc unused.
+// est_pairs: the pairs expected on this GPU (the EP share's fraction of
+// tokens * topk when the caller knows it), a launch-shape hint only.
 static void stage2_dispatch(const uint8_t* a2, const float* a2s, const uint8_t* w2,
                             WScale w2s, const int32_t* sid, const float* sw,
                             const int32_t* seid, const int32_t* nv, float* acc, int64_t a_rows,
                             int64_t I, int64_t H, int64_t E, int64_t topk, int64_t bm,
-                            int64_t mblocks, int sh, hipStream_t s, uint16_t* part = nullptr) {
+                            int64_t mblocks, int sh, hipStream_t s, uint16_t* part = nullptr,
+                            int64_t est_pairs = -1) {
     AMD_CHECK(!part || stage2_on_prefill(bm, I, H, w2s), "per-pair rows need the prefill kernel");
     if (stream_supported(bm, I) && H % 256 == 0)
         launch_moe_stage2_stream(a2, a2s, w2, w2s.f32, w2s.e8m0, sid, sw, seid, nv, acc, a_rows,
                                  I, H, E, topk, bm, mblocks, sh, s);
     else if (prefill_supported(bm, I) && H % 256 == 0 && (!w2s.e8m0 || bm == 128))
         launch_moe_stage2_prefill(a2, a2s, w2, w2s.f32, w2s.e8m0, sid, sw, seid, nv, acc, part,
-                                  a_rows, I, H, E, topk, bm, mblocks, sh, s);
+                                  a_rows, I, H, E, topk, bm, mblocks, sh, s,
+                                  est_pairs < 0 ? a_rows : est_pairs);
     else if (v2_supported(bm, I) && H % 256 == 0)
         launch_moe_stage2_fp8bs_v2(a2, a2s, w2, w2s.f32, w2s.e8m0, sid, sw, seid, nv, acc, a_rows,
                                    I, H, E, topk, bm, mblocks, sh, s);
@@ -341,7 +345,8 @@ void fused_entry(const void* hidden_states, int hidden_dtype, const void* w1, WS
                     num_experts, topk, block_m, L.blocks, sh, s);
     stage2_dispatch(a2, a2_scale, (const uint8_t*)w2, w2s, sorted_ids, sorted_w, sorted_eids,
                     num_valid, part ? nullptr : acc, tokens * topk, inter_dim, model_dim,
-                    num_experts, topk, block_m, L.blocks, sh, s, part);
+                    num_experts, topk, block_m, L.blocks, sh, s, part,
+                    tokens * topk * num_experts / E_sort);
     if (part)
         launch_slot_sum(part, topk_ids, expert_mask, E_sort, num_valid, out, out_dtype, tokens,
                         topk, model_dim, s);

@@ -717,18 +717,19 @@ static void launch(int bm, int KB, int grid, const Args& a, int shuffled, hipStr
 // then run one after another instead of side by side on one XCD, so A is
 // fetched into L2 once per tile. Measured on MI355X at T=8192 (MiMo dims):
 // stage 1 1735 -> 1783 us at two tiles; stage 2 1237 -> 1192 us at two,
-// 1223 us at four; with fewer than ~16 rounds of workgroups the longer tail
-// costs more (EP share T=4096: stage 2 116 -> 120 us). So stage 2 walks two
-// tiles on large grids, stage 1 none. AITER_AMD_PF_NTW1 / AITER_AMD_PF_NTW2
-// force a count (tests use them; any divisor of n_tiles with ntw * KB <=
-// kMaxKB).
+// 1223 us at four; T=2048 (64-row blocks) 441 -> 421 us at two; a grid of a
+// few rounds loses more to the longer tail (EP share T=4096, 32 of 256
+// experts: 116 -> 120 us). So stage 2 walks two tiles when the pairs
+// expected on this GPU fill at least kMinRounds rounds of workgroups after
+// halving, stage 1 none. AITER_AMD_PF_NTW1 / AITER_AMD_PF_NTW2 force a count
+// (tests use them; any divisor of n_tiles with ntw * KB <= kMaxKB).
 static int pick_ntw(int stage, int n_tiles, int KB, int64_t pairs, int rows) {
     if (const char* env = getenv(stage == 1 ? "AITER_AMD_PF_NTW1" : "AITER_AMD_PF_NTW2")) {
         const int c = atoi(env);
         if (c >= 1 && n_tiles % c == 0 && c * KB <= kMaxKB) return c;
     }
     constexpr int64_t kSlots = 512;   // 256 CUs x 2 workgroups
-    constexpr int64_t kMinRounds = 16;
+    constexpr int64_t kMinRounds = 8;
     const int64_t wgs = (pairs + rows - 1) / rows * n_tiles;
     if (stage == 2 && n_tiles % 2 == 0 && (n_tiles / 2) % 8 == 0 && 2 * KB <= kMaxKB &&
         wgs / 2 >= kMinRounds * kSlots)
@@ -785,7 +786,7 @@ void launch_moe_stage2_prefill(const uint8_t* a2, const float* a2_scale, const u
                                const int32_t* sorted_eids, const int32_t* num_valid, float* acc,
                                uint16_t* part, int64_t a_rows, int64_t inter, int64_t hidden,
                                int64_t E, int64_t topk, int64_t block_m, int64_t max_m_blocks,
-                               int shuffled, hipStream_t stream) {
+                               int shuffled, hipStream_t stream, int64_t est_pairs) {
     pf::Args g{};
     g.a = a2;
     g.a_scale = a2_scale;
@@ -809,7 +810,7 @@ void launch_moe_stage2_prefill(const uint8_t* a2, const float* a2_scale, const u
     g.n_tiles = (int)(hidden / 128);
     g.block_m = (int)block_m;
     g.m_tiles = (int)(max_m_blocks * (block_m / pf::wg_rows<2>((int)block_m)));
-    g.ntw = pf::pick_ntw(2, g.n_tiles, (int)(inter / 128), a_rows, (int)block_m);
+    g.ntw = pf::pick_ntw(2, g.n_tiles, (int)(inter / 128), est_pairs, (int)block_m);
     const int64_t grid = (int64_t)(g.n_tiles / g.ntw) * g.m_tiles;
     if (grid == 0) return;
     pf::launch<2>((int)block_m, (int)(inter / 128), (int)grid, g, shuffled, stream);
