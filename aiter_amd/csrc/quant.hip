@@ -143,8 +143,16 @@ void launch_acc_to_out(const float* acc, void* out, int out_dtype, const int32_t
 // out[t, :] = round(sum over the token's routed slots j of part[t*topk + j, :])
 // for t < tokens (= *num_valid[1]), summed in fp32 in slot order. A slot is
 // routed when sorting kept its pair: expert id in [0, num_experts) and, with
-// an expert mask, mask[id] != 0. 8 elements per thread.
-template <bool kBf16>
+// an expert mask, mask[id] != 0. topk <= 32.
+// One token per workgroup (kPerWave false: each lane sums two 8-column pieces
+// of a 4096-column row in one pass) or one token per wave (kPerWave true: four
+// independent tokens per workgroup, so the short id -> mask -> row chains of
+// sparse expert-parallel rows overlap). Either way the token's valid slots
+// are checked once (lane j checks slot j; a ballot gives the bit mask) and
+// the loads of 8 slots of both pieces are in flight before any sum. Measured
+// on MI355X at MiMo dims: dense T=8192 95 us per workgroup vs 110 per wave;
+// EP share T=4096 (one routed slot in eight) 21 vs 17 us.
+template <bool kBf16, bool kPerWave>
 __global__ __launch_bounds__(256) void slot_sum_kernel(const uint16_t* __restrict__ part,
                                                        const int32_t* __restrict__ topk_ids,
                                                        const int32_t* __restrict__ mask,
@@ -155,46 +163,81 @@ __global__ __launch_bounds__(256) void slot_sum_kernel(const uint16_t* __restric
     int64_t tokens = (int64_t)num_valid[1];
     tokens = tokens < rows ? tokens : rows;
     const int c8 = cols / 8;
-    const int64_t n8 = tokens * c8;
-    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n8;
-         i += (int64_t)gridDim.x * 256) {
-        const int64_t t = i / c8;
-        const int64_t col = (i % c8) * 8;
-        float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        for (int j = 0; j < topk; ++j) {
-            const int id = topk_ids[t * topk + j];
-            if (id < 0 || id >= num_experts || (mask && mask[id] == 0)) continue;
-            const v4i v = *reinterpret_cast<const v4i*>(part + (t * topk + j) * cols + col);
+    const int lane = threadIdx.x & 63;
+    constexpr int kPer = kPerWave ? 4 : 1;              // tokens per workgroup pass
+    constexpr int kSpan = kPerWave ? 64 : 256;          // lanes that share a token
+    const int first = kPerWave ? (int)(threadIdx.x >> 6) : 0;
+    const int tl = kPerWave ? lane : (int)threadIdx.x;  // lane index within the token
+    for (int64_t t = (int64_t)blockIdx.x * kPer + first; t < tokens;
+         t += (int64_t)gridDim.x * kPer) {
+        int ok = 0;
+        if (lane < topk) {
+            const int id = topk_ids[t * topk + lane];
+            ok = id >= 0 && id < num_experts && (!mask || mask[id] != 0);
+        }
+        const uint32_t valid = (uint32_t)__builtin_amdgcn_ballot_w64(ok);
+        const uint16_t* src = part + t * topk * (int64_t)cols;
+        for (int c0 = tl; c0 < c8; c0 += 2 * kSpan) {
+            const int cc[2] = {c0, c0 + kSpan};
+            float a[2][8] = {};
+            for (int j0 = 0; j0 < topk; j0 += 8) {
+                v4i v[2][8];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                a[2 * e] += bf16_bits_to_f32((uint16_t)((uint32_t)v[e] & 0xFFFFu));
-                a[2 * e + 1] += bf16_bits_to_f32((uint16_t)((uint32_t)v[e] >> 16));
+                for (int h = 0; h < 2; ++h)
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) {
+                        const int j = j0 + u;
+                        v[h][u] = v4i{0, 0, 0, 0};
+                        if (cc[h] < c8 && j < topk && ((valid >> j) & 1u))
+                            v[h][u] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(
+                                src + (int64_t)j * cols + cc[h] * 8));
+                    }
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) {
+                        const int j = j0 + u;
+                        if (j >= topk || !((valid >> j) & 1u)) continue;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            a[h][2 * e] += bf16_bits_to_f32((uint16_t)((uint32_t)v[h][u][e] & 0xFFFFu));
+                            a[h][2 * e + 1] += bf16_bits_to_f32((uint16_t)((uint32_t)v[h][u][e] >> 16));
+                        }
+                    }
+            }
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                if (cc[h] >= c8) continue;
+                uint32_t w[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    w[e] = kBf16 ? f32_to_bf16_bits(a[h][2 * e]) |
+                                       ((uint32_t)f32_to_bf16_bits(a[h][2 * e + 1]) << 16)
+                                 : f32_to_fp16_bits(a[h][2 * e]) |
+                                       ((uint32_t)f32_to_fp16_bits(a[h][2 * e + 1]) << 16);
+                *reinterpret_cast<v4i*>(out + t * cols + cc[h] * 8) =
+                    v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
             }
         }
-        uint32_t w[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-            w[e] = kBf16 ? f32_to_bf16_bits(a[2 * e]) | ((uint32_t)f32_to_bf16_bits(a[2 * e + 1]) << 16)
-                         : f32_to_fp16_bits(a[2 * e]) | ((uint32_t)f32_to_fp16_bits(a[2 * e + 1]) << 16);
-        v4i o = {(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
-        *reinterpret_cast<v4i*>(out + t * cols + col) = o;
     }
 }
 
 void launch_slot_sum(const uint16_t* part, const int32_t* topk_ids, const int32_t* mask,
                      int64_t num_experts, const int32_t* num_valid, void* out, int out_dtype,
                      int64_t rows, int64_t topk, int64_t cols, hipStream_t stream) {
-    const int64_t n8 = rows * cols / 8;
-    if (n8 == 0) return;
-    const int blocks = (int)std::min<int64_t>(ceil_div(n8, 256), 16384);
+    if (rows == 0 || cols == 0) return;
+    // an expert mask means an expert-parallel share: most slots are not routed here
+    const bool per_wave = mask != nullptr;
+    const int blocks = (int)std::min<int64_t>(ceil_div(rows, per_wave ? 4 : 1), 8192);
+    auto go = [&](auto kern) {
+        hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), 0, stream, part, topk_ids, mask,
+                           (int)num_experts, num_valid, (uint16_t*)out, rows, (int)topk,
+                           (int)cols);
+    };
     if (out_dtype == DT_BF16)
-        hipLaunchKernelGGL(slot_sum_kernel<true>, dim3(blocks), dim3(256), 0, stream, part,
-                           topk_ids, mask, (int)num_experts, num_valid, (uint16_t*)out, rows,
-                           (int)topk, (int)cols);
+        per_wave ? go(slot_sum_kernel<true, true>) : go(slot_sum_kernel<true, false>);
     else
-        hipLaunchKernelGGL(slot_sum_kernel<false>, dim3(blocks), dim3(256), 0, stream, part,
-                           topk_ids, mask, (int)num_experts, num_valid, (uint16_t*)out, rows,
-                           (int)topk, (int)cols);
+        per_wave ? go(slot_sum_kernel<false, true>) : go(slot_sum_kernel<false, false>);
     AMD_HIP_CHECK(hipGetLastError());
 }
 
