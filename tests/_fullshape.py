@@ -74,14 +74,20 @@ def stagewise_check(cfg, device, block_ms, log=print):
     tw, ids = W.make_routing(cfg, device=device)
     w1, s1, w2, s2 = wts["w1"], wts["w1_scale"], wts["w2"], wts["w2_scale"]
     w1s, w2s = A.shuffle_weight(w1), A.shuffle_weight(w2)
-    experts = torch.unique(ids).tolist()
+    # an expert-parallel share holds global experts 0 .. local-1 (their
+    # local ids are the same); the other pairs contribute nothing and their
+    # a2 rows are never written, so the stage-1 checks skip them
+    mask = W.make_expert_mask(cfg, device=device)
+    local = cfg.local_experts or E
+    experts = [e for e in torch.unique(ids).tolist() if e < local]
     routes = {e: torch.nonzero(ids == e, as_tuple=True) for e in experts}
+    rows_l = torch.nonzero((ids < local).view(-1)).squeeze(1)
 
     # the fp8 activation quant is bit-exact with the oracle (its own tests);
     # both stage-1 paths start from the kernel's a1
     a1, a1s = A.per_group_quant_hip(x)
     a1d = deq1x128(a1, a1s)
-    y = torch.empty(T, k, 2 * I, device=device)
+    y = (torch.empty if mask is None else torch.zeros)(T, k, 2 * I, device=device)
     for e in experts:
         tok, slot = routes[e]
         y[tok, slot] = a1d[tok] @ deq(w1[e], s1[e]).T
@@ -102,15 +108,17 @@ def stagewise_check(cfg, device, block_ms, log=print):
     chain_ref = stage2_torch(a2_ref)
     for bm in block_ms:
         tag = f"{cfg.name} bm={bm}"
-        sid, sw, se, nv, _ = A.moe_sorting(ids, tw, E, H, torch.bfloat16, bm)
+        sid, sw, se, nv, _ = A.moe_sorting(ids, tw, E, H, torch.bfloat16, bm, mask)
         a2, a2s = stage1(a1, a1s, w1s, s1, sid, se, nv, k, bm, True)
         a2s = a2s.view(T * k, -1)
         a2 = a2.view(T * k, I)
-        srel = ((a2s - sc_ref).abs() / sc_ref).max().item()
         a2d = deq1x128(a2, a2s)
-        err = ((a2d - a2_ref).abs().view(T * k, -1, 128) /
-               (sc_ref.view(T * k, -1, 1) * 448)).max().item()
-        codes = (a2.view(torch.uint8) != q_ref.view(torch.uint8)).float().mean().item()
+        n_l = rows_l.numel()
+        srel = ((a2s[rows_l] - sc_ref[rows_l]).abs() / sc_ref[rows_l]).max().item()
+        err = ((a2d[rows_l] - a2_ref[rows_l]).abs().view(n_l, -1, 128) /
+               (sc_ref[rows_l].view(n_l, -1, 1) * 448)).max().item()
+        codes = (a2.view(torch.uint8)[rows_l] !=
+                 q_ref.view(torch.uint8)[rows_l]).float().mean().item()
         log(f"[{tag}] stage 1: scale rel {srel:.2e}, element err/amax {err:.4f}, "
             f"codes differing {codes:.3%}")
         assert srel <= BF16_ULP * (1 + 1e-6), srel
@@ -123,8 +131,8 @@ def stagewise_check(cfg, device, block_ms, log=print):
         log(f"[{tag}] stage 2 on the kernel's a2: max-rel {mx:.2e} rms-rel {rms:.2e}")
         assert mx <= R.MAXTOL and rms <= R.RMSTOL, (mx, rms)
 
-        out = A.fused_moe(x, w1s, w2s, tw, ids, quant_type=qt, w1_scale=s1, w2_scale=s2,
-                          block_size_M=bm).float()
+        out = A.fused_moe(x, w1s, w2s, tw, ids, expert_mask=mask, quant_type=qt, w1_scale=s1,
+                          w2_scale=s2, block_size_M=bm).float()
         ref = chain_ref.to(torch.bfloat16).float()
         far = (~torch.isclose(out, ref, rtol=0.05, atol=0.05)).float().mean().item()
         mx, rms = R.normalized_errors(ref.cpu().numpy(), out.cpu().numpy())

@@ -380,6 +380,20 @@ def test_stream_stage2_column_walk(cuda_device, monkeypatch, weights, bm, ntw):
             assert (acc1 - accc).abs().max().item() <= tol
 
 
+def test_fused_moe_mimo_decode_t128_stagewise(cuda_device):
+    """Decode T=128 at MiMo dims (the stream kernels, stage 2 walking two
+    column groups per workgroup), checked per stage."""
+    _fullshape.stagewise_check(W.mimo_decode(128), cuda_device, (16, 32))
+
+
+def test_fused_moe_ep_share_full_stagewise(cuda_device):
+    """The expert-parallel share at its benchmark shape: T=4096, 32 of 256
+    experts local, sigmoid top-8 renormalised routing, checked per stage on
+    the local pairs and end to end with the expert mask."""
+    cfg = W.mimo_ep_share(4096)
+    _fullshape.stagewise_check(cfg, cuda_device, (128, 64))
+
+
 # --------------------------------------------------------- edge cases ---
 def test_fused_moe_empty_batch(cuda_device):
     cfg = W.CONFIG_A
