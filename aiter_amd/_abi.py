@@ -47,8 +47,8 @@ _SIGNATURES = {
         c_int, [c_vp, c_int, c_i64, c_i64, c_i64, c_vp, c_vp, c_int, c_vp, c_i64, c_vp]),
     "aiter_amd_moe_stage1_fp8_blockscale": (
         c_int,
-        [c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64,
-         c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_vp],
+        [c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64,
+         c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_vp],
     ),
     "aiter_amd_moe_stage2_fp8_blockscale": (
         c_int,
@@ -57,8 +57,8 @@ _SIGNATURES = {
     ),
     "aiter_amd_moe_stage1_a8w4": (
         c_int,
-        [c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64,
-         c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_vp],
+        [c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64,
+         c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_vp],
     ),
     "aiter_amd_moe_stage2_a8w4": (
         c_int,
@@ -70,12 +70,12 @@ _SIGNATURES = {
     "aiter_amd_fused_moe_fp8_blockscale": (
         c_int,
         [c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_i64, c_i64,
-         c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp],
+         c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp],
     ),
     "aiter_amd_fused_moe_a8w4": (
         c_int,
         [c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_i64, c_i64,
-         c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp],
+         c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp],
     ),
 }
 

@@ -29,7 +29,8 @@ void launch_acc_to_out(const float*, void*, int, const int32_t*, int64_t, int64_
 void launch_moe_stage1_fp8bs(const uint8_t*, const float*, int64_t, int64_t, const uint8_t*,
                              const float*, const uint8_t*, const int32_t*, const int32_t*,
                              const int32_t*, uint8_t*, float*, int64_t, int64_t, int64_t, int64_t,
-                             int64_t, int64_t, int64_t, int, hipStream_t);
+                             int64_t, int64_t, int64_t, int, hipStream_t,
+                             const float*);
 void launch_moe_stage2_fp8bs(const uint8_t*, const float*, const uint8_t*, const float*,
                              const uint8_t*, const int32_t*, const float*, const int32_t*,
                              const int32_t*, float*, int64_t, int64_t, int64_t, int64_t, int64_t,
@@ -39,7 +40,8 @@ bool v2_supported(int64_t block_m, int64_t K);
 void launch_moe_stage1_fp8bs_v2(const uint8_t*, const float*, int64_t, int64_t, const uint8_t*,
                                 const float*, const uint8_t*, const int32_t*, const int32_t*,
                                 const int32_t*, uint8_t*, float*, int64_t, int64_t, int64_t,
-                                int64_t, int64_t, int64_t, int64_t, int, hipStream_t);
+                                int64_t, int64_t, int64_t, int64_t, int, hipStream_t,
+                             const float*);
 void launch_moe_stage2_fp8bs_v2(const uint8_t*, const float*, const uint8_t*, const float*,
                                 const uint8_t*, const int32_t*, const float*, const int32_t*,
                                 const int32_t*, float*, int64_t, int64_t, int64_t, int64_t,
@@ -50,7 +52,8 @@ bool stream_supported(int64_t block_m, int64_t K);
 void launch_moe_stage1_stream(const uint8_t*, const float*, int64_t, int64_t, const uint8_t*,
                               const float*, const uint8_t*, const int32_t*, const int32_t*,
                               const int32_t*, uint8_t*, float*, int64_t, int64_t, int64_t,
-                              int64_t, int64_t, int64_t, int64_t, int, hipStream_t);
+                              int64_t, int64_t, int64_t, int64_t, int, hipStream_t,
+                             const float*);
 void launch_moe_stage2_stream(const uint8_t*, const float*, const uint8_t*, const float*,
                               const uint8_t*, const int32_t*, const float*, const int32_t*,
                               const int32_t*, float*, int64_t, int64_t, int64_t, int64_t,
@@ -73,7 +76,8 @@ bool prefill_supported(int64_t block_m, int64_t K);
 void launch_moe_stage1_prefill(const uint8_t*, const float*, int64_t, int64_t, const uint8_t*,
                                const float*, const uint8_t*, const int32_t*, const int32_t*,
                                const int32_t*, uint8_t*, float*, int64_t, int64_t, int64_t,
-                               int64_t, int64_t, int64_t, int64_t, int, hipStream_t);
+                               int64_t, int64_t, int64_t, int64_t, int, hipStream_t,
+                             const float*);
 void launch_moe_stage2_prefill(const uint8_t*, const float*, const uint8_t*, const float*,
                                const uint8_t*, const int32_t*, const float*, const int32_t*,
                                const int32_t*, float*, uint16_t*, int64_t, int64_t, int64_t,
@@ -94,23 +98,26 @@ struct WScale {
 // tile is faster for both.  Stage 2 of all of them needs 256-column output tiles
 // (model_dim % 256 == 0); other shapes take the general kernels of
 // moe_gemm_fp8bs.hip.
+// sw: sorted routing weights for doweight_stage1 (applied to gate and up
+// before the activation), or NULL.
 static void stage1_dispatch(const uint8_t* a, const float* sa, int64_t sa_row, int64_t sa_kb,
                             const uint8_t* w1, WScale w1s, const int32_t* sid,
                             const int32_t* seid, const int32_t* nv, uint8_t* a2, float* a2s,
                             int64_t a_rows, int64_t K, int64_t I, int64_t E, int64_t topk,
-                            int64_t bm, int64_t mblocks, int sh, hipStream_t s) {
+                            int64_t bm, int64_t mblocks, int sh, hipStream_t s,
+                            const float* sw = nullptr) {
     if (stream_supported(bm, K))
         launch_moe_stage1_stream(a, sa, sa_row, sa_kb, w1, w1s.f32, w1s.e8m0, sid, seid, nv, a2,
-                                 a2s, a_rows, K, I, E, topk, bm, mblocks, sh, s);
+                                 a2s, a_rows, K, I, E, topk, bm, mblocks, sh, s, sw);
     else if (prefill_supported(bm, K) && !w1s.e8m0)
         launch_moe_stage1_prefill(a, sa, sa_row, sa_kb, w1, w1s.f32, w1s.e8m0, sid, seid, nv, a2,
-                                  a2s, a_rows, K, I, E, topk, bm, mblocks, sh, s);
+                                  a2s, a_rows, K, I, E, topk, bm, mblocks, sh, s, sw);
     else if (v2_supported(bm, K))
         launch_moe_stage1_fp8bs_v2(a, sa, sa_row, sa_kb, w1, w1s.f32, w1s.e8m0, sid, seid, nv, a2,
-                                   a2s, a_rows, K, I, E, topk, bm, mblocks, sh, s);
+                                   a2s, a_rows, K, I, E, topk, bm, mblocks, sh, s, sw);
     else
         launch_moe_stage1_fp8bs(a, sa, sa_row, sa_kb, w1, w1s.f32, w1s.e8m0, sid, seid, nv, a2,
-                                a2s, a_rows, K, I, E, topk, bm, mblocks, sh, s);
+                                a2s, a_rows, K, I, E, topk, bm, mblocks, sh, s, sw);
 }
 
 // Stage 2 runs on the prefill kernel for this shape (the only stage-2
@@ -245,7 +252,8 @@ void check_e8m0(const uint8_t* p, const char* name) {
 
 void stage1_entry(const void* a1, const float* a1_scale, int64_t a1_scale_transposed,
                   const void* w1, WScale w1s, const int32_t* sorted_ids,
-                  const int32_t* sorted_expert_ids, const int32_t* num_valid_ids, void* a2,
+                  const float* sorted_weights, const int32_t* sorted_expert_ids,
+                  const int32_t* num_valid_ids, void* a2,
                   float* a2_scale, int64_t tokens, int64_t model_dim, int64_t inter_dim,
                   int64_t num_experts, int64_t topk, int64_t block_m, int64_t max_m_blocks,
                   int64_t activation, int64_t w_shuffled, void* stream) {
@@ -267,7 +275,7 @@ void stage1_entry(const void* a1, const float* a1_scale, int64_t a1_scale_transp
     stage1_dispatch((const uint8_t*)a1, a1_scale, sa_row, sa_kb, (const uint8_t*)w1, w1s,
                     sorted_ids, sorted_expert_ids, num_valid_ids, (uint8_t*)a2, a2_scale, tokens,
                     model_dim, inter_dim, num_experts, topk, block_m, max_m_blocks,
-                    (int)(w_shuffled != 0), (hipStream_t)stream);
+                    (int)(w_shuffled != 0), (hipStream_t)stream, sorted_weights);
 }
 
 void stage2_entry(const void* a2, const float* a2_scale, const void* w2, WScale w2s,
@@ -284,7 +292,8 @@ void stage2_entry(const void* a2, const float* a2_scale, const void* w2, WScale 
     check_ptr(a2, "a2");
     check_ptr(w2, "w2");
     check_ptr(out_acc, "out_acc");
-    AMD_CHECK(a2_scale && sorted_ids && sorted_weights && sorted_expert_ids && num_valid_ids,
+    // sorted_weights NULL: unit weights (the routing weights went into stage 1)
+    AMD_CHECK(a2_scale && sorted_ids && sorted_expert_ids && num_valid_ids,
               "a required pointer is NULL");
     stage2_dispatch((const uint8_t*)a2, a2_scale, (const uint8_t*)w2, w2s, sorted_ids,
                     sorted_weights, sorted_expert_ids, num_valid_ids, out_acc, tokens * topk,
@@ -297,7 +306,8 @@ void fused_entry(const void* hidden_states, int hidden_dtype, const void* w1, WS
                  const int32_t* expert_mask, const int32_t* num_local_tokens, void* out,
                  int out_dtype, int64_t tokens, int64_t model_dim, int64_t inter_dim,
                  int64_t num_experts, int64_t global_experts, int64_t topk, int64_t block_m,
-                 int64_t w_shuffled, void* workspace, int64_t workspace_bytes, void* stream) {
+                 int64_t doweight_stage1, int64_t w_shuffled, void* workspace,
+                 int64_t workspace_bytes, void* stream) {
     check_dims(model_dim, inter_dim);
     check_topk_experts(tokens, topk, num_experts);
     AMD_CHECK(hidden_dtype == DT_BF16 || hidden_dtype == DT_FP16,
@@ -340,10 +350,13 @@ void fused_entry(const void* hidden_states, int hidden_dtype, const void* w1, WS
     launch_per_group_quant_fp8(hidden_states, hidden_dtype, a1, a1_scale, tokens, model_dim, 0,
                                num_local_tokens, 1, s);
     const int sh = (int)(w_shuffled != 0);
+    // doweight_stage1: the routing weights scale stage 1's gate and up, stage 2 sums unweighted
+    const bool dw = doweight_stage1 != 0;
     stage1_dispatch(a1, a1_scale, model_dim / 128, 1, (const uint8_t*)w1, w1s, sorted_ids,
                     sorted_eids, num_valid, a2, a2_scale, tokens, model_dim, inter_dim,
-                    num_experts, topk, block_m, L.blocks, sh, s);
-    stage2_dispatch(a2, a2_scale, (const uint8_t*)w2, w2s, sorted_ids, sorted_w, sorted_eids,
+                    num_experts, topk, block_m, L.blocks, sh, s, dw ? sorted_w : nullptr);
+    stage2_dispatch(a2, a2_scale, (const uint8_t*)w2, w2s, sorted_ids, dw ? nullptr : sorted_w,
+                    sorted_eids,
                     num_valid, part ? nullptr : acc, tokens * topk, inter_dim, model_dim,
                     num_experts, topk, block_m, L.blocks, sh, s, part,
                     tokens * topk * num_experts / E_sort);
@@ -439,6 +452,7 @@ int aiter_amd_dynamic_per_group_quant_fp8(const void* input, int input_dtype, in
 int aiter_amd_moe_stage1_fp8_blockscale(const void* a1, const float* a1_scale,
                                         int64_t a1_scale_transposed, const void* w1,
                                         const float* w1_scale, const int32_t* sorted_ids,
+                                        const float* sorted_weights,
                                         const int32_t* sorted_expert_ids,
                                         const int32_t* num_valid_ids, void* a2, float* a2_scale,
                                         int64_t tokens, int64_t model_dim, int64_t inter_dim,
@@ -448,6 +462,7 @@ int aiter_amd_moe_stage1_fp8_blockscale(const void* a1, const float* a1_scale,
     return safe_call([&] {
         AMD_CHECK(w1_scale != nullptr, "w1_scale is NULL");
         stage1_entry(a1, a1_scale, a1_scale_transposed, w1, WScale{w1_scale, nullptr}, sorted_ids,
+                     sorted_weights,
                      sorted_expert_ids, num_valid_ids, a2, a2_scale, tokens, model_dim, inter_dim,
                      num_experts, topk, block_m, max_m_blocks, activation, w_shuffled, stream);
     });
@@ -455,7 +470,8 @@ int aiter_amd_moe_stage1_fp8_blockscale(const void* a1, const float* a1_scale,
 
 int aiter_amd_moe_stage1_a8w4(const void* a1, const float* a1_scale, int64_t a1_scale_transposed,
                               const void* w1, const uint8_t* w1_scale,
-                              const int32_t* sorted_ids, const int32_t* sorted_expert_ids,
+                              const int32_t* sorted_ids,
+                                        const float* sorted_weights, const int32_t* sorted_expert_ids,
                               const int32_t* num_valid_ids, void* a2, float* a2_scale,
                               int64_t tokens, int64_t model_dim, int64_t inter_dim,
                               int64_t num_experts, int64_t topk, int64_t block_m,
@@ -464,6 +480,7 @@ int aiter_amd_moe_stage1_a8w4(const void* a1, const float* a1_scale, int64_t a1_
     return safe_call([&] {
         check_e8m0(w1_scale, "w1_scale");
         stage1_entry(a1, a1_scale, a1_scale_transposed, w1, WScale{nullptr, w1_scale}, sorted_ids,
+                     sorted_weights,
                      sorted_expert_ids, num_valid_ids, a2, a2_scale, tokens, model_dim, inter_dim,
                      num_experts, topk, block_m, max_m_blocks, activation, w_shuffled, stream);
     });
@@ -530,14 +547,15 @@ int aiter_amd_fused_moe_fp8_blockscale(const void* hidden_states, int hidden_dty
                                        const int32_t* num_local_tokens, void* out, int out_dtype,
                                        int64_t tokens, int64_t model_dim, int64_t inter_dim,
                                        int64_t num_experts, int64_t global_experts, int64_t topk,
-                                       int64_t block_m, int64_t w_shuffled, void* workspace,
+                                       int64_t block_m, int64_t doweight_stage1, int64_t w_shuffled, void* workspace,
                                        int64_t workspace_bytes, void* stream) {
     return safe_call([&] {
         AMD_CHECK(w1_scale && w2_scale, "a required pointer is NULL");
         fused_entry(hidden_states, hidden_dtype, w1, WScale{w1_scale, nullptr}, w2,
                     WScale{w2_scale, nullptr}, topk_weights, topk_ids, expert_mask,
                     num_local_tokens, out, out_dtype, tokens, model_dim, inter_dim, num_experts,
-                    global_experts, topk, block_m, w_shuffled, workspace, workspace_bytes, stream);
+                    global_experts, topk, block_m, doweight_stage1, w_shuffled, workspace,
+                    workspace_bytes, stream);
     });
 }
 
@@ -547,7 +565,7 @@ int aiter_amd_fused_moe_a8w4(const void* hidden_states, int hidden_dtype, const 
                              const int32_t* expert_mask, const int32_t* num_local_tokens,
                              void* out, int out_dtype, int64_t tokens, int64_t model_dim,
                              int64_t inter_dim, int64_t num_experts, int64_t global_experts,
-                             int64_t topk, int64_t block_m, int64_t w_shuffled, void* workspace,
+                             int64_t topk, int64_t block_m, int64_t doweight_stage1, int64_t w_shuffled, void* workspace,
                              int64_t workspace_bytes, void* stream) {
     return safe_call([&] {
         check_e8m0(w1_scale, "w1_scale");
@@ -555,7 +573,8 @@ int aiter_amd_fused_moe_a8w4(const void* hidden_states, int hidden_dtype, const 
         fused_entry(hidden_states, hidden_dtype, w1, WScale{nullptr, w1_scale}, w2,
                     WScale{nullptr, w2_scale}, topk_weights, topk_ids, expert_mask,
                     num_local_tokens, out, out_dtype, tokens, model_dim, inter_dim, num_experts,
-                    global_experts, topk, block_m, w_shuffled, workspace, workspace_bytes, stream);
+                    global_experts, topk, block_m, doweight_stage1, w_shuffled, workspace,
+                    workspace_bytes, stream);
     });
 }
 

@@ -117,7 +117,9 @@ __global__ __launch_bounds__(kGemmThreads) void moe_gemm_fp8bs_kernel(GemmArgs g
         }
         s_arow[r] = arow;
         s_orow[r] = orow;
-        s_w[r] = STAGE == 2 && valid ? g.sorted_w[mb * BM + r] : 0.0f;
+        // routing weight of the pair (1 when none is passed: stage 2 without
+        // weights, or stage 1 without doweight); stage 1 applies it only when given
+        s_w[r] = valid ? (g.sorted_w ? g.sorted_w[mb * BM + r] : 1.0f) : 0.0f;
     }
     __syncthreads();
 
@@ -313,8 +315,12 @@ __global__ __launch_bounds__(kGemmThreads) void moe_gemm_fp8bs_kernel(GemmArgs g
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int v = 0; v < 4; ++v)
-                h[rt][j][v] = bf16_round(silu_f32(acc[rt][j][v]) * acc[rt][2 + j][v]);
+            for (int v = 0; v < 4; ++v) {
+                // doweight_stage1: the pair's weight scales gate and up before the
+                // activation (aiter/fused_moe.py:1568-1571)
+                const float wg = g.sorted_w ? s_w[rt * 16 + 4 * lq + v] : 1.0f;
+                h[rt][j][v] = bf16_round(silu_f32(acc[rt][j][v] * wg) * (acc[rt][2 + j][v] * wg));
+            }
 #pragma unroll
     for (int rt = 0; rt < NRT; ++rt)
 #pragma unroll
@@ -400,8 +406,9 @@ void launch_moe_stage1_fp8bs(const uint8_t* a, const float* a_scale, int64_t sa_
                              const int32_t* num_valid, uint8_t* a2, float* a2_scale,
                              int64_t a_rows, int64_t K, int64_t inter, int64_t E, int64_t topk,
                              int64_t block_m, int64_t max_m_blocks, int shuffled,
-                             hipStream_t stream) {
+                             hipStream_t stream, const float* sorted_w) {
     GemmArgs g{};
+    g.sorted_w = sorted_w;                 // doweight_stage1 (or NULL)
     g.a = a;
     g.a_scale = a_scale;
     g.sa_row = sa_row;
@@ -410,7 +417,6 @@ void launch_moe_stage1_fp8bs(const uint8_t* a, const float* a_scale, int64_t sa_
     g.w_scale = w1_scale;
     g.w_scale8 = w1_scale_e8m0;
     g.sorted_ids = sorted_ids;
-    g.sorted_w = nullptr;
     g.sorted_eids = sorted_eids;
     g.num_valid = num_valid;
     g.a2 = a2;

@@ -227,7 +227,9 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
         }
         s_arow[r] = (int32_t)arow;
         s_orow[r] = orow;
-        s_w[r] = STAGE == 2 && valid ? g.sorted_w[srow0 + r] : 0.0f;
+        // routing weight of the pair (1 when none is passed: stage 2 without
+        // weights, or stage 1 without doweight); stage 1 applies it only when given
+        s_w[r] = valid ? (g.sorted_w ? g.sorted_w[srow0 + r] : 1.0f) : 0.0f;
         any_valid |= (int)valid;
     }
     // a tile whose rows are all padding (the end of an expert's last
@@ -527,8 +529,14 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
 #pragma unroll
             for (int j = 0; j < NH1; ++j)
 #pragma unroll
-                for (int v = 0; v < 4; ++v)
-                    h[rt][j][v] = bf16_round(silu_f32(acc[rt][j][v]) * acc[rt][NH1 + j][v]);
+                for (int v = 0; v < 4; ++v) {
+                    // doweight_stage1: the pair's weight scales gate and up before the
+                    // activation (aiter/fused_moe.py:1568-1571)
+                    const float wg = g.sorted_w ? s_w[row_base + rt * 16 + (TR ? lr : 4 * lq + v)]
+                                                : 1.0f;
+                    h[rt][j][v] = bf16_round(silu_f32(acc[rt][j][v] * wg) *
+                                             (acc[rt][NH1 + j][v] * wg));
+                }
         if constexpr (TR) {
 #pragma unroll
             for (int rt = 0; rt < NRT; ++rt) {
@@ -750,8 +758,9 @@ void launch_moe_stage1_prefill(const uint8_t* a, const float* a_scale, int64_t s
                                const int32_t* sorted_eids, const int32_t* num_valid,
                                uint8_t* a2, float* a2_scale, int64_t a_rows, int64_t K,
                                int64_t inter, int64_t E, int64_t topk, int64_t block_m,
-                               int64_t max_m_blocks, int shuffled, hipStream_t stream) {
+                               int64_t max_m_blocks, int shuffled, hipStream_t stream, const float* sorted_w) {
     pf::Args g{};
+    g.sorted_w = sorted_w;                 // doweight_stage1 (or NULL)
     g.a = a;
     g.a_scale = a_scale;
     g.sa_row = sa_row;

@@ -79,10 +79,15 @@ int aiter_amd_dynamic_per_group_quant_fp8(const void* input, int input_dtype, in
  *   w1 [E, 2*inter_dim, model_dim] fp8, w1_scale [E, 2*inter_dim/128, model_dim/128]
  *   a2 [tokens, topk, inter_dim] fp8, a2_scale [tokens, topk, inter_dim/128]
  *   activation must be 0 (Silu); w_shuffled: 1 for the (16,16) layout.
+ *   sorted_weights: NULL, or the sorted routing weights for doweight_stage1
+ *   (they scale gate and up before the activation, aiter/fused_moe.py:
+ *   1568-1571; fused_moe_2stages passes them to stage 1 and none to stage 2,
+ *   fused_moe.py:1253, 1330).
  *   block_m in {16, 32, 64, 128}; max_m_blocks = capacity of sorted_expert_ids. */
 int aiter_amd_moe_stage1_fp8_blockscale(const void* a1, const float* a1_scale,
                                         int64_t a1_scale_transposed, const void* w1,
                                         const float* w1_scale, const int32_t* sorted_ids,
+                                        const float* sorted_weights,
                                         const int32_t* sorted_expert_ids,
                                         const int32_t* num_valid_ids, void* a2, float* a2_scale,
                                         int64_t tokens, int64_t model_dim, int64_t inter_dim,
@@ -94,7 +99,8 @@ int aiter_amd_moe_stage1_fp8_blockscale(const void* a1, const float* a1_scale,
  *   a2 [tokens, topk, inter_dim] fp8 + a2_scale [tokens, topk, inter_dim/128]
  *   w2 [E, model_dim, inter_dim] fp8, w2_scale [E, model_dim/128, inter_dim/128]
  *   out_acc [tokens, model_dim] f32 accumulates sorted_weight * row (it must
- *   be zeroed first, e.g. by aiter_amd_moe_sorting_fwd's moe_buf). */
+ *   be zeroed first, e.g. by aiter_amd_moe_sorting_fwd's moe_buf);
+ *   sorted_weights NULL: unit weights (doweight_stage1 applied them). */
 int aiter_amd_moe_stage2_fp8_blockscale(const void* a2, const float* a2_scale, const void* w2,
                                         const float* w2_scale, const int32_t* sorted_ids,
                                         const float* sorted_weights,
@@ -116,7 +122,8 @@ int aiter_amd_moe_stage2_fp8_blockscale(const void* a2, const float* a2_scale, c
  *   Everything else as aiter_amd_moe_stage1_fp8_blockscale. */
 int aiter_amd_moe_stage1_a8w4(const void* a1, const float* a1_scale, int64_t a1_scale_transposed,
                               const void* w1, const uint8_t* w1_scale,
-                              const int32_t* sorted_ids, const int32_t* sorted_expert_ids,
+                              const int32_t* sorted_ids, const float* sorted_weights,
+                              const int32_t* sorted_expert_ids,
                               const int32_t* num_valid_ids, void* a2, float* a2_scale,
                               int64_t tokens, int64_t model_dim, int64_t inter_dim,
                               int64_t num_experts, int64_t topk, int64_t block_m,
@@ -166,8 +173,8 @@ int aiter_amd_fused_moe_fp8_blockscale(const void* hidden_states, int hidden_dty
                                        int out_dtype, int64_t tokens, int64_t model_dim,
                                        int64_t inter_dim, int64_t num_experts,
                                        int64_t global_experts, int64_t topk, int64_t block_m,
-                                       int64_t w_shuffled, void* workspace,
-                                       int64_t workspace_bytes, void* stream);
+                                       int64_t doweight_stage1, int64_t w_shuffled,
+                                       void* workspace, int64_t workspace_bytes, void* stream);
 
 /* The whole 2-stage A8W4 MoE in one call: fused_moe_ with quant_type per_1x32
  * and fp4x2 weights (aiter/fused_moe.py:255-275, 1103-1334), fp8 1x128
@@ -179,8 +186,9 @@ int aiter_amd_fused_moe_a8w4(const void* hidden_states, int hidden_dtype, const 
                              const int32_t* expert_mask, const int32_t* num_local_tokens,
                              void* out, int out_dtype, int64_t tokens, int64_t model_dim,
                              int64_t inter_dim, int64_t num_experts, int64_t global_experts,
-                             int64_t topk, int64_t block_m, int64_t w_shuffled, void* workspace,
-                             int64_t workspace_bytes, void* stream);
+                             int64_t topk, int64_t block_m, int64_t doweight_stage1,
+                             int64_t w_shuffled, void* workspace, int64_t workspace_bytes,
+                             void* stream);
 
 /* ---- routing: top-k experts per token from the router logits ----
  * gating [tokens, num_experts] fp32/bf16/fp16 (dtype code as above),

@@ -325,12 +325,14 @@ def local_expert_ids(topk_ids: np.ndarray, expert_mask=None) -> np.ndarray:
     return lut[np.asarray(topk_ids, dtype=np.int64)]
 
 
-def moe_stage1_ref(a1: np.ndarray, w1: np.ndarray, topk_ids_local: np.ndarray) -> np.ndarray:
+def moe_stage1_ref(a1: np.ndarray, w1: np.ndarray, topk_ids_local: np.ndarray,
+                   topk_w: np.ndarray = None) -> np.ndarray:
     """torch_moe_stage1 with per_1x128 (aiter/fused_moe.py:1483-1585), given
     already-dequantised fp32 a1 [T, H] and w1 [E, 2I, H]:
     out[t, j] = silu(g) * u with [g, u] = a1[t] @ w1[e_tj]^T, fp32, then bf16.
-    Rows whose expert is not local stay 0.  Returns fp32 holding bf16 values
-    [T, topk, I]."""
+    topk_w given (doweight): [g, u] are first scaled by w[t, j]
+    (fused_moe.py:1568-1571).  Rows whose expert is not local stay 0.
+    Returns fp32 holding bf16 values [T, topk, I]."""
     T, _ = a1.shape
     topk = topk_ids_local.shape[1]
     E, N1, _ = w1.shape
@@ -341,6 +343,8 @@ def moe_stage1_ref(a1: np.ndarray, w1: np.ndarray, topk_ids_local: np.ndarray) -
         if mask.any():
             tok, slot = np.nonzero(mask)
             out[tok, slot] = a1[tok] @ w1[e].T
+            if topk_w is not None:
+                out[tok, slot] *= np.asarray(topk_w, np.float32)[tok, slot][:, None]
     h = silu(out[..., :inter]) * out[..., inter:]
     return bf16_round(h)
 
@@ -349,7 +353,8 @@ def moe_stage2_ref(a2: np.ndarray, w2: np.ndarray, topk_ids_local: np.ndarray,
                    topk_w: np.ndarray) -> np.ndarray:
     """torch_moe_stage2 with per_1x128 (aiter/fused_moe.py:1588-1666), given
     dequantised fp32 a2 [T, topk, I] and w2 [E, H, I]: sum over slots of
-    w[t, j] * a2[t, j] @ w2[e]^T in fp32, then bf16.  Returns fp32 [T, H]."""
+    w[t, j] * a2[t, j] @ w2[e]^T in fp32, then bf16 (topk_w None: w = 1, the
+    doweight=False branch, 1664-1666).  Returns fp32 [T, H]."""
     T, topk, _ = a2.shape
     E, H, _ = w2.shape
     out = np.zeros((T, topk, H), dtype=np.float32)
@@ -358,13 +363,14 @@ def moe_stage2_ref(a2: np.ndarray, w2: np.ndarray, topk_ids_local: np.ndarray,
         if mask.any():
             tok, slot = np.nonzero(mask)
             out[tok, slot] = a2[tok, slot] @ w2[e].T
-    out = out * np.asarray(topk_w, np.float32)[..., None]
+    if topk_w is not None:
+        out = out * np.asarray(topk_w, np.float32)[..., None]
     return bf16_round(out.sum(axis=1, dtype=np.float32))
 
 
 def fused_moe_ref(x_bf16: np.ndarray, w1q, w1s, w2q, w2s, topk_ids, topk_w,
                   expert_mask=None, num_local_tokens=None, act_quant="kernel",
-                  weight_format="fp8_128x128"):
+                  weight_format="fp8_128x128", doweight_stage1=False):
     """The whole 2-stage FP8 blockscale layer as the reference's fused_moe
     computes it (aiter/fused_moe.py:1103-1334 with the oracles of
     op_tests/test_moe_2stage.py:187-231): 1x128 quant of x, stage 1 with
@@ -375,6 +381,8 @@ def fused_moe_ref(x_bf16: np.ndarray, w1q, w1s, w2q, w2s, topk_ids, topk_w,
     with packed e2m1 weights [E, N, K/2] and e8m0 scales [E, N, K/32]
     dequantised as in torch_moe_stage1/2's per_1x32 weight branch
     (aiter/fused_moe.py:1539-1553, 1635-1649).
+    doweight_stage1: the routing weights go to stage 1 and stage 2 sums
+    unweighted (fused_moe.py:1253, 1330).
     Returns dict with out [T, H] (fp32 of bf16 values) and intermediates."""
     deq = dequant_weight_mxfp4 if weight_format == "mxfp4" else dequant_weight_128x128
     q = quant_1x128_kernel if act_quant == "kernel" else pertoken_quant_torch_semantics
@@ -386,13 +394,13 @@ def fused_moe_ref(x_bf16: np.ndarray, w1q, w1s, w2q, w2s, topk_ids, topk_w,
     a1q, a1s = q(x)
     a1 = dequant_1x128(a1q, a1s)
     w1 = deq(w1q, w1s)
-    h = moe_stage1_ref(a1, w1, ids_local)
+    h = moe_stage1_ref(a1, w1, ids_local, topk_w if doweight_stage1 else None)
     topk = h.shape[1]
     inter = h.shape[2]
     a2q, a2s = q(h.reshape(T * topk, inter))
     a2 = dequant_1x128(a2q, a2s).reshape(T, topk, inter)
     w2 = deq(w2q, w2s)
-    out = moe_stage2_ref(a2, w2, ids_local, topk_w)
+    out = moe_stage2_ref(a2, w2, ids_local, None if doweight_stage1 else topk_w)
     return {"out": out, "a1q": a1q, "a1s": a1s, "h": h, "a2q": a2q.reshape(T, topk, inter),
             "a2s": a2s.reshape(T, topk, inter // 128), "ids_local": ids_local}
 

@@ -78,7 +78,9 @@ def test_quant_validation_errors():
 
 
 def test_stage_validation_errors():
-    args = [16, 16, 0, 16, 16, 16, 16, 16, 16, 16]
+    # a1, a1_scale, transposed, w1, w1_scale, sorted_ids, sorted_weights (NULL: no
+    # doweight_stage1), sorted_expert_ids, num_valid_ids, a2, a2_scale
+    args = [16, 16, 0, 16, 16, 16, None, 16, 16, 16, 16]
     _expect_error("aiter_amd_moe_stage1_fp8_blockscale", *args, 4, 4096, 2000, 8, 2, 32, 10, 0, 1,
                   None, match="inter_dim must be")
     _expect_error("aiter_amd_moe_stage1_fp8_blockscale", *args, 4, 4096, 2048, 8, 2, 256, 10, 0,
@@ -94,11 +96,13 @@ def test_stage_validation_errors():
 
 def test_fused_validation_errors(lib):
     base = [16, 3, 16, 16, 16, 16, 16, 16, None, None, 16, 3]
-    _expect_error("aiter_amd_fused_moe_fp8_blockscale", *base, 4, 4096, 2048, 8, 8, 2, 0, 1, 16,
-                  10, None, match="workspace of")
+    # ... tokens, model_dim, inter_dim, E, global E, topk, block_m, doweight_stage1,
+    # w_shuffled, workspace, workspace_bytes, stream
+    _expect_error("aiter_amd_fused_moe_fp8_blockscale", *base, 4, 4096, 2048, 8, 8, 2, 0, 0, 1,
+                  16, 10, None, match="workspace of")
     masked = [16, 3, 16, 16, 16, 16, 16, 16, 16, None, 16, 3]    # expert_mask given
-    _expect_error("aiter_amd_fused_moe_fp8_blockscale", *masked, 4, 4096, 2048, 8, 4, 2, 0, 1,
-                  16, 10**9, None, match="global_experts")
+    _expect_error("aiter_amd_fused_moe_fp8_blockscale", *masked, 4, 4096, 2048, 8, 4, 2, 0, 0,
+                  1, 16, 10**9, None, match="global_experts")
     ws = lib.aiter_amd_fused_moe_workspace_bytes(8192, 4096, 2048, 256, 8, 64)
     # sorted ids/weights + a1 + a2 + f32 accumulator dominate
     assert ws > 8192 * 4096 * (1 + 4) + 8192 * 8 * 2048
@@ -131,8 +135,8 @@ def test_python_layer_rejects_unsupported_modes():
     with pytest.raises(NotImplementedError, match="activation"):
         fused_moe(x, w1, w2, tw, ids, quant_type=QuantType.per_128x128,
                   activation=ActivationType.Gelu, w1_scale=s1, w2_scale=s2)
-    with pytest.raises(NotImplementedError, match="doweight_stage1"):
-        fused_moe(x, w1, w2, tw, ids, quant_type=QuantType.per_128x128, doweight_stage1=True,
+    with pytest.raises(NotImplementedError, match="bias"):
+        fused_moe(x, w1, w2, tw, ids, quant_type=QuantType.per_128x128, bias1=torch.zeros(2, 256),
                   w1_scale=s1, w2_scale=s2)
     with pytest.raises(ValueError, match="w1_scale"):
         fused_moe(x, w1, w2, tw, ids, quant_type=QuantType.per_128x128)
@@ -190,13 +194,13 @@ def test_torch_mxfp4_quant_matches_oracle():
 
 def test_a8w4_validation_errors():
     args = [16, 16, 0, 16]
-    tail = [16, 16, 16, 16, 16, 4, 4096, 2048, 8, 2, 32, 10, 0, 1, None]
+    tail = [16, None, 16, 16, 16, 16, 4, 4096, 2048, 8, 2, 32, 10, 0, 1, None]
     _expect_error("aiter_amd_moe_stage1_a8w4", *args, None, *tail, match="w1_scale is NULL")
     _expect_error("aiter_amd_moe_stage1_a8w4", *args, 18, *tail, match="4-byte aligned")
     _expect_error("aiter_amd_moe_stage2_a8w4", 16, 16, 16, None, 16, 16, 16, 16, 16, 4, 4096,
                   2048, 8, 2, 32, 10, 1, None, match="w2_scale is NULL")
     base = [16, 3, 16, 16, 16, None, 16, 16, None, None, 16, 3]
-    _expect_error("aiter_amd_fused_moe_a8w4", *base, 4, 4096, 2048, 8, 8, 2, 0, 1, 16, 10,
+    _expect_error("aiter_amd_fused_moe_a8w4", *base, 4, 4096, 2048, 8, 8, 2, 0, 0, 1, 16, 10,
                   None, match="w2_scale is NULL")
 
 

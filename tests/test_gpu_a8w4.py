@@ -32,14 +32,15 @@ def _a8w4(cfg):
     return dataclasses.replace(cfg, weights="mxfp4")
 
 
-def _make_layer(cfg, device, shuffle):
+def _make_layer(cfg, device, shuffle, doweight=False):
     wts = W.make_weights(cfg, device="cpu", shuffle=False)
     x = W.make_hidden(cfg)
     tw, ids = W.make_routing(cfg)
     mask = W.make_expert_mask(cfg)
     ref = R.fused_moe_ref(x.float().numpy(), wts["w1"].numpy(), wts["w1_scale"].numpy(),
                           wts["w2"].numpy(), wts["w2_scale"].numpy(), ids.numpy(), tw.numpy(),
-                          None if mask is None else mask.numpy(), weight_format="mxfp4")
+                          None if mask is None else mask.numpy(), weight_format="mxfp4",
+                          doweight_stage1=doweight)
     w1, w2 = wts["w1"], wts["w2"]
     if shuffle:
         w1, w2 = A.shuffle_weight(w1), A.shuffle_weight(w2)
@@ -72,6 +73,17 @@ def test_a8w4_config_a(cuda_device, shuffle, bm):
     out = _run(dev, block_size_M=bm)
     assert out.dtype == torch.bfloat16 and out.shape == (cfg.tokens, cfg.model_dim)
     _check(ref["out"], _np(out.float()), f"A8W4 A shuffle={shuffle} bm={bm}")
+
+
+@pytest.mark.parametrize("bm", [16, 64, 128])
+def test_a8w4_doweight_stage1(cuda_device, bm):
+    """doweight_stage1 on the A8W4 layer: the stream (bm 16) and direct-to-LDS
+    (bm 64/128) stage-1 kernels, stage 2 unweighted (the prefill kernel's
+    per-pair rows at bm 128)."""
+    cfg = _a8w4(W.CONFIG_A)
+    dev, ref = _make_layer(cfg, cuda_device, True, doweight=True)
+    out = _run(dev, block_size_M=bm, doweight_stage1=True)
+    _check(ref["out"], _np(out.float()), f"A8W4 doweight_stage1 bm={bm}")
 
 
 def test_a8w4_torch_dtypes_match_byte_views(cuda_device):

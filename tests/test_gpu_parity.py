@@ -105,7 +105,7 @@ def test_act_quant_num_rows(cuda_device):
 
 
 # ------------------------------------------------------ fused MoE layer ---
-def _make_layer(cfg, device, shuffle):
+def _make_layer(cfg, device, shuffle, doweight=False):
     wts = W.make_weights(cfg, device="cpu", shuffle=False)
     x = W.make_hidden(cfg)
     tw, ids = W.make_routing(cfg)
@@ -114,7 +114,7 @@ def _make_layer(cfg, device, shuffle):
     w2u = wts["w2"].view(torch.uint8).numpy()
     ref = R.fused_moe_ref(x.float().numpy(), w1u, wts["w1_scale"].numpy(), w2u,
                           wts["w2_scale"].numpy(), ids.numpy(), tw.numpy(),
-                          None if mask is None else mask.numpy())
+                          None if mask is None else mask.numpy(), doweight_stage1=doweight)
     w1, w2 = wts["w1"], wts["w2"]
     if shuffle:
         w1, w2 = A.shuffle_weight(w1), A.shuffle_weight(w2)
@@ -189,6 +189,62 @@ def test_fused_moe_fp8_input_path(cuda_device):
                       quant_type=A.QuantType.per_128x128, w1_scale=dev["s1"], w2_scale=dev["s2"],
                       a1_scale=a1s, dtype=torch.bfloat16)
     _check(ref["out"], _np(out.float()), "fp8 input")
+
+
+@pytest.mark.parametrize("bm", [16, 32, 64, 128])
+def test_fused_moe_doweight_stage1(cuda_device, bm):
+    """doweight_stage1: the routing weight scales gate and up before SiLU
+    and stage 2 sums unweighted (aiter/fused_moe.py:1253, 1330, 1568-1571),
+    on the stream (bm 16/32) and prefill (bm 64/128) stage-1 kernels; at bm 32
+    also on the stage-wise fp8-input path. The layer with weights after the
+    activation differs from it by far more than the tolerance."""
+    cfg = W.CONFIG_A
+    dev, ref = _make_layer(cfg, cuda_device, True, doweight=True)
+    out = _np(_run(dev, block_size_M=bm, doweight_stage1=True).float())
+    _check(ref["out"], out, f"doweight_stage1 bm={bm}")
+    _, ref_late = _make_layer(cfg, cuda_device, True)
+    assert R.normalized_errors(ref_late["out"], out)[0] > 10 * MAXTOL
+    if bm == 32:
+        a1, a1s = A.per_group_quant_hip(dev["x"])
+        out8 = A.fused_moe(a1, dev["w1"], dev["w2"], dev["tw"], dev["ids"],
+                           quant_type=A.QuantType.per_128x128, w1_scale=dev["s1"],
+                           w2_scale=dev["s2"], a1_scale=a1s, dtype=torch.bfloat16,
+                           block_size_M=bm, doweight_stage1=True)
+        _check(ref["out"], _np(out8.float()), "doweight_stage1 fp8 input")
+
+
+@pytest.mark.parametrize("bm", [32, 128])
+def test_fused_moe_doweight_stage1_ep_share(cuda_device, bm):
+    """doweight_stage1 with an expert mask (stream kernels at bm 32, the
+    prefill kernels with per-pair stage-2 rows at bm 128). Weighting gate and
+    up before SiLU shrinks a2 by about w^2 while the output keeps the
+    unweighted sum, so one one-step fp8 requant flip of a2 moves a small
+    output by more than the end-to-end max-rel bar; the check is therefore
+    per stage, as for the full-size layers: stage 1's fp8 codes on the local
+    pairs against the oracle's (at most 1% different, each within one
+    top-binade e4m3 step of its group, 32/448 of the group amax), then
+    the reference's own end-to-end bar (allclose rtol = atol = 0.05 on at
+    least 95% of the outputs, op_tests/test_moe_blockscale.py:288) and
+    RMS-rel <= 4e-3."""
+    cfg = W.MoEConfig("ep_dw", 96, 512, 512, 16, 4, routing="sigmoid", local_experts=4, seed=4)
+    dev, ref = _make_layer(cfg, cuda_device, True, doweight=True)
+    a1, a1s = A.per_group_quant_hip(dev["x"])
+    sid, sw, se, nv, _ = A.moe_sorting(dev["ids"], dev["tw"], cfg.experts, cfg.model_dim,
+                                        torch.float32, bm, dev["mask"])
+    a2, _ = A.moe_stage1_fp8_blockscale(a1, a1s, dev["w1"], dev["s1"], sid, se, nv, cfg.topk, bm,
+                                        True, sorted_weights=sw)
+    loc = ref["ids_local"] >= 0
+    got = _np(a2.view(torch.uint8))[loc]
+    exp = ref["a2q"][loc]
+    assert (got != exp).mean() <= 0.01
+    # in the group's own units (codes span +-448): within one top-binade step
+    assert np.abs(R.fp8_decode(got) - R.fp8_decode(exp)).max() <= 32
+    out = _np(_run(dev, block_size_M=bm, doweight_stage1=True).float())
+    far = (~np.isclose(out, ref["out"], rtol=0.05, atol=0.05)).mean()
+    mx, rms = R.normalized_errors(ref["out"], out)
+    print(f"[doweight_stage1 EP bm={bm}] outside allclose(0.05) {far:.4%} max-rel {mx:.2e} "
+          f"rms-rel {rms:.2e}", flush=True)
+    assert far <= 0.05 and rms <= RMSTOL
 
 
 @pytest.mark.parametrize("bm", [None, 64, 128])

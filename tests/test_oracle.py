@@ -210,6 +210,39 @@ def test_stage_oracles_vs_fp64_brute_force():
     assert R.normalized_errors(hb, R.moe_stage1_ref(x, w1_swapped, ids))[0] > 0.1
 
 
+def test_doweight_stage1_oracle():
+    """doweight_stage1 (aiter/fused_moe.py:1568-1571, 1664-1666): the routing
+    weight scales gate and up before SiLU and stage 2 sums unweighted. Pinned
+    by fp64 loops; with unit weights both placements agree exactly; and since
+    SiLU is not linear, the placement matters otherwise."""
+    rng = np.random.default_rng(16)
+    T, H, I, E, k = 7, 256, 128, 4, 2
+    x = R.bf16_round(rng.standard_normal((T, H)).astype(np.float32))
+    w1d = rng.standard_normal((E, 2 * I, H)).astype(np.float32) * 0.05
+    w2d = rng.standard_normal((E, H, I)).astype(np.float32) * 0.05
+    ids = np.stack([rng.permutation(E)[:k] for _ in range(T)])
+    tw = (rng.random((T, k)) + 0.5).astype(np.float32)
+    h = R.moe_stage1_ref(x, w1d, ids, tw)
+    out = R.moe_stage2_ref(h, w2d, ids, None)
+    hb = np.zeros((T, k, I))
+    ob = np.zeros((T, H))
+    for t in range(T):
+        for j in range(k):
+            y = (w1d[ids[t, j]].astype(np.float64) @ x[t].astype(np.float64)) * tw[t, j]
+            hb[t, j] = y[:I] / (1 + np.exp(-y[:I])) * y[I:]
+            ob[t] += w2d[ids[t, j]].astype(np.float64) @ hb[t, j]
+    np.testing.assert_allclose(h, hb, rtol=1e-2, atol=1e-3)
+    mx, rms = R.normalized_errors(ob, out)
+    assert mx < 1e-2 and rms < 3e-3
+    ones = np.ones_like(tw)
+    np.testing.assert_array_equal(R.moe_stage1_ref(x, w1d, ids, ones), R.moe_stage1_ref(x, w1d, ids))
+    np.testing.assert_array_equal(R.moe_stage2_ref(h, w2d, ids, ones),
+                                  R.moe_stage2_ref(h, w2d, ids, None))
+    # weighting after the activation instead is a different layer
+    out_late = R.moe_stage2_ref(R.moe_stage1_ref(x, w1d, ids), w2d, ids, tw)
+    assert R.normalized_errors(out, out_late)[0] > 0.05
+
+
 def test_stage1_e1_k1_is_dense_blockscale_gemm():
     rng = np.random.default_rng(7)
     T, H, I = 5, 384, 128
