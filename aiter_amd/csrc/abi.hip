@@ -30,7 +30,7 @@ void launch_moe_stage1_fp8bs(const uint8_t*, const float*, int64_t, int64_t, con
                              const float*, const uint8_t*, const int32_t*, const int32_t*,
                              const int32_t*, uint8_t*, float*, int64_t, int64_t, int64_t, int64_t,
                              int64_t, int64_t, int64_t, int, hipStream_t,
-                             const float*);
+                             const float*, int);
 void launch_moe_stage2_fp8bs(const uint8_t*, const float*, const uint8_t*, const float*,
                              const uint8_t*, const int32_t*, const float*, const int32_t*,
                              const int32_t*, float*, int64_t, int64_t, int64_t, int64_t, int64_t,
@@ -41,7 +41,7 @@ void launch_moe_stage1_fp8bs_v2(const uint8_t*, const float*, int64_t, int64_t, 
                                 const float*, const uint8_t*, const int32_t*, const int32_t*,
                                 const int32_t*, uint8_t*, float*, int64_t, int64_t, int64_t,
                                 int64_t, int64_t, int64_t, int64_t, int, hipStream_t,
-                             const float*);
+                             const float*, int);
 void launch_moe_stage2_fp8bs_v2(const uint8_t*, const float*, const uint8_t*, const float*,
                                 const uint8_t*, const int32_t*, const float*, const int32_t*,
                                 const int32_t*, float*, int64_t, int64_t, int64_t, int64_t,
@@ -53,7 +53,7 @@ void launch_moe_stage1_stream(const uint8_t*, const float*, int64_t, int64_t, co
                               const float*, const uint8_t*, const int32_t*, const int32_t*,
                               const int32_t*, uint8_t*, float*, int64_t, int64_t, int64_t,
                               int64_t, int64_t, int64_t, int64_t, int, hipStream_t,
-                             const float*);
+                             const float*, int);
 void launch_moe_stage2_stream(const uint8_t*, const float*, const uint8_t*, const float*,
                               const uint8_t*, const int32_t*, const float*, const int32_t*,
                               const int32_t*, float*, int64_t, int64_t, int64_t, int64_t,
@@ -77,7 +77,7 @@ void launch_moe_stage1_prefill(const uint8_t*, const float*, int64_t, int64_t, c
                                const float*, const uint8_t*, const int32_t*, const int32_t*,
                                const int32_t*, uint8_t*, float*, int64_t, int64_t, int64_t,
                                int64_t, int64_t, int64_t, int64_t, int, hipStream_t,
-                             const float*);
+                             const float*, int);
 void launch_moe_stage2_prefill(const uint8_t*, const float*, const uint8_t*, const float*,
                                const uint8_t*, const int32_t*, const float*, const int32_t*,
                                const int32_t*, float*, uint16_t*, int64_t, int64_t, int64_t,
@@ -99,25 +99,25 @@ struct WScale {
 // (model_dim % 256 == 0); other shapes take the general kernels of
 // moe_gemm_fp8bs.hip.
 // sw: sorted routing weights for doweight_stage1 (applied to gate and up
-// before the activation), or NULL.
+// before the activation), or NULL; act: kActSilu or kActGelu.
 static void stage1_dispatch(const uint8_t* a, const float* sa, int64_t sa_row, int64_t sa_kb,
                             const uint8_t* w1, WScale w1s, const int32_t* sid,
                             const int32_t* seid, const int32_t* nv, uint8_t* a2, float* a2s,
                             int64_t a_rows, int64_t K, int64_t I, int64_t E, int64_t topk,
                             int64_t bm, int64_t mblocks, int sh, hipStream_t s,
-                            const float* sw = nullptr) {
+                            const float* sw, int act) {
     if (stream_supported(bm, K))
         launch_moe_stage1_stream(a, sa, sa_row, sa_kb, w1, w1s.f32, w1s.e8m0, sid, seid, nv, a2,
-                                 a2s, a_rows, K, I, E, topk, bm, mblocks, sh, s, sw);
+                                 a2s, a_rows, K, I, E, topk, bm, mblocks, sh, s, sw, act);
     else if (prefill_supported(bm, K) && !w1s.e8m0)
         launch_moe_stage1_prefill(a, sa, sa_row, sa_kb, w1, w1s.f32, w1s.e8m0, sid, seid, nv, a2,
-                                  a2s, a_rows, K, I, E, topk, bm, mblocks, sh, s, sw);
+                                  a2s, a_rows, K, I, E, topk, bm, mblocks, sh, s, sw, act);
     else if (v2_supported(bm, K))
         launch_moe_stage1_fp8bs_v2(a, sa, sa_row, sa_kb, w1, w1s.f32, w1s.e8m0, sid, seid, nv, a2,
-                                   a2s, a_rows, K, I, E, topk, bm, mblocks, sh, s, sw);
+                                   a2s, a_rows, K, I, E, topk, bm, mblocks, sh, s, sw, act);
     else
         launch_moe_stage1_fp8bs(a, sa, sa_row, sa_kb, w1, w1s.f32, w1s.e8m0, sid, seid, nv, a2,
-                                a2s, a_rows, K, I, E, topk, bm, mblocks, sh, s, sw);
+                                a2s, a_rows, K, I, E, topk, bm, mblocks, sh, s, sw, act);
 }
 
 // Stage 2 runs on the prefill kernel for this shape (the only stage-2
@@ -260,8 +260,9 @@ void stage1_entry(const void* a1, const float* a1_scale, int64_t a1_scale_transp
     check_dims(model_dim, inter_dim);
     check_topk_experts(tokens, topk, num_experts);
     check_block_m_gemm(block_m, model_dim, inter_dim);
-    AMD_CHECK(activation == 0, "only ActivationType.Silu (0) is supported, got " +
-                                   std::to_string(activation));
+    AMD_CHECK(activation == kActSilu || activation == kActGelu,
+              "only ActivationType.Silu (0) and Gelu (1) are supported, got " +
+                  std::to_string(activation));
     AMD_CHECK(max_m_blocks >= 0, "max_m_blocks must be >= 0");
     if (tokens == 0 || max_m_blocks == 0) return;
     check_ptr(a1, "a1");
@@ -275,7 +276,7 @@ void stage1_entry(const void* a1, const float* a1_scale, int64_t a1_scale_transp
     stage1_dispatch((const uint8_t*)a1, a1_scale, sa_row, sa_kb, (const uint8_t*)w1, w1s,
                     sorted_ids, sorted_expert_ids, num_valid_ids, (uint8_t*)a2, a2_scale, tokens,
                     model_dim, inter_dim, num_experts, topk, block_m, max_m_blocks,
-                    (int)(w_shuffled != 0), (hipStream_t)stream, sorted_weights);
+                    (int)(w_shuffled != 0), (hipStream_t)stream, sorted_weights, (int)activation);
 }
 
 void stage2_entry(const void* a2, const float* a2_scale, const void* w2, WScale w2s,
@@ -306,9 +307,12 @@ void fused_entry(const void* hidden_states, int hidden_dtype, const void* w1, WS
                  const int32_t* expert_mask, const int32_t* num_local_tokens, void* out,
                  int out_dtype, int64_t tokens, int64_t model_dim, int64_t inter_dim,
                  int64_t num_experts, int64_t global_experts, int64_t topk, int64_t block_m,
-                 int64_t doweight_stage1, int64_t w_shuffled, void* workspace,
-                 int64_t workspace_bytes, void* stream) {
+                 int64_t activation, int64_t doweight_stage1, int64_t w_shuffled,
+                 void* workspace, int64_t workspace_bytes, void* stream) {
     check_dims(model_dim, inter_dim);
+    AMD_CHECK(activation == kActSilu || activation == kActGelu,
+              "only ActivationType.Silu (0) and Gelu (1) are supported, got " +
+                  std::to_string(activation));
     check_topk_experts(tokens, topk, num_experts);
     AMD_CHECK(hidden_dtype == DT_BF16 || hidden_dtype == DT_FP16,
               "hidden_states dtype must be bf16 or fp16");
@@ -354,7 +358,8 @@ void fused_entry(const void* hidden_states, int hidden_dtype, const void* w1, WS
     const bool dw = doweight_stage1 != 0;
     stage1_dispatch(a1, a1_scale, model_dim / 128, 1, (const uint8_t*)w1, w1s, sorted_ids,
                     sorted_eids, num_valid, a2, a2_scale, tokens, model_dim, inter_dim,
-                    num_experts, topk, block_m, L.blocks, sh, s, dw ? sorted_w : nullptr);
+                    num_experts, topk, block_m, L.blocks, sh, s, dw ? sorted_w : nullptr,
+                    (int)activation);
     stage2_dispatch(a2, a2_scale, (const uint8_t*)w2, w2s, sorted_ids, dw ? nullptr : sorted_w,
                     sorted_eids,
                     num_valid, part ? nullptr : acc, tokens * topk, inter_dim, model_dim,
@@ -547,14 +552,15 @@ int aiter_amd_fused_moe_fp8_blockscale(const void* hidden_states, int hidden_dty
                                        const int32_t* num_local_tokens, void* out, int out_dtype,
                                        int64_t tokens, int64_t model_dim, int64_t inter_dim,
                                        int64_t num_experts, int64_t global_experts, int64_t topk,
-                                       int64_t block_m, int64_t doweight_stage1, int64_t w_shuffled, void* workspace,
+                                       int64_t block_m, int64_t activation,
+                                       int64_t doweight_stage1, int64_t w_shuffled, void* workspace,
                                        int64_t workspace_bytes, void* stream) {
     return safe_call([&] {
         AMD_CHECK(w1_scale && w2_scale, "a required pointer is NULL");
         fused_entry(hidden_states, hidden_dtype, w1, WScale{w1_scale, nullptr}, w2,
                     WScale{w2_scale, nullptr}, topk_weights, topk_ids, expert_mask,
                     num_local_tokens, out, out_dtype, tokens, model_dim, inter_dim, num_experts,
-                    global_experts, topk, block_m, doweight_stage1, w_shuffled, workspace,
+                    global_experts, topk, block_m, activation, doweight_stage1, w_shuffled, workspace,
                     workspace_bytes, stream);
     });
 }
@@ -565,7 +571,8 @@ int aiter_amd_fused_moe_a8w4(const void* hidden_states, int hidden_dtype, const 
                              const int32_t* expert_mask, const int32_t* num_local_tokens,
                              void* out, int out_dtype, int64_t tokens, int64_t model_dim,
                              int64_t inter_dim, int64_t num_experts, int64_t global_experts,
-                             int64_t topk, int64_t block_m, int64_t doweight_stage1, int64_t w_shuffled, void* workspace,
+                             int64_t topk, int64_t block_m, int64_t activation,
+                             int64_t doweight_stage1, int64_t w_shuffled, void* workspace,
                              int64_t workspace_bytes, void* stream) {
     return safe_call([&] {
         check_e8m0(w1_scale, "w1_scale");
@@ -573,7 +580,7 @@ int aiter_amd_fused_moe_a8w4(const void* hidden_states, int hidden_dtype, const 
         fused_entry(hidden_states, hidden_dtype, w1, WScale{nullptr, w1_scale}, w2,
                     WScale{nullptr, w2_scale}, topk_weights, topk_ids, expert_mask,
                     num_local_tokens, out, out_dtype, tokens, model_dim, inter_dim, num_experts,
-                    global_experts, topk, block_m, doweight_stage1, w_shuffled, workspace,
+                    global_experts, topk, block_m, activation, doweight_stage1, w_shuffled, workspace,
                     workspace_bytes, stream);
     });
 }

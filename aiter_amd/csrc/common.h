@@ -145,6 +145,15 @@ __device__ __forceinline__ float silu_f32(float x) {
     return x / (1.0f + __expf(-x));
 }
 
+// torch.nn.functional.gelu (approximate='none'): x/2 * (1 + erf(x/sqrt(2)))
+__device__ __forceinline__ float gelu_f32(float x) {
+    return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f));
+}
+
+// ActivationType values (csrc/include/aiter_enum.h:7-12) the GEMMs apply to gate
+constexpr int kActSilu = 0;
+constexpr int kActGelu = 1;
+
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 }  // namespace aiter_amd

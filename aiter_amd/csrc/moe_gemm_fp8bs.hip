@@ -58,6 +58,7 @@ struct GemmArgs {
     const uint8_t* w_scale8;    // [E, N, K/32] e8m0 (MXFP4 weights)
     const int32_t* sorted_ids;
     const float* sorted_w;
+    int act;                   // stage 1: activation of gate (kActSilu / kActGelu)
     const int32_t* sorted_eids;
     const int32_t* num_valid;
     uint8_t* a2;                // stage 1 out: fp8 [T*topk, I]
@@ -310,17 +311,24 @@ __global__ __launch_bounds__(kGemmThreads) void moe_gemm_fp8bs_kernel(GemmArgs g
 
     // ---- stage 1 epilogue: silu(gate)*up -> bf16 -> 1x128 fp8 requant ----
     float h[NRT][2][4];
+    // act(gate) * up; the activation is chosen once per workgroup
+    auto act_up = [&](auto act) {
 #pragma unroll
-    for (int rt = 0; rt < NRT; ++rt)
+        for (int rt = 0; rt < NRT; ++rt)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+            for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                // doweight_stage1: the pair's weight scales gate and up before the
-                // activation (aiter/fused_moe.py:1568-1571)
-                const float wg = g.sorted_w ? s_w[rt * 16 + 4 * lq + v] : 1.0f;
-                h[rt][j][v] = bf16_round(silu_f32(acc[rt][j][v] * wg) * (acc[rt][2 + j][v] * wg));
-            }
+                for (int v = 0; v < 4; ++v) {
+                    // doweight_stage1: the pair's weight scales gate and up before the
+                    // activation (aiter/fused_moe.py:1568-1571)
+                    const float wg = g.sorted_w ? s_w[rt * 16 + 4 * lq + v] : 1.0f;
+                    h[rt][j][v] = bf16_round(act(acc[rt][j][v] * wg) * (acc[rt][2 + j][v] * wg));
+                }
+    };
+    if (g.act == kActGelu)
+        act_up([](float x) { return gelu_f32(x); });
+    else
+        act_up([](float x) { return silu_f32(x); });
 #pragma unroll
     for (int rt = 0; rt < NRT; ++rt)
 #pragma unroll
@@ -406,9 +414,10 @@ void launch_moe_stage1_fp8bs(const uint8_t* a, const float* a_scale, int64_t sa_
                              const int32_t* num_valid, uint8_t* a2, float* a2_scale,
                              int64_t a_rows, int64_t K, int64_t inter, int64_t E, int64_t topk,
                              int64_t block_m, int64_t max_m_blocks, int shuffled,
-                             hipStream_t stream, const float* sorted_w) {
+                             hipStream_t stream, const float* sorted_w, int act) {
     GemmArgs g{};
     g.sorted_w = sorted_w;                 // doweight_stage1 (or NULL)
+    g.act = act;
     g.a = a;
     g.a_scale = a_scale;
     g.sa_row = sa_row;

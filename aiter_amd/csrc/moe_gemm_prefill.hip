@@ -54,6 +54,7 @@ struct Args {
     const uint8_t* w_scale8;   // [E, N, K/32] e8m0 (MXFP4 weights)
     const int32_t* sorted_ids;
     const float* sorted_w;
+    int act;                   // stage 1: activation of gate (kActSilu / kActGelu)
     const int32_t* sorted_eids;
     const int32_t* num_valid;
     uint8_t* a2;
@@ -524,19 +525,26 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
         constexpr int NH1 = NCT / 2;
         const int nc = n0 + jt * TROWS;
         float h[NRT][NH1][4];
+        // act(gate) * up; the activation is chosen once per workgroup
+        auto act_up = [&](auto act) {
 #pragma unroll
-        for (int rt = 0; rt < NRT; ++rt)
+            for (int rt = 0; rt < NRT; ++rt)
 #pragma unroll
-            for (int j = 0; j < NH1; ++j)
+                for (int j = 0; j < NH1; ++j)
 #pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    // doweight_stage1: the pair's weight scales gate and up before the
-                    // activation (aiter/fused_moe.py:1568-1571)
-                    const float wg = g.sorted_w ? s_w[row_base + rt * 16 + (TR ? lr : 4 * lq + v)]
-                                                : 1.0f;
-                    h[rt][j][v] = bf16_round(silu_f32(acc[rt][j][v] * wg) *
-                                             (acc[rt][NH1 + j][v] * wg));
-                }
+                    for (int v = 0; v < 4; ++v) {
+                        // doweight_stage1: the pair's weight scales gate and up before
+                        // the activation (aiter/fused_moe.py:1568-1571)
+                        const float wg =
+                            g.sorted_w ? s_w[row_base + rt * 16 + (TR ? lr : 4 * lq + v)] : 1.0f;
+                        h[rt][j][v] = bf16_round(act(acc[rt][j][v] * wg) *
+                                                 (acc[rt][NH1 + j][v] * wg));
+                    }
+        };
+        if (g.act == kActGelu)
+            act_up([](float x) { return gelu_f32(x); });
+        else
+            act_up([](float x) { return silu_f32(x); });
         if constexpr (TR) {
 #pragma unroll
             for (int rt = 0; rt < NRT; ++rt) {
@@ -758,9 +766,10 @@ void launch_moe_stage1_prefill(const uint8_t* a, const float* a_scale, int64_t s
                                const int32_t* sorted_eids, const int32_t* num_valid,
                                uint8_t* a2, float* a2_scale, int64_t a_rows, int64_t K,
                                int64_t inter, int64_t E, int64_t topk, int64_t block_m,
-                               int64_t max_m_blocks, int shuffled, hipStream_t stream, const float* sorted_w) {
+                               int64_t max_m_blocks, int shuffled, hipStream_t stream, const float* sorted_w, int act) {
     pf::Args g{};
     g.sorted_w = sorted_w;                 // doweight_stage1 (or NULL)
+    g.act = act;
     g.a = a;
     g.a_scale = a_scale;
     g.sa_row = sa_row;

@@ -9,7 +9,7 @@ HIP kernels of libaiter_amd.so through the C ABI:
   stage-2 down-GEMM with top-k weighted accumulate -> f32 -> bf16/fp16.
 
 Supported: quant_type per_128x128 / per_1x128 with fp8 e4m3fn weights and
-fp32 block scales (or per_1x32 with MXFP4 weights), activation Silu, g1u1
+fp32 block scales (or per_1x32 with MXFP4 weights), activation Silu or Gelu, g1u1
 (w1 holds gate and up), bf16/fp16 activations (or fp8 activations with
 a1_scale), expert_mask (EP share), num_local_tokens, doweight_stage1.
 Anything else raises NotImplementedError; there is no fallback path.
@@ -211,8 +211,8 @@ def _check_supported(hidden_states, w1, w2, activation, quant_type, doweight_sta
         raise NotImplementedError(
             f"quant_type {quant_type!r}: only per_128x128 / per_1x128 fp8 blockscale and "
             "per_1x32 MXFP4 weights (A8W4) are implemented")
-    if activation != ActivationType.Silu:
-        raise NotImplementedError(f"activation {activation!r}: only Silu is implemented")
+    if activation not in (ActivationType.Silu, ActivationType.Gelu):
+        raise NotImplementedError(f"activation {activation!r}: only Silu and Gelu are implemented")
     if hidden_pad or intermediate_pad or bias1 is not None or bias2 is not None:
         raise NotImplementedError("hidden_pad / intermediate_pad / bias are not implemented")
     if w1_scale is None or w2_scale is None:
@@ -291,8 +291,8 @@ def fused_moe_(hidden_states, w1, w2, topk_weight, topk_ids, expert_mask=None,
             x.data_ptr(), AITER_DTYPE[x.dtype], w1c.data_ptr(), w1s.data_ptr(), w2c.data_ptr(),
             w2s.data_ptr(), topk_weight.data_ptr(), topk_ids.data_ptr(), _ptr(mask),
             _ptr(num_local_tokens), out.data_ptr(), AITER_DTYPE[out_dtype], M, model_dim,
-            inter_dim, E, global_E, topk, block_m, int(bool(doweight_stage1)), int(shuffled),
-            ws.data_ptr(), ws_bytes, stream)
+            inter_dim, E, global_E, topk, block_m, int(activation), int(bool(doweight_stage1)),
+            int(shuffled), ws.data_ptr(), ws_bytes, stream)
         return out
 
     # fp8 activations with caller-provided 1x128 scales: skip the quant step
@@ -305,7 +305,7 @@ def fused_moe_(hidden_states, w1, w2, topk_weight, topk_ids, expert_mask=None,
     # (aiter/fused_moe.py:1253, 1330)
     a2, a2s = st1(hidden_states.contiguous(), a1_scale.contiguous(), w1c, w1s, sorted_ids,
                   sorted_eids, num_valid, topk, block_m, shuffled,
-                  sorted_weights=sorted_w if doweight_stage1 else None)
+                  sorted_weights=sorted_w if doweight_stage1 else None, activation=activation)
     st2(a2, a2s, w2c, w2s, sorted_ids, None if doweight_stage1 else sorted_w, sorted_eids,
         num_valid, acc, block_m, shuffled)
     _abi.call("aiter_amd_moe_acc_to_out", acc.data_ptr(), out.data_ptr(), AITER_DTYPE[out_dtype],
@@ -314,7 +314,7 @@ def fused_moe_(hidden_states, w1, w2, topk_weight, topk_ids, expert_mask=None,
 
 
 def _stage1(entry, a1, a1_scale, w1, w1_scale, sorted_ids, sorted_expert_ids, num_valid_ids,
-            topk, block_m, shuffled, a1_scale_transposed, sorted_weights):
+            topk, block_m, shuffled, a1_scale_transposed, sorted_weights, activation):
     T, H = a1.shape
     E, N1, _ = w1.shape
     inter = N1 // 2
@@ -326,28 +326,31 @@ def _stage1(entry, a1, a1_scale, w1, w1_scale, sorted_ids, sorted_expert_ids, nu
         w1_scale.data_ptr(), sorted_ids.data_ptr(), _ptr(sorted_weights),
         sorted_expert_ids.data_ptr(), num_valid_ids.data_ptr(), a2.data_ptr(), a2s.data_ptr(),
         T, H, inter, E, topk,
-        int(block_m), sorted_expert_ids.numel(), int(ActivationType.Silu), int(bool(shuffled)),
+        int(block_m), sorted_expert_ids.numel(), int(ActivationType(activation)),
+        int(bool(shuffled)),
         _stream(a1.device))
     return a2, a2s
 
 
 def moe_stage1_fp8_blockscale(a1, a1_scale, w1, w1_scale, sorted_ids, sorted_expert_ids,
                               num_valid_ids, topk, block_m, shuffled, a1_scale_transposed=False,
-                              sorted_weights=None):
+                              sorted_weights=None, activation=ActivationType.Silu):
     """Stage 1 (gate+up GEMM, SiLU*up, fp8 1x128 requant).
 
     Returns (a2 fp8 [T, topk, I], a2_scale f32 [T, topk, I/128]) -- the pair
     the reference builds from ck_moe_stage1 + quant (fused_moe.py:1297-1314).
     sorted_weights (doweight_stage1): each pair's routing weight scales its
     gate and up rows before the activation (fused_moe.py:1568-1571).
+    activation: Silu or Gelu (torch's exact erf form) on gate.
     """
     return _stage1("aiter_amd_moe_stage1_fp8_blockscale", a1, a1_scale, w1, w1_scale,
                    sorted_ids, sorted_expert_ids, num_valid_ids, topk, block_m, shuffled,
-                   a1_scale_transposed, sorted_weights)
+                   a1_scale_transposed, sorted_weights, activation)
 
 
 def moe_stage1_a8w4(a1, a1_scale, w1, w1_scale, sorted_ids, sorted_expert_ids, num_valid_ids,
-                    topk, block_m, shuffled, a1_scale_transposed=False, sorted_weights=None):
+                    topk, block_m, shuffled, a1_scale_transposed=False, sorted_weights=None,
+                    activation=ActivationType.Silu):
     """A8W4 stage 1: fp8 1x128 activations x MXFP4 w1 (packed uint8 [E, 2I, H/2],
     e8m0 [E, 2I, H/32] or its 2-D e8m0_shuffle layout); same outputs as
     moe_stage1_fp8_blockscale."""
@@ -355,7 +358,7 @@ def moe_stage1_a8w4(a1, a1_scale, w1, w1_scale, sorted_ids, sorted_expert_ids, n
     w1_scale = e8m0_rowmajor(w1_scale, E, N1, a1.shape[1] // 32)
     return _stage1("aiter_amd_moe_stage1_a8w4", a1, a1_scale, w1.view(torch.uint8),
                    w1_scale.view(torch.uint8), sorted_ids, sorted_expert_ids, num_valid_ids,
-                   topk, block_m, shuffled, a1_scale_transposed, sorted_weights)
+                   topk, block_m, shuffled, a1_scale_transposed, sorted_weights, activation)
 
 
 def _stage2(entry, a2, a2_scale, w2, w2_scale, sorted_ids, sorted_weights, sorted_expert_ids,

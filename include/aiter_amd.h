@@ -78,7 +78,8 @@ int aiter_amd_dynamic_per_group_quant_fp8(const void* input, int input_dtype, in
  *   (or [model_dim/128, tokens] when a1_scale_transposed != 0)
  *   w1 [E, 2*inter_dim, model_dim] fp8, w1_scale [E, 2*inter_dim/128, model_dim/128]
  *   a2 [tokens, topk, inter_dim] fp8, a2_scale [tokens, topk, inter_dim/128]
- *   activation must be 0 (Silu); w_shuffled: 1 for the (16,16) layout.
+ *   activation: 0 Silu or 1 Gelu (torch's exact erf form), applied to gate
+ *   (aiter/ops/quant.py:398-404); w_shuffled: 1 for the (16,16) layout.
  *   sorted_weights: NULL, or the sorted routing weights for doweight_stage1
  *   (they scale gate and up before the activation, aiter/fused_moe.py:
  *   1568-1571; fused_moe_2stages passes them to stage 1 and none to stage 2,
@@ -164,7 +165,9 @@ int64_t aiter_amd_fused_moe_workspace_bytes(int64_t tokens, int64_t model_dim,
  *   [tokens, topk]; expert_mask [global_experts] or NULL (then
  *   global_experts == num_experts); num_local_tokens device i32[1] or NULL.
  *   out [tokens, model_dim] in out_dtype (bf16/fp16).
- *   block_m = 0 picks the default for the token count. */
+ *   block_m = 0 picks the default for the token count; activation 0 Silu /
+ *   1 Gelu; doweight_stage1 as fused_moe's (the routing weights scale gate
+ *   and up before the activation, stage 2 sums unweighted). */
 int aiter_amd_fused_moe_fp8_blockscale(const void* hidden_states, int hidden_dtype,
                                        const void* w1, const float* w1_scale, const void* w2,
                                        const float* w2_scale, const float* topk_weights,
@@ -173,8 +176,9 @@ int aiter_amd_fused_moe_fp8_blockscale(const void* hidden_states, int hidden_dty
                                        int out_dtype, int64_t tokens, int64_t model_dim,
                                        int64_t inter_dim, int64_t num_experts,
                                        int64_t global_experts, int64_t topk, int64_t block_m,
-                                       int64_t doweight_stage1, int64_t w_shuffled,
-                                       void* workspace, int64_t workspace_bytes, void* stream);
+                                       int64_t activation, int64_t doweight_stage1,
+                                       int64_t w_shuffled, void* workspace,
+                                       int64_t workspace_bytes, void* stream);
 
 /* The whole 2-stage A8W4 MoE in one call: fused_moe_ with quant_type per_1x32
  * and fp4x2 weights (aiter/fused_moe.py:255-275, 1103-1334), fp8 1x128
@@ -186,9 +190,9 @@ int aiter_amd_fused_moe_a8w4(const void* hidden_states, int hidden_dtype, const 
                              const int32_t* expert_mask, const int32_t* num_local_tokens,
                              void* out, int out_dtype, int64_t tokens, int64_t model_dim,
                              int64_t inter_dim, int64_t num_experts, int64_t global_experts,
-                             int64_t topk, int64_t block_m, int64_t doweight_stage1,
-                             int64_t w_shuffled, void* workspace, int64_t workspace_bytes,
-                             void* stream);
+                             int64_t topk, int64_t block_m, int64_t activation,
+                             int64_t doweight_stage1, int64_t w_shuffled, void* workspace,
+                             int64_t workspace_bytes, void* stream);
 
 /* ---- routing: top-k experts per token from the router logits ----
  * gating [tokens, num_experts] fp32/bf16/fp16 (dtype code as above),

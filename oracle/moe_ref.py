@@ -325,8 +325,16 @@ def local_expert_ids(topk_ids: np.ndarray, expert_mask=None) -> np.ndarray:
     return lut[np.asarray(topk_ids, dtype=np.int64)]
 
 
+def gelu(x: np.ndarray) -> np.ndarray:
+    """torch.nn.functional.gelu, approximate='none' (aiter/ops/quant.py:398-404):
+    x/2 * (1 + erf(x/sqrt(2))), in fp64 then fp32."""
+    from scipy.special import erf
+    x = np.asarray(x, dtype=np.float64)
+    return (0.5 * x * (1.0 + erf(x / np.sqrt(2.0)))).astype(np.float32)
+
+
 def moe_stage1_ref(a1: np.ndarray, w1: np.ndarray, topk_ids_local: np.ndarray,
-                   topk_w: np.ndarray = None) -> np.ndarray:
+                   topk_w: np.ndarray = None, activation: str = "silu") -> np.ndarray:
     """torch_moe_stage1 with per_1x128 (aiter/fused_moe.py:1483-1585), given
     already-dequantised fp32 a1 [T, H] and w1 [E, 2I, H]:
     out[t, j] = silu(g) * u with [g, u] = a1[t] @ w1[e_tj]^T, fp32, then bf16.
@@ -345,7 +353,8 @@ def moe_stage1_ref(a1: np.ndarray, w1: np.ndarray, topk_ids_local: np.ndarray,
             out[tok, slot] = a1[tok] @ w1[e].T
             if topk_w is not None:
                 out[tok, slot] *= np.asarray(topk_w, np.float32)[tok, slot][:, None]
-    h = silu(out[..., :inter]) * out[..., inter:]
+    act = gelu if activation == "gelu" else silu
+    h = act(out[..., :inter]) * out[..., inter:]
     return bf16_round(h)
 
 
@@ -370,7 +379,7 @@ def moe_stage2_ref(a2: np.ndarray, w2: np.ndarray, topk_ids_local: np.ndarray,
 
 def fused_moe_ref(x_bf16: np.ndarray, w1q, w1s, w2q, w2s, topk_ids, topk_w,
                   expert_mask=None, num_local_tokens=None, act_quant="kernel",
-                  weight_format="fp8_128x128", doweight_stage1=False):
+                  weight_format="fp8_128x128", doweight_stage1=False, activation="silu"):
     """The whole 2-stage FP8 blockscale layer as the reference's fused_moe
     computes it (aiter/fused_moe.py:1103-1334 with the oracles of
     op_tests/test_moe_2stage.py:187-231): 1x128 quant of x, stage 1 with
@@ -382,7 +391,7 @@ def fused_moe_ref(x_bf16: np.ndarray, w1q, w1s, w2q, w2s, topk_ids, topk_w,
     dequantised as in torch_moe_stage1/2's per_1x32 weight branch
     (aiter/fused_moe.py:1539-1553, 1635-1649).
     doweight_stage1: the routing weights go to stage 1 and stage 2 sums
-    unweighted (fused_moe.py:1253, 1330).
+    unweighted (fused_moe.py:1253, 1330). activation 'silu' or 'gelu'.
     Returns dict with out [T, H] (fp32 of bf16 values) and intermediates."""
     deq = dequant_weight_mxfp4 if weight_format == "mxfp4" else dequant_weight_128x128
     q = quant_1x128_kernel if act_quant == "kernel" else pertoken_quant_torch_semantics
@@ -394,7 +403,7 @@ def fused_moe_ref(x_bf16: np.ndarray, w1q, w1s, w2q, w2s, topk_ids, topk_w,
     a1q, a1s = q(x)
     a1 = dequant_1x128(a1q, a1s)
     w1 = deq(w1q, w1s)
-    h = moe_stage1_ref(a1, w1, ids_local, topk_w if doweight_stage1 else None)
+    h = moe_stage1_ref(a1, w1, ids_local, topk_w if doweight_stage1 else None, activation)
     topk = h.shape[1]
     inter = h.shape[2]
     a2q, a2s = q(h.reshape(T * topk, inter))

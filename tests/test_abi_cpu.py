@@ -87,8 +87,8 @@ def test_stage_validation_errors():
                   1, None, match="block_m must be 16, 32, 64 or 128")
     _expect_error("aiter_amd_moe_stage1_fp8_blockscale", *args, 4, 4224, 1152, 8, 2, 128, 10, 0,
                   1, None, match="block_m 128 needs")
-    _expect_error("aiter_amd_moe_stage1_fp8_blockscale", *args, 4, 4096, 2048, 8, 2, 32, 10, 1, 1,
-                  None, match="Silu")
+    _expect_error("aiter_amd_moe_stage1_fp8_blockscale", *args, 4, 4096, 2048, 8, 2, 32, 10, 2, 1,
+                  None, match=r"Silu \(0\) and Gelu \(1\)")
     _expect_error("aiter_amd_moe_stage2_fp8_blockscale", 16, 16, 16, 16, 16, 16, 16, 16, 16, 4,
                   4096, 2048, 8, 40, 32, 10, 1, None, match="topk must be")
     _expect_error("aiter_amd_moe_acc_to_out", 16, 16, 4, 16, 4, 64, None, match="bf16 or fp16")
@@ -96,12 +96,14 @@ def test_stage_validation_errors():
 
 def test_fused_validation_errors(lib):
     base = [16, 3, 16, 16, 16, 16, 16, 16, None, None, 16, 3]
-    # ... tokens, model_dim, inter_dim, E, global E, topk, block_m, doweight_stage1,
-    # w_shuffled, workspace, workspace_bytes, stream
-    _expect_error("aiter_amd_fused_moe_fp8_blockscale", *base, 4, 4096, 2048, 8, 8, 2, 0, 0, 1,
+    # ... tokens, model_dim, inter_dim, E, global E, topk, block_m, activation,
+    # doweight_stage1, w_shuffled, workspace, workspace_bytes, stream
+    _expect_error("aiter_amd_fused_moe_fp8_blockscale", *base, 4, 4096, 2048, 8, 8, 2, 0, 0, 0, 1,
                   16, 10, None, match="workspace of")
+    _expect_error("aiter_amd_fused_moe_fp8_blockscale", *base, 4, 4096, 2048, 8, 8, 2, 0, 2, 0, 1,
+                  16, 10, None, match="Gelu")
     masked = [16, 3, 16, 16, 16, 16, 16, 16, 16, None, 16, 3]    # expert_mask given
-    _expect_error("aiter_amd_fused_moe_fp8_blockscale", *masked, 4, 4096, 2048, 8, 4, 2, 0, 0,
+    _expect_error("aiter_amd_fused_moe_fp8_blockscale", *masked, 4, 4096, 2048, 8, 4, 2, 0, 0, 0,
                   1, 16, 10**9, None, match="global_experts")
     ws = lib.aiter_amd_fused_moe_workspace_bytes(8192, 4096, 2048, 256, 8, 64)
     # sorted ids/weights + a1 + a2 + f32 accumulator dominate
@@ -134,7 +136,7 @@ def test_python_layer_rejects_unsupported_modes():
         fused_moe(x, w1, w2, tw, ids, quant_type=QuantType.No)
     with pytest.raises(NotImplementedError, match="activation"):
         fused_moe(x, w1, w2, tw, ids, quant_type=QuantType.per_128x128,
-                  activation=ActivationType.Gelu, w1_scale=s1, w2_scale=s2)
+                  activation=ActivationType.Swiglu, w1_scale=s1, w2_scale=s2)
     with pytest.raises(NotImplementedError, match="bias"):
         fused_moe(x, w1, w2, tw, ids, quant_type=QuantType.per_128x128, bias1=torch.zeros(2, 256),
                   w1_scale=s1, w2_scale=s2)
@@ -200,7 +202,7 @@ def test_a8w4_validation_errors():
     _expect_error("aiter_amd_moe_stage2_a8w4", 16, 16, 16, None, 16, 16, 16, 16, 16, 4, 4096,
                   2048, 8, 2, 32, 10, 1, None, match="w2_scale is NULL")
     base = [16, 3, 16, 16, 16, None, 16, 16, None, None, 16, 3]
-    _expect_error("aiter_amd_fused_moe_a8w4", *base, 4, 4096, 2048, 8, 8, 2, 0, 0, 1, 16, 10,
+    _expect_error("aiter_amd_fused_moe_a8w4", *base, 4, 4096, 2048, 8, 8, 2, 0, 0, 0, 1, 16, 10,
                   None, match="w2_scale is NULL")
 
 

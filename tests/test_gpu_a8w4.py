@@ -32,7 +32,7 @@ def _a8w4(cfg):
     return dataclasses.replace(cfg, weights="mxfp4")
 
 
-def _make_layer(cfg, device, shuffle, doweight=False):
+def _make_layer(cfg, device, shuffle, doweight=False, activation="silu"):
     wts = W.make_weights(cfg, device="cpu", shuffle=False)
     x = W.make_hidden(cfg)
     tw, ids = W.make_routing(cfg)
@@ -40,7 +40,7 @@ def _make_layer(cfg, device, shuffle, doweight=False):
     ref = R.fused_moe_ref(x.float().numpy(), wts["w1"].numpy(), wts["w1_scale"].numpy(),
                           wts["w2"].numpy(), wts["w2_scale"].numpy(), ids.numpy(), tw.numpy(),
                           None if mask is None else mask.numpy(), weight_format="mxfp4",
-                          doweight_stage1=doweight)
+                          doweight_stage1=doweight, activation=activation)
     w1, w2 = wts["w1"], wts["w2"]
     if shuffle:
         w1, w2 = A.shuffle_weight(w1), A.shuffle_weight(w2)
@@ -84,6 +84,18 @@ def test_a8w4_doweight_stage1(cuda_device, bm):
     dev, ref = _make_layer(cfg, cuda_device, True, doweight=True)
     out = _run(dev, block_size_M=bm, doweight_stage1=True)
     _check(ref["out"], _np(out.float()), f"A8W4 doweight_stage1 bm={bm}")
+
+
+@pytest.mark.parametrize("bm", [16, 128])
+def test_a8w4_gelu(cuda_device, bm):
+    """ActivationType.Gelu on the A8W4 stage-1 kernels (stream at bm 16,
+    direct-to-LDS at bm 128). Here one a2 value sits on an fp8 requant tie
+    whose one-step flip moves a small output 3% (normalised) from the
+    oracle's, so the check is split at the stage boundary."""
+    cfg = _a8w4(W.CONFIG_A)
+    dev, ref = _make_layer(cfg, cuda_device, True, activation="gelu")
+    out = _run(dev, block_size_M=bm, activation=A.ActivationType.Gelu)
+    _fullshape.stagewise_vs_oracle(cfg, dev, ref, _np(out.float()), bm, A.ActivationType.Gelu)
 
 
 def test_a8w4_torch_dtypes_match_byte_views(cuda_device):

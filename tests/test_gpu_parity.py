@@ -105,7 +105,7 @@ def test_act_quant_num_rows(cuda_device):
 
 
 # ------------------------------------------------------ fused MoE layer ---
-def _make_layer(cfg, device, shuffle, doweight=False):
+def _make_layer(cfg, device, shuffle, doweight=False, activation="silu"):
     wts = W.make_weights(cfg, device="cpu", shuffle=False)
     x = W.make_hidden(cfg)
     tw, ids = W.make_routing(cfg)
@@ -114,7 +114,7 @@ def _make_layer(cfg, device, shuffle, doweight=False):
     w2u = wts["w2"].view(torch.uint8).numpy()
     ref = R.fused_moe_ref(x.float().numpy(), w1u, wts["w1_scale"].numpy(), w2u,
                           wts["w2_scale"].numpy(), ids.numpy(), tw.numpy(),
-                          None if mask is None else mask.numpy(), doweight_stage1=doweight)
+                          None if mask is None else mask.numpy(), doweight_stage1=doweight, activation=activation)
     w1, w2 = wts["w1"], wts["w2"]
     if shuffle:
         w1, w2 = A.shuffle_weight(w1), A.shuffle_weight(w2)
@@ -211,6 +211,26 @@ def test_fused_moe_doweight_stage1(cuda_device, bm):
                            w2_scale=dev["s2"], a1_scale=a1s, dtype=torch.bfloat16,
                            block_size_M=bm, doweight_stage1=True)
         _check(ref["out"], _np(out8.float()), "doweight_stage1 fp8 input")
+
+
+@pytest.mark.parametrize("bm", [16, 32, 64, 128])
+def test_fused_moe_gelu(cuda_device, bm):
+    """ActivationType.Gelu: exact-erf GELU(gate)·up (aiter/ops/quant.py:398-404)
+    in every stage-1 kernel (stream at bm 16/32, prefill at bm 64/128); at bm
+    64 also with doweight_stage1. The SiLU layer differs by far more than the
+    tolerance."""
+    cfg = W.CONFIG_A
+    dev, ref = _make_layer(cfg, cuda_device, True, activation="gelu")
+    out = _np(_run(dev, block_size_M=bm, activation=A.ActivationType.Gelu).float())
+    _check(ref["out"], out, f"gelu bm={bm}")
+    _fullshape.stagewise_vs_oracle(cfg, dev, ref, out, bm, A.ActivationType.Gelu)
+    _, ref_silu = _make_layer(cfg, cuda_device, True)
+    assert R.normalized_errors(ref_silu["out"], out)[0] > 10 * MAXTOL
+    if bm == 64:
+        dev, ref = _make_layer(cfg, cuda_device, True, doweight=True, activation="gelu")
+        out = _run(dev, block_size_M=bm, activation=A.ActivationType.Gelu, doweight_stage1=True)
+        _fullshape.stagewise_vs_oracle(cfg, dev, ref, _np(out.float()), bm,
+                                       A.ActivationType.Gelu, doweight=True)
 
 
 @pytest.mark.parametrize("bm", [32, 128])

@@ -243,6 +243,28 @@ def test_doweight_stage1_oracle():
     assert R.normalized_errors(out, out_late)[0] > 0.05
 
 
+def test_gelu_oracle():
+    """F.gelu's exact form (aiter/ops/quant.py:398-404): known values, a
+    scalar math.erf restatement, gelu(x) - gelu(-x) == x, and the
+    stage-1 oracle applying it to gate only."""
+    import math
+    x = np.array([0.0, 1.0, -1.0, 2.0, -3.0, 0.5], dtype=np.float32)
+    np.testing.assert_allclose(R.gelu(x), [0.0, 0.8413447, -0.1586553, 1.9544997, -0.0040497,
+                                           0.3457312], rtol=2e-6, atol=1e-7)
+    y = np.linspace(-8, 8, 1001).astype(np.float32)
+    ref = np.array([0.5 * v * (1 + math.erf(v / math.sqrt(2))) for v in y.astype(np.float64)])
+    np.testing.assert_allclose(R.gelu(y), ref, rtol=1e-6, atol=1e-7)
+    # gelu(x) - x/2 = (x/2)·erf(x/sqrt2) is even: gelu(x) - gelu(-x) == x
+    np.testing.assert_allclose(R.gelu(y) - R.gelu(-y), y, atol=2e-6)
+    rng = np.random.default_rng(17)
+    a1 = R.bf16_round(rng.standard_normal((5, 256)).astype(np.float32))
+    w1 = rng.standard_normal((2, 256, 256)).astype(np.float32) * 0.05
+    ids = np.array([[0], [1], [0], [1], [0]])
+    g = np.stack([a1[t] @ w1[ids[t, 0]].T for t in range(5)])
+    expect = R.bf16_round(R.gelu(g[:, :128]) * g[:, 128:])
+    np.testing.assert_array_equal(R.moe_stage1_ref(a1, w1, ids, activation="gelu")[:, 0], expect)
+
+
 def test_stage1_e1_k1_is_dense_blockscale_gemm():
     rng = np.random.default_rng(7)
     T, H, I = 5, 384, 128
