@@ -1,12 +1,17 @@
 """Build libaiter_amd.so (gfx950) from aiter_amd/csrc/*.hip with hipcc.
 
 Objects go to aiter_amd/_build/, the shared library next to this file so it
-is loaded in-tree.  Usage: ``python -m aiter_amd.build`` (or ``build()``).
+is loaded in-tree.  Each kernel's registers, spills, scratch, LDS and
+occupancy, as the compiler reports them, go to
+aiter_amd/_build/resource_usage.json.  Usage: ``python -m aiter_amd.build``
+(or ``build()``).
 """
 from __future__ import annotations
 
 import concurrent.futures as cf
+import json
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -39,14 +44,45 @@ def _hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm is required to build aiter_amd)")
 
 
-def _compile(src: Path, hipcc: str) -> Path:
+RESOURCE_USAGE = BUILD_DIR / "resource_usage.json"
+
+_REMARKS = {
+    "vgpr": re.compile(r"remark:\s+VGPRs: (\d+)"),
+    "agpr": re.compile(r"remark:\s+AGPRs: (\d+)"),
+    "vgpr_spill": re.compile(r"remark:\s+VGPRs Spill: (\d+)"),
+    "sgpr_spill": re.compile(r"remark:\s+SGPRs Spill: (\d+)"),
+    "scratch": re.compile(r"remark:\s+ScratchSize \[bytes/lane\]: (\d+)"),
+    "lds": re.compile(r"remark:\s+LDS Size \[bytes/block\]: (\d+)"),
+    "occupancy": re.compile(r"remark:\s+Occupancy \[waves/SIMD\]: (\d+)"),
+}
+
+
+def _resource_usage(stderr: str) -> dict:
+    """Per-kernel register, spill, scratch, LDS and occupancy figures from
+    the compiler's kernel-resource-usage remarks, keyed by mangled name."""
+    out, cur = {}, None
+    for line in stderr.splitlines():
+        m = re.search(r"remark:\s+Function Name: (\S+)", line)
+        if m:
+            cur = out.setdefault(m.group(1), {})
+            continue
+        if cur is None:
+            continue
+        for key, pat in _REMARKS.items():
+            m = pat.search(line)
+            if m:
+                cur[key] = int(m.group(1))
+    return out
+
+
+def _compile(src: Path, hipcc: str):
     obj = BUILD_DIR / (src.stem + ".o")
-    cmd = [hipcc, *HIPCC_FLAGS, "-I", str(CSRC), "-I", str(PKG_DIR.parent / "include"),
-           "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc, *HIPCC_FLAGS, "-Rpass-analysis=kernel-resource-usage", "-I", str(CSRC),
+           "-I", str(PKG_DIR.parent / "include"), "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stderr}")
-    return obj
+    return obj, _resource_usage(res.stderr)
 
 
 def build(verbose: bool = True) -> Path:
@@ -54,13 +90,16 @@ def build(verbose: bool = True) -> Path:
     BUILD_DIR.mkdir(exist_ok=True)
     srcs = sorted(CSRC.glob("*.hip"))
     with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
-        objs = list(ex.map(lambda s: _compile(s, hipcc), srcs))
+        done = list(ex.map(lambda s: _compile(s, hipcc), srcs))
+    objs = [o for o, _ in done]
+    usage = {src.name: u for src, (_, u) in zip(srcs, done)}
     tmp = LIB_PATH.with_suffix(".so.tmp")
     cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
     os.replace(tmp, LIB_PATH)
+    RESOURCE_USAGE.write_text(json.dumps(usage, indent=1, sort_keys=True))
     if verbose:
         print(f"[aiter_amd] built {LIB_PATH} from {len(srcs)} sources", file=sys.stderr)
     return LIB_PATH

@@ -145,9 +145,11 @@ __device__ __forceinline__ float silu_f32(float x) {
     return x / (1.0f + __expf(-x));
 }
 
-// torch.nn.functional.gelu (approximate='none'): x/2 * (1 + erf(x/sqrt(2)))
+// torch.nn.functional.gelu (approximate='none'): x/2 * (1 + erf(x/sqrt(2))),
+// evaluated as x/2 * erfc(-x/sqrt(2)), which has no cancellation for x < 0
+// (and in the unrolled GEMM epilogues needs fewer registers than erff)
 __device__ __forceinline__ float gelu_f32(float x) {
-    return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f));
+    return 0.5f * x * erfcf(x * -0.70710678118654752f);
 }
 
 // ActivationType values (csrc/include/aiter_enum.h:7-12) the GEMMs apply to gate
