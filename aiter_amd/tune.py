@@ -143,7 +143,10 @@ def main(argv=None):
     with open(a.out, "w", newline="") as f:
         w = csv.DictWriter(f, fieldnames=COLUMNS)
         w.writeheader()
-        for r in keep + rows:
+        order = lambda r: (str(r["cu_num"]), str(r["q_dtype_w"]), str(r["q_type"]),
+                           str(r["act_type"]), int(r["model_dim"]), int(r["inter_dim"]),
+                           int(r["expert"]), int(r["topk"]), int(r["token"]))
+        for r in sorted(keep + rows, key=order):
             w.writerow({c: r.get(c, "") for c in COLUMNS})
     _load.cache_clear()
     print(f"wrote {len(keep) + len(rows)} rows to {a.out}", file=sys.stderr)
