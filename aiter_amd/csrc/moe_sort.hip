@@ -79,39 +79,48 @@ __device__ void zero_rows(const SortParams& p, int tokens, int block, int nblock
         dst[i] = z;
 }
 
-// Slot-mask cell (token tl, expert e) of the chunk table.  Cells are one
-// byte when topk <= 8 and one u32 otherwise; byte cells are set with a u32
-// atomicOr on the aligned word that holds them.
-__device__ __forceinline__ uint32_t table_cell(const SortParams& p, const uint32_t* table, int tl,
-                                               int e) {
-    const int i = tl * p.E + e;
-    if (p.cell_bytes == 1) return reinterpret_cast<const uint8_t*>(table)[i];
-    return table[i];
-}
-
+// The chunk table holds a slot-mask cell per (token, expert): one byte when
+// topk <= 8 and one u32 otherwise; byte cells are set with a u32 atomicOr
+// on the aligned word that holds them.
 __device__ __forceinline__ int chunk_rows(const SortParams& p, int c, int tokens) {
     return max(0, min(p.ct, tokens - c * p.ct));
 }
 
 // Fill table[rows][E] with slot bitmasks of chunk c (only the chunk's rows
 // are cleared and used) and, when s_wt is given, stage the chunk's routing
-// weights there as [row][slot].
+// weights there as [row][slot].  Each thread's ids and weights are loaded
+// kPairBatch at a time before any of them is used, so one batch costs one
+// memory round trip (the first batch is in flight while the table clears).
+constexpr int kPairBatch = 4;
+
 __device__ void build_table(const SortParams& p, uint32_t* table, int c, int tokens,
                             float* s_wt) {
     const int nrows = chunk_rows(p, c, tokens);
     const int nwords = (nrows * p.E * p.cell_bytes + 3) / 4;
-    for (int i = threadIdx.x; i < nwords; i += kSortThreads) table[i] = 0u;
-    __syncthreads();
-    const int t0 = c * p.ct;
     const int npairs = nrows * p.topk;
-    for (int i = threadIdx.x; i < npairs; i += kSortThreads) {
-        int tl = i / p.topk;
-        int j = i - tl * p.topk;
-        int t = t0 + tl;
-        if (s_wt) s_wt[i] = p.topk_w[(int64_t)t0 * p.topk + i];
-        {
-            int e = p.topk_ids[(int64_t)t * p.topk + j];
+    const int64_t base = (int64_t)c * p.ct * p.topk;
+    for (int i0 = 0; i0 < npairs; i0 += kPairBatch * kSortThreads) {
+        int ev[kPairBatch];
+        float wv[kPairBatch];
+#pragma unroll
+        for (int u = 0; u < kPairBatch; ++u) {
+            const int i = i0 + u * kSortThreads + (int)threadIdx.x;
+            ev[u] = i < npairs ? p.topk_ids[base + i] : -1;
+            wv[u] = (s_wt && i < npairs) ? p.topk_w[base + i] : 0.0f;
+        }
+        if (i0 == 0) {   // block-uniform: every thread takes the first batch
+            for (int i = threadIdx.x; i < nwords; i += kSortThreads) table[i] = 0u;
+            __syncthreads();
+        }
+#pragma unroll
+        for (int u = 0; u < kPairBatch; ++u) {
+            const int i = i0 + u * kSortThreads + (int)threadIdx.x;
+            if (i >= npairs) continue;
+            if (s_wt) s_wt[i] = wv[u];
+            const int e = ev[u];
             if (e >= 0 && e < p.E) {
+                const int tl = i / p.topk;
+                const int j = i - tl * p.topk;
                 const int cell = tl * p.E + e;
                 if (p.cell_bytes == 1)
                     atomicOr(&table[cell >> 2], (1u << j) << (8 * (cell & 3)));
@@ -121,10 +130,6 @@ __device__ void build_table(const SortParams& p, uint32_t* table, int c, int tok
         }
     }
     __syncthreads();
-}
-
-__device__ __forceinline__ int expert_enabled(const SortParams& p, int e) {
-    return p.expert_mask ? (p.expert_mask[e] != 0) : 1;
 }
 
 __device__ __forceinline__ int wave_incl_scan(int v) {
@@ -160,8 +165,9 @@ __device__ int block_excl_scan(int v, int* scratch, int* total) {
 // Given per-expert pair counts in s_total, lay out segments: s_start (padded
 // start offset) and s_local (local expert id); write sorted_expert_ids, the
 // padding entries and num_valid_ids.
-__device__ void finalize_segments(const SortParams& p, const int* s_total, int* s_start,
-                                  int* s_local, int* scratch, int tokens, bool write) {
+__device__ void finalize_segments(const SortParams& p, const int* s_total, const int* s_mask,
+                                  int* s_start, int* s_local, int* scratch, int tokens,
+                                  bool write) {
     const int E = p.E;
     const int bm = p.bm;
     const int ept = (E + kSortThreads - 1) / kSortThreads;
@@ -170,10 +176,9 @@ __device__ void finalize_segments(const SortParams& p, const int* s_total, int* 
     for (int i = 0; i < ept; ++i) {
         int e = base + i;
         if (e < E) {
-            int en = expert_enabled(p, e);
             int cnt = s_total[e];
-            psum += en ? ((cnt + bm - 1) / bm) * bm : 0;
-            msum += p.expert_mask ? p.expert_mask[e] : 1;
+            psum += s_mask[e] != 0 ? ((cnt + bm - 1) / bm) * bm : 0;
+            msum += s_mask[e];
         }
     }
     int ptot, mtot;
@@ -182,12 +187,11 @@ __device__ void finalize_segments(const SortParams& p, const int* s_total, int* 
     for (int i = 0; i < ept; ++i) {
         int e = base + i;
         if (e < E) {
-            int en = expert_enabled(p, e);
             int cnt = s_total[e];
             s_start[e] = ppre;
             s_local[e] = mpre;
-            ppre += en ? ((cnt + bm - 1) / bm) * bm : 0;
-            mpre += p.expert_mask ? p.expert_mask[e] : 1;
+            ppre += s_mask[e] != 0 ? ((cnt + bm - 1) / bm) * bm : 0;
+            mpre += s_mask[e];
         }
     }
     if (threadIdx.x == 0 && write) {
@@ -198,7 +202,7 @@ __device__ void finalize_segments(const SortParams& p, const int* s_total, int* 
     if (!write) return;
     const int32_t pad_id = (int32_t)(((uint32_t)(p.topk & 0xFF) << 24) | ((uint32_t)tokens & 0xFFFFFFu));
     for (int e = threadIdx.x; e < E; e += kSortThreads) {
-        if (!expert_enabled(p, e)) continue;
+        if (s_mask[e] == 0) continue;
         int cnt = s_total[e];
         if (cnt == 0) continue;
         int start = s_start[e];
@@ -212,31 +216,74 @@ __device__ void finalize_segments(const SortParams& p, const int* s_total, int* 
     }
 }
 
-// Emit the pairs of chunk c for every expert, starting at s_pos[e]; the
-// routing weights come from the chunk's LDS copy s_wt.
+// Emit the pairs of chunk c for every enabled expert, starting at s_pos[e];
+// the routing weights come from the chunk's LDS copy s_wt.  With byte cells
+// (topk <= 8) a thread reads kCellBatch rows' cells at once and walks the
+// set bits of the packed 64-bit word: bit 8u + j is slot j of row u, so
+// ascending bits are ascending (token, slot).
+constexpr int kCellBatch = 8;
+
 __device__ void scatter_chunk(const SortParams& p, const uint32_t* table, int c, int tokens,
-                              const int* s_pos, const float* s_wt) {
+                              const int* s_pos, const int* s_mask, const float* s_wt) {
     const int E = p.E;
     const int t0 = c * p.ct;
     const int nrows = chunk_rows(p, c, tokens);
+    const uint8_t* cells = reinterpret_cast<const uint8_t*>(table);
     for (int e = threadIdx.x; e < E; e += kSortThreads) {
-        if (!expert_enabled(p, e)) continue;
+        if (s_mask[e] == 0) continue;
         int pos = s_pos[e];
-        for (int tl = 0; tl < nrows; ++tl) {
-            uint32_t m = table_cell(p, table, tl, e);
-            while (m) {
-                int j = __ffs(m) - 1;
-                m &= m - 1u;
-                p.sorted_ids[pos] = (int32_t)(((uint32_t)j << 24) | (uint32_t)(t0 + tl));
-                p.sorted_w[pos] = s_wt[tl * p.topk + j];
-                ++pos;
+        if (p.cell_bytes == 1) {
+            for (int tl0 = 0; tl0 < nrows; tl0 += kCellBatch) {
+                uint64_t mm = 0;
+#pragma unroll
+                for (int u = 0; u < kCellBatch; ++u)
+                    if (tl0 + u < nrows) mm |= (uint64_t)cells[(tl0 + u) * E + e] << (8 * u);
+                while (mm) {
+                    const int b = __ffsll((unsigned long long)mm) - 1;
+                    mm &= mm - 1u;
+                    const int tl = tl0 + (b >> 3);
+                    const int j = b & 7;
+                    p.sorted_ids[pos] = (int32_t)(((uint32_t)j << 24) | (uint32_t)(t0 + tl));
+                    p.sorted_w[pos] = s_wt[tl * p.topk + j];
+                    ++pos;
+                }
+            }
+        } else {
+            for (int tl = 0; tl < nrows; ++tl) {
+                uint32_t m = table[tl * E + e];
+                while (m) {
+                    const int j = __ffs(m) - 1;
+                    m &= m - 1u;
+                    p.sorted_ids[pos] = (int32_t)(((uint32_t)j << 24) | (uint32_t)(t0 + tl));
+                    p.sorted_w[pos] = s_wt[tl * p.topk + j];
+                    ++pos;
+                }
             }
         }
     }
 }
 
+// Pairs of expert e in the chunk's table (popcount of its slot masks).
+__device__ __forceinline__ int table_count(const SortParams& p, const uint32_t* table, int nrows,
+                                           int e) {
+    int cnt = 0;
+    if (p.cell_bytes == 1) {
+        const uint8_t* cells = reinterpret_cast<const uint8_t*>(table);
+        for (int tl0 = 0; tl0 < nrows; tl0 += kCellBatch) {
+            uint64_t mm = 0;
+#pragma unroll
+            for (int u = 0; u < kCellBatch; ++u)
+                if (tl0 + u < nrows) mm |= (uint64_t)cells[(tl0 + u) * p.E + e] << (8 * u);
+            cnt += __popcll((unsigned long long)mm);
+        }
+    } else {
+        for (int tl = 0; tl < nrows; ++tl) cnt += __popc(table[tl * p.E + e]);
+    }
+    return cnt;
+}
+
 // LDS layout of the sorting kernels: table[ct*E] | s_wt[ct*topk] | s_total[E] |
-// s_start[E] | s_local[E] | s_pos[E] | scratch[kSortThreads/64]
+// s_start[E] | s_local[E] | s_pos[E] | s_mask[E] | scratch[kSortThreads/64]
 struct SortLds {
     uint32_t* table;
     float* s_wt;
@@ -244,6 +291,7 @@ struct SortLds {
     int* s_start;
     int* s_local;
     int* s_pos;
+    int* s_mask;
     int* scratch;
 };
 
@@ -255,7 +303,8 @@ __device__ SortLds carve_lds(const SortParams& p, uint32_t* smem) {
     L.s_start = L.s_total + p.E;
     L.s_local = L.s_start + p.E;
     L.s_pos = L.s_local + p.E;
-    L.scratch = L.s_pos + p.E;
+    L.s_mask = L.s_pos + p.E;
+    L.scratch = L.s_mask + p.E;
     return L;
 }
 
@@ -270,16 +319,17 @@ __global__ __launch_bounds__(kSortThreads) void moe_sort_oneshot_kernel(SortPara
     build_table(p, L.table, 0, tokens, L.s_wt);
     const int nrows = chunk_rows(p, 0, tokens);
     for (int e = threadIdx.x; e < p.E; e += kSortThreads) {
-        int cnt = 0;
-        for (int tl = 0; tl < nrows; ++tl) cnt += __popc(table_cell(p, L.table, tl, e));
-        L.s_total[e] = cnt;
+        L.s_mask[e] = p.expert_mask ? p.expert_mask[e] : 1;
+        L.s_total[e] = table_count(p, L.table, nrows, e);
     }
     __syncthreads();
-    finalize_segments(p, L.s_total, L.s_start, L.s_local, L.scratch, tokens, true);
+    finalize_segments(p, L.s_total, L.s_mask, L.s_start, L.s_local, L.scratch, tokens, true);
     __syncthreads();
-    scatter_chunk(p, L.table, 0, tokens, L.s_start, L.s_wt);
+    scatter_chunk(p, L.table, 0, tokens, L.s_start, L.s_mask, L.s_wt);
 }
 
+// Per-chunk expert counts by an LDS histogram of the chunk's ids (every
+// (token, slot) pair with an id in range counts once, as in the table).
 __global__ __launch_bounds__(kSortThreads) void moe_sort_count_kernel(SortParams p) {
     extern __shared__ uint32_t smem[];
     const int tokens = sort_tokens(p);
@@ -288,19 +338,34 @@ __global__ __launch_bounds__(kSortThreads) void moe_sort_count_kernel(SortParams
         return;
     }
     const int c = blockIdx.x;
-    build_table(p, smem, c, tokens, nullptr);
-    const int nrows = chunk_rows(p, c, tokens);
-    for (int e = threadIdx.x; e < p.E; e += kSortThreads) {
-        int cnt = 0;
-        for (int tl = 0; tl < nrows; ++tl) cnt += __popc(table_cell(p, smem, tl, e));
-        p.ws[(int64_t)c * p.E + e] = cnt;
+    int* s_cnt = reinterpret_cast<int*>(smem);
+    const int npairs = chunk_rows(p, c, tokens) * p.topk;
+    const int64_t base = (int64_t)c * p.ct * p.topk;
+    for (int i0 = 0; i0 < npairs || i0 == 0; i0 += kPairBatch * kSortThreads) {
+        int ev[kPairBatch];
+#pragma unroll
+        for (int u = 0; u < kPairBatch; ++u) {
+            const int i = i0 + u * kSortThreads + (int)threadIdx.x;
+            ev[u] = i < npairs ? p.topk_ids[base + i] : -1;
+        }
+        if (i0 == 0) {
+            for (int e = threadIdx.x; e < p.E; e += kSortThreads) s_cnt[e] = 0;
+            __syncthreads();
+        }
+#pragma unroll
+        for (int u = 0; u < kPairBatch; ++u)
+            if (ev[u] >= 0 && ev[u] < p.E) atomicAdd(&s_cnt[ev[u]], 1);
     }
+    __syncthreads();
+    for (int e = threadIdx.x; e < p.E; e += kSortThreads) p.ws[(int64_t)c * p.E + e] = s_cnt[e];
 }
 
 // Block c: per expert, the pairs of chunks before c (its write offset inside
 // the expert's segment) and of all chunks (the segment layout, which every
 // block derives identically); block 0 also writes the padding, the
 // sorted_expert_ids and num_valid_ids.  Then the chunk's pairs.
+constexpr int kChunkBatch = 16;   // per-chunk counts loaded per round trip
+
 __global__ __launch_bounds__(kSortThreads) void moe_sort_scatter_kernel(SortParams p) {
     extern __shared__ uint32_t smem[];
     const int tokens = sort_tokens(p);
@@ -308,37 +373,33 @@ __global__ __launch_bounds__(kSortThreads) void moe_sort_scatter_kernel(SortPara
     const SortLds L = carve_lds(p, smem);
     const int E = p.E;
     for (int e = threadIdx.x; e < E; e += kSortThreads) {
+        L.s_mask[e] = p.expert_mask ? p.expert_mask[e] : 1;   // in flight with the counts
         int before = 0, total = 0;
-        int k = 0;
-        for (; k + 8 <= p.num_chunks; k += 8) {   // 8 independent loads in flight
-            int v[8];
+        for (int k = 0; k < p.num_chunks; k += kChunkBatch) {
+            int v[kChunkBatch];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = p.ws[(int64_t)(k + u) * E + e];
+            for (int u = 0; u < kChunkBatch; ++u)
+                v[u] = k + u < p.num_chunks ? p.ws[(int64_t)(k + u) * E + e] : 0;
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
+            for (int u = 0; u < kChunkBatch; ++u) {
                 before += k + u < c ? v[u] : 0;
                 total += v[u];
             }
-        }
-        for (; k < p.num_chunks; ++k) {
-            const int v = p.ws[(int64_t)k * E + e];
-            before += k < c ? v : 0;
-            total += v;
         }
         L.s_total[e] = total;
         L.s_pos[e] = before;
     }
     __syncthreads();
-    finalize_segments(p, L.s_total, L.s_start, L.s_local, L.scratch, tokens, c == 0);
+    finalize_segments(p, L.s_total, L.s_mask, L.s_start, L.s_local, L.scratch, tokens, c == 0);
     for (int e = threadIdx.x; e < E; e += kSortThreads) L.s_pos[e] += L.s_start[e];
     if (c * p.ct >= tokens) return;
     build_table(p, L.table, c, tokens, L.s_wt);   // its barriers also publish s_pos
-    scatter_chunk(p, L.table, c, tokens, L.s_pos, L.s_wt);
+    scatter_chunk(p, L.table, c, tokens, L.s_pos, L.s_mask, L.s_wt);
 }
 
-// ---------------------------------------------------------------- host ---
 // Tokens per chunk: the largest power of two <= 256 whose slot-mask table
-// fits in 48 KB of LDS (so table + scan arrays stay within 64 KB).
+// fits in 48 KB of LDS. With the five per-expert arrays (80 KB at E = 4096)
+// a block's LDS stays under gfx950's 160 KB.
 static int sort_chunk_tokens(int E, int topk) {
     const int cell = topk <= 8 ? 1 : 4;
     int ct = 256;
@@ -387,7 +448,7 @@ void launch_moe_sort(const int32_t* topk_ids, const float* topk_w, const int32_t
     }
     const size_t table_lds = (size_t)table_words(p.ct, (int)E, p.cell_bytes) * 4;
     const size_t full_lds =
-        table_lds + (size_t)p.ct * p.topk * 4 + (size_t)(4 * E + kSortThreads / 64) * 4;
+        table_lds + (size_t)p.ct * p.topk * 4 + (size_t)(5 * E + kSortThreads / 64) * 4;
     if (p.num_chunks == 1) {
         p.sort_blocks = 1;
         hipLaunchKernelGGL(moe_sort_oneshot_kernel, dim3(1 + zero_blocks), dim3(kSortThreads),
@@ -397,7 +458,7 @@ void launch_moe_sort(const int32_t* topk_ids, const float* topk_w, const int32_t
                   "sorting workspace too small");
         p.sort_blocks = p.num_chunks;
         hipLaunchKernelGGL(moe_sort_count_kernel, dim3(p.num_chunks + zero_blocks),
-                           dim3(kSortThreads), table_lds, stream, p);
+                           dim3(kSortThreads), (size_t)E * 4, stream, p);
         hipLaunchKernelGGL(moe_sort_scatter_kernel, dim3(p.num_chunks), dim3(kSortThreads),
                            full_lds, stream, p);
     }
