@@ -8,7 +8,9 @@ activation quant, stage 1, stage 2, output conversion) on inputs resident
 in HBM.  The decode leg (T=32, uniform softmax routing) is reported under
 "decode"; the other single-GPU configurations -- A8W4 (fp8 activations x
 MXFP4 weights) at T=32/1024/8192 and the expert-parallel share (32 of 256
-experts, T=4096) -- under "legs".  Prints one JSON line.
+experts, T=4096), the router, and the library's plain dense FP8 GEMM at
+the stage-1 shape (context for the MFMA fraction) -- under "legs".  Prints
+one JSON line.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload prefill8192|decode32|...]
                   [--legs a8w4_32,a8w4_1024,a8w4_8192,ep4096|none]
@@ -44,9 +46,12 @@ def parse():
     p.add_argument("--workload", default="prefill8192", type=_workload,
                    help="prefill<T> | decode<T> | a8w4_<T> | ep<T> (e.g. prefill8192, "
                         "decode32, a8w4_1024, ep4096)")
-    p.add_argument("--legs", default="a8w4_32,a8w4_1024,a8w4_8192,ep4096,route_32,route_8192",
+    p.add_argument("--legs",
+                   default="a8w4_32,a8w4_1024,a8w4_8192,ep4096,route_32,route_8192,"
+                           "dense_fp8_ceiling",
                    help="comma-separated extra workloads reported under 'legs' ('none': "
-                        "skip); route_<T> times the router top-k kernels at T tokens")
+                        "skip); route_<T> times the router top-k kernels at T tokens; "
+                        "dense_fp8_ceiling times the library's plain FP8 GEMM")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-decode", action="store_true")
     p.add_argument("--kernel-iters", type=int, default=10)
@@ -360,11 +365,44 @@ def route_leg(name, args, dev):
     return out
 
 
+def dense_ceiling_leg(name, args, dev):
+    """Context for the stage-1 MFMA fraction, not part of the layer: the
+    vendor library's plain dense FP8 GEMM (torch._scaled_mm, hipBLASLt) at
+    the stage-1 shape of all T=8192 pairs as one matrix (M = 65536 rows,
+    N = 2I = 4096, K = H = 4096) and at one expert's share (M = 512). It has
+    no block scales, no gather and no fused epilogue, so it bounds what an
+    FP8 MFMA GEMM of this size reaches on the card."""
+    import torch
+
+    f8 = torch.float8_e4m3fn
+    out = {"workload": name, "library": "torch._scaled_mm (hipBLASLt)"}
+    for M, N, K in ((65536, 4096, 4096), (512, 4096, 4096)):
+        a = torch.randn(M, K, device=dev).to(f8)
+        b = torch.randn(N, K, device=dev).to(f8).t()
+        for scales in ("tensor", "rowwise"):
+            if scales == "tensor":
+                sa = torch.tensor(1.0, device=dev)
+                sb = torch.tensor(1.0, device=dev)
+            else:
+                sa = torch.rand(M, 1, device=dev) + 0.5
+                sb = torch.rand(1, N, device=dev) + 0.5
+            fn = lambda: torch._scaled_mm(a, b, scale_a=sa, scale_b=sb, out_dtype=torch.bfloat16)
+            ms, _ = time_steps(fn, max(args.steps, 20), args.warmup)
+            tf = 2.0 * M * N * K / (ms * 1e-3)
+            out[f"M{M}_{scales}"] = {"us": round(ms * 1e3, 1), "tflops": round(tf / 1e12, 1),
+                                     "fp8_peak_frac": round(tf / PEAK_FP8_FLOPS, 4)}
+        del a, b
+    torch.cuda.empty_cache()
+    return out
+
+
 def leg(name, args, dev):
     """One extra workload: layer time, throughput, roofline fractions and
     per-stage kernel times."""
     if name.startswith("route_"):
         return route_leg(name, args, dev)
+    if name == "dense_fp8_ceiling":
+        return dense_ceiling_leg(name, args, dev)
     import torch
 
     from aiter_amd import workloads as W
