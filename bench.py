@@ -8,8 +8,9 @@ activation quant, stage 1, stage 2, output conversion) on inputs resident
 in HBM.  The decode leg (T=32, uniform softmax routing) is reported under
 "decode"; the other single-GPU configurations -- A8W4 (fp8 activations x
 MXFP4 weights) at T=32/1024/8192 and the expert-parallel share (32 of 256
-experts, T=4096), the router, and the library's plain dense FP8 GEMM at
-the stage-1 shape (context for the MFMA fraction) -- under "legs".  Prints
+experts, T=4096), the router, and two references for the roofline
+fractions (the library's plain dense FP8 GEMM at the stage-1 shape, torch's
+streaming read and copy) -- under "legs".  Prints
 one JSON line.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload prefill8192|decode32|...]
@@ -48,10 +49,11 @@ def parse():
                         "decode32, a8w4_1024, ep4096)")
     p.add_argument("--legs",
                    default="a8w4_32,a8w4_1024,a8w4_8192,ep4096,route_32,route_8192,"
-                           "dense_fp8_ceiling",
+                           "dense_fp8_ceiling,hbm_ceiling",
                    help="comma-separated extra workloads reported under 'legs' ('none': "
                         "skip); route_<T> times the router top-k kernels at T tokens; "
-                        "dense_fp8_ceiling times the library's plain FP8 GEMM")
+                        "dense_fp8_ceiling times the library's plain FP8 GEMM and "
+                        "hbm_ceiling torch's streaming read and copy")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-decode", action="store_true")
     p.add_argument("--kernel-iters", type=int, default=10)
@@ -396,6 +398,27 @@ def dense_ceiling_leg(name, args, dev):
     return out
 
 
+def hbm_ceiling_leg(name, args, dev):
+    """Context for the decode HBM fraction, not part of the layer: torch's
+    own streaming kernels on 4 GiB resident in HBM -- a read-only reduction
+    (sum over int64) and a device copy (read + write bytes)."""
+    import torch
+
+    n = 4 << 30
+    x = torch.empty(n, dtype=torch.uint8, device=dev).random_()
+    y = torch.empty_like(x)
+    out = {"workload": name, "bytes": n}
+    for tag, fn, byts in (("sum_read", lambda: torch.sum(x.view(torch.int64)), n),
+                          ("copy", lambda: y.copy_(x), 2 * n)):
+        ms, _ = time_steps(fn, max(args.steps, 20), args.warmup)
+        bw = byts / (ms * 1e-3)
+        out[tag] = {"us": round(ms * 1e3, 1), "tbps": round(bw / 1e12, 3),
+                    "hbm_peak_frac": round(bw / PEAK_HBM_BPS, 4)}
+    del x, y
+    torch.cuda.empty_cache()
+    return out
+
+
 def leg(name, args, dev):
     """One extra workload: layer time, throughput, roofline fractions and
     per-stage kernel times."""
@@ -403,6 +426,8 @@ def leg(name, args, dev):
         return route_leg(name, args, dev)
     if name == "dense_fp8_ceiling":
         return dense_ceiling_leg(name, args, dev)
+    if name == "hbm_ceiling":
+        return hbm_ceiling_leg(name, args, dev)
     import torch
 
     from aiter_amd import workloads as W
