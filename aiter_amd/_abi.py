@@ -16,7 +16,7 @@ _LIB_PATH = Path(__file__).resolve().parent / "libaiter_amd.so"
 _lock = threading.Lock()
 _lib = None
 
-ABI_VERSION = 1
+ABI_VERSION = 2   # AITER_AMD_ABI_VERSION of include/aiter_amd.h
 
 c_i32p = ctypes.c_void_p
 c_vp = ctypes.c_void_p

@@ -24,7 +24,10 @@
 extern "C" {
 #endif
 
-#define AITER_AMD_ABI_VERSION 1
+/* Raised whenever an entry point's arguments change: 2 added sorted_weights
+   to the stage-1 entries and activation / doweight_stage1 to the one-call
+   entries. */
+#define AITER_AMD_ABI_VERSION 2
 
 /* Replaces aiter_ctypes_abi_version (aiter_ctypes_error.h:120-147). */
 int aiter_amd_abi_version(void);

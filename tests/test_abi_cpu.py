@@ -31,6 +31,8 @@ def lib():
 
 def test_header_and_binding_agree():
     assert _declared_symbols() == sorted(_abi.EXPORTED)
+    text = (ROOT / "include" / "aiter_amd.h").read_text()
+    assert int(re.search(r"#define AITER_AMD_ABI_VERSION (\d+)", text).group(1)) == _abi.ABI_VERSION
 
 
 def test_library_exports_every_declared_symbol(lib):
@@ -39,7 +41,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.aiter_amd_abi_version() == 1
+    assert lib.aiter_amd_abi_version() == _abi.ABI_VERSION == 2
 
 
 def _expect_error(name, *args, match):
