@@ -83,6 +83,11 @@ void launch_moe_stage2_prefill(const uint8_t*, const float*, const uint8_t*, con
                                const int32_t*, float*, uint16_t*, int64_t, int64_t, int64_t,
                                int64_t, int64_t, int64_t, int64_t, int, hipStream_t, int64_t);
 
+// The 64/128-row kernels (prefill, v2) read their activation operand through
+// 32-bit buffer offsets, so its a_rows * K bytes must stay below 4 GiB.
+// Larger operands take the general kernel (64-bit addresses, block_m <= 64).
+static bool a_fits32(int64_t a_rows, int64_t K) { return a_rows * K < (int64_t(1) << 32); }
+
 // Weight scales of one layer: fp32 128x128 blocks (fp8 weights) or e8m0
 // bytes per 1x32 K block (MXFP4 weights); exactly one is set.
 struct WScale {
@@ -109,10 +114,10 @@ static void stage1_dispatch(const uint8_t* a, const float* sa, int64_t sa_row, i
     if (stream_supported(bm, K))
         launch_moe_stage1_stream(a, sa, sa_row, sa_kb, w1, w1s.f32, w1s.e8m0, sid, seid, nv, a2,
                                  a2s, a_rows, K, I, E, topk, bm, mblocks, sh, s, sw, act);
-    else if (prefill_supported(bm, K) && !w1s.e8m0)
+    else if (prefill_supported(bm, K) && !w1s.e8m0 && a_fits32(a_rows, K))
         launch_moe_stage1_prefill(a, sa, sa_row, sa_kb, w1, w1s.f32, w1s.e8m0, sid, seid, nv, a2,
                                   a2s, a_rows, K, I, E, topk, bm, mblocks, sh, s, sw, act);
-    else if (v2_supported(bm, K))
+    else if (v2_supported(bm, K) && a_fits32(a_rows, K))
         launch_moe_stage1_fp8bs_v2(a, sa, sa_row, sa_kb, w1, w1s.f32, w1s.e8m0, sid, seid, nv, a2,
                                    a2s, a_rows, K, I, E, topk, bm, mblocks, sh, s, sw, act);
     else
@@ -122,8 +127,9 @@ static void stage1_dispatch(const uint8_t* a, const float* sa, int64_t sa_row, i
 
 // Stage 2 runs on the prefill kernel for this shape (the only stage-2
 // kernel that can also write per-pair bf16 rows instead of accumulating).
-static bool stage2_on_prefill(int64_t bm, int64_t I, int64_t H, WScale w2s) {
+static bool stage2_on_prefill(int64_t bm, int64_t I, int64_t H, WScale w2s, int64_t a_rows) {
     return !(stream_supported(bm, I) && H % 256 == 0) && prefill_supported(bm, I) &&
+           a_fits32(a_rows, I) &&
            H % 256 == 0 && (!w2s.e8m0 || bm == 128);
 }
 
@@ -137,15 +143,17 @@ static void stage2_dispatch(const uint8_t* a2, const float* a2s, const uint8_t* 
                             int64_t I, int64_t H, int64_t E, int64_t topk, int64_t bm,
                             int64_t mblocks, int sh, hipStream_t s, uint16_t* part = nullptr,
                             int64_t est_pairs = -1) {
-    AMD_CHECK(!part || stage2_on_prefill(bm, I, H, w2s), "per-pair rows need the prefill kernel");
+    AMD_CHECK(!part || stage2_on_prefill(bm, I, H, w2s, a_rows),
+              "per-pair rows need the prefill kernel");
     if (stream_supported(bm, I) && H % 256 == 0)
         launch_moe_stage2_stream(a2, a2s, w2, w2s.f32, w2s.e8m0, sid, sw, seid, nv, acc, a_rows,
                                  I, H, E, topk, bm, mblocks, sh, s);
-    else if (prefill_supported(bm, I) && H % 256 == 0 && (!w2s.e8m0 || bm == 128))
+    else if (prefill_supported(bm, I) && H % 256 == 0 && (!w2s.e8m0 || bm == 128) &&
+             a_fits32(a_rows, I))
         launch_moe_stage2_prefill(a2, a2s, w2, w2s.f32, w2s.e8m0, sid, sw, seid, nv, acc, part,
                                   a_rows, I, H, E, topk, bm, mblocks, sh, s,
                                   est_pairs < 0 ? a_rows : est_pairs);
-    else if (v2_supported(bm, I) && H % 256 == 0)
+    else if (v2_supported(bm, I) && H % 256 == 0 && a_fits32(a_rows, I))
         launch_moe_stage2_fp8bs_v2(a2, a2s, w2, w2s.f32, w2s.e8m0, sid, sw, seid, nv, acc, a_rows,
                                    I, H, E, topk, bm, mblocks, sh, s);
     else
@@ -170,7 +178,8 @@ int64_t sorted_capacity_for(int64_t tokens, int64_t topk, int64_t E, int64_t bm)
     return tokens * topk + E * bm - topk;
 }
 
-void check_block_m_gemm(int64_t bm, int64_t model_dim, int64_t inter_dim) {
+void check_block_m_gemm(int64_t bm, int64_t model_dim, int64_t inter_dim, int64_t tokens,
+                        int64_t topk) {
     AMD_CHECK(bm == 16 || bm == 32 || bm == 64 || bm == 128,
               "block_m must be 16, 32, 64 or 128 for the fp8 blockscale GEMMs, got " +
                   std::to_string(bm));
@@ -178,6 +187,10 @@ void check_block_m_gemm(int64_t bm, int64_t model_dim, int64_t inter_dim) {
         AMD_CHECK(v2_supported(bm, model_dim) && v2_supported(bm, inter_dim) &&
                       model_dim % 256 == 0,
                   "block_m 128 needs model_dim a multiple of 256 and model_dim, inter_dim <= 8192");
+    if (bm == 128)
+        AMD_CHECK(a_fits32(tokens, model_dim) && a_fits32(tokens * topk, inter_dim),
+                  "block_m 128 needs tokens*model_dim and tokens*topk*inter_dim below 2^32 "
+                  "(the 128-row kernels use 32-bit offsets); use block_m 64 or less");
 }
 
 void check_dims(int64_t model_dim, int64_t inter_dim) {
@@ -239,7 +252,8 @@ int64_t default_block_m(int64_t tokens, int64_t topk, int64_t E, int64_t model_d
     if (avg <= 8) return 16;
     if (avg <= 20) return 32;
     if (avg >= 64 && v2_supported(128, model_dim) && v2_supported(128, inter_dim) &&
-        model_dim % 256 == 0)
+        model_dim % 256 == 0 && a_fits32(tokens, model_dim) &&
+        a_fits32(tokens * topk, inter_dim))
         return 128;
     return 64;
 }
@@ -259,7 +273,7 @@ void stage1_entry(const void* a1, const float* a1_scale, int64_t a1_scale_transp
                   int64_t activation, int64_t w_shuffled, void* stream) {
     check_dims(model_dim, inter_dim);
     check_topk_experts(tokens, topk, num_experts);
-    check_block_m_gemm(block_m, model_dim, inter_dim);
+    check_block_m_gemm(block_m, model_dim, inter_dim, tokens, topk);
     AMD_CHECK(activation == kActSilu || activation == kActGelu,
               "only ActivationType.Silu (0) and Gelu (1) are supported, got " +
                   std::to_string(activation));
@@ -287,7 +301,7 @@ void stage2_entry(const void* a2, const float* a2_scale, const void* w2, WScale 
                   void* stream) {
     check_dims(model_dim, inter_dim);
     check_topk_experts(tokens, topk, num_experts);
-    check_block_m_gemm(block_m, model_dim, inter_dim);
+    check_block_m_gemm(block_m, model_dim, inter_dim, tokens, topk);
     AMD_CHECK(max_m_blocks >= 0, "max_m_blocks must be >= 0");
     if (tokens == 0 || max_m_blocks == 0) return;
     check_ptr(a2, "a2");
@@ -321,7 +335,7 @@ void fused_entry(const void* hidden_states, int hidden_dtype, const void* w1, WS
     AMD_CHECK(E_sort >= num_experts && E_sort <= kMaxExperts,
               "global_experts must be in [num_experts, 4096]");
     if (block_m <= 0) block_m = default_block_m(tokens, topk, num_experts, model_dim, inter_dim);
-    check_block_m_gemm(block_m, model_dim, inter_dim);
+    check_block_m_gemm(block_m, model_dim, inter_dim, tokens, topk);
     if (tokens == 0) return;
     check_ptr(hidden_states, "hidden_states");
     check_ptr(w1, "w1");
@@ -345,7 +359,7 @@ void fused_entry(const void* hidden_states, int hidden_dtype, const void* w1, WS
     float* acc = reinterpret_cast<float*>(ws + L.off_acc);
     // stage 2 on the prefill kernel writes each pair's weighted row once (bf16)
     // and one pass sums a token's slots: no fp32 atomics, no accumulator to clear
-    uint16_t* part = stage2_on_prefill(block_m, inter_dim, model_dim, w2s)
+    uint16_t* part = stage2_on_prefill(block_m, inter_dim, model_dim, w2s, tokens * topk)
                          ? reinterpret_cast<uint16_t*>(ws + L.off_acc) : nullptr;
     hipStream_t s = (hipStream_t)stream;
     launch_moe_sort(topk_ids, topk_weights, expert_mask, num_local_tokens, sorted_ids, sorted_w,

@@ -175,7 +175,11 @@ def select_block_m(tokens: int, topk: int, num_experts: int, model_dim: int, int
     else the heuristic default_block_m."""
     tuned = tuned_block_m(_cu_num(device), tokens, model_dim, inter_dim, num_experts, topk,
                           "per_1x32" if a8w4 else "per_1x128", "fp4x2" if a8w4 else "fp8")
-    return tuned or default_block_m(tokens, topk, num_experts, model_dim, inter_dim)
+    bm = tuned or default_block_m(tokens, topk, num_experts, model_dim, inter_dim)
+    # the 128-row kernels address their activation operand with 32-bit offsets
+    if bm == 128 and max(tokens * model_dim, tokens * topk * inter_dim) >= 1 << 32:
+        bm = 64
+    return bm
 
 
 def e8m0_rowmajor(scale: torch.Tensor, E: int, N: int, KS: int) -> torch.Tensor:

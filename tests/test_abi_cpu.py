@@ -112,6 +112,22 @@ def test_fused_validation_errors(lib):
     assert ws > 8192 * 4096 * (1 + 4) + 8192 * 8 * 2048
 
 
+def test_block_m_128_needs_32bit_operands(lib, monkeypatch):
+    # the 128-row kernels use 32-bit buffer offsets: T*topk*inter >= 2^32 bytes
+    # (T = 262144 at topk 8, inter 2048) must not pick or accept them
+    assert lib.aiter_amd_default_block_m(262143, 8, 256, 4096, 2048) == 128
+    assert lib.aiter_amd_default_block_m(262144, 8, 256, 4096, 2048) == 64
+    args = [16, 16, 0, 16, 16, 16, None, 16, 16, 16, 16]
+    _expect_error("aiter_amd_moe_stage1_fp8_blockscale", *args, 262144, 4096, 2048, 256, 8, 128,
+                  10, 0, 1, None, match="32-bit offsets")
+    import importlib
+
+    F = importlib.import_module("aiter_amd.fused_moe")   # the module, not the function
+    monkeypatch.setattr(F, "_cu_num", lambda dev: 256)    # the MI355X's CU count, no GPU here
+    assert F.select_block_m(8192, 8, 256, 4096, 2048, False, torch.device("cpu")) == 128
+    assert F.select_block_m(262144, 8, 256, 4096, 2048, False, torch.device("cpu")) == 64
+
+
 def test_default_block_m(lib):
     assert lib.aiter_amd_default_block_m(1, 8, 256, 4096, 2048) == 16
     assert lib.aiter_amd_default_block_m(32, 8, 256, 4096, 2048) == 16

@@ -5,6 +5,8 @@ oracle; the MoE outputs agree with the fp32-dequant oracle within the
 normalised tolerance of the reference's MoE tests (max-rel <= 2e-2,
 RMS-rel <= 4e-3, op_tests/triton_tests/moe/test_moe_gemm_a8w4.py:104-160).
 """
+import importlib
+
 import numpy as np
 import pytest
 import torch
@@ -477,6 +479,36 @@ def test_fused_moe_empty_batch(cuda_device):
     out = A.fused_moe(dev["x"][:0], dev["w1"], dev["w2"], dev["tw"][:0], dev["ids"][:0],
                       quant_type=A.QuantType.per_128x128, w1_scale=dev["s1"], w2_scale=dev["s2"])
     assert out.shape == (0, cfg.model_dim) and out.dtype == torch.bfloat16
+
+
+def test_fused_moe_beyond_4gib_operand(cuda_device):
+    """A layer whose stage-2 activation operand (T*topk*inter fp8 bytes) is
+    just over 4 GiB: the 64/128-row kernels address it with 32-bit offsets,
+    so block_m falls back from 128 to 64 and stage 2 runs on the general
+    kernel (64-bit addresses). Tokens are independent, so the oracle checks
+    the first and last 16 tokens; the last ones' a2 rows lie past the 4 GiB
+    offset."""
+    T = (1 << 32) // (8 * 2048) + 64
+    cfg = W.MoEConfig("big", T, 512, 2048, 16, 8, seed=21)
+    wts = W.make_weights(cfg, device="cpu", shuffle=False)
+    x = W.make_hidden(cfg)
+    tw, ids = W.make_routing(cfg)
+    dev = cuda_device
+    w1, w2 = A.shuffle_weight(wts["w1"]).to(dev), A.shuffle_weight(wts["w2"]).to(dev)
+    w1.is_shuffled = w2.is_shuffled = True
+    fm = importlib.import_module("aiter_amd.fused_moe")
+    assert fm.select_block_m(T, 8, 16, 512, 2048, False, torch.device(dev)) == 64
+    out = A.fused_moe(x.to(dev), w1, w2, tw.to(dev), ids.to(dev),
+                      quant_type=A.QuantType.per_128x128, w1_scale=wts["w1_scale"].to(dev),
+                      w2_scale=wts["w2_scale"].to(dev))
+    torch.cuda.synchronize()
+    for rows in (slice(0, 16), slice(T - 16, T)):
+        ref = R.fused_moe_ref(x[rows].float().numpy(), wts["w1"].view(torch.uint8).numpy(),
+                              wts["w1_scale"].numpy(), wts["w2"].view(torch.uint8).numpy(),
+                              wts["w2_scale"].numpy(), ids[rows].numpy(), tw[rows].numpy())
+        _check(ref["out"], _np(out[rows].float()), f"T={T} rows {rows.start}..")
+    del out, w1, w2
+    torch.cuda.empty_cache()
 
 
 @pytest.mark.parametrize("T,E,k,seed", [(37, 32, 16, 12), (45, 1, 1, 13), (1, 8, 8, 14)])
