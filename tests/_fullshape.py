@@ -143,8 +143,8 @@ def stagewise_check(cfg, device, block_ms, log=print):
 
 def stagewise_vs_oracle(cfg, dev, ref, out, bm, activation, doweight=False, log=print):
     """The same split for a small layer, against the CPU oracle: stage 1's
-    fp8 codes against the oracle's a2 (at most 1% different, each by one
-    code step), the layer's output against the oracle's stage 2 applied to
+    fp8 codes against the oracle's a2 (at most 1% different, each element
+    within one top-binade e4m3 step of its group), the layer's output against the oracle's stage 2 applied to
     the kernel's own a2 (the strict normalised bar), and RMS-rel against the
     whole oracle chain. For layers whose smallest outputs sit next to a
     one-step requant flip (GELU(gate)·up makes such ties common), where the
@@ -161,12 +161,18 @@ def stagewise_vs_oracle(cfg, dev, ref, out, bm, activation, doweight=False, log=
                      sorted_weights=sw if doweight else None, activation=activation)
     loc = ref["ids_local"] >= 0
     codes = a2.view(torch.uint8).cpu().numpy()
-    step = np.abs(codes.astype(np.int32) - ref["a2q"].astype(np.int32))[loc]
-    log(f"[{cfg.name} bm={bm}] stage 1 codes differing {(step != 0).mean():.3%}, "
-        f"max step {step.max()}")
-    assert (step != 0).mean() <= 0.01 and step.max() <= 1
     a2d = R.dequant_1x128(codes.reshape(T * k, I),
                           a2s.cpu().numpy().reshape(T * k, -1)).reshape(T, k, I)
+    ref_d = R.dequant_1x128(ref["a2q"].reshape(T * k, I),
+                            ref["a2s"].reshape(T * k, -1)).reshape(T, k, I)
+    # each element within one top-binade e4m3 step of its group (32/448 of the
+    # group amax, i.e. 32 x the oracle's scale), as in stagewise_check
+    sc = np.repeat(ref["a2s"], 128, axis=-1)
+    err = (np.abs(a2d - ref_d) / (sc * 448))[loc]
+    differ = (codes != ref["a2q"])[loc].mean()
+    log(f"[{cfg.name} bm={bm}] stage 1 codes differing {differ:.3%}, element err/amax "
+        f"{err.max():.4f}")
+    assert differ <= 0.01 and err.max() <= E4M3_TOP_ULP * (1 + 2 * BF16_ULP), (differ, err.max())
     a2d[~loc] = 0
     wts = W.make_weights(cfg, device="cpu", shuffle=False)
     w2 = wts["w2"].numpy() if mx4 else wts["w2"].view(torch.uint8).numpy()
