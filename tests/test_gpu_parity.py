@@ -69,15 +69,26 @@ def test_sorting_bit_exact(cuda_device, T, E, k, bm, masked, local):
 
 
 def test_sorting_worked_example(cuda_device):
-    # csrc/include/moe_sorting_opus.h:277-339
-    ids = torch.tensor([[0, 3, 5], [2, 3, 5], [1, 3, 5], [1, 2, 3], [1, 3, 5]], dtype=torch.int32,
-                       device=cuda_device)
-    w = torch.arange(15, dtype=torch.float32, device=cuda_device).view(5, 3) + 1
-    sid, sw, se, nv, _ = A.moe_sorting(ids, w, 6, 128, torch.bfloat16, 4)
-    assert _np(nv).tolist() == [24, 5] and _np(se)[:6].tolist() == [0, 1, 2, 3, 3, 5]
-    mask = torch.tensor([1, 0, 1, 1, 0, 1], dtype=torch.int32, device=cuda_device)
-    sid, sw, se, nv, _ = A.moe_sorting(ids, w, 6, 128, torch.bfloat16, 4, mask)
-    assert _np(nv).tolist() == [20, 5] and _np(se)[:5].tolist() == [0, 1, 2, 2, 3]
+    """The reference's worked example (csrc/include/moe_sorting_opus.h:277-339,
+    fixture tests/golden/moe_sorting_worked_example.json), every output array."""
+    from pathlib import Path
+    import json
+
+    g = json.loads((Path(__file__).resolve().parent / "golden" /
+                    "moe_sorting_worked_example.json").read_text())
+    ids = torch.tensor(g["topk_ids"], dtype=torch.int32, device=cuda_device)
+    w = torch.tensor(g["topk_weights"], dtype=torch.float32, device=cuda_device)
+    for variant in ("unmasked", "masked"):
+        exp = g[variant]
+        mask = exp.get("expert_mask")
+        mask = None if mask is None else torch.tensor(mask, dtype=torch.int32, device=cuda_device)
+        sid, sw, se, nv, _ = A.moe_sorting(ids, w, g["num_experts"], 128, torch.bfloat16,
+                                            g["block_size"], mask)
+        n = exp["num_valid_ids"][0]
+        assert _np(nv).tolist() == exp["num_valid_ids"], variant
+        assert _np(sid)[:n].tolist() == exp["sorted_token_ids"], variant
+        assert _np(sw)[:n].tolist() == exp["sorted_weights"], variant
+        assert _np(se)[:n // g["block_size"]].tolist() == exp["sorted_expert_ids"], variant
 
 
 # ---------------------------------------------------------------- quant ---

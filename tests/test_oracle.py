@@ -8,6 +8,9 @@ exactly 448; E=1,k=1 is a dense block-scale GEMM) and fp64 brute force on
 tiny inputs.  Each check is chosen so a plausible slip (dropped scale, wrong
 slot/token order, swapped gate/up, transposed weight) fails it.
 """
+import json
+from pathlib import Path
+
 import numpy as np
 import pytest
 import torch
@@ -115,25 +118,38 @@ def test_shuffle_matches_definition():
 
 
 # -------------------------------------------------------------- sorting ---
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
 def _header_example():
-    # csrc/include/moe_sorting_opus.h:277-339 (E=6, topk=3, block 4, 5 tokens)
-    ids = np.array([[0, 3, 5], [2, 3, 5], [1, 3, 5], [1, 2, 3], [1, 3, 5]], np.int32)
-    w = np.arange(15, dtype=np.float32).reshape(5, 3) + 1
-    return ids, w
+    """The reference's worked example of sorting (csrc/include/moe_sorting_opus.h:
+    277-339), as the fixture tests/golden/make_sorting_example.py transcribes it."""
+    return json.loads((GOLDEN / "moe_sorting_worked_example.json").read_text())
+
+
+def test_sorting_fixture_matches_its_generator():
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location("make_sorting_example",
+                                                  GOLDEN / "make_sorting_example.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    assert _header_example() == json.loads(json.dumps(mod.fixture()))
 
 
 def test_sorting_reference_worked_example():
-    ids, w = _header_example()
-    sid, sw, se, nv = R.moe_sorting_ref(ids, w, 6, 4)
-    assert list(se) == [0, 1, 2, 3, 3, 5] and list(nv) == [24, 5]
-    tok = (sid & 0xFFFFFF).tolist()
-    assert tok == [0, 5, 5, 5, 2, 3, 4, 5, 1, 3, 5, 5, 0, 1, 2, 3, 4, 5, 5, 5, 0, 1, 2, 4]
-    slot = (sid >> 24).tolist()
-    assert slot[:4] == [0, 3, 3, 3] and slot[12:17] == [1, 1, 1, 2, 1]
-    assert sw[0] == 1 and sw[4] == w[2, 0] and np.all(sw[1:4] == 0)
-    # masked variant: experts 1 and 4 are off -> local ids [0, 1, 2, 2, 3], total 20
-    sid, sw, se, nv = R.moe_sorting_ref(ids, w, 6, 4, expert_mask=np.array([1, 0, 1, 1, 0, 1]))
-    assert list(se) == [0, 1, 2, 2, 3] and list(nv) == [20, 5]
+    g = _header_example()
+    ids = np.array(g["topk_ids"], np.int32)
+    w = np.array(g["topk_weights"], np.float32)
+    for variant, mask in (("unmasked", None), ("masked", g["masked"]["expert_mask"])):
+        exp = g[variant]
+        sid, sw, se, nv = R.moe_sorting_ref(ids, w, g["num_experts"], g["block_size"],
+                                            None if mask is None else np.array(mask))
+        n = exp["num_valid_ids"][0]
+        assert list(nv) == exp["num_valid_ids"], variant
+        assert sid[:n].tolist() == exp["sorted_token_ids"], variant
+        assert sw[:n].tolist() == exp["sorted_weights"], variant
+        assert se[:n // g["block_size"]].tolist() == exp["sorted_expert_ids"], variant
 
 
 @pytest.mark.parametrize("T,E,k,bm,masked,local", [
