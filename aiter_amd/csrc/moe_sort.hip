@@ -163,8 +163,8 @@ __device__ int block_excl_scan(int v, int* scratch, int* total) {
 }
 
 // Given per-expert pair counts in s_total, lay out segments: s_start (padded
-// start offset) and s_local (local expert id); write sorted_expert_ids, the
-// padding entries and num_valid_ids.
+// start offset) and s_local (local expert id); write num_valid_ids when
+// `write` (the padding and sorted_expert_ids are write_segments').
 __device__ void finalize_segments(const SortParams& p, const int* s_total, const int* s_mask,
                                   int* s_start, int* s_local, int* scratch, int tokens,
                                   bool write) {
@@ -199,17 +199,33 @@ __device__ void finalize_segments(const SortParams& p, const int* s_total, const
         p.num_valid[1] = tokens;
     }
     __syncthreads();
-    if (!write) return;
+}
+
+// Padding entries and sorted_expert_ids of the segment layout. One block
+// (the one-shot kernel) gives each thread an expert. The nranks blocks of the
+// multi-chunk scatter share the work instead: block `rank` takes every
+// nranks-th expert, one wave per expert with its lanes writing consecutive
+// entries, so a heavy expert's many M-block ids and padding entries are not
+// one thread's serial loop on the launch's critical path.
+__device__ void write_segments(const SortParams& p, const int* s_total, const int* s_mask,
+                               const int* s_start, const int* s_local, int tokens, int rank,
+                               int nranks) {
+    const int bm = p.bm;
     const int32_t pad_id = (int32_t)(((uint32_t)(p.topk & 0xFF) << 24) | ((uint32_t)tokens & 0xFFFFFFu));
-    for (int e = threadIdx.x; e < E; e += kSortThreads) {
+    const bool per_wave = nranks > 1;
+    const int lane = per_wave ? (int)(threadIdx.x & 63) : 0;
+    const int step = per_wave ? 64 : 1;
+    const int e0 = per_wave ? rank + (int)(threadIdx.x >> 6) * nranks : (int)threadIdx.x;
+    const int estep = per_wave ? nranks * (kSortThreads / 64) : kSortThreads;
+    for (int e = e0; e < p.E; e += estep) {
         if (s_mask[e] == 0) continue;
-        int cnt = s_total[e];
+        const int cnt = s_total[e];
         if (cnt == 0) continue;
-        int start = s_start[e];
-        int padded = ((cnt + bm - 1) / bm) * bm;
-        int eid = p.expert_mask ? s_local[e] : e;
-        for (int b = start / bm; b < (start + padded) / bm; ++b) p.sorted_eids[b] = eid;
-        for (int i = start + cnt; i < start + padded; ++i) {
+        const int start = s_start[e];
+        const int padded = ((cnt + bm - 1) / bm) * bm;
+        const int eid = p.expert_mask ? s_local[e] : e;
+        for (int b = start / bm + lane; b < (start + padded) / bm; b += step) p.sorted_eids[b] = eid;
+        for (int i = start + cnt + lane; i < start + padded; i += step) {
             p.sorted_ids[i] = pad_id;
             p.sorted_w[i] = 0.0f;
         }
@@ -324,7 +340,7 @@ __global__ __launch_bounds__(kSortThreads) void moe_sort_oneshot_kernel(SortPara
     }
     __syncthreads();
     finalize_segments(p, L.s_total, L.s_mask, L.s_start, L.s_local, L.scratch, tokens, true);
-    __syncthreads();
+    write_segments(p, L.s_total, L.s_mask, L.s_start, L.s_local, tokens, 0, 1);
     scatter_chunk(p, L.table, 0, tokens, L.s_start, L.s_mask, L.s_wt);
 }
 
@@ -391,6 +407,7 @@ __global__ __launch_bounds__(kSortThreads) void moe_sort_scatter_kernel(SortPara
     }
     __syncthreads();
     finalize_segments(p, L.s_total, L.s_mask, L.s_start, L.s_local, L.scratch, tokens, c == 0);
+    write_segments(p, L.s_total, L.s_mask, L.s_start, L.s_local, tokens, c, (int)gridDim.x);
     for (int e = threadIdx.x; e < E; e += kSortThreads) L.s_pos[e] += L.s_start[e];
     if (c * p.ct >= tokens) return;
     build_table(p, L.table, c, tokens, L.s_wt);   // its barriers also publish s_pos
