@@ -17,9 +17,12 @@ void set_last_error(const std::string& msg) { g_last_error = msg; }
 
 // launchers (moe_sort.hip, quant.hip, moe_gemm_fp8bs.hip)
 int64_t sort_workspace_bytes(int64_t rows, int64_t topk, int64_t E);
-void launch_moe_sort(const int32_t*, const float*, const int32_t*, const int32_t*, int32_t*,
+// returns true when it also ran the activation quant given by the last five arguments
+bool launch_moe_sort(const int32_t*, const float*, const int32_t*, const int32_t*, int32_t*,
                      float*, int32_t*, int32_t*, void*, int64_t, int64_t, int64_t, int64_t,
-                     int64_t, void*, int64_t, hipStream_t);
+                     int64_t, void*, int64_t, hipStream_t, const void* qx = nullptr,
+                     int qx_dtype = 0, uint8_t* qq = nullptr, float* qs = nullptr,
+                     int64_t q_cols = 0);
 void launch_per_group_quant_fp8(const void*, int, void*, float*, int64_t, int64_t, int,
                                 const int32_t*, int64_t, hipStream_t);
 void launch_acc_to_out(const float*, void*, int, const int32_t*, int64_t, int64_t, hipStream_t);
@@ -362,11 +365,15 @@ void fused_entry(const void* hidden_states, int hidden_dtype, const void* w1, WS
     uint16_t* part = stage2_on_prefill(block_m, inter_dim, model_dim, w2s, tokens * topk)
                          ? reinterpret_cast<uint16_t*>(ws + L.off_acc) : nullptr;
     hipStream_t s = (hipStream_t)stream;
-    launch_moe_sort(topk_ids, topk_weights, expert_mask, num_local_tokens, sorted_ids, sorted_w,
-                    sorted_eids, num_valid, part ? nullptr : acc, model_dim * 4, tokens, topk,
-                    E_sort, block_m, ws + L.off_sort_ws, L.sort_ws_bytes, s);
-    launch_per_group_quant_fp8(hidden_states, hidden_dtype, a1, a1_scale, tokens, model_dim, 0,
-                               num_local_tokens, 1, s);
+    // decode-sized batches: the sorting launch also quantises the activations
+    const bool quantised = launch_moe_sort(
+        topk_ids, topk_weights, expert_mask, num_local_tokens, sorted_ids, sorted_w, sorted_eids,
+        num_valid, part ? nullptr : acc, model_dim * 4, tokens, topk, E_sort, block_m,
+        ws + L.off_sort_ws, L.sort_ws_bytes, s, hidden_states, (int)hidden_dtype, a1, a1_scale,
+        model_dim);
+    if (!quantised)
+        launch_per_group_quant_fp8(hidden_states, hidden_dtype, a1, a1_scale, tokens, model_dim,
+                                   0, num_local_tokens, 1, s);
     const int sh = (int)(w_shuffled != 0);
     // doweight_stage1: the routing weights scale stage 1's gate and up, stage 2 sums unweighted
     const bool dw = doweight_stage1 != 0;

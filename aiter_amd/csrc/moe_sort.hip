@@ -31,6 +31,7 @@
 // for the segment layout) and writes its pairs -- the prefix is recomputed
 // by every block in parallel instead of by a serial scan launch.
 #include "common.h"
+#include "quant_dev.h"
 
 namespace aiter_amd {
 
@@ -56,6 +57,17 @@ struct SortParams {
     int cell_bytes;             // 1 when topk <= 8 (u8 slot masks), else 4
     int num_chunks;
     int sort_blocks;            // blocks of the launch doing sorting work
+    int zero_blocks;            // then blocks clearing zero_buf
+    // optional 1x128 fp8 quant of the activations (one-shot launch only), run
+    // by q_blocks blocks after the zero blocks
+    const uint16_t* qx;
+    uint8_t* qq;
+    float* qs;
+    const int32_t* q_num_rows;
+    int64_t q_rows;
+    int q_cols;
+    int q_bf16;
+    int q_blocks;
 };
 
 __host__ __device__ inline int table_words(int ct, int E, int cell_bytes) {
@@ -328,7 +340,15 @@ __global__ __launch_bounds__(kSortThreads) void moe_sort_oneshot_kernel(SortPara
     extern __shared__ uint32_t smem[];
     const int tokens = sort_tokens(p);
     if ((int)blockIdx.x >= p.sort_blocks) {
-        zero_rows(p, tokens, blockIdx.x - p.sort_blocks, gridDim.x - p.sort_blocks);
+        const int b = (int)blockIdx.x - p.sort_blocks;
+        if (b < p.zero_blocks)
+            zero_rows(p, tokens, b, p.zero_blocks);
+        else if (p.q_bf16)
+            quant_groups_block<true>(p.qx, p.qq, p.qs, p.q_rows, p.q_cols, 0, p.q_num_rows, 1,
+                                     b - p.zero_blocks);
+        else
+            quant_groups_block<false>(p.qx, p.qq, p.qs, p.q_rows, p.q_cols, 0, p.q_num_rows, 1,
+                                      b - p.zero_blocks);
         return;
     }
     const SortLds L = carve_lds(p, smem);
@@ -431,11 +451,16 @@ int64_t sort_workspace_bytes(int64_t rows, int64_t topk, int64_t E) {
     return chunks * E * 4;
 }
 
-void launch_moe_sort(const int32_t* topk_ids, const float* topk_w, const int32_t* expert_mask,
+// Returns true when the launch also ran the activation quant given by qx
+// (rows x q_cols, bf16 or fp16, scales row-major, num_rows = local_tokens):
+// the one-shot path does, in extra blocks; the multi-chunk path leaves it to
+// the caller.
+bool launch_moe_sort(const int32_t* topk_ids, const float* topk_w, const int32_t* expert_mask,
                      const int32_t* local_tokens, int32_t* sorted_ids, float* sorted_w,
                      int32_t* sorted_eids, int32_t* num_valid, void* zero_buf,
                      int64_t zero_row_bytes, int64_t rows, int64_t topk, int64_t E, int64_t bm,
-                     void* ws, int64_t ws_bytes, hipStream_t stream) {
+                     void* ws, int64_t ws_bytes, hipStream_t stream, const void* qx,
+                     int qx_dtype, uint8_t* qq, float* qs, int64_t q_cols) {
     SortParams p;
     p.topk_ids = topk_ids;
     p.topk_w = topk_w;
@@ -455,6 +480,14 @@ void launch_moe_sort(const int32_t* topk_ids, const float* topk_w, const int32_t
     p.cell_bytes = topk <= 8 ? 1 : 4;
     p.num_chunks = (int)ceil_div(rows > 0 ? rows : 1, p.ct);
     p.ws = reinterpret_cast<int32_t*>(ws);
+    p.qx = nullptr;
+    p.qq = nullptr;
+    p.qs = nullptr;
+    p.q_num_rows = nullptr;
+    p.q_rows = 0;
+    p.q_cols = 0;
+    p.q_bf16 = 0;
+    p.q_blocks = 0;
 
     // zero blocks: about one 16-byte store per thread per 4 iterations
     int zero_blocks = 0;
@@ -466,10 +499,23 @@ void launch_moe_sort(const int32_t* topk_ids, const float* topk_w, const int32_t
     const size_t table_lds = (size_t)table_words(p.ct, (int)E, p.cell_bytes) * 4;
     const size_t full_lds =
         table_lds + (size_t)p.ct * p.topk * 4 + (size_t)(5 * E + kSortThreads / 64) * 4;
+    p.zero_blocks = zero_blocks;
+    bool quant_done = false;
     if (p.num_chunks == 1) {
         p.sort_blocks = 1;
-        hipLaunchKernelGGL(moe_sort_oneshot_kernel, dim3(1 + zero_blocks), dim3(kSortThreads),
-                           full_lds, stream, p);
+        if (qx && rows > 0 && q_cols >= 128) {
+            p.qx = reinterpret_cast<const uint16_t*>(qx);
+            p.qq = qq;
+            p.qs = qs;
+            p.q_num_rows = local_tokens;
+            p.q_rows = rows;
+            p.q_cols = (int)q_cols;
+            p.q_bf16 = qx_dtype == DT_BF16;
+            p.q_blocks = (int)ceil_div(rows * (q_cols / 128), kQuantThreads / 16);
+            quant_done = true;
+        }
+        hipLaunchKernelGGL(moe_sort_oneshot_kernel, dim3(1 + zero_blocks + p.q_blocks),
+                           dim3(kSortThreads), full_lds, stream, p);
     } else {
         AMD_CHECK(ws != nullptr && ws_bytes >= sort_workspace_bytes(rows, topk, E),
                   "sorting workspace too small");
@@ -480,6 +526,7 @@ void launch_moe_sort(const int32_t* topk_ids, const float* topk_w, const int32_t
                            full_lds, stream, p);
     }
     AMD_HIP_CHECK(hipGetLastError());
+    return quant_done;
 }
 
 }  // namespace aiter_amd

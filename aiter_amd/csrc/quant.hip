@@ -15,63 +15,17 @@
 // group; a 256-thread block quantises 16 groups; the group amax is a 4-step
 // xor-shuffle inside the 16-lane quarter of the wave.
 #include "common.h"
+#include "quant_dev.h"
 
 namespace aiter_amd {
-
-constexpr int kQuantThreads = 256;
 
 template <bool kBf16>
 __global__ __launch_bounds__(kQuantThreads) void per_group_quant_fp8_kernel(
     const uint16_t* __restrict__ x, uint8_t* __restrict__ q, float* __restrict__ scale,
     int64_t rows, int cols, int transpose_scale, const int32_t* __restrict__ num_rows,
     int num_rows_factor) {
-    int64_t rows_eff = rows;
-    if (num_rows) {
-        int64_t r = (int64_t)num_rows[0] * num_rows_factor;
-        rows_eff = r < 0 ? 0 : (r < rows ? r : rows);
-    }
-    const int G = cols / 128;
-    const int64_t g = (int64_t)blockIdx.x * (kQuantThreads / 16) + (threadIdx.x >> 4);
-    const int sub = threadIdx.x & 15;
-    const int64_t row = g / G;
-    const int gc = (int)(g - row * G);
-    const bool active = row < rows_eff;
-    const int64_t off = row * cols + (int64_t)gc * 128 + sub * 8;
-
-    float v[8];
-    float amax = 1e-10f;
-    if (active) {
-        v4i raw = *reinterpret_cast<const v4i*>(x + off);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            uint32_t w = (uint32_t)raw[i];
-            if (kBf16) {
-                v[2 * i] = bf16_bits_to_f32((uint16_t)(w & 0xFFFFu));
-                v[2 * i + 1] = bf16_bits_to_f32((uint16_t)(w >> 16));
-            } else {
-                v[2 * i] = fp16_bits_to_f32((uint16_t)(w & 0xFFFFu));
-                v[2 * i + 1] = fp16_bits_to_f32((uint16_t)(w >> 16));
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[i]));
-    }
-    amax = warp_max_16(amax);
-    if (!active) return;
-    const float s = amax * kInvFp8Max;
-    const float inv = 1.0f / s;
-    uint32_t lo = f32x4_to_fp8x4(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv);
-    uint32_t hi = f32x4_to_fp8x4(v[4] * inv, v[5] * inv, v[6] * inv, v[7] * inv);
-    uint2 packed;
-    packed.x = lo;
-    packed.y = hi;
-    *reinterpret_cast<uint2*>(q + off) = packed;
-    if (sub == 0) {
-        if (transpose_scale)
-            scale[(int64_t)gc * rows_eff + row] = s;
-        else
-            scale[row * G + gc] = s;
-    }
+    quant_groups_block<kBf16>(x, q, scale, rows, cols, transpose_scale, num_rows,
+                              num_rows_factor, (int64_t)blockIdx.x);
 }
 
 void launch_per_group_quant_fp8(const void* x, int x_dtype, void* q, float* scale, int64_t rows,
