@@ -370,7 +370,15 @@ __global__ __launch_bounds__(kSortThreads) void moe_sort_count_kernel(SortParams
     extern __shared__ uint32_t smem[];
     const int tokens = sort_tokens(p);
     if ((int)blockIdx.x >= p.sort_blocks) {
-        zero_rows(p, tokens, blockIdx.x - p.sort_blocks, gridDim.x - p.sort_blocks);
+        const int b = (int)blockIdx.x - p.sort_blocks;
+        if (b < p.zero_blocks)
+            zero_rows(p, tokens, b, p.zero_blocks);
+        else if (p.q_bf16)
+            quant_groups_block<true>(p.qx, p.qq, p.qs, p.q_rows, p.q_cols, 0, p.q_num_rows, 1,
+                                     b - p.zero_blocks);
+        else
+            quant_groups_block<false>(p.qx, p.qq, p.qs, p.q_rows, p.q_cols, 0, p.q_num_rows, 1,
+                                      b - p.zero_blocks);
         return;
     }
     const int c = blockIdx.x;
@@ -452,9 +460,8 @@ int64_t sort_workspace_bytes(int64_t rows, int64_t topk, int64_t E) {
 }
 
 // Returns true when the launch also ran the activation quant given by qx
-// (rows x q_cols, bf16 or fp16, scales row-major, num_rows = local_tokens):
-// the one-shot path does, in extra blocks; the multi-chunk path leaves it to
-// the caller.
+// (rows x q_cols, bf16 or fp16, scales row-major, num_rows = local_tokens),
+// in extra blocks of the one-shot or the counting launch.
 bool launch_moe_sort(const int32_t* topk_ids, const float* topk_w, const int32_t* expert_mask,
                      const int32_t* local_tokens, int32_t* sorted_ids, float* sorted_w,
                      int32_t* sorted_eids, int32_t* num_valid, void* zero_buf,
@@ -500,27 +507,30 @@ bool launch_moe_sort(const int32_t* topk_ids, const float* topk_w, const int32_t
     const size_t full_lds =
         table_lds + (size_t)p.ct * p.topk * 4 + (size_t)(5 * E + kSortThreads / 64) * 4;
     p.zero_blocks = zero_blocks;
+    // the activation quant rides in the first launch's extra blocks
     bool quant_done = false;
+    if (qx && rows > 0 && q_cols >= 128) {
+        const int64_t qb = ceil_div(rows * (q_cols / 128), kQuantThreads / 16);
+        AMD_CHECK(qb < (1ll << 30), "too many rows to quantise");
+        p.qx = reinterpret_cast<const uint16_t*>(qx);
+        p.qq = qq;
+        p.qs = qs;
+        p.q_num_rows = local_tokens;
+        p.q_rows = rows;
+        p.q_cols = (int)q_cols;
+        p.q_bf16 = qx_dtype == DT_BF16;
+        p.q_blocks = (int)qb;
+        quant_done = true;
+    }
     if (p.num_chunks == 1) {
         p.sort_blocks = 1;
-        if (qx && rows > 0 && q_cols >= 128) {
-            p.qx = reinterpret_cast<const uint16_t*>(qx);
-            p.qq = qq;
-            p.qs = qs;
-            p.q_num_rows = local_tokens;
-            p.q_rows = rows;
-            p.q_cols = (int)q_cols;
-            p.q_bf16 = qx_dtype == DT_BF16;
-            p.q_blocks = (int)ceil_div(rows * (q_cols / 128), kQuantThreads / 16);
-            quant_done = true;
-        }
         hipLaunchKernelGGL(moe_sort_oneshot_kernel, dim3(1 + zero_blocks + p.q_blocks),
                            dim3(kSortThreads), full_lds, stream, p);
     } else {
         AMD_CHECK(ws != nullptr && ws_bytes >= sort_workspace_bytes(rows, topk, E),
                   "sorting workspace too small");
         p.sort_blocks = p.num_chunks;
-        hipLaunchKernelGGL(moe_sort_count_kernel, dim3(p.num_chunks + zero_blocks),
+        hipLaunchKernelGGL(moe_sort_count_kernel, dim3(p.num_chunks + zero_blocks + p.q_blocks),
                            dim3(kSortThreads), (size_t)E * 4, stream, p);
         hipLaunchKernelGGL(moe_sort_scatter_kernel, dim3(p.num_chunks), dim3(kSortThreads),
                            full_lds, stream, p);
