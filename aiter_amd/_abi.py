@@ -72,6 +72,11 @@ _SIGNATURES = {
         [c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_i64, c_i64,
          c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp],
     ),
+    "aiter_amd_fused_moe_fp8_blockscale_noalloc": (
+        c_int,
+        [c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_i64, c_i64,
+         c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_vp],
+    ),
     "aiter_amd_fused_moe_a8w4": (
         c_int,
         [c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_i64, c_i64,

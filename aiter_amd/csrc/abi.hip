@@ -5,6 +5,7 @@
 #include "../../include/aiter_amd.h"
 
 #include <algorithm>
+#include <mutex>
 #include <string>
 
 #include "common.h"
@@ -393,6 +394,34 @@ void fused_entry(const void* hidden_states, int hidden_dtype, const void* w1, WS
         launch_acc_to_out(acc, out, out_dtype, num_valid, tokens, model_dim, s);
 }
 
+// ---- the library's own device workspace for callers that cannot allocate ----
+// One copy per GPU the library runs on, held until the process ends. In host
+// code `scratch` names a host-side stand-in, not device memory: the device
+// address of each GPU's copy comes from hipGetSymbolAddress with that GPU
+// current, and only that address is ever handed to kernels.
+constexpr int64_t kScratchBytes = AITER_AMD_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices];
+
+// Device address of the current GPU's scratch copy, looked up on the first
+// call per device and cached.
+void* device_scratch() {
+    int dev = -1;
+    AMD_HIP_CHECK(hipGetDevice(&dev));
+    AMD_CHECK(dev >= 0 && dev < kMaxDevices, "device ordinal out of range");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        AMD_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        AMD_CHECK(p != nullptr, "hipGetSymbolAddress returned NULL for the scratch buffer");
+        g_scratch_ptr[dev] = p;
+    }
+    return g_scratch_ptr[dev];
+}
+
 }  // namespace
 }  // namespace aiter_amd
 
@@ -583,6 +612,51 @@ int aiter_amd_fused_moe_fp8_blockscale(const void* hidden_states, int hidden_dty
                     num_local_tokens, out, out_dtype, tokens, model_dim, inter_dim, num_experts,
                     global_experts, topk, block_m, activation, doweight_stage1, w_shuffled, workspace,
                     workspace_bytes, stream);
+    });
+}
+
+int aiter_amd_fused_moe_fp8_blockscale_noalloc(
+    const void* hidden_states, int hidden_dtype, const void* w1, const float* w1_scale,
+    const void* w2, const float* w2_scale, const float* topk_weights, const int32_t* topk_ids,
+    const int32_t* expert_mask, const int32_t* num_local_tokens, void* out, int out_dtype,
+    int64_t tokens, int64_t model_dim, int64_t inter_dim, int64_t num_experts,
+    int64_t global_experts, int64_t topk, int64_t block_m, int64_t activation,
+    int64_t doweight_stage1, int64_t w_shuffled, void* stream) {
+    return safe_call([&] {
+        AMD_CHECK(w1_scale && w2_scale, "a required pointer is NULL");
+        check_dims(model_dim, inter_dim);
+        check_topk_experts(tokens, topk, num_experts);
+        const int64_t E_sort = expert_mask ? global_experts : num_experts;
+        AMD_CHECK(E_sort >= num_experts && E_sort <= kMaxExperts,
+                  "global_experts must be in [num_experts, 4096]");
+        const int64_t bm =
+            block_m > 0 ? block_m
+                        : default_block_m(tokens, topk, num_experts, model_dim, inter_dim);
+        check_block_m_gemm(bm, model_dim, inter_dim, tokens, topk);
+        const int64_t need = fused_layout(tokens, model_dim, inter_dim, E_sort, topk, bm).total;
+        AMD_CHECK(need <= kScratchBytes,
+                  "this layer needs " + std::to_string(need) + " bytes of workspace; the "
+                  "no-alloc entry point holds " + std::to_string(kScratchBytes) +
+                  " (AITER_AMD_SCRATCH_BYTES): pass a workspace to "
+                  "aiter_amd_fused_moe_fp8_blockscale instead");
+        if (tokens == 0) return;
+        // the stream must belong to the current device, whose scratch copy is used
+        if (stream) {
+            hipDevice_t sdev;
+            int cur = -1;
+            AMD_HIP_CHECK(hipStreamGetDevice((hipStream_t)stream, &sdev));
+            AMD_HIP_CHECK(hipGetDevice(&cur));
+            AMD_CHECK((int)sdev == cur, "stream belongs to device " + std::to_string(sdev) +
+                                            ", the current device is " + std::to_string(cur));
+        }
+        // every section the layer reads before writing (the f32 accumulator)
+        // is cleared by the sorting launch on each call, so a previous call's
+        // contents never leak into this one
+        fused_entry(hidden_states, hidden_dtype, w1, WScale{w1_scale, nullptr}, w2,
+                    WScale{w2_scale, nullptr}, topk_weights, topk_ids, expert_mask,
+                    num_local_tokens, out, out_dtype, tokens, model_dim, inter_dim, num_experts,
+                    global_experts, topk, bm, activation, doweight_stage1, w_shuffled,
+                    device_scratch(), kScratchBytes, stream);
     });
 }
 

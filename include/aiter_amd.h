@@ -183,6 +183,31 @@ int aiter_amd_fused_moe_fp8_blockscale(const void* hidden_states, int hidden_dty
                                        int64_t w_shuffled, void* workspace,
                                        int64_t workspace_bytes, void* stream);
 
+/* Bytes of the library-owned device workspace behind
+ * aiter_amd_fused_moe_fp8_blockscale_noalloc (one copy per GPU). */
+#define AITER_AMD_SCRATCH_BYTES (32ll << 20)
+
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture that must not allocate, tight serving
+ * loops, harnesses that forbid hipMalloc): aiter_amd_fused_moe_fp8_blockscale
+ * with its workspace taken from a static device buffer of
+ * AITER_AMD_SCRATCH_BYTES that the library holds per GPU until the process
+ * ends.  It calls no hipMalloc / hipFree.  A layer whose workspace
+ * (aiter_amd_fused_moe_workspace_bytes) exceeds the buffer is rejected with
+ * an error; at MiMo dims (hidden 4096, inter 2048, 256 experts, top-8) that
+ * is above ~370 tokens.  The stream must belong to the current device.
+ * Every call on one GPU shares that GPU's buffer: calls that overlap on one
+ * GPU (other streams, other threads) race and must be serialised by the
+ * caller.  The buffer keeps the last call's contents; the call itself clears
+ * what it reads before writing. */
+int aiter_amd_fused_moe_fp8_blockscale_noalloc(
+    const void* hidden_states, int hidden_dtype, const void* w1, const float* w1_scale,
+    const void* w2, const float* w2_scale, const float* topk_weights, const int32_t* topk_ids,
+    const int32_t* expert_mask, const int32_t* num_local_tokens, void* out, int out_dtype,
+    int64_t tokens, int64_t model_dim, int64_t inter_dim, int64_t num_experts,
+    int64_t global_experts, int64_t topk, int64_t block_m, int64_t activation,
+    int64_t doweight_stage1, int64_t w_shuffled, void* stream);
+
 /* The whole 2-stage A8W4 MoE in one call: fused_moe_ with quant_type per_1x32
  * and fp4x2 weights (aiter/fused_moe.py:255-275, 1103-1334), fp8 1x128
  * activations.  Arguments as aiter_amd_fused_moe_fp8_blockscale with the

@@ -342,3 +342,25 @@ def test_tuned_dispatch_table():
     assert T.tuned_block_m(256, 32, 4096, 2048, 256, 8, "per_1x32", "fp4x2") in (16, 32, 64, 128)
     assert T.tuned_block_m(304, 32, 4096, 2048, 256, 8, "per_1x128", "fp8") is None
     assert T.tuned_block_m(256, 32, 1024, 512, 8, 2, "per_1x128", "fp8") is None
+
+
+def test_no_alloc_rejects_layers_over_the_buffer():
+    """The size check comes before any device work: placeholder pointers are
+    never dereferenced."""
+    from aiter_amd import workloads as W
+    from aiter_amd.enums import AITER_DTYPE
+
+    cfg = W.mimo_prefill(2048)
+    need = _abi.query("aiter_amd_fused_moe_workspace_bytes", cfg.tokens, cfg.model_dim,
+                      cfg.inter_dim, cfg.experts, cfg.topk, 128)
+    assert need > 32 << 20
+    lib = _abi.load()
+    p = 256
+    rc = lib.aiter_amd_fused_moe_fp8_blockscale_noalloc(
+        p, AITER_DTYPE[torch.bfloat16], p, p, p, p, p, p, None, None, p,
+        AITER_DTYPE[torch.bfloat16], cfg.tokens, cfg.model_dim, cfg.inter_dim, cfg.experts,
+        cfg.experts, cfg.topk, 128, 0, 0, 1, ctypes.c_void_p(0))
+    assert rc == -1
+    msg = lib.aiter_amd_get_last_error().decode()
+    lib.aiter_amd_clear_last_error()
+    assert "bytes of workspace" in msg, msg
