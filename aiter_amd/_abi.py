@@ -16,7 +16,7 @@ _LIB_PATH = Path(__file__).resolve().parent / "libaiter_amd.so"
 _lock = threading.Lock()
 _lib = None
 
-ABI_VERSION = 2   # AITER_AMD_ABI_VERSION of include/aiter_amd.h
+ABI_VERSION = 3   # AITER_AMD_ABI_VERSION of include/aiter_amd.h
 
 c_i32p = ctypes.c_void_p
 c_vp = ctypes.c_void_p
@@ -52,8 +52,8 @@ _SIGNATURES = {
     ),
     "aiter_amd_moe_stage2_fp8_blockscale": (
         c_int,
-        [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64,
-         c_i64, c_i64, c_i64, c_i64, c_vp],
+        [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_i64, c_i64, c_i64,
+         c_i64, c_i64, c_i64, c_i64, c_i64, c_vp],
     ),
     "aiter_amd_moe_stage1_a8w4": (
         c_int,
@@ -62,11 +62,11 @@ _SIGNATURES = {
     ),
     "aiter_amd_moe_stage2_a8w4": (
         c_int,
-        [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64,
-         c_i64, c_i64, c_i64, c_i64, c_vp],
+        [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_i64, c_i64, c_i64,
+         c_i64, c_i64, c_i64, c_i64, c_i64, c_vp],
     ),
     "aiter_amd_moe_acc_to_out": (c_int, [c_vp, c_vp, c_int, c_vp, c_i64, c_i64, c_vp]),
-    "aiter_amd_fused_moe_workspace_bytes": (c_i64, [c_i64, c_i64, c_i64, c_i64, c_i64, c_i64]),
+    "aiter_amd_fused_moe_workspace_bytes": (c_i64, [c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64]),
     "aiter_amd_fused_moe_fp8_blockscale": (
         c_int,
         [c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_i64, c_i64,

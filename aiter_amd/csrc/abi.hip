@@ -3,6 +3,7 @@
 // dispatch to the kernel launchers.  Declarations and the reference
 // interface each entry point replaces are in include/aiter_amd.h.
 #include "../../include/aiter_amd.h"
+#include "../../include/aiter_ctypes.h"
 
 #include <algorithm>
 #include <mutex>
@@ -15,6 +16,7 @@ namespace aiter_amd {
 static thread_local std::string g_last_error;
 
 void set_last_error(const std::string& msg) { g_last_error = msg; }
+void clear_last_error() { g_last_error.clear(); }
 
 // launchers (moe_sort.hip, quant.hip, moe_gemm_fp8bs.hip)
 int64_t sort_workspace_bytes(int64_t rows, int64_t topk, int64_t E);
@@ -37,7 +39,7 @@ void launch_moe_stage1_fp8bs(const uint8_t*, const float*, int64_t, int64_t, con
                              const float*, int);
 void launch_moe_stage2_fp8bs(const uint8_t*, const float*, const uint8_t*, const float*,
                              const uint8_t*, const int32_t*, const float*, const int32_t*,
-                             const int32_t*, float*, int64_t, int64_t, int64_t, int64_t, int64_t,
+                             const int32_t*, void*, int, int64_t, int64_t, int64_t, int64_t, int64_t,
                              int64_t, int64_t, int, hipStream_t);
 // moe_gemm_fp8bs_v2.hip (64/128-row M-blocks)
 bool v2_supported(int64_t block_m, int64_t K);
@@ -48,7 +50,7 @@ void launch_moe_stage1_fp8bs_v2(const uint8_t*, const float*, int64_t, int64_t, 
                              const float*, int);
 void launch_moe_stage2_fp8bs_v2(const uint8_t*, const float*, const uint8_t*, const float*,
                                 const uint8_t*, const int32_t*, const float*, const int32_t*,
-                                const int32_t*, float*, int64_t, int64_t, int64_t, int64_t,
+                                const int32_t*, void*, int, int64_t, int64_t, int64_t, int64_t,
                                 int64_t, int64_t, int64_t, int, hipStream_t);
 
 // moe_gemm_stream.hip (16/32-row M-blocks, weights streamed into registers)
@@ -60,7 +62,7 @@ void launch_moe_stage1_stream(const uint8_t*, const float*, int64_t, int64_t, co
                              const float*, int);
 void launch_moe_stage2_stream(const uint8_t*, const float*, const uint8_t*, const float*,
                               const uint8_t*, const int32_t*, const float*, const int32_t*,
-                              const int32_t*, float*, int64_t, int64_t, int64_t, int64_t,
+                              const int32_t*, void*, int, int64_t, int64_t, int64_t, int64_t,
                               int64_t, int64_t, int64_t, int, hipStream_t);
 
 // quant.hip: per-pair bf16 rows -> output
@@ -84,7 +86,7 @@ void launch_moe_stage1_prefill(const uint8_t*, const float*, int64_t, int64_t, c
                              const float*, int);
 void launch_moe_stage2_prefill(const uint8_t*, const float*, const uint8_t*, const float*,
                                const uint8_t*, const int32_t*, const float*, const int32_t*,
-                               const int32_t*, float*, uint16_t*, int64_t, int64_t, int64_t,
+                               const int32_t*, void*, int, uint16_t*, int64_t, int64_t, int64_t,
                                int64_t, int64_t, int64_t, int64_t, int, hipStream_t, int64_t);
 
 // The 64/128-row kernels (prefill, v2) read their activation operand through
@@ -137,32 +139,33 @@ static bool stage2_on_prefill(int64_t bm, int64_t I, int64_t H, WScale w2s, int6
            H % 256 == 0 && (!w2s.e8m0 || bm == 128);
 }
 
-// acc: fp32 [tokens, H] accumulated atomically; part (prefill kernel only):
-// bf16 [pairs, H] rows written once each, acc unused.
+// acc: [tokens, H] accumulated atomically, fp32 or (the reference's moe_buf)
+// bf16 / fp16 by acc_dtype; part (prefill kernel only): bf16 [pairs, H] rows
+// written once each, acc unused.
 // est_pairs: the pairs expected on this GPU (the EP share's fraction of
 // tokens * topk when the caller knows it), a launch-shape hint only.
 static void stage2_dispatch(const uint8_t* a2, const float* a2s, const uint8_t* w2,
                             WScale w2s, const int32_t* sid, const float* sw,
-                            const int32_t* seid, const int32_t* nv, float* acc, int64_t a_rows,
-                            int64_t I, int64_t H, int64_t E, int64_t topk, int64_t bm,
-                            int64_t mblocks, int sh, hipStream_t s, uint16_t* part = nullptr,
-                            int64_t est_pairs = -1) {
+                            const int32_t* seid, const int32_t* nv, void* acc, int acc_dtype,
+                            int64_t a_rows, int64_t I, int64_t H, int64_t E, int64_t topk,
+                            int64_t bm, int64_t mblocks, int sh, hipStream_t s,
+                            uint16_t* part = nullptr, int64_t est_pairs = -1) {
     AMD_CHECK(!part || stage2_on_prefill(bm, I, H, w2s, a_rows),
               "per-pair rows need the prefill kernel");
     if (stream_supported(bm, I) && H % 256 == 0)
-        launch_moe_stage2_stream(a2, a2s, w2, w2s.f32, w2s.e8m0, sid, sw, seid, nv, acc, a_rows,
-                                 I, H, E, topk, bm, mblocks, sh, s);
+        launch_moe_stage2_stream(a2, a2s, w2, w2s.f32, w2s.e8m0, sid, sw, seid, nv, acc,
+                                 acc_dtype, a_rows, I, H, E, topk, bm, mblocks, sh, s);
     else if (prefill_supported(bm, I) && H % 256 == 0 && (!w2s.e8m0 || bm == 128) &&
              a_fits32(a_rows, I))
-        launch_moe_stage2_prefill(a2, a2s, w2, w2s.f32, w2s.e8m0, sid, sw, seid, nv, acc, part,
-                                  a_rows, I, H, E, topk, bm, mblocks, sh, s,
+        launch_moe_stage2_prefill(a2, a2s, w2, w2s.f32, w2s.e8m0, sid, sw, seid, nv, acc,
+                                  acc_dtype, part, a_rows, I, H, E, topk, bm, mblocks, sh, s,
                                   est_pairs < 0 ? a_rows : est_pairs);
     else if (v2_supported(bm, I) && H % 256 == 0 && a_fits32(a_rows, I))
-        launch_moe_stage2_fp8bs_v2(a2, a2s, w2, w2s.f32, w2s.e8m0, sid, sw, seid, nv, acc, a_rows,
-                                   I, H, E, topk, bm, mblocks, sh, s);
+        launch_moe_stage2_fp8bs_v2(a2, a2s, w2, w2s.f32, w2s.e8m0, sid, sw, seid, nv, acc,
+                                   acc_dtype, a_rows, I, H, E, topk, bm, mblocks, sh, s);
     else
-        launch_moe_stage2_fp8bs(a2, a2s, w2, w2s.f32, w2s.e8m0, sid, sw, seid, nv, acc, a_rows, I,
-                                H, E, topk, bm, mblocks, sh, s);
+        launch_moe_stage2_fp8bs(a2, a2s, w2, w2s.f32, w2s.e8m0, sid, sw, seid, nv, acc,
+                                acc_dtype, a_rows, I, H, E, topk, bm, mblocks, sh, s);
 }
 
 namespace {
@@ -299,11 +302,13 @@ void stage1_entry(const void* a1, const float* a1_scale, int64_t a1_scale_transp
 
 void stage2_entry(const void* a2, const float* a2_scale, const void* w2, WScale w2s,
                   const int32_t* sorted_ids, const float* sorted_weights,
-                  const int32_t* sorted_expert_ids, const int32_t* num_valid_ids, float* out_acc,
-                  int64_t tokens, int64_t model_dim, int64_t inter_dim, int64_t num_experts,
-                  int64_t topk, int64_t block_m, int64_t max_m_blocks, int64_t w_shuffled,
-                  void* stream) {
+                  const int32_t* sorted_expert_ids, const int32_t* num_valid_ids, void* out_acc,
+                  int out_dtype, int64_t tokens, int64_t model_dim, int64_t inter_dim,
+                  int64_t num_experts, int64_t topk, int64_t block_m, int64_t max_m_blocks,
+                  int64_t w_shuffled, void* stream) {
     check_dims(model_dim, inter_dim);
+    AMD_CHECK(out_dtype == DT_FP32 || out_dtype == DT_BF16 || out_dtype == DT_FP16,
+              "stage-2 output dtype must be fp32, bf16 or fp16");
     check_topk_experts(tokens, topk, num_experts);
     check_block_m_gemm(block_m, model_dim, inter_dim, tokens, topk);
     AMD_CHECK(max_m_blocks >= 0, "max_m_blocks must be >= 0");
@@ -315,7 +320,8 @@ void stage2_entry(const void* a2, const float* a2_scale, const void* w2, WScale 
     AMD_CHECK(a2_scale && sorted_ids && sorted_expert_ids && num_valid_ids,
               "a required pointer is NULL");
     stage2_dispatch((const uint8_t*)a2, a2_scale, (const uint8_t*)w2, w2s, sorted_ids,
-                    sorted_weights, sorted_expert_ids, num_valid_ids, out_acc, tokens * topk,
+                    sorted_weights, sorted_expert_ids, num_valid_ids, out_acc, out_dtype,
+                    tokens * topk,
                     inter_dim, model_dim, num_experts, topk, block_m, max_m_blocks,
                     (int)(w_shuffled != 0), (hipStream_t)stream);
 }
@@ -347,10 +353,10 @@ void fused_entry(const void* hidden_states, int hidden_dtype, const void* w1, WS
     check_ptr(out, "out");
     AMD_CHECK(topk_weights && topk_ids, "a required pointer is NULL");
     const FusedLayout L = fused_layout(tokens, model_dim, inter_dim, E_sort, topk, block_m);
-    check_ptr(workspace, "workspace");
     AMD_CHECK(workspace_bytes >= L.total, "workspace of " + std::to_string(L.total) +
                                               " bytes required, got " +
                                               std::to_string(workspace_bytes));
+    check_ptr(workspace, "workspace");
     uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
     int32_t* sorted_ids = reinterpret_cast<int32_t*>(ws + L.off_sorted_ids);
     float* sorted_w = reinterpret_cast<float*>(ws + L.off_sorted_w);
@@ -384,7 +390,7 @@ void fused_entry(const void* hidden_states, int hidden_dtype, const void* w1, WS
                     (int)activation);
     stage2_dispatch(a2, a2_scale, (const uint8_t*)w2, w2s, sorted_ids, dw ? nullptr : sorted_w,
                     sorted_eids,
-                    num_valid, part ? nullptr : acc, tokens * topk, inter_dim, model_dim,
+                    num_valid, part ? nullptr : acc, DT_FP32, tokens * topk, inter_dim, model_dim,
                     num_experts, topk, block_m, L.blocks, sh, s, part,
                     tokens * topk * num_experts / E_sort);
     if (part)
@@ -434,6 +440,16 @@ int aiter_amd_abi_version(void) { return AITER_AMD_ABI_VERSION; }
 const char* aiter_amd_get_last_error(void) { return g_last_error.c_str(); }
 
 void aiter_amd_clear_last_error(void) { g_last_error.clear(); }
+
+// the reference's names for the same error state (aiter_ctypes_error.h:60-72):
+// version 2 is its status-return convention, and no error reads as NULL
+int aiter_ctypes_abi_version(void) { return 2; }
+
+const char* aiter_get_last_error(void) {
+    return g_last_error.empty() ? nullptr : g_last_error.c_str();
+}
+
+void aiter_clear_last_error(void) { g_last_error.clear(); }
 
 int64_t aiter_amd_moe_sorting_workspace_bytes(int64_t tokens, int64_t topk, int64_t num_experts) {
     if (tokens < 0 || topk < 1 || num_experts < 1) return 0;
@@ -545,30 +561,30 @@ int aiter_amd_moe_stage2_fp8_blockscale(const void* a2, const float* a2_scale, c
                                         const float* w2_scale, const int32_t* sorted_ids,
                                         const float* sorted_weights,
                                         const int32_t* sorted_expert_ids,
-                                        const int32_t* num_valid_ids, float* out_acc,
+                                        const int32_t* num_valid_ids, void* out_acc, int out_dtype,
                                         int64_t tokens, int64_t model_dim, int64_t inter_dim,
                                         int64_t num_experts, int64_t topk, int64_t block_m,
                                         int64_t max_m_blocks, int64_t w_shuffled, void* stream) {
     return safe_call([&] {
         AMD_CHECK(w2_scale != nullptr, "w2_scale is NULL");
         stage2_entry(a2, a2_scale, w2, WScale{w2_scale, nullptr}, sorted_ids, sorted_weights,
-                     sorted_expert_ids, num_valid_ids, out_acc, tokens, model_dim, inter_dim,
-                     num_experts, topk, block_m, max_m_blocks, w_shuffled, stream);
+                     sorted_expert_ids, num_valid_ids, out_acc, out_dtype, tokens, model_dim,
+                     inter_dim, num_experts, topk, block_m, max_m_blocks, w_shuffled, stream);
     });
 }
 
 int aiter_amd_moe_stage2_a8w4(const void* a2, const float* a2_scale, const void* w2,
                               const uint8_t* w2_scale, const int32_t* sorted_ids,
                               const float* sorted_weights, const int32_t* sorted_expert_ids,
-                              const int32_t* num_valid_ids, float* out_acc, int64_t tokens,
+                              const int32_t* num_valid_ids, void* out_acc, int out_dtype, int64_t tokens,
                               int64_t model_dim, int64_t inter_dim, int64_t num_experts,
                               int64_t topk, int64_t block_m, int64_t max_m_blocks,
                               int64_t w_shuffled, void* stream) {
     return safe_call([&] {
         check_e8m0(w2_scale, "w2_scale");
         stage2_entry(a2, a2_scale, w2, WScale{nullptr, w2_scale}, sorted_ids, sorted_weights,
-                     sorted_expert_ids, num_valid_ids, out_acc, tokens, model_dim, inter_dim,
-                     num_experts, topk, block_m, max_m_blocks, w_shuffled, stream);
+                     sorted_expert_ids, num_valid_ids, out_acc, out_dtype, tokens, model_dim,
+                     inter_dim, num_experts, topk, block_m, max_m_blocks, w_shuffled, stream);
     });
 }
 
@@ -588,11 +604,14 @@ int aiter_amd_moe_acc_to_out(const float* acc, void* out, int out_dtype,
 }
 
 int64_t aiter_amd_fused_moe_workspace_bytes(int64_t tokens, int64_t model_dim, int64_t inter_dim,
-                                            int64_t num_experts, int64_t topk, int64_t block_m) {
-    if (tokens < 0 || model_dim <= 0 || inter_dim <= 0 || num_experts < 1 || topk < 1)
+                                            int64_t num_experts, int64_t global_experts,
+                                            int64_t topk, int64_t block_m) {
+    if (tokens < 0 || model_dim <= 0 || inter_dim <= 0 || num_experts < 1 || topk < 1 ||
+        global_experts < num_experts)
         return -1;
+    // the block size the one-call entries resolve, from the local experts
     if (block_m <= 0) block_m = default_block_m(tokens, topk, num_experts, model_dim, inter_dim);
-    return fused_layout(tokens, model_dim, inter_dim, num_experts, topk, block_m).total;
+    return fused_layout(tokens, model_dim, inter_dim, global_experts, topk, block_m).total;
 }
 
 int aiter_amd_fused_moe_fp8_blockscale(const void* hidden_states, int hidden_dtype,

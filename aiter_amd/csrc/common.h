@@ -17,6 +17,7 @@ namespace aiter_amd {
 
 // ---------------------------------------------------------------- errors ---
 void set_last_error(const std::string& msg);
+void clear_last_error();
 
 struct AbiError : public std::runtime_error {
     explicit AbiError(const std::string& m) : std::runtime_error(m) {}
@@ -38,9 +39,11 @@ struct AbiError : public std::runtime_error {
         }                                                                      \
     } while (0)
 
-// Runs `fn` and converts any exception into the thread-local error + -1.
+// Runs `fn` and converts any exception into the thread-local error + -1; a
+// call clears the error left by an earlier one first.
 template <typename F>
 inline int safe_call(F&& fn) {
+    clear_last_error();
     try {
         fn();
         return 0;
@@ -150,6 +153,27 @@ __device__ __forceinline__ float silu_f32(float x) {
 // (and in the unrolled GEMM epilogues needs fewer registers than erff)
 __device__ __forceinline__ float gelu_f32(float x) {
     return 0.5f * x * erfcf(x * -0.70710678118654752f);
+}
+
+// Stage-2 accumulation: adds v to element i of the output, which is fp32
+// (the hardware fp32 atomic) or, as the reference's moe_buf, bf16 / fp16:
+// the packed 16-bit atomic on the aligned pair holding the element, with 0
+// added to its neighbour (x + 0 = x), so every add rounds once to 16 bits.
+typedef __bf16 v2bf16 __attribute__((ext_vector_type(2)));
+typedef _Float16 v2f16 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ void acc_add(void* base, int dtype, int64_t i, float v) {
+    if (dtype == DT_FP32) {
+        unsafeAtomicAdd(reinterpret_cast<float*>(base) + i, v);
+    } else if (dtype == DT_BF16) {
+        const __bf16 b = (__bf16)v, z = (__bf16)0.0f;
+        v2bf16* pair = reinterpret_cast<v2bf16*>(reinterpret_cast<uint16_t*>(base) + (i & ~int64_t(1)));
+        __builtin_amdgcn_global_atomic_fadd_v2bf16(pair, (i & 1) ? v2bf16{z, b} : v2bf16{b, z});
+    } else {
+        const _Float16 h = (_Float16)v, z = (_Float16)0.0f;
+        v2f16* pair = reinterpret_cast<v2f16*>(reinterpret_cast<uint16_t*>(base) + (i & ~int64_t(1)));
+        __builtin_amdgcn_global_atomic_fadd_v2f16(pair, (i & 1) ? v2f16{z, h} : v2f16{h, z});
+    }
 }
 
 // ActivationType values (csrc/include/aiter_enum.h:7-12) the GEMMs apply to gate

@@ -63,7 +63,8 @@ struct GemmArgs {
     const int32_t* num_valid;
     uint8_t* a2;                // stage 1 out: fp8 [T*topk, I]
     float* a2_scale;            // stage 1 out: [T*topk, I/128]
-    float* acc;                 // stage 2 out: fp32 [T, N]
+    void* acc;                  // stage 2 out [T, N]: fp32, bf16 or fp16 (acc_dtype)
+    int acc_dtype;
     int K;
     int N;                      // weight rows per expert (2I or H)
     int inter;                  // I (stage 1)
@@ -303,7 +304,7 @@ __global__ __launch_bounds__(kGemmThreads) void moe_gemm_fp8bs_kernel(GemmArgs g
 #pragma unroll
                 for (int ct = 0; ct < NCT; ++ct) {
                     const int col = n0 + 32 * wv + 16 * ct + lr;
-                    unsafeAtomicAdd(g.acc + t * g.N + col, acc[rt][ct][v] * wgt);
+                    acc_add(g.acc, g.acc_dtype, t * g.N + col, acc[rt][ct][v] * wgt);
                 }
             }
         return;
@@ -447,7 +448,7 @@ void launch_moe_stage2_fp8bs(const uint8_t* a2, const float* a2_scale, const uin
                              const float* w2_scale, const uint8_t* w2_scale_e8m0,
                              const int32_t* sorted_ids,
                              const float* sorted_w, const int32_t* sorted_eids,
-                             const int32_t* num_valid, float* acc, int64_t a_rows, int64_t inter,
+                             const int32_t* num_valid, void* acc, int acc_dtype, int64_t a_rows, int64_t inter,
                              int64_t hidden, int64_t E, int64_t topk, int64_t block_m,
                              int64_t max_m_blocks, int shuffled, hipStream_t stream) {
     GemmArgs g{};
@@ -465,6 +466,7 @@ void launch_moe_stage2_fp8bs(const uint8_t* a2, const float* a2_scale, const uin
     g.a2 = nullptr;
     g.a2_scale = nullptr;
     g.acc = acc;
+    g.acc_dtype = acc_dtype;
     g.K = (int)inter;
     g.N = (int)hidden;
     g.inter = (int)inter;

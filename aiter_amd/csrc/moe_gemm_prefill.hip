@@ -59,7 +59,8 @@ struct Args {
     const int32_t* num_valid;
     uint8_t* a2;
     float* a2_scale;
-    float* acc;
+    void* acc;                 // stage 2 out [T, N]: fp32, bf16 or fp16 (acc_dtype)
+    int acc_dtype;
     uint16_t* part;            // stage 2: bf16 rows [pairs, N] instead of acc (or NULL)
     int K;
     int N;                     // weight rows per expert
@@ -510,10 +511,10 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
                         const int64_t t = s_orow[row];
                         if (t < 0) continue;
                         const float wgt = s_w[row];
-                        float* dst = g.acc + t * g.N + nc + wn * NCT * 16 + lr;
+                        const int64_t dst = t * g.N + nc + wn * NCT * 16 + lr;
 #pragma unroll
                         for (int ct = 0; ct < NCT; ++ct)
-                            unsafeAtomicAdd(dst + ct * 16, acc[rt][ct][v] * wgt);
+                            acc_add(g.acc, g.acc_dtype, dst + ct * 16, acc[rt][ct][v] * wgt);
                     }
             }
             return;
@@ -801,7 +802,7 @@ void launch_moe_stage1_prefill(const uint8_t* a, const float* a_scale, int64_t s
 void launch_moe_stage2_prefill(const uint8_t* a2, const float* a2_scale, const uint8_t* w2,
                                const float* w2_scale, const uint8_t* w2_scale_e8m0,
                                const int32_t* sorted_ids, const float* sorted_w,
-                               const int32_t* sorted_eids, const int32_t* num_valid, float* acc,
+                               const int32_t* sorted_eids, const int32_t* num_valid, void* acc, int acc_dtype,
                                uint16_t* part, int64_t a_rows, int64_t inter, int64_t hidden,
                                int64_t E, int64_t topk, int64_t block_m, int64_t max_m_blocks,
                                int shuffled, hipStream_t stream, int64_t est_pairs) {
@@ -818,6 +819,7 @@ void launch_moe_stage2_prefill(const uint8_t* a2, const float* a2_scale, const u
     g.sorted_eids = sorted_eids;
     g.num_valid = num_valid;
     g.acc = acc;
+    g.acc_dtype = acc_dtype;
     g.part = part;
     g.K = (int)inter;
     g.N = (int)hidden;

@@ -55,7 +55,8 @@ struct Args {
     const int32_t* num_valid;
     uint8_t* a2;
     float* a2_scale;
-    float* acc;
+    void* acc;                 // stage 2 out [T, N]: fp32, bf16 or fp16 (acc_dtype)
+    int acc_dtype;
     int K;
     int N;                     // weight rows per expert
     int inter;
@@ -264,9 +265,10 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
                 const int64_t t = s_orow[row];
                 if (t < 0) continue;
                 const float wgt = s_w[row];
-                float* dst = g.acc + t * g.N + n0 + jt * 256 + 64 * wv + lr;
+                const int64_t dst = t * g.N + n0 + jt * 256 + 64 * wv + lr;
 #pragma unroll
-                for (int ct = 0; ct < kNCT; ++ct) unsafeAtomicAdd(dst + 16 * ct, acc[rt][ct][v] * wgt);
+                for (int ct = 0; ct < kNCT; ++ct)
+                    acc_add(g.acc, g.acc_dtype, dst + 16 * ct, acc[rt][ct][v] * wgt);
             }
     };
 
@@ -506,7 +508,7 @@ void launch_moe_stage1_stream(const uint8_t* a, const float* a_scale, int64_t sa
 void launch_moe_stage2_stream(const uint8_t* a2, const float* a2_scale, const uint8_t* w2,
                               const float* w2_scale, const uint8_t* w2_scale_e8m0,
                               const int32_t* sorted_ids, const float* sorted_w,
-                              const int32_t* sorted_eids, const int32_t* num_valid, float* acc,
+                              const int32_t* sorted_eids, const int32_t* num_valid, void* acc, int acc_dtype,
                               int64_t a_rows, int64_t inter, int64_t hidden, int64_t E,
                               int64_t topk, int64_t block_m, int64_t max_m_blocks, int shuffled,
                               hipStream_t stream) {
@@ -523,6 +525,7 @@ void launch_moe_stage2_stream(const uint8_t* a2, const float* a2_scale, const ui
     g.sorted_eids = sorted_eids;
     g.num_valid = num_valid;
     g.acc = acc;
+    g.acc_dtype = acc_dtype;
     g.K = (int)inter;
     g.N = (int)hidden;
     g.inter = (int)inter;

@@ -49,6 +49,8 @@ struct SortParams {
     int32_t* ws;                // per-chunk expert counts [num_chunks][E]
     void* zero_buf;             // cleared for `tokens` rows (may be null)
     int64_t zero_row_bytes;     // multiple of 16
+    int64_t zero_skip16;        // leading 16-byte units of zero_buf left to the clear launch
+                                // (they hold the chunk counts when ws lives in zero_buf)
     int rows;
     int topk;
     int E;
@@ -86,8 +88,17 @@ __device__ void zero_rows(const SortParams& p, int tokens, int block, int nblock
     int64_t n16 = (int64_t)tokens * p.zero_row_bytes / 16;
     v4i z = {0, 0, 0, 0};
     v4i* dst = reinterpret_cast<v4i*>(p.zero_buf);
-    for (int64_t i = (int64_t)block * kSortThreads + threadIdx.x; i < n16;
+    for (int64_t i = p.zero_skip16 + (int64_t)block * kSortThreads + threadIdx.x; i < n16;
          i += (int64_t)nblocks * kSortThreads)
+        dst[i] = z;
+}
+
+// Clears the chunk counts once the scatter launch has read them, when they
+// were kept at the start of the caller's moe_buf instead of a workspace.
+__global__ __launch_bounds__(kSortThreads) void moe_sort_clear_kernel(v4i* dst, int64_t n16) {
+    const v4i z = {0, 0, 0, 0};
+    for (int64_t i = (int64_t)blockIdx.x * kSortThreads + threadIdx.x; i < n16;
+         i += (int64_t)gridDim.x * kSortThreads)
         dst[i] = z;
 }
 
@@ -479,6 +490,7 @@ bool launch_moe_sort(const int32_t* topk_ids, const float* topk_w, const int32_t
     p.num_valid = num_valid;
     p.zero_buf = zero_buf;
     p.zero_row_bytes = zero_row_bytes;
+    p.zero_skip16 = 0;
     p.rows = (int)rows;
     p.topk = (int)topk;
     p.E = (int)E;
@@ -527,13 +539,26 @@ bool launch_moe_sort(const int32_t* topk_ids, const float* topk_w, const int32_t
         hipLaunchKernelGGL(moe_sort_oneshot_kernel, dim3(1 + zero_blocks + p.q_blocks),
                            dim3(kSortThreads), full_lds, stream, p);
     } else {
-        AMD_CHECK(ws != nullptr && ws_bytes >= sort_workspace_bytes(rows, topk, E),
-                  "sorting workspace too small");
+        const int64_t need = sort_workspace_bytes(rows, topk, E);
+        AMD_CHECK(ws != nullptr && ws_bytes >= need, "sorting workspace too small");
+        // the counts may live at the start of zero_buf itself (moe_buf, for
+        // callers that pass no workspace): the counting launch then leaves
+        // those bytes alone and a third launch clears them after the scatter
+        const bool ws_in_buf = ws == zero_buf;
+        if (ws_in_buf) {
+            AMD_CHECK(rows * zero_row_bytes >= need, "moe_buf too small to hold the sorting counts");
+            p.zero_skip16 = ceil_div(need, 16);
+        }
         p.sort_blocks = p.num_chunks;
         hipLaunchKernelGGL(moe_sort_count_kernel, dim3(p.num_chunks + zero_blocks + p.q_blocks),
                            dim3(kSortThreads), (size_t)E * 4, stream, p);
         hipLaunchKernelGGL(moe_sort_scatter_kernel, dim3(p.num_chunks), dim3(kSortThreads),
                            full_lds, stream, p);
+        if (ws_in_buf) {
+            const int64_t nb = std::min<int64_t>(ceil_div(p.zero_skip16, kSortThreads), 1024);
+            hipLaunchKernelGGL(moe_sort_clear_kernel, dim3(nb), dim3(kSortThreads), 0, stream,
+                               reinterpret_cast<v4i*>(zero_buf), p.zero_skip16);
+        }
     }
     AMD_HIP_CHECK(hipGetLastError());
     return quant_done;

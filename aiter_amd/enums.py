@@ -50,4 +50,9 @@ AITER_DTYPE = {
     torch.bfloat16: 3,
     torch.float32: 4,
     torch.int32: 8,
+    torch.uint8: 11,
 }
+if dtypes.fp8_e8m0 is not torch.uint8:
+    AITER_DTYPE[dtypes.fp8_e8m0] = 1
+if dtypes.fp4x2 is not torch.uint8:
+    AITER_DTYPE[dtypes.fp4x2] = 6

@@ -1,0 +1,272 @@
+"""The reference-shaped ctypes boundary of libaiter_amd.so (include/aiter_ctypes.h).
+
+`ctypes_op` binds a typed Python stub to the library function of the same
+name the way the reference's `compile_ops(..., ffi_type="ctypes")` does
+(aiter/jit/core.py:1105-1363), from the stub's type hints:
+
+    Tensor / Optional[Tensor] -> aiter_tensor_t* (NULL for None)
+    int / Optional[int]       -> int64_t (-1 for None)
+    bool -> int,  float -> float,  str / Optional[str] -> const char*
+    (appended)                -> hipStream_t: torch's current stream
+
+A call clears the library's last error, calls, and raises RuntimeError with
+`aiter_get_last_error()` when the status is non-zero or an error was left.
+The stubs below carry the reference's names and signatures
+(aiter/ops/moe_sorting.py:11-25, aiter/ops/quant.py:472-481,
+aiter/ops/moe_op.py:15-42, 196-213, 319-340, aiter/ops/topk.py:15-38), so
+a maintainer's own `compile_ops` stubs bind the same symbols unchanged.
+"""
+from __future__ import annotations
+
+import ctypes
+import functools
+import inspect
+import typing
+from typing import Optional
+
+import torch
+from torch import Tensor
+
+from . import _abi
+from .enums import AITER_DTYPE, ActivationType, QuantType
+
+
+class aiter_tensor_t(ctypes.Structure):
+    """csrc/include/aiter_tensor.h:8-37: the layout is the contract (160 bytes)."""
+
+    _fields_ = [
+        ("ptr", ctypes.c_void_p),
+        ("numel_", ctypes.c_size_t),
+        ("ndim", ctypes.c_int),
+        ("shape", ctypes.c_int64 * 8),
+        ("strides", ctypes.c_int64 * 8),
+        ("dtype_", ctypes.c_int),
+        ("device_id", ctypes.c_int),
+    ]
+
+
+assert ctypes.sizeof(aiter_tensor_t) == 160
+
+
+def to_aiter_tensor(t: Tensor) -> aiter_tensor_t:
+    """Describe a torch tensor (device memory, at most 8 dims) without copying."""
+    if t.dim() > 8:
+        raise ValueError(f"aiter_tensor_t holds at most 8 dims, got {t.dim()}")
+    if t.dtype not in AITER_DTYPE:
+        raise ValueError(f"dtype {t.dtype} has no AiterDtype code")
+    d = aiter_tensor_t()
+    d.ptr = t.data_ptr()
+    d.numel_ = t.numel()
+    d.ndim = t.dim()
+    for i, (n, s) in enumerate(zip(t.shape, t.stride())):
+        d.shape[i] = n
+        d.strides[i] = s
+    d.dtype_ = AITER_DTYPE[t.dtype]
+    d.device_id = t.device.index if t.device.type == "cuda" and t.device.index is not None \
+        else (torch.cuda.current_device() if t.device.type == "cuda" else -1)
+    return d
+
+
+def _kind(hint):
+    origin, args = typing.get_origin(hint), typing.get_args(hint)
+    optional = origin is typing.Union and type(None) in args
+    base = next((a for a in args if a is not type(None)), hint) if optional else hint
+    return base, optional
+
+
+def ctypes_op(func):
+    """Bind `func`'s signature to the library symbol of its name."""
+    hints = typing.get_type_hints(func)
+    sig = inspect.signature(func)
+    names = list(sig.parameters)
+    kinds = [_kind(hints[n]) for n in names]
+    argtypes = []
+    for base, _ in kinds:
+        if base is Tensor:
+            argtypes.append(ctypes.POINTER(aiter_tensor_t))
+        elif base is bool:
+            argtypes.append(ctypes.c_int)
+        elif base is int:
+            argtypes.append(ctypes.c_int64)
+        elif base is float:
+            argtypes.append(ctypes.c_float)
+        elif base is str:
+            argtypes.append(ctypes.c_char_p)
+        else:
+            raise TypeError(f"{func.__name__}: no C type for parameter hint {base!r}")
+    argtypes.append(ctypes.c_void_p)   # hipStream_t
+
+    @functools.lru_cache(maxsize=1)
+    def symbol():
+        lib = _abi.load()
+        fn = getattr(lib, func.__name__)
+        fn.restype = ctypes.c_int
+        fn.argtypes = argtypes
+        lib.aiter_get_last_error.restype = ctypes.c_char_p
+        lib.aiter_get_last_error.argtypes = []
+        lib.aiter_clear_last_error.restype = None
+        lib.aiter_clear_last_error.argtypes = []
+        return lib, fn
+
+    @functools.wraps(func)
+    def call(*args, **kwargs):
+        lib, fn = symbol()
+        bound = sig.bind(*args, **kwargs)
+        bound.apply_defaults()
+        keep, cargs, device = [], [], None
+        for name, (base, optional) in zip(names, kinds):
+            v = bound.arguments[name]
+            if base is Tensor:
+                if v is None:
+                    if not optional:
+                        raise TypeError(f"{func.__name__}: '{name}' is required")
+                    cargs.append(ctypes.POINTER(aiter_tensor_t)())
+                    continue
+                if not isinstance(v, Tensor):
+                    raise TypeError(f"{func.__name__}: '{name}' expects a tensor")
+                device = device or v.device
+                d = to_aiter_tensor(v)
+                keep.append(d)
+                cargs.append(ctypes.byref(d))
+            elif base is bool:
+                cargs.append(1 if v else 0)
+            elif base is int:
+                cargs.append(-1 if v is None else int(v))
+            elif base is float:
+                cargs.append(float(v))
+            else:
+                cargs.append(None if v is None else str(v).encode())
+        stream = torch.cuda.current_stream(device).cuda_stream if device is not None \
+            and device.type == "cuda" else None
+        lib.aiter_clear_last_error()
+        rc = fn(*cargs, stream)
+        err = lib.aiter_get_last_error()
+        if rc != 0 or err:
+            lib.aiter_clear_last_error()
+            raise RuntimeError(f"{func.__name__} failed: "
+                               f"{err.decode(errors='replace') if err else f'status {rc}'}")
+
+    call.argtypes = argtypes
+    return call
+
+
+# ------------------------------------------------------------- the entries ---
+@ctypes_op
+def moe_sorting_fwd(
+    topk_ids: Tensor,
+    topk_weights: Tensor,
+    sorted_token_ids: Tensor,
+    sorted_weights: Tensor,
+    sorted_expert_ids: Tensor,
+    num_valid_ids: Tensor,
+    moe_buf: Tensor,
+    num_experts: int,
+    unit_size: int,
+    local_expert_mask: Optional[Tensor] = None,
+    num_local_tokens: Optional[Tensor] = None,
+    dispatch_policy: int = 0,
+) -> None: ...
+
+
+@ctypes_op
+def dynamic_per_token_scaled_quant(
+    out: Tensor,
+    input: Tensor,
+    scales: Tensor,
+    scale_ub: Optional[Tensor] = None,
+    shuffle_scale: bool = False,
+    num_rows: Optional[Tensor] = None,
+    num_rows_factor: int = 1,
+) -> None: ...
+
+
+@ctypes_op
+def moe_stage1_g1u1(
+    input: Tensor,
+    w1: Tensor,
+    w2: Tensor,
+    sorted_token_ids: Tensor,
+    sorted_expert_ids: Tensor,
+    num_valid_ids: Tensor,
+    out: Tensor,
+    inter_dim: int,
+    kernelName: Optional[str],
+    block_m: int,
+    ksplit: int = 0,
+    activation: Optional[int] = ActivationType.Silu.value,
+    quant_type: Optional[int] = QuantType.No.value,
+    a1_scale: Optional[Tensor] = None,
+    w1_scale: Optional[Tensor] = None,
+    sorted_weights: Optional[Tensor] = None,
+) -> None: ...
+
+
+@ctypes_op
+def ck_moe_stage2(
+    inter_states: Tensor,
+    w1: Tensor,
+    w2: Tensor,
+    sorted_token_ids: Tensor,
+    sorted_expert_ids: Tensor,
+    num_valid_ids: Tensor,
+    out: Tensor,
+    topk: int,
+    kernelName: Optional[str] = None,
+    w2_scale: Optional[Tensor] = None,
+    a2_scale: Optional[Tensor] = None,
+    block_m: Optional[int] = 32,
+    sorted_weights: Optional[Tensor] = None,
+    quant_type: int = 0,
+    activation: int = 0,
+    splitk: int = 1,
+    use_non_temporal_load: bool = False,
+    dst_type: Optional[str] = None,
+    is_shuffled: bool = True,
+) -> None: ...
+
+
+@ctypes_op
+def topk_softmax(
+    topk_weights: Tensor,
+    topk_indices: Tensor,
+    token_expert_indices: Optional[Tensor],
+    gating_output: Tensor,
+    need_renorm: bool,
+    num_shared_experts: int = 0,
+    shared_expert_scoring_func: str = "",
+) -> None: ...
+
+
+@ctypes_op
+def topk_sigmoid(topk_weights: Tensor, topk_indices: Tensor, gating_output: Tensor) -> None: ...
+
+
+@ctypes_op
+def grouped_topk(
+    gating_output: Tensor,
+    topk_weights: Tensor,
+    topk_ids: Tensor,
+    num_expert_group: int,
+    topk_group: int,
+    need_renorm: bool,
+    is_softmax: bool = True,
+    routed_scaling_factor: float = 1.0,
+) -> None: ...
+
+
+@ctypes_op
+def biased_grouped_topk(
+    gating_output: Tensor,
+    correction_bias: Tensor,
+    topk_weights: Tensor,
+    topk_ids: Tensor,
+    num_expert_group: int,
+    topk_grp: int,
+    need_renorm: bool,
+    routed_scaling_factor: float = 1.0,
+) -> None: ...
+
+
+ENTRIES = ("moe_sorting_fwd", "dynamic_per_token_scaled_quant", "moe_stage1_g1u1",
+           "ck_moe_stage2", "topk_softmax", "topk_sigmoid", "grouped_topk",
+           "biased_grouped_topk")

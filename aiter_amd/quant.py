@@ -16,16 +16,7 @@ from typing import Optional, Tuple
 
 import torch
 
-from . import _abi
-from .enums import AITER_DTYPE, dtypes
-
-
-def _stream_ptr(t: torch.Tensor) -> int:
-    return torch.cuda.current_stream(t.device).cuda_stream
-
-
-def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
-    return None if t is None else t.data_ptr()
+from .enums import dtypes
 
 
 def dynamic_per_token_scaled_quant(
@@ -40,24 +31,15 @@ def dynamic_per_token_scaled_quant(
     """Quantise `input` viewed as [rows, 128] groups into fp8 `out` (in place).
 
     `input` has shape [..., 128] (the reference passes x.view(-1, 128)); `out`
-    has the original [rows, cols] shape and fixes `cols`.
+    has the original [rows, cols] shape and fixes `cols`. Runs the
+    reference-shaped entry of the same name (include/aiter_ctypes.h).
     """
     if scale_ub is not None:
         raise NotImplementedError("scale_ub is not supported for 1x128 group quant")
-    if not (input.is_contiguous() and out.is_contiguous() and scales.is_contiguous()):
-        raise ValueError("input, out and scales must be contiguous")
-    if out.dtype != dtypes.fp8:
-        raise ValueError(f"out must be {dtypes.fp8}, got {out.dtype}")
-    group = input.shape[-1]
-    cols = out.shape[-1]
-    rows = out.numel() // cols
-    if input.numel() != out.numel():
-        raise ValueError("input and out sizes differ")
-    _abi.call(
-        "aiter_amd_dynamic_per_group_quant_fp8",
-        input.data_ptr(), AITER_DTYPE[input.dtype], rows, cols, group, out.data_ptr(),
-        scales.data_ptr(), int(bool(shuffle_scale)), _ptr(num_rows), int(num_rows_factor),
-        _stream_ptr(input))
+    from . import ffi
+
+    ffi.dynamic_per_token_scaled_quant(out, input, scales, None, shuffle_scale, num_rows,
+                                       num_rows_factor)
 
 
 def per_group_quant_hip(

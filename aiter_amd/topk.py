@@ -27,12 +27,8 @@ from typing import Optional, Tuple
 
 import torch
 
-from . import _abi
-from .enums import AITER_DTYPE, dtypes
-
-
-def _stream(dev: torch.device) -> int:
-    return torch.cuda.current_stream(dev).cuda_stream
+from . import ffi
+from .enums import dtypes
 
 
 def _check(gating_output: torch.Tensor, topk_weights: torch.Tensor, topk_ids: torch.Tensor):
@@ -62,16 +58,12 @@ def topk_softmax(topk_weights: torch.Tensor, topk_indices: torch.Tensor,
     the whole row; token_expert_indices[t, j] = j * tokens + t
     (csrc/kernels/topk_softmax_kernels.cu:380-500)."""
     M, E, k = _check(gating_output, topk_weights, topk_indices)
-    tei = 0
     if token_expert_indices is not None:
         if (token_expert_indices.dtype != dtypes.i32 or not token_expert_indices.is_contiguous()
                 or tuple(token_expert_indices.shape) != (M, k)):
             raise ValueError("token_expert_indices must be a contiguous [tokens, topk] i32 tensor")
-        tei = token_expert_indices.data_ptr()
-    _abi.call("aiter_amd_topk_softmax", gating_output.data_ptr(),
-              AITER_DTYPE[gating_output.dtype], M, E, k, topk_weights.data_ptr(),
-              topk_weights.stride(0), topk_indices.data_ptr(), topk_indices.stride(0), tei,
-              int(bool(need_renorm)), _stream(gating_output.device))
+    ffi.topk_softmax(topk_weights, topk_indices, token_expert_indices, gating_output,
+                     bool(need_renorm))
 
 
 def topk_sigmoid(topk_weights: torch.Tensor, topk_indices: torch.Tensor,
@@ -79,25 +71,22 @@ def topk_sigmoid(topk_weights: torch.Tensor, topk_indices: torch.Tensor,
     """Experts ranked by logit; weight sigmoid(logit)
     (op_tests/test_moe_topk_sigmoid.py:28-32)."""
     M, E, k = _check(gating_output, topk_weights, topk_indices)
-    _abi.call("aiter_amd_topk_sigmoid", gating_output.data_ptr(),
-              AITER_DTYPE[gating_output.dtype], M, E, k, topk_weights.data_ptr(),
-              topk_weights.stride(0), topk_indices.data_ptr(), topk_indices.stride(0),
-              _stream(gating_output.device))
+    ffi.topk_sigmoid(topk_weights, topk_indices, gating_output)
 
 
 def _grouped(gating_output, bias, topk_weights, topk_ids, num_expert_group, topk_group,
              need_renorm, is_softmax, routed_scaling_factor):
     M, E, k = _check(gating_output, topk_weights, topk_ids)
-    bptr = 0
     if bias is not None:
         if bias.dtype != dtypes.fp32 or bias.numel() != E or not bias.is_contiguous():
             raise ValueError("correction_bias must be a contiguous f32 [num_experts] tensor")
-        bptr = bias.data_ptr()
-    _abi.call("aiter_amd_grouped_topk", gating_output.data_ptr(),
-              AITER_DTYPE[gating_output.dtype], bptr, M, E, k, int(num_expert_group),
-              int(topk_group), int(bool(need_renorm)), int(bool(is_softmax)),
-              float(routed_scaling_factor), topk_weights.data_ptr(), topk_weights.stride(0),
-              topk_ids.data_ptr(), topk_ids.stride(0), _stream(gating_output.device))
+        ffi.biased_grouped_topk(gating_output, bias.view(E), topk_weights, topk_ids,
+                                int(num_expert_group), int(topk_group), bool(need_renorm),
+                                float(routed_scaling_factor))
+    else:
+        ffi.grouped_topk(gating_output, topk_weights, topk_ids, int(num_expert_group),
+                         int(topk_group), bool(need_renorm), bool(is_softmax),
+                         float(routed_scaling_factor))
 
 
 def grouped_topk(gating_output: torch.Tensor, topk_weights: torch.Tensor,

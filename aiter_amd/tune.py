@@ -74,7 +74,6 @@ def tune(tokens, weights, model_dim, inter_dim, experts, topk, steps, warmup, lo
     """Time the layer at every block_m for each (weights, token count); returns rows."""
     import torch
 
-    import aiter_amd as A
     from aiter_amd import workloads as W
 
     dev = torch.device("cuda:0")
@@ -83,7 +82,6 @@ def tune(tokens, weights, model_dim, inter_dim, experts, topk, steps, warmup, lo
     for wfmt in weights:
         base = W.MoEConfig("tune", 1, model_dim, inter_dim, experts, topk, seed=11, weights=wfmt)
         wts = W.make_weights(base, device=dev, shuffle=True)
-        qt = A.QuantType.per_1x32 if wfmt == "mxfp4" else A.QuantType.per_1x128
         for T in tokens:
             cfg = W.MoEConfig("tune", T, model_dim, inter_dim, experts, topk, seed=T,
                               weights=wfmt)
@@ -92,7 +90,7 @@ def tune(tokens, weights, model_dim, inter_dim, experts, topk, steps, warmup, lo
             times = {}
             for bm in _candidates(model_dim, inter_dim):
                 def run():
-                    A.fused_moe(x, wts["w1"], wts["w2"], tw, ids, quant_type=qt,
+                    W.run_layer(wfmt, x, wts["w1"], wts["w2"], tw, ids,
                                 w1_scale=wts["w1_scale"], w2_scale=wts["w2_scale"],
                                 block_size_M=bm)
                 for _ in range(warmup):
@@ -106,7 +104,8 @@ def tune(tokens, weights, model_dim, inter_dim, experts, topk, steps, warmup, lo
                 torch.cuda.synchronize()
                 times[bm] = s.elapsed_time(e) / steps * 1e3
             best = min(times, key=times.get)
-            row = dict(zip(_KEY, _key(cu_num, T, model_dim, inter_dim, experts, topk, qt.name,
+            qt = "per_1x32" if wfmt == "mxfp4" else "per_1x128"
+            row = dict(zip(_KEY, _key(cu_num, T, model_dim, inter_dim, experts, topk, qt,
                                       "fp4x2" if wfmt == "mxfp4" else "fp8")))
             row.update(block_m=best, us=round(times[best], 2),
                        **{f"us_bm{bm}": round(times.get(bm, float("nan")), 2)

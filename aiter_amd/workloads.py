@@ -183,3 +183,16 @@ def layer_bytes(cfg: MoEConfig, distinct_experts: int, tokens: Optional[int] = N
     T = cfg.tokens if tokens is None else tokens
     return float(distinct_experts * expert_bytes(cfg) +
                  T * (cfg.model_dim * 2 + cfg.model_dim * 2 + 8 * cfg.topk))
+
+
+def run_layer(weights: str, hidden_states, w1, w2, topk_weight, topk_ids, **kw):
+    """One MoE layer of the given weight format: fused_moe with the FP8
+    128x128 blockscale quant type, or, for "mxfp4", fused_moe_a8w4 (fp8
+    activations x MXFP4 weights); keyword arguments go through unchanged."""
+    from .enums import QuantType
+    from .fused_moe import fused_moe, fused_moe_a8w4
+
+    if weights == "mxfp4":
+        return fused_moe_a8w4(hidden_states, w1, w2, topk_weight, topk_ids, **kw)
+    return fused_moe(hidden_states, w1, w2, topk_weight, topk_ids,
+                     quant_type=QuantType.per_128x128, **kw)

@@ -110,13 +110,11 @@ class Layer:
         return self.cfg.weights == "mxfp4"
 
     def run(self):
-        import aiter_amd as A
+        from aiter_amd import workloads as W
 
-        qt = A.QuantType.per_1x32 if self.a8w4 else A.QuantType.per_128x128
-        return A.fused_moe(self.x, self.w["w1"], self.w["w2"], self.tw, self.ids,
-                           expert_mask=self.mask, quant_type=qt,
-                           w1_scale=self.w["w1_scale"], w2_scale=self.w["w2_scale"],
-                           block_size_M=self.block_m or None)
+        return W.run_layer(self.cfg.weights, self.x, self.w["w1"], self.w["w2"], self.tw,
+                           self.ids, expert_mask=self.mask, w1_scale=self.w["w1_scale"],
+                           w2_scale=self.w["w2_scale"], block_size_M=self.block_m or None)
 
     def stages(self):
         """(stage-1 fn, stage-2 fn) of this layer's weight format."""

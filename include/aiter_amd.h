@@ -26,8 +26,9 @@ extern "C" {
 
 /* Raised whenever an entry point's arguments change: 2 added sorted_weights
    to the stage-1 entries and activation / doweight_stage1 to the one-call
-   entries. */
-#define AITER_AMD_ABI_VERSION 2
+   entries; 3 the output dtype of the stage-2 entries and global_experts of
+   the workspace query. */
+#define AITER_AMD_ABI_VERSION 3
 
 /* Replaces aiter_ctypes_abi_version (aiter_ctypes_error.h:120-147). */
 int aiter_amd_abi_version(void);
@@ -102,14 +103,18 @@ int aiter_amd_moe_stage1_fp8_blockscale(const void* a1, const float* a1_scale,
 /* Replaces ck_moe_stage2 with per_1x128 fp8 (gemm_moe_ck2stages.cu:118-181).
  *   a2 [tokens, topk, inter_dim] fp8 + a2_scale [tokens, topk, inter_dim/128]
  *   w2 [E, model_dim, inter_dim] fp8, w2_scale [E, model_dim/128, inter_dim/128]
- *   out_acc [tokens, model_dim] f32 accumulates sorted_weight * row (it must
- *   be zeroed first, e.g. by aiter_amd_moe_sorting_fwd's moe_buf);
+ *   out_acc [tokens, model_dim] accumulates sorted_weight * row with atomics;
+ *   it must be zeroed first, e.g. by aiter_amd_moe_sorting_fwd's moe_buf.
+ *   out_dtype 4 (fp32) keeps the sum in fp32 (aiter_amd_moe_acc_to_out then
+ *   rounds once); 3 (bf16) or 2 (fp16) accumulate into the reference's
+ *   moe_buf itself, rounding after every add as its 16-bit atomics do.
  *   sorted_weights NULL: unit weights (doweight_stage1 applied them). */
 int aiter_amd_moe_stage2_fp8_blockscale(const void* a2, const float* a2_scale, const void* w2,
                                         const float* w2_scale, const int32_t* sorted_ids,
                                         const float* sorted_weights,
                                         const int32_t* sorted_expert_ids,
-                                        const int32_t* num_valid_ids, float* out_acc,
+                                        const int32_t* num_valid_ids, void* out_acc,
+                                        int out_dtype,
                                         int64_t tokens, int64_t model_dim, int64_t inter_dim,
                                         int64_t num_experts, int64_t topk, int64_t block_m,
                                         int64_t max_m_blocks, int64_t w_shuffled, void* stream);
@@ -141,7 +146,8 @@ int aiter_amd_moe_stage1_a8w4(const void* a1, const float* a1_scale, int64_t a1_
 int aiter_amd_moe_stage2_a8w4(const void* a2, const float* a2_scale, const void* w2,
                               const uint8_t* w2_scale, const int32_t* sorted_ids,
                               const float* sorted_weights, const int32_t* sorted_expert_ids,
-                              const int32_t* num_valid_ids, float* out_acc, int64_t tokens,
+                              const int32_t* num_valid_ids, void* out_acc, int out_dtype,
+                              int64_t tokens,
                               int64_t model_dim, int64_t inter_dim, int64_t num_experts,
                               int64_t topk, int64_t block_m, int64_t max_m_blocks,
                               int64_t w_shuffled, void* stream);
@@ -155,10 +161,14 @@ int aiter_amd_moe_acc_to_out(const float* acc, void* out, int out_dtype,
                              void* stream);
 
 /* Bytes of workspace for aiter_amd_fused_moe_fp8_blockscale and
- * aiter_amd_fused_moe_a8w4. */
+ * aiter_amd_fused_moe_a8w4, given the same num_experts (experts held in
+ * w1/w2), global_experts (expert_mask entries; num_experts when there is no
+ * mask) and block_m (0: the default the one-call entries pick, from the
+ * token count and num_experts). */
 int64_t aiter_amd_fused_moe_workspace_bytes(int64_t tokens, int64_t model_dim,
                                             int64_t inter_dim, int64_t num_experts,
-                                            int64_t topk, int64_t block_m);
+                                            int64_t global_experts, int64_t topk,
+                                            int64_t block_m);
 
 /* The whole 2-stage FP8 blockscale MoE in one call; replaces the sequence
  * of fused_moe_ -> moe_sorting -> fused_moe_2stages (aiter/fused_moe.py:

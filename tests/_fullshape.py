@@ -11,8 +11,8 @@ stage to what it can be held to instead:
 
 * stage 1 against torch's stage 1 (same fp8 activations): every 1x128
   scale within one bf16 ulp of amax/448, every dequantised a2 element
-  within one top-binade e4m3 ulp of its group, and at most 1% of the fp8
-  codes different;
+  within one top-binade e4m3 ulp of its group, and at most 0.5% of the fp8
+  codes different (measured 0.03-0.2%);
 * stage 2 on the kernel's own a2 against torch's fp32 product: the strict
   normalised bar (max-rel <= 2e-2, RMS-rel <= 4e-3,
   op_tests/triton_tests/moe/test_moe_gemm_a8w4.py:104-160);
@@ -61,10 +61,61 @@ def deq1x128(q, sc):
     return (q.float().view(rows, -1, 128) * sc.view(rows, -1, 1)).view(rows, -1)
 
 
+class TorchChain:
+    """The 2-stage layer in plain torch fp32 on any device: per touched expert,
+    stage 1 from dequantised activations, act(gate)*up rounded to bf16, the
+    kernel-semantics 1x128 fp8 requant, and stage 2's routing-weighted sum
+    (the semantics of torch_moe_stage1/2, aiter/fused_moe.py:1483-1666). It is
+    the checker of the full-size GPU tests, where the numpy oracle is too
+    slow; tests/test_fullshape_ref.py pins it against the oracle on the CPU.
+    Experts >= `local` hold no weights here (an expert-parallel share)."""
+
+    def __init__(self, w1, s1, w2, s2, ids, tw, deq=deq_fp8_128x128, local=None):
+        self.w1, self.s1, self.w2, self.s2, self.tw, self.deq = w1, s1, w2, s2, tw, deq
+        self.T, self.k = ids.shape
+        self.H = w2.shape[1]
+        self.I = s2.shape[2] * (32 if deq is deq_mxfp4 else 128)
+        local = w1.shape[0] if local is None else local
+        self.experts = [e for e in torch.unique(ids).tolist() if 0 <= e < local]
+        self.routes = {e: torch.nonzero(ids == e, as_tuple=True) for e in self.experts}
+        self.local_rows = torch.nonzero(((ids >= 0) & (ids < local)).view(-1)).squeeze(1)
+
+    def stage1(self, a1d):
+        """(codes, scales) [T*k, I] of the requantised act(gate)*up from the
+        dequantised activations a1d [T, H]; rows of pairs with no local
+        expert are zero."""
+        T, k, I = self.T, self.k, self.I
+        y = torch.zeros(T, k, 2 * I, device=a1d.device)
+        for e in self.experts:
+            tok, slot = self.routes[e]
+            y[tok, slot] = a1d[tok] @ self.deq(self.w1[e], self.s1[e]).T
+        h = (torch.nn.functional.silu(y[..., :I]) * y[..., I:]).to(torch.bfloat16)
+        del y
+        return q1x128(h.view(T * k, I))
+
+    def stage2(self, a2d):
+        """fp32 [T, H]: sum over slots of tw * (a2 row . w2^T) from the
+        dequantised a2d [T*k, I]."""
+        out = torch.zeros(self.T, self.H, device=a2d.device)
+        for e in self.experts:
+            tok, slot = self.routes[e]
+            rows = tok * self.k + slot
+            out.index_add_(0, tok, (a2d[rows] @ self.deq(self.w2[e], self.s2[e]).T) *
+                           self.tw[tok, slot][:, None])
+        return out
+
+
+def torch_layer_ref(x, w1, s1, w2, s2, ids, tw, deq=deq_fp8_128x128):
+    """The layer from bf16 x through TorchChain, rounded to bf16 (as fp32)."""
+    c = TorchChain(w1, s1, w2, s2, ids, tw, deq)
+    a1q, a1s = q1x128(x)
+    q, sc = c.stage1(deq1x128(a1q, a1s))
+    return c.stage2(deq1x128(q, sc)).to(torch.bfloat16).float()
+
+
 def stagewise_check(cfg, device, block_ms, log=print):
     mx4 = cfg.weights == "mxfp4"
     deq = deq_mxfp4 if mx4 else deq_fp8_128x128
-    qt = A.QuantType.per_1x32 if mx4 else A.QuantType.per_128x128
     stage1 = A.moe_stage1_a8w4 if mx4 else A.moe_stage1_fp8_blockscale
     stage2 = A.moe_stage2_a8w4 if mx4 else A.moe_stage2_fp8_blockscale
     T, H, I, E, k = cfg.tokens, cfg.model_dim, cfg.inter_dim, cfg.experts, cfg.topk
@@ -78,33 +129,15 @@ def stagewise_check(cfg, device, block_ms, log=print):
     # local ids are the same); the other pairs contribute nothing and their
     # a2 rows are never written, so the stage-1 checks skip them
     mask = W.make_expert_mask(cfg, device=device)
-    local = cfg.local_experts or E
-    experts = [e for e in torch.unique(ids).tolist() if e < local]
-    routes = {e: torch.nonzero(ids == e, as_tuple=True) for e in experts}
-    rows_l = torch.nonzero((ids < local).view(-1)).squeeze(1)
+    chain = TorchChain(w1, s1, w2, s2, ids, tw, deq, cfg.local_experts)
+    rows_l = chain.local_rows
 
     # the fp8 activation quant is bit-exact with the oracle (its own tests);
     # both stage-1 paths start from the kernel's a1
     a1, a1s = A.per_group_quant_hip(x)
-    a1d = deq1x128(a1, a1s)
-    y = (torch.empty if mask is None else torch.zeros)(T, k, 2 * I, device=device)
-    for e in experts:
-        tok, slot = routes[e]
-        y[tok, slot] = a1d[tok] @ deq(w1[e], s1[e]).T
-    h = (torch.nn.functional.silu(y[..., :I]) * y[..., I:]).to(torch.bfloat16)
-    del y
-    q_ref, sc_ref = q1x128(h.view(T * k, I))
-    del h
+    q_ref, sc_ref = chain.stage1(deq1x128(a1, a1s))
     a2_ref = deq1x128(q_ref, sc_ref)
-
-    def stage2_torch(a2d):
-        out = torch.zeros(T, H, device=device)
-        for e in experts:
-            tok, slot = routes[e]
-            rows = tok * k + slot
-            out.index_add_(0, tok, (a2d[rows] @ deq(w2[e], s2[e]).T) * tw[tok, slot][:, None])
-        return out
-
+    stage2_torch = chain.stage2
     chain_ref = stage2_torch(a2_ref)
     for bm in block_ms:
         tag = f"{cfg.name} bm={bm}"
@@ -123,7 +156,7 @@ def stagewise_check(cfg, device, block_ms, log=print):
             f"codes differing {codes:.3%}")
         assert srel <= BF16_ULP * (1 + 1e-6), srel
         assert err <= E4M3_TOP_ULP * (1 + 2 * BF16_ULP), err
-        assert codes <= 0.01, codes
+        assert codes <= 0.005, codes
 
         acc = torch.zeros(T, H, dtype=torch.float32, device=device)
         stage2(a2.view(T, k, I), a2s.view(T, k, -1), w2s, s2, sid, sw, se, nv, acc, bm, True)
@@ -131,7 +164,7 @@ def stagewise_check(cfg, device, block_ms, log=print):
         log(f"[{tag}] stage 2 on the kernel's a2: max-rel {mx:.2e} rms-rel {rms:.2e}")
         assert mx <= R.MAXTOL and rms <= R.RMSTOL, (mx, rms)
 
-        out = A.fused_moe(x, w1s, w2s, tw, ids, expert_mask=mask, quant_type=qt, w1_scale=s1,
+        out = W.run_layer(cfg.weights, x, w1s, w2s, tw, ids, expert_mask=mask, w1_scale=s1,
                           w2_scale=s2, block_size_M=bm).float()
         ref = chain_ref.to(torch.bfloat16).float()
         far = (~torch.isclose(out, ref, rtol=0.05, atol=0.05)).float().mean().item()
@@ -143,7 +176,7 @@ def stagewise_check(cfg, device, block_ms, log=print):
 
 def stagewise_vs_oracle(cfg, dev, ref, out, bm, activation, doweight=False, log=print):
     """The same split for a small layer, against the CPU oracle: stage 1's
-    fp8 codes against the oracle's a2 (at most 1% different, each element
+    fp8 codes against the oracle's a2 (at most 0.5% different, each element
     within one top-binade e4m3 step of its group), the layer's output against the oracle's stage 2 applied to
     the kernel's own a2 (the strict normalised bar), and RMS-rel against the
     whole oracle chain. For layers whose smallest outputs sit next to a
@@ -172,7 +205,7 @@ def stagewise_vs_oracle(cfg, dev, ref, out, bm, activation, doweight=False, log=
     differ = (codes != ref["a2q"])[loc].mean()
     log(f"[{cfg.name} bm={bm}] stage 1 codes differing {differ:.3%}, element err/amax "
         f"{err.max():.4f}")
-    assert differ <= 0.01 and err.max() <= E4M3_TOP_ULP * (1 + 2 * BF16_ULP), (differ, err.max())
+    assert differ <= 0.005 and err.max() <= E4M3_TOP_ULP * (1 + 2 * BF16_ULP), (differ, err.max())
     a2d[~loc] = 0
     wts = W.make_weights(cfg, device="cpu", shuffle=False)
     w2 = wts["w2"].numpy() if mx4 else wts["w2"].view(torch.uint8).numpy()

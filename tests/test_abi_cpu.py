@@ -41,7 +41,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.aiter_amd_abi_version() == _abi.ABI_VERSION == 2
+    assert lib.aiter_amd_abi_version() == _abi.ABI_VERSION == 3
 
 
 def _expect_error(name, *args, match):
@@ -92,7 +92,9 @@ def test_stage_validation_errors():
     _expect_error("aiter_amd_moe_stage1_fp8_blockscale", *args, 4, 4096, 2048, 8, 2, 32, 10, 2, 1,
                   None, match=r"Silu \(0\) and Gelu \(1\)")
     _expect_error("aiter_amd_moe_stage2_fp8_blockscale", 16, 16, 16, 16, 16, 16, 16, 16, 16, 4,
-                  4096, 2048, 8, 40, 32, 10, 1, None, match="topk must be")
+                  4, 4096, 2048, 8, 40, 32, 10, 1, None, match="topk must be")
+    _expect_error("aiter_amd_moe_stage2_fp8_blockscale", 16, 16, 16, 16, 16, 16, 16, 16, 16, 0,
+                  4, 4096, 2048, 8, 2, 32, 10, 1, None, match="fp32, bf16 or fp16")
     _expect_error("aiter_amd_moe_acc_to_out", 16, 16, 4, 16, 4, 64, None, match="bf16 or fp16")
 
 
@@ -107,9 +109,31 @@ def test_fused_validation_errors(lib):
     masked = [16, 3, 16, 16, 16, 16, 16, 16, 16, None, 16, 3]    # expert_mask given
     _expect_error("aiter_amd_fused_moe_fp8_blockscale", *masked, 4, 4096, 2048, 8, 4, 2, 0, 0, 0,
                   1, 16, 10**9, None, match="global_experts")
-    ws = lib.aiter_amd_fused_moe_workspace_bytes(8192, 4096, 2048, 256, 8, 64)
+    ws = lib.aiter_amd_fused_moe_workspace_bytes(8192, 4096, 2048, 256, 256, 8, 64)
     # sorted ids/weights + a1 + a2 + f32 accumulator dominate
     assert ws > 8192 * 4096 * (1 + 4) + 8192 * 8 * 2048
+    assert lib.aiter_amd_fused_moe_workspace_bytes(64, 4096, 2048, 32, 16, 8, 0) == -1
+
+
+def test_workspace_query_resolves_block_m_like_the_layer(lib):
+    """block_m = 0 resolves from the local experts in both the workspace
+    query and the one-call entries: an EP share (32 of 256 experts) at T=64,
+    top-8 picks 32 (16 rows per local expert on average, where dividing by
+    all 256 would give 16). The workspace the query reports is accepted by
+    the entry: the call gets past the size check to the pointer checks."""
+    T, H, I, E, G, k = 64, 4096, 2048, 32, 256, 8
+    assert lib.aiter_amd_default_block_m(T, k, E, H, I) == 32
+    assert lib.aiter_amd_default_block_m(T, k, G, H, I) == 16
+    ws = lib.aiter_amd_fused_moe_workspace_bytes(T, H, I, E, G, k, 0)
+    assert ws == lib.aiter_amd_fused_moe_workspace_bytes(T, H, I, E, G, k, 32)
+    assert ws > lib.aiter_amd_fused_moe_workspace_bytes(T, H, I, E, G, k, 16)
+    masked = [16, 3, 16, 16, 16, 16, 16, 16, 16, None, 16, 3]
+    # one byte short is rejected, the reported size passes the size check and
+    # stops at the (misaligned) workspace pointer
+    _expect_error("aiter_amd_fused_moe_fp8_blockscale", *masked, T, H, I, E, G, k, 0, 0, 0, 1,
+                  16, ws - 1, None, match="workspace of")
+    _expect_error("aiter_amd_fused_moe_fp8_blockscale", *masked, T, H, I, E, G, k, 0, 0, 0, 1,
+                  8, ws, None, match="workspace is not 16-byte aligned")
 
 
 def test_block_m_128_needs_32bit_operands(lib, monkeypatch):
@@ -160,6 +184,77 @@ def test_python_layer_rejects_unsupported_modes():
                   w1_scale=s1, w2_scale=s2)
     with pytest.raises(ValueError, match="w1_scale"):
         fused_moe(x, w1, w2, tw, ids, quant_type=QuantType.per_128x128)
+
+
+def test_python_layer_validates_tensors_before_the_c_abi():
+    """Every tensor fused_moe hands to the raw-pointer C ABI is checked first
+    (dtype, shape, device): a wrong one raises ValueError on the host instead
+    of a kernel reading out of bounds. CPU tensors pass every check up to
+    the device one, so each case below fails at its own check."""
+    from aiter_amd import QuantType, fused_moe
+
+    M, H, I, E, k = 4, 256, 128, 2, 2
+    x = torch.zeros(M, H, dtype=torch.bfloat16)
+    w1 = torch.zeros(E, 2 * I, H, dtype=torch.float8_e4m3fn)
+    w2 = torch.zeros(E, H, I, dtype=torch.float8_e4m3fn)
+    ids = torch.zeros(M, k, dtype=torch.int32)
+    tw = torch.ones(M, k)
+    s1 = torch.ones(E, 2 * I // 128, H // 128)
+    s2 = torch.ones(E, H // 128, I // 128)
+    qt = QuantType.per_128x128
+    run = lambda **kw: fused_moe(**{**dict(hidden_states=x, w1=w1, w2=w2, topk_weight=tw,
+                                           topk_ids=ids, quant_type=qt, w1_scale=s1,
+                                           w2_scale=s2), **kw})
+    with pytest.raises(ValueError, match="runs on the GPU"):
+        run()
+    with pytest.raises(ValueError, match="static a2_scale"):
+        run(a2_scale=torch.ones(M, k, I // 128))
+    with pytest.raises(ValueError, match="hidden_states must be"):
+        run(hidden_states=torch.zeros(M, H + 128, dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="hidden_states must be"):
+        run(hidden_states=torch.zeros(M + 1, H, dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="topk_weight must be"):
+        run(topk_weight=torch.ones(M, k + 1))
+    with pytest.raises(ValueError, match="w1_scale must be the 128x128"):
+        run(w1_scale=torch.ones(E, 2 * I // 128, 1))
+    with pytest.raises(ValueError, match="w2_scale must be the 128x128"):
+        run(w2_scale=torch.ones(E, H // 128, 2))
+    x8 = torch.zeros(M, H, dtype=torch.float8_e4m3fn)
+    with pytest.raises(ValueError, match="a1_scale must be provided"):
+        run(hidden_states=x8)
+    with pytest.raises(ValueError, match="a1_scale must be the f32 1x128"):
+        run(hidden_states=x8, a1_scale=torch.ones(M, 1))
+    with pytest.raises(ValueError, match="expert_mask must be"):
+        run(expert_mask=torch.ones(1, dtype=torch.int32))
+    with pytest.raises(ValueError, match="num_local_tokens"):
+        run(num_local_tokens=torch.ones(1, dtype=torch.int64))
+    with pytest.raises(ValueError, match="multiples of 128"):
+        run(w1=torch.zeros(E, 2 * 64, H, dtype=torch.float8_e4m3fn),
+            w2=torch.zeros(E, H, 64, dtype=torch.float8_e4m3fn))
+
+
+def test_fused_moe_is_a_registered_custom_op():
+    """fused_moe_ is torch.ops.aiter_amd.fused_moe_ with fused_moe_fake as its
+    fake (the reference's registration, aiter/fused_moe.py:172-205): under
+    FakeTensorMode the op produces the [M, model_dim] output's shape and
+    dtype without running anything."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    from aiter_amd import QuantType
+
+    op = torch.ops.aiter_amd.fused_moe_.default
+    names = [a.name for a in op._schema.arguments]
+    assert names[:5] == ["hidden_states", "w1", "w2", "topk_weight", "topk_ids"]
+    assert names[-2:] == ["bias1", "bias2"]
+    with FakeTensorMode():
+        x = torch.empty(6, 256, dtype=torch.float16, device="cuda")
+        w1 = torch.empty(2, 256, 256, dtype=torch.float8_e4m3fn, device="cuda")
+        w2 = torch.empty(2, 256, 128, dtype=torch.float8_e4m3fn, device="cuda")
+        ids = torch.empty(6, 2, dtype=torch.int32, device="cuda")
+        tw = torch.empty(6, 2, device="cuda")
+        out = torch.ops.aiter_amd.fused_moe_(x, w1, w2, tw, ids, None, 0,
+                                             int(QuantType.per_128x128))
+        assert out.shape == (6, 256) and out.dtype == torch.float16
 
 
 def test_enum_values_match_reference():
@@ -217,15 +312,15 @@ def test_a8w4_validation_errors():
     tail = [16, None, 16, 16, 16, 16, 4, 4096, 2048, 8, 2, 32, 10, 0, 1, None]
     _expect_error("aiter_amd_moe_stage1_a8w4", *args, None, *tail, match="w1_scale is NULL")
     _expect_error("aiter_amd_moe_stage1_a8w4", *args, 18, *tail, match="4-byte aligned")
-    _expect_error("aiter_amd_moe_stage2_a8w4", 16, 16, 16, None, 16, 16, 16, 16, 16, 4, 4096,
-                  2048, 8, 2, 32, 10, 1, None, match="w2_scale is NULL")
+    _expect_error("aiter_amd_moe_stage2_a8w4", 16, 16, 16, None, 16, 16, 16, 16, 16, 4, 4,
+                  4096, 2048, 8, 2, 32, 10, 1, None, match="w2_scale is NULL")
     base = [16, 3, 16, 16, 16, None, 16, 16, None, None, 16, 3]
     _expect_error("aiter_amd_fused_moe_a8w4", *base, 4, 4096, 2048, 8, 8, 2, 0, 0, 0, 1, 16, 10,
                   None, match="w2_scale is NULL")
 
 
 def test_python_layer_a8w4_checks():
-    from aiter_amd import QuantType, fused_moe
+    from aiter_amd import QuantType, fused_moe, fused_moe_a8w4
 
     x = torch.zeros(4, 256, dtype=torch.bfloat16)
     ids = torch.zeros(4, 1, dtype=torch.int32)
@@ -235,15 +330,19 @@ def test_python_layer_a8w4_checks():
     s1 = torch.zeros(2, 256, 8, dtype=torch.uint8)
     s2 = torch.zeros(2, 256, 4, dtype=torch.uint8)
     assert A.get_inter_dim(w1.shape, w2.shape) == (2, 256, 128)
+    # the drop-in's per_1x32 is A4W4 in the reference (fp4 activations): refused,
+    # the A8W4 layer has its own entry
+    with pytest.raises(NotImplementedError, match="A4W4"):
+        fused_moe(x, w1, w2, tw, ids, quant_type=QuantType.per_1x32, w1_scale=s1, w2_scale=s2)
     with pytest.raises(ValueError, match="e8m0 scales must be"):
-        fused_moe(x, w1, w2, tw, ids, quant_type=QuantType.per_1x32, w1_scale=s1[..., :4],
-                  w2_scale=s2)
+        fused_moe_a8w4(x, w1, w2, tw, ids, w1_scale=s1[..., :4], w2_scale=s2)
     with pytest.raises(ValueError, match="per_1x32 needs packed fp4x2"):
-        fused_moe(x, w1.view(torch.float8_e4m3fn), w2.view(torch.float8_e4m3fn), tw, ids,
-                  quant_type=QuantType.per_1x32, w1_scale=s1, w2_scale=s2)
+        fused_moe_a8w4(x, w1.view(torch.float8_e4m3fn), w2.view(torch.float8_e4m3fn), tw, ids,
+                       w1_scale=s1, w2_scale=s2)
     with pytest.raises(ValueError, match="e8m0"):
-        fused_moe(x, w1, w2, tw, ids, quant_type=QuantType.per_1x32, w1_scale=s1.float(),
-                  w2_scale=s2)
+        fused_moe_a8w4(x, w1, w2, tw, ids, w1_scale=s1.float(), w2_scale=s2)
+    with pytest.raises(ValueError, match="runs on the GPU"):   # checks all pass up to the device
+        fused_moe_a8w4(x, w1, w2, tw, ids, w1_scale=s1, w2_scale=s2)
 
 
 def test_routing_validation_errors(lib):
@@ -352,7 +451,7 @@ def test_no_alloc_rejects_layers_over_the_buffer():
 
     cfg = W.mimo_prefill(2048)
     need = _abi.query("aiter_amd_fused_moe_workspace_bytes", cfg.tokens, cfg.model_dim,
-                      cfg.inter_dim, cfg.experts, cfg.topk, 128)
+                      cfg.inter_dim, cfg.experts, cfg.experts, cfg.topk, 128)
     assert need > 32 << 20
     lib = _abi.load()
     p = 256

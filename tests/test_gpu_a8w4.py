@@ -54,9 +54,8 @@ def _make_layer(cfg, device, shuffle, doweight=False, activation="silu"):
 
 
 def _run(dev, **kw):
-    return A.fused_moe(dev["x"], dev["w1"], dev["w2"], dev["tw"], dev["ids"],
-                       expert_mask=dev["mask"], quant_type=A.QuantType.per_1x32,
-                       w1_scale=dev["s1"], w2_scale=dev["s2"], **kw)
+    return A.fused_moe_a8w4(dev["x"], dev["w1"], dev["w2"], dev["tw"], dev["ids"],
+                            expert_mask=dev["mask"], w1_scale=dev["s1"], w2_scale=dev["s2"], **kw)
 
 
 def _check(ref_out, got, tag):
@@ -127,9 +126,9 @@ def test_a8w4_fp8_input_path(cuda_device):
     cfg = _a8w4(W.CONFIG_A)
     dev, ref = _make_layer(cfg, cuda_device, True)
     a1, a1s = A.per_group_quant_hip(dev["x"])
-    out = A.fused_moe(a1, dev["w1"], dev["w2"], dev["tw"], dev["ids"],
-                      quant_type=A.QuantType.per_1x32, w1_scale=dev["s1"], w2_scale=dev["s2"],
-                      a1_scale=a1s, dtype=torch.bfloat16)
+    out = A.fused_moe_a8w4(a1, dev["w1"], dev["w2"], dev["tw"], dev["ids"],
+                           w1_scale=dev["s1"], w2_scale=dev["s2"], a1_scale=a1s,
+                           dtype=torch.bfloat16)
     _check(ref["out"], _np(out.float()), "A8W4 fp8 input")
 
 
@@ -145,36 +144,11 @@ def test_a8w4_ep_share_small(cuda_device):
 
 
 # ------------------------------------------- full MiMo shape (decode) ---
-def _deq_mxfp4(wp, sc):
-    """[N, K/2] packed e2m1 + [N, K/32] e8m0 -> fp32 [N, K] on the GPU."""
-    lut = torch.tensor(R.FP4_LUT, device=wp.device)
-    N = wp.shape[0]
-    v = torch.stack([lut[(wp & 15).long()], lut[(wp >> 4).long()]], dim=-1).view(N, -1)
-    s = torch.exp2(sc.float() - 127.0)
-    return (v.view(N, -1, 32) * s[..., None]).view(N, -1)
-
 
 def _torch_ref_gpu(x, w1, s1, w2, s2, ids, tw, inter):
-    """Plain torch fp32 reference on the GPU: kernel-semantics 1x128 quant of
-    x and h, MXFP4 dequant of the touched experts' weights."""
-    T, H = x.shape
-
-    def q1x128(v):
-        g = v.float().view(v.shape[0], -1, 128)
-        amax = g.abs().amax(-1, keepdim=True).clamp_min(1e-10)
-        sc = amax * np.float32(1 / 448)
-        q = (g * (1.0 / sc)).clamp(-448, 448).to(torch.float8_e4m3fn).float()
-        return (q * sc).view_as(v)
-
-    a1 = q1x128(x)
-    out = torch.zeros(T, H, device=x.device)
-    for e in torch.unique(ids).tolist():
-        tok, slot = torch.nonzero(ids == e, as_tuple=True)
-        y = a1[tok] @ _deq_mxfp4(w1[e], s1[e]).T
-        h = (torch.nn.functional.silu(y[:, :inter]) * y[:, inter:]).to(torch.bfloat16)
-        a2 = q1x128(h)
-        out.index_add_(0, tok, (a2 @ _deq_mxfp4(w2[e], s2[e]).T) * tw[tok, slot][:, None])
-    return out.to(torch.bfloat16).float()
+    """Plain torch fp32 reference on the GPU with the LUT dequant of the MXFP4
+    weights (tests/_fullshape.TorchChain)."""
+    return _fullshape.torch_layer_ref(x, w1, s1, w2, s2, ids, tw, _fullshape.deq_mxfp4)
 
 
 def test_a8w4_mimo_decode_T32(cuda_device):
@@ -185,8 +159,8 @@ def test_a8w4_mimo_decode_T32(cuda_device):
     ref = _torch_ref_gpu(x, wts["w1"], wts["w1_scale"], wts["w2"], wts["w2_scale"], ids, tw,
                          cfg.inter_dim)
     w1s, w2s = A.shuffle_weight(wts["w1"]), A.shuffle_weight(wts["w2"])
-    out = A.fused_moe(x, w1s, w2s, tw, ids, quant_type=A.QuantType.per_1x32,
-                      w1_scale=wts["w1_scale"], w2_scale=wts["w2_scale"])
+    out = A.fused_moe_a8w4(x, w1s, w2s, tw, ids, w1_scale=wts["w1_scale"],
+                           w2_scale=wts["w2_scale"])
     _check(_np(ref), _np(out.float()), "A8W4 MiMo T=32")
 
 

@@ -182,7 +182,8 @@ def test_stage1_fused_requant_matches_oracle(cuda_device):
     print(f"[stage1 a2] max-rel {mx:.3e} rms-rel {rms:.3e}", flush=True)
     ref_codes = ref["a2q"].reshape(T * k, -1)
     flips = codes != ref_codes
-    assert flips.mean() < 1e-2 and rms <= RMSTOL
+    print(f"[stage1 a2] codes differing {flips.mean():.3%}", flush=True)
+    assert flips.mean() <= 5e-3 and rms <= RMSTOL
 
     def signed_step(c):  # position on the e4m3fn number line (+0 and -0 both 0)
         c = c.astype(np.int32)
@@ -254,7 +255,7 @@ def test_fused_moe_doweight_stage1_ep_share(cuda_device, bm):
     unweighted sum, so one one-step fp8 requant flip of a2 moves a small
     output by more than the end-to-end max-rel bar; the check is therefore
     per stage, as for the full-size layers: stage 1's fp8 codes on the local
-    pairs against the oracle's (at most 1% different, each within one
+    pairs against the oracle's (at most 0.5% different, each within one
     top-binade e4m3 step of its group, 32/448 of the group amax), then
     the reference's own end-to-end bar (allclose rtol = atol = 0.05 on at
     least 95% of the outputs, op_tests/test_moe_blockscale.py:288) and
@@ -269,7 +270,9 @@ def test_fused_moe_doweight_stage1_ep_share(cuda_device, bm):
     loc = ref["ids_local"] >= 0
     got = _np(a2.view(torch.uint8))[loc]
     exp = ref["a2q"][loc]
-    assert (got != exp).mean() <= 0.01
+    print(f"[doweight_stage1 EP bm={bm}] stage 1 codes differing {(got != exp).mean():.3%}",
+          flush=True)
+    assert (got != exp).mean() <= 0.005
     # in the group's own units (codes span +-448): within one top-binade step
     assert np.abs(R.fp8_decode(got) - R.fp8_decode(exp)).max() <= 32
     out = _np(_run(dev, block_size_M=bm, doweight_stage1=True).float())
@@ -296,61 +299,59 @@ def test_fused_moe_ep_share_small(cuda_device, bm):
     assert torch.count_nonzero(out[torch.from_numpy(none_local).to(cuda_device)]).item() == 0
 
 
-@pytest.mark.parametrize("bm", [None, 64, 128])
-def test_fused_moe_num_local_tokens(cuda_device, bm):
-    cfg = W.MoEConfig("local_tok", 80, 512, 512, 8, 2, seed=4)
+@pytest.mark.parametrize("T,local,bm", [(80, 50, None), (80, 50, 64), (80, 50, 128),
+                                         (600, 450, None), (600, 450, 16), (600, 290, 128)])
+def test_fused_moe_num_local_tokens(cuda_device, T, local, bm):
+    """num_local_tokens (a device scalar) limits the layer to the first rows;
+    T=600 at E=8 is three sorting chunks, where the counting launch also
+    quantises the activations and reads the row count from the device."""
+    cfg = W.MoEConfig("local_tok", T, 512, 512, 8, 2, seed=4)
     dev, _ = _make_layer(cfg, cuda_device, True)
-    loc = torch.tensor([50], dtype=torch.int32, device=cuda_device)
+    loc = torch.tensor([local], dtype=torch.int32, device=cuda_device)
     out = _run(dev, num_local_tokens=loc, block_size_M=bm)
     wts = W.make_weights(cfg, device="cpu", shuffle=False)
     ref = R.fused_moe_ref(dev["x"].float().cpu().numpy(), wts["w1"].view(torch.uint8).numpy(),
                           wts["w1_scale"].numpy(), wts["w2"].view(torch.uint8).numpy(),
                           wts["w2_scale"].numpy(), _np(dev["ids"]), _np(dev["tw"]),
-                          num_local_tokens=50)
-    _check(ref["out"][:50], _np(out.float())[:50], "num_local_tokens")
+                          num_local_tokens=local)
+    got = _np(out.float())
+    if T <= 256:
+        _check(ref["out"][:local], got[:local], f"num_local_tokens T={T} bm={bm}")
+    else:
+        # many more outputs: one of them sits next to an fp8 requant tie
+        # (max-rel 5e-2 at RMS-rel 2.6e-3 measured), so the check is per stage
+        got[local:] = 0
+        ref["ids_local"][local:] = -1
+        bm_used = bm or A.select_block_m(T, cfg.topk, cfg.experts, cfg.model_dim,
+                                         cfg.inter_dim, False, cuda_device)
+        _fullshape.stagewise_vs_oracle(cfg, dev, ref, got, bm_used, A.ActivationType.Silu)
 
 
-@pytest.mark.parametrize("bm", [None, 128])
-def test_fused_moe_fp16_io(cuda_device, bm):
-    cfg = W.MoEConfig("fp16", 40, 512, 512, 8, 2, seed=6)
+@pytest.mark.parametrize("T,bm", [(40, None), (40, 128), (600, None), (600, 16)])
+def test_fused_moe_fp16_io(cuda_device, T, bm):
+    """fp16 in and out; T=600 at E=8 is three sorting chunks (the counting
+    launch quantises the fp16 activations)."""
+    cfg = W.MoEConfig("fp16", T, 512, 512, 8, 2, seed=6)
     dev, ref = _make_layer(cfg, cuda_device, True)
     dev["x"] = dev["x"].to(torch.float16)
     out = _run(dev, block_size_M=bm)
     assert out.dtype == torch.float16
-    _check(ref["out"], _np(out.float()), "fp16")
+    if T <= 256:
+        _check(ref["out"], _np(out.float()), "fp16")
+    else:   # per stage, as for num_local_tokens at this size
+        bm_used = bm or A.select_block_m(T, cfg.topk, cfg.experts, cfg.model_dim,
+                                         cfg.inter_dim, False, cuda_device)
+        _fullshape.stagewise_vs_oracle(cfg, dev, ref, _np(out.float()), bm_used,
+                                       A.ActivationType.Silu)
 
 
 # ------------------------------------------- full MiMo shape (decode) ---
 def _torch_ref_gpu(x, w1, s1, w2, s2, ids, tw, inter):
-    """Plain torch fp32 reference on the GPU (kernel-semantics 1x128 quant
-    of x and h, 128x128 dequant of touched experts' weights)."""
-    T, H = x.shape
-    k = ids.shape[1]
-
-    def q1x128(v):
-        g = v.float().view(v.shape[0], -1, 128)
-        amax = g.abs().amax(-1, keepdim=True).clamp_min(1e-10)
-        sc = amax * np.float32(1 / 448)
-        q = (g * (1.0 / sc)).clamp(-448, 448).to(torch.float8_e4m3fn).float()
-        return (q * sc).view_as(v)
-
-    def deq(wq, sc):
-        N, K = wq.shape
-        return (wq.float().view(N // 128, 128, K // 128, 128) *
-                sc.view(N // 128, 1, K // 128, 1)).view(N, K)
-
-    a1 = q1x128(x)
-    out = torch.zeros(T, H, device=x.device)
-    for e in torch.unique(ids).tolist():
-        tok, slot = torch.nonzero(ids == e, as_tuple=True)
-        y = a1[tok] @ deq(w1[e], s1[e]).T
-        h = (torch.nn.functional.silu(y[:, :inter]) * y[:, inter:]).to(torch.bfloat16)
-        a2 = q1x128(h)
-        out.index_add_(0, tok, (a2 @ deq(w2[e], s2[e]).T) * tw[tok, slot][:, None])
-    return out.to(torch.bfloat16).float()
+    """Plain torch fp32 reference on the GPU (tests/_fullshape.TorchChain)."""
+    return _fullshape.torch_layer_ref(x, w1, s1, w2, s2, ids, tw)
 
 
-@pytest.mark.parametrize("T", [1, 32])
+@pytest.mark.parametrize("T", [1, 8, 32])
 def test_fused_moe_mimo_decode(cuda_device, T):
     cfg = W.mimo_decode(T)
     wts = W.make_weights(cfg, device=cuda_device, shuffle=False)
@@ -403,13 +404,12 @@ def test_prefill_column_walk_bit_exact(cuda_device, monkeypatch, weights, bm, nt
     wts = W.make_weights(cfg, device=cuda_device, shuffle=True)
     x = W.make_hidden(cfg, device=cuda_device)
     tw, ids = W.make_routing(cfg, device=cuda_device)
-    qt = A.QuantType.per_1x32 if weights == "mxfp4" else A.QuantType.per_128x128
 
     def layer(c):
         monkeypatch.setenv("AITER_AMD_PF_NTW1", str(c))
         monkeypatch.setenv("AITER_AMD_PF_NTW2", str(c))
-        out = A.fused_moe(x, wts["w1"], wts["w2"], tw, ids, quant_type=qt,
-                          w1_scale=wts["w1_scale"], w2_scale=wts["w2_scale"], block_size_M=bm)
+        out = W.run_layer(weights, x, wts["w1"], wts["w2"], tw, ids, w1_scale=wts["w1_scale"],
+                          w2_scale=wts["w2_scale"], block_size_M=bm)
         a2 = None
         if weights == "fp8":
             a1, a1s = A.per_group_quant_hip(x)

@@ -427,6 +427,22 @@ def test_a8w4_layer_oracle_vs_fp64_brute_force():
             y = W1[ids[t, j]] @ a[t]
             h[t, j] = y[:I] / (1 + np.exp(-y[:I])) * y[I:]
     np.testing.assert_allclose(ref["h"], h, rtol=1e-2, atol=1e-3 * np.abs(h).max())
+    # stage 2 and the weighted sum, from the oracle's own fp8 a2 (the requant
+    # is pinned by the activation-quant tests): down GEMM with LUT-decoded w2
+    # in fp64, routing weights, sum over the slots, bf16 output
+    W2 = np.stack([np.array([[R.FP4_LUT[(w2p[e, n, kk // 2] >> (4 * (kk % 2))) & 15]
+                              * 2.0 ** (int(w2s[e, n, kk // 32]) - 127) for kk in range(I)]
+                             for n in range(H)]) for e in range(E)])
+    a2 = (R.fp8_decode(ref["a2q"]).astype(np.float64) *
+          np.repeat(ref["a2s"].astype(np.float64), 128, axis=2))
+    out = np.zeros((T, H))
+    for t in range(T):
+        for j in range(k):
+            out[t] += tw[t, j] * (W2[ids[t, j]] @ a2[t, j])
+    np.testing.assert_allclose(ref["out"], R.bf16_round(out.astype(np.float32)), rtol=0,
+                               atol=2.0 ** -7 * np.abs(out).max())
+    mx, rms = R.normalized_errors(out, ref["out"])
+    assert mx <= 8e-3 and rms <= 2e-3, (mx, rms)   # bf16 output rounding only
 
 
 # -------------------------------------------------------------- routing ---

@@ -41,7 +41,7 @@ def _with_workspace(d, cfg, bm):
     dev = d["x"].device
     out = torch.empty(cfg.tokens, cfg.model_dim, dtype=torch.bfloat16, device=dev)
     nbytes = _abi.query("aiter_amd_fused_moe_workspace_bytes", cfg.tokens, cfg.model_dim,
-                        cfg.inter_dim, cfg.experts, cfg.topk, bm)
+                        cfg.inter_dim, cfg.experts, cfg.experts, cfg.topk, bm)
     ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
     _abi.call("aiter_amd_fused_moe_fp8_blockscale", *_args(d, cfg, out, bm), ws.data_ptr(),
               nbytes, torch.cuda.current_stream(dev).cuda_stream)
