@@ -8,6 +8,7 @@
 #include <algorithm>
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "common.h"
 
@@ -326,6 +327,30 @@ void stage2_entry(const void* a2, const float* a2_scale, const void* w2, WScale 
                     (int)(w_shuffled != 0), (hipStream_t)stream);
 }
 
+// ---- launch timing of the one-call layer (measurement hooks) ----
+// While enabled, the one-call entries record a HIP event on their stream
+// before the first launch and after each step -- sorting (with the fused
+// activation quant), the separate activation quant, stage 1, stage 2, the
+// finishing pass -- for up to `cap` calls; the elapsed times between
+// consecutive events are the steps' device times.
+constexpr int kTimedSteps = 5;
+
+struct LaunchTiming {
+    bool on = false;
+    int64_t cap = 0, calls = 0;
+    std::vector<hipEvent_t> ev;   // [cap][kTimedSteps + 1]
+};
+
+static thread_local LaunchTiming g_timing;
+
+// Records event `step` (0 = before the first launch) of the current call.
+static void timing_mark(int step, hipStream_t s) {
+    LaunchTiming& t = g_timing;
+    if (!t.on || t.calls >= t.cap) return;
+    AMD_HIP_CHECK(hipEventRecord(t.ev[t.calls * (kTimedSteps + 1) + step], s));
+    if (step == kTimedSteps) ++t.calls;
+}
+
 void fused_entry(const void* hidden_states, int hidden_dtype, const void* w1, WScale w1s,
                  const void* w2, WScale w2s, const float* topk_weights, const int32_t* topk_ids,
                  const int32_t* expert_mask, const int32_t* num_local_tokens, void* out,
@@ -372,15 +397,18 @@ void fused_entry(const void* hidden_states, int hidden_dtype, const void* w1, WS
     uint16_t* part = stage2_on_prefill(block_m, inter_dim, model_dim, w2s, tokens * topk)
                          ? reinterpret_cast<uint16_t*>(ws + L.off_acc) : nullptr;
     hipStream_t s = (hipStream_t)stream;
+    timing_mark(0, s);
     // decode-sized batches: the sorting launch also quantises the activations
     const bool quantised = launch_moe_sort(
         topk_ids, topk_weights, expert_mask, num_local_tokens, sorted_ids, sorted_w, sorted_eids,
         num_valid, part ? nullptr : acc, model_dim * 4, tokens, topk, E_sort, block_m,
         ws + L.off_sort_ws, L.sort_ws_bytes, s, hidden_states, (int)hidden_dtype, a1, a1_scale,
         model_dim);
+    timing_mark(1, s);
     if (!quantised)
         launch_per_group_quant_fp8(hidden_states, hidden_dtype, a1, a1_scale, tokens, model_dim,
                                    0, num_local_tokens, 1, s);
+    timing_mark(2, s);
     const int sh = (int)(w_shuffled != 0);
     // doweight_stage1: the routing weights scale stage 1's gate and up, stage 2 sums unweighted
     const bool dw = doweight_stage1 != 0;
@@ -388,16 +416,19 @@ void fused_entry(const void* hidden_states, int hidden_dtype, const void* w1, WS
                     sorted_eids, num_valid, a2, a2_scale, tokens, model_dim, inter_dim,
                     num_experts, topk, block_m, L.blocks, sh, s, dw ? sorted_w : nullptr,
                     (int)activation);
+    timing_mark(3, s);
     stage2_dispatch(a2, a2_scale, (const uint8_t*)w2, w2s, sorted_ids, dw ? nullptr : sorted_w,
                     sorted_eids,
                     num_valid, part ? nullptr : acc, DT_FP32, tokens * topk, inter_dim, model_dim,
                     num_experts, topk, block_m, L.blocks, sh, s, part,
                     tokens * topk * num_experts / E_sort);
+    timing_mark(4, s);
     if (part)
         launch_slot_sum(part, topk_ids, expert_mask, E_sort, num_valid, out, out_dtype, tokens,
                         topk, model_dim, s);
     else
         launch_acc_to_out(acc, out, out_dtype, num_valid, tokens, model_dim, s);
+    timing_mark(5, s);
 }
 
 // ---- the library's own device workspace for callers that cannot allocate ----
@@ -454,6 +485,42 @@ void aiter_clear_last_error(void) { g_last_error.clear(); }
 int64_t aiter_amd_moe_sorting_workspace_bytes(int64_t tokens, int64_t topk, int64_t num_experts) {
     if (tokens < 0 || topk < 1 || num_experts < 1) return 0;
     return sort_workspace_bytes(tokens, topk, num_experts);
+}
+
+int aiter_amd_layer_timing_begin(int64_t max_calls) {
+    return safe_call([&] {
+        AMD_CHECK(max_calls >= 1 && max_calls <= 100000, "max_calls must be in [1, 100000]");
+        LaunchTiming& t = g_timing;
+        AMD_CHECK(!t.on, "layer timing is already on (call aiter_amd_layer_timing_end first)");
+        t.ev.assign(max_calls * (kTimedSteps + 1), nullptr);
+        for (auto& e : t.ev) AMD_HIP_CHECK(hipEventCreate(&e));
+        t.cap = max_calls;
+        t.calls = 0;
+        t.on = true;
+    });
+}
+
+int64_t aiter_amd_layer_timing_end(float* step_ms, int64_t max_calls) {
+    LaunchTiming& t = g_timing;
+    int64_t n = -1;
+    const int rc = safe_call([&] {
+        AMD_CHECK(t.on, "layer timing is off");
+        t.on = false;
+        n = std::min(t.calls, max_calls);
+        if (n > 0) AMD_HIP_CHECK(hipEventSynchronize(t.ev[(n - 1) * (kTimedSteps + 1) + kTimedSteps]));
+        for (int64_t c = 0; c < n; ++c)
+            for (int k = 0; k < kTimedSteps; ++k) {
+                float ms = 0.f;
+                AMD_HIP_CHECK(hipEventElapsedTime(&ms, t.ev[c * (kTimedSteps + 1) + k],
+                                                  t.ev[c * (kTimedSteps + 1) + k + 1]));
+                step_ms[c * kTimedSteps + k] = ms;
+            }
+    });
+    for (auto& e : t.ev)
+        if (e) (void)hipEventDestroy(e);
+    t.ev.clear();
+    t.on = false;
+    return rc == 0 ? n : -1;
 }
 
 int64_t aiter_amd_default_block_m(int64_t tokens, int64_t topk, int64_t num_experts,

@@ -108,20 +108,20 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // compiler's wait-count pass does not see them (it would drain the whole
 // prefetch before every LDS read); the kernel waits for them itself with
 // an explicit s_waitcnt vmcnt(N) and issues no other vector loads in the
-// pipeline.  m0 holds the LDS base; nothing the compiler emits in this
-// kernel reads m0.
+// pipeline.  m0 holds the LDS base, and both statements declare it
+// clobbered, so the compiler keeps nothing of its own there across them.
 __device__ __forceinline__ void dma16(const Rsrc& r, uint32_t voff, uint32_t soff, uint32_t lds) {
     asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
                  :
                  : "v"(voff), "s"(r.w), "s"(soff), "s"(lds)
-                 : "memory");
+                 : "memory", "m0");
 }
 
 __device__ __forceinline__ void dma4(const Rsrc& r, uint32_t voff, uint32_t soff, uint32_t lds) {
     asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dword %0, %1, %2 offen lds"
                  :
                  : "v"(voff), "s"(r.w), "s"(soff), "s"(lds)
-                 : "memory");
+                 : "memory", "m0");
 }
 
 template <int N>

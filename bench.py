@@ -56,7 +56,6 @@ def parse():
                         "hbm_ceiling torch's streaming read and copy")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-decode", action="store_true")
-    p.add_argument("--kernel-iters", type=int, default=10)
     p.add_argument("--block-m", type=int, default=0, help="override the M-block (0 = default)")
     p.add_argument("--kernel-only", choices=["stage1", "stage2"], default=None,
                    help="profiling mode: run a 256 MiB device copy (counter calibration) "
@@ -152,43 +151,40 @@ def time_steps(fn, steps, warmup):
     return s.elapsed_time(e) / steps, wall
 
 
-def stage_kernel_times(layer, iters):
-    """Average device time of each stage's kernel, measured with HIP events
-    on torch's current stream (the stream the kernels are launched on)."""
+STEP_NAMES = ("sorting", "act_quant", "stage1", "stage2", "finish")
+
+
+def layer_step_times(layer, steps):
+    """Device time of each step of the one-call layer, averaged over `steps`
+    calls: the library records HIP events on the layer's stream (torch's
+    current stream) around its launches -- sorting (with the activation quant
+    when it rides in that launch), the separate activation quant, stage 1,
+    stage 2 and the finishing pass (aiter_amd_layer_timing_begin / _end).
+    Returns ({step: seconds}, ms per instrumented call)."""
+    import ctypes
+
     import torch
 
-    import aiter_amd as A
+    from aiter_amd import _abi
 
-    cfg = layer.cfg
-    bm = layer.block_m_used()
-    st1, st2 = layer.stages()
-    E_sort = cfg.experts
-    sid, sw, se, nv, acc = A.moe_sorting(layer.ids, layer.tw, E_sort, cfg.model_dim,
-                                         torch.float32, bm, layer.mask)
-    a1, a1s = A.per_group_quant_hip(layer.x)
-    a2, a2s = st1(a1, a1s, layer.w["w1"], layer.w["w1_scale"], sid, se, nv, cfg.topk, bm, True)
     torch.cuda.synchronize()
-
-    def timed(fn):
-        fn()
-        torch.cuda.synchronize()
+    _abi.call("aiter_amd_layer_timing_begin", steps)
+    try:
         s = torch.cuda.Event(enable_timing=True)
         e = torch.cuda.Event(enable_timing=True)
         s.record()
-        for _ in range(iters):
-            fn()
+        for _ in range(steps):
+            layer.run()
         e.record()
-        torch.cuda.synchronize()
-        return s.elapsed_time(e) / iters * 1e-3
-
-    t1 = timed(lambda: st1(a1, a1s, layer.w["w1"], layer.w["w1_scale"], sid, se, nv, cfg.topk,
-                           bm, True))
-    t2 = timed(lambda: st2(a2, a2s, layer.w["w2"], layer.w["w2_scale"], sid, sw, se, nv, acc,
-                           bm, True))
-    tq = timed(lambda: A.per_group_quant_hip(layer.x))
-    ts = timed(lambda: A.moe_sorting(layer.ids, layer.tw, E_sort, cfg.model_dim, torch.float32,
-                                     bm, layer.mask))
-    return {"stage1_s": t1, "stage2_s": t2, "act_quant_s": tq, "sorting_s": ts, "block_m": bm}
+    finally:
+        buf = (ctypes.c_float * (steps * len(STEP_NAMES)))()
+        n = _abi.query("aiter_amd_layer_timing_end", ctypes.addressof(buf), steps)
+    torch.cuda.synchronize()
+    if n < 1:
+        raise RuntimeError("the layer timing hooks recorded no call")
+    per = [sum(buf[c * len(STEP_NAMES) + k] for c in range(n)) / n
+           for k in range(len(STEP_NAMES))]
+    return {k: v * 1e-3 for k, v in zip(STEP_NAMES, per)}, s.elapsed_time(e) / steps
 
 
 def kernel_only(layer, which, steps):
@@ -263,13 +259,78 @@ def roofline(flops, bytes_, seconds):
             "hbm_frac": round(bytes_ / seconds / PEAK_HBM_BPS, 4)}
 
 
-def cpu_baseline(layer, budget_s=12.0):
-    """Oracle (numpy 'port' of the reference torch path) timed on this host on
-    a bounded sample of the same workload: a seeded random sample of the
-    touched experts, each processed for all of its routed pairs (dequant of
-    its weights, stage-1 GEMM, SiLU*up, requant, stage-2 GEMM).  The full
-    layer time is extrapolated as D * (mean dequant time per expert) +
-    P * (mean GEMM time per pair)."""
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or "unknown"
+
+
+def _blas_threads():
+    """Threads the numpy BLAS actually runs with (threadpoolctl), else 1."""
+    try:
+        from threadpoolctl import threadpool_info
+
+        n = [p.get("num_threads", 1) for p in threadpool_info() if p.get("user_api") == "blas"]
+        return int(max(n)) if n else 1
+    except Exception:  # pragma: no cover
+        return 1
+
+
+def cpu_baseline_config_a(warmup=2, runs=10):
+    """The oracle ('port': the numpy restatement of the reference's torch MoE
+    path, aiter/fused_moe.py:1483-1666 with pertoken_quant activations) timed
+    on this host at BASELINE.json's CPU configuration (config A: E=8, top-2,
+    hidden 1024, inter 512, T=64, the seeded inputs of the GPU tests): the
+    whole layer -- weight dequant, activation quant, both GEMM stages, the
+    requant and the weighted sum -- 2 warm-ups, then the median of 10
+    wall-clock runs."""
+    import statistics
+
+    import torch
+
+    from aiter_amd import workloads as W
+    from oracle import moe_ref as R
+
+    cfg = W.CONFIG_A
+    wts = W.make_weights(cfg, device="cpu", shuffle=False)
+    x = W.make_hidden(cfg).float().numpy()
+    tw, ids = W.make_routing(cfg)
+    args = (x, wts["w1"].view(torch.uint8).numpy(), wts["w1_scale"].numpy(),
+            wts["w2"].view(torch.uint8).numpy(), wts["w2_scale"].numpy(), ids.numpy(),
+            tw.numpy())
+    for _ in range(warmup):
+        R.fused_moe_ref(*args, act_quant="torch")
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        R.fused_moe_ref(*args, act_quant="torch")
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    flops = 2.0 * cfg.tokens * cfg.topk * 3 * cfg.inter_dim * cfg.model_dim
+    threads = _blas_threads()
+    return {
+        "value": round(cfg.tokens / t, 1), "unit": "tokens/s", "cores": threads,
+        "kind": "port", "measured": True,
+        "sample": (f"config A full layer (T={cfg.tokens}, E={cfg.experts}, top-{cfg.topk}, "
+                   f"hidden {cfg.model_dim}, inter {cfg.inter_dim}) through the numpy oracle: "
+                   f"{warmup} warm-ups, median of {runs} runs"),
+        "latency_ms": round(t * 1e3, 3), "gflops": round(flops / t / 1e9, 2),
+        "cpu_model": _cpu_model(), "os_cpu_count": os.cpu_count(), "blas_threads": threads,
+    }
+
+
+def cpu_extrapolated_mimo(layer, budget_s=8.0):
+    """A bounded sample of the headline workload itself, extrapolated (second,
+    labelled figure): the oracle on a seeded sample of the touched experts,
+    each for all of its routed pairs (dequant of its weights, stage-1 GEMM,
+    SiLU*up, requant, stage-2 GEMM); full layer time = D * (mean dequant time
+    per expert) + P * (mean GEMM time per pair)."""
     import numpy as np
     import torch
 
@@ -311,7 +372,7 @@ def cpu_baseline(layer, budget_s=12.0):
         y = a1[tok] @ w1.T
         h = R.bf16_round(R.silu(y[:, :I]) * y[:, I:])
         hq, hs = R.quant_1x128_kernel(h)
-        o = (R.dequant_1x128(hq, hs) @ w2.T) * tw[tok, slot][:, None]
+        (R.dequant_1x128(hq, hs) @ w2.T) * tw[tok, slot][:, None]
         t2 = time.perf_counter()
         t_deq += t1 - t0
         t_gemm += t2 - t1
@@ -320,20 +381,11 @@ def cpu_baseline(layer, budget_s=12.0):
         if time.perf_counter() - t_start > budget_s and n_exp >= 2:
             break
     full = t_quant + len(experts) * (t_deq / n_exp) + layer.pairs * (t_gemm / max(n_pairs, 1))
-    threads = torch.get_num_threads()
-    try:
-        import numpy.__config__  # noqa: F401
-        cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    except Exception:  # pragma: no cover
-        cores = threads
-    return {
-        "value": round(cfg.tokens / full, 2), "unit": "tokens/s", "cores": cores,
-        "kind": "port",
-        "sample": (f"numpy oracle on {n_exp} of {len(experts)} touched experts "
-                   f"({n_pairs} of {layer.pairs} routed pairs) of the same T={cfg.tokens} "
-                   f"layer; full-layer time extrapolated as D*dequant/expert + P*gemm/pair "
-                   f"= {full:.2f} s"),
-    }
+    return {"value": round(cfg.tokens / full, 2), "unit": "tokens/s", "measured": False,
+            "cores": _blas_threads(),
+            "sample": (f"numpy oracle on {n_exp} of {len(experts)} touched experts "
+                       f"({n_pairs} of {layer.pairs} routed pairs) of the T={cfg.tokens} layer; "
+                       f"extrapolated as D*dequant/expert + P*gemm/pair = {full:.2f} s")}
 
 
 def route_leg(name, args, dev):
@@ -437,7 +489,7 @@ def leg(name, args, dev):
     sec = ms * 1e-3
     flops = 2.0 * lay.pairs * 3 * cfg.inter_dim * cfg.model_dim
     byts = W.layer_bytes(cfg, lay.distinct)
-    kt = stage_kernel_times(lay, args.kernel_iters)
+    kt, _ = layer_step_times(lay, max(args.steps, 20))
     f1, b1 = stage1_work(lay)
     out = {"workload": cfg.name, "weights": cfg.weights, "tokens": cfg.tokens,
            "ms_per_step": round(ms, 4), "tokens_per_s": round(cfg.tokens / sec, 1),
@@ -446,9 +498,9 @@ def leg(name, args, dev):
            "hbm_gbps": round(byts / sec / 1e9, 1),
            "hbm_peak_frac": round(byts / sec / PEAK_HBM_BPS, 4),
            "routed_pairs": lay.pairs, "distinct_experts": lay.distinct,
-           "block_m": kt["block_m"],
-           "kernels_us": {k: round(v * 1e6, 1) for k, v in kt.items() if k.endswith("_s")},
-           "stage1_roofline": roofline(f1, b1, kt["stage1_s"])}
+           "block_m": lay.block_m_used(),
+           "kernels_us": {k: round(v * 1e6, 1) for k, v in kt.items()},
+           "stage1_roofline": roofline(f1, b1, kt["stage1"])}
     del lay
     torch.cuda.empty_cache()
     return out
@@ -471,13 +523,14 @@ def main():
         return
     log(f"timing {args.steps} steps after {args.warmup} warmup")
     ms, wall = time_steps(layer.run, args.steps, args.warmup)
-    log(f"layer {ms:.3f} ms/step; timing kernels")
+    log(f"layer {ms:.3f} ms/step; timing its kernels")
     layer_s = ms * 1e-3
     flops_layer = 2.0 * layer.pairs * 3 * cfg.inter_dim * cfg.model_dim
     from aiter_amd import workloads as W
 
     bytes_layer = W.layer_bytes(cfg, layer.distinct)
-    kt = stage_kernel_times(layer, args.kernel_iters)
+    # the same one-call layer again, with the library's launch-timing events
+    kt, ms_hooked = layer_step_times(layer, args.steps)
     f1, b1 = stage1_work(layer)
     fmt = "A8W4 (fp8 x MXFP4)" if layer.a8w4 else "FP8 blockscale"
     line = {
@@ -497,22 +550,27 @@ def main():
         "config": {"workload": cfg.name, "tokens": cfg.tokens, "model_dim": cfg.model_dim,
                    "inter_dim": cfg.inter_dim, "experts": cfg.experts, "topk": cfg.topk,
                    "routing": cfg.routing, "local_experts": cfg.local_experts,
-                   "block_m": kt["block_m"], "distinct_experts": layer.distinct},
+                   "block_m": layer.block_m_used(), "distinct_experts": layer.distinct},
         "layer": {"tflops": round(flops_layer / layer_s / 1e12, 2),
                   "fp8_peak_frac": round(flops_layer / layer_s / PEAK_FP8_FLOPS, 4),
                   "hbm_gbps": round(bytes_layer / layer_s / 1e9, 1),
                   "hbm_peak_frac": round(bytes_layer / layer_s / PEAK_HBM_BPS, 4),
                   "alg_flops": flops_layer, "alg_bytes": bytes_layer,
                   "wall_s_timed_region": round(wall, 4)},
-        "kernels_us": {k: round(v * 1e6, 1) for k, v in kt.items() if k.endswith("_s")},
-        "roofline": dict(roofline(f1, b1, kt["stage1_s"]), kernel="stage-1 gather-GEMM",
+        # device time of each launch of the one-call layer (HIP events around
+        # its launches on the layer's stream, averaged over `steps` calls)
+        "kernels_us": dict({k: round(v * 1e6, 1) for k, v in kt.items()},
+                           sum=round(sum(kt.values()) * 1e6, 1),
+                           layer_with_events=round(ms_hooked * 1e3, 1)),
+        "roofline": dict(roofline(f1, b1, kt["stage1"]), kernel="stage-1 gather-GEMM",
                          traffic=measured_traffic(args.workload),
                          alg_bytes=round(b1)),
     }
     legs = [] if args.legs in ("", "none") else [x for x in args.legs.split(",") if x]
     if not args.no_cpu_baseline:
-        log("cpu baseline (oracle sample)")
-        line["cpu_baseline"] = cpu_baseline(layer)
+        log("cpu baseline: the oracle at config A, then a sample of this workload")
+        line["cpu_baseline"] = cpu_baseline_config_a()
+        line["cpu_baseline"]["extrapolated_" + cfg.name] = cpu_extrapolated_mimo(layer)
     if not args.no_decode and not args.workload.startswith("decode"):
         dcfg = make_cfg("decode32")
         del layer

@@ -275,6 +275,18 @@ int aiter_amd_grouped_topk(const void* gating, int gating_dtype, const float* co
                            int64_t weights_stride, int32_t* topk_ids, int64_t ids_stride,
                            void* stream);
 
+/* Measurement hooks of the one-call entries, the per-kernel device times the
+ * reference's perftest reads from a profiler trace (aiter/test_common.py:
+ * 46-120).  Between begin and end, each of up to max_calls calls of
+ * aiter_amd_fused_moe_* on this thread records HIP events on its stream
+ * around its five steps: sorting (with the activation quant when it rides
+ * in that launch), the separate activation quant, stage 1, stage 2, and the
+ * finishing pass (slot sum or f32 -> 16-bit).  end waits for the last
+ * event, writes step_ms[call * 5 + step] (a step that launched nothing
+ * reads ~0) and returns the number of calls recorded, or -1 on error. */
+int aiter_amd_layer_timing_begin(int64_t max_calls);
+int64_t aiter_amd_layer_timing_end(float* step_ms, int64_t max_calls);
+
 /* Default M-block (sorted rows per GEMM tile) for a token count: 16 / 32 / 64 by the average
  * rows per expert (<= 8, <= 20, else), 128 once experts average >= 64 rows and the dims allow
  * 128-row tiles.
