@@ -26,7 +26,7 @@ bool launch_moe_sort(const int32_t*, const float*, const int32_t*, const int32_t
                      float*, int32_t*, int32_t*, void*, int64_t, int64_t, int64_t, int64_t,
                      int64_t, void*, int64_t, hipStream_t, const void* qx = nullptr,
                      int qx_dtype = 0, uint8_t* qq = nullptr, float* qs = nullptr,
-                     int64_t q_cols = 0);
+                     int64_t q_cols = 0, void* zero2 = nullptr, int64_t zero2_bytes = 0);
 void launch_per_group_quant_fp8(const void*, int, void*, float*, int64_t, int64_t, int,
                                 const int32_t*, int64_t, hipStream_t);
 void launch_acc_to_out(const float*, void*, int, const int32_t*, int64_t, int64_t, hipStream_t);
@@ -60,7 +60,12 @@ void launch_moe_stage1_stream(const uint8_t*, const float*, int64_t, int64_t, co
                               const float*, const uint8_t*, const int32_t*, const int32_t*,
                               const int32_t*, uint8_t*, float*, int64_t, int64_t, int64_t,
                               int64_t, int64_t, int64_t, int64_t, int, hipStream_t,
-                             const float*, int);
+                              const float*, int, int ksplit = 1, void* kpart = nullptr,
+                              int32_t* kcnt = nullptr, int64_t kmb = 0);
+// stage-1 split-K of the stream kernel: K ranges per tile for a layer
+// expected to route est_blocks M-blocks, and its partial-sum bytes
+int stream_stage1_ksplit(int64_t block_m, int64_t K, int64_t inter, int64_t est_blocks);
+int64_t stream_ksplit_part_bytes(int64_t block_m, int64_t mblocks, int64_t inter, int64_t ksplit);
 void launch_moe_stage2_stream(const uint8_t*, const float*, const uint8_t*, const float*,
                               const uint8_t*, const int32_t*, const float*, const int32_t*,
                               const int32_t*, void*, int, int64_t, int64_t, int64_t, int64_t,
@@ -117,10 +122,12 @@ static void stage1_dispatch(const uint8_t* a, const float* sa, int64_t sa_row, i
                             const int32_t* seid, const int32_t* nv, uint8_t* a2, float* a2s,
                             int64_t a_rows, int64_t K, int64_t I, int64_t E, int64_t topk,
                             int64_t bm, int64_t mblocks, int sh, hipStream_t s,
-                            const float* sw, int act) {
+                            const float* sw, int act, int ksplit = 1, void* kpart = nullptr,
+                            int32_t* kcnt = nullptr, int64_t kmb = 0) {
     if (stream_supported(bm, K))
         launch_moe_stage1_stream(a, sa, sa_row, sa_kb, w1, w1s.f32, w1s.e8m0, sid, seid, nv, a2,
-                                 a2s, a_rows, K, I, E, topk, bm, mblocks, sh, s, sw, act);
+                                 a2s, a_rows, K, I, E, topk, bm, mblocks, sh, s, sw, act, ksplit,
+                                 kpart, kcnt, kmb);
     else if (prefill_supported(bm, K) && !w1s.e8m0 && a_fits32(a_rows, K))
         launch_moe_stage1_prefill(a, sa, sa_row, sa_kb, w1, w1s.f32, w1s.e8m0, sid, seid, nv, a2,
                                   a2s, a_rows, K, I, E, topk, bm, mblocks, sh, s, sw, act);
@@ -224,15 +231,27 @@ struct FusedLayout {
     int64_t off_sorted_ids, off_sorted_w, off_sorted_eids, off_num_valid, off_sort_ws;
     int64_t off_a1, off_a1_scale, off_a2, off_a2_scale, off_acc, total;
     int64_t sort_ws_bytes;
+    // stage-1 split-K (decode): K ranges per tile, the M-blocks its buffers
+    // cover, the arrival counters (cleared by the sorting launch) and partials
+    int ksplit;
+    int64_t kmb, off_kcnt, kcnt_bytes, off_kpart;
 };
 
 int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
 
-FusedLayout fused_layout(int64_t T, int64_t H, int64_t I, int64_t E_sort, int64_t k,
-                         int64_t bm) {
+// E_local: the experts this GPU holds (E_sort: the ids' range, global under
+// an expert mask).
+FusedLayout fused_layout(int64_t T, int64_t H, int64_t I, int64_t E_sort, int64_t E_local,
+                         int64_t k, int64_t bm) {
     FusedLayout L;
     L.cap = sorted_capacity_for(T, k, E_sort, bm);
     L.blocks = ceil_div(L.cap, bm);
+    // every routed M-block holds at least one of the T*k pairs
+    L.kmb = std::min(L.blocks, T * k);
+    // M-blocks expected at decode sizes: one per touched local expert, at most
+    // the pairs routed here (an expert-parallel share gets ~E_local / E_sort of them)
+    const int64_t est_blocks = std::min(ceil_div(T * k * E_local, E_sort), E_local);
+    L.ksplit = T > 0 ? stream_stage1_ksplit(bm, H, I, est_blocks) : 1;
     L.sort_ws_bytes = sort_workspace_bytes(T, k, E_sort);
     int64_t o = 0;
     L.off_sorted_ids = o;  o = align256(o + L.cap * 4);
@@ -247,6 +266,9 @@ FusedLayout fused_layout(int64_t T, int64_t H, int64_t I, int64_t E_sort, int64_
     // fp32 accumulator [T, H], or per-pair bf16 rows [T*k, H] when stage 2
     // runs on the prefill kernel: room for either
     L.off_acc = o;         o = align256(o + std::max(T * H * 4, T * k * H * 2));
+    L.kcnt_bytes = L.ksplit > 1 ? align256(L.kmb * (I / 128) * 4) : 0;
+    L.off_kcnt = o;        o += L.kcnt_bytes;
+    L.off_kpart = o;       o = align256(o + stream_ksplit_part_bytes(bm, L.kmb, I, L.ksplit));
     L.total = o;
     return L;
 }
@@ -377,7 +399,8 @@ void fused_entry(const void* hidden_states, int hidden_dtype, const void* w1, WS
     check_ptr(w2, "w2");
     check_ptr(out, "out");
     AMD_CHECK(topk_weights && topk_ids, "a required pointer is NULL");
-    const FusedLayout L = fused_layout(tokens, model_dim, inter_dim, E_sort, topk, block_m);
+    const FusedLayout L =
+        fused_layout(tokens, model_dim, inter_dim, E_sort, num_experts, topk, block_m);
     AMD_CHECK(workspace_bytes >= L.total, "workspace of " + std::to_string(L.total) +
                                               " bytes required, got " +
                                               std::to_string(workspace_bytes));
@@ -403,7 +426,7 @@ void fused_entry(const void* hidden_states, int hidden_dtype, const void* w1, WS
         topk_ids, topk_weights, expert_mask, num_local_tokens, sorted_ids, sorted_w, sorted_eids,
         num_valid, part ? nullptr : acc, model_dim * 4, tokens, topk, E_sort, block_m,
         ws + L.off_sort_ws, L.sort_ws_bytes, s, hidden_states, (int)hidden_dtype, a1, a1_scale,
-        model_dim);
+        model_dim, ws + L.off_kcnt, L.kcnt_bytes);
     timing_mark(1, s);
     if (!quantised)
         launch_per_group_quant_fp8(hidden_states, hidden_dtype, a1, a1_scale, tokens, model_dim,
@@ -415,7 +438,8 @@ void fused_entry(const void* hidden_states, int hidden_dtype, const void* w1, WS
     stage1_dispatch(a1, a1_scale, model_dim / 128, 1, (const uint8_t*)w1, w1s, sorted_ids,
                     sorted_eids, num_valid, a2, a2_scale, tokens, model_dim, inter_dim,
                     num_experts, topk, block_m, L.blocks, sh, s, dw ? sorted_w : nullptr,
-                    (int)activation);
+                    (int)activation, L.ksplit, ws + L.off_kpart,
+                    reinterpret_cast<int32_t*>(ws + L.off_kcnt), L.kmb);
     timing_mark(3, s);
     stage2_dispatch(a2, a2_scale, (const uint8_t*)w2, w2s, sorted_ids, dw ? nullptr : sorted_w,
                     sorted_eids,
@@ -678,7 +702,8 @@ int64_t aiter_amd_fused_moe_workspace_bytes(int64_t tokens, int64_t model_dim, i
         return -1;
     // the block size the one-call entries resolve, from the local experts
     if (block_m <= 0) block_m = default_block_m(tokens, topk, num_experts, model_dim, inter_dim);
-    return fused_layout(tokens, model_dim, inter_dim, global_experts, topk, block_m).total;
+    return fused_layout(tokens, model_dim, inter_dim, global_experts, num_experts, topk, block_m)
+        .total;
 }
 
 int aiter_amd_fused_moe_fp8_blockscale(const void* hidden_states, int hidden_dtype,
@@ -719,7 +744,8 @@ int aiter_amd_fused_moe_fp8_blockscale_noalloc(
             block_m > 0 ? block_m
                         : default_block_m(tokens, topk, num_experts, model_dim, inter_dim);
         check_block_m_gemm(bm, model_dim, inter_dim, tokens, topk);
-        const int64_t need = fused_layout(tokens, model_dim, inter_dim, E_sort, topk, bm).total;
+        const int64_t need =
+            fused_layout(tokens, model_dim, inter_dim, E_sort, num_experts, topk, bm).total;
         AMD_CHECK(need <= kScratchBytes,
                   "this layer needs " + std::to_string(need) + " bytes of workspace; the "
                   "no-alloc entry point holds " + std::to_string(kScratchBytes) +

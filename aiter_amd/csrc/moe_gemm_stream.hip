@@ -39,6 +39,7 @@ constexpr int kThreads = 256;
 constexpr int kWaves = 4;
 constexpr int kNCT = 4;      // 16-row weight groups (MFMA column tiles) per wave
 constexpr int kMaxKB = 64;   // K <= 8192
+constexpr int kMaxSplit = 8; // stage-1 K ranges per tile
 
 struct Args {
     const uint8_t* a;          // activation rows, fp8 [a_rows, K]
@@ -64,6 +65,14 @@ struct Args {
     int E;
     int64_t a_rows;
     int ntw;                   // stage 2: 256-column groups per workgroup, one K loop
+    // stage 1 split-K: ksplit workgroups per tile, each over KB / ksplit K
+    // steps, leave fp32 partial sums in kpart; the last to arrive (counted in
+    // kcnt[tile], zero on entry and left zero) adds them in split order and
+    // runs the epilogue.  kmb: the M-blocks kpart and kcnt cover.
+    int ksplit;
+    v4f* kpart;
+    int32_t* kcnt;
+    int kmb;
 };
 
 // One K step of one wave's operands.
@@ -86,6 +95,7 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
     __shared__ float s_w[BM];
     __shared__ float s_amax[kWaves][BM];
     __shared__ __attribute__((aligned(16))) uint8_t s_q[STAGE == 1 ? BM * 144 : 16];
+    __shared__ int s_last;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -100,9 +110,14 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
     const int e = g.sorted_eids[mb];
     if (e < 0 || e >= g.E) return;
     // stage 2 may walk ntw consecutive 256-column groups in one K loop (steps
-    // s = jt * KB + kb); stage 1 always has one tile
+    // s = jt * KB + kb); stage 1 always has one tile, whose K range the S
+    // workgroups blockIdx.x = tile * S + ks split
     const int ntw = STAGE == 2 ? g.ntw : 1;
-    const int n0 = blockIdx.x * (STAGE == 1 ? 128 : 256 * ntw);
+    const int S = STAGE == 1 ? g.ksplit : 1;
+    const int nt = (int)blockIdx.x / S;
+    const int ks = (int)blockIdx.x - nt * S;
+    if (S > 1 && mb >= g.kmb) return;    // never: a routed M-block holds >= 1 of the tokens*topk pairs
+    const int n0 = nt * (STAGE == 1 ? 128 : 256 * ntw);
 
     for (int r = tid; r < BM; r += kThreads) {
         const uint32_t id = (uint32_t)g.sorted_ids[mb * BM + r];
@@ -127,10 +142,14 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
     const int K = g.K;
     const int KB = K / 128;
     const int KBY = W4 ? K / 2 : K;
+    // this workgroup's K steps [kbeg, kend): all of them unless split
+    const int KBS = KB / S;
+    const int kbeg = ks * KBS;
+    const int kend = kbeg + KBS;
     // activation scales of the block's rows, [kb][row]; weight-scale blocks
     // of the tile (stage 1: gate / up; stage 2: the two 128-column halves)
-    for (int i = tid; i < BM * KB; i += kThreads) {
-        const int r = i % BM, kb = i / BM;
+    for (int i = tid; i < BM * KBS; i += kThreads) {
+        const int r = i % BM, kb = kbeg + i / BM;
         const int arow = s_arow[r];
         s_sa[kb * BM + r] = arow >= 0 ? g.a_scale[arow * g.sa_row + kb * g.sa_kb] : 0.0f;
     }
@@ -178,9 +197,8 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
         asrc[rt] = g.a + (int64_t)arow * K + (W4 ? lq * 16 : lq * 32);
     }
 
-    using S = Step<NRT, W4>;
     // operands of K block kb of column group jt
-    auto load = [&](S& s, int kb, int jt) {
+    auto load = [&](Step<NRT, W4>& s, int kb, int jt) {
 #pragma unroll
         for (int ct = 0; ct < kNCT; ++ct) {
             const uint8_t* p = bsrc[ct] + (int64_t)kb * BSTEP + (int64_t)jt * 256 * KBY;
@@ -222,7 +240,7 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
         }
     };
 
-    auto compute = [&](const S& s, int kb, int jt, const int (&sg)[kNCT][D], int d) {
+    auto compute = [&](const Step<NRT, W4>& s, int kb, int jt, const int (&sg)[kNCT][D], int d) {
         // stage 1: tiles 0,1 gate (scale block 0), 2,3 up (block 1); stage 2:
         // the wave's 64 columns lie in 128-column block wv/2 of group jt
         const float sw0 = W4 ? 1.0f : STAGE == 1 ? s_sw[kb] : s_sw[(2 * jt + (wv >> 1)) * KB + kb];
@@ -272,11 +290,11 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
             }
     };
 
-    S buf[D];
+    Step<NRT, W4> buf[D];
     int sgc[kNCT][D], sgn[kNCT][D];            // A8W4 scales: current / next group
-    if (W4) load_sg(sgc, 0, 0);
+    if (W4) load_sg(sgc, kbeg, 0);
 #pragma unroll
-    for (int d = 0; d < D; ++d) load(buf[d], d, 0);
+    for (int d = 0; d < D; ++d) load(buf[d], kbeg + d, 0);
     auto next_scales = [&]() {
         if (W4) {
 #pragma unroll
@@ -286,8 +304,8 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
         }
     };
     if constexpr (STAGE == 1) {
-        // ---- K loop: D steps in flight ----
-        for (int kb0 = 0; kb0 < KB - D; kb0 += D) {
+        // ---- K loop over [kbeg, kend): D steps in flight ----
+        for (int kb0 = kbeg; kb0 < kend - D; kb0 += D) {
             if (W4) load_sg(sgn, kb0 + D, 0);
 #pragma unroll
             for (int d = 0; d < D; ++d) {
@@ -297,7 +315,51 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
             next_scales();
         }
 #pragma unroll
-        for (int d = 0; d < D; ++d) compute(buf[d], KB - D + d, 0, sgc, d);
+        for (int d = 0; d < D; ++d) compute(buf[d], kend - D + d, 0, sgc, d);
+        if (S > 1) {
+            // ---- split-K: publish this K range's partial sums; the last
+            // workgroup of the tile to arrive adds all S in split order (the
+            // same sum whichever arrives last) and finishes the tile. The
+            // partials are stored and loaded with the sc1 cache policy, which
+            // makes each access coherent across the XCDs' L2s by itself (the
+            // gfx94x/gfx950 form of an agent-scope atomic store / load), and
+            // the stores are waited for before the arrival count: an
+            // agent-scope release fence would instead write back the XCD's
+            // whole L2 in every workgroup.
+            constexpr int NP = NRT * kNCT;                 // v4f per thread
+            constexpr int kSc1 = 16;                       // buffer cache policy: sc1
+            const int64_t tile = (int64_t)mb * (gridDim.x / S) + nt;
+            const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+                g.kpart + tile * S * NP * kThreads, (short)0, S * NP * kThreads * 16, 0x00020000);
+#pragma unroll
+            for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+                for (int ct = 0; ct < kNCT; ++ct)
+                    __builtin_amdgcn_raw_buffer_store_b128(
+                        __builtin_bit_cast(v4i, acc[rt][ct]), rp,
+                        ((ks * NP + rt * kNCT + ct) * kThreads + tid) * 16, 0, kSc1);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+            if (tid == 0) s_last = atomicAdd(&g.kcnt[tile], 1) == S - 1;
+            __syncthreads();
+            if (!s_last) return;
+#pragma unroll
+            for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+                for (int ct = 0; ct < kNCT; ++ct) {
+                    const int j = rt * kNCT + ct;
+                    auto part = [&](int q) {
+                        return __builtin_bit_cast(
+                            v4f, __builtin_amdgcn_raw_buffer_load_b128(
+                                     rp, ((q * NP + j) * kThreads + tid) * 16, 0, kSc1));
+                    };
+                    v4f sum = ks == 0 ? acc[rt][ct] : part(0);
+                    for (int q = 1; q < S; ++q) sum += q == ks ? acc[rt][ct] : part(q);
+                    acc[rt][ct] = sum;
+                }
+            if (tid == 0)                                  // zero again for the next call
+                __hip_atomic_store(&g.kcnt[tile], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     } else {
         // ---- K loop over ntw * KB steps: D steps in flight; a group's last
         // steps are followed by its epilogue while the next group's first D
@@ -398,6 +460,7 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
 template <int BM>
 constexpr int max_depth() { return BM == 16 ? 4 : 2; }
 
+// KB: the K steps of one workgroup (split-K: KB / ksplit).
 template <int BM, int STAGE, bool SHUFFLED, bool W4>
 static void launch_depth(int KB, dim3 grid, const Args& a, hipStream_t s) {
     constexpr int DM = max_depth<BM>();
@@ -462,7 +525,42 @@ static int pick_ntw2(int64_t groups, int64_t KB, int64_t KBY, int64_t est_blocks
     return 1;
 }
 
+// Stage-1 split-K: K ranges per column tile. Measured on MI355X at MiMo
+// dims (stage 1, HIP-event times): a layer that routes to few experts has
+// few tiles, and two K ranges per tile help there -- one expert (16 tiles,
+// an expert-parallel share at T=2) 18.7 -> 15.9 us, six experts (96 tiles)
+// 29.0 -> 26.1 us -- while at 128 tiles (T=1, eight experts) the split
+// costs 30.4 -> 33.5 us, and four or eight ranges are slower everywhere
+// (each range then streams too few bytes to amortise the setup chain). So
+// the K range is halved when fewer than 128 tiles are expected.
+// AITER_AMD_ST_KSPLIT1 forces a count (tests use it; a power of two up to
+// 8 that divides the K steps into whole rounds of D).
+static int pick_ksplit1(int64_t bm, int64_t KB, int64_t n_tiles, int64_t est_blocks) {
+    const int64_t D = (bm == 16 && KB % 4 == 0) ? 4 : (KB % 2 == 0 ? 2 : 1);
+    auto fits = [&](int64_t c) { return KB % c == 0 && (KB / c) % D == 0; };
+    if (const char* env = getenv("AITER_AMD_ST_KSPLIT1")) {
+        const int c = atoi(env);
+        if (c >= 1 && c <= kMaxSplit && (c & (c - 1)) == 0 && fits(c)) return c;
+    }
+    constexpr int64_t kSplitBelow = 128;          // expected tiles
+    return est_blocks * n_tiles < kSplitBelow && fits(2) ? 2 : 1;
+}
+
 }  // namespace stream
+
+bool stream_supported(int64_t block_m, int64_t K);
+
+int stream_stage1_ksplit(int64_t block_m, int64_t K, int64_t inter, int64_t est_blocks) {
+    if (!stream_supported(block_m, K)) return 1;
+    return stream::pick_ksplit1(block_m, K / 128, inter / 128, est_blocks);
+}
+
+// Partial sums of split-K stage 1: per tile and split, 256 threads x
+// (block_m / 16) x 4 v4f.
+int64_t stream_ksplit_part_bytes(int64_t block_m, int64_t mblocks, int64_t inter, int64_t ksplit) {
+    if (ksplit <= 1) return 0;
+    return mblocks * (inter / 128) * ksplit * stream::kThreads * (block_m / 16) * stream::kNCT * 16;
+}
 
 // 16/32-row M-blocks, K a multiple of 128 up to 8192; stage 2 also needs
 // 256-column output tiles (model_dim % 256 == 0).
@@ -477,8 +575,15 @@ void launch_moe_stage1_stream(const uint8_t* a, const float* a_scale, int64_t sa
                               const int32_t* sorted_eids, const int32_t* num_valid, uint8_t* a2,
                               float* a2_scale, int64_t a_rows, int64_t K, int64_t inter,
                               int64_t E, int64_t topk, int64_t block_m, int64_t max_m_blocks,
-                              int shuffled, hipStream_t stream, const float* sorted_w, int act) {
+                              int shuffled, hipStream_t stream, const float* sorted_w, int act,
+                              int ksplit, void* kpart, int32_t* kcnt, int64_t kmb) {
     stream::Args g{};
+    g.ksplit = ksplit > 1 ? ksplit : 1;
+    AMD_CHECK(g.ksplit == 1 || (kpart && kcnt && kmb > 0 && (K / 128) % g.ksplit == 0),
+              "split-K needs partial and counter buffers and K steps divisible by the split");
+    g.kpart = reinterpret_cast<v4f*>(kpart);
+    g.kcnt = kcnt;
+    g.kmb = (int)std::min<int64_t>(kmb, max_m_blocks);
     g.sorted_w = sorted_w;                 // doweight_stage1 (or NULL)
     g.act = act;
     g.a = a;
@@ -500,8 +605,10 @@ void launch_moe_stage1_stream(const uint8_t* a, const float* a_scale, int64_t sa
     g.E = (int)E;
     g.a_rows = a_rows;
     if (max_m_blocks == 0) return;
-    const dim3 grid((unsigned)(inter / 128), (unsigned)max_m_blocks);
-    stream::launch<1>((int)block_m, (int)(K / 128), grid, g, shuffled, stream);
+    // split-K: only the M-blocks the partial buffers cover can hold routed rows
+    const int64_t mblocks = g.ksplit > 1 ? g.kmb : max_m_blocks;
+    const dim3 grid((unsigned)(inter / 128 * g.ksplit), (unsigned)mblocks);
+    stream::launch<1>((int)block_m, (int)(K / 128 / g.ksplit), grid, g, shuffled, stream);
     AMD_HIP_CHECK(hipGetLastError());
 }
 

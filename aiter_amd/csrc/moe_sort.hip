@@ -51,6 +51,8 @@ struct SortParams {
     int64_t zero_row_bytes;     // multiple of 16
     int64_t zero_skip16;        // leading 16-byte units of zero_buf left to the clear launch
                                 // (they hold the chunk counts when ws lives in zero_buf)
+    void* zero2;                // a second region cleared whole (may be null): the
+    int64_t zero2_n16;          // stage-1 split-K arrival counters, in 16-byte units
     int rows;
     int topk;
     int E;
@@ -81,16 +83,22 @@ __device__ __forceinline__ int sort_tokens(const SortParams& p) {
     return min(max(t, 0), p.rows);
 }
 
-// Clear the accumulator rows [0, tokens) with 16-byte stores; run by the
-// blocks of a launch that are not sorting.
+// Clear the accumulator rows [0, tokens) and the whole second region with
+// 16-byte stores; run by the blocks of a launch that are not sorting.
 __device__ void zero_rows(const SortParams& p, int tokens, int block, int nblocks) {
-    if (!p.zero_buf || nblocks <= 0) return;
-    int64_t n16 = (int64_t)tokens * p.zero_row_bytes / 16;
-    v4i z = {0, 0, 0, 0};
-    v4i* dst = reinterpret_cast<v4i*>(p.zero_buf);
-    for (int64_t i = p.zero_skip16 + (int64_t)block * kSortThreads + threadIdx.x; i < n16;
-         i += (int64_t)nblocks * kSortThreads)
-        dst[i] = z;
+    if (nblocks <= 0) return;
+    const v4i z = {0, 0, 0, 0};
+    const int64_t first = (int64_t)block * kSortThreads + threadIdx.x;
+    const int64_t stride = (int64_t)nblocks * kSortThreads;
+    if (p.zero_buf) {
+        const int64_t n16 = (int64_t)tokens * p.zero_row_bytes / 16;
+        v4i* dst = reinterpret_cast<v4i*>(p.zero_buf);
+        for (int64_t i = p.zero_skip16 + first; i < n16; i += stride) dst[i] = z;
+    }
+    if (p.zero2) {
+        v4i* dst = reinterpret_cast<v4i*>(p.zero2);
+        for (int64_t i = first; i < p.zero2_n16; i += stride) dst[i] = z;
+    }
 }
 
 // Clears the chunk counts once the scatter launch has read them, when they
@@ -478,7 +486,9 @@ bool launch_moe_sort(const int32_t* topk_ids, const float* topk_w, const int32_t
                      int32_t* sorted_eids, int32_t* num_valid, void* zero_buf,
                      int64_t zero_row_bytes, int64_t rows, int64_t topk, int64_t E, int64_t bm,
                      void* ws, int64_t ws_bytes, hipStream_t stream, const void* qx,
-                     int qx_dtype, uint8_t* qq, float* qs, int64_t q_cols) {
+                     int qx_dtype, uint8_t* qq, float* qs, int64_t q_cols, void* zero2,
+                     int64_t zero2_bytes) {
+    AMD_CHECK(zero2_bytes % 16 == 0, "second clear region must be a multiple of 16 bytes");
     SortParams p;
     p.topk_ids = topk_ids;
     p.topk_w = topk_w;
@@ -491,6 +501,8 @@ bool launch_moe_sort(const int32_t* topk_ids, const float* topk_w, const int32_t
     p.zero_buf = zero_buf;
     p.zero_row_bytes = zero_row_bytes;
     p.zero_skip16 = 0;
+    p.zero2 = zero2_bytes > 0 ? zero2 : nullptr;
+    p.zero2_n16 = zero2_bytes / 16;
     p.rows = (int)rows;
     p.topk = (int)topk;
     p.E = (int)E;
@@ -510,8 +522,8 @@ bool launch_moe_sort(const int32_t* topk_ids, const float* topk_w, const int32_t
 
     // zero blocks: about one 16-byte store per thread per 4 iterations
     int zero_blocks = 0;
-    if (zero_buf && rows > 0) {
-        int64_t n16 = rows * zero_row_bytes / 16;
+    if ((zero_buf || p.zero2) && rows > 0) {
+        int64_t n16 = (zero_buf ? rows * zero_row_bytes / 16 : 0) + p.zero2_n16;
         zero_blocks = (int)std::min<int64_t>(ceil_div(n16, (int64_t)kSortThreads * 4), 2048);
         if (zero_blocks < 1) zero_blocks = 1;
     }

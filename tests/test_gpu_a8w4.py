@@ -207,3 +207,19 @@ def test_a8w4_reference_scale_layout(cuda_device, bm):
     mx, _ = R.normalized_errors(_np(out_rm.float()), _np(out_sh.float()))
     assert mx <= 1e-2, mx
     _check(ref["out"], _np(out_sh.float()), f"A8W4 e8m0_shuffle scales bm={bm}")
+
+
+@pytest.mark.parametrize("bm,split", [(16, 2), (16, 4), (32, 8)])
+def test_a8w4_stream_stage1_split_k(cuda_device, monkeypatch, bm, split):
+    """The A8W4 decode stage 1 with its K range split over several
+    workgroups per tile (AITER_AMD_ST_KSPLIT1 forces the count): the e8m0
+    scale groups start at the split's first K step. Same bar as the unsplit
+    layer, and a second call gives the same output."""
+    cfg = _a8w4(W.MoEConfig("ksplit4", 5, 2048, 512, 8, 4, seed=42))
+    dev, ref = _make_layer(cfg, cuda_device, True)
+    monkeypatch.setenv("AITER_AMD_ST_KSPLIT1", str(split))
+    out = _run(dev, block_size_M=bm)
+    again = _run(dev, block_size_M=bm)
+    torch.cuda.synchronize()
+    _check(ref["out"], _np(out.float()), f"A8W4 split-K {split} bm={bm}")
+    assert torch.equal(out, again)

@@ -469,6 +469,28 @@ def test_stream_stage2_column_walk(cuda_device, monkeypatch, weights, bm, ntw):
             assert (acc1 - accc).abs().max().item() <= tol
 
 
+@pytest.mark.parametrize("bm,splits", [(16, (2, 4)), (32, (2, 4, 8))])
+def test_stream_stage1_split_k(cuda_device, monkeypatch, bm, splits):
+    """Decode stage 1 with its K range split over 2, 4 or 8 workgroups per
+    tile (AITER_AMD_ST_KSPLIT1 forces the count): the last workgroup of a
+    tile to arrive adds the fp32 partial sums in split order and runs the
+    SiLU*up + requant epilogue. Every split meets the oracle bar, gives the
+    same output on a second call (the arrival counters are left at zero and
+    the sum order does not depend on arrival order), and so does the
+    automatic choice (2 here: 32 tiles, fewer than 128)."""
+    cfg = W.MoEConfig("ksplit", 5, 2048, 512, 8, 4, seed=41)
+    dev, ref = _make_layer(cfg, cuda_device, True)
+    for c in (1,) + splits:
+        monkeypatch.setenv("AITER_AMD_ST_KSPLIT1", str(c))
+        out = _run(dev, block_size_M=bm)
+        again = _run(dev, block_size_M=bm)
+        torch.cuda.synchronize()
+        _check(ref["out"], _np(out.float()), f"split-K {c} bm={bm}")
+        assert torch.equal(out, again), f"split {c}: second call differs"
+    monkeypatch.delenv("AITER_AMD_ST_KSPLIT1")
+    _check(ref["out"], _np(_run(dev, block_size_M=bm).float()), f"split-K auto bm={bm}")
+
+
 def test_fused_moe_mimo_decode_t128_stagewise(cuda_device):
     """Decode T=128 at MiMo dims (the stream kernels, stage 2 walking two
     column groups per workgroup), checked per stage."""
