@@ -62,6 +62,14 @@ void launch_moe_stage1_stream(const uint8_t*, const float*, int64_t, int64_t, co
                               int64_t, int64_t, int64_t, int64_t, int, hipStream_t,
                               const float*, int, int ksplit = 1, void* kpart = nullptr,
                               int32_t* kcnt = nullptr, int64_t kmb = 0);
+// the fused layer (both GEMMs in one launch) on the stream kernel
+bool stream_fused_supported(int64_t block_m, int64_t hidden, int64_t inter);
+void launch_moe_fused_stream(const uint8_t*, const float*, int64_t, int64_t, const uint8_t*,
+                             const float*, const uint8_t*, const uint8_t*, const float*,
+                             const uint8_t*, const int32_t*, const float*, const float*,
+                             const int32_t*, const int32_t*, float*, int64_t, int64_t, int64_t,
+                             int64_t, int64_t, int64_t, int64_t, int, hipStream_t, int, int, void*,
+                             int32_t*, int64_t);
 // stage-1 split-K of the stream kernel: K ranges per tile for a layer
 // expected to route est_blocks M-blocks, and its partial-sum bytes
 int stream_stage1_ksplit(int64_t block_m, int64_t K, int64_t inter, int64_t est_blocks);
@@ -273,6 +281,20 @@ FusedLayout fused_layout(int64_t T, int64_t H, int64_t I, int64_t E_sort, int64_
     return L;
 }
 
+// Whether the two-launch entries run both GEMMs in one launch anyway
+// (AITER_AMD_FUSED=1, a test and measurement switch). By default they keep
+// two launches: measured on MI355X at MiMo dims, the one-launch layer is
+// 2-4% faster at T = 2..4 and 3-20% slower at T = 1, 8, 32 (FP8 and A8W4),
+// so the caller chooses it per shape (the tuned table's run_1stage) through
+// the _1stage entries.
+bool use_fused_layer(int64_t tokens, int64_t topk, int64_t bm, int64_t H, int64_t I) {
+    (void)tokens;
+    (void)topk;
+    if (!stream_fused_supported(bm, H, I)) return false;
+    const char* env = getenv("AITER_AMD_FUSED");
+    return env && atoi(env) != 0;
+}
+
 int64_t default_block_m(int64_t tokens, int64_t topk, int64_t E, int64_t model_dim,
                         int64_t inter_dim) {
     // measured on MI355X (MiMo shape, FP8 and A8W4): 16-row blocks while experts
@@ -379,7 +401,7 @@ void fused_entry(const void* hidden_states, int hidden_dtype, const void* w1, WS
                  int out_dtype, int64_t tokens, int64_t model_dim, int64_t inter_dim,
                  int64_t num_experts, int64_t global_experts, int64_t topk, int64_t block_m,
                  int64_t activation, int64_t doweight_stage1, int64_t w_shuffled,
-                 void* workspace, int64_t workspace_bytes, void* stream) {
+                 void* workspace, int64_t workspace_bytes, void* stream, bool one_launch = false) {
     check_dims(model_dim, inter_dim);
     AMD_CHECK(activation == kActSilu || activation == kActGelu,
               "only ActivationType.Silu (0) and Gelu (1) are supported, got " +
@@ -393,6 +415,9 @@ void fused_entry(const void* hidden_states, int hidden_dtype, const void* w1, WS
               "global_experts must be in [num_experts, 4096]");
     if (block_m <= 0) block_m = default_block_m(tokens, topk, num_experts, model_dim, inter_dim);
     check_block_m_gemm(block_m, model_dim, inter_dim, tokens, topk);
+    AMD_CHECK(!one_launch || stream_fused_supported(block_m, model_dim, inter_dim),
+              "the one-launch layer needs block_m 16 or 32 and model_dim a multiple of 256 up "
+              "to 8192");
     if (tokens == 0) return;
     check_ptr(hidden_states, "hidden_states");
     check_ptr(w1, "w1");
@@ -435,6 +460,21 @@ void fused_entry(const void* hidden_states, int hidden_dtype, const void* w1, WS
     const int sh = (int)(w_shuffled != 0);
     // doweight_stage1: the routing weights scale stage 1's gate and up, stage 2 sums unweighted
     const bool dw = doweight_stage1 != 0;
+    if (!part && (one_launch || use_fused_layer(tokens, topk, block_m, model_dim, inter_dim))) {
+        // decode sizes: both GEMMs in one launch, a2 kept per workgroup in LDS
+        launch_moe_fused_stream(a1, a1_scale, model_dim / 128, 1, (const uint8_t*)w1, w1s.f32,
+                                w1s.e8m0, (const uint8_t*)w2, w2s.f32, w2s.e8m0, sorted_ids,
+                                dw ? sorted_w : nullptr, dw ? nullptr : sorted_w, sorted_eids,
+                                num_valid, acc, tokens, model_dim, inter_dim, num_experts, topk,
+                                block_m, L.blocks, sh, s, (int)activation, L.ksplit,
+                                ws + L.off_kpart, reinterpret_cast<int32_t*>(ws + L.off_kcnt),
+                                L.kmb);
+        timing_mark(3, s);
+        timing_mark(4, s);
+        launch_acc_to_out(acc, out, out_dtype, num_valid, tokens, model_dim, s);
+        timing_mark(5, s);
+        return;
+    }
     stage1_dispatch(a1, a1_scale, model_dim / 128, 1, (const uint8_t*)w1, w1s, sorted_ids,
                     sorted_eids, num_valid, a2, a2_scale, tokens, model_dim, inter_dim,
                     num_experts, topk, block_m, L.blocks, sh, s, dw ? sorted_w : nullptr,
@@ -789,6 +829,43 @@ int aiter_amd_fused_moe_a8w4(const void* hidden_states, int hidden_dtype, const 
                     num_local_tokens, out, out_dtype, tokens, model_dim, inter_dim, num_experts,
                     global_experts, topk, block_m, activation, doweight_stage1, w_shuffled, workspace,
                     workspace_bytes, stream);
+    });
+}
+
+int aiter_amd_fused_moe_1stage_fp8_blockscale(
+    const void* hidden_states, int hidden_dtype, const void* w1, const float* w1_scale,
+    const void* w2, const float* w2_scale, const float* topk_weights, const int32_t* topk_ids,
+    const int32_t* expert_mask, const int32_t* num_local_tokens, void* out, int out_dtype,
+    int64_t tokens, int64_t model_dim, int64_t inter_dim, int64_t num_experts,
+    int64_t global_experts, int64_t topk, int64_t block_m, int64_t activation,
+    int64_t doweight_stage1, int64_t w_shuffled, void* workspace, int64_t workspace_bytes,
+    void* stream) {
+    return safe_call([&] {
+        AMD_CHECK(w1_scale && w2_scale, "a required pointer is NULL");
+        fused_entry(hidden_states, hidden_dtype, w1, WScale{w1_scale, nullptr}, w2,
+                    WScale{w2_scale, nullptr}, topk_weights, topk_ids, expert_mask,
+                    num_local_tokens, out, out_dtype, tokens, model_dim, inter_dim, num_experts,
+                    global_experts, topk, block_m, activation, doweight_stage1, w_shuffled, workspace,
+                    workspace_bytes, stream, true);
+    });
+}
+
+int aiter_amd_fused_moe_1stage_a8w4(
+    const void* hidden_states, int hidden_dtype, const void* w1, const uint8_t* w1_scale,
+    const void* w2, const uint8_t* w2_scale, const float* topk_weights, const int32_t* topk_ids,
+    const int32_t* expert_mask, const int32_t* num_local_tokens, void* out, int out_dtype,
+    int64_t tokens, int64_t model_dim, int64_t inter_dim, int64_t num_experts,
+    int64_t global_experts, int64_t topk, int64_t block_m, int64_t activation,
+    int64_t doweight_stage1, int64_t w_shuffled, void* workspace, int64_t workspace_bytes,
+    void* stream) {
+    return safe_call([&] {
+        check_e8m0(w1_scale, "w1_scale");
+        check_e8m0(w2_scale, "w2_scale");
+        fused_entry(hidden_states, hidden_dtype, w1, WScale{nullptr, w1_scale}, w2,
+                    WScale{nullptr, w2_scale}, topk_weights, topk_ids, expert_mask,
+                    num_local_tokens, out, out_dtype, tokens, model_dim, inter_dim, num_experts,
+                    global_experts, topk, block_m, activation, doweight_stage1, w_shuffled, workspace,
+                    workspace_bytes, stream, true);
     });
 }
 

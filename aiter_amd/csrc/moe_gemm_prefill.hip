@@ -289,7 +289,7 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
 
     using BS = BStep<W4, NCT>;
     // B of K block kb of column tile jt (wave-uniform offsets)
-    auto load_b = [&](BS& s, int kb, int jt) {
+    auto load_b = [&](BS& s, int kb, int jt) __attribute__((always_inline)) {
         const int so = __builtin_amdgcn_readfirstlane(kb * BSTEP + jt * (TROWS * KBY));
         const int sso = __builtin_amdgcn_readfirstlane(kb * 4 + jt * (TROWS * KS));
 #pragma unroll
@@ -304,12 +304,12 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
     // A of step k is staged in areg[k & 1]: loaded two steps ahead, stored
     // to LDS stage k & 1 one step ahead
     v4i areg[2][A_PT];
-    auto load_a = [&](int buf, int kb) {
+    auto load_a = [&](int buf, int kb) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < A_PT; ++j)
             areg[buf][j] = __builtin_amdgcn_raw_buffer_load_b128(ra, a_off[j], kb * 128, 0);
     };
-    auto store_a = [&](int buf) {
+    auto store_a = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < A_PT; ++j)
             *reinterpret_cast<v4i*>(&s_a[buf][a_dst[j]]) = areg[buf][j];
@@ -338,7 +338,7 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
     // (issued one region earlier) into the accumulators. The regions are
     // fenced so the scheduler cannot pair an FMA with the MFMA that feeds it
     // (which serialises a wave on MFMA latency).
-    auto compute = [&](const BS& bsv, int st, int stage, auto na) {
+    auto compute = [&](const BS& bsv, int st, int stage, auto na) __attribute__((always_inline)) {
         constexpr int NA = decltype(na)::value;
         const uint8_t* sa_src = &s_a[stage][0];
         auto afrag = [&](int rt) {
@@ -441,7 +441,7 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
     // second block (NH == 2 only): stage 1's up rows, stage 2's next 128 columns
     const float* sr_w1 = sr_w + (STAGE == 1 ? (g.inter + n0) / 128 : n0 / 128 + NH - 1) * KB;
     auto last = [&](int m) { return m < KB ? m : KB - 1; };
-    auto preheader = [&](auto nj) {
+    auto preheader = [&](auto nj) __attribute__((always_inline)) {
         constexpr int NJ = decltype(nj)::value;
         ScaleRegs<W4, NJ> sr;
         scale_load<BM, NH, W4, NJ>(sr, sr_a, g.sa_kb, sr_w0, sr_w1, KB, KBT, sr_q);
@@ -466,7 +466,7 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
     __syncthreads();                      // stage 0 and the scale products
 
     // ---- epilogue of column tile jt; stage stg of s_a holds no live A ----
-    auto epilogue = [&](int jt, int stg) {
+    auto epilogue = [&](int jt, int stg) __attribute__((always_inline)) {
         if constexpr (STAGE == 2) {
             const int nc = n0 + jt * TROWS;
             if (g.part) {
@@ -619,7 +619,7 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
         }
     };
 
-    auto kloop = [&](auto na) {
+    auto kloop = [&](auto na) __attribute__((always_inline)) {
         int kbl = 0, jt = 0;             // K block and column tile of step kb0
         for (int kb0 = 0; kb0 < KBT; kb0 += D) {
 #pragma unroll

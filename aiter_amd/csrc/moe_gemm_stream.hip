@@ -73,6 +73,20 @@ struct Args {
     v4f* kpart;
     int32_t* kcnt;
     int kmb;
+    // fused layer (STAGE 3): after stage 1 of its 128-wide slice of the
+    // intermediate dim, a workgroup multiplies the slice's requantised rows
+    // (kept in LDS) by the matching 128-wide K block of w2 [E, H, inter] for
+    // all H outputs and adds w2_route * row into acc2 [tokens, H] (fp32
+    // atomics); the per-pair a2 never leaves the workgroup
+    const uint8_t* w2;
+    const float* w2_scale;     // [E, H/128, inter/128]
+    const uint8_t* w2_scale8;  // [E, H, inter/32] e8m0 (MXFP4)
+    const float* w2_route;     // sorted routing weights for stage 2 (NULL: 1)
+    float* acc2;
+    int H;
+    // stage 1 / fused: start each workgroup's K walk (and the fused down
+    // GEMM's column walk) at a staggered offset
+    int krot;
 };
 
 // One K step of one wave's operands.
@@ -82,19 +96,27 @@ struct Step {
     v4i b[kNCT][W4 ? 1 : 2];
 };
 
+// STAGE 1: gate+up GEMM -> SiLU*up -> a2 (fp8 + 1x128 scales); STAGE 2:
+// down GEMM accumulated into acc; STAGE 3: both for one 128-wide slice of
+// the intermediate dim per workgroup (the fused layer).
 template <int BM, int STAGE, bool SHUFFLED, bool W4, int D>
 __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
     constexpr int NRT = BM / 16;
+    constexpr bool G1 = STAGE != 2;                      // runs the gate+up GEMM
+    constexpr bool FUSED = STAGE == 3;
     static_assert(BM == 16 || BM == 32, "stream tiles are 16 or 32 rows");
     __shared__ __attribute__((aligned(16))) float s_sa[kMaxKB * BM];   // [kb][row]
     // weight-scale blocks [block][kb]: stage 1 gate / up (row stride kMaxKB),
     // stage 2 the 2 * ntw 128-column blocks (row stride KB)
     __shared__ float s_sw[2 * kMaxKB];
+    __shared__ float s_w2s[FUSED ? kMaxKB : 1];          // fused: w2 scales of the slice's K block
     __shared__ int32_t s_arow[BM];
     __shared__ int64_t s_orow[BM];
     __shared__ float s_w[BM];
     __shared__ float s_amax[kWaves][BM];
-    __shared__ __attribute__((aligned(16))) uint8_t s_q[STAGE == 1 ? BM * 144 : 16];
+    __shared__ int32_t s_tok[FUSED ? BM : 1];            // fused: token of the row (or -1)
+    __shared__ float s_rs[FUSED ? BM : 1];               // fused: a2 scale x routing weight
+    __shared__ __attribute__((aligned(16))) uint8_t s_q[G1 ? BM * 144 : 16];
     __shared__ int s_last;
 
     const int tid = threadIdx.x;
@@ -113,11 +135,11 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
     // s = jt * KB + kb); stage 1 always has one tile, whose K range the S
     // workgroups blockIdx.x = tile * S + ks split
     const int ntw = STAGE == 2 ? g.ntw : 1;
-    const int S = STAGE == 1 ? g.ksplit : 1;
+    const int S = G1 ? g.ksplit : 1;
     const int nt = (int)blockIdx.x / S;
     const int ks = (int)blockIdx.x - nt * S;
     if (S > 1 && mb >= g.kmb) return;    // never: a routed M-block holds >= 1 of the tokens*topk pairs
-    const int n0 = nt * (STAGE == 1 ? 128 : 256 * ntw);
+    const int n0 = nt * (G1 ? 128 : 256 * ntw);
 
     for (int r = tid; r < BM; r += kThreads) {
         const uint32_t id = (uint32_t)g.sorted_ids[mb * BM + r];
@@ -127,12 +149,16 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
         const int64_t pair = (int64_t)t * g.topk + s;
         int64_t arow = -1, orow = -1;
         if (valid) {
-            arow = STAGE == 1 ? (int64_t)t : pair;
-            orow = STAGE == 1 ? pair : (int64_t)t;
+            arow = G1 ? (int64_t)t : pair;
+            orow = G1 ? pair : (int64_t)t;
             if (arow >= g.a_rows) arow = orow = -1;
         }
         s_arow[r] = (int32_t)arow;
         s_orow[r] = orow;
+        if constexpr (FUSED) {
+            s_tok[r] = orow >= 0 ? t : -1;
+            s_rs[r] = orow >= 0 && g.w2_route ? g.w2_route[mb * BM + r] : 1.0f;
+        }
         // routing weight of the pair (1 when none is passed: stage 2 without
         // weights, or stage 1 without doweight); stage 1 applies it only when given
         s_w[r] = valid ? (g.sorted_w ? g.sorted_w[mb * BM + r] : 1.0f) : 0.0f;
@@ -157,11 +183,17 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
         // stage 1: blocks gate, up; stage 2: the 2 * ntw 128-column blocks
         const float* wse = g.w_scale + (int64_t)e * (g.N / 128) * KB;
         const int nb0 = n0 / 128;
-        const int nb1 = STAGE == 1 ? (g.inter + n0) / 128 : n0 / 128 + 1;
+        const int nb1 = G1 ? (g.inter + n0) / 128 : n0 / 128 + 1;
         for (int i = tid; i < 2 * ntw * KB; i += kThreads) {
             const int blk = i / KB;
-            s_sw[blk * (STAGE == 1 ? kMaxKB : KB) + i % KB] =
-                wse[(STAGE == 1 ? (blk == 0 ? nb0 : nb1) : nb0 + blk) * KB + (i % KB)];
+            s_sw[blk * (G1 ? kMaxKB : KB) + i % KB] =
+                wse[(G1 ? (blk == 0 ? nb0 : nb1) : nb0 + blk) * KB + (i % KB)];
+        }
+        if constexpr (FUSED) {
+            // w2_scale[e, nb, n0 / 128] for the H / 128 output blocks nb
+            const int KB2 = g.inter / 128;
+            for (int nb = tid; nb < g.H / 128; nb += kThreads)
+                s_w2s[nb] = g.w2_scale[((int64_t)e * (g.H / 128) + nb) * KB2 + n0 / 128];
         }
     }
     __syncthreads();
@@ -173,7 +205,7 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
 #pragma unroll
     for (int ct = 0; ct < kNCT; ++ct) {
         int row0;
-        if (STAGE == 1)
+        if (G1)
             row0 = ct < 2 ? n0 + 32 * wv + 16 * ct : g.inter + n0 + 32 * wv + 16 * (ct - 2);
         else
             row0 = n0 + 64 * wv + 16 * ct;
@@ -243,9 +275,9 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
     auto compute = [&](const Step<NRT, W4>& s, int kb, int jt, const int (&sg)[kNCT][D], int d) {
         // stage 1: tiles 0,1 gate (scale block 0), 2,3 up (block 1); stage 2:
         // the wave's 64 columns lie in 128-column block wv/2 of group jt
-        const float sw0 = W4 ? 1.0f : STAGE == 1 ? s_sw[kb] : s_sw[(2 * jt + (wv >> 1)) * KB + kb];
+        const float sw0 = W4 ? 1.0f : G1 ? s_sw[kb] : s_sw[(2 * jt + (wv >> 1)) * KB + kb];
         const float sw1 =
-            W4 ? 1.0f : STAGE == 1 ? s_sw[kMaxKB + kb] : s_sw[(2 * jt + (wv >> 1)) * KB + kb];
+            W4 ? 1.0f : G1 ? s_sw[kMaxKB + kb] : s_sw[(2 * jt + (wv >> 1)) * KB + kb];
 #pragma unroll
         for (int rt = 0; rt < NRT; ++rt) {
             const v4f sa = *reinterpret_cast<const v4f*>(&s_sa[kb * BM + rt * 16 + 4 * lq]);
@@ -290,11 +322,20 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
             }
     };
 
+    // stage 1: K step k of the walk is K block km(k), the walk rotated by a
+    // per-workgroup multiple of D so that concurrent workgroups stream
+    // different offsets of their weight rows
+    const int krot = G1 && g.krot ? D * (int)((blockIdx.x * 5u + blockIdx.y * 3u) % (KBS / D)) : 0;
+    auto km = [&](int k) {
+        int r = k - kbeg + krot;
+        if (r >= KBS) r -= KBS;
+        return kbeg + r;
+    };
     Step<NRT, W4> buf[D];
     int sgc[kNCT][D], sgn[kNCT][D];            // A8W4 scales: current / next group
-    if (W4) load_sg(sgc, kbeg, 0);
+    if (W4) load_sg(sgc, G1 ? km(kbeg) : kbeg, 0);
 #pragma unroll
-    for (int d = 0; d < D; ++d) load(buf[d], kbeg + d, 0);
+    for (int d = 0; d < D; ++d) load(buf[d], G1 ? km(kbeg + d) : kbeg + d, 0);
     auto next_scales = [&]() {
         if (W4) {
 #pragma unroll
@@ -303,19 +344,19 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
                 for (int d = 0; d < D; ++d) sgc[ct][d] = sgn[ct][d];
         }
     };
-    if constexpr (STAGE == 1) {
+    if constexpr (G1) {
         // ---- K loop over [kbeg, kend): D steps in flight ----
         for (int kb0 = kbeg; kb0 < kend - D; kb0 += D) {
-            if (W4) load_sg(sgn, kb0 + D, 0);
+            if (W4) load_sg(sgn, km(kb0 + D), 0);
 #pragma unroll
             for (int d = 0; d < D; ++d) {
-                compute(buf[d], kb0 + d, 0, sgc, d);
-                load(buf[d], kb0 + d + D, 0);
+                compute(buf[d], km(kb0 + d), 0, sgc, d);
+                load(buf[d], km(kb0 + d + D), 0);
             }
             next_scales();
         }
 #pragma unroll
-        for (int d = 0; d < D; ++d) compute(buf[d], kend - D + d, 0, sgc, d);
+        for (int d = 0; d < D; ++d) compute(buf[d], km(kend - D + d), 0, sgc, d);
         if (S > 1) {
             // ---- split-K: publish this K range's partial sums; the last
             // workgroup of the tile to arrive adds all S in split order (the
@@ -396,6 +437,55 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
         return;
     }
 
+    // ---- fused: the down GEMM's weight sources; its first D2 column groups
+    // are loaded before the stage-1 epilogue, which they do not depend on ----
+    const int H = g.H;
+    const int NG = FUSED ? H / 256 : 0;
+    // groups of w2 fragments in flight (fp8 fragments take twice the registers)
+    constexpr int D2 = W4 || D < 2 ? D : 2;
+    const int I2 = g.inter;
+    const int kb2 = n0 / 128;
+    const int64_t KY2 = W4 ? I2 / 2 : I2;
+    const uint8_t* w2e = g.w2 + (int64_t)e * H * KY2;
+    const uint8_t* b2src[kNCT];
+    const uint8_t* b2ssrc[kNCT];
+#pragma unroll
+    for (int ct = 0; ct < kNCT; ++ct) {
+        const int row0 = 64 * wv + 16 * ct;
+        if (W4)
+            b2src[ct] = SHUFFLED ? w2e + row0 * KY2 + lane * 16 + kb2 * 1024
+                                 : w2e + (row0 + lr) * KY2 + lq * 16 + kb2 * 64;
+        else
+            b2src[ct] = SHUFFLED ? w2e + (int64_t)row0 * I2 + lq * 512 + lr * 16 + kb2 * 2048
+                                 : w2e + (int64_t)(row0 + lr) * I2 + lq * 32 + kb2 * 128;
+        b2ssrc[ct] = W4 ? g.w2_scale8 + ((int64_t)e * H + row0 + lr) * (I2 / 32) + kb2 * 4
+                        : nullptr;
+    }
+    struct B2 {
+        v4i b[kNCT][W4 ? 1 : 2];
+        int sc[kNCT];
+    };
+    auto load2 = [&](B2& q, int gi) {
+#pragma unroll
+        for (int ct = 0; ct < kNCT; ++ct) {
+            const uint8_t* p = b2src[ct] + (int64_t)gi * 256 * KY2;
+            q.b[ct][0] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(p));
+            if (!W4)
+                q.b[ct][W4 ? 0 : 1] =
+                    __builtin_nontemporal_load(reinterpret_cast<const v4i*>(p + BHI));
+            q.sc[ct] = W4 ? *reinterpret_cast<const int*>(b2ssrc[ct] + (int64_t)gi * 256 * (I2 / 32))
+                          : 0;
+        }
+    };
+    // column group of walk position p (rotated like stage 1's K walk)
+    const int grot =
+        FUSED && g.krot ? (int)((blockIdx.x * 5u + blockIdx.y * 3u) % (unsigned)NG) : 0;
+    auto gm = [&](int p) { return p + grot < NG ? p + grot : p + grot - NG; };
+    B2 bq[D2];
+#pragma unroll
+    for (int d = 0; d < D2; ++d)
+        if (d < NG) load2(bq[d], gm(d));
+
     // ---- stage 1 epilogue: silu(gate)*up -> bf16 -> 1x128 fp8 requant ----
     // wave wv holds output columns 32*wv + 16*j + lr (j = 0, 1) of the tile's 128
     float h[NRT][2][4];
@@ -445,13 +535,72 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
         }
     __syncthreads();
     const int I = g.inter;
-    for (int q = tid; q < BM * 8; q += kThreads) {
-        const int row = q >> 3, part = q & 7;
-        const int64_t orow = s_orow[row];
-        if (orow < 0) continue;
-        *reinterpret_cast<v4i*>(g.a2 + orow * I + n0 + part * 16) =
-            *reinterpret_cast<const v4i*>(s_q + row * 144 + part * 16);
-        if (part == 0) g.a2_scale[orow * (I / 128) + n0 / 128] = row_amax(row) * kInvFp8Max;
+    if constexpr (!FUSED) {
+        for (int q = tid; q < BM * 8; q += kThreads) {
+            const int row = q >> 3, part = q & 7;
+            const int64_t orow = s_orow[row];
+            if (orow < 0) continue;
+            *reinterpret_cast<v4i*>(g.a2 + orow * I + n0 + part * 16) =
+                *reinterpret_cast<const v4i*>(s_q + row * 144 + part * 16);
+            if (part == 0) g.a2_scale[orow * (I / 128) + n0 / 128] = row_amax(row) * kInvFp8Max;
+        }
+    } else {
+        // ---- fused: the slice's requantised rows (s_q, row scale
+        // amax / 448) times w2's K block n0 / 128, for all H outputs in
+        // 256-column groups (wave wv: columns 64 wv .. 64 wv + 63 of each),
+        // D groups of weight fragments in flight; each routed row adds
+        // route_w * a2_scale * w2_scale * (a2 . w2) into acc2[token] ----
+        float rs[NRT][4];
+        float* dst[NRT][4];              // the row's accumulator at this wave's first column
+        v8i af[NRT];
+#pragma unroll
+        for (int rt = 0; rt < NRT; ++rt) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int row = rt * 16 + 4 * lq + v;
+                const int t = s_tok[row];
+                rs[rt][v] = t >= 0 ? row_amax(row) * kInvFp8Max * s_rs[row] : 0.0f;
+                dst[rt][v] = t >= 0 ? g.acc2 + (int64_t)t * H + 64 * wv + lr : nullptr;
+            }
+            // fp8 x fp8 pairs K 32q..32q+31; fp8 x fp4 takes K 16q..16q+15 and
+            // 64+16q..64+16q+15 in the A lane
+            const uint8_t* p = s_q + (rt * 16 + lr) * 144 + (W4 ? lq * 16 : lq * 32);
+            const v4i lo = *reinterpret_cast<const v4i*>(p);
+            const v4i hi = *reinterpret_cast<const v4i*>(p + (W4 ? 64 : 16));
+            af[rt] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        }
+        for (int gi0 = 0; gi0 < NG; gi0 += D2) {
+#pragma unroll
+            for (int d = 0; d < D2; ++d) {
+                if (gi0 + d >= NG) break;
+                const int gi = gm(gi0 + d);
+                const float w2s = W4 ? 1.0f : s_w2s[2 * gi + (wv >> 1)];
+#pragma unroll
+                for (int ct = 0; ct < kNCT; ++ct) {
+#pragma unroll
+                    for (int rt = 0; rt < NRT; ++rt) {
+                        v4f blk;
+                        if (W4) {
+                            const v8i bf = v8i{bq[d].b[ct][0][0], bq[d].b[ct][0][1],
+                                               bq[d].b[ct][0][2], bq[d].b[ct][0][3], 0, 0, 0, 0};
+                            blk = mfma16x16x128_fp8_fp4(af[rt], bf, bq[d].sc[ct] >> (8 * lq));
+                        } else {
+                            const v8i bf = v8i{bq[d].b[ct][0][0], bq[d].b[ct][0][1],
+                                               bq[d].b[ct][0][2], bq[d].b[ct][0][3],
+                                               bq[d].b[ct][W4 ? 0 : 1][0], bq[d].b[ct][W4 ? 0 : 1][1],
+                                               bq[d].b[ct][W4 ? 0 : 1][2], bq[d].b[ct][W4 ? 0 : 1][3]};
+                            blk = mfma16x16x128_fp8(af[rt], bf);
+                        }
+#pragma unroll
+                        for (int v = 0; v < 4; ++v)
+                            if (dst[rt][v])
+                                unsafeAtomicAdd(dst[rt][v] + gi * 256 + 16 * ct,
+                                                blk[v] * (rs[rt][v] * w2s));
+                    }
+                }
+                if (gi0 + d + D2 < NG) load2(bq[d], gm(gi0 + d + D2));
+            }
+        }
     }
 }
 
@@ -546,6 +695,15 @@ static int pick_ksplit1(int64_t bm, int64_t KB, int64_t n_tiles, int64_t est_blo
     return est_blocks * n_tiles < kSplitBelow && fits(2) ? 2 : 1;
 }
 
+// Staggered K walks: measured on MI355X at MiMo dims, T=32 FP8 0.6515 ->
+// 0.6386 ms and A8W4 0.3744 -> 0.3680 ms, T=1 and T=8 unchanged (every
+// workgroup then reads a different 2 KB of its 64 KB weight-row groups at a
+// time). AITER_AMD_ST_ROT=0 turns it off.
+static int k_rotation() {
+    const char* env = getenv("AITER_AMD_ST_ROT");
+    return !env || atoi(env) != 0;
+}
+
 }  // namespace stream
 
 bool stream_supported(int64_t block_m, int64_t K);
@@ -584,6 +742,7 @@ void launch_moe_stage1_stream(const uint8_t* a, const float* a_scale, int64_t sa
     g.kpart = reinterpret_cast<v4f*>(kpart);
     g.kcnt = kcnt;
     g.kmb = (int)std::min<int64_t>(kmb, max_m_blocks);
+    g.krot = stream::k_rotation();
     g.sorted_w = sorted_w;                 // doweight_stage1 (or NULL)
     g.act = act;
     g.a = a;
@@ -644,6 +803,70 @@ void launch_moe_stage2_stream(const uint8_t* a2, const float* a2_scale, const ui
                               std::min<int64_t>(a_rows, E));
     const dim3 grid((unsigned)(hidden / 256 / g.ntw), (unsigned)max_m_blocks);
     stream::launch<2>((int)block_m, (int)(inter / 128), grid, g, shuffled, stream);
+    AMD_HIP_CHECK(hipGetLastError());
+}
+
+// The fused layer on the stream kernel: 16/32-row M-blocks, model_dim a
+// multiple of 256 up to 8192.
+bool stream_fused_supported(int64_t block_m, int64_t hidden, int64_t inter) {
+    return stream_supported(block_m, hidden) && hidden % 256 == 0 && inter % 128 == 0;
+}
+
+// One launch for both GEMMs of a decode-sized layer (see Args::w2): grid =
+// 128-wide intermediate slices (x ksplit) x M-blocks. acc2 [tokens, hidden]
+// fp32 must be zero on entry (the sorting launch clears it); sw1: routing
+// weights applied before the activation (doweight_stage1) or NULL; sw2: the
+// routing weights of the down GEMM or NULL.
+void launch_moe_fused_stream(const uint8_t* a, const float* a_scale, int64_t sa_row,
+                             int64_t sa_kb, const uint8_t* w1, const float* w1_scale,
+                             const uint8_t* w1_scale_e8m0, const uint8_t* w2,
+                             const float* w2_scale, const uint8_t* w2_scale_e8m0,
+                             const int32_t* sorted_ids, const float* sw1, const float* sw2,
+                             const int32_t* sorted_eids, const int32_t* num_valid, float* acc2,
+                             int64_t a_rows, int64_t hidden, int64_t inter, int64_t E,
+                             int64_t topk, int64_t block_m, int64_t max_m_blocks, int shuffled,
+                             hipStream_t stream, int act, int ksplit, void* kpart, int32_t* kcnt,
+                             int64_t kmb) {
+    AMD_CHECK(stream_fused_supported(block_m, hidden, inter),
+              "the fused layer needs block_m 16 or 32 and model_dim a multiple of 256 up to 8192");
+    AMD_CHECK((w1_scale_e8m0 != nullptr) == (w2_scale_e8m0 != nullptr),
+              "w1 and w2 must both be fp8 or both MXFP4");
+    stream::Args g{};
+    g.ksplit = ksplit > 1 ? ksplit : 1;
+    AMD_CHECK(g.ksplit == 1 || (kpart && kcnt && kmb > 0 && (hidden / 128) % g.ksplit == 0),
+              "split-K needs partial and counter buffers and K steps divisible by the split");
+    g.kpart = reinterpret_cast<v4f*>(kpart);
+    g.kcnt = kcnt;
+    g.kmb = (int)std::min<int64_t>(kmb, max_m_blocks);
+    g.krot = stream::k_rotation();
+    g.sorted_w = sw1;
+    g.w2_route = sw2;
+    g.act = act;
+    g.a = a;
+    g.a_scale = a_scale;
+    g.sa_row = sa_row;
+    g.sa_kb = sa_kb;
+    g.w = w1;
+    g.w_scale = w1_scale;
+    g.w_scale8 = w1_scale_e8m0;
+    g.w2 = w2;
+    g.w2_scale = w2_scale;
+    g.w2_scale8 = w2_scale_e8m0;
+    g.acc2 = acc2;
+    g.H = (int)hidden;
+    g.sorted_ids = sorted_ids;
+    g.sorted_eids = sorted_eids;
+    g.num_valid = num_valid;
+    g.K = (int)hidden;
+    g.N = (int)(2 * inter);
+    g.inter = (int)inter;
+    g.topk = (int)topk;
+    g.E = (int)E;
+    g.a_rows = a_rows;
+    if (max_m_blocks == 0) return;
+    const int64_t mblocks = g.ksplit > 1 ? g.kmb : max_m_blocks;
+    const dim3 grid((unsigned)(inter / 128 * g.ksplit), (unsigned)mblocks);
+    stream::launch<3>((int)block_m, (int)(hidden / 128 / g.ksplit), grid, g, shuffled, stream);
     AMD_HIP_CHECK(hipGetLastError());
 }
 

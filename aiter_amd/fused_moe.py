@@ -17,6 +17,7 @@ Anything else raises NotImplementedError; there is no fallback path.
 from __future__ import annotations
 
 import functools
+import os
 from typing import Optional
 
 import torch
@@ -25,7 +26,7 @@ from . import _abi, ffi
 from .enums import AITER_DTYPE, ActivationType, QuantType, dtypes, quant_remap
 from .quant import e8m0_unshuffle, per_group_quant_hip
 from .topk import fused_topk  # noqa: F401  (aiter.fused_moe.fused_topk)
-from .tune import tuned_block_m
+from .tune import tuned_block_m, tuned_config
 
 BLOCK_SIZE_M = 32
 
@@ -232,6 +233,23 @@ def select_block_m(tokens: int, topk: int, num_experts: int, model_dim: int, int
     return bm
 
 
+def select_run_1stage(tokens: int, topk: int, num_experts: int, model_dim: int,
+                      inter_dim: int, a8w4: bool, block_m: int, device: torch.device) -> bool:
+    """Whether fused_moe runs the one-launch layer (both GEMMs in one kernel,
+    the role of the reference's fused_moe_1stage): AITER_AMD_FUSED=0/1 when
+    set, else the tuned table's run_1stage for this shape (the reference's
+    cfg["run_1stage"], aiter/fused_moe.py:903-911). The one-launch kernel
+    runs 16/32-row M-blocks with model_dim a multiple of 256 up to 8192."""
+    if block_m not in (16, 32) or model_dim % 256 or model_dim > 8192:
+        return False
+    env = os.environ.get("AITER_AMD_FUSED")
+    if env is not None:
+        return int(env) != 0
+    cfg = tuned_config(_cu_num(device), tokens, model_dim, inter_dim, num_experts, topk,
+                       "per_1x32" if a8w4 else "per_1x128", "fp4x2" if a8w4 else "fp8")
+    return bool(cfg and cfg[1])
+
+
 def e8m0_rowmajor(scale: torch.Tensor, E: int, N: int, KS: int) -> torch.Tensor:
     """The kernels' MXFP4 scale layout, row-major e8m0 bytes [E, N, KS], from
     either form a caller may hold:
@@ -424,8 +442,11 @@ def _fused_moe_impl(hidden_states, w1, w2, topk_weight, topk_ids, expert_mask, a
         ws_bytes = _abi.query("aiter_amd_fused_moe_workspace_bytes", M, model_dim, inter_dim,
                               E, global_E, topk, block_m)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
+        one = select_run_1stage(M, topk, E, model_dim, inter_dim, a8w4, block_m, device)
         _abi.call(
-            "aiter_amd_fused_moe_a8w4" if a8w4 else "aiter_amd_fused_moe_fp8_blockscale",
+            ("aiter_amd_fused_moe_1stage_a8w4" if one else "aiter_amd_fused_moe_a8w4") if a8w4
+            else ("aiter_amd_fused_moe_1stage_fp8_blockscale" if one
+                  else "aiter_amd_fused_moe_fp8_blockscale"),
             x.data_ptr(), AITER_DTYPE[x.dtype], w1c.data_ptr(), w1s.data_ptr(), w2c.data_ptr(),
             w2s.data_ptr(), topk_weight.data_ptr(), topk_ids.data_ptr(), _ptr(mask),
             _ptr(num_local_tokens), out.data_ptr(), AITER_DTYPE[out_dtype], M, model_dim,

@@ -3,8 +3,10 @@
 Plays the part of aiter's get_2stage_cfgs + tuned_fmoe.csv
 (aiter/fused_moe.py:719-1100, aiter/configs/tuned_fmoe.csv) for this path:
 one row per (cu_num, padded token count, model_dim, inter_dim, expert, topk,
-act_type, q_type, q_dtype_w) holding the block_m that measured fastest, and
-the layer time of every candidate. Token counts are bucketed as the
+act_type, q_type, q_dtype_w) holding the block_m that measured fastest, the
+layer time of every candidate, and run_1stage: 1 when the one-launch layer
+(both GEMMs in one kernel, block_m 16 or 32) beat every two-launch candidate,
+as the reference's tuned_fmoe.csv records it. Token counts are bucketed as the
 reference does (next power of two below 32768, get_padded_M,
 aiter/fused_moe.py:600-612). Shapes without a row use the heuristic
 default_block_m.
@@ -26,7 +28,8 @@ from pathlib import Path
 
 TABLE = Path(__file__).resolve().parent / "configs" / "tuned_fmoe.csv"
 COLUMNS = ["cu_num", "token", "model_dim", "inter_dim", "expert", "topk", "act_type", "q_type",
-           "q_dtype_w", "block_m", "us", "us_bm16", "us_bm32", "us_bm64", "us_bm128"]
+           "q_dtype_w", "block_m", "run_1stage", "us", "us_bm16", "us_bm32", "us_bm64",
+           "us_bm128", "us_1stage_bm16", "us_1stage_bm32"]
 _KEY = COLUMNS[:9]
 CANDIDATES = (16, 32, 64, 128)
 
@@ -42,10 +45,12 @@ def padded_tokens(m: int) -> int:
 
 @functools.lru_cache(maxsize=8)
 def _load(path: str):
+    """{key: (block_m, run_1stage)}; rows without run_1stage run two launches."""
     if not os.path.exists(path):
         return {}
     with open(path, newline="") as f:
-        return {tuple(r[c] for c in _KEY): int(r["block_m"]) for r in csv.DictReader(f)}
+        return {tuple(r[c] for c in _KEY): (int(r["block_m"]), int(r.get("run_1stage") or 0))
+                for r in csv.DictReader(f)}
 
 
 def _key(cu_num, token, model_dim, inter_dim, expert, topk, q_type, q_dtype_w):
@@ -57,6 +62,13 @@ def tuned_block_m(cu_num: int, token: int, model_dim: int, inter_dim: int, exper
                   topk: int, q_type: str, q_dtype_w: str):
     """The tuned block_m for this shape, or None when the table has no row
     (AITER_AMD_TUNED_FMOE overrides the table's path)."""
+    cfg = tuned_config(cu_num, token, model_dim, inter_dim, expert, topk, q_type, q_dtype_w)
+    return cfg[0] if cfg else None
+
+
+def tuned_config(cu_num: int, token: int, model_dim: int, inter_dim: int, expert: int,
+                 topk: int, q_type: str, q_dtype_w: str):
+    """(block_m, run_1stage) for this shape, or None when the table has no row."""
     table = _load(os.environ.get("AITER_AMD_TUNED_FMOE", str(TABLE)))
     return table.get(_key(cu_num, token, model_dim, inter_dim, expert, topk, q_type, q_dtype_w))
 
@@ -88,7 +100,15 @@ def tune(tokens, weights, model_dim, inter_dim, experts, topk, steps, warmup, lo
             x = W.make_hidden(cfg, device=dev)
             tw, ids = W.make_routing(cfg, device=dev)
             times = {}
-            for bm in _candidates(model_dim, inter_dim):
+            # (block_m, one launch): every two-launch block_m, and the
+            # one-launch layer at the block sizes it runs on
+            cands = [(bm, False) for bm in _candidates(model_dim, inter_dim)]
+            if model_dim % 256 == 0 and model_dim <= 8192:
+                cands += [(16, True), (32, True)]
+            for bm, one in cands:
+                # AITER_AMD_FUSED picks the one- or two-launch layer over the table
+                os.environ["AITER_AMD_FUSED"] = "1" if one else "0"
+
                 def run():
                     W.run_layer(wfmt, x, wts["w1"], wts["w2"], tw, ids,
                                 w1_scale=wts["w1_scale"], w2_scale=wts["w2_scale"],
@@ -102,17 +122,22 @@ def tune(tokens, weights, model_dim, inter_dim, experts, topk, steps, warmup, lo
                     run()
                 e.record()
                 torch.cuda.synchronize()
-                times[bm] = s.elapsed_time(e) / steps * 1e3
+                times[(bm, one)] = s.elapsed_time(e) / steps * 1e3
+            os.environ.pop("AITER_AMD_FUSED", None)
             best = min(times, key=times.get)
             qt = "per_1x32" if wfmt == "mxfp4" else "per_1x128"
             row = dict(zip(_KEY, _key(cu_num, T, model_dim, inter_dim, experts, topk, qt,
                                       "fp4x2" if wfmt == "mxfp4" else "fp8")))
-            row.update(block_m=best, us=round(times[best], 2),
-                       **{f"us_bm{bm}": round(times.get(bm, float("nan")), 2)
-                          for bm in CANDIDATES})
+            nan = float("nan")
+            row.update(block_m=best[0], run_1stage=int(best[1]), us=round(times[best], 2),
+                       **{f"us_bm{bm}": round(times.get((bm, False), nan), 2)
+                          for bm in CANDIDATES},
+                       **{f"us_1stage_bm{bm}": round(times.get((bm, True), nan), 2)
+                          for bm in (16, 32)})
             rows.append(row)
-            log(f"[tune] {wfmt} T={T}: block_m {best} ({times[best]:.1f} us); "
-                + ", ".join(f"{b}: {t:.1f}" for b, t in times.items()))
+            log(f"[tune] {wfmt} T={T}: block_m {best[0]}{' one launch' if best[1] else ''} "
+                f"({times[best]:.1f} us); "
+                + ", ".join(f"{b}{'/1' if o else ''}: {t:.1f}" for (b, o), t in times.items()))
     return rows
 
 

@@ -232,6 +232,38 @@ int aiter_amd_fused_moe_a8w4(const void* hidden_states, int hidden_dtype, const 
                              int64_t doweight_stage1, int64_t w_shuffled, void* workspace,
                              int64_t workspace_bytes, void* stream);
 
+/* The whole layer with both GEMMs in ONE launch; replaces fused_moe_1stage
+ * -> fmoe_fp8_blockscale_g1u1 (aiter/fused_moe.py:367-511,
+ * csrc/py_itfs_cu/asm_fmoe.cu:858-922), which the reference picks per shape
+ * from its tuned table (run_1stage). Each workgroup runs stage 1 for one
+ * 128-wide slice of inter_dim of one M-block, keeps the slice's fp8 rows
+ * (one 1x128 quant group each, as the reference's a2) on chip and adds their
+ * down-GEMM share into the fp32 accumulator; then one pass writes out.
+ * Arguments as aiter_amd_fused_moe_fp8_blockscale (same workspace size);
+ * block_m must be 16 or 32 (0: the default, which must then be one of them)
+ * and model_dim a multiple of 256 up to 8192. */
+int aiter_amd_fused_moe_1stage_fp8_blockscale(
+    const void* hidden_states, int hidden_dtype, const void* w1, const float* w1_scale,
+    const void* w2, const float* w2_scale, const float* topk_weights, const int32_t* topk_ids,
+    const int32_t* expert_mask, const int32_t* num_local_tokens, void* out, int out_dtype,
+    int64_t tokens, int64_t model_dim, int64_t inter_dim, int64_t num_experts,
+    int64_t global_experts, int64_t topk, int64_t block_m, int64_t activation,
+    int64_t doweight_stage1, int64_t w_shuffled, void* workspace, int64_t workspace_bytes,
+    void* stream);
+
+/* The one-launch layer on MXFP4 weights (A8W4); arguments as
+ * aiter_amd_fused_moe_a8w4, constraints as
+ * aiter_amd_fused_moe_1stage_fp8_blockscale. Replaces the same reference
+ * path with quant_type per_1x32 (aiter/fused_moe.py:367-511). */
+int aiter_amd_fused_moe_1stage_a8w4(
+    const void* hidden_states, int hidden_dtype, const void* w1, const uint8_t* w1_scale,
+    const void* w2, const uint8_t* w2_scale, const float* topk_weights, const int32_t* topk_ids,
+    const int32_t* expert_mask, const int32_t* num_local_tokens, void* out, int out_dtype,
+    int64_t tokens, int64_t model_dim, int64_t inter_dim, int64_t num_experts,
+    int64_t global_experts, int64_t topk, int64_t block_m, int64_t activation,
+    int64_t doweight_stage1, int64_t w_shuffled, void* workspace, int64_t workspace_bytes,
+    void* stream);
+
 /* ---- routing: top-k experts per token from the router logits ----
  * gating [tokens, num_experts] fp32/bf16/fp16 (dtype code as above),
  * contiguous; outputs topk_weights f32 and topk_ids i32 with row strides

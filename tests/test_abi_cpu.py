@@ -109,6 +109,12 @@ def test_fused_validation_errors(lib):
     masked = [16, 3, 16, 16, 16, 16, 16, 16, 16, None, 16, 3]    # expert_mask given
     _expect_error("aiter_amd_fused_moe_fp8_blockscale", *masked, 4, 4096, 2048, 8, 4, 2, 0, 0, 0,
                   1, 16, 10**9, None, match="global_experts")
+    # the one-launch entries take 16/32-row blocks and model_dim % 256 == 0 only
+    for name in ("aiter_amd_fused_moe_1stage_fp8_blockscale", "aiter_amd_fused_moe_1stage_a8w4"):
+        _expect_error(name, *base, 4, 4096, 2048, 8, 8, 2, 64, 0, 0, 1, 16, 10**9, None,
+                      match="one-launch layer needs block_m 16 or 32")
+        _expect_error(name, *base, 4, 384, 256, 8, 8, 2, 16, 0, 0, 1, 16, 10**9, None,
+                      match="one-launch layer needs")
     ws = lib.aiter_amd_fused_moe_workspace_bytes(8192, 4096, 2048, 256, 256, 8, 64)
     # sorted ids/weights + a1 + a2 + f32 accumulator dominate
     assert ws > 8192 * 4096 * (1 + 4) + 8192 * 8 * 2048
@@ -463,3 +469,39 @@ def test_no_alloc_rejects_layers_over_the_buffer():
     msg = lib.aiter_amd_get_last_error().decode()
     lib.aiter_amd_clear_last_error()
     assert "bytes of workspace" in msg, msg
+
+
+def test_tuned_table_run_1stage(tmp_path, monkeypatch):
+    """The tuned table's run_1stage column picks the one-launch layer per shape
+    (the reference's cfg["run_1stage"], aiter/fused_moe.py:903-911);
+    AITER_AMD_FUSED overrides it; rows without the column, shapes without a
+    row and block sizes the one-launch kernel does not run keep two launches."""
+    import importlib
+
+    from aiter_amd import tune
+
+    F = importlib.import_module("aiter_amd.fused_moe")   # the module, not the function
+
+    table = tmp_path / "t.csv"
+    table.write_text(
+        "cu_num,token,model_dim,inter_dim,expert,topk,act_type,q_type,q_dtype_w,block_m,"
+        "run_1stage,us\n"
+        "256,2,4096,2048,256,8,Silu,per_1x128,fp8,16,1,76.0\n"
+        "256,4,4096,2048,256,8,Silu,per_1x128,fp8,16,0,133.0\n")
+    monkeypatch.setenv("AITER_AMD_TUNED_FMOE", str(table))
+    monkeypatch.delenv("AITER_AMD_FUSED", raising=False)
+    monkeypatch.setattr(F, "_cu_num", lambda dev: 256)
+    tune._load.cache_clear()
+    try:
+        args = (4096, 2048, False, 16, torch.device("cpu"))
+        assert F.select_run_1stage(2, 8, 256, *args)
+        assert not F.select_run_1stage(4, 8, 256, *args)
+        assert not F.select_run_1stage(8, 8, 256, *args)                 # no row
+        assert not F.select_run_1stage(2, 8, 256, 4096, 2048, False, 64, torch.device("cpu"))
+        assert tune.tuned_block_m(256, 2, 4096, 2048, 256, 8, "per_1x128", "fp8") == 16
+        monkeypatch.setenv("AITER_AMD_FUSED", "0")
+        assert not F.select_run_1stage(2, 8, 256, *args)
+        monkeypatch.setenv("AITER_AMD_FUSED", "1")
+        assert F.select_run_1stage(8, 8, 256, *args)
+    finally:
+        tune._load.cache_clear()

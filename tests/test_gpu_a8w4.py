@@ -214,12 +214,27 @@ def test_a8w4_stream_stage1_split_k(cuda_device, monkeypatch, bm, split):
     """The A8W4 decode stage 1 with its K range split over several
     workgroups per tile (AITER_AMD_ST_KSPLIT1 forces the count): the e8m0
     scale groups start at the split's first K step. Same bar as the unsplit
-    layer, and a second call gives the same output."""
+    layer on two calls in a row, through both the two-launch and the
+    one-launch layer."""
     cfg = _a8w4(W.MoEConfig("ksplit4", 5, 2048, 512, 8, 4, seed=42))
     dev, ref = _make_layer(cfg, cuda_device, True)
     monkeypatch.setenv("AITER_AMD_ST_KSPLIT1", str(split))
-    out = _run(dev, block_size_M=bm)
-    again = _run(dev, block_size_M=bm)
-    torch.cuda.synchronize()
-    _check(ref["out"], _np(out.float()), f"A8W4 split-K {split} bm={bm}")
-    assert torch.equal(out, again)
+    for fused in (0, 1):
+        monkeypatch.setenv("AITER_AMD_FUSED", str(fused))
+        for call in range(2):
+            out = _run(dev, block_size_M=bm)
+            _check(ref["out"], _np(out.float()),
+                   f"A8W4 split-K {split} bm={bm} fused={fused} call {call}")
+
+
+@pytest.mark.parametrize("bm", [16, 32])
+def test_a8w4_fused_layer_one_launch(cuda_device, monkeypatch, bm):
+    """The one-launch layer on MXFP4 weights (AITER_AMD_FUSED=1): the slice's
+    fp8 rows from LDS against the fp4 K block of w2 on the scaled MFMA, with
+    the e8m0 bytes of that block. Config A against the mxfp4 oracle."""
+    monkeypatch.setenv("AITER_AMD_FUSED", "1")
+    cfg = _a8w4(W.CONFIG_A)
+    for shuffle in (True, False):
+        dev, ref = _make_layer(cfg, cuda_device, shuffle)
+        _check(ref["out"], _np(_run(dev, block_size_M=bm).float()),
+               f"A8W4 one-launch shuffle={shuffle} bm={bm}")

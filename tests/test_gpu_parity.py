@@ -474,21 +474,84 @@ def test_stream_stage1_split_k(cuda_device, monkeypatch, bm, splits):
     """Decode stage 1 with its K range split over 2, 4 or 8 workgroups per
     tile (AITER_AMD_ST_KSPLIT1 forces the count): the last workgroup of a
     tile to arrive adds the fp32 partial sums in split order and runs the
-    SiLU*up + requant epilogue. Every split meets the oracle bar, gives the
-    same output on a second call (the arrival counters are left at zero and
-    the sum order does not depend on arrival order), and so does the
-    automatic choice (2 here: 32 tiles, fewer than 128)."""
+    SiLU*up + requant epilogue. Every split meets the oracle bar on two calls
+    in a row (the arrival counters are left at zero), and so does the
+    automatic choice (2 here: 32 tiles, fewer than 128). The two-launch
+    layer is pinned, so stage 1's a2 goes through HBM."""
+    monkeypatch.setenv("AITER_AMD_FUSED", "0")
     cfg = W.MoEConfig("ksplit", 5, 2048, 512, 8, 4, seed=41)
     dev, ref = _make_layer(cfg, cuda_device, True)
     for c in (1,) + splits:
         monkeypatch.setenv("AITER_AMD_ST_KSPLIT1", str(c))
-        out = _run(dev, block_size_M=bm)
-        again = _run(dev, block_size_M=bm)
-        torch.cuda.synchronize()
-        _check(ref["out"], _np(out.float()), f"split-K {c} bm={bm}")
-        assert torch.equal(out, again), f"split {c}: second call differs"
+        for call in range(2):
+            out = _run(dev, block_size_M=bm)
+            _check(ref["out"], _np(out.float()), f"split-K {c} bm={bm} call {call}")
     monkeypatch.delenv("AITER_AMD_ST_KSPLIT1")
     _check(ref["out"], _np(_run(dev, block_size_M=bm).float()), f"split-K auto bm={bm}")
+
+
+@pytest.mark.parametrize("bm", [16, 32])
+@pytest.mark.parametrize("shuffle", [True, False])
+def test_fused_layer_one_launch(cuda_device, monkeypatch, bm, shuffle):
+    """The one-launch layer (AITER_AMD_FUSED=1 forces it): each workgroup runs
+    stage 1 for one 128-wide slice of the intermediate dim, keeps the slice's
+    requantised rows (exactly one 1x128 quant group per row, as the
+    reference's a2) in LDS and adds their down-GEMM share into the fp32
+    accumulator. Config A against the oracle at the strict bar, with the
+    plain, doweight_stage1 and Gelu variants, and with split-K (the last
+    workgroup of a slice runs both the epilogue and the down GEMM)."""
+    monkeypatch.setenv("AITER_AMD_FUSED", "1")
+    cfg = W.CONFIG_A
+    dev, ref = _make_layer(cfg, cuda_device, shuffle)
+    _check(ref["out"], _np(_run(dev, block_size_M=bm).float()), f"one-launch bm={bm}")
+    monkeypatch.setenv("AITER_AMD_ST_KSPLIT1", "2")
+    _check(ref["out"], _np(_run(dev, block_size_M=bm).float()), f"one-launch split-K bm={bm}")
+    monkeypatch.delenv("AITER_AMD_ST_KSPLIT1")
+    if shuffle:
+        dev, ref = _make_layer(cfg, cuda_device, True, doweight=True)
+        out = _run(dev, block_size_M=bm, doweight_stage1=True)
+        _check(ref["out"], _np(out.float()), f"one-launch doweight bm={bm}")
+        dev, ref = _make_layer(cfg, cuda_device, True, activation="gelu")
+        out = _run(dev, block_size_M=bm, activation=A.ActivationType.Gelu)
+        _check(ref["out"], _np(out.float()), f"one-launch gelu bm={bm}")
+
+
+@pytest.mark.parametrize("bm", [16, 32])
+def test_fused_layer_one_launch_ep_share(cuda_device, monkeypatch, bm):
+    """The one-launch layer with an expert mask: tokens with no local expert
+    give zero rows, the rest match the oracle."""
+    monkeypatch.setenv("AITER_AMD_FUSED", "1")
+    cfg = W.MoEConfig("ep_small", 96, 512, 512, 16, 4, routing="sigmoid", local_experts=4,
+                      seed=3)
+    dev, ref = _make_layer(cfg, cuda_device, True)
+    out = _run(dev, block_size_M=bm)
+    _check(ref["out"], _np(out.float()), "one-launch EP small")
+    none_local = (ref["ids_local"] < 0).all(axis=1)
+    assert none_local.any()
+    assert torch.count_nonzero(out[torch.from_numpy(none_local).to(cuda_device)]).item() == 0
+
+
+@pytest.mark.parametrize("T", [1, 8, 32])
+def test_fused_layer_one_launch_vs_two_stage_mimo(cuda_device, monkeypatch, T):
+    """At MiMo decode dims the one-launch layer and the two-launch layer
+    compute the same a2 (same kernel code, same requant) and differ only in
+    the fp32 atomic order of the down GEMM: outputs agree to a few bf16 ulps
+    of the largest element."""
+    cfg = W.mimo_decode(T)
+    wts = W.make_weights(cfg, device=cuda_device, shuffle=True)
+    x = W.make_hidden(cfg, device=cuda_device)
+    tw, ids = W.make_routing(cfg, device=cuda_device)
+
+    def layer(fused):
+        monkeypatch.setenv("AITER_AMD_FUSED", str(fused))
+        return A.fused_moe(x, wts["w1"], wts["w2"], tw, ids, quant_type=A.QuantType.per_128x128,
+                           w1_scale=wts["w1_scale"], w2_scale=wts["w2_scale"]).float()
+
+    one, two = layer(1), layer(0)
+    torch.cuda.synchronize()
+    mx, rms = R.normalized_errors(_np(two), _np(one))
+    print(f"[one vs two launches T={T}] max-rel {mx:.3e} rms-rel {rms:.3e}", flush=True)
+    assert mx <= 2e-2 and rms <= 2e-3 and torch.count_nonzero(one).item() > 0
 
 
 def test_fused_moe_mimo_decode_t128_stagewise(cuda_device):
