@@ -310,6 +310,15 @@ __global__ __launch_bounds__(kThreads, 1) void moe_gemm_fp8bs_v2_kernel(Args g) 
         for (int ct = 0; ct < 4; ++ct) acc[rt][ct] = v4f{0.f, 0.f, 0.f, 0.f};
     const int row_base = wm * (BM / 2);
     const int h0 = frag_swap(lr);
+    // a wave whose BM/2 rows are all padding (sorting pads an expert's last
+    // block at its end, so the second half of a block at most half full)
+    // skips its MFMAs and FMAs: it still issues its share of every step's
+    // loads and meets every barrier, its accumulators stay 0 and no row of
+    // it is stored
+    bool wave_rows = false;
+#pragma unroll
+    for (int rt = 0; rt < NRT; ++rt)
+        wave_rows |= __builtin_amdgcn_ballot_w64(s_arow[row_base + rt * 16 + lr] >= 0) != 0;
 
     // One K step of the wave's (BM/2) x 128 tile, software-pipelined across
     // column tiles: the NRT MFMAs of tile c+1 go into the other of two
@@ -406,7 +415,7 @@ __global__ __launch_bounds__(kThreads, 1) void moe_gemm_fp8bs_v2_kernel(Args g) 
         __syncthreads();
         const int ls = cs == 0 ? kStages - 1 : cs - 1;   // buffer step kb-1 used
         issue(kb + kStages - 1, ls);
-        compute(kb, cs);
+        if (wave_rows) compute(kb, cs);
         cs = cs == kStages - 1 ? 0 : cs + 1;
     }
     wait_vm<0>();
