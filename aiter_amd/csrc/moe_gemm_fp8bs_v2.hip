@@ -25,7 +25,8 @@
 // reads.  Within each slot the two 16-byte halves are swapped for rows
 // with h0(r) = ((r >> 2) ^ (r >> 3)) & 1, so each 16-byte read of 8 or 16
 // consecutive lanes covers distinct banks.
-//   A tile: [kq 4][row BM][32 B];  B tile: 16 groups of 16 weight rows,
+//   A tile: [row BM][128 B], the 16-byte pieces of row r XOR-swizzled by
+//   a_swz(r), so each A DMA reads 8 whole rows;  B tile: 16 groups of 16 weight rows,
 //   each [kq 4][row 16][32 B] (the (16,16) shuffled 2 KB block with the two
 //   16-byte halves of a row brought together).  The DMA lane -> global
 //   address map does the reordering.
@@ -96,8 +97,14 @@ __device__ __forceinline__ Rsrc make_rsrc(const void* base, uint32_t bytes) {
     return r;
 }
 
-// Which 16-byte half of row r's 32-byte fragment slot holds K bytes 0-15.
+// Which 16-byte half of row r's 32-byte fragment slot holds K bytes 0-15
+// (the B tile).
 __device__ __forceinline__ int frag_swap(int r) { return ((r >> 2) ^ (r >> 3)) & 1; }
+
+// The A tile of a K step is [row][128 B] with piece p of row r at slot
+// p ^ a_swz(r): 16 consecutive rows put one piece in 16 distinct
+// (bank-half, slot) pairs, so fragment reads are conflict-free.
+__device__ __forceinline__ int a_swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
     return (uint32_t)reinterpret_cast<uintptr_t>((lds_void_t)(void*)p);
@@ -233,15 +240,15 @@ __global__ __launch_bounds__(kThreads, 1) void moe_gemm_fp8bs_v2_kernel(Args g) 
     // ---- per-lane DMA sources (byte offsets; the K step goes in soffset) ----
     uint32_t a_off[A_INSTR];
 #pragma unroll
-    for (int i = 0; i < A_INSTR; ++i) {   // 1 KB chunk c: rows r0..r0+31 of quarter kq
+    for (int i = 0; i < A_INSTR; ++i) {   // 1 KB chunk c: whole rows 8c .. 8c+7
+        // lane l fills LDS slot l % 8 of row 8c + l / 8, i.e. fetches the piece
+        // (l % 8) ^ a_swz(row): each DMA reads 8 whole 128-byte rows
         const int c = wvu * A_INSTR + i;
-        const int kq = c / (BM / 32);
-        const int row = (c % (BM / 32)) * 32 + (lane >> 1);
-        const int h = (lane & 1) ^ frag_swap(row);
+        const int row = c * 8 + (lane >> 3);
+        const int pc = (lane & 7) ^ a_swz(row);
         int arow = s_arow[row];
         if (arow < 0) arow = 0;           // pad rows: any valid row, result unused
-        a_off[i] = (uint32_t)arow * (uint32_t)K +
-                   (uint32_t)(W4 ? kq * 16 + h * 64 : kq * 32 + h * 16);
+        a_off[i] = (uint32_t)arow * (uint32_t)K + (uint32_t)(pc * 16);
     }
     uint32_t b_off[B_INSTR];
 #pragma unroll
@@ -336,11 +343,17 @@ __global__ __launch_bounds__(kThreads, 1) void moe_gemm_fp8bs_v2_kernel(Args g) 
             const v4i hi = *reinterpret_cast<const v4i*>(slot + (h0 ^ 1) * 16);
             return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         };
+        // the lane's 32 K bytes of row tile rt: fp8 x fp8 pieces 2 lq, 2 lq + 1
+        // (K 32 lq ..); fp8 x fp4 pieces lq, lq + 4 (K 16 lq .. and 64 + 16 lq ..)
         v8i afrag[NRT];
 #pragma unroll
         for (int rt = 0; rt < NRT; ++rt) {
             const int row = row_base + rt * 16 + lr;
-            afrag[rt] = frag(sa_src + lq * (BM * 32) + row * 32);
+            const uint8_t* rp = sa_src + row * 128;
+            const int p0 = W4 ? lq : 2 * lq, p1 = W4 ? lq + 4 : 2 * lq + 1;
+            const v4i lo = *reinterpret_cast<const v4i*>(rp + ((p0 ^ a_swz(row)) << 4));
+            const v4i hi = *reinterpret_cast<const v4i*>(rp + ((p1 ^ a_swz(row)) << 4));
+            afrag[rt] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         }
         // column tile ct (0..3) -> 16-row weight group: stage 1 tiles 0,1 are gate
         // rows, 2,3 the matching up rows; stage 2 four consecutive groups

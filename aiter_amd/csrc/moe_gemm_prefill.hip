@@ -74,7 +74,11 @@ struct Args {
     int ntw;                   // column tiles per workgroup, walked in one pipelined K loop
 };
 
-__device__ __forceinline__ int frag_swap(int r) { return ((r >> 2) ^ (r >> 3)) & 1; }
+// Slot of a row's 16-byte A piece in LDS: piece p of row r sits at slot
+// p ^ a_swz(r). Any 16 consecutive rows then put one piece in 16 distinct
+// (bank-half, slot) pairs, and any 8 in 8 distinct slots, so the fragment
+// reads of a row tile and the row stores are conflict-free.
+__device__ __forceinline__ int a_swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
 // Raw buffer resource over [base, base + bytes): loads take a 32-bit lane
 // offset plus a wave-uniform K-step offset, and read 0 past the end.
@@ -242,23 +246,22 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
     const int KB = K / 128;
     const int KBY = W4 ? K / 2 : K;
 
-    // ---- A staging: piece p = tid + j*512 -> 1 KB chunk c = p/64 (rows
-    // 32*(c % (BM/32)) .. +31 of K quarter kq = c / (BM/32)), position l = p%64
-    // (row 32*.. + l/2, half l&1 of its 32-byte slot, swapped per row) ----
+    // ---- A staging: a K step of the tile's rows is [row][128 B] in LDS with
+    // the 16-byte pieces of row r at slots p ^ a_swz(r). Piece q = tid + j*256
+    // of the step is piece q % 8 of row q / 8, so each load instruction reads
+    // 8 whole 128-byte rows (8 cache lines, every byte used) and each group
+    // of 8 lanes stores one row's 8 distinct slots ----
     const __amdgpu_buffer_rsrc_t ra = rsrc(g.a, g.a_rows * K);
     uint32_t a_off[A_PT];
     int a_dst[A_PT];
 #pragma unroll
     for (int j = 0; j < A_PT; ++j) {
-        const int p = tid + j * kThreads;
-        const int c = p >> 6, l = p & 63;
-        const int kq = c / (BM / 32);
-        const int row = (c % (BM / 32)) * 32 + (l >> 1);
-        const int h = (l & 1) ^ frag_swap(row);
+        const int q = tid + j * kThreads;
+        const int row = q >> 3, pc = q & 7;
         int arow = s_arow[row];
         if (arow < 0) arow = 0;                          // pad rows: any valid row, result unused
-        a_off[j] = (uint32_t)arow * (uint32_t)K + (uint32_t)(W4 ? kq * 16 + h * 64 : kq * 32 + h * 16);
-        a_dst[j] = c * 1024 + l * 16;
+        a_off[j] = (uint32_t)arow * (uint32_t)K + (uint32_t)(pc * 16);
+        a_dst[j] = row * 128 + ((pc ^ a_swz(row)) << 4);
     }
 
     // ---- B sources of this wave's four 16-row weight groups ----
@@ -321,7 +324,6 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
 #pragma unroll
         for (int ct = 0; ct < NCT; ++ct) acc[rt][ct] = v4f{0.f, 0.f, 0.f, 0.f};
     const int row_base = wm * (BM / kWM);
-    const int h0 = frag_swap(lr);
     // row tiles of this wave that hold a routed row (sorting pads each
     // expert's last block at its end): the MFMAs and FMAs of the others
     // are skipped, their accumulators stay 0 and their rows are not stored
@@ -341,10 +343,14 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
     auto compute = [&](const BS& bsv, int st, int stage, auto na) __attribute__((always_inline)) {
         constexpr int NA = decltype(na)::value;
         const uint8_t* sa_src = &s_a[stage][0];
+        // the lane's 32 K bytes of row tile rt: fp8 x fp8 pieces 2 lq, 2 lq + 1
+        // (K 32 lq ..); fp8 x fp4 pieces lq, lq + 4 (K 16 lq .. and 64 + 16 lq ..)
         auto afrag = [&](int rt) {
-            const uint8_t* slot = sa_src + lq * (BM * 32) + (row_base + rt * 16 + lr) * 32;
-            const v4i lo = *reinterpret_cast<const v4i*>(slot + h0 * 16);
-            const v4i hi = *reinterpret_cast<const v4i*>(slot + (h0 ^ 1) * 16);
+            const int row = row_base + rt * 16 + lr;
+            const uint8_t* rp = sa_src + row * 128;
+            const int p0 = W4 ? lq : 2 * lq, p1 = W4 ? lq + 4 : 2 * lq + 1;
+            const v4i lo = *reinterpret_cast<const v4i*>(rp + ((p0 ^ a_swz(row)) << 4));
+            const v4i hi = *reinterpret_cast<const v4i*>(rp + ((p1 ^ a_swz(row)) << 4));
             return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         };
         auto bfrag = [&](int ct) {
