@@ -223,6 +223,10 @@ void check_dims(int64_t model_dim, int64_t inter_dim) {
               "inter_dim must be a positive multiple of 128, got " + std::to_string(inter_dim));
 }
 
+// E: the range of the routed expert ids (the global expert count under an
+// expert mask). An expert-parallel share may hold fewer experts than topk
+// (e.g. 4 local experts with top-8 routing); the sorted-length bound
+// tokens*topk + E*block - topk needs topk <= E of the id range only.
 void check_topk_experts(int64_t tokens, int64_t topk, int64_t E) {
     AMD_CHECK(tokens >= 0 && tokens <= kMaxTokens,
               "tokens must be in [0, 2^24), got " + std::to_string(tokens));
@@ -230,8 +234,18 @@ void check_topk_experts(int64_t tokens, int64_t topk, int64_t E) {
               "topk must be in [1, 32], got " + std::to_string(topk));
     AMD_CHECK(E >= 1 && E <= kMaxExperts,
               "num_experts must be in [1, 4096], got " + std::to_string(E));
-    // the padded-length bound tokens*topk + E*block - topk assumes topk <= E
-    AMD_CHECK(topk <= E, "topk must not exceed num_experts");
+    AMD_CHECK(topk <= E, "topk must not exceed the number of experts the ids range over");
+}
+
+// The stage GEMMs index experts by sorted_expert_ids (local ids under a
+// mask) and do not bound topk by the expert count.
+void check_stage_dims(int64_t tokens, int64_t topk, int64_t E) {
+    AMD_CHECK(tokens >= 0 && tokens <= kMaxTokens,
+              "tokens must be in [0, 2^24), got " + std::to_string(tokens));
+    AMD_CHECK(topk >= 1 && topk <= kMaxTopk,
+              "topk must be in [1, 32], got " + std::to_string(topk));
+    AMD_CHECK(E >= 1 && E <= kMaxExperts,
+              "num_experts must be in [1, 4096], got " + std::to_string(E));
 }
 
 struct FusedLayout {
@@ -324,7 +338,7 @@ void stage1_entry(const void* a1, const float* a1_scale, int64_t a1_scale_transp
                   int64_t num_experts, int64_t topk, int64_t block_m, int64_t max_m_blocks,
                   int64_t activation, int64_t w_shuffled, void* stream) {
     check_dims(model_dim, inter_dim);
-    check_topk_experts(tokens, topk, num_experts);
+    check_stage_dims(tokens, topk, num_experts);
     check_block_m_gemm(block_m, model_dim, inter_dim, tokens, topk);
     AMD_CHECK(activation == kActSilu || activation == kActGelu,
               "only ActivationType.Silu (0) and Gelu (1) are supported, got " +
@@ -354,7 +368,7 @@ void stage2_entry(const void* a2, const float* a2_scale, const void* w2, WScale 
     check_dims(model_dim, inter_dim);
     AMD_CHECK(out_dtype == DT_FP32 || out_dtype == DT_BF16 || out_dtype == DT_FP16,
               "stage-2 output dtype must be fp32, bf16 or fp16");
-    check_topk_experts(tokens, topk, num_experts);
+    check_stage_dims(tokens, topk, num_experts);
     check_block_m_gemm(block_m, model_dim, inter_dim, tokens, topk);
     AMD_CHECK(max_m_blocks >= 0, "max_m_blocks must be >= 0");
     if (tokens == 0 || max_m_blocks == 0) return;
@@ -406,13 +420,14 @@ void fused_entry(const void* hidden_states, int hidden_dtype, const void* w1, WS
     AMD_CHECK(activation == kActSilu || activation == kActGelu,
               "only ActivationType.Silu (0) and Gelu (1) are supported, got " +
                   std::to_string(activation));
-    check_topk_experts(tokens, topk, num_experts);
+    check_stage_dims(tokens, topk, num_experts);
     AMD_CHECK(hidden_dtype == DT_BF16 || hidden_dtype == DT_FP16,
               "hidden_states dtype must be bf16 or fp16");
     AMD_CHECK(out_dtype == DT_BF16 || out_dtype == DT_FP16, "out dtype must be bf16 or fp16");
     const int64_t E_sort = expert_mask ? global_experts : num_experts;
     AMD_CHECK(E_sort >= num_experts && E_sort <= kMaxExperts,
               "global_experts must be in [num_experts, 4096]");
+    check_topk_experts(tokens, topk, E_sort);
     if (block_m <= 0) block_m = default_block_m(tokens, topk, num_experts, model_dim, inter_dim);
     check_block_m_gemm(block_m, model_dim, inter_dim, tokens, topk);
     AMD_CHECK(!one_launch || stream_fused_supported(block_m, model_dim, inter_dim),
@@ -776,10 +791,11 @@ int aiter_amd_fused_moe_fp8_blockscale_noalloc(
     return safe_call([&] {
         AMD_CHECK(w1_scale && w2_scale, "a required pointer is NULL");
         check_dims(model_dim, inter_dim);
-        check_topk_experts(tokens, topk, num_experts);
+        check_stage_dims(tokens, topk, num_experts);
         const int64_t E_sort = expert_mask ? global_experts : num_experts;
         AMD_CHECK(E_sort >= num_experts && E_sort <= kMaxExperts,
                   "global_experts must be in [num_experts, 4096]");
+        check_topk_experts(tokens, topk, E_sort);
         const int64_t bm =
             block_m > 0 ? block_m
                         : default_block_m(tokens, topk, num_experts, model_dim, inter_dim);

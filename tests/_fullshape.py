@@ -174,7 +174,8 @@ def stagewise_check(cfg, device, block_ms, log=print):
         assert far <= 0.05 and rms <= R.RMSTOL, (far, rms)
 
 
-def stagewise_vs_oracle(cfg, dev, ref, out, bm, activation, doweight=False, log=print):
+def stagewise_vs_oracle(cfg, dev, ref, out, bm, activation, doweight=False, log=print,
+                        e2e_rms=True):
     """The same split for a small layer, against the CPU oracle: stage 1's
     fp8 codes against the oracle's a2 (at most 0.5% different, each element
     within one top-binade e4m3 step of its group), the layer's output against the oracle's stage 2 applied to
@@ -183,14 +184,18 @@ def stagewise_vs_oracle(cfg, dev, ref, out, bm, activation, doweight=False, log=
     one-step requant flip (GELU(gate)·up makes such ties common), where the
     end-to-end max-rel bar would test the fp8 tie, not the kernel.
     dev / ref: the device tensors and the oracle's fused_moe_ref dict;
-    doweight: the layer ran with doweight_stage1."""
+    doweight: the layer ran with doweight_stage1; e2e_rms=False drops the
+    last check (RMS-rel against the whole oracle chain) for layers of a few
+    routed pairs, where one flipped code on a dominant element moves the RMS
+    of the whole output."""
     mx4 = cfg.weights == "mxfp4"
     stage1 = A.moe_stage1_a8w4 if mx4 else A.moe_stage1_fp8_blockscale
     T, I, k = cfg.tokens, cfg.inter_dim, cfg.topk
     a1, a1s = A.per_group_quant_hip(dev["x"])
     sid, sw, se, nv, _ = A.moe_sorting(dev["ids"], dev["tw"], cfg.experts, cfg.model_dim,
                                         torch.float32, bm, dev["mask"])
-    a2, a2s = stage1(a1, a1s, dev["w1"], dev["s1"], sid, se, nv, k, bm, True,
+    a2, a2s = stage1(a1, a1s, dev["w1"], dev["s1"], sid, se, nv, k, bm,
+                     bool(getattr(dev["w1"], "is_shuffled", False)),
                      sorted_weights=sw if doweight else None, activation=activation)
     loc = ref["ids_local"] >= 0
     codes = a2.view(torch.uint8).cpu().numpy()
@@ -201,7 +206,8 @@ def stagewise_vs_oracle(cfg, dev, ref, out, bm, activation, doweight=False, log=
     # each element within one top-binade e4m3 step of its group (32/448 of the
     # group amax, i.e. 32 x the oracle's scale), as in stagewise_check
     sc = np.repeat(ref["a2s"], 128, axis=-1)
-    err = (np.abs(a2d - ref_d) / (sc * 448))[loc]
+    with np.errstate(divide="ignore", over="ignore", invalid="ignore"):   # unrouted pairs
+        err = (np.abs(a2d - ref_d) / (sc * 448))[loc]
     differ = (codes != ref["a2q"])[loc].mean()
     log(f"[{cfg.name} bm={bm}] stage 1 codes differing {differ:.3%}, element err/amax "
         f"{err.max():.4f}")
@@ -215,4 +221,5 @@ def stagewise_vs_oracle(cfg, dev, ref, out, bm, activation, doweight=False, log=
     mx, rms = R.normalized_errors(own, out)
     log(f"[{cfg.name} bm={bm}] on the kernel's a2: max-rel {mx:.2e} rms-rel {rms:.2e}")
     assert mx <= R.MAXTOL and rms <= R.RMSTOL, (mx, rms)
-    assert R.normalized_errors(ref["out"], out)[1] <= R.RMSTOL
+    if e2e_rms:
+        assert R.normalized_errors(ref["out"], out)[1] <= R.RMSTOL

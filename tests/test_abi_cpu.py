@@ -109,6 +109,12 @@ def test_fused_validation_errors(lib):
     masked = [16, 3, 16, 16, 16, 16, 16, 16, 16, None, 16, 3]    # expert_mask given
     _expect_error("aiter_amd_fused_moe_fp8_blockscale", *masked, 4, 4096, 2048, 8, 4, 2, 0, 0, 0,
                   1, 16, 10**9, None, match="global_experts")
+    # an expert-parallel share may hold fewer experts than topk (4 local of 33
+    # with top-8): validation passes and stops only at the too-small workspace
+    _expect_error("aiter_amd_fused_moe_fp8_blockscale", *masked, 4, 4096, 2048, 4, 33, 8, 0, 0, 0,
+                  1, 16, 10, None, match="workspace of")
+    _expect_error("aiter_amd_fused_moe_fp8_blockscale", *masked, 4, 4096, 2048, 4, 6, 8, 0, 0, 0,
+                  1, 16, 10, None, match="topk must not exceed")
     # the one-launch entries take 16/32-row blocks and model_dim % 256 == 0 only
     for name in ("aiter_amd_fused_moe_1stage_fp8_blockscale", "aiter_amd_fused_moe_1stage_a8w4"):
         _expect_error(name, *base, 4, 4096, 2048, 8, 8, 2, 64, 0, 0, 1, 16, 10**9, None,

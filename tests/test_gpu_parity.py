@@ -299,6 +299,20 @@ def test_fused_moe_ep_share_small(cuda_device, bm):
     assert torch.count_nonzero(out[torch.from_numpy(none_local).to(cuda_device)]).item() == 0
 
 
+@pytest.mark.parametrize("bm", [16, 64])
+def test_fused_moe_ep_share_fewer_experts_than_topk(cuda_device, bm):
+    """An expert-parallel share holding fewer experts than topk (4 local
+    experts of 32, top-8 routing, as 8 GPUs would hold them): the layer runs
+    and matches the oracle; tokens with no local expert give zero rows."""
+    cfg = W.MoEConfig("ep_few", 64, 512, 512, 32, 8, routing="sigmoid", local_experts=4,
+                      seed=5)
+    dev, ref = _make_layer(cfg, cuda_device, True)
+    out = _run(dev, block_size_M=bm)
+    _check(ref["out"], _np(out.float()), f"EP 4 of 32 experts, top-8, bm={bm}")
+    none_local = (ref["ids_local"] < 0).all(axis=1)
+    assert torch.count_nonzero(out[torch.from_numpy(none_local).to(cuda_device)]).item() == 0
+
+
 @pytest.mark.parametrize("T,local,bm", [(80, 50, None), (80, 50, 64), (80, 50, 128),
                                          (600, 450, None), (600, 450, 16), (600, 290, 128)])
 def test_fused_moe_num_local_tokens(cuda_device, T, local, bm):
