@@ -98,3 +98,82 @@ def test_random_layer_vs_oracle(cuda_device, seed):
     if mask is not None:
         none_local = (ref["ids_local"] < 0).all(axis=1)
         assert np.count_nonzero(got[none_local]) == 0
+
+
+def _variant(seed):
+    rnd = random.Random(seed)
+    c = _case(seed)
+    c["E"] = rnd.choice([8, 16, 33, 64])
+    c["k"] = rnd.randint(1, min(16, c["E"]))
+    c["T"] = rnd.choice([2, 40, 257, 600])
+    c["local"] = rnd.choice([None, max(1, c["E"] // 4)])
+    c["doweight"] = rnd.random() < 0.4
+    c["gelu"] = rnd.random() < 0.4
+    c["fp16"] = rnd.random() < 0.3
+    c["num_local"] = rnd.choice([None, None, max(1, (3 * c["T"]) // 4)])
+    return c
+
+
+VARIANTS = list(range(2000, 2016))
+
+
+@pytest.mark.parametrize("seed", VARIANTS)
+def test_random_layer_variants_vs_oracle(cuda_device, seed):
+    """As above with doweight_stage1, Gelu, fp16 in/out, num_local_tokens
+    (outputs past the local rows are not compared), topk up to 16, up to 64
+    experts and token counts of several sorting chunks."""
+    c = _variant(seed)
+    print(f"[random variant {seed}] {c}", flush=True)
+    cfg = W.MoEConfig(f"randv{seed}", c["T"], c["H"], c["I"], c["E"], c["k"],
+                      routing=c["routing"], local_experts=c["local"], seed=seed,
+                      weights=c["weights"])
+    act = "gelu" if c["gelu"] else "silu"
+    wts = W.make_weights(cfg, device="cpu", shuffle=False)
+    x = W.make_hidden(cfg)
+    tw, ids = W.make_routing(cfg)
+    mask = W.make_expert_mask(cfg)
+    mx4 = c["weights"] == "mxfp4"
+    ref = R.fused_moe_ref(x.float().numpy(), wts["w1"].view(torch.uint8).numpy(),
+                          wts["w1_scale"].numpy(), wts["w2"].view(torch.uint8).numpy(),
+                          wts["w2_scale"].numpy(), ids.numpy(), tw.numpy(),
+                          None if mask is None else mask.numpy(),
+                          doweight_stage1=c["doweight"], activation=act,
+                          num_local_tokens=c["num_local"],
+                          **({"weight_format": "mxfp4"} if mx4 else {}))
+    w1, w2 = wts["w1"], wts["w2"]
+    if c["shuffle"]:
+        w1, w2 = A.shuffle_weight(w1), A.shuffle_weight(w2)
+    w1, w2 = w1.to(cuda_device), w2.to(cuda_device)
+    if c["shuffle"]:
+        w1.is_shuffled = True
+        w2.is_shuffled = True
+    xd = x.to(cuda_device)
+    if c["fp16"]:
+        xd = xd.to(torch.float16)        # N(0,1) bf16 values are exact in fp16
+    dev = dict(x=xd, w1=w1, w2=w2, s1=wts["w1_scale"].to(cuda_device),
+               s2=wts["w2_scale"].to(cuda_device), tw=tw.to(cuda_device), ids=ids.to(cuda_device),
+               mask=None if mask is None else mask.to(cuda_device))
+    nl = None
+    if c["num_local"] is not None:
+        nl = torch.tensor([c["num_local"]], dtype=torch.int32, device=cuda_device)
+    out = W.run_layer(c["weights"], dev["x"], w1, w2, dev["tw"], dev["ids"],
+                      expert_mask=dev["mask"], w1_scale=dev["s1"], w2_scale=dev["s2"],
+                      block_size_M=c["bm"], doweight_stage1=c["doweight"],
+                      activation=A.ActivationType.Gelu if c["gelu"] else A.ActivationType.Silu,
+                      num_local_tokens=nl)
+    assert out.dtype == (torch.float16 if c["fp16"] else torch.bfloat16)
+    rows = c["num_local"] if c["num_local"] is not None else c["T"]
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got[:rows]).all()
+    mx, rms = R.normalized_errors(ref["out"][:rows], got[:rows])
+    print(f"[random variant {seed}] max-rel {mx:.3e} rms-rel {rms:.3e}", flush=True)
+    if not (mx <= R.MAXTOL and rms <= R.RMSTOL):
+        got[rows:] = 0
+        ref["ids_local"][rows:] = -1
+        bm = c["bm"] or A.select_block_m(c["T"], c["k"], cfg.local_experts or c["E"], c["H"],
+                                         c["I"], mx4, cuda_device)
+        pairs = int((ref["ids_local"] >= 0).sum())
+        _fullshape.stagewise_vs_oracle(
+            cfg, dev, ref, got, bm,
+            A.ActivationType.Gelu if c["gelu"] else A.ActivationType.Silu,
+            doweight=c["doweight"], log=lambda m: print(m, flush=True), e2e_rms=pairs >= 32)
