@@ -182,4 +182,39 @@ constexpr int kActGelu = 1;
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// XCD-aware order of a 1-D grid of (M-tile, column group) workgroups.
+// Workgroup L runs on XCD L % 8. With ng % 8 == 0 the 8 XCDs form ms groups
+// along M x 8/ms along N: XCD x takes column groups [(x % (8/ms)) * per, +per)
+// (per = ng / (8/ms)) of the valid M-tiles [(x / (8/ms)) * chunk, +chunk),
+// M-major; with rot its walk starts (x % (8/ms)) / (8/ms) of the way into
+// the range. m_slots is the grid's M-tiles per group (ceil(m_tiles / ms)),
+// mv the valid M-tiles. Returns false for a workgroup with no tile.
+__device__ __forceinline__ bool xcd_tile(int L, int ng, int m_slots, int mv, int ms, int rot,
+                                         int& nt, int& mt) {
+    if ((ng & 7) != 0) {
+        nt = L % ng;
+        mt = L / ng;
+        return true;
+    }
+    const int nsplit = 8 / ms;
+    const int per = ng / nsplit;
+    const int idx = L >> 3;
+    const int x = L & 7;
+    const int chunk = (ms == 1 && !rot) ? m_slots : (mv + ms - 1) / ms;
+    int ml = idx / per;
+    if (ml >= chunk) return false;
+    if (rot) {
+        ml += ((x % nsplit) * chunk) / nsplit;
+        if (ml >= chunk) ml -= chunk;
+    }
+    nt = (x % nsplit) * per + idx % per;
+    mt = (x / nsplit) * chunk + ml;
+    return true;
+}
+
+// Grid size of xcd_tile's order: every group gets ceil(m_tiles / ms) M-tiles' slots.
+inline int64_t xcd_grid(int ng, int64_t m_tiles, int ms) {
+    return (ng & 7) != 0 ? (int64_t)ng * m_tiles : (int64_t)ng * ceil_div(m_tiles, ms) * ms;
+}
+
 }  // namespace aiter_amd

@@ -30,9 +30,11 @@
 //   each [kq 4][row 16][32 B] (the (16,16) shuffled 2 KB block with the two
 //   16-byte halves of a row brought together).  The DMA lane -> global
 //   address map does the reordering.
-// Tile order: the grid is 1-D; workgroup L runs on XCD L % 8 and each XCD
-// owns n_tiles/8 column tiles for every M-block, so the weight slice of an
-// expert stays in that XCD's L2 across the expert's consecutive M-blocks.
+// Tile order (xcd_tile): the grid is 1-D; workgroup L runs on XCD L % 8;
+// the XCDs form two groups along M (half the valid M-blocks each) x 4
+// along N, so the weight slice of an expert stays in one XCD's L2 across
+// the expert's consecutive M-blocks and each block's A rows are gathered by
+// 4 XCDs, not 8.
 //
 // A8W4 (W4 = true): MXFP4 weights (packed e2m1 [E, N, K/2], e8m0 scales
 // [E, N, K/32]).  A 16-row group's K step is 1 KB, kept lane-linear in LDS
@@ -79,8 +81,10 @@ struct Args {
     int topk;
     int E;
     int64_t a_rows;
-    int n_tiles;     // column tiles (grid = n_tiles * m_blocks)
+    int n_tiles;     // column tiles
     int m_blocks;
+    int msplit;      // XCD groups along M (xcd_tile)
+    int mrot;        // stagger the M walk of the XCDs in a group
 };
 
 // Buffer resource (base, byte size) for the LDS-DMA loads: word1 carries
@@ -181,19 +185,12 @@ __global__ __launch_bounds__(kThreads, 1) void moe_gemm_fp8bs_v2_kernel(Args g) 
 
     // ---- XCD-aware tile order ----
     const int L = blockIdx.x;
-    int nt, mb;
-    if ((g.n_tiles & 7) == 0) {
-        const int per = g.n_tiles >> 3;
-        const int xcd = L & 7;
-        const int idx = L >> 3;
-        nt = xcd * per + idx % per;
-        mb = idx / per;
-    } else {
-        nt = L % g.n_tiles;
-        mb = L / g.n_tiles;
-    }
-    if (mb >= g.m_blocks) return;
     const int nvalid = g.num_valid[0];
+    int nt, mb;
+    if (!xcd_tile(L, g.n_tiles, (g.m_blocks + g.msplit - 1) / g.msplit, (nvalid + BM - 1) / BM,
+                  g.msplit, g.mrot, nt, mb))
+        return;
+    if (mb >= g.m_blocks) return;
     if (mb * BM >= nvalid) return;
     const int tokens = g.num_valid[1];
     const int e = g.sorted_eids[mb];
@@ -544,6 +541,31 @@ static int64_t scale_bytes(int64_t rows, int64_t KB, int64_t sa_row, int64_t sa_
 
 }  // namespace v2
 
+namespace v2 {
+
+// XCD groups along M and the staggered walk (xcd_tile): two groups for both
+// stages, stage 1 staggered. Measured on MI355X at MiMo dims (A8W4) against
+// one unstaggered group: T=8192 stage 1 1765 -> 1714 us, stage 2 unchanged
+// (1144 us; staggered 1195); T=1024 stage 1 519 -> 502 us, stage 2 270 ->
+// 258 us (staggered 296). AITER_AMD_V2_MSPLIT1 / _2 (1, 2, 4 or 8) and
+// AITER_AMD_V2_MROT1 / _2 force them.
+static int pick_msplit(int stage, int ng) {
+    if (ng % 8 != 0) return 1;
+    if (const char* env = getenv(stage == 1 ? "AITER_AMD_V2_MSPLIT1" : "AITER_AMD_V2_MSPLIT2")) {
+        const int c = atoi(env);
+        if (c == 1 || c == 2 || c == 4 || c == 8) return c;
+    }
+    return 2;
+}
+
+static int pick_mrot(int stage) {
+    if (const char* env = getenv(stage == 1 ? "AITER_AMD_V2_MROT1" : "AITER_AMD_V2_MROT2"))
+        return atoi(env) != 0;
+    return stage == 1;
+}
+
+}  // namespace v2
+
 bool v2_supported(int64_t block_m, int64_t K) {
     return (block_m == 64 || block_m == 128) && K > 0 && K % 128 == 0 && K / 128 <= 64;
 }
@@ -582,7 +604,9 @@ void launch_moe_stage1_fp8bs_v2(const uint8_t* a, const float* a_scale, int64_t 
     AMD_CHECK(a_rows * K < (1ll << 32) && 2 * inter * K < (1ll << 32) &&
                   g.sa_bytes < (1ll << 32),
               "v2 GEMM needs 32-bit buffer offsets");
-    const int64_t grid = (int64_t)g.n_tiles * max_m_blocks;
+    g.msplit = v2::pick_msplit(1, g.n_tiles);
+    g.mrot = v2::pick_mrot(1);
+    const int64_t grid = xcd_grid(g.n_tiles, max_m_blocks, g.msplit);
     if (grid == 0) return;
     v2::launch<1>((int)block_m, (int)grid, g, shuffled, w1_scale_e8m0 != nullptr, stream);
     AMD_HIP_CHECK(hipGetLastError());
@@ -622,7 +646,9 @@ void launch_moe_stage2_fp8bs_v2(const uint8_t* a2, const float* a2_scale, const 
     AMD_CHECK(a_rows * inter < (1ll << 32) && hidden * inter < (1ll << 32) &&
                   g.sa_bytes < (1ll << 32),
               "v2 GEMM needs 32-bit buffer offsets");
-    const int64_t grid = (int64_t)g.n_tiles * max_m_blocks;
+    g.msplit = v2::pick_msplit(2, g.n_tiles);
+    g.mrot = v2::pick_mrot(2);
+    const int64_t grid = xcd_grid(g.n_tiles, max_m_blocks, g.msplit);
     if (grid == 0) return;
     v2::launch<2>((int)block_m, (int)grid, g, shuffled, w2_scale_e8m0 != nullptr, stream);
     AMD_HIP_CHECK(hipGetLastError());

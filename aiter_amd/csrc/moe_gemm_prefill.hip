@@ -27,8 +27,10 @@
 // weight rows (128 gate + the matching 128 up rows = one 1x128 quant group
 // per row); stage 2: 128 (or 64) rows x 128 output columns.  A tile whose
 // rows are all padding exits at once.  Tile order is XCD-aware: workgroup L
-// runs on XCD L % 8, and each XCD owns n_tiles/8 column tiles of every
-// M-block so an expert's weight slice stays in its L2.  A workgroup may walk
+// runs on XCD L % 8; the XCDs form msplit groups along M (a contiguous range
+// of the valid M-tiles each) x 8/msplit along N (each XCD owns that many
+// column tiles of its range), so an expert's weight slice stays in one L2
+// and each M-tile's A rows are gathered by 8/msplit XCDs.  A workgroup may walk
 // ntw consecutive column tiles of its M-block in one pipelined K loop (setup
 // paid once; the next tile's first loads are in flight during a tile's
 // epilogue).
@@ -72,6 +74,8 @@ struct Args {
     int m_tiles;               // sorted M-blocks x workgroups per M-block
     int block_m;               // rows per sorted M-block (BM or 2 BM)
     int ntw;                   // column tiles per workgroup, walked in one pipelined K loop
+    int msplit;                // XCD groups along M (1, 2, 4 or 8; see the tile order)
+    int mrot;                  // stagger the M walk of the XCDs in a group
 };
 
 // Slot of a row's 16-byte A piece in LDS: piece p of row r sits at slot
@@ -197,21 +201,15 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
     const int L = blockIdx.x;
     const int ntw = g.ntw;
     const int ng = g.n_tiles / ntw;
+    const int nvalid = g.num_valid[0];
     int nt, mt;
-    if ((ng & 7) == 0) {
-        const int per = ng >> 3;
-        const int idx = L >> 3;
-        nt = (L & 7) * per + idx % per;
-        mt = idx / per;
-    } else {
-        nt = L % ng;
-        mt = L / ng;
-    }
+    if (!xcd_tile(L, ng, (g.m_tiles + g.msplit - 1) / g.msplit, (nvalid + BM - 1) / BM, g.msplit,
+                  g.mrot, nt, mt))
+        return;
     if (mt >= g.m_tiles) return;
     const int subs = g.block_m / BM;                     // workgroups per sorted M-block
     const int mb = mt / subs;
     const int srow0 = mb * g.block_m + (mt % subs) * BM; // first sorted row of the tile
-    const int nvalid = g.num_valid[0];
     if (srow0 >= nvalid) return;
     const int tokens = g.num_valid[1];
     const int e = g.sorted_eids[mb];
@@ -746,6 +744,34 @@ static void launch(int bm, int KB, int grid, const Args& a, int shuffled, hipStr
 // expected on this GPU fill at least kMinRounds rounds of workgroups after
 // halving, stage 1 none. AITER_AMD_PF_NTW1 / AITER_AMD_PF_NTW2 force a count
 // (tests use them; any divisor of n_tiles with ntw * KB <= kMaxKB).
+// XCD groups along M. Both stages split the 8 XCDs into 2 groups along M x
+// 4 along N, and stage 1 also staggers the walk of the 4 XCDs of a group
+// (each starts a quarter of the group's M-tiles further on), so the XCDs
+// gather different A rows and stream different experts' weights at any one
+// time. Measured on MI355X at MiMo dims against one group (every XCD walks
+// every M-tile in the same order): stage 1 T=8192 1720 -> 1603 us, T=2048
+// 597 -> 581 us, EP share T=4096 (32 of 256 experts) 174 -> 160 us; stage 2
+// 935 -> 939, 365 -> 362, 102 -> 98 us (staggering stage 2 made T=8192
+// 969 us). Four groups: stage 1 1664 / 612 / 164 us. HBM fetch rises with
+// the groups (stage 1 T=8192 6.5 -> 6.8 GB at two): an expert's weight slice
+// on one XCD is then 4 column tiles (4 MB, the size of its L2), not 2.
+// AITER_AMD_PF_MSPLIT1 / _2 force 1, 2, 4 or 8 groups and
+// AITER_AMD_PF_MROT1 / _2 the stagger (tests use them).
+static int pick_msplit(int stage, int ng) {
+    if (ng % 8 != 0) return 1;
+    if (const char* env = getenv(stage == 1 ? "AITER_AMD_PF_MSPLIT1" : "AITER_AMD_PF_MSPLIT2")) {
+        const int c = atoi(env);
+        if (c == 1 || c == 2 || c == 4 || c == 8) return c;
+    }
+    return 2;
+}
+
+static int pick_mrot(int stage) {
+    if (const char* env = getenv(stage == 1 ? "AITER_AMD_PF_MROT1" : "AITER_AMD_PF_MROT2"))
+        return atoi(env) != 0;
+    return stage == 1;
+}
+
 static int pick_ntw(int stage, int n_tiles, int KB, int64_t pairs, int rows) {
     if (const char* env = getenv(stage == 1 ? "AITER_AMD_PF_NTW1" : "AITER_AMD_PF_NTW2")) {
         const int c = atoi(env);
@@ -799,7 +825,9 @@ void launch_moe_stage1_prefill(const uint8_t* a, const float* a_scale, int64_t s
     g.block_m = (int)block_m;
     g.m_tiles = (int)(max_m_blocks * (block_m / pf::wg_rows<1>((int)block_m)));
     g.ntw = pf::pick_ntw(1, g.n_tiles, (int)(K / 128), a_rows * topk, 64);
-    const int64_t grid = (int64_t)(g.n_tiles / g.ntw) * g.m_tiles;
+    g.msplit = pf::pick_msplit(1, g.n_tiles / g.ntw);
+    g.mrot = pf::pick_mrot(1);
+    const int64_t grid = xcd_grid(g.n_tiles / g.ntw, g.m_tiles, g.msplit);
     if (grid == 0) return;
     pf::launch<1>((int)block_m, (int)(K / 128), (int)grid, g, shuffled, stream);
     AMD_HIP_CHECK(hipGetLastError());
@@ -837,7 +865,9 @@ void launch_moe_stage2_prefill(const uint8_t* a2, const float* a2_scale, const u
     g.block_m = (int)block_m;
     g.m_tiles = (int)(max_m_blocks * (block_m / pf::wg_rows<2>((int)block_m)));
     g.ntw = pf::pick_ntw(2, g.n_tiles, (int)(inter / 128), est_pairs, (int)block_m);
-    const int64_t grid = (int64_t)(g.n_tiles / g.ntw) * g.m_tiles;
+    g.msplit = pf::pick_msplit(2, g.n_tiles / g.ntw);
+    g.mrot = pf::pick_mrot(2);
+    const int64_t grid = xcd_grid(g.n_tiles / g.ntw, g.m_tiles, g.msplit);
     if (grid == 0) return;
     pf::launch<2>((int)block_m, (int)(inter / 128), (int)grid, g, shuffled, stream);
     AMD_HIP_CHECK(hipGetLastError());

@@ -443,6 +443,55 @@ def test_prefill_column_walk_bit_exact(cuda_device, monkeypatch, weights, bm, nt
     assert torch.count_nonzero(out1).item() > 0
 
 
+@pytest.mark.parametrize("weights,bm", [("fp8", 64), ("fp8", 128), ("mxfp4", 64),
+                                       ("mxfp4", 128)])
+@pytest.mark.parametrize("order", [(2, 1, 2, 0, 1), (4, 0, 4, 1, 2), (8, 1, 1, 1, 1),
+                                   (1, 1, 8, 0, 2)])
+def test_prefill_xcd_order_bit_exact(cuda_device, monkeypatch, weights, bm, order):
+    """The prefill and MXFP4 (v2) kernels' tile order (XCD groups along M,
+    staggered walks; AITER_AMD_PF_MSPLIT1/2, AITER_AMD_PF_MROT1/2 and the
+    AITER_AMD_V2_ ones force them) only moves tiles between XCDs and in
+    time: stage 1's a2 and the layer output are bitwise equal to the plain
+    order's (one group, no stagger). order = (groups 1, stagger 1, groups 2,
+    stagger 2, stage-2 column walk); the walk of 2 leaves the prefill stage 2
+    with 8 column groups instead of 16. The v2 stage 2 (MXFP4 at 64 rows)
+    accumulates with fp32 atomics, whose order differs between runs at top-4,
+    so there the two outputs are compared at the layer bar instead (the plain
+    order itself is checked against the oracle by the A8W4 layer tests)."""
+    cfg = W.MoEConfig("xcd", 300, 2048, 1024, 16, 4, seed=23, weights=weights)
+    wts = W.make_weights(cfg, device=cuda_device, shuffle=True)
+    x = W.make_hidden(cfg, device=cuda_device)
+    tw, ids = W.make_routing(cfg, device=cuda_device)
+
+    def layer(m1, r1, m2, r2, ntw2):
+        for k, v in (("MSPLIT1", m1), ("MROT1", r1), ("MSPLIT2", m2), ("MROT2", r2)):
+            monkeypatch.setenv("AITER_AMD_PF_" + k, str(v))
+            monkeypatch.setenv("AITER_AMD_V2_" + k, str(v))
+        monkeypatch.setenv("AITER_AMD_PF_NTW2", str(ntw2))
+        out = W.run_layer(weights, x, wts["w1"], wts["w2"], tw, ids, w1_scale=wts["w1_scale"],
+                          w2_scale=wts["w2_scale"], block_size_M=bm)
+        a2 = None
+        if weights == "fp8":
+            a1, a1s = A.per_group_quant_hip(x)
+            sid, sw, se, nv, _ = A.moe_sorting(ids, tw, cfg.experts, cfg.model_dim,
+                                                torch.bfloat16, bm)
+            a2, a2s = A.moe_stage1_fp8_blockscale(a1, a1s, wts["w1"], wts["w1_scale"], sid, se,
+                                                  nv, cfg.topk, bm, True)
+            a2 = (a2.view(torch.uint8).clone(), a2s.clone())
+        torch.cuda.synchronize()
+        return out, a2
+
+    out1, a21 = layer(1, 0, 1, 0, order[4])
+    outc, a2c = layer(*order)
+    if a21 is not None:
+        assert torch.equal(a21[0], a2c[0]) and torch.equal(a21[1], a2c[1])
+    assert torch.count_nonzero(out1).item() > 0
+    if weights == "mxfp4" and bm == 64:
+        _check(_np(out1.float()), _np(outc.float()), f"xcd order {order} vs plain")
+    else:
+        assert torch.equal(out1, outc), (out1.float() - outc.float()).abs().max().item()
+
+
 @pytest.mark.parametrize("weights", ["fp8", "mxfp4"])
 @pytest.mark.parametrize("bm", [16, 32])
 @pytest.mark.parametrize("ntw", [2, 4])
