@@ -23,7 +23,11 @@
 // cut into chunks of `ct` tokens.  Each chunk builds an LDS bitmap
 // table[token][expert] of slot masks (a byte per cell for topk <= 8, a u32
 // up to topk 32, so duplicates of an expert inside one token's top-k are all
-// kept, in slot order) and stages its routing weights in LDS.  Small batches
+// kept, in slot order); a thread per expert then counts the expert's pairs
+// in each group of 8 rows (1 for u32 cells) into an LDS prefix, and a thread
+// per pair writes the pair at its segment's start + the expert's pairs in
+// earlier chunks + in earlier row groups + in earlier bits of its own group
+// (no thread walks an expert's pairs one store after another).  Small batches
 // (one chunk) run the whole sort in one block of one launch; the other
 // blocks of that launch clear the accumulator.  Larger batches take two
 // launches: per-chunk expert counts (plus the clearing), then one block per
@@ -118,26 +122,22 @@ __device__ __forceinline__ int chunk_rows(const SortParams& p, int c, int tokens
 }
 
 // Fill table[rows][E] with slot bitmasks of chunk c (only the chunk's rows
-// are cleared and used) and, when s_wt is given, stage the chunk's routing
-// weights there as [row][slot].  Each thread's ids and weights are loaded
+// are cleared and used).  Each thread's ids and weights are loaded
 // kPairBatch at a time before any of them is used, so one batch costs one
 // memory round trip (the first batch is in flight while the table clears).
 constexpr int kPairBatch = 4;
 
-__device__ void build_table(const SortParams& p, uint32_t* table, int c, int tokens,
-                            float* s_wt) {
+__device__ void build_table(const SortParams& p, uint32_t* table, int c, int tokens) {
     const int nrows = chunk_rows(p, c, tokens);
     const int nwords = (nrows * p.E * p.cell_bytes + 3) / 4;
     const int npairs = nrows * p.topk;
     const int64_t base = (int64_t)c * p.ct * p.topk;
     for (int i0 = 0; i0 < npairs; i0 += kPairBatch * kSortThreads) {
         int ev[kPairBatch];
-        float wv[kPairBatch];
 #pragma unroll
         for (int u = 0; u < kPairBatch; ++u) {
             const int i = i0 + u * kSortThreads + (int)threadIdx.x;
             ev[u] = i < npairs ? p.topk_ids[base + i] : -1;
-            wv[u] = (s_wt && i < npairs) ? p.topk_w[base + i] : 0.0f;
         }
         if (i0 == 0) {   // block-uniform: every thread takes the first batch
             for (int i = threadIdx.x; i < nwords; i += kSortThreads) table[i] = 0u;
@@ -147,7 +147,6 @@ __device__ void build_table(const SortParams& p, uint32_t* table, int c, int tok
         for (int u = 0; u < kPairBatch; ++u) {
             const int i = i0 + u * kSortThreads + (int)threadIdx.x;
             if (i >= npairs) continue;
-            if (s_wt) s_wt[i] = wv[u];
             const int e = ev[u];
             if (e >= 0 && e < p.E) {
                 const int tl = i / p.topk;
@@ -263,95 +262,115 @@ __device__ void write_segments(const SortParams& p, const int* s_total, const in
     }
 }
 
-// Emit the pairs of chunk c for every enabled expert, starting at s_pos[e];
-// the routing weights come from the chunk's LDS copy s_wt.  With byte cells
-// (topk <= 8) a thread reads kCellBatch rows' cells at once and walks the
-// set bits of the packed 64-bit word: bit 8u + j is slot j of row u, so
-// ascending bits are ascending (token, slot).
-constexpr int kCellBatch = 8;
+// Rows per prefix group of the chunk table: 8 byte cells form one 64-bit
+// word (bit 8u + j is slot j of row u, so ascending bits are ascending
+// (token, slot)); u32 cells are one row each.
+__device__ __forceinline__ int prefix_rows(const SortParams& p) { return p.cell_bytes == 1 ? 8 : 1; }
 
-__device__ void scatter_chunk(const SortParams& p, const uint32_t* table, int c, int tokens,
-                              const int* s_pos, const int* s_mask, const float* s_wt) {
+// The slot masks of expert e in the 8 rows from tl0 (byte cells).
+__device__ __forceinline__ uint64_t cells8(const SortParams& p, const uint8_t* cells, int tl0,
+                                           int nrows, int e) {
+    // the 8 rows' cells as two little-endian dwords (rows past nrows read 0)
+    uint32_t lo = 0, hi = 0;
+    const uint8_t* src = cells + tl0 * p.E + e;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        if (tl0 + u < nrows) lo |= (uint32_t)src[u * p.E] << (8 * u);
+        if (tl0 + 4 + u < nrows) hi |= (uint32_t)src[(4 + u) * p.E] << (8 * u);
+    }
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// Per expert (a thread each), the pairs of the chunk's row groups before
+// each group: s_pre[group][e]; the chunk's total goes to s_tot when given.
+__device__ void chunk_prefix(const SortParams& p, const uint32_t* table, int nrows,
+                             uint16_t* s_pre, int* s_tot) {
     const int E = p.E;
-    const int t0 = c * p.ct;
-    const int nrows = chunk_rows(p, c, tokens);
     const uint8_t* cells = reinterpret_cast<const uint8_t*>(table);
     for (int e = threadIdx.x; e < E; e += kSortThreads) {
-        if (s_mask[e] == 0) continue;
-        int pos = s_pos[e];
+        int run = 0;
         if (p.cell_bytes == 1) {
-            for (int tl0 = 0; tl0 < nrows; tl0 += kCellBatch) {
-                uint64_t mm = 0;
-#pragma unroll
-                for (int u = 0; u < kCellBatch; ++u)
-                    if (tl0 + u < nrows) mm |= (uint64_t)cells[(tl0 + u) * E + e] << (8 * u);
-                while (mm) {
-                    const int b = __ffsll((unsigned long long)mm) - 1;
-                    mm &= mm - 1u;
-                    const int tl = tl0 + (b >> 3);
-                    const int j = b & 7;
-                    p.sorted_ids[pos] = (int32_t)(((uint32_t)j << 24) | (uint32_t)(t0 + tl));
-                    p.sorted_w[pos] = s_wt[tl * p.topk + j];
-                    ++pos;
-                }
+            for (int tl0 = 0, g = 0; tl0 < nrows; tl0 += 8, ++g) {
+                s_pre[g * E + e] = (uint16_t)run;
+                run += __popcll((unsigned long long)cells8(p, cells, tl0, nrows, e));
             }
         } else {
             for (int tl = 0; tl < nrows; ++tl) {
-                uint32_t m = table[tl * E + e];
-                while (m) {
-                    const int j = __ffs(m) - 1;
-                    m &= m - 1u;
-                    p.sorted_ids[pos] = (int32_t)(((uint32_t)j << 24) | (uint32_t)(t0 + tl));
-                    p.sorted_w[pos] = s_wt[tl * p.topk + j];
-                    ++pos;
-                }
+                s_pre[tl * E + e] = (uint16_t)run;
+                run += __popc(table[tl * E + e]);
             }
         }
+        if (s_tot) s_tot[e] = run;
     }
 }
 
-// Pairs of expert e in the chunk's table (popcount of its slot masks).
-__device__ __forceinline__ int table_count(const SortParams& p, const uint32_t* table, int nrows,
-                                           int e) {
-    int cnt = 0;
-    if (p.cell_bytes == 1) {
-        const uint8_t* cells = reinterpret_cast<const uint8_t*>(table);
-        for (int tl0 = 0; tl0 < nrows; tl0 += kCellBatch) {
-            uint64_t mm = 0;
-#pragma unroll
-            for (int u = 0; u < kCellBatch; ++u)
-                if (tl0 + u < nrows) mm |= (uint64_t)cells[(tl0 + u) * p.E + e] << (8 * u);
-            cnt += __popcll((unsigned long long)mm);
+// Emit the pairs of chunk c, a thread per pair: the pair's place in its
+// expert's segment is s_pos[e] (the segment start plus the pairs of earlier
+// chunks) + the expert's pairs in earlier row groups of the chunk (s_pre) +
+// those before it in its own group; experts switched off by the mask are
+// skipped. Ids and routing weights are read again from global memory (the
+// table's build just brought them into L2), coalesced.
+__device__ void scatter_pairs(const SortParams& p, const uint32_t* table, int c, int tokens,
+                              const int* s_pos, const int* s_mask, const uint16_t* s_pre) {
+    const int E = p.E;
+    const int t0 = c * p.ct;
+    const int nrows = chunk_rows(p, c, tokens);
+    const int npairs = nrows * p.topk;
+    const int32_t* ids = p.topk_ids + (int64_t)t0 * p.topk;
+    const float* wts = p.topk_w + (int64_t)t0 * p.topk;
+    const uint8_t* cells = reinterpret_cast<const uint8_t*>(table);
+    // i / topk by a float reciprocal: i < 2^13 and topk <= 32, so (i + 1/2) / topk
+    // is at least 1/64 from an integer and the product rounds to the right side
+    const float rtk = 1.0f / (float)p.topk;
+    for (int i = threadIdx.x; i < npairs; i += kSortThreads) {
+        const int e = ids[i];
+        if (e < 0 || e >= E || s_mask[e] == 0) continue;
+        const int tl = (int)(((float)i + 0.5f) * rtk);
+        const int j = i - tl * p.topk;
+        int rank;
+        if (p.cell_bytes == 1) {
+            const int tl0 = tl & ~7;
+            const uint64_t mm = cells8(p, cells, tl0, nrows, e);
+            rank = s_pre[(tl0 >> 3) * E + e] +
+                   __popcll((unsigned long long)(mm & ((1ull << (8 * (tl - tl0) + j)) - 1ull)));
+        } else {
+            rank = s_pre[tl * E + e] + __popc(table[tl * E + e] & ((1u << j) - 1u));
         }
-    } else {
-        for (int tl = 0; tl < nrows; ++tl) cnt += __popc(table[tl * p.E + e]);
+        const int pos = s_pos[e] + rank;
+        p.sorted_ids[pos] = (int32_t)(((uint32_t)j << 24) | (uint32_t)(t0 + tl));
+        p.sorted_w[pos] = wts[i];
     }
-    return cnt;
 }
 
-// LDS layout of the sorting kernels: table[ct*E] | s_wt[ct*topk] | s_total[E] |
-// s_start[E] | s_local[E] | s_pos[E] | s_mask[E] | scratch[kSortThreads/64]
+// LDS layout of the sorting kernels: table[ct*E] | s_total[E] | s_start[E] |
+// s_local[E] | s_pos[E] | s_mask[E] | scratch[kSortThreads/64] |
+// s_pre[ceil(ct/prefix_rows)*E] u16
 struct SortLds {
     uint32_t* table;
-    float* s_wt;
     int* s_total;
     int* s_start;
     int* s_local;
     int* s_pos;
     int* s_mask;
     int* scratch;
+    uint16_t* s_pre;
 };
+
+__host__ __device__ inline int prefix_groups(int ct, int cell_bytes) {
+    const int g = cell_bytes == 1 ? 8 : 1;
+    return (ct + g - 1) / g;
+}
 
 __device__ SortLds carve_lds(const SortParams& p, uint32_t* smem) {
     SortLds L;
     L.table = smem;
-    L.s_wt = reinterpret_cast<float*>(smem + table_words(p.ct, p.E, p.cell_bytes));
-    L.s_total = reinterpret_cast<int*>(L.s_wt + p.ct * p.topk);
+    L.s_total = reinterpret_cast<int*>(smem + table_words(p.ct, p.E, p.cell_bytes));
     L.s_start = L.s_total + p.E;
     L.s_local = L.s_start + p.E;
     L.s_pos = L.s_local + p.E;
     L.s_mask = L.s_pos + p.E;
     L.scratch = L.s_mask + p.E;
+    L.s_pre = reinterpret_cast<uint16_t*>(L.scratch + kSortThreads / 64);
     return L;
 }
 
@@ -371,16 +390,14 @@ __global__ __launch_bounds__(kSortThreads) void moe_sort_oneshot_kernel(SortPara
         return;
     }
     const SortLds L = carve_lds(p, smem);
-    build_table(p, L.table, 0, tokens, L.s_wt);
-    const int nrows = chunk_rows(p, 0, tokens);
-    for (int e = threadIdx.x; e < p.E; e += kSortThreads) {
-        L.s_mask[e] = p.expert_mask ? p.expert_mask[e] : 1;
-        L.s_total[e] = table_count(p, L.table, nrows, e);
-    }
+    for (int e = threadIdx.x; e < p.E; e += kSortThreads)
+        L.s_mask[e] = p.expert_mask ? p.expert_mask[e] : 1;   // published by the table's barriers
+    build_table(p, L.table, 0, tokens);
+    chunk_prefix(p, L.table, chunk_rows(p, 0, tokens), L.s_pre, L.s_total);
     __syncthreads();
     finalize_segments(p, L.s_total, L.s_mask, L.s_start, L.s_local, L.scratch, tokens, true);
     write_segments(p, L.s_total, L.s_mask, L.s_start, L.s_local, tokens, 0, 1);
-    scatter_chunk(p, L.table, 0, tokens, L.s_start, L.s_mask, L.s_wt);
+    scatter_pairs(p, L.table, 0, tokens, L.s_start, L.s_mask, L.s_pre);
 }
 
 // Per-chunk expert counts by an LDS histogram of the chunk's ids (every
@@ -457,13 +474,16 @@ __global__ __launch_bounds__(kSortThreads) void moe_sort_scatter_kernel(SortPara
     write_segments(p, L.s_total, L.s_mask, L.s_start, L.s_local, tokens, c, (int)gridDim.x);
     for (int e = threadIdx.x; e < E; e += kSortThreads) L.s_pos[e] += L.s_start[e];
     if (c * p.ct >= tokens) return;
-    build_table(p, L.table, c, tokens, L.s_wt);   // its barriers also publish s_pos
-    scatter_chunk(p, L.table, c, tokens, L.s_pos, L.s_mask, L.s_wt);
+    build_table(p, L.table, c, tokens);   // its barriers also publish s_pos
+    chunk_prefix(p, L.table, chunk_rows(p, c, tokens), L.s_pre, nullptr);
+    __syncthreads();
+    scatter_pairs(p, L.table, c, tokens, L.s_pos, L.s_mask, L.s_pre);
 }
 
 // Tokens per chunk: the largest power of two <= 256 whose slot-mask table
 // fits in 48 KB of LDS. With the five per-expert arrays (80 KB at E = 4096)
-// a block's LDS stays under gfx950's 160 KB.
+// and the row-group prefix (at most 16 KB) a block's LDS stays under
+// gfx950's 160 KB.
 static int sort_chunk_tokens(int E, int topk) {
     const int cell = topk <= 8 ? 1 : 4;
     int ct = 256;
@@ -528,8 +548,8 @@ bool launch_moe_sort(const int32_t* topk_ids, const float* topk_w, const int32_t
         if (zero_blocks < 1) zero_blocks = 1;
     }
     const size_t table_lds = (size_t)table_words(p.ct, (int)E, p.cell_bytes) * 4;
-    const size_t full_lds =
-        table_lds + (size_t)p.ct * p.topk * 4 + (size_t)(5 * E + kSortThreads / 64) * 4;
+    const size_t full_lds = table_lds + (size_t)(5 * E + kSortThreads / 64) * 4 +
+                            (size_t)prefix_groups(p.ct, p.cell_bytes) * E * 2;
     p.zero_blocks = zero_blocks;
     // the activation quant rides in the first launch's extra blocks
     bool quant_done = false;
