@@ -94,8 +94,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, int64_t
 // a_scale[row, kb] * w_scale[block h, kb] for row r, steps c = q, q + RP, ...
 // (RP = threads per row) into s_sc[c][h][row]. Step c is K block c % KB of
 // the workgroup's column tile c / KB, whose weight-scale blocks follow the
-// first tile's at a stride of KB, so w0 / w1 are indexed by c itself; NJ
-// covers the KBT steps of all tiles. The loads (clamped addresses, no
+// first tile's TSM blocks (TSM * KB floats) on, TSM = the 128-column blocks
+// of a stage-2 tile (1 in stage 1, whose gate and up blocks each advance by
+// one), so w0 / w1 are indexed by (c - c % KB) * TSM + c % KB; NJ covers the
+// KBT steps of all tiles. The loads (clamped addresses, no
 // branches) and the products are separate calls so the caller can issue
 // other loads in between.
 template <int N>
@@ -110,7 +112,7 @@ struct ScaleRegs {
     float b1[W4 ? 1 : NJ];
 };
 
-template <int BM, int NH, bool W4, int NJ>
+template <int BM, int NH, bool W4, int NJ, int TSM = 1>
 __device__ __forceinline__ void scale_load(ScaleRegs<W4, NJ>& sr, const float* sa, int64_t sa_kb,
                                            const float* w0, const float* w1, int KB, int KBT,
                                            int q) {
@@ -125,8 +127,10 @@ __device__ __forceinline__ void scale_load(ScaleRegs<W4, NJ>& sr, const float* s
         const int kc = cc - KB * (int)(((float)cc + 0.5f) * rkb);
         sr.av[j] = sa[(int64_t)kc * sa_kb];
         if (!W4) {
-            sr.b0[j] = w0[cc];
-            if (NH == 2) sr.b1[j] = w1[cc];
+            // column tile cc / KB's blocks are TSM blocks on from the previous tile's
+            const int wi = (cc - kc) * TSM + kc;
+            sr.b0[j] = w0[wi];
+            if (NH == 2) sr.b1[j] = w1[wi];
         }
     }
 }
@@ -156,12 +160,12 @@ struct BStep {
     int bs[NCT];
 };
 
-template <int BM, int STAGE, bool SHUFFLED, bool W4, int D, int kWM>
+template <int BM, int STAGE, bool SHUFFLED, bool W4, int D, int kWM, int NW2 = 128>
 __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
     constexpr int WN = kWaves / kWM;                     // waves along N
     // 16-row weight groups per wave: stage 1 256 weight rows (128 gate + the
-    // matching 128 up rows) per workgroup, stage 2 128
-    constexpr int NCT = STAGE == 1 ? 16 / WN : 8 / WN;
+    // matching 128 up rows) per workgroup, stage 2 NW2 (128 or 256)
+    constexpr int NCT = STAGE == 1 ? 16 / WN : (NW2 / 16) / WN;
     constexpr int NW = 16 * NCT * WN;                    // weight rows per workgroup
     constexpr int NRT = BM / 16 / kWM;                   // 16-row MFMA tiles per wave
     // FP8 stage 1 computes the transposed tile (weights as the MFMA's A
@@ -448,7 +452,8 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
     auto preheader = [&](auto nj) __attribute__((always_inline)) {
         constexpr int NJ = decltype(nj)::value;
         ScaleRegs<W4, NJ> sr;
-        scale_load<BM, NH, W4, NJ>(sr, sr_a, g.sa_kb, sr_w0, sr_w1, KB, KBT, sr_q);
+        scale_load<BM, NH, W4, NJ, STAGE == 1 ? 1 : NW / 128>(sr, sr_a, g.sa_kb, sr_w0, sr_w1, KB,
+                                                             KBT, sr_q);
 #pragma unroll
         for (int m = 0; m < D - 3; ++m) load_b(bbuf[m], last(m), 0);
         load_a(0, 0);                                           // step -3
@@ -475,21 +480,22 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
             const int nc = n0 + jt * TROWS;
             if (g.part) {
                 // the pair's weighted row, rounded once to bf16, staged through
-                // the free A stage half the rows at a time and stored as whole
+                // the free A stage RPP rows at a time and stored as whole
                 // 16-byte pieces at part[pair, nc ..]
-                static_assert(STAGE != 2 || (BM / 2) * NW * 2 <= A_BYTES,
-                              "half a tile of bf16 rows fits one A stage");
-                uint16_t* s_p = reinterpret_cast<uint16_t*>(&s_a[stg][0]);   // [BM/2][NW]
+                constexpr int RPP = A_BYTES / (NW * 2) >= BM ? BM : A_BYTES / (NW * 2);
+                static_assert(RPP % 16 == 0 && BM % RPP == 0,
+                              "a pass of bf16 rows is whole row tiles and fits one A stage");
+                uint16_t* s_p = reinterpret_cast<uint16_t*>(&s_a[stg][0]);   // [RPP][NW]
 #pragma unroll
-                for (int hf = 0; hf < 2; ++hf) {
+                for (int hf = 0; hf < BM / RPP; ++hf) {
 #pragma unroll
                     for (int rt = 0; rt < NRT; ++rt) {
-                        if ((row_base + rt * 16) / (BM / 2) != hf) continue;
+                        if ((row_base + rt * 16) / RPP != hf) continue;
 #pragma unroll
                         for (int v = 0; v < 4; ++v) {
                             const int row = row_base + rt * 16 + 4 * lq + v;
                             const float wgt = s_w[row];
-                            const int lrow = row - hf * (BM / 2);
+                            const int lrow = row - hf * RPP;
 #pragma unroll
                             for (int ct = 0; ct < NCT; ++ct)
                                 s_p[lrow * NW + wn * NCT * 16 + ct * 16 + lr] =
@@ -497,9 +503,9 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
                         }
                     }
                     __syncthreads();
-                    for (int q = tid; q < (BM / 2) * (NW / 8); q += kThreads) {
+                    for (int q = tid; q < RPP * (NW / 8); q += kThreads) {
                         const int lrow = q / (NW / 8), piece = q % (NW / 8);
-                        const int64_t pair = s_arow[lrow + hf * (BM / 2)];
+                        const int64_t pair = s_arow[lrow + hf * RPP];
                         if (pair < 0) continue;
                         *reinterpret_cast<v4i*>(g.part + pair * g.N + nc + piece * 8) =
                             *reinterpret_cast<const v4i*>(s_p + lrow * NW + piece * 8);
@@ -682,21 +688,22 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
         kloop(IntC<NRT>{});
 }
 
-template <int BM, int STAGE, bool SHUFFLED, bool W4>
+template <int BM, int STAGE, bool SHUFFLED, bool W4, int NW2 = 128>
 static void launch_depth(int KB, int grid, const Args& a, hipStream_t s) {
     // 1 x 4 waves: stage 1 64 rows x 64 weight rows per wave, B two steps
-    // ahead; stage 2 BM rows x 32 columns, B four steps ahead (measured on
-    // MI355X against 2 x 2 waves for stage 2: 1230 vs 1282 us at T=8192)
+    // ahead; stage 2 BM rows x NW2/4 columns, B four steps ahead at 32
+    // columns (measured on MI355X against 2 x 2 waves for stage 2: 1230 vs
+    // 1282 us at T=8192), two at 64
     constexpr int WM = 1;
-    constexpr int DM = STAGE == 1 ? 2 : 4;
+    constexpr int DM = STAGE == 1 || NW2 > 128 ? 2 : 4;
     if (DM >= 4 && KB % 4 == 0)
-        hipLaunchKernelGGL((moe_gemm_prefill_kernel<BM, STAGE, SHUFFLED, W4, DM >= 4 ? 4 : 2, WM>),
+        hipLaunchKernelGGL((moe_gemm_prefill_kernel<BM, STAGE, SHUFFLED, W4, DM >= 4 ? 4 : 2, WM, NW2>),
                            dim3(grid), dim3(kThreads), 0, s, a);
     else if (KB % 2 == 0)
-        hipLaunchKernelGGL((moe_gemm_prefill_kernel<BM, STAGE, SHUFFLED, W4, 2, WM>), dim3(grid),
+        hipLaunchKernelGGL((moe_gemm_prefill_kernel<BM, STAGE, SHUFFLED, W4, 2, WM, NW2>), dim3(grid),
                            dim3(kThreads), 0, s, a);
     else
-        hipLaunchKernelGGL((moe_gemm_prefill_kernel<BM, STAGE, SHUFFLED, W4, 1, WM>), dim3(grid),
+        hipLaunchKernelGGL((moe_gemm_prefill_kernel<BM, STAGE, SHUFFLED, W4, 1, WM, NW2>), dim3(grid),
                            dim3(kThreads), 0, s, a);
 }
 
@@ -706,10 +713,12 @@ template <int STAGE>
 constexpr int wg_rows(int block_m) { return STAGE == 1 ? 64 : block_m; }
 
 template <int STAGE, bool SHUFFLED, bool W4>
-static void launch_bm(int bm, int KB, int grid, const Args& a, hipStream_t s) {
+static void launch_bm(int bm, int KB, int grid, const Args& a, hipStream_t s, bool wide) {
     AMD_CHECK(bm == 64 || bm == 128, "prefill GEMM block_m must be 64 or 128");
     if constexpr (STAGE == 1)
         launch_depth<64, STAGE, SHUFFLED, W4>(KB, grid, a, s);
+    else if (wide)
+        launch_depth<64, STAGE, SHUFFLED, W4, 256>(KB, grid, a, s);
     else if (bm == 64)
         launch_depth<64, STAGE, SHUFFLED, W4>(KB, grid, a, s);
     else
@@ -717,19 +726,33 @@ static void launch_bm(int bm, int KB, int grid, const Args& a, hipStream_t s) {
 }
 
 template <int STAGE>
-static void launch(int bm, int KB, int grid, const Args& a, int shuffled, hipStream_t s) {
+static void launch(int bm, int KB, int grid, const Args& a, int shuffled, hipStream_t s,
+                   bool wide = false) {
     const bool w4 = a.w_scale8 != nullptr;
     if (w4) {
         if (shuffled)
-            launch_bm<STAGE, true, true>(bm, KB, grid, a, s);
+            launch_bm<STAGE, true, true>(bm, KB, grid, a, s, wide);
         else
-            launch_bm<STAGE, false, true>(bm, KB, grid, a, s);
+            launch_bm<STAGE, false, true>(bm, KB, grid, a, s, wide);
     } else {
         if (shuffled)
-            launch_bm<STAGE, true, false>(bm, KB, grid, a, s);
+            launch_bm<STAGE, true, false>(bm, KB, grid, a, s, wide);
         else
-            launch_bm<STAGE, false, false>(bm, KB, grid, a, s);
+            launch_bm<STAGE, false, false>(bm, KB, grid, a, s, wide);
     }
+}
+
+// FP8 stage 2 as 64-row x 256-column workgroups (two per 128-row sorted
+// block; each wave 64 rows x 64 columns, as stage 1) instead of block_m x
+// 128: half the LDS reads per MFMA, and a 128-row block's empty second half
+// exits at once. Measured on MI355X at MiMo dims: T=2048 (64-row blocks)
+// 363-367 -> 338 us, EP share T=4096 97-99 -> 90-91 us, T=8192 950 -> 943 us,
+// T=4096 neutral (571 us); MXFP4 weights 924-931 -> 995-997 us at T=8192, so
+// they keep the narrow tile. AITER_AMD_PF_WIDE2 = 0 / 1 forces it.
+static bool pick_wide2(int64_t hidden, bool w4) {
+    if (hidden % 256 != 0) return false;
+    if (const char* env = getenv("AITER_AMD_PF_WIDE2")) return atoi(env) != 0;
+    return !w4;
 }
 
 // Column tiles per workgroup. Walking two amortises a tile's setup chain
@@ -772,11 +795,15 @@ static int pick_mrot(int stage) {
     return stage == 1;
 }
 
-static int pick_ntw(int stage, int n_tiles, int KB, int64_t pairs, int rows) {
+static int pick_ntw(int stage, int n_tiles, int KB, int64_t pairs, int rows, bool wide = false) {
     if (const char* env = getenv(stage == 1 ? "AITER_AMD_PF_NTW1" : "AITER_AMD_PF_NTW2")) {
         const int c = atoi(env);
         if (c >= 1 && n_tiles % c == 0 && c * KB <= kMaxKB) return c;
     }
+    // the 256-column stage-2 tiles walk one: at two, T=8192 935-942 vs
+    // 939-944 us, T=4096 569 vs 537-540 us, T=2048 342 vs 336 us, EP share
+    // 99.7 vs 89.5-91.7 us (four: 1030 / 662 / 358 / 148 us)
+    if (wide) return 1;
     constexpr int64_t kSlots = 512;   // 256 CUs x 2 workgroups
     constexpr int64_t kMinRounds = 8;
     const int64_t wgs = (pairs + rows - 1) / rows * n_tiles;
@@ -861,15 +888,17 @@ void launch_moe_stage2_prefill(const uint8_t* a2, const float* a2_scale, const u
     g.topk = (int)topk;
     g.E = (int)E;
     g.a_rows = a_rows;
-    g.n_tiles = (int)(hidden / 128);
+    const bool wide = pf::pick_wide2(hidden, w2_scale_e8m0 != nullptr);
+    const int rows = wide ? 64 : (int)block_m;
+    g.n_tiles = (int)(hidden / (wide ? 256 : 128));
     g.block_m = (int)block_m;
-    g.m_tiles = (int)(max_m_blocks * (block_m / pf::wg_rows<2>((int)block_m)));
-    g.ntw = pf::pick_ntw(2, g.n_tiles, (int)(inter / 128), est_pairs, (int)block_m);
+    g.m_tiles = (int)(max_m_blocks * (block_m / rows));
+    g.ntw = pf::pick_ntw(2, g.n_tiles, (int)(inter / 128), est_pairs, rows, wide);
     g.msplit = pf::pick_msplit(2, g.n_tiles / g.ntw);
     g.mrot = pf::pick_mrot(2);
     const int64_t grid = xcd_grid(g.n_tiles / g.ntw, g.m_tiles, g.msplit);
     if (grid == 0) return;
-    pf::launch<2>((int)block_m, (int)(inter / 128), (int)grid, g, shuffled, stream);
+    pf::launch<2>((int)block_m, (int)(inter / 128), (int)grid, g, shuffled, stream, wide);
     AMD_HIP_CHECK(hipGetLastError());
 }
 

@@ -492,6 +492,32 @@ def test_prefill_xcd_order_bit_exact(cuda_device, monkeypatch, weights, bm, orde
         assert torch.equal(out1, outc), (out1.float() - outc.float()).abs().max().item()
 
 
+@pytest.mark.parametrize("weights,bm", [("fp8", 64), ("fp8", 128), ("mxfp4", 128)])
+@pytest.mark.parametrize("T", [300, 2000])
+def test_prefill_stage2_wide_tile_bit_exact(cuda_device, monkeypatch, weights, bm, T):
+    """The prefill stage 2 as 64-row x 256-column workgroups (the FP8
+    default; AITER_AMD_PF_WIDE2 forces either) and as block_m x 128-column
+    ones compute every output element with the same MFMAs and the same
+    scale-fold order, so the layer outputs (per-pair rows summed in slot
+    order) are bitwise equal. T=2000 walks two column tiles in the narrow
+    order (the wide one walks one)."""
+    cfg = W.MoEConfig("wide", T, 2048, 1024, 16, 4, seed=25, weights=weights)
+    wts = W.make_weights(cfg, device=cuda_device, shuffle=True)
+    x = W.make_hidden(cfg, device=cuda_device)
+    tw, ids = W.make_routing(cfg, device=cuda_device)
+
+    def layer(wide):
+        monkeypatch.setenv("AITER_AMD_PF_WIDE2", str(wide))
+        out = W.run_layer(weights, x, wts["w1"], wts["w2"], tw, ids, w1_scale=wts["w1_scale"],
+                          w2_scale=wts["w2_scale"], block_size_M=bm)
+        torch.cuda.synchronize()
+        return out
+
+    narrow, wide = layer(0), layer(1)
+    assert torch.count_nonzero(narrow).item() > 0
+    assert torch.equal(narrow, wide), (narrow.float() - wide.float()).abs().max().item()
+
+
 @pytest.mark.parametrize("weights", ["fp8", "mxfp4"])
 @pytest.mark.parametrize("bm", [16, 32])
 @pytest.mark.parametrize("ntw", [2, 4])
