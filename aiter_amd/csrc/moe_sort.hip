@@ -34,6 +34,8 @@
 // chunk that sums the counts of the chunks before it (and of all chunks,
 // for the segment layout) and writes its pairs -- the prefix is recomputed
 // by every block in parallel instead of by a serial scan launch.
+#include <cstdlib>
+
 #include "common.h"
 #include "quant_dev.h"
 
@@ -480,19 +482,35 @@ __global__ __launch_bounds__(kSortThreads) void moe_sort_scatter_kernel(SortPara
     scatter_pairs(p, L.table, c, tokens, L.s_pos, L.s_mask, L.s_pre);
 }
 
-// Tokens per chunk: the largest power of two <= 256 whose slot-mask table
-// fits in 48 KB of LDS. With the five per-expert arrays (80 KB at E = 4096)
-// and the row-group prefix (at most 16 KB) a block's LDS stays under
-// gfx950's 160 KB.
-static int sort_chunk_tokens(int E, int topk) {
+// Tokens per chunk: at most the largest power of two <= 256 whose slot-mask
+// table fits in 48 KB of LDS (one chunk, the one-shot launch, when the batch
+// fits). With the five per-expert arrays (80 KB at E = 4096) and the
+// row-group prefix (at most 16 KB) a block's LDS stays under gfx950's 160 KB.
+// With several chunks, smaller ones spread the per-chunk walks over more
+// blocks: about 64 chunks (ct = rows / 64 rounded down to a power of two, at
+// least 16). Measured on MI355X at MiMo dims (E = 256, top-8; sort launches'
+// time in the layer): T=512 30.2 -> 17.7 us (ct 16), T=1024 29.2 -> 20.2 us
+// (16), T=2048 28.6 -> 21.6 us (32), EP share T=4096 33.2 -> 29.3 us (64),
+// T=8192 43.3 us (128; 41.1 at 64, 45.2 at 32). AITER_AMD_SORT_CT forces a
+// power of two up to the table limit.
+static int sort_chunk_tokens(int E, int topk, int64_t rows) {
     const int cell = topk <= 8 ? 1 : 4;
     int ct = 256;
     while (ct > 1 && (int64_t)ct * E * cell > 48 * 1024) ct >>= 1;
+    if (rows > ct) {
+        if (const char* env = getenv("AITER_AMD_SORT_CT")) {
+            const int c = atoi(env);
+            if (c >= 1 && c <= ct && (c & (c - 1)) == 0) return c;
+        }
+        int c = 16;
+        while (c * 2 <= ct && (int64_t)c * 2 * 64 <= rows) c *= 2;
+        ct = c < ct ? c : ct;
+    }
     return ct;
 }
 
 int64_t sort_workspace_bytes(int64_t rows, int64_t topk, int64_t E) {
-    int ct = sort_chunk_tokens((int)E, (int)topk);
+    int ct = sort_chunk_tokens((int)E, (int)topk, rows);
     int64_t chunks = ceil_div(rows > 0 ? rows : 1, ct);
     if (chunks <= 1) return 0;
     return chunks * E * 4;
@@ -527,7 +545,7 @@ bool launch_moe_sort(const int32_t* topk_ids, const float* topk_w, const int32_t
     p.topk = (int)topk;
     p.E = (int)E;
     p.bm = (int)bm;
-    p.ct = sort_chunk_tokens((int)E, (int)topk);
+    p.ct = sort_chunk_tokens((int)E, (int)topk, rows);
     p.cell_bytes = topk <= 8 ? 1 : 4;
     p.num_chunks = (int)ceil_div(rows > 0 ? rows : 1, p.ct);
     p.ws = reinterpret_cast<int32_t*>(ws);
