@@ -144,8 +144,11 @@ __device__ __forceinline__ T warp_max_16(T v) {
     return v;
 }
 
+// x * sigmoid(x) with the hardware reciprocal (1 ulp) instead of a correctly
+// rounded division: for x -> -inf the reciprocal of inf is 0 (result -0), for
+// x -> +inf it is 1
 __device__ __forceinline__ float silu_f32(float x) {
-    return x / (1.0f + __expf(-x));
+    return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x));
 }
 
 // torch.nn.functional.gelu (approximate='none'): x/2 * (1 + erf(x/sqrt(2))),
