@@ -264,12 +264,10 @@ __device__ void write_segments(const SortParams& p, const int* s_total, const in
     }
 }
 
-// Rows per prefix group of the chunk table: 8 byte cells form one 64-bit
-// word (bit 8u + j is slot j of row u, so ascending bits are ascending
-// (token, slot)); u32 cells are one row each.
-__device__ __forceinline__ int prefix_rows(const SortParams& p) { return p.cell_bytes == 1 ? 8 : 1; }
-
-// The slot masks of expert e in the 8 rows from tl0 (byte cells).
+// The slot masks of expert e in the 8 rows from tl0 (byte cells) as one
+// 64-bit word: bit 8u + j is slot j of row tl0 + u, so ascending bits are
+// ascending (token, slot). The prefix groups of the chunk table are these 8
+// rows for byte cells and one row for u32 cells.
 __device__ __forceinline__ uint64_t cells8(const SortParams& p, const uint8_t* cells, int tl0,
                                            int nrows, int e) {
     // the 8 rows' cells as two little-endian dwords (rows past nrows read 0)
@@ -346,7 +344,7 @@ __device__ void scatter_pairs(const SortParams& p, const uint32_t* table, int c,
 
 // LDS layout of the sorting kernels: table[ct*E] | s_total[E] | s_start[E] |
 // s_local[E] | s_pos[E] | s_mask[E] | scratch[kSortThreads/64] |
-// s_pre[ceil(ct/prefix_rows)*E] u16
+// s_pre[prefix_groups(ct)*E] u16
 struct SortLds {
     uint32_t* table;
     int* s_total;
