@@ -82,7 +82,9 @@ struct Args {
     int E;
     int64_t a_rows;
     int n_tiles;     // column tiles
-    int m_blocks;
+    int m_blocks;    // M-tiles of BM rows
+    int block_m;     // rows per sorted block (BM or 2 BM): the expert of tile m is
+                     // sorted_eids[m * BM / block_m]
     int msplit;      // XCD groups along M (xcd_tile)
     int mrot;        // stagger the M walk of the XCDs in a group
 };
@@ -193,7 +195,7 @@ __global__ __launch_bounds__(kThreads, 1) void moe_gemm_fp8bs_v2_kernel(Args g) 
     if (mb >= g.m_blocks) return;
     if (mb * BM >= nvalid) return;
     const int tokens = g.num_valid[1];
-    const int e = g.sorted_eids[mb];
+    const int e = g.sorted_eids[(mb * BM) / g.block_m];
     if (e < 0 || e >= g.E) return;
     const int n0 = STAGE == 1 ? nt * 128 : nt * 256;
 
@@ -233,6 +235,10 @@ __global__ __launch_bounds__(kThreads, 1) void moe_gemm_fp8bs_v2_kernel(Args g) 
     const int swsel0 = STAGE == 1 ? 0 : (wn >> 1);
     const int swsel1 = STAGE == 1 ? 1 : (wn >> 1);
     __syncthreads();
+    // a tile with only padding rows (the empty half of a 128-row block) has
+    // nothing to compute; sorting pads each expert's segment at its end, so
+    // such a tile is one whose first row is padding
+    if (s_orow[0] < 0) return;
 
     // ---- per-lane DMA sources (byte offsets; the K step goes in soffset) ----
     uint32_t a_off[A_INSTR];
@@ -600,15 +606,23 @@ void launch_moe_stage1_fp8bs_v2(const uint8_t* a, const float* a_scale, int64_t 
     g.E = (int)E;
     g.a_rows = a_rows;
     g.n_tiles = (int)(inter / 128);
-    g.m_blocks = (int)max_m_blocks;
+    // MXFP4 stage 1 on 128-row sorted blocks runs 64-row tiles (two per
+    // block; an empty second half exits at once), as fast as on 64-row
+    // blocks, so the layer can take 128-row blocks for its stage 2 (the
+    // prefill kernel's). AITER_AMD_V2_TILE1=128 keeps whole-block tiles.
+    int tile = (w1_scale_e8m0 != nullptr && block_m == 128) ? 64 : (int)block_m;
+    if (const char* env = getenv("AITER_AMD_V2_TILE1"))
+        if (atoi(env) == 128 && block_m == 128) tile = 128;
+    g.block_m = (int)block_m;
+    g.m_blocks = (int)(max_m_blocks * (block_m / tile));
     AMD_CHECK(a_rows * K < (1ll << 32) && 2 * inter * K < (1ll << 32) &&
                   g.sa_bytes < (1ll << 32),
               "v2 GEMM needs 32-bit buffer offsets");
     g.msplit = v2::pick_msplit(1, g.n_tiles);
     g.mrot = v2::pick_mrot(1);
-    const int64_t grid = xcd_grid(g.n_tiles, max_m_blocks, g.msplit);
+    const int64_t grid = xcd_grid(g.n_tiles, g.m_blocks, g.msplit);
     if (grid == 0) return;
-    v2::launch<1>((int)block_m, (int)grid, g, shuffled, w1_scale_e8m0 != nullptr, stream);
+    v2::launch<1>(tile, (int)grid, g, shuffled, w1_scale_e8m0 != nullptr, stream);
     AMD_HIP_CHECK(hipGetLastError());
 }
 
@@ -643,6 +657,7 @@ void launch_moe_stage2_fp8bs_v2(const uint8_t* a2, const float* a2_scale, const 
     g.a_rows = a_rows;
     g.n_tiles = (int)(hidden / 256);
     g.m_blocks = (int)max_m_blocks;
+    g.block_m = (int)block_m;
     AMD_CHECK(a_rows * inter < (1ll << 32) && hidden * inter < (1ll << 32) &&
                   g.sa_bytes < (1ll << 32),
               "v2 GEMM needs 32-bit buffer offsets");
