@@ -249,9 +249,10 @@ __global__ __launch_bounds__(kThreads, 1) void moe_gemm_fp8bs_v2_kernel(Args g) 
         const int c = wvu * A_INSTR + i;
         const int row = c * 8 + (lane >> 3);
         const int pc = (lane & 7) ^ a_swz(row);
-        int arow = s_arow[row];
-        if (arow < 0) arow = 0;           // pad rows: any valid row, result unused
-        a_off[i] = (uint32_t)arow * (uint32_t)K + (uint32_t)(pc * 16);
+        const int arow = s_arow[row];
+        // pad rows read past the buffer's end (zeros, no memory access;
+        // results unused, and zero operands switch less in the MFMAs)
+        a_off[i] = arow >= 0 ? (uint32_t)arow * (uint32_t)K + (uint32_t)(pc * 16) : 0xFFFFF000u;
     }
     uint32_t b_off[B_INSTR];
 #pragma unroll

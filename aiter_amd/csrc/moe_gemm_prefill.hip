@@ -260,9 +260,13 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
     for (int j = 0; j < A_PT; ++j) {
         const int q = tid + j * kThreads;
         const int row = q >> 3, pc = q & 7;
-        int arow = s_arow[row];
-        if (arow < 0) arow = 0;                          // pad rows: any valid row, result unused
-        a_off[j] = (uint32_t)arow * (uint32_t)K + (uint32_t)(pc * 16);
+        const int arow = s_arow[row];
+        // pad rows read past the buffer's end, which returns zeros without a
+        // memory access. Their results are unused, and zero operands switch
+        // less in the MFMAs: measured on MI355X against re-reading row 0, the
+        // T=8192 layer 2.644 -> 2.624 ms, T=2048 1.030 -> 1.015 ms, EP share
+        // T=4096 0.307 -> 0.303 ms (the clock is power-bound under these GEMMs)
+        a_off[j] = arow >= 0 ? (uint32_t)arow * (uint32_t)K + (uint32_t)(pc * 16) : 0xFFFFF000u;
         a_dst[j] = row * 128 + ((pc ^ a_swz(row)) << 4);
     }
 
