@@ -199,8 +199,10 @@ def stagewise_vs_oracle(cfg, dev, ref, out, bm, activation, doweight=False, log=
                      sorted_weights=sw if doweight else None, activation=activation)
     loc = ref["ids_local"] >= 0
     codes = a2.view(torch.uint8).cpu().numpy()
-    a2d = R.dequant_1x128(codes.reshape(T * k, I),
-                          a2s.cpu().numpy().reshape(T * k, -1)).reshape(T, k, I)
+    # rows of unrouted pairs hold whatever the buffers held (masked out below)
+    with np.errstate(over="ignore", invalid="ignore"):
+        a2d = R.dequant_1x128(codes.reshape(T * k, I),
+                              a2s.cpu().numpy().reshape(T * k, -1)).reshape(T, k, I)
     ref_d = R.dequant_1x128(ref["a2q"].reshape(T * k, I),
                             ref["a2s"].reshape(T * k, -1)).reshape(T, k, I)
     # each element within one top-binade e4m3 step of its group (32/448 of the

@@ -15,6 +15,7 @@ full-size tests (tests/_fullshape.stagewise_vs_oracle): at most 0.5% of
 stage 1's codes differ from the oracle's, each by at most one top-binade
 step, and the output meets the strict bar against the oracle's stage 2 on
 the kernel's own a2."""
+import os
 import random
 
 import numpy as np
@@ -48,7 +49,13 @@ def _case(seed):
                 routing=routing, local=local)
 
 
-CASES = list(range(1000, 1016))
+def _seeds(base, n=16):
+    """n seeds from base; AITER_AMD_RANDOM_CASES sets n for a longer sweep."""
+    env = os.environ.get("AITER_AMD_RANDOM_CASES")
+    return list(range(base, base + (int(env) if env else n)))
+
+
+CASES = _seeds(1000)
 
 
 @pytest.mark.parametrize("seed", CASES)
@@ -114,7 +121,7 @@ def _variant(seed):
     return c
 
 
-VARIANTS = list(range(2000, 2016))
+VARIANTS = _seeds(2000)
 
 
 @pytest.mark.parametrize("seed", VARIANTS)
