@@ -5,6 +5,17 @@ is loaded in-tree.  Each kernel's registers, spills, scratch, LDS and
 occupancy, as the compiler reports them, go to
 aiter_amd/_build/resource_usage.json.  Usage: ``python -m aiter_amd.build``
 (or ``build()``).
+
+``python -m aiter_amd.build --sanitize`` builds a second library,
+aiter_amd/_build_san/libaiter_amd_san.so, whose host code (the C ABI's
+argument checks, layouts and launch set-up) carries AddressSanitizer and
+UndefinedBehaviorSanitizer; the device code is built as usual.  The CPU tests
+run against it with
+
+    ASAN_OPTIONS=detect_leaks=0 LD_PRELOAD=<clang's libclang_rt.asan-x86_64.so> \
+    AITER_AMD_LIB=aiter_amd/_build_san/libaiter_amd_san.so python -m pytest tests -m "not gpu"
+
+(``sanitizer_runtime()`` finds the runtime; the GPU tests are not run so).
 """
 from __future__ import annotations
 
@@ -85,6 +96,51 @@ def _compile(src: Path, hipcc: str):
     return obj, _resource_usage(res.stderr)
 
 
+SAN_DIR = PKG_DIR / "_build_san"
+SAN_LIB_PATH = SAN_DIR / "libaiter_amd_san.so"
+# host-only sanitizers: each -fsanitize= applies to the host pass alone
+SAN_FLAGS = ["-g", "-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+             "-Xarch_host", "-fno-omit-frame-pointer"]
+
+
+def sanitizer_runtime() -> Path:
+    """clang's AddressSanitizer runtime, preloaded into python for the sanitized library."""
+    hipcc = Path(_hipcc()).resolve()
+    for root in (hipcc.parent.parent / "lib" / "llvm" / "lib" / "clang",
+                 Path("/opt/rocm/lib/llvm/lib/clang")):
+        hits = sorted(root.glob("*/lib/linux/libclang_rt.asan-x86_64.so"))
+        if hits:
+            return hits[-1]
+    raise RuntimeError("libclang_rt.asan-x86_64.so not found next to hipcc")
+
+
+def build_sanitized(verbose: bool = True) -> Path:
+    """The library with AddressSanitizer + UndefinedBehaviorSanitizer host code."""
+    hipcc = _hipcc()
+    SAN_DIR.mkdir(exist_ok=True)
+    srcs = sorted(CSRC.glob("*.hip"))
+
+    def one(src: Path) -> Path:
+        obj = SAN_DIR / (src.stem + ".o")
+        cmd = [hipcc, *HIPCC_FLAGS, *SAN_FLAGS, "-I", str(CSRC),
+               "-I", str(PKG_DIR.parent / "include"), "-c", str(src), "-o", str(obj)]
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stderr}")
+        return obj
+
+    with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
+        objs = list(ex.map(one, srcs))
+    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Xarch_host", "-fsanitize=address",
+           "-Xarch_host", "-fsanitize=undefined", "-o", str(SAN_LIB_PATH), *map(str, objs)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed:\n{res.stderr}")
+    if verbose:
+        print(f"[aiter_amd] built {SAN_LIB_PATH} (host sanitizers)", file=sys.stderr)
+    return SAN_LIB_PATH
+
+
 def build(verbose: bool = True) -> Path:
     hipcc = _hipcc()
     BUILD_DIR.mkdir(exist_ok=True)
@@ -106,4 +162,7 @@ def build(verbose: bool = True) -> Path:
 
 
 if __name__ == "__main__":
-    build()
+    if "--sanitize" in sys.argv[1:]:
+        build_sanitized()
+    else:
+        build()
