@@ -68,8 +68,9 @@ struct SortParams {
     int num_chunks;
     int sort_blocks;            // blocks of the launch doing sorting work
     int zero_blocks;            // then blocks clearing zero_buf
-    // optional 1x128 fp8 quant of the activations (one-shot launch only), run
-    // by q_blocks blocks after the zero blocks
+    // optional 1x128 fp8 quant of the activations, run by q_blocks blocks
+    // after the zero blocks of the one-shot or the counting launch, or after
+    // the chunks of the scatter launch
     const uint16_t* qx;
     uint8_t* qq;
     float* qs;
@@ -448,6 +449,14 @@ constexpr int kChunkBatch = 16;   // per-chunk counts loaded per round trip
 
 __global__ __launch_bounds__(kSortThreads) void moe_sort_scatter_kernel(SortParams p) {
     extern __shared__ uint32_t smem[];
+    if ((int)blockIdx.x >= p.num_chunks) {   // the activation quant, beside the chunks
+        const int b = (int)blockIdx.x - p.num_chunks;
+        if (p.q_bf16)
+            quant_groups_block<true>(p.qx, p.qq, p.qs, p.q_rows, p.q_cols, 0, p.q_num_rows, 1, b);
+        else
+            quant_groups_block<false>(p.qx, p.qq, p.qs, p.q_rows, p.q_cols, 0, p.q_num_rows, 1, b);
+        return;
+    }
     const int tokens = sort_tokens(p);
     const int c = blockIdx.x;
     const SortLds L = carve_lds(p, smem);
@@ -471,7 +480,7 @@ __global__ __launch_bounds__(kSortThreads) void moe_sort_scatter_kernel(SortPara
     }
     __syncthreads();
     finalize_segments(p, L.s_total, L.s_mask, L.s_start, L.s_local, L.scratch, tokens, c == 0);
-    write_segments(p, L.s_total, L.s_mask, L.s_start, L.s_local, tokens, c, (int)gridDim.x);
+    write_segments(p, L.s_total, L.s_mask, L.s_start, L.s_local, tokens, c, p.num_chunks);
     for (int e = threadIdx.x; e < E; e += kSortThreads) L.s_pos[e] += L.s_start[e];
     if (c * p.ct >= tokens) return;
     build_table(p, L.table, c, tokens);   // its barriers also publish s_pos
@@ -516,7 +525,7 @@ int64_t sort_workspace_bytes(int64_t rows, int64_t topk, int64_t E) {
 
 // Returns true when the launch also ran the activation quant given by qx
 // (rows x q_cols, bf16 or fp16, scales row-major, num_rows = local_tokens),
-// in extra blocks of the one-shot or the counting launch.
+// in extra blocks of the one-shot, the counting or the scatter launch.
 bool launch_moe_sort(const int32_t* topk_ids, const float* topk_w, const int32_t* expert_mask,
                      const int32_t* local_tokens, int32_t* sorted_ids, float* sorted_w,
                      int32_t* sorted_eids, int32_t* num_valid, void* zero_buf,
@@ -567,7 +576,7 @@ bool launch_moe_sort(const int32_t* topk_ids, const float* topk_w, const int32_t
     const size_t full_lds = table_lds + (size_t)(5 * E + kSortThreads / 64) * 4 +
                             (size_t)prefix_groups(p.ct, p.cell_bytes) * E * 2;
     p.zero_blocks = zero_blocks;
-    // the activation quant rides in the first launch's extra blocks
+    // the activation quant rides in extra blocks of one of the sorting launches
     bool quant_done = false;
     if (qx && rows > 0 && q_cols >= 128) {
         const int64_t qb = ceil_div(rows * (q_cols / 128), kQuantThreads / 16);
@@ -598,10 +607,19 @@ bool launch_moe_sort(const int32_t* topk_ids, const float* topk_w, const int32_t
             p.zero_skip16 = ceil_div(need, 16);
         }
         p.sort_blocks = p.num_chunks;
-        hipLaunchKernelGGL(moe_sort_count_kernel, dim3(p.num_chunks + zero_blocks + p.q_blocks),
+        // Up to 4096 rows the activation quant rides in the scatter launch,
+        // whose few sorting blocks leave most CUs free; larger quants go in
+        // the counting launch, where they do not slow the latency-bound
+        // scatter. Measured on MI355X at MiMo dims (sort launches' time in the
+        // layer): EP share T=4096 28.7 -> 23.0 us (layer 0.304 -> 0.298 ms),
+        // T=2048 20.6 -> 18.8 us, T=8192 42.7 -> 45.0 us with the quant moved.
+        const bool q_in_scatter = rows <= 4096;
+        hipLaunchKernelGGL(moe_sort_count_kernel,
+                           dim3(p.num_chunks + zero_blocks + (q_in_scatter ? 0 : p.q_blocks)),
                            dim3(kSortThreads), (size_t)E * 4, stream, p);
-        hipLaunchKernelGGL(moe_sort_scatter_kernel, dim3(p.num_chunks), dim3(kSortThreads),
-                           full_lds, stream, p);
+        hipLaunchKernelGGL(moe_sort_scatter_kernel,
+                           dim3(p.num_chunks + (q_in_scatter ? p.q_blocks : 0)),
+                           dim3(kSortThreads), full_lds, stream, p);
         if (ws_in_buf) {
             const int64_t nb = std::min<int64_t>(ceil_div(p.zero_skip16, kSortThreads), 1024);
             hipLaunchKernelGGL(moe_sort_clear_kernel, dim3(nb), dim3(kSortThreads), 0, stream,
