@@ -49,9 +49,10 @@ def parse():
                         "decode32, a8w4_1024, ep4096)")
     p.add_argument("--legs",
                    default="a8w4_32,a8w4_1024,a8w4_8192,ep4096,route_32,route_8192,"
-                           "dense_fp8_ceiling,hbm_ceiling",
+                           "one_launch_1,one_launch_4,one_launch_32,dense_fp8_ceiling,hbm_ceiling",
                    help="comma-separated extra workloads reported under 'legs' ('none': "
                         "skip); route_<T> times the router top-k kernels at T tokens; "
+                        "one_launch_<T> the one-launch layer against the two-launch one; "
                         "dense_fp8_ceiling times the library's plain FP8 GEMM and "
                         "hbm_ceiling torch's streaming read and copy")
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -469,11 +470,51 @@ def hbm_ceiling_leg(name, args, dev):
     return out
 
 
+def one_launch_leg(name, args, dev):
+    """The one-launch layer (both GEMMs in one kernel, the role of the
+    reference's fused_moe_1stage) against the two-launch layer on the same
+    MiMo FP8 decode inputs at T tokens: layer times with AITER_AMD_FUSED=1 and
+    =0, and the tuned table's choice."""
+    import importlib
+    import os
+
+    import torch
+
+    from aiter_amd import workloads as W
+
+    fm = importlib.import_module("aiter_amd.fused_moe")   # the module, not the function
+    T = int(name[len("one_launch_"):])
+    cfg = W.mimo_decode(T)
+    log(f"leg {name}")
+    lay = Layer(cfg, dev)
+    bm = lay.block_m_used()
+    out = {"workload": name, "tokens": T, "block_m": bm,
+           "table_picks_one_launch": bool(fm.select_run_1stage(
+               T, cfg.topk, cfg.experts, cfg.model_dim, cfg.inter_dim, False, bm, dev))}
+    old = os.environ.get("AITER_AMD_FUSED")
+    try:
+        for tag, v in (("one_launch", "1"), ("two_launch", "0")):
+            os.environ["AITER_AMD_FUSED"] = v
+            ms, _ = time_steps(lay.run, max(args.steps, 20), args.warmup)
+            out[f"{tag}_ms"] = round(ms, 4)
+    finally:
+        if old is None:
+            os.environ.pop("AITER_AMD_FUSED", None)
+        else:
+            os.environ["AITER_AMD_FUSED"] = old
+    out["one_launch_speedup"] = round(out["two_launch_ms"] / out["one_launch_ms"], 3)
+    del lay
+    torch.cuda.empty_cache()
+    return out
+
+
 def leg(name, args, dev):
     """One extra workload: layer time, throughput, roofline fractions and
     per-stage kernel times."""
     if name.startswith("route_"):
         return route_leg(name, args, dev)
+    if name.startswith("one_launch_"):
+        return one_launch_leg(name, args, dev)
     if name == "dense_fp8_ceiling":
         return dense_ceiling_leg(name, args, dev)
     if name == "hbm_ceiling":
