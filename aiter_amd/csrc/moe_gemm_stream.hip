@@ -659,11 +659,23 @@ static void launch(int bm, int KB, dim3 grid, const Args& a, int shuffled, hipSt
 // groups, T=128 378 -> 351 us; fp4 T=32 128 -> 124 us at four; T=1 15 ->
 // 24 us at two (64 workgroups), hence the grid floor. est_blocks: the
 // expected M-blocks (at decode sizes one per touched expert).
+// fp8 weights follow a table of the single-walk grid's rounds r1 (est_blocks
+// x groups / 512 workgroup slots), measured on MI355X at MiMo dims (stage 2,
+// us at one / two / four groups): T=8 (r1 = 2) 81.7 / 78.2 / 81.5, T=16
+// (r1 = 4) 151 / 148 / 139, T=32 (r1 = 8) 237 / 217 / 222, T=128 (r1 = 32)
+// 377 / 352 / 343 -- a walk that leaves one full round wins, and larger
+// grids prefer two groups up to ~24 rounds, four beyond.
 // AITER_AMD_ST_NTW2 forces a count (tests use it).
 static int pick_ntw2(int64_t groups, int64_t KB, int64_t KBY, int64_t est_blocks) {
     if (const char* env = getenv("AITER_AMD_ST_NTW2")) {
         const int c = atoi(env);
         if (c >= 1 && groups % c == 0 && c * KB <= kMaxKB) return c;
+    }
+    if (KBY == KB * 128) {   // fp8 weights
+        const int64_t w1 = est_blocks * groups;     // workgroups of the single walk
+        int c = w1 >= 24 * 512 ? 4 : w1 >= 6 * 512 ? 2 : w1 >= 3 * 512 ? 4 : w1 >= 768 ? 2 : 1;
+        while (c > 1 && (groups % c != 0 || c * KB > kMaxKB)) c /= 2;
+        return c;
     }
     constexpr int64_t kMinWgs = 1024;             // 256 CUs x 2 workgroups x 2 rounds
     constexpr int64_t kTargetBytes = 1 << 20;     // weight bytes per workgroup
