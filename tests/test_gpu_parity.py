@@ -68,6 +68,32 @@ def test_sorting_bit_exact(cuda_device, T, E, k, bm, masked, local):
     assert np.array_equal(_np(se)[: n // bm], ref[2])
 
 
+@pytest.mark.parametrize("ct", [1, 8, 32, 128])
+def test_sorting_chunk_size_invariant(cuda_device, monkeypatch, ct):
+    """The multi-chunk sort (AITER_AMD_SORT_CT forces tokens per chunk) gives
+    the oracle's arrays bit for bit whatever the chunking: one token per
+    chunk, a chunk per 8 tokens (one 64-bit word of slot masks), and larger
+    ones; with a duplicated id inside a token's top-k, an out-of-range id and
+    an expert mask."""
+    monkeypatch.setenv("AITER_AMD_SORT_CT", str(ct))
+    T, E, k, bm = 1000, 64, 6, 32
+    ids, w = _routing_np(T, E, k, seed=ct + 5)
+    ids[3, 1] = ids[3, 0]          # a duplicate expert inside one token's top-k
+    ids[7, 2] = E + 3              # an id out of range
+    mask = np.random.default_rng(ct).integers(0, 2, E).astype(np.int32)
+    sid, sw, se, nv, buf = A.moe_sorting(torch.from_numpy(ids).to(cuda_device),
+                                         torch.from_numpy(w).to(cuda_device), E, 256,
+                                         torch.bfloat16, bm, torch.from_numpy(mask).to(cuda_device))
+    ref = R.moe_sorting_argsort(ids, w, E, bm, mask, None)
+    nv = _np(nv)
+    assert np.array_equal(nv, ref[3])
+    n = int(nv[0])
+    assert np.array_equal(_np(sid)[:n], ref[0])
+    assert np.array_equal(_np(sw)[:n].view(np.int32), ref[1].view(np.int32))
+    assert np.array_equal(_np(se)[: n // bm], ref[2])
+    assert torch.count_nonzero(buf).item() == 0
+
+
 def test_sorting_worked_example(cuda_device):
     """The reference's worked example (csrc/include/moe_sorting_opus.h:277-339,
     fixture tests/golden/moe_sorting_worked_example.json), every output array."""
