@@ -77,6 +77,7 @@ struct Args {
     int ntw;                   // column tiles per workgroup, walked in one pipelined K loop
     int msplit;                // XCD groups along M (1, 2, 4 or 8; see the tile order)
     int mrot;                  // stagger the M walk of the XCDs in a group
+    int pad_skip;              // run tiles of few routed rows on a body without their padding MFMAs
 };
 
 // Slot of a row's 16-byte A piece in LDS: piece p of row r sits at slot
@@ -245,6 +246,20 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
     // M-block) has nothing to compute
     if (__syncthreads_or(any_valid) == 0) return;
 
+    const int row_base = wm * (BM / kWM);
+    // row tiles of this wave that hold a routed row (sorting pads each
+    // expert's last block at its end): the MFMAs and FMAs of the others
+    // are skipped, their accumulators stay 0 and their rows are not stored
+    int nact = 0;
+#pragma unroll
+    for (int rt = 0; rt < NRT; ++rt)
+        if (__builtin_amdgcn_ballot_w64(s_arow[row_base + rt * 16 + lr] >= 0) != 0) nact = rt + 1;
+    nact = __builtin_amdgcn_readfirstlane(nact);
+
+    // The rest of the tile, for waves with NA active row tiles. Each NA is a
+    // whole copy from here on, so the copies share no live registers (a
+    // second K-loop copy after a shared prologue spilled).
+    auto body = [&](auto na) __attribute__((always_inline)) {
     const int K = g.K;
     const int KB = K / 128;
     const int KBY = W4 ? K / 2 : K;
@@ -330,16 +345,6 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
     for (int rt = 0; rt < NRT; ++rt)
 #pragma unroll
         for (int ct = 0; ct < NCT; ++ct) acc[rt][ct] = v4f{0.f, 0.f, 0.f, 0.f};
-    const int row_base = wm * (BM / kWM);
-    // row tiles of this wave that hold a routed row (sorting pads each
-    // expert's last block at its end): the MFMAs and FMAs of the others
-    // are skipped, their accumulators stay 0 and their rows are not stored
-    int nact = 0;
-#pragma unroll
-    for (int rt = 0; rt < NRT; ++rt)
-        if (__builtin_amdgcn_ballot_w64(s_arow[row_base + rt * 16 + lr] >= 0) != 0) nact = rt + 1;
-    nact = __builtin_amdgcn_readfirstlane(nact);
-
     // One K step: nact x NCT MFMAs, row tile by row tile (the B fragments
     // stay in registers for the whole step). Region r of the step issues the
     // MFMAs of row tile r+1 into one of two result sets, prefetches the next
@@ -684,13 +689,29 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
             }
         }
     };
-    // a wave whose rows are all padding runs a copy of the K loop without
-    // math (it still stages A and meets every barrier); more copies, one
-    // per active row-tile count, push the kernel past 256 registers
+    kloop(na);
+    };
+    // A wave whose rows are all padding runs the body without math (it still
+    // stages A and meets every barrier, as every copy does). With pad_skip, a
+    // stage-2 tile of at most NRT/4 (and, in 128-row tiles, NRT/2) active row
+    // tiles runs a copy that skips the MFMAs of the rest. Each copy adds ~20 KB
+    // of code (the instruction cache is shared by two CUs), so 64-row tiles
+    // get one. Not in the FP8 128-row tile (FP8 takes the 64-row wide tile),
+    // where the copies spill. Measured on MI355X at MiMo dims, same boxes,
+    // stage 2: T=8192 926-938 -> 920-928 us, T=2048 331-333 -> 329-331 us,
+    // A8W4 T=8192 (128-row tiles) 960-971 -> 931-934 us. Stage 1 (a copy
+    // at NRT/4) was no faster: T=8192 1540-1559 -> 1530-1538 us but T=2048
+    // 574-577 -> 580-584 us and the EP share 160-162 -> 162-165 us; its small
+    // tiles are bound by their weight stream, not by their MFMAs.
+    constexpr bool kPadCopies = STAGE == 2 && NRT >= 4 && !(BM == 128 && !W4);
     if (kWM > 1 && nact == 0)
-        kloop(IntC<0>{});
+        body(IntC<0>{});
+    else if (kPadCopies && g.pad_skip && nact <= NRT / 4)
+        body(IntC<kPadCopies ? NRT / 4 : NRT>{});
+    else if (kPadCopies && NRT >= 8 && g.pad_skip && nact <= NRT / 2)
+        body(IntC<kPadCopies && NRT >= 8 ? NRT / 2 : NRT>{});
     else
-        kloop(IntC<NRT>{});
+        body(IntC<NRT>{});
 }
 
 template <int BM, int STAGE, bool SHUFFLED, bool W4, int NW2 = 128>
@@ -794,6 +815,16 @@ static int pick_msplit(int stage, int ng) {
     return 2;
 }
 
+// Stage-2 tiles with few routed rows (the end of an expert's last block, and
+// the many experts of a skewed routing that get a handful of rows) run a copy
+// of the tile's body that skips the MFMAs and FMAs of their padding row
+// tiles. AITER_AMD_PF_PADSKIP = 0 runs every tile on the full body (tests
+// use it).
+static int pick_pad_skip() {
+    if (const char* env = getenv("AITER_AMD_PF_PADSKIP")) return atoi(env) != 0;
+    return 1;
+}
+
 static int pick_mrot(int stage) {
     if (const char* env = getenv(stage == 1 ? "AITER_AMD_PF_MROT1" : "AITER_AMD_PF_MROT2"))
         return atoi(env) != 0;
@@ -859,6 +890,7 @@ void launch_moe_stage1_prefill(const uint8_t* a, const float* a_scale, int64_t s
     g.ntw = pf::pick_ntw(1, g.n_tiles, (int)(K / 128), a_rows * topk, 64);
     g.msplit = pf::pick_msplit(1, g.n_tiles / g.ntw);
     g.mrot = pf::pick_mrot(1);
+    g.pad_skip = pf::pick_pad_skip();
     const int64_t grid = xcd_grid(g.n_tiles / g.ntw, g.m_tiles, g.msplit);
     if (grid == 0) return;
     pf::launch<1>((int)block_m, (int)(K / 128), (int)grid, g, shuffled, stream);
@@ -901,6 +933,7 @@ void launch_moe_stage2_prefill(const uint8_t* a2, const float* a2_scale, const u
     g.ntw = pf::pick_ntw(2, g.n_tiles, (int)(inter / 128), est_pairs, rows, wide);
     g.msplit = pf::pick_msplit(2, g.n_tiles / g.ntw);
     g.mrot = pf::pick_mrot(2);
+    g.pad_skip = pf::pick_pad_skip();
     const int64_t grid = xcd_grid(g.n_tiles / g.ntw, g.m_tiles, g.msplit);
     if (grid == 0) return;
     pf::launch<2>((int)block_m, (int)(inter / 128), (int)grid, g, shuffled, stream, wide);

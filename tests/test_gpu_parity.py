@@ -519,6 +519,47 @@ def test_prefill_xcd_order_bit_exact(cuda_device, monkeypatch, weights, bm, orde
 
 
 @pytest.mark.parametrize("weights,bm", [("fp8", 64), ("fp8", 128), ("mxfp4", 128)])
+@pytest.mark.parametrize("T,E", [(300, 64), (2000, 64), (700, 16)])
+def test_prefill_pad_skip_bit_exact(cuda_device, monkeypatch, weights, bm, T, E):
+    """Prefill stage-2 tiles with at most a quarter (or, in 128-row tiles,
+    half) of their 16-row tiles routed run a copy of the kernel body that
+    skips the padding tiles' MFMAs (AITER_AMD_PF_PADSKIP = 0 runs every tile
+    on the full body). Routed rows get the same MFMAs and fold order either
+    way, so the layer output is bitwise equal (and stage 1's a2, which has no
+    such copy, too). Zipf routing over 64 experts leaves most experts a
+    handful of rows, so tiles of 1-16, 17-32 and more rows all occur. MXFP4
+    runs its stage 2 (128-row tiles) on the prefill kernel at bm 128."""
+    cfg = W.MoEConfig("padskip", T, 2048, 1024, E, 4, routing="zipf", seed=27, weights=weights)
+    wts = W.make_weights(cfg, device=cuda_device, shuffle=True)
+    x = W.make_hidden(cfg, device=cuda_device)
+    tw, ids = W.make_routing(cfg, device=cuda_device)
+    counts = torch.bincount(ids.flatten().long().cpu(), minlength=E)
+    assert int(((counts > 0) & (counts <= 32)).sum()) > 0 and int((counts > 64).sum()) > 0
+
+    def layer(skip):
+        monkeypatch.setenv("AITER_AMD_PF_PADSKIP", str(skip))
+        out = W.run_layer(weights, x, wts["w1"], wts["w2"], tw, ids, w1_scale=wts["w1_scale"],
+                          w2_scale=wts["w2_scale"], block_size_M=bm)
+        a2 = None
+        if weights == "fp8":
+            a1, a1s = A.per_group_quant_hip(x)
+            sid, sw, se, nv, _ = A.moe_sorting(ids, tw, cfg.experts, cfg.model_dim,
+                                                torch.bfloat16, bm)
+            a2, a2s = A.moe_stage1_fp8_blockscale(a1, a1s, wts["w1"], wts["w1_scale"], sid, se,
+                                                  nv, cfg.topk, bm, True)
+            a2 = (a2.view(torch.uint8).clone(), a2s.clone())
+        torch.cuda.synchronize()
+        return out, a2
+
+    out0, a20 = layer(0)
+    out1, a21 = layer(1)
+    if a20 is not None:
+        assert torch.equal(a20[0], a21[0]) and torch.equal(a20[1], a21[1])
+    assert torch.count_nonzero(out0).item() > 0
+    assert torch.equal(out0, out1), (out0.float() - out1.float()).abs().max().item()
+
+
+@pytest.mark.parametrize("weights,bm", [("fp8", 64), ("fp8", 128), ("mxfp4", 128)])
 @pytest.mark.parametrize("T", [300, 2000])
 def test_prefill_stage2_wide_tile_bit_exact(cuda_device, monkeypatch, weights, bm, T):
     """The prefill stage 2 as 64-row x 256-column workgroups (the FP8
