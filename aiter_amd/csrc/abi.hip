@@ -118,25 +118,38 @@ struct WScale {
 // Kernel choice per shape (measured on MI355X): 16/32-row M-blocks
 // (decode-sized layers) take the register-streaming kernels; 64/128-row
 // M-blocks take, for FP8 weights, the register-B prefill kernels and, for
-// MXFP4 weights (half the weight bytes per K step), the direct-to-LDS
-// kernels -- except stage 2 at 128 rows, where the register-B kernel's 1 x 8
-// tile is faster for both.  Stage 2 of all of them needs 256-column output tiles
+// MXFP4 weights, the same kernels once the experts average 32 routed rows
+// (below that the direct-to-LDS kernels, and stage 2 at 128 rows always the
+// prefill kernel).  Stage 2 of all of them needs 256-column output tiles
 // (model_dim % 256 == 0); other shapes take the general kernels of
 // moe_gemm_fp8bs.hip.
 // sw: sorted routing weights for doweight_stage1 (applied to gate and up
 // before the activation), or NULL; act: kActSilu or kActGelu.
+// MXFP4 weights take the prefill kernels (weights in registers, their e8m0
+// bytes one load per few K steps) once the experts average at least 32 routed
+// rows, and the direct-to-LDS MXFP4 kernels below that, whose waves skip
+// padding-only 32-row halves. Measured on MI355X at MiMo dims (bm 64; stage
+// 1 / stage 2 / layer): T=2048 664 -> 581 us / 367 -> 288 us / 1.039 -> 0.966
+// ms, T=1024 501 -> 498 / 258 -> 244 / 0.792 -> 0.784 ms; T=8192 (bm 128)
+// layer 2.74 -> 2.40 ms; T=512 (16 rows per expert) stage 1 453 vs 486 us on
+// the prefill kernel.
+constexpr int64_t kW4PrefillRows = 32;
+static bool w4_on_prefill(int64_t pairs, int64_t E) { return pairs >= kW4PrefillRows * E; }
+
 static void stage1_dispatch(const uint8_t* a, const float* sa, int64_t sa_row, int64_t sa_kb,
                             const uint8_t* w1, WScale w1s, const int32_t* sid,
                             const int32_t* seid, const int32_t* nv, uint8_t* a2, float* a2s,
                             int64_t a_rows, int64_t K, int64_t I, int64_t E, int64_t topk,
                             int64_t bm, int64_t mblocks, int sh, hipStream_t s,
                             const float* sw, int act, int ksplit = 1, void* kpart = nullptr,
-                            int32_t* kcnt = nullptr, int64_t kmb = 0) {
+                            int32_t* kcnt = nullptr, int64_t kmb = 0, int64_t est_pairs = -1) {
     if (stream_supported(bm, K))
         launch_moe_stage1_stream(a, sa, sa_row, sa_kb, w1, w1s.f32, w1s.e8m0, sid, seid, nv, a2,
                                  a2s, a_rows, K, I, E, topk, bm, mblocks, sh, s, sw, act, ksplit,
                                  kpart, kcnt, kmb);
-    else if (prefill_supported(bm, K) && !w1s.e8m0 && a_fits32(a_rows, K))
+    else if (prefill_supported(bm, K) &&
+             (!w1s.e8m0 || w4_on_prefill(est_pairs < 0 ? a_rows * topk : est_pairs, E)) &&
+             a_fits32(a_rows, K))
         launch_moe_stage1_prefill(a, sa, sa_row, sa_kb, w1, w1s.f32, w1s.e8m0, sid, seid, nv, a2,
                                   a2s, a_rows, K, I, E, topk, bm, mblocks, sh, s, sw, act);
     else if (v2_supported(bm, K) && a_fits32(a_rows, K))
@@ -149,10 +162,12 @@ static void stage1_dispatch(const uint8_t* a, const float* sa, int64_t sa_row, i
 
 // Stage 2 runs on the prefill kernel for this shape (the only stage-2
 // kernel that can also write per-pair bf16 rows instead of accumulating).
-static bool stage2_on_prefill(int64_t bm, int64_t I, int64_t H, WScale w2s, int64_t a_rows) {
+static bool stage2_on_prefill(int64_t bm, int64_t I, int64_t H, WScale w2s, int64_t a_rows,
+                              int64_t E, int64_t est_pairs) {
     return !(stream_supported(bm, I) && H % 256 == 0) && prefill_supported(bm, I) &&
            a_fits32(a_rows, I) &&
-           H % 256 == 0 && (!w2s.e8m0 || bm == 128);
+           H % 256 == 0 &&
+           (!w2s.e8m0 || bm == 128 || w4_on_prefill(est_pairs < 0 ? a_rows : est_pairs, E));
 }
 
 // acc: [tokens, H] accumulated atomically, fp32 or (the reference's moe_buf)
@@ -166,13 +181,12 @@ static void stage2_dispatch(const uint8_t* a2, const float* a2s, const uint8_t* 
                             int64_t a_rows, int64_t I, int64_t H, int64_t E, int64_t topk,
                             int64_t bm, int64_t mblocks, int sh, hipStream_t s,
                             uint16_t* part = nullptr, int64_t est_pairs = -1) {
-    AMD_CHECK(!part || stage2_on_prefill(bm, I, H, w2s, a_rows),
-              "per-pair rows need the prefill kernel");
+    const bool on_prefill = stage2_on_prefill(bm, I, H, w2s, a_rows, E, est_pairs);
+    AMD_CHECK(!part || on_prefill, "per-pair rows need the prefill kernel");
     if (stream_supported(bm, I) && H % 256 == 0)
         launch_moe_stage2_stream(a2, a2s, w2, w2s.f32, w2s.e8m0, sid, sw, seid, nv, acc,
                                  acc_dtype, a_rows, I, H, E, topk, bm, mblocks, sh, s);
-    else if (prefill_supported(bm, I) && H % 256 == 0 && (!w2s.e8m0 || bm == 128) &&
-             a_fits32(a_rows, I))
+    else if (on_prefill)
         launch_moe_stage2_prefill(a2, a2s, w2, w2s.f32, w2s.e8m0, sid, sw, seid, nv, acc,
                                   acc_dtype, part, a_rows, I, H, E, topk, bm, mblocks, sh, s,
                                   est_pairs < 0 ? a_rows : est_pairs);
@@ -457,7 +471,10 @@ void fused_entry(const void* hidden_states, int hidden_dtype, const void* w1, WS
     float* acc = reinterpret_cast<float*>(ws + L.off_acc);
     // stage 2 on the prefill kernel writes each pair's weighted row once (bf16)
     // and one pass sums a token's slots: no fp32 atomics, no accumulator to clear
-    uint16_t* part = stage2_on_prefill(block_m, inter_dim, model_dim, w2s, tokens * topk)
+    // pairs expected on this GPU (the expert-parallel share of tokens * topk)
+    const int64_t local_pairs = tokens * topk * num_experts / E_sort;
+    uint16_t* part = stage2_on_prefill(block_m, inter_dim, model_dim, w2s, tokens * topk,
+                                       num_experts, local_pairs)
                          ? reinterpret_cast<uint16_t*>(ws + L.off_acc) : nullptr;
     hipStream_t s = (hipStream_t)stream;
     timing_mark(0, s);
@@ -494,13 +511,12 @@ void fused_entry(const void* hidden_states, int hidden_dtype, const void* w1, WS
                     sorted_eids, num_valid, a2, a2_scale, tokens, model_dim, inter_dim,
                     num_experts, topk, block_m, L.blocks, sh, s, dw ? sorted_w : nullptr,
                     (int)activation, L.ksplit, ws + L.off_kpart,
-                    reinterpret_cast<int32_t*>(ws + L.off_kcnt), L.kmb);
+                    reinterpret_cast<int32_t*>(ws + L.off_kcnt), L.kmb, local_pairs);
     timing_mark(3, s);
     stage2_dispatch(a2, a2_scale, (const uint8_t*)w2, w2s, sorted_ids, dw ? nullptr : sorted_w,
                     sorted_eids,
                     num_valid, part ? nullptr : acc, DT_FP32, tokens * topk, inter_dim, model_dim,
-                    num_experts, topk, block_m, L.blocks, sh, s, part,
-                    tokens * topk * num_experts / E_sort);
+                    num_experts, topk, block_m, L.blocks, sh, s, part, local_pairs);
     timing_mark(4, s);
     if (part)
         launch_slot_sum(part, topk_ids, expert_mask, E_sort, num_valid, out, out_dtype, tokens,

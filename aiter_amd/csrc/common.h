@@ -133,6 +133,14 @@ __device__ __forceinline__ v4f mfma16x16x128_fp8_fp4(const v8i& a, const v8i& b,
     return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, z, 0, 4, 0, 127, 0, b_scale);
 }
 
+// The same product with the operands' roles swapped: fp4 e2m1 weights as the
+// MFMA's A operand (e8m0 scale per A lane from byte 0 of a_scale) and fp8 e4m3
+// activations as B (scale 127 = 1.0), fragments laid out per lane as above.
+__device__ __forceinline__ v4f mfma16x16x128_fp4_fp8(const v8i& a, const v8i& b, int a_scale) {
+    v4f z = {0.f, 0.f, 0.f, 0.f};
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, z, 4, 0, 0, a_scale, 0, 127);
+}
+
 template <typename T>
 __device__ __forceinline__ T warp_max_16(T v) {
     // max over the 16 lanes that share lane/16 (xor over lane bits 0..3)

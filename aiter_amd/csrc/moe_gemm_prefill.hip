@@ -159,7 +159,6 @@ __device__ __forceinline__ void scale_store(const ScaleRegs<W4, NJ>& sr, float* 
 template <bool W4, int NCT>
 struct BStep {
     v4i b[NCT][W4 ? 1 : 2];
-    int bs[NCT];
 };
 
 template <int BM, int STAGE, bool SHUFFLED, bool W4, int D, int kWM, int NW2 = 128>
@@ -174,7 +173,7 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
     // operand): a lane then holds one token row and four consecutive output
     // columns, so its activation scale is one value per row tile and its
     // fp8 outputs pack into one dword
-    constexpr bool TR = STAGE == 1 && !W4;
+    constexpr bool TR = STAGE == 1;
     constexpr int A_BYTES = BM * 128;
     constexpr int A_PT = A_BYTES / 16 / kThreads;        // 16-byte A pieces per thread
     // scale products per (row, kb): stage 1 gate / up blocks; stage 2 the
@@ -307,7 +306,7 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
         else
             boff[ct] = SHUFFLED ? (uint32_t)(row0 * K + lq * 512 + lr * 16)
                                 : (uint32_t)((row0 + lr) * K + lq * 32);
-        bsoff[ct] = (uint32_t)((row0 + lr) * KS + lq);
+        bsoff[ct] = (uint32_t)((row0 + lr) * KS);
     }
     constexpr int BSTEP = W4 ? (SHUFFLED ? 1024 : 64) : (SHUFFLED ? 2048 : 128);
     constexpr int BHI = SHUFFLED ? 256 : 16;
@@ -323,7 +322,32 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
             if (!W4)
                 s.b[ct][W4 ? 0 : 1] =
                     __builtin_amdgcn_raw_buffer_load_b128(rb, boff[ct] + BHI, so, 0);
-            s.bs[ct] = W4 ? (int)__builtin_amdgcn_raw_buffer_load_b8(rbs, bsoff[ct], sso, 0) : 0;
+        }
+    };
+    // A8W4: the e8m0 bytes of the D K steps kb .. kb + D - 1 of each of the
+    // lane's weight rows in one load per D steps (4 D bytes per row, D
+    // divides KB): dword d holds step kb + d's byte for lane group q in byte
+    // q. A byte load per step and row group made the MXFP4 stage 1 wait on
+    // its scale loads (each touches 16 rows' cache lines): measured on MI355X
+    // at T=8192 with no scale loads at all, 1806 -> 1189 us.
+    int sg_cur[NCT][D], sg_nxt[NCT][D];
+    auto load_sg = [&](int (&dst)[NCT][D], int kb, int jt) __attribute__((always_inline)) {
+        if constexpr (W4) {
+            const int sso = __builtin_amdgcn_readfirstlane(kb * 4 + jt * (TROWS * KS));
+#pragma unroll
+            for (int ct = 0; ct < NCT; ++ct) {
+                if constexpr (D == 4) {
+                    const auto v = __builtin_amdgcn_raw_buffer_load_b128(rbs, bsoff[ct], sso, 0);
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) dst[ct][d] = (int)v[d];
+                } else if constexpr (D == 2) {
+                    const auto v = __builtin_amdgcn_raw_buffer_load_b64(rbs, bsoff[ct], sso, 0);
+                    dst[ct][0] = (int)v[0];
+                    dst[ct][1] = (int)v[1];
+                } else {
+                    dst[ct][0] = (int)__builtin_amdgcn_raw_buffer_load_b32(rbs, bsoff[ct], sso, 0);
+                }
+            }
         }
     };
     // A of step k is staged in areg[k & 1]: loaded two steps ahead, stored
@@ -352,8 +376,13 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
     // (issued one region earlier) into the accumulators. The regions are
     // fenced so the scheduler cannot pair an FMA with the MFMA that feeds it
     // (which serialises a wave on MFMA latency).
-    auto compute = [&](const BS& bsv, int st, int stage, auto na) __attribute__((always_inline)) {
+    auto compute = [&](const BS& bsv, int st, int stage, auto na, int d)
+                       __attribute__((always_inline)) {
         constexpr int NA = decltype(na)::value;
+        // A8W4: this step's e8m0 byte of the lane's weight row in byte 0
+        int bsc[NCT];
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct) bsc[ct] = W4 ? sg_cur[ct][d] >> (8 * lq) : 0;
         const uint8_t* sa_src = &s_a[stage][0];
         // the lane's 32 K bytes of row tile rt: fp8 x fp8 pieces 2 lq, 2 lq + 1
         // (K 32 lq ..); fp8 x fp4 pieces lq, lq + 4 (K 16 lq .. and 64 + 16 lq ..)
@@ -374,8 +403,10 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
                        bsv.b[ct][W4 ? 0 : 1][2], bsv.b[ct][W4 ? 0 : 1][3]};
         };
         auto mfma = [&](const v8i& a, int ct) {
-            if constexpr (TR) return mfma16x16x128_fp8(bfrag(ct), a);
-            return W4 ? mfma16x16x128_fp8_fp4(a, bfrag(ct), bsv.bs[ct])
+            if constexpr (TR)
+                return W4 ? mfma16x16x128_fp4_fp8(bfrag(ct), a, bsc[ct])
+                          : mfma16x16x128_fp8(bfrag(ct), a);
+            return W4 ? mfma16x16x128_fp8_fp4(a, bfrag(ct), bsc[ct])
                       : mfma16x16x128_fp8(a, bfrag(ct));
         };
         // scale half of column tile ct: stage 1 gate (ct < NCT/2) / up;
@@ -464,16 +495,28 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
         ScaleRegs<W4, NJ> sr;
         scale_load<BM, NH, W4, NJ, STAGE == 1 ? 1 : NW / 128>(sr, sr_a, g.sa_kb, sr_w0, sr_w1, KB,
                                                              KBT, sr_q);
+        // the e8m0 group of steps 0 .. D-1 follows the load of B step 0, as
+        // the loop's group loads follow its step-0 B load
 #pragma unroll
-        for (int m = 0; m < D - 3; ++m) load_b(bbuf[m], last(m), 0);
+        for (int m = 0; m < D - 3; ++m) {
+            load_b(bbuf[m], last(m), 0);
+            if (m == 0) load_sg(sg_cur, 0, 0);
+        }
         load_a(0, 0);                                           // step -3
-        if constexpr (D >= 3) load_b(bbuf[D - 3], last(D - 3), 0);
+        if constexpr (D >= 3) {
+            load_b(bbuf[D - 3], last(D - 3), 0);
+            if (D == 3) load_sg(sg_cur, 0, 0);
+        }
         load_a(1, last(1));                                     // step -2
-        if constexpr (D >= 2) load_b(bbuf[D - 2], last(D - 2), 0);
+        if constexpr (D >= 2) {
+            load_b(bbuf[D - 2], last(D - 2), 0);
+            if (D == 2) load_sg(sg_cur, 0, 0);
+        }
         scale_store<BM, NH, W4, NJ>(sr, s_sc, KBT, sr_r, sr_q, sr_arow >= 0);
         store_a(0);                                             // step -1
         load_a(0, last(2));
         load_b(bbuf[D - 1], last(D - 1), 0);
+        if (D == 1) load_sg(sg_cur, 0, 0);
     };
     constexpr int RP = kThreads / BM;
     if (KBT <= 16)
@@ -658,7 +701,7 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
                 load_a((k + 1) & 1, ka);
                 // issue the A loads before the step's math (a full step to land)
                 __builtin_amdgcn_sched_barrier(0);
-                compute(bbuf[d], k, k & 1, na);
+                compute(bbuf[d], k, k & 1, na, d);
                 // B of step k + D: this column tile or the next (D divides KB)
                 int kn = kbl + d + D, jn = jt;
                 if (kn >= KB) {
@@ -670,10 +713,18 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
                     jn = ntw - 1;
                 }
                 load_b(bbuf[d], kn, jn);
+                // the next D steps' e8m0 group (past the end: the last group)
+                if (d == 0) load_sg(sg_nxt, kn - (kn % D), jn);
                 __syncthreads();
                 // keep the scheduler from interleaving the unrolled steps (their
                 // operand sets would all be live at once)
                 __builtin_amdgcn_sched_barrier(0);
+            }
+            if constexpr (W4) {
+#pragma unroll
+                for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+                    for (int d = 0; d < D; ++d) sg_cur[ct][d] = sg_nxt[ct][d];
             }
             kbl += D;
             if (kbl == KB) {
@@ -768,17 +819,18 @@ static void launch(int bm, int KB, int grid, const Args& a, int shuffled, hipStr
     }
 }
 
-// FP8 stage 2 as 64-row x 256-column workgroups (two per 128-row sorted
-// block; each wave 64 rows x 64 columns, as stage 1) instead of block_m x
-// 128: half the LDS reads per MFMA, and a 128-row block's empty second half
-// exits at once. Measured on MI355X at MiMo dims: T=2048 (64-row blocks)
-// 363-367 -> 338 us, EP share T=4096 97-99 -> 90-91 us, T=8192 950 -> 943 us,
-// T=4096 neutral (571 us); MXFP4 weights 924-931 -> 995-997 us at T=8192, so
-// they keep the narrow tile. AITER_AMD_PF_WIDE2 = 0 / 1 forces it.
-static bool pick_wide2(int64_t hidden, bool w4) {
+// Stage 2 as 64-row x 256-column workgroups (two per 128-row sorted block;
+// each wave 64 rows x 64 columns, as stage 1) instead of block_m x 128: half
+// the LDS reads per MFMA, and a 128-row block's empty second half exits at
+// once. Measured on MI355X at MiMo dims, FP8: T=2048 (64-row blocks) 363-367
+// -> 338 us, EP share T=4096 97-99 -> 90-91 us, T=8192 950 -> 943 us, T=4096
+// neutral (571 us); MXFP4 (with the e8m0 bytes loaded a group of K steps at
+// a time): T=8192 (128-row blocks) 820 -> 767 us. AITER_AMD_PF_WIDE2 = 0 / 1
+// forces it.
+static bool pick_wide2(int64_t hidden) {
     if (hidden % 256 != 0) return false;
     if (const char* env = getenv("AITER_AMD_PF_WIDE2")) return atoi(env) != 0;
-    return !w4;
+    return true;
 }
 
 // Column tiles per workgroup. Walking two amortises a tile's setup chain
@@ -925,7 +977,7 @@ void launch_moe_stage2_prefill(const uint8_t* a2, const float* a2_scale, const u
     g.topk = (int)topk;
     g.E = (int)E;
     g.a_rows = a_rows;
-    const bool wide = pf::pick_wide2(hidden, w2_scale_e8m0 != nullptr);
+    const bool wide = pf::pick_wide2(hidden);
     const int rows = wide ? 64 : (int)block_m;
     g.n_tiles = (int)(hidden / (wide ? 256 : 128));
     g.block_m = (int)block_m;

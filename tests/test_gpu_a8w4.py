@@ -75,23 +75,27 @@ def test_a8w4_config_a(cuda_device, shuffle, bm):
 
 
 @pytest.mark.parametrize("bm", [16, 64, 128])
-def test_a8w4_doweight_stage1(cuda_device, bm):
-    """doweight_stage1 on the A8W4 layer: the stream (bm 16) and direct-to-LDS
-    (bm 64/128) stage-1 kernels, stage 2 unweighted (the prefill kernel's
-    per-pair rows at bm 128)."""
-    cfg = _a8w4(W.CONFIG_A)
+@pytest.mark.parametrize("T", [64, 512])
+def test_a8w4_doweight_stage1(cuda_device, bm, T):
+    """doweight_stage1 on the A8W4 layer: the stream (bm 16) and, at bm
+    64/128, the direct-to-LDS (T=64, 16 routed rows per expert) or prefill
+    (T=512, 128) stage-1 kernels; stage 2 unweighted (per-pair rows on the
+    prefill kernel)."""
+    cfg = dataclasses.replace(_a8w4(W.CONFIG_A), tokens=T)
     dev, ref = _make_layer(cfg, cuda_device, True, doweight=True)
     out = _run(dev, block_size_M=bm, doweight_stage1=True)
-    _check(ref["out"], _np(out.float()), f"A8W4 doweight_stage1 bm={bm}")
+    _check(ref["out"], _np(out.float()), f"A8W4 doweight_stage1 T={T} bm={bm}")
 
 
 @pytest.mark.parametrize("bm", [16, 128])
-def test_a8w4_gelu(cuda_device, bm):
-    """ActivationType.Gelu on the A8W4 stage-1 kernels (stream at bm 16,
-    direct-to-LDS at bm 128). Here one a2 value sits on an fp8 requant tie
-    whose one-step flip moves a small output 3% (normalised) from the
-    oracle's, so the check is split at the stage boundary."""
-    cfg = _a8w4(W.CONFIG_A)
+@pytest.mark.parametrize("T", [64, 512])
+def test_a8w4_gelu(cuda_device, bm, T):
+    """ActivationType.Gelu on the A8W4 stage-1 kernels (stream at bm 16; at
+    bm 128 direct-to-LDS at T=64, prefill at T=512). At T=64 one a2 value
+    sits on an fp8 requant tie whose one-step flip moves a small output 3%
+    (normalised) from the oracle's, so the check is split at the stage
+    boundary."""
+    cfg = dataclasses.replace(_a8w4(W.CONFIG_A), tokens=T)
     dev, ref = _make_layer(cfg, cuda_device, True, activation="gelu")
     out = _run(dev, block_size_M=bm, activation=A.ActivationType.Gelu)
     _fullshape.stagewise_vs_oracle(cfg, dev, ref, _np(out.float()), bm, A.ActivationType.Gelu)
@@ -115,11 +119,15 @@ def test_a8w4_torch_dtypes_match_byte_views(cuda_device):
 
 
 @pytest.mark.parametrize("bm", [64, 128])
-def test_a8w4_prefill_shape(cuda_device, bm):
-    """Large M-blocks (the direct-to-LDS kernels) with K > 1 pipeline depth."""
-    cfg = W.MoEConfig("a8w4_prefill", 512, 1024, 512, 8, 2, seed=11, weights="mxfp4")
+@pytest.mark.parametrize("T", [512, 96])
+def test_a8w4_prefill_shape(cuda_device, bm, T):
+    """Large M-blocks with K > 1 pipeline depth: at T=512 the experts average
+    128 routed rows (the prefill kernels, e8m0 bytes a group of K steps per
+    load), at T=96 24 (the direct-to-LDS kernels; stage 2 at 128 rows the
+    prefill kernel)."""
+    cfg = W.MoEConfig("a8w4_prefill", T, 1024, 512, 8, 2, seed=11, weights="mxfp4")
     dev, ref = _make_layer(cfg, cuda_device, True)
-    _check(ref["out"], _np(_run(dev, block_size_M=bm).float()), f"A8W4 T=512 bm={bm}")
+    _check(ref["out"], _np(_run(dev, block_size_M=bm).float()), f"A8W4 T={T} bm={bm}")
 
 
 def test_a8w4_fp8_input_path(cuda_device):
@@ -184,10 +192,12 @@ def test_a8w4_num_local_tokens(cuda_device):
     _check(ref["out"][:50], _np(out.float())[:50], "A8W4 num_local_tokens")
 
 
-@pytest.mark.parametrize("T,block_ms", [(1024, (64, 128)), (8192, (128,))])
+@pytest.mark.parametrize("T,block_ms", [(512, (64,)), (1024, (64, 128)), (8192, (128,))])
 def test_a8w4_mimo_stagewise(cuda_device, T, block_ms):
     """Full MiMo dims for the A8W4 mid-size and prefill configs, checked per
-    stage (64 is the direct-to-LDS kernels, 128 the prefill stage 2)."""
+    stage. From T=1024 (32 routed rows per expert on average) both stages run
+    on the prefill kernels; T=512 at 64-row blocks runs the direct-to-LDS
+    kernels."""
     _fullshape.stagewise_check(W.mimo_a8w4(T), cuda_device, block_ms)
 
 
