@@ -78,6 +78,7 @@ struct Args {
     int msplit;                // XCD groups along M (1, 2, 4 or 8; see the tile order)
     int mrot;                  // stagger the M walk of the XCDs in a group
     int pad_skip;              // run tiles of few routed rows on a body without their padding MFMAs
+    int e8_lds;                // A8W4: the tile's e8m0 bytes in LDS where they fit
 };
 
 // Slot of a row's 16-byte A piece in LDS: piece p of row r sits at slot
@@ -155,13 +156,22 @@ __device__ __forceinline__ void scale_store(const ScaleRegs<W4, NJ>& sr, float* 
 // Waves along M (template kWM): 1 -> every wave owns all BM rows; 2 -> 2 x 2
 // waves of BM/2 rows (the two M-waves load the same weight fragments).
 
+// A8W4 with the tile's e8m0 bytes in LDS: the largest K/32 the LDS rows hold
+// (two workgroups per CU still fit), and the row pitch: 16-byte aligned, and
+// 16 consecutive rows put a step's dword in 16 distinct banks.
+template <int STAGE, int BM>
+constexpr int e8_max_ks() { return STAGE == 2 && BM == 128 ? 64 : 128; }
+template <int STAGE, int BM>
+constexpr int e8_pitch() { return e8_max_ks<STAGE, BM>() + 16; }
+
 // One K step of a wave's B operand (NCT 16-row weight groups).
 template <bool W4, int NCT>
 struct BStep {
     v4i b[NCT][W4 ? 1 : 2];
 };
 
-template <int BM, int STAGE, bool SHUFFLED, bool W4, int D, int kWM, int NW2 = 128>
+template <int BM, int STAGE, bool SHUFFLED, bool W4, int D, int kWM, int NW2 = 128,
+          bool E8L = false>
 __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
     constexpr int WN = kWaves / kWM;                     // waves along N
     // 16-row weight groups per wave: stage 1 256 weight rows (128 gate + the
@@ -192,6 +202,10 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
     __shared__ int64_t s_orow[BM];
     __shared__ float s_w[BM];
     __shared__ float s_amax[WN][BM];
+    // A8W4 (E8L): the e8m0 bytes of the tile's NW weight rows over the whole K
+    // range, loaded once per tile; row r at r * E8P
+    constexpr int E8P = e8_pitch<STAGE, BM>();
+    __shared__ __attribute__((aligned(16))) uint8_t s_e8[E8L ? NW * E8P : 16];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -308,6 +322,43 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
                                 : (uint32_t)((row0 + lr) * K + lq * 32);
         bsoff[ct] = (uint32_t)((row0 + lr) * KS);
     }
+    // E8L: the lane's e8m0 byte of step kb sits at s_e8[e8o[ct] + 4 kb]; the
+    // tile's weight row r is stage 1's gate row n0 + r (r < 128) or up row
+    // inter + n0 + r - 128, stage 2's row n0 + r
+    int e8o[NCT];
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) {
+        const int lrow = STAGE == 1 ? (ct < NCT / 2 ? 16 * (wn * (NCT / 2) + ct)
+                                                    : 128 + 16 * (wn * (NCT / 2) + ct - NCT / 2))
+                                    : 16 * (wn * NCT + ct);
+        e8o[ct] = (lrow + lr) * E8P + lq;
+    }
+    constexpr int kE8Pieces = E8L ? NW * e8_max_ks<STAGE, BM>() / 16 / kThreads : 1;
+    v4i e8r[kE8Pieces];
+    const int e8_ppr = KS / 16;                          // 16-byte pieces per weight row
+    auto e8_load = [&]() __attribute__((always_inline)) {
+        if constexpr (E8L) {
+#pragma unroll
+            for (int j = 0; j < kE8Pieces; ++j) {
+                const int q = tid + j * kThreads;
+                const int r = q / e8_ppr, c = q - (q / e8_ppr) * e8_ppr;
+                const int grow = STAGE == 1 ? (r < 128 ? n0 + r : g.inter + n0 + r - 128) : n0 + r;
+                if (r < NW)
+                    e8r[j] = __builtin_amdgcn_raw_buffer_load_b128(rbs, (uint32_t)(grow * KS + c * 16),
+                                                                   0, 0);
+            }
+        }
+    };
+    auto e8_store = [&]() __attribute__((always_inline)) {
+        if constexpr (E8L) {
+#pragma unroll
+            for (int j = 0; j < kE8Pieces; ++j) {
+                const int q = tid + j * kThreads;
+                const int r = q / e8_ppr, c = q - (q / e8_ppr) * e8_ppr;
+                if (r < NW) *reinterpret_cast<v4i*>(&s_e8[r * E8P + c * 16]) = e8r[j];
+            }
+        }
+    };
     constexpr int BSTEP = W4 ? (SHUFFLED ? 1024 : 64) : (SHUFFLED ? 2048 : 128);
     constexpr int BHI = SHUFFLED ? 256 : 16;
 
@@ -332,7 +383,7 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
     // at T=8192 with no scale loads at all, 1806 -> 1189 us.
     int sg_cur[NCT][D], sg_nxt[NCT][D];
     auto load_sg = [&](int (&dst)[NCT][D], int kb, int jt) __attribute__((always_inline)) {
-        if constexpr (W4) {
+        if constexpr (W4 && !E8L) {
             const int sso = __builtin_amdgcn_readfirstlane(kb * 4 + jt * (TROWS * KS));
 #pragma unroll
             for (int ct = 0; ct < NCT; ++ct) {
@@ -382,7 +433,8 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
         // A8W4: this step's e8m0 byte of the lane's weight row in byte 0
         int bsc[NCT];
 #pragma unroll
-        for (int ct = 0; ct < NCT; ++ct) bsc[ct] = W4 ? sg_cur[ct][d] >> (8 * lq) : 0;
+        for (int ct = 0; ct < NCT; ++ct)
+            bsc[ct] = !W4 ? 0 : E8L ? (int)s_e8[e8o[ct] + 4 * st] : sg_cur[ct][d] >> (8 * lq);
         const uint8_t* sa_src = &s_a[stage][0];
         // the lane's 32 K bytes of row tile rt: fp8 x fp8 pieces 2 lq, 2 lq + 1
         // (K 32 lq ..); fp8 x fp4 pieces lq, lq + 4 (K 16 lq .. and 64 + 16 lq ..)
@@ -495,6 +547,7 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
         ScaleRegs<W4, NJ> sr;
         scale_load<BM, NH, W4, NJ, STAGE == 1 ? 1 : NW / 128>(sr, sr_a, g.sa_kb, sr_w0, sr_w1, KB,
                                                              KBT, sr_q);
+        e8_load();
         // the e8m0 group of steps 0 .. D-1 follows the load of B step 0, as
         // the loop's group loads follow its step-0 B load
 #pragma unroll
@@ -513,6 +566,7 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
             if (D == 2) load_sg(sg_cur, 0, 0);
         }
         scale_store<BM, NH, W4, NJ>(sr, s_sc, KBT, sr_r, sr_q, sr_arow >= 0);
+        e8_store();
         store_a(0);                                             // step -1
         load_a(0, last(2));
         load_b(bbuf[D - 1], last(D - 1), 0);
@@ -720,7 +774,7 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
                 // operand sets would all be live at once)
                 __builtin_amdgcn_sched_barrier(0);
             }
-            if constexpr (W4) {
+            if constexpr (W4 && !E8L) {
 #pragma unroll
                 for (int ct = 0; ct < NCT; ++ct)
 #pragma unroll
@@ -765,8 +819,8 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
         body(IntC<NRT>{});
 }
 
-template <int BM, int STAGE, bool SHUFFLED, bool W4, int NW2 = 128>
-static void launch_depth(int KB, int grid, const Args& a, hipStream_t s) {
+template <int BM, int STAGE, bool SHUFFLED, bool W4, int NW2, bool E8L>
+static void launch_e8(int KB, int grid, const Args& a, hipStream_t s) {
     // 1 x 4 waves: stage 1 64 rows x 64 weight rows per wave, B two steps
     // ahead; stage 2 BM rows x NW2/4 columns, B four steps ahead at 32
     // columns (measured on MI355X against 2 x 2 waves for stage 2: 1230 vs
@@ -774,14 +828,34 @@ static void launch_depth(int KB, int grid, const Args& a, hipStream_t s) {
     constexpr int WM = 1;
     constexpr int DM = STAGE == 1 || NW2 > 128 ? 2 : 4;
     if (DM >= 4 && KB % 4 == 0)
-        hipLaunchKernelGGL((moe_gemm_prefill_kernel<BM, STAGE, SHUFFLED, W4, DM >= 4 ? 4 : 2, WM, NW2>),
+        hipLaunchKernelGGL((moe_gemm_prefill_kernel<BM, STAGE, SHUFFLED, W4, DM >= 4 ? 4 : 2, WM,
+                                                    NW2, E8L>),
                            dim3(grid), dim3(kThreads), 0, s, a);
     else if (KB % 2 == 0)
-        hipLaunchKernelGGL((moe_gemm_prefill_kernel<BM, STAGE, SHUFFLED, W4, 2, WM, NW2>), dim3(grid),
-                           dim3(kThreads), 0, s, a);
+        hipLaunchKernelGGL((moe_gemm_prefill_kernel<BM, STAGE, SHUFFLED, W4, 2, WM, NW2, E8L>),
+                           dim3(grid), dim3(kThreads), 0, s, a);
     else
-        hipLaunchKernelGGL((moe_gemm_prefill_kernel<BM, STAGE, SHUFFLED, W4, 1, WM, NW2>), dim3(grid),
-                           dim3(kThreads), 0, s, a);
+        hipLaunchKernelGGL((moe_gemm_prefill_kernel<BM, STAGE, SHUFFLED, W4, 1, WM, NW2, E8L>),
+                           dim3(grid), dim3(kThreads), 0, s, a);
+}
+
+// A8W4: the tile's e8m0 bytes go into LDS once per tile when they fit (K/32
+// a multiple of 16 up to e8_max_ks) and the workgroup walks one column tile;
+// otherwise each wave loads them a group of D K steps at a time (each such
+// load still touches 16 weight rows' cache lines). Measured on MI355X at MiMo
+// dims, stage 1: T=8192 1491-1497 -> 1277-1281 us, T=4096 876 -> 747 us,
+// T=2048 586 -> 499 us, T=1024 495 -> 452 us. AITER_AMD_PF_E8LDS = 0 forces
+// the grouped loads.
+template <int BM, int STAGE, bool SHUFFLED, bool W4, int NW2 = 128>
+static void launch_depth(int KB, int grid, const Args& a, hipStream_t s) {
+    if constexpr (W4) {
+        const int ks = KB * 4;
+        if (a.ntw == 1 && ks % 16 == 0 && ks <= e8_max_ks<STAGE, BM>() && a.e8_lds) {
+            launch_e8<BM, STAGE, SHUFFLED, W4, NW2, true>(KB, grid, a, s);
+            return;
+        }
+    }
+    launch_e8<BM, STAGE, SHUFFLED, W4, NW2, false>(KB, grid, a, s);
 }
 
 // Rows per workgroup: stage 1 always 64 (a 128-row sorted block is two
@@ -877,6 +951,11 @@ static int pick_pad_skip() {
     return 1;
 }
 
+static int pick_e8_lds() {
+    if (const char* env = getenv("AITER_AMD_PF_E8LDS")) return atoi(env) != 0;
+    return 1;
+}
+
 static int pick_mrot(int stage) {
     if (const char* env = getenv(stage == 1 ? "AITER_AMD_PF_MROT1" : "AITER_AMD_PF_MROT2"))
         return atoi(env) != 0;
@@ -942,6 +1021,7 @@ void launch_moe_stage1_prefill(const uint8_t* a, const float* a_scale, int64_t s
     g.ntw = pf::pick_ntw(1, g.n_tiles, (int)(K / 128), a_rows * topk, 64);
     g.msplit = pf::pick_msplit(1, g.n_tiles / g.ntw);
     g.mrot = pf::pick_mrot(1);
+    g.e8_lds = pf::pick_e8_lds();
     g.pad_skip = pf::pick_pad_skip();
     const int64_t grid = xcd_grid(g.n_tiles / g.ntw, g.m_tiles, g.msplit);
     if (grid == 0) return;
@@ -985,6 +1065,7 @@ void launch_moe_stage2_prefill(const uint8_t* a2, const float* a2_scale, const u
     g.ntw = pf::pick_ntw(2, g.n_tiles, (int)(inter / 128), est_pairs, rows, wide);
     g.msplit = pf::pick_msplit(2, g.n_tiles / g.ntw);
     g.mrot = pf::pick_mrot(2);
+    g.e8_lds = pf::pick_e8_lds();
     g.pad_skip = pf::pick_pad_skip();
     const int64_t grid = xcd_grid(g.n_tiles / g.ntw, g.m_tiles, g.msplit);
     if (grid == 0) return;
