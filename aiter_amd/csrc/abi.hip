@@ -118,23 +118,29 @@ struct WScale {
 // Kernel choice per shape (measured on MI355X): 16/32-row M-blocks
 // (decode-sized layers) take the register-streaming kernels; 64/128-row
 // M-blocks take, for FP8 weights, the register-B prefill kernels and, for
-// MXFP4 weights, the same kernels once the experts average 32 routed rows
-// (below that the direct-to-LDS kernels, and stage 2 at 128 rows always the
+// MXFP4 weights, the same kernels once the experts average enough routed rows
+// (below that the direct-to-LDS kernels; stage 2 at 128 rows always takes the
 // prefill kernel).  Stage 2 of all of them needs 256-column output tiles
 // (model_dim % 256 == 0); other shapes take the general kernels of
 // moe_gemm_fp8bs.hip.
 // sw: sorted routing weights for doweight_stage1 (applied to gate and up
 // before the activation), or NULL; act: kActSilu or kActGelu.
-// MXFP4 weights take the prefill kernels (weights in registers, their e8m0
-// bytes one load per few K steps) once the experts average at least 32 routed
-// rows, and the direct-to-LDS MXFP4 kernels below that, whose waves skip
-// padding-only 32-row halves. Measured on MI355X at MiMo dims (bm 64; stage
-// 1 / stage 2 / layer): T=2048 664 -> 581 us / 367 -> 288 us / 1.039 -> 0.966
-// ms, T=1024 501 -> 498 / 258 -> 244 / 0.792 -> 0.784 ms; T=8192 (bm 128)
-// layer 2.74 -> 2.40 ms; T=512 (16 rows per expert) stage 1 453 vs 486 us on
-// the prefill kernel.
-constexpr int64_t kW4PrefillRows = 32;
-static bool w4_on_prefill(int64_t pairs, int64_t E) { return pairs >= kW4PrefillRows * E; }
+// MXFP4 weights take the prefill kernels (weights in registers, the tile's
+// e8m0 bytes in LDS) once the experts average at least 16 routed rows for
+// stage 1 and 48 for stage 2, and the direct-to-LDS MXFP4 kernels below
+// (their waves skip padding-only 32-row halves, and their stage 2 adds into
+// an fp32 accumulator instead of writing per-pair rows that a second pass
+// sums). Measured on MI355X at MiMo dims, bm 64, prefill vs MXFP4 kernel:
+// stage 1 T=512 (16 rows per expert) 443-449 vs 452-454 us, T=2048 499 vs
+// 664 us; stage 2 with its finishing pass T=1024 (32 rows) 274 vs 266 us,
+// T=2048 316 vs 379 us. AITER_AMD_W4_PF_ROWS1 / _2 override the thresholds
+// (tests use them).
+static bool w4_on_prefill(int64_t pairs, int64_t E, int stage) {
+    int64_t rows = stage == 1 ? 16 : 48;
+    if (const char* env = getenv(stage == 1 ? "AITER_AMD_W4_PF_ROWS1" : "AITER_AMD_W4_PF_ROWS2"))
+        rows = atoll(env);
+    return pairs >= rows * E;
+}
 
 static void stage1_dispatch(const uint8_t* a, const float* sa, int64_t sa_row, int64_t sa_kb,
                             const uint8_t* w1, WScale w1s, const int32_t* sid,
@@ -148,7 +154,7 @@ static void stage1_dispatch(const uint8_t* a, const float* sa, int64_t sa_row, i
                                  a2s, a_rows, K, I, E, topk, bm, mblocks, sh, s, sw, act, ksplit,
                                  kpart, kcnt, kmb);
     else if (prefill_supported(bm, K) &&
-             (!w1s.e8m0 || w4_on_prefill(est_pairs < 0 ? a_rows * topk : est_pairs, E)) &&
+             (!w1s.e8m0 || w4_on_prefill(est_pairs < 0 ? a_rows * topk : est_pairs, E, 1)) &&
              a_fits32(a_rows, K))
         launch_moe_stage1_prefill(a, sa, sa_row, sa_kb, w1, w1s.f32, w1s.e8m0, sid, seid, nv, a2,
                                   a2s, a_rows, K, I, E, topk, bm, mblocks, sh, s, sw, act);
@@ -167,7 +173,7 @@ static bool stage2_on_prefill(int64_t bm, int64_t I, int64_t H, WScale w2s, int6
     return !(stream_supported(bm, I) && H % 256 == 0) && prefill_supported(bm, I) &&
            a_fits32(a_rows, I) &&
            H % 256 == 0 &&
-           (!w2s.e8m0 || bm == 128 || w4_on_prefill(est_pairs < 0 ? a_rows : est_pairs, E));
+           (!w2s.e8m0 || bm == 128 || w4_on_prefill(est_pairs < 0 ? a_rows : est_pairs, E, 2));
 }
 
 // acc: [tokens, H] accumulated atomically, fp32 or (the reference's moe_buf)

@@ -75,12 +75,11 @@ def test_a8w4_config_a(cuda_device, shuffle, bm):
 
 
 @pytest.mark.parametrize("bm", [16, 64, 128])
-@pytest.mark.parametrize("T", [64, 512])
+@pytest.mark.parametrize("T", [32, 512])
 def test_a8w4_doweight_stage1(cuda_device, bm, T):
     """doweight_stage1 on the A8W4 layer: the stream (bm 16) and, at bm
-    64/128, the direct-to-LDS (T=64, 16 routed rows per expert) or prefill
-    (T=512, 128) stage-1 kernels; stage 2 unweighted (per-pair rows on the
-    prefill kernel)."""
+    64/128, the direct-to-LDS (T=32, 8 routed rows per expert) or prefill
+    (T=512, 128) stage-1 kernels; stage 2 unweighted."""
     cfg = dataclasses.replace(_a8w4(W.CONFIG_A), tokens=T)
     dev, ref = _make_layer(cfg, cuda_device, True, doweight=True)
     out = _run(dev, block_size_M=bm, doweight_stage1=True)
@@ -88,12 +87,12 @@ def test_a8w4_doweight_stage1(cuda_device, bm, T):
 
 
 @pytest.mark.parametrize("bm", [16, 128])
-@pytest.mark.parametrize("T", [64, 512])
+@pytest.mark.parametrize("T", [32, 64, 512])
 def test_a8w4_gelu(cuda_device, bm, T):
     """ActivationType.Gelu on the A8W4 stage-1 kernels (stream at bm 16; at
-    bm 128 direct-to-LDS at T=64, prefill at T=512). At T=64 one a2 value
-    sits on an fp8 requant tie whose one-step flip moves a small output 3%
-    (normalised) from the oracle's, so the check is split at the stage
+    bm 128 direct-to-LDS at T=32, prefill at T=64 and 512). At T=64 one a2
+    value sits on an fp8 requant tie whose one-step flip moves a small output
+    3% (normalised) from the oracle's, so the check is split at the stage
     boundary."""
     cfg = dataclasses.replace(_a8w4(W.CONFIG_A), tokens=T)
     dev, ref = _make_layer(cfg, cuda_device, True, activation="gelu")
@@ -119,12 +118,13 @@ def test_a8w4_torch_dtypes_match_byte_views(cuda_device):
 
 
 @pytest.mark.parametrize("bm", [64, 128])
-@pytest.mark.parametrize("T", [512, 96])
+@pytest.mark.parametrize("T", [512, 96, 48])
 def test_a8w4_prefill_shape(cuda_device, bm, T):
-    """Large M-blocks with K > 1 pipeline depth: at T=512 the experts average
-    128 routed rows (the prefill kernels, e8m0 bytes a group of K steps per
-    load), at T=96 24 (the direct-to-LDS kernels; stage 2 at 128 rows the
-    prefill kernel)."""
+    """Large M-blocks with K > 1 pipeline depth. The experts average 128
+    routed rows at T=512 (both stages on the prefill kernels, the tile's
+    e8m0 bytes in LDS), 24 at T=96 (stage 1 prefill, stage 2 direct-to-LDS
+    at 64 rows) and 12 at T=48 (both direct-to-LDS at 64 rows); stage 2 at
+    128 rows is always the prefill kernel."""
     cfg = W.MoEConfig("a8w4_prefill", T, 1024, 512, 8, 2, seed=11, weights="mxfp4")
     dev, ref = _make_layer(cfg, cuda_device, True)
     _check(ref["out"], _np(_run(dev, block_size_M=bm).float()), f"A8W4 T={T} bm={bm}")
@@ -192,12 +192,14 @@ def test_a8w4_num_local_tokens(cuda_device):
     _check(ref["out"][:50], _np(out.float())[:50], "A8W4 num_local_tokens")
 
 
-@pytest.mark.parametrize("T,block_ms", [(512, (64,)), (1024, (64, 128)), (8192, (128,))])
+@pytest.mark.parametrize("T,block_ms", [(256, (64,)), (1024, (64, 128)), (2048, (64,)),
+                                        (8192, (128,))])
 def test_a8w4_mimo_stagewise(cuda_device, T, block_ms):
     """Full MiMo dims for the A8W4 mid-size and prefill configs, checked per
-    stage. From T=1024 (32 routed rows per expert on average) both stages run
-    on the prefill kernels; T=512 at 64-row blocks runs the direct-to-LDS
-    kernels."""
+    stage. At 64-row blocks stage 1 runs on the prefill kernel from 16 routed
+    rows per expert on average (T=512) and stage 2 from 48 (T=2048); T=256
+    runs both on the direct-to-LDS kernels; 128-row blocks run stage 2 on the
+    prefill kernel."""
     _fullshape.stagewise_check(W.mimo_a8w4(T), cuda_device, block_ms)
 
 

@@ -471,7 +471,7 @@ def test_prefill_column_walk_bit_exact(cuda_device, monkeypatch, weights, bm, nt
 
 @pytest.mark.parametrize("weights,bm,T", [("fp8", 64, 300), ("fp8", 128, 300),
                                          ("mxfp4", 64, 300), ("mxfp4", 128, 300),
-                                         ("mxfp4", 64, 100), ("mxfp4", 128, 100)])
+                                         ("mxfp4", 64, 50), ("mxfp4", 128, 50)])
 @pytest.mark.parametrize("order", [(2, 1, 2, 0, 1), (4, 0, 4, 1, 2), (8, 1, 1, 1, 1),
                                    (1, 1, 8, 0, 2)])
 def test_prefill_xcd_order_bit_exact(cuda_device, monkeypatch, weights, bm, T, order):
@@ -482,7 +482,7 @@ def test_prefill_xcd_order_bit_exact(cuda_device, monkeypatch, weights, bm, T, o
     order's (one group, no stagger). order = (groups 1, stagger 1, groups 2,
     stagger 2, stage-2 column walk); the walk of 2 leaves the prefill stage 2
     with 8 column groups instead of 16. MXFP4 at T=300 (75 routed rows per
-    expert) runs on the prefill kernels, at T=100 (25) on v2, whose stage 2
+    expert) runs on the prefill kernels, at T=50 (12.5) on v2, whose stage 2
     (at 64 rows) accumulates with fp32 atomics: their order differs between
     runs at top-4, so there the two outputs are compared at the layer bar
     instead (the plain order itself is checked against the oracle by the A8W4
@@ -515,7 +515,7 @@ def test_prefill_xcd_order_bit_exact(cuda_device, monkeypatch, weights, bm, T, o
     if a21 is not None:
         assert torch.equal(a21[0], a2c[0]) and torch.equal(a21[1], a2c[1])
     assert torch.count_nonzero(out1).item() > 0
-    if weights == "mxfp4" and bm == 64 and T * cfg.topk < 32 * cfg.experts:
+    if weights == "mxfp4" and bm == 64 and T * cfg.topk < 48 * cfg.experts:
         _check(_np(out1.float()), _np(outc.float()), f"xcd order {order} vs plain")
     else:
         assert torch.equal(out1, outc), (out1.float() - outc.float()).abs().max().item()
