@@ -192,6 +192,30 @@ def test_a8w4_num_local_tokens(cuda_device):
     _check(ref["out"][:50], _np(out.float())[:50], "A8W4 num_local_tokens")
 
 
+@pytest.mark.parametrize("bm", [64, 128])
+def test_a8w4_e8m0_lds_bit_exact(cuda_device, monkeypatch, bm):
+    """On the prefill kernels the tile's e8m0 bytes are staged in LDS once per
+    tile (AITER_AMD_PF_E8LDS = 0 loads them a group of K steps at a time
+    instead); both feed the same byte to every MFMA, so the layer outputs are
+    bitwise equal. 150 routed rows per expert put both stages on the prefill
+    kernels."""
+    cfg = W.MoEConfig("e8lds", 600, 2048, 1024, 16, 4, seed=31, weights="mxfp4")
+    wts = W.make_weights(cfg, device=cuda_device, shuffle=True)
+    x = W.make_hidden(cfg, device=cuda_device)
+    tw, ids = W.make_routing(cfg, device=cuda_device)
+
+    def layer(e8):
+        monkeypatch.setenv("AITER_AMD_PF_E8LDS", str(e8))
+        out = W.run_layer("mxfp4", x, wts["w1"], wts["w2"], tw, ids, w1_scale=wts["w1_scale"],
+                          w2_scale=wts["w2_scale"], block_size_M=bm)
+        torch.cuda.synchronize()
+        return out
+
+    out0, out1 = layer(0), layer(1)
+    assert torch.count_nonzero(out1).item() > 0
+    assert torch.equal(out0, out1), (out0.float() - out1.float()).abs().max().item()
+
+
 @pytest.mark.parametrize("T,block_ms", [(256, (64,)), (1024, (64, 128)), (2048, (64,)),
                                         (8192, (128,))])
 def test_a8w4_mimo_stagewise(cuda_device, T, block_ms):
