@@ -29,7 +29,7 @@ _SIGNATURES = {
     "aiter_amd_get_last_error": (ctypes.c_char_p, []),
     "aiter_amd_clear_last_error": (None, []),
     "aiter_amd_moe_sorting_workspace_bytes": (c_i64, [c_i64, c_i64, c_i64]),
-    "aiter_amd_default_block_m": (c_i64, [c_i64, c_i64, c_i64, c_i64, c_i64]),
+    "aiter_amd_default_block_m": (c_i64, [c_i64, c_i64, c_i64, c_i64, c_i64, c_i64]),
     "aiter_amd_layer_timing_begin": (c_int, [c_i64]),
     "aiter_amd_layer_timing_end": (c_i64, [c_vp, c_i64]),
     "aiter_amd_topk_softmax": (

@@ -329,16 +329,24 @@ bool use_fused_layer(int64_t tokens, int64_t topk, int64_t bm, int64_t H, int64_
     return env && atoi(env) != 0;
 }
 
-int64_t default_block_m(int64_t tokens, int64_t topk, int64_t E, int64_t model_dim,
+// E: the experts this GPU holds; G: the experts the router spreads the
+// tokens over (an expert-parallel share's global count; E otherwise).
+int64_t default_block_m(int64_t tokens, int64_t topk, int64_t E, int64_t G, int64_t model_dim,
                         int64_t inter_dim) {
     // measured on MI355X (MiMo shape, FP8 and A8W4): 16-row blocks while experts
     // average <= 8 rows, 32 up to ~20, then 64; 128-row tiles halve the weight
-    // re-reads once experts average >= 64 rows
-    const int64_t avg = E > 0 ? tokens * topk / E : 0;
+    // re-reads once experts average >= 64 rows, and pay once stage 1 is at least
+    // 16 rounds of 64-row workgroups (pairs * inter_dim >= 2^26: T=4096 at
+    // MiMo dims). A share of a few rounds loses more to its last partial round:
+    // the 32-of-256 EP share ran 64-row blocks 3.6-5.5% faster at T=2048..8192,
+    // and T=2048 of the full layer 1.5% faster.
+    if (G <= 0) G = E;
+    const int64_t avg = G > 0 ? tokens * topk / G : 0;
     if (avg <= 8) return 16;
     if (avg <= 20) return 32;
-    if (avg >= 64 && v2_supported(128, model_dim) && v2_supported(128, inter_dim) &&
-        model_dim % 256 == 0 && a_fits32(tokens, model_dim) &&
+    const int64_t pairs = G > 0 ? tokens * topk * E / G : 0;
+    if (avg >= 64 && pairs * inter_dim >= (int64_t(1) << 26) && v2_supported(128, model_dim) &&
+        v2_supported(128, inter_dim) && model_dim % 256 == 0 && a_fits32(tokens, model_dim) &&
         a_fits32(tokens * topk, inter_dim))
         return 128;
     return 64;
@@ -448,7 +456,8 @@ void fused_entry(const void* hidden_states, int hidden_dtype, const void* w1, WS
     AMD_CHECK(E_sort >= num_experts && E_sort <= kMaxExperts,
               "global_experts must be in [num_experts, 4096]");
     check_topk_experts(tokens, topk, E_sort);
-    if (block_m <= 0) block_m = default_block_m(tokens, topk, num_experts, model_dim, inter_dim);
+    if (block_m <= 0)
+        block_m = default_block_m(tokens, topk, num_experts, E_sort, model_dim, inter_dim);
     check_block_m_gemm(block_m, model_dim, inter_dim, tokens, topk);
     AMD_CHECK(!one_launch || stream_fused_supported(block_m, model_dim, inter_dim),
               "the one-launch layer needs block_m 16 or 32 and model_dim a multiple of 256 up "
@@ -625,8 +634,8 @@ int64_t aiter_amd_layer_timing_end(float* step_ms, int64_t max_calls) {
 }
 
 int64_t aiter_amd_default_block_m(int64_t tokens, int64_t topk, int64_t num_experts,
-                                  int64_t model_dim, int64_t inter_dim) {
-    return default_block_m(tokens, topk, num_experts, model_dim, inter_dim);
+                                  int64_t global_experts, int64_t model_dim, int64_t inter_dim) {
+    return default_block_m(tokens, topk, num_experts, global_experts, model_dim, inter_dim);
 }
 
 int aiter_amd_moe_sorting_fwd(const int32_t* topk_ids, const float* topk_weights, int64_t tokens,
@@ -777,8 +786,9 @@ int64_t aiter_amd_fused_moe_workspace_bytes(int64_t tokens, int64_t model_dim, i
     if (tokens < 0 || model_dim <= 0 || inter_dim <= 0 || num_experts < 1 || topk < 1 ||
         global_experts < num_experts)
         return -1;
-    // the block size the one-call entries resolve, from the local experts
-    if (block_m <= 0) block_m = default_block_m(tokens, topk, num_experts, model_dim, inter_dim);
+    // the block size the one-call entries resolve
+    if (block_m <= 0)
+        block_m = default_block_m(tokens, topk, num_experts, global_experts, model_dim, inter_dim);
     return fused_layout(tokens, model_dim, inter_dim, global_experts, num_experts, topk, block_m)
         .total;
 }
@@ -818,9 +828,9 @@ int aiter_amd_fused_moe_fp8_blockscale_noalloc(
         AMD_CHECK(E_sort >= num_experts && E_sort <= kMaxExperts,
                   "global_experts must be in [num_experts, 4096]");
         check_topk_experts(tokens, topk, E_sort);
-        const int64_t bm =
-            block_m > 0 ? block_m
-                        : default_block_m(tokens, topk, num_experts, model_dim, inter_dim);
+        const int64_t bm = block_m > 0 ? block_m
+                                       : default_block_m(tokens, topk, num_experts, E_sort,
+                                                         model_dim, inter_dim);
         check_block_m_gemm(bm, model_dim, inter_dim, tokens, topk);
         const int64_t need =
             fused_layout(tokens, model_dim, inter_dim, E_sort, num_experts, topk, bm).total;

@@ -119,9 +119,11 @@ def get_inter_dim(w1_shape, w2_shape):
 
 
 def default_block_m(tokens: int, topk: int, num_experts: int, model_dim: int = 0,
-                    inter_dim: int = 0) -> int:
-    """M-block for a layer; model_dim/inter_dim 0 rule out 128-row tiles."""
-    return _abi.query("aiter_amd_default_block_m", tokens, topk, num_experts, model_dim, inter_dim)
+                    inter_dim: int = 0, global_experts: int = 0) -> int:
+    """M-block for a layer; model_dim/inter_dim 0 rule out 128-row tiles.
+    global_experts: the expert_mask size of an expert-parallel share (0: num_experts)."""
+    return _abi.query("aiter_amd_default_block_m", tokens, topk, num_experts, global_experts,
+                      model_dim, inter_dim)
 
 
 def fused_moe(
@@ -220,13 +222,14 @@ _E8M0_DTYPES = (torch.uint8, dtypes.fp8_e8m0)
 
 
 def select_block_m(tokens: int, topk: int, num_experts: int, model_dim: int, inter_dim: int,
-                   a8w4: bool, device: torch.device) -> int:
+                   a8w4: bool, device: torch.device, global_experts: int = 0) -> int:
     """fused_moe's block_m when the caller gives none: the tuned table
     (aiter_amd/tune.py, the get_2stage_cfgs lookup of aiter/fused_moe.py:719-1100),
-    else the heuristic default_block_m."""
+    else the heuristic default_block_m (global_experts: the expert_mask size of
+    an expert-parallel share)."""
     tuned = tuned_block_m(_cu_num(device), tokens, model_dim, inter_dim, num_experts, topk,
                           "per_1x32" if a8w4 else "per_1x128", "fp4x2" if a8w4 else "fp8")
-    bm = tuned or default_block_m(tokens, topk, num_experts, model_dim, inter_dim)
+    bm = tuned or default_block_m(tokens, topk, num_experts, model_dim, inter_dim, global_experts)
     # the 128-row kernels address their activation operand with 32-bit offsets
     if bm == 128 and max(tokens * model_dim, tokens * topk * inter_dim) >= 1 << 32:
         bm = 64
@@ -421,7 +424,8 @@ def _fused_moe_impl(hidden_states, w1, w2, topk_weight, topk_ids, expert_mask, a
     if block_size_M not in (None, -1):
         block_m = int(block_size_M)
     else:
-        block_m = select_block_m(M, topk, E, model_dim, inter_dim, a8w4, topk_ids.device)
+        block_m = select_block_m(M, topk, E, model_dim, inter_dim, a8w4, topk_ids.device,
+                                 global_E)
     device = topk_ids.device
     topk_ids = topk_ids.to(torch.int32).contiguous()
     topk_weight = topk_weight.to(torch.float32).contiguous()

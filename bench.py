@@ -130,7 +130,7 @@ class Layer:
         cfg = self.cfg
         return self.block_m or A.select_block_m(
             cfg.tokens, cfg.topk, cfg.local_experts or cfg.experts, cfg.model_dim,
-            cfg.inter_dim, self.a8w4, self.dev)
+            cfg.inter_dim, self.a8w4, self.dev, cfg.experts if cfg.local_experts else 0)
 
 
 def time_steps(fn, steps, warmup):

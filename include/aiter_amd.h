@@ -320,11 +320,14 @@ int aiter_amd_layer_timing_begin(int64_t max_calls);
 int64_t aiter_amd_layer_timing_end(float* step_ms, int64_t max_calls);
 
 /* Default M-block (sorted rows per GEMM tile) for a token count: 16 / 32 / 64 by the average
- * rows per expert (<= 8, <= 20, else), 128 once experts average >= 64 rows and the dims allow
- * 128-row tiles.
+ * rows per expert, tokens * topk / global_experts (<= 8, <= 20, else); 128 once experts average
+ * >= 64 rows, the pairs this GPU holds (tokens * topk * num_experts / global_experts) times
+ * inter_dim reach 2^26, and the dims allow 128-row tiles. global_experts: the expert_mask
+ * entries of an expert-parallel share, or <= 0 (or num_experts) without one. The one-call
+ * entries and the workspace query resolve block_m <= 0 with this rule.
  * Plays the part of the block_m choice in aiter's get_2stage_cfgs (aiter/fused_moe.py:830-905). */
 int64_t aiter_amd_default_block_m(int64_t tokens, int64_t topk, int64_t num_experts,
-                                  int64_t model_dim, int64_t inter_dim);
+                                  int64_t global_experts, int64_t model_dim, int64_t inter_dim);
 
 #ifdef __cplusplus
 }

@@ -128,17 +128,18 @@ def test_fused_validation_errors(lib):
 
 
 def test_workspace_query_resolves_block_m_like_the_layer(lib):
-    """block_m = 0 resolves from the local experts in both the workspace
-    query and the one-call entries: an EP share (32 of 256 experts) at T=64,
-    top-8 picks 32 (16 rows per local expert on average, where dividing by
-    all 256 would give 16). The workspace the query reports is accepted by
-    the entry: the call gets past the size check to the pointer checks."""
+    """block_m = 0 resolves the same way in the workspace query and the
+    one-call entries, from the routed rows per expert over all the router's
+    experts: an EP share (32 of 256 experts) at T=64, top-8 averages 2 rows
+    per expert and picks 16, where the 32 local experts alone would suggest
+    16 rows and 32. The workspace the query reports is accepted by the
+    entry: the call gets past the size check to the pointer checks."""
     T, H, I, E, G, k = 64, 4096, 2048, 32, 256, 8
-    assert lib.aiter_amd_default_block_m(T, k, E, H, I) == 32
-    assert lib.aiter_amd_default_block_m(T, k, G, H, I) == 16
+    assert lib.aiter_amd_default_block_m(T, k, E, 0, H, I) == 32
+    assert lib.aiter_amd_default_block_m(T, k, E, G, H, I) == 16
     ws = lib.aiter_amd_fused_moe_workspace_bytes(T, H, I, E, G, k, 0)
-    assert ws == lib.aiter_amd_fused_moe_workspace_bytes(T, H, I, E, G, k, 32)
-    assert ws > lib.aiter_amd_fused_moe_workspace_bytes(T, H, I, E, G, k, 16)
+    assert ws == lib.aiter_amd_fused_moe_workspace_bytes(T, H, I, E, G, k, 16)
+    assert ws < lib.aiter_amd_fused_moe_workspace_bytes(T, H, I, E, G, k, 32)
     masked = [16, 3, 16, 16, 16, 16, 16, 16, 16, None, 16, 3]
     # one byte short is rejected, the reported size passes the size check and
     # stops at the (misaligned) workspace pointer
@@ -151,8 +152,8 @@ def test_workspace_query_resolves_block_m_like_the_layer(lib):
 def test_block_m_128_needs_32bit_operands(lib, monkeypatch):
     # the 128-row kernels use 32-bit buffer offsets: T*topk*inter >= 2^32 bytes
     # (T = 262144 at topk 8, inter 2048) must not pick or accept them
-    assert lib.aiter_amd_default_block_m(262143, 8, 256, 4096, 2048) == 128
-    assert lib.aiter_amd_default_block_m(262144, 8, 256, 4096, 2048) == 64
+    assert lib.aiter_amd_default_block_m(262143, 8, 256, 0, 4096, 2048) == 128
+    assert lib.aiter_amd_default_block_m(262144, 8, 256, 0, 4096, 2048) == 64
     args = [16, 16, 0, 16, 16, 16, None, 16, 16, 16, 16]
     _expect_error("aiter_amd_moe_stage1_fp8_blockscale", *args, 262144, 4096, 2048, 256, 8, 128,
                   10, 0, 1, None, match="32-bit offsets")
@@ -165,15 +166,21 @@ def test_block_m_128_needs_32bit_operands(lib, monkeypatch):
 
 
 def test_default_block_m(lib):
-    assert lib.aiter_amd_default_block_m(1, 8, 256, 4096, 2048) == 16
-    assert lib.aiter_amd_default_block_m(32, 8, 256, 4096, 2048) == 16
-    assert lib.aiter_amd_default_block_m(512, 8, 256, 4096, 2048) == 32
-    assert lib.aiter_amd_default_block_m(1024, 8, 256, 4096, 2048) == 64
-    assert lib.aiter_amd_default_block_m(2048, 8, 256, 4096, 2048) == 128
-    assert lib.aiter_amd_default_block_m(8192, 8, 256, 4096, 2048) == 128
+    assert lib.aiter_amd_default_block_m(1, 8, 256, 0, 4096, 2048) == 16
+    assert lib.aiter_amd_default_block_m(32, 8, 256, 0, 4096, 2048) == 16
+    assert lib.aiter_amd_default_block_m(512, 8, 256, 0, 4096, 2048) == 32
+    assert lib.aiter_amd_default_block_m(1024, 8, 256, 0, 4096, 2048) == 64
+    # 128-row tiles once experts average >= 64 rows and stage 1 is >= 16
+    # rounds of 64-row workgroups (pairs * inter_dim >= 2^26)
+    assert lib.aiter_amd_default_block_m(2048, 8, 256, 0, 4096, 2048) == 64
+    assert lib.aiter_amd_default_block_m(4096, 8, 256, 256, 4096, 2048) == 128
+    assert lib.aiter_amd_default_block_m(8192, 8, 256, 0, 4096, 2048) == 128
+    # an EP share (32 of 256 experts) holds an eighth of the pairs
+    assert lib.aiter_amd_default_block_m(8192, 8, 32, 256, 4096, 2048) == 64
+    assert lib.aiter_amd_default_block_m(65536, 8, 32, 256, 4096, 2048) == 128
     # 128-row tiles need model_dim % 256 == 0 and dims <= 8192
-    assert lib.aiter_amd_default_block_m(8192, 8, 256, 4224, 2048) == 64
-    assert lib.aiter_amd_default_block_m(8192, 8, 256, 0, 0) == 64
+    assert lib.aiter_amd_default_block_m(8192, 8, 256, 0, 4224, 2048) == 64
+    assert lib.aiter_amd_default_block_m(8192, 8, 256, 0, 0, 0) == 64
 
 
 def test_python_layer_rejects_unsupported_modes():
