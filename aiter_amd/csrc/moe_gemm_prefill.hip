@@ -798,8 +798,8 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
     };
     // A wave whose rows are all padding runs the body without math (it still
     // stages A and meets every barrier, as every copy does). With pad_skip, a
-    // stage-2 tile of at most NRT/4 (and, in 128-row tiles, NRT/2) active row
-    // tiles runs a copy that skips the MFMAs of the rest. Each copy adds ~20 KB
+    // stage-2 (or MXFP4 stage-1) tile of at most NRT/4 (and, in 128-row tiles,
+    // NRT/2) active row tiles runs a copy that skips the MFMAs of the rest. Each copy adds ~20 KB
     // of code (the instruction cache is shared by two CUs), so 64-row tiles
     // get one. Not in the FP8 128-row tile (FP8 takes the 64-row wide tile),
     // where the copies spill. Measured on MI355X at MiMo dims, same boxes,
@@ -807,8 +807,10 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
     // A8W4 T=8192 (128-row tiles) 960-971 -> 931-934 us. Stage 1 (a copy
     // at NRT/4) was no faster: T=8192 1540-1559 -> 1530-1538 us but T=2048
     // 574-577 -> 580-584 us and the EP share 160-162 -> 162-165 us; its small
-    // tiles are bound by their weight stream, not by their MFMAs.
-    constexpr bool kPadCopies = STAGE == 2 && NRT >= 4 && !(BM == 128 && !W4);
+    // tiles are bound by their weight stream, not by their MFMAs. MXFP4 stage 1
+    // (half the weight bytes) gains: T=8192 1264-1271 -> 1237-1238 us, T=2048
+    // and 1024 level.
+    constexpr bool kPadCopies = (STAGE == 2 || W4) && NRT >= 4 && !(BM == 128 && !W4);
     if (kWM > 1 && nact == 0)
         body(IntC<0>{});
     else if (kPadCopies && g.pad_skip && nact <= NRT / 4)
