@@ -528,10 +528,11 @@ def test_prefill_pad_skip_bit_exact(cuda_device, monkeypatch, weights, bm, T, E)
     half) of their 16-row tiles routed run a copy of the kernel body that
     skips the padding tiles' MFMAs (AITER_AMD_PF_PADSKIP = 0 runs every tile
     on the full body). Routed rows get the same MFMAs and fold order either
-    way, so the layer output is bitwise equal (and stage 1's a2, which has no
-    such copy, too). Zipf routing over 64 experts leaves most experts a
-    handful of rows, so tiles of 1-16, 17-32 and more rows all occur. MXFP4
-    runs its stage 2 (128-row tiles) on the prefill kernel at bm 128."""
+    way, so the layer output is bitwise equal (and FP8 stage 1's a2, which
+    has no such copy, too). Zipf routing over 64 experts leaves most experts
+    a handful of rows, so tiles of 1-16, 17-32 and more rows all occur. MXFP4
+    at bm 128 runs stage 2 (128-row tiles) and, from 16 routed rows per
+    expert, stage 1 (with its own copy) on the prefill kernel."""
     cfg = W.MoEConfig("padskip", T, 2048, 1024, E, 4, routing="zipf", seed=27, weights=weights)
     wts = W.make_weights(cfg, device=cuda_device, shuffle=True)
     x = W.make_hidden(cfg, device=cuda_device)
