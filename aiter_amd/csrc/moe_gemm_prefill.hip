@@ -586,39 +586,52 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
         if constexpr (STAGE == 2) {
             const int nc = n0 + jt * TROWS;
             if (g.part) {
-                // the pair's weighted row, rounded once to bf16, staged through
-                // the free A stage RPP rows at a time and stored as whole
-                // 16-byte pieces at part[pair, nc ..]
-                constexpr int RPP = A_BYTES / (NW * 2) >= BM ? BM : A_BYTES / (NW * 2);
-                static_assert(RPP % 16 == 0 && BM % RPP == 0,
-                              "a pass of bf16 rows is whole row tiles and fits one A stage");
-                uint16_t* s_p = reinterpret_cast<uint16_t*>(&s_a[stg][0]);   // [RPP][NW]
+                // the pair's weighted row, rounded once to bf16, staged in LDS
+                // RPP rows at a time and stored as whole 16-byte pieces at
+                // part[pair, nc ..]: the 256-column tile (which walks one column
+                // tile) through the scale products' buffer, whose last reader
+                // was the final K step (an FP8 tile's 64 rows in one pass; four
+                // through an A stage took T=8192 924-928 us against 917-921), the
+                // 128-column tile through the free A stage
+                auto stage_rows = [&](uint16_t* s_p, auto rpp) __attribute__((always_inline)) {
+                    constexpr int RPP = decltype(rpp)::value;
+                    static_assert(RPP % 16 == 0 && BM % RPP == 0,
+                                  "a pass of bf16 rows is whole row tiles");
 #pragma unroll
-                for (int hf = 0; hf < BM / RPP; ++hf) {
+                    for (int hf = 0; hf < BM / RPP; ++hf) {
 #pragma unroll
-                    for (int rt = 0; rt < NRT; ++rt) {
-                        if ((row_base + rt * 16) / RPP != hf) continue;
+                        for (int rt = 0; rt < NRT; ++rt) {
+                            if ((row_base + rt * 16) / RPP != hf) continue;
 #pragma unroll
-                        for (int v = 0; v < 4; ++v) {
-                            const int row = row_base + rt * 16 + 4 * lq + v;
-                            const float wgt = s_w[row];
-                            const int lrow = row - hf * RPP;
+                            for (int v = 0; v < 4; ++v) {
+                                const int row = row_base + rt * 16 + 4 * lq + v;
+                                const float wgt = s_w[row];
+                                const int lrow = row - hf * RPP;
 #pragma unroll
-                            for (int ct = 0; ct < NCT; ++ct)
-                                s_p[lrow * NW + wn * NCT * 16 + ct * 16 + lr] =
-                                    f32_to_bf16_bits(acc[rt][ct][v] * wgt);
+                                for (int ct = 0; ct < NCT; ++ct)
+                                    s_p[lrow * NW + wn * NCT * 16 + ct * 16 + lr] =
+                                        f32_to_bf16_bits(acc[rt][ct][v] * wgt);
+                            }
                         }
+                        __syncthreads();
+                        for (int q = tid; q < RPP * (NW / 8); q += kThreads) {
+                            const int lrow = q / (NW / 8), piece = q % (NW / 8);
+                            const int64_t pair = s_arow[lrow + hf * RPP];
+                            if (pair < 0) continue;
+                            *reinterpret_cast<v4i*>(g.part + pair * g.N + nc + piece * 8) =
+                                *reinterpret_cast<const v4i*>(s_p + lrow * NW + piece * 8);
+                        }
+                        __syncthreads();
                     }
-                    __syncthreads();
-                    for (int q = tid; q < RPP * (NW / 8); q += kThreads) {
-                        const int lrow = q / (NW / 8), piece = q % (NW / 8);
-                        const int64_t pair = s_arow[lrow + hf * RPP];
-                        if (pair < 0) continue;
-                        *reinterpret_cast<v4i*>(g.part + pair * g.N + nc + piece * 8) =
-                            *reinterpret_cast<const v4i*>(s_p + lrow * NW + piece * 8);
-                    }
-                    __syncthreads();
-                }
+                };
+                constexpr int SC_ROWS = (int)(sizeof(s_sc) / (NW * 2));
+                constexpr int A_ROWS = A_BYTES / (NW * 2);
+                if constexpr (NW2 > 128)
+                    stage_rows(reinterpret_cast<uint16_t*>(s_sc),
+                               IntC<(SC_ROWS >= BM ? BM : SC_ROWS)>{});
+                else
+                    stage_rows(reinterpret_cast<uint16_t*>(&s_a[stg][0]),
+                               IntC<(A_ROWS >= BM ? BM : A_ROWS)>{});
             } else {
 #pragma unroll
                 for (int rt = 0; rt < NRT; ++rt)
@@ -965,14 +978,16 @@ static int pick_mrot(int stage) {
 }
 
 static int pick_ntw(int stage, int n_tiles, int KB, int64_t pairs, int rows, bool wide = false) {
+    // the 256-column stage-2 tiles walk one (their epilogue stages the output
+    // rows in the scale products' buffer, which a next tile would still need):
+    // at two, T=8192 935-942 vs 939-944 us, T=4096 569 vs 537-540 us, T=2048
+    // 342 vs 336 us, EP share 99.7 vs 89.5-91.7 us (four: 1030 / 662 / 358 /
+    // 148 us)
+    if (stage == 2 && wide) return 1;
     if (const char* env = getenv(stage == 1 ? "AITER_AMD_PF_NTW1" : "AITER_AMD_PF_NTW2")) {
         const int c = atoi(env);
         if (c >= 1 && n_tiles % c == 0 && c * KB <= kMaxKB) return c;
     }
-    // the 256-column stage-2 tiles walk one: at two, T=8192 935-942 vs
-    // 939-944 us, T=4096 569 vs 537-540 us, T=2048 342 vs 336 us, EP share
-    // 99.7 vs 89.5-91.7 us (four: 1030 / 662 / 358 / 148 us)
-    if (wide) return 1;
     constexpr int64_t kSlots = 512;   // 256 CUs x 2 workgroups
     constexpr int64_t kMinRounds = 8;
     const int64_t wgs = (pairs + rows - 1) / rows * n_tiles;

@@ -423,11 +423,12 @@ def test_fused_moe_odd_model_dim(cuda_device, bm):
 # ------------------------------------------- full MiMo shape (prefill) ---
 @pytest.mark.parametrize("T,block_ms", [(2048, (128, 64, 32)), (8192, (128,))])
 def test_fused_moe_mimo_prefill_stagewise(cuda_device, T, block_ms):
-    """Full MiMo dims with Zipf routing (128 is the default block_m: the
-    register-B prefill kernels at K = 4096 / 2048), checked per stage."""
+    """Full MiMo dims with Zipf routing (the register-B prefill kernels at
+    K = 4096 / 2048; the default block_m is 128 at T=8192 and 64 at T=2048,
+    below 16 rounds of 64-row workgroups), checked per stage."""
     cfg = W.mimo_prefill(T)
     assert A.default_block_m(cfg.tokens, cfg.topk, cfg.experts, cfg.model_dim,
-                             cfg.inter_dim) == 128
+                             cfg.inter_dim) == (128 if T == 8192 else 64)
     _fullshape.stagewise_check(cfg, cuda_device, block_ms)
 
 
@@ -437,13 +438,15 @@ def test_prefill_column_walk_bit_exact(cuda_device, monkeypatch, weights, bm, nt
     """A prefill workgroup that walks ntw column tiles in one pipelined K loop
     (AITER_AMD_PF_NTW1/2 force the count) computes every tile as a
     one-tile workgroup does: stage 1's a2 and the layer's output (per-pair
-    rows summed in slot order) are bitwise equal. Stage 1 has 8 column tiles
-    and stage 2 16, so both the XCD order (8 column groups) and the plain
-    order are walked."""
+    rows summed in slot order) are bitwise equal. Stage 2 walks on its
+    128-column tile (AITER_AMD_PF_WIDE2=0; the 256-column tile always takes
+    one). Stage 1 has 8 column tiles and stage 2 16, so both the XCD order
+    (8 column groups) and the plain order are walked."""
     cfg = W.MoEConfig("walk", 300, 2048, 1024, 16, 4, seed=21, weights=weights)
     wts = W.make_weights(cfg, device=cuda_device, shuffle=True)
     x = W.make_hidden(cfg, device=cuda_device)
     tw, ids = W.make_routing(cfg, device=cuda_device)
+    monkeypatch.setenv("AITER_AMD_PF_WIDE2", "0")
 
     def layer(c):
         monkeypatch.setenv("AITER_AMD_PF_NTW1", str(c))
