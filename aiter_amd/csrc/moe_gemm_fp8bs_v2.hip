@@ -3,7 +3,10 @@
 //
 // Same contract as moe_gemm_fp8bs.hip (stage 1: gate+up GEMM, SiLU*up,
 // bf16 rounding and 1x128 fp8 requant; stage 2: down GEMM, routing weight,
-// f32 atomic accumulate), for M-blocks of 64 or 128 sorted rows.
+// f32 atomic accumulate), for M-blocks of 64 or 128 sorted rows. The library
+// runs it for MXFP4 layers whose experts average few routed rows (its waves
+// skip padding-only halves); the prefill kernels take FP8 and larger MXFP4
+// layers.
 //
 // Workgroup: 512 threads = 2 (M) x 4 (N) wave64s, two waves per SIMD so the
 // block-scale FMAs of one wave run beside the other wave's MFMAs; tile BM

@@ -25,9 +25,11 @@
 // of each per SIMD), so one workgroup's prologue and epilogue run under the
 // other's K loop.  Stage 1: 64 rows (half a 128-row sorted block) x 256
 // weight rows (128 gate + the matching 128 up rows = one 1x128 quant group
-// per row); stage 2: 64 rows x 256 output columns (FP8), or 128 (or 64)
-// rows x 128 columns (MXFP4).  A tile whose rows are all padding exits at
-// once, and padding rows of the others read zeros.  Tile order is XCD-aware: workgroup L
+// per row); stage 2: 64 rows x 256 output columns (or, forced, block_m rows x
+// 128 columns).  MXFP4 weights (A8W4) run the same tiles with half the weight
+// bytes per K step and the tile's e8m0 scale bytes staged in LDS.  A tile
+// whose rows are all padding exits at once, and padding rows of the others
+// read zeros.  Tile order is XCD-aware: workgroup L
 // runs on XCD L % 8; the XCDs form msplit groups along M (a contiguous range
 // of the valid M-tiles each) x 8/msplit along N (each XCD owns that many
 // column tiles of its range), so an expert's weight slice stays in one L2
