@@ -89,6 +89,18 @@ struct Args {
 // reads of a row tile and the row stores are conflict-free.
 __device__ __forceinline__ int a_swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
+// Slot order of a row's eight 16-byte A pieces before the swizzle: identity
+// for fp8 x fp8, whose lane q reads pieces 2q and 2q + 1; for fp8 x fp4,
+// whose lane q reads pieces q and q + 4, piece p goes to slot 2p (p < 4) or
+// 2(p - 4) + 1, so both read the same slots. Reading pieces q and q + 4 in
+// place conflicted in LDS: measured on MI355X, A8W4 stage 1 at T=8192 had
+// 9.2e7 bank-conflict cycles (FP8: 1.7e6); with this order 2.0e7, and stage
+// 1 took 1194-1202 instead of 1213-1215 us.
+template <bool W4>
+__device__ __forceinline__ int a_slot(int p) {
+    return W4 ? (p < 4 ? 2 * p : 2 * (p - 4) + 1) : p;
+}
+
 // Raw buffer resource over [base, base + bytes): loads take a 32-bit lane
 // offset plus a wave-uniform K-step offset, and read 0 past the end.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, int64_t bytes) {
@@ -298,7 +310,7 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
         // T=8192 layer 2.644 -> 2.624 ms, T=2048 1.030 -> 1.015 ms, EP share
         // T=4096 0.307 -> 0.303 ms (the clock is power-bound under these GEMMs)
         a_off[j] = arow >= 0 ? (uint32_t)arow * (uint32_t)K + (uint32_t)(pc * 16) : 0xFFFFF000u;
-        a_dst[j] = row * 128 + ((pc ^ a_swz(row)) << 4);
+        a_dst[j] = row * 128 + ((a_slot<W4>(pc) ^ a_swz(row)) << 4);
     }
 
     // ---- B sources of this wave's four 16-row weight groups ----
@@ -324,7 +336,8 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
                                 : (uint32_t)((row0 + lr) * K + lq * 32);
         bsoff[ct] = (uint32_t)((row0 + lr) * KS);
     }
-    // E8L: the lane's e8m0 byte of step kb sits at s_e8[e8o[ct] + 4 kb]; the
+    // E8L: the lane's e8m0 byte of step kb is byte lq of the dword at
+    // s_e8[e8o[ct] + 4 kb] (the four lanes of a row read one address); the
     // tile's weight row r is stage 1's gate row n0 + r (r < 128) or up row
     // inter + n0 + r - 128, stage 2's row n0 + r
     int e8o[NCT];
@@ -333,7 +346,7 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
         const int lrow = STAGE == 1 ? (ct < NCT / 2 ? 16 * (wn * (NCT / 2) + ct)
                                                     : 128 + 16 * (wn * (NCT / 2) + ct - NCT / 2))
                                     : 16 * (wn * NCT + ct);
-        e8o[ct] = (lrow + lr) * E8P + lq;
+        e8o[ct] = (lrow + lr) * E8P;
     }
     constexpr int kE8Pieces = E8L ? NW * e8_max_ks<STAGE, BM>() / 16 / kThreads : 1;
     v4i e8r[kE8Pieces];
@@ -436,14 +449,18 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
         int bsc[NCT];
 #pragma unroll
         for (int ct = 0; ct < NCT; ++ct)
-            bsc[ct] = !W4 ? 0 : E8L ? (int)s_e8[e8o[ct] + 4 * st] : sg_cur[ct][d] >> (8 * lq);
+            bsc[ct] = !W4 ? 0
+                      : E8L ? (int)(*reinterpret_cast<const uint32_t*>(&s_e8[e8o[ct] + 4 * st]) >>
+                                    (8 * lq))
+                            : sg_cur[ct][d] >> (8 * lq);
         const uint8_t* sa_src = &s_a[stage][0];
         // the lane's 32 K bytes of row tile rt: fp8 x fp8 pieces 2 lq, 2 lq + 1
         // (K 32 lq ..); fp8 x fp4 pieces lq, lq + 4 (K 16 lq .. and 64 + 16 lq ..)
         auto afrag = [&](int rt) {
             const int row = row_base + rt * 16 + lr;
             const uint8_t* rp = sa_src + row * 128;
-            const int p0 = W4 ? lq : 2 * lq, p1 = W4 ? lq + 4 : 2 * lq + 1;
+            // (stored at slots a_slot(p) ^ a_swz: 2 lq and 2 lq + 1 either way)
+            const int p0 = a_slot<W4>(W4 ? lq : 2 * lq), p1 = a_slot<W4>(W4 ? lq + 4 : 2 * lq + 1);
             const v4i lo = *reinterpret_cast<const v4i*>(rp + ((p0 ^ a_swz(row)) << 4));
             const v4i hi = *reinterpret_cast<const v4i*>(rp + ((p1 ^ a_swz(row)) << 4));
             return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
