@@ -193,6 +193,17 @@ def test_a8w4_num_local_tokens(cuda_device):
 
 
 @pytest.mark.parametrize("bm", [64, 128])
+def test_a8w4_prefill_large_k_grouped_e8m0(cuda_device, bm):
+    """model_dim 8192 (K/32 = 256 e8m0 bytes per weight row, more than the
+    LDS rows hold) with 32 routed rows per expert: stage 1 runs on the
+    prefill kernel with the e8m0 bytes loaded a group of K steps at a time,
+    64 K steps long; checked against the oracle."""
+    cfg = W.MoEConfig("a8w4_bigk", 64, 8192, 256, 8, 4, seed=17, weights="mxfp4")
+    dev, ref = _make_layer(cfg, cuda_device, True)
+    _check(ref["out"], _np(_run(dev, block_size_M=bm).float()), f"A8W4 H=8192 bm={bm}")
+
+
+@pytest.mark.parametrize("bm", [64, 128])
 def test_a8w4_e8m0_lds_bit_exact(cuda_device, monkeypatch, bm):
     """On the prefill kernels the tile's e8m0 bytes are staged in LDS once per
     tile (AITER_AMD_PF_E8LDS = 0 loads them a group of K steps at a time
