@@ -212,7 +212,15 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
     static_assert(BM == 64 || BM == 128, "prefill tiles are 64 or 128 rows");
     static_assert(A_PT >= 1, "one A piece per thread at least");
     __shared__ __attribute__((aligned(1024))) uint8_t s_a[2][A_BYTES];
-    __shared__ __attribute__((aligned(16))) float s_sc[kMaxKB * NH * BM];   // [step][h][row]
+    // [step][h][row]; the 256-column stage-2 tile also stages its bf16 output
+    // rows here at a pitch of NW + 8 elements (SC_PW), rows that one write
+    // instruction covers (4 apart) then start 16 banks apart
+    constexpr int SC_PW = NW + 8;
+    constexpr int SC_BASE = kMaxKB * NH * BM;
+    constexpr int SC_RPP = (SC_BASE * 4 / (NW * 2)) >= BM ? BM : SC_BASE * 4 / (NW * 2);
+    constexpr int SC_FLOATS = STAGE == 2 && NW2 > 128 && SC_RPP * SC_PW / 2 > SC_BASE
+                                  ? SC_RPP * SC_PW / 2 : SC_BASE;
+    __shared__ __attribute__((aligned(16))) float s_sc[SC_FLOATS];
     __shared__ __attribute__((aligned(16))) uint8_t s_q[STAGE == 1 ? BM * QP : 16];
     __shared__ int32_t s_arow[BM];
     __shared__ int64_t s_orow[BM];
@@ -614,8 +622,9 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
                 // was the final K step (an FP8 tile's 64 rows in one pass; four
                 // through an A stage took T=8192 924-928 us against 917-921), the
                 // 128-column tile through the free A stage
-                auto stage_rows = [&](uint16_t* s_p, auto rpp) __attribute__((always_inline)) {
+                auto stage_rows = [&](uint16_t* s_p, auto rpp, auto pw) __attribute__((always_inline)) {
                     constexpr int RPP = decltype(rpp)::value;
+                    constexpr int PW = decltype(pw)::value;   // staged row pitch (elements)
                     static_assert(RPP % 16 == 0 && BM % RPP == 0,
                                   "a pass of bf16 rows is whole row tiles");
 #pragma unroll
@@ -630,7 +639,7 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
                                 const int lrow = row - hf * RPP;
 #pragma unroll
                                 for (int ct = 0; ct < NCT; ++ct)
-                                    s_p[lrow * NW + wn * NCT * 16 + ct * 16 + lr] =
+                                    s_p[lrow * PW + wn * NCT * 16 + ct * 16 + lr] =
                                         f32_to_bf16_bits(acc[rt][ct][v] * wgt);
                             }
                         }
@@ -640,19 +649,17 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_prefill_kernel(Args g) {
                             const int64_t pair = s_arow[lrow + hf * RPP];
                             if (pair < 0) continue;
                             *reinterpret_cast<v4i*>(g.part + pair * g.N + nc + piece * 8) =
-                                *reinterpret_cast<const v4i*>(s_p + lrow * NW + piece * 8);
+                                *reinterpret_cast<const v4i*>(s_p + lrow * PW + piece * 8);
                         }
                         __syncthreads();
                     }
                 };
-                constexpr int SC_ROWS = (int)(sizeof(s_sc) / (NW * 2));
                 constexpr int A_ROWS = A_BYTES / (NW * 2);
                 if constexpr (NW2 > 128)
-                    stage_rows(reinterpret_cast<uint16_t*>(s_sc),
-                               IntC<(SC_ROWS >= BM ? BM : SC_ROWS)>{});
+                    stage_rows(reinterpret_cast<uint16_t*>(s_sc), IntC<SC_RPP>{}, IntC<SC_PW>{});
                 else
                     stage_rows(reinterpret_cast<uint16_t*>(&s_a[stg][0]),
-                               IntC<(A_ROWS >= BM ? BM : A_ROWS)>{});
+                               IntC<(A_ROWS >= BM ? BM : A_ROWS)>{}, IntC<NW>{});
             } else {
 #pragma unroll
                 for (int rt = 0; rt < NRT; ++rt)
