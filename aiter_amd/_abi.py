@@ -67,6 +67,19 @@ _SIGNATURES = {
         [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_i64, c_i64, c_i64,
          c_i64, c_i64, c_i64, c_i64, c_i64, c_vp],
     ),
+    "aiter_amd_moe_stage1_rows": (
+        c_int,
+        [c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_i64,
+         c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_vp],
+    ),
+    "aiter_amd_act_and_mul": (c_int, [c_vp, c_int, c_vp, c_int, c_i64, c_i64, c_i64, c_vp]),
+    "aiter_amd_fused_moe_sorted_workspace_bytes": (
+        c_i64, [c_i64, c_i64, c_i64, c_i64, c_i64, c_i64]),
+    "aiter_amd_fused_moe_sorted_fp8_blockscale": (
+        c_int,
+        [c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_vp,
+         c_int, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp],
+    ),
     "aiter_amd_moe_acc_to_out": (c_int, [c_vp, c_vp, c_int, c_vp, c_i64, c_i64, c_vp]),
     "aiter_amd_fused_moe_workspace_bytes": (c_i64, [c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64]),
     "aiter_amd_fused_moe_fp8_blockscale": (

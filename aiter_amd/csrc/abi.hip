@@ -29,7 +29,26 @@ bool launch_moe_sort(const int32_t*, const float*, const int32_t*, const int32_t
                      int64_t q_cols = 0, void* zero2 = nullptr, int64_t zero2_bytes = 0);
 void launch_per_group_quant_fp8(const void*, int, void*, float*, int64_t, int64_t, int,
                                 const int32_t*, int64_t, hipStream_t);
-void launch_acc_to_out(const float*, void*, int, const int32_t*, int64_t, int64_t, hipStream_t);
+// addend (optional): a [rows, cols] tensor of the output dtype added before
+// the rounding (it may be out itself)
+void launch_acc_to_out(const float*, void*, int, const int32_t*, int64_t, int64_t, hipStream_t,
+                       const void* addend = nullptr);
+// out[r, c] = act(in[r, c]) * in[r, d + c], rows of in 2d wide (quant.hip)
+void launch_act_and_mul(const void* in, int in_dtype, void* out, int out_dtype, int64_t rows,
+                        int64_t d, int act, hipStream_t stream);
+// zero `bytes` (a multiple of 16) at a 16-byte aligned p with a kernel (quant.hip)
+void launch_zero(void* p, int64_t bytes, hipStream_t stream);
+// moe_sort.hip: per-pair expert ids and weights [tokens, topk] recovered from
+// a layer's sorted metadata (-1 / 0 where the pair was not routed here)
+void launch_unsort(const int32_t* sorted_ids, const float* sorted_w, const int32_t* sorted_eids,
+                   const int32_t* num_valid, int64_t sorted_capacity, int64_t block_m,
+                   int32_t* topk_ids, float* topk_w, int64_t tokens, int64_t topk, int64_t E,
+                   hipStream_t stream);
+void launch_moe_stage1_stream_rows(const uint8_t*, const float*, int64_t, int64_t,
+                                   const uint8_t*, const float*, const uint8_t*, const int32_t*,
+                                   const int32_t*, const int32_t*, void*, int, int, int64_t,
+                                   int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int,
+                                   hipStream_t, const float*, int, int);
 // The GEMM launchers take the weight scales either as fp32 128x128 blocks
 // (FP8 weights) or, when the e8m0 pointer is non-null, as e8m0 bytes per
 // 1x32 K block (MXFP4 weights, A8W4).
@@ -82,7 +101,8 @@ void launch_moe_stage2_stream(const uint8_t*, const float*, const uint8_t*, cons
 // quant.hip: per-pair bf16 rows -> output
 void launch_slot_sum(const uint16_t* part, const int32_t* topk_ids, const int32_t* mask,
                      int64_t num_experts, const int32_t* num_valid, void* out, int out_dtype,
-                     int64_t rows, int64_t topk, int64_t cols, hipStream_t stream);
+                     int64_t rows, int64_t topk, int64_t cols, hipStream_t stream,
+                     const void* addend = nullptr);
 
 // moe_route.hip (router top-k)
 bool route_supported(int64_t E, int64_t k);
@@ -352,6 +372,15 @@ int64_t default_block_m(int64_t tokens, int64_t topk, int64_t E, int64_t G, int6
     return 64;
 }
 
+// Workspace of a layer run from a caller's sorted metadata: the recovered
+// per-pair ids and weights, then the one-call layer's sections (its own
+// sorting at its own block size; G: the experts the router spread the
+// tokens over, a block-size hint).
+int64_t sorted_layer_bytes(int64_t T, int64_t H, int64_t I, int64_t E, int64_t G, int64_t k) {
+    const int64_t bm = default_block_m(T, k, E, std::max(G, E), H, I);
+    return 2 * align256(T * k * 4) + fused_layout(T, H, I, E, E, k, bm).total;
+}
+
 void check_e8m0(const uint8_t* p, const char* name) {
     AMD_CHECK(p != nullptr, std::string(name) + " is NULL");
     AMD_CHECK((reinterpret_cast<uintptr_t>(p) & 3u) == 0,
@@ -437,20 +466,33 @@ static void timing_mark(int step, hipStream_t s) {
     if (step == kTimedSteps) ++t.calls;
 }
 
+// Activations already quantised by the caller (fp8 [tokens, model_dim] and
+// their 1x128 scales at a1_scale[row * sa_row + kb * sa_kb]) instead of
+// bf16 / fp16 hidden states.
+struct PreQuant {
+    const uint8_t* a1 = nullptr;
+    const float* a1_scale = nullptr;
+    int64_t sa_row = 0, sa_kb = 0;
+};
+
+// accumulate: the layer is added to out's previous contents (rounded once
+// from fp32) instead of replacing them.
 void fused_entry(const void* hidden_states, int hidden_dtype, const void* w1, WScale w1s,
                  const void* w2, WScale w2s, const float* topk_weights, const int32_t* topk_ids,
                  const int32_t* expert_mask, const int32_t* num_local_tokens, void* out,
                  int out_dtype, int64_t tokens, int64_t model_dim, int64_t inter_dim,
                  int64_t num_experts, int64_t global_experts, int64_t topk, int64_t block_m,
                  int64_t activation, int64_t doweight_stage1, int64_t w_shuffled,
-                 void* workspace, int64_t workspace_bytes, void* stream, bool one_launch = false) {
+                 void* workspace, int64_t workspace_bytes, void* stream, bool one_launch = false,
+                 PreQuant pre = PreQuant{}, bool accumulate = false) {
     check_dims(model_dim, inter_dim);
     AMD_CHECK(activation == kActSilu || activation == kActGelu,
               "only ActivationType.Silu (0) and Gelu (1) are supported, got " +
                   std::to_string(activation));
     check_stage_dims(tokens, topk, num_experts);
-    AMD_CHECK(hidden_dtype == DT_BF16 || hidden_dtype == DT_FP16,
-              "hidden_states dtype must be bf16 or fp16");
+    if (!pre.a1)
+        AMD_CHECK(hidden_dtype == DT_BF16 || hidden_dtype == DT_FP16,
+                  "hidden_states dtype must be bf16 or fp16");
     AMD_CHECK(out_dtype == DT_BF16 || out_dtype == DT_FP16, "out dtype must be bf16 or fp16");
     const int64_t E_sort = expert_mask ? global_experts : num_experts;
     AMD_CHECK(E_sort >= num_experts && E_sort <= kMaxExperts,
@@ -463,7 +505,12 @@ void fused_entry(const void* hidden_states, int hidden_dtype, const void* w1, WS
               "the one-launch layer needs block_m 16 or 32 and model_dim a multiple of 256 up "
               "to 8192");
     if (tokens == 0) return;
-    check_ptr(hidden_states, "hidden_states");
+    if (pre.a1) {
+        check_ptr(pre.a1, "a1");
+        AMD_CHECK(pre.a1_scale != nullptr, "a1_scale is NULL");
+    } else {
+        check_ptr(hidden_states, "hidden_states");
+    }
     check_ptr(w1, "w1");
     check_ptr(w2, "w2");
     check_ptr(out, "out");
@@ -479,8 +526,11 @@ void fused_entry(const void* hidden_states, int hidden_dtype, const void* w1, WS
     float* sorted_w = reinterpret_cast<float*>(ws + L.off_sorted_w);
     int32_t* sorted_eids = reinterpret_cast<int32_t*>(ws + L.off_sorted_eids);
     int32_t* num_valid = reinterpret_cast<int32_t*>(ws + L.off_num_valid);
-    uint8_t* a1 = ws + L.off_a1;
-    float* a1_scale = reinterpret_cast<float*>(ws + L.off_a1_scale);
+    uint8_t* a1 = pre.a1 ? const_cast<uint8_t*>(pre.a1) : ws + L.off_a1;
+    float* a1_scale =
+        pre.a1 ? const_cast<float*>(pre.a1_scale) : reinterpret_cast<float*>(ws + L.off_a1_scale);
+    const int64_t sa_row = pre.a1 ? pre.sa_row : model_dim / 128;
+    const int64_t sa_kb = pre.a1 ? pre.sa_kb : 1;
     uint8_t* a2 = ws + L.off_a2;
     float* a2_scale = reinterpret_cast<float*>(ws + L.off_a2_scale);
     float* acc = reinterpret_cast<float*>(ws + L.off_acc);
@@ -497,19 +547,20 @@ void fused_entry(const void* hidden_states, int hidden_dtype, const void* w1, WS
     const bool quantised = launch_moe_sort(
         topk_ids, topk_weights, expert_mask, num_local_tokens, sorted_ids, sorted_w, sorted_eids,
         num_valid, part ? nullptr : acc, model_dim * 4, tokens, topk, E_sort, block_m,
-        ws + L.off_sort_ws, L.sort_ws_bytes, s, hidden_states, (int)hidden_dtype, a1, a1_scale,
-        model_dim, ws + L.off_kcnt, L.kcnt_bytes);
+        ws + L.off_sort_ws, L.sort_ws_bytes, s, pre.a1 ? nullptr : hidden_states,
+        (int)hidden_dtype, a1, a1_scale, model_dim, ws + L.off_kcnt, L.kcnt_bytes);
     timing_mark(1, s);
-    if (!quantised)
+    if (!quantised && !pre.a1)
         launch_per_group_quant_fp8(hidden_states, hidden_dtype, a1, a1_scale, tokens, model_dim,
                                    0, num_local_tokens, 1, s);
     timing_mark(2, s);
     const int sh = (int)(w_shuffled != 0);
     // doweight_stage1: the routing weights scale stage 1's gate and up, stage 2 sums unweighted
     const bool dw = doweight_stage1 != 0;
+    const void* addend = accumulate ? out : nullptr;
     if (!part && (one_launch || use_fused_layer(tokens, topk, block_m, model_dim, inter_dim))) {
         // decode sizes: both GEMMs in one launch, a2 kept per workgroup in LDS
-        launch_moe_fused_stream(a1, a1_scale, model_dim / 128, 1, (const uint8_t*)w1, w1s.f32,
+        launch_moe_fused_stream(a1, a1_scale, sa_row, sa_kb, (const uint8_t*)w1, w1s.f32,
                                 w1s.e8m0, (const uint8_t*)w2, w2s.f32, w2s.e8m0, sorted_ids,
                                 dw ? sorted_w : nullptr, dw ? nullptr : sorted_w, sorted_eids,
                                 num_valid, acc, tokens, model_dim, inter_dim, num_experts, topk,
@@ -518,11 +569,11 @@ void fused_entry(const void* hidden_states, int hidden_dtype, const void* w1, WS
                                 L.kmb);
         timing_mark(3, s);
         timing_mark(4, s);
-        launch_acc_to_out(acc, out, out_dtype, num_valid, tokens, model_dim, s);
+        launch_acc_to_out(acc, out, out_dtype, num_valid, tokens, model_dim, s, addend);
         timing_mark(5, s);
         return;
     }
-    stage1_dispatch(a1, a1_scale, model_dim / 128, 1, (const uint8_t*)w1, w1s, sorted_ids,
+    stage1_dispatch(a1, a1_scale, sa_row, sa_kb, (const uint8_t*)w1, w1s, sorted_ids,
                     sorted_eids, num_valid, a2, a2_scale, tokens, model_dim, inter_dim,
                     num_experts, topk, block_m, L.blocks, sh, s, dw ? sorted_w : nullptr,
                     (int)activation, L.ksplit, ws + L.off_kpart,
@@ -535,9 +586,9 @@ void fused_entry(const void* hidden_states, int hidden_dtype, const void* w1, WS
     timing_mark(4, s);
     if (part)
         launch_slot_sum(part, topk_ids, expert_mask, E_sort, num_valid, out, out_dtype, tokens,
-                        topk, model_dim, s);
+                        topk, model_dim, s, addend);
     else
-        launch_acc_to_out(acc, out, out_dtype, num_valid, tokens, model_dim, s);
+        launch_acc_to_out(acc, out, out_dtype, num_valid, tokens, model_dim, s, addend);
     timing_mark(5, s);
 }
 
@@ -914,6 +965,137 @@ int aiter_amd_fused_moe_1stage_a8w4(
                     num_local_tokens, out, out_dtype, tokens, model_dim, inter_dim, num_experts,
                     global_experts, topk, block_m, activation, doweight_stage1, w_shuffled, workspace,
                     workspace_bytes, stream, true);
+    });
+}
+
+int aiter_amd_moe_stage1_rows(const void* a1, const float* a1_scale, int64_t a1_scale_transposed,
+                              const void* w1, const float* w1_scale,
+                              const uint8_t* w1_scale_e8m0, const int32_t* sorted_ids,
+                              const float* sorted_weights, const int32_t* sorted_expert_ids,
+                              const int32_t* num_valid_ids, void* out, int out_form,
+                              int out_dtype, int64_t tokens, int64_t model_dim,
+                              int64_t inter_dim, int64_t num_experts, int64_t topk,
+                              int64_t block_m, int64_t max_m_blocks, int64_t activation,
+                              int64_t ksplit, int64_t w_shuffled, void* stream) {
+    return safe_call([&] {
+        check_dims(model_dim, inter_dim);
+        check_stage_dims(tokens, topk, num_experts);
+        AMD_CHECK(out_form == kOutAct || out_form == kOutGateUp,
+                  "out_form must be 1 (act(gate) * up rows) or 2 (fp32 gate | up rows)");
+        AMD_CHECK(out_form == kOutGateUp ? out_dtype == DT_FP32
+                                         : (out_dtype == DT_BF16 || out_dtype == DT_FP16 ||
+                                            out_dtype == DT_FP32),
+                  out_form == kOutGateUp ? "gate | up rows are fp32"
+                                         : "act rows must be bf16, fp16 or fp32");
+        AMD_CHECK(block_m == 16 || block_m == 32 || block_m == 64 || block_m == 128,
+                  "block_m must be 16, 32, 64 or 128, got " + std::to_string(block_m));
+        AMD_CHECK(model_dim <= 8192, "model_dim must be at most 8192");
+        AMD_CHECK(activation == kActSilu || activation == kActGelu,
+                  "only ActivationType.Silu (0) and Gelu (1) are supported, got " +
+                      std::to_string(activation));
+        AMD_CHECK((w1_scale != nullptr) != (w1_scale_e8m0 != nullptr),
+                  "exactly one of w1_scale (fp8 weights) and w1_scale_e8m0 (MXFP4) is given");
+        const int64_t KB = model_dim / 128;
+        AMD_CHECK(ksplit >= 0 && ksplit <= KB && (ksplit <= 1 || KB % ksplit == 0),
+                  "ksplit must divide model_dim / 128 = " + std::to_string(KB) + ", got " +
+                      std::to_string(ksplit));
+        AMD_CHECK(ksplit <= 1 || out_form == kOutGateUp,
+                  "a K split (ksplit > 1) writes fp32 gate | up rows (out_form 2)");
+        AMD_CHECK(max_m_blocks >= 0, "max_m_blocks must be >= 0");
+        if (w1_scale_e8m0) check_e8m0(w1_scale_e8m0, "w1_scale");
+        if (tokens == 0 || max_m_blocks == 0) return;
+        check_ptr(a1, "a1");
+        check_ptr(w1, "w1");
+        check_ptr(out, "out");
+        AMD_CHECK(a1_scale && sorted_ids && sorted_expert_ids && num_valid_ids,
+                  "a required pointer is NULL");
+        hipStream_t s = (hipStream_t)stream;
+        // the K ranges of a split tile add into zeroed rows
+        if (ksplit > 1) launch_zero(out, tokens * topk * 2 * inter_dim * 4, s);
+        launch_moe_stage1_stream_rows(
+            (const uint8_t*)a1, a1_scale, a1_scale_transposed ? 1 : model_dim / 128,
+            a1_scale_transposed ? tokens : 1, (const uint8_t*)w1, w1_scale, w1_scale_e8m0,
+            sorted_ids, sorted_expert_ids, num_valid_ids, out, out_form, out_dtype, tokens,
+            model_dim, inter_dim, num_experts, topk, block_m, max_m_blocks,
+            (int)(w_shuffled != 0), s, sorted_weights, (int)activation, (int)ksplit);
+    });
+}
+
+int aiter_amd_act_and_mul(const void* input, int input_dtype, void* out, int out_dtype,
+                          int64_t rows, int64_t d, int64_t activation, void* stream) {
+    return safe_call([&] {
+        AMD_CHECK(input_dtype == DT_FP32 || input_dtype == DT_BF16 || input_dtype == DT_FP16,
+                  "input dtype must be fp32, bf16 or fp16");
+        AMD_CHECK(out_dtype == DT_FP32 || out_dtype == DT_BF16 || out_dtype == DT_FP16,
+                  "out dtype must be fp32, bf16 or fp16");
+        AMD_CHECK(activation == kActSilu || activation == kActGelu,
+                  "only ActivationType.Silu (0) and Gelu (1) are supported, got " +
+                      std::to_string(activation));
+        AMD_CHECK(rows >= 0 && d >= 0, "rows and d must be >= 0");
+        AMD_CHECK(rows * d < (int64_t(1) << 40), "too many elements");
+        AMD_CHECK(d < (int64_t(1) << 31), "d must be below 2^31");
+        if (rows == 0 || d == 0) return;
+        AMD_CHECK(input && out, "a required pointer is NULL");
+        launch_act_and_mul(input, input_dtype, out, out_dtype, rows, d, (int)activation,
+                           (hipStream_t)stream);
+    });
+}
+
+int64_t aiter_amd_fused_moe_sorted_workspace_bytes(int64_t tokens, int64_t model_dim,
+                                                   int64_t inter_dim, int64_t num_experts,
+                                                   int64_t global_experts, int64_t topk) {
+    if (tokens < 0 || model_dim <= 0 || inter_dim <= 0 || num_experts < 1 || topk < 1)
+        return -1;
+    return sorted_layer_bytes(tokens, model_dim, inter_dim, num_experts, global_experts, topk);
+}
+
+int aiter_amd_fused_moe_sorted_fp8_blockscale(
+    const void* a1, const float* a1_scale, int64_t a1_scale_transposed, const void* w1,
+    const float* w1_scale, const void* w2, const float* w2_scale, const int32_t* sorted_ids,
+    const float* sorted_weights, const int32_t* sorted_expert_ids, const int32_t* num_valid_ids,
+    int64_t sorted_capacity, int64_t sorted_block_m, void* out, int out_dtype, int64_t tokens,
+    int64_t model_dim, int64_t inter_dim, int64_t num_experts, int64_t global_experts,
+    int64_t topk, int64_t activation, int64_t w_shuffled, void* workspace,
+    int64_t workspace_bytes, void* stream) {
+    return safe_call([&] {
+        AMD_CHECK(w1_scale && w2_scale, "a required pointer is NULL");
+        check_dims(model_dim, inter_dim);
+        check_stage_dims(tokens, topk, num_experts);
+        AMD_CHECK(out_dtype == DT_BF16 || out_dtype == DT_FP16, "out dtype must be bf16 or fp16");
+        AMD_CHECK(sorted_block_m >= 1 && sorted_block_m <= 256,
+                  "sorted_block_m must be in [1, 256]");
+        AMD_CHECK(sorted_capacity >= 0, "sorted_capacity must be >= 0");
+        const int64_t need = sorted_layer_bytes(tokens, model_dim, inter_dim, num_experts,
+                                                global_experts, topk);
+        AMD_CHECK(workspace_bytes >= need, "workspace of " + std::to_string(need) +
+                                               " bytes required, got " +
+                                               std::to_string(workspace_bytes));
+        if (tokens == 0) return;
+        check_ptr(workspace, "workspace");
+        AMD_CHECK(sorted_ids && sorted_weights && sorted_expert_ids && num_valid_ids,
+                  "a required pointer is NULL");
+        hipStream_t s = (hipStream_t)stream;
+        uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
+        int32_t* ids = reinterpret_cast<int32_t*>(ws);
+        float* wts = reinterpret_cast<float*>(ws + align256(tokens * topk * 4));
+        const int64_t off = 2 * align256(tokens * topk * 4);
+        // the pairs routed to these experts, recovered from the caller's sorting
+        launch_unsort(sorted_ids, sorted_weights, sorted_expert_ids, num_valid_ids,
+                      sorted_capacity, sorted_block_m, ids, wts, tokens, topk, num_experts, s);
+        const int64_t G = std::max(global_experts, num_experts);
+        const int64_t bm =
+            default_block_m(tokens, topk, num_experts, G, model_dim, inter_dim);
+        PreQuant pre;
+        pre.a1 = (const uint8_t*)a1;
+        pre.a1_scale = a1_scale;
+        pre.sa_row = a1_scale_transposed ? 1 : model_dim / 128;
+        pre.sa_kb = a1_scale_transposed ? tokens : 1;
+        // the caller's token count (num_valid_ids[1]) bounds the rows; the
+        // layer is added to out, which the caller's sorting zeroed
+        fused_entry(nullptr, DT_FP8, w1, WScale{w1_scale, nullptr}, w2, WScale{w2_scale, nullptr},
+                    wts, ids, nullptr, num_valid_ids + 1, out, out_dtype, tokens, model_dim,
+                    inter_dim, num_experts, num_experts, topk, bm, activation, 0, w_shuffled,
+                    ws + off, workspace_bytes - off, stream, false, pre, true);
     });
 }
 

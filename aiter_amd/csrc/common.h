@@ -190,6 +190,15 @@ __device__ __forceinline__ void acc_add(void* base, int dtype, int64_t i, float 
 constexpr int kActSilu = 0;
 constexpr int kActGelu = 1;
 
+// Stage-1 output forms: the fp8 a2 with its 1x128 scales (the fused requant);
+// act(gate) * up rows [pairs, inter] in bf16 / fp16 / fp32 (the reference's
+// ck_moe_stage1 output, quantised by a separate launch); fp32 gate | up rows
+// [pairs, 2 * inter] before the activation (its split-K output, which
+// silu_and_mul / gelu_and_mul finish).
+constexpr int kOutA2 = 0;
+constexpr int kOutAct = 1;
+constexpr int kOutGateUp = 2;
+
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // XCD-aware order of a 1-D grid of (M-tile, column group) workgroups.

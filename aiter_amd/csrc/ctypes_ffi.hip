@@ -9,7 +9,10 @@
 #include "../../include/aiter_ctypes.h"
 
 #include <algorithm>
+#include <map>
+#include <mutex>
 #include <string>
+#include <utility>
 
 #include "common.h"
 
@@ -130,6 +133,50 @@ struct DeviceGuard {
 // message it left (safe_call stores it back).
 void run(int rc) {
     if (rc != 0) throw AbiError(aiter_amd_get_last_error());
+}
+
+// Device workspace the library holds for the reference-shaped entries whose
+// signatures carry none (fmoe_fp8_blockscale_g1u1): one buffer per (device,
+// stream), grown on demand with hipMalloc and kept until the process ends.
+// Growing waits for the stream's earlier work, frees the old buffer and is
+// refused while the stream is being captured into a HIP graph (a call of
+// the same or a larger size made before capture avoids it). Calls on one
+// stream are ordered by the stream; calls on different streams use
+// different buffers.
+struct Pooled {
+    void* p = nullptr;
+    int64_t bytes = 0;
+};
+std::mutex g_pool_mu;
+std::map<std::pair<int, void*>, Pooled> g_pool;
+
+void* pooled_workspace(int dev, void* stream, int64_t bytes, const char* who) {
+    std::lock_guard<std::mutex> lock(g_pool_mu);
+    Pooled& w = g_pool[{dev, stream}];
+    if (w.bytes >= bytes) return w.p;
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    AMD_HIP_CHECK(hipStreamIsCapturing((hipStream_t)stream, &st));
+    AMD_CHECK(st == hipStreamCaptureStatusNone,
+              std::string(who) + " needs " + std::to_string(bytes) +
+                  " bytes of library workspace on this stream, which cannot be allocated "
+                  "during graph capture: make one call of this size before capturing");
+    // grow by at least a quarter, in 2 MiB steps, so a slowly growing batch
+    // does not reallocate on every call
+    int64_t want = std::max(bytes, w.bytes + w.bytes / 4);
+    want = (want + (2 << 20) - 1) / (2 << 20) * (2 << 20);
+    if (w.p) {
+        AMD_HIP_CHECK(hipStreamSynchronize((hipStream_t)stream));
+        AMD_HIP_CHECK(hipFree(w.p));
+        w.p = nullptr;
+        w.bytes = 0;
+    }
+    void* p = nullptr;
+    const hipError_t e = hipMalloc(&p, (size_t)want);
+    AMD_CHECK(e == hipSuccess && p, std::string(who) + ": hipMalloc of " + std::to_string(want) +
+                                        " bytes of workspace failed: " + hipGetErrorString(e));
+    w.p = p;
+    w.bytes = want;
+    return p;
 }
 
 }  // namespace
@@ -305,6 +352,163 @@ int ck_moe_stage2(aiter_tensor_t* inter_states, aiter_tensor_t* w1, aiter_tensor
                 (const int32_t*)sid.ptr, (const float*)ptr(sw), (const int32_t*)se.ptr,
                 (const int32_t*)nv.ptr, o.ptr, o.dtype_, T, H, I, E, topk, block_m, se.numel_,
                 is_shuffled != 0, stream));
+    });
+}
+
+int ck_moe_stage1(aiter_tensor_t* hidden_states, aiter_tensor_t* w1, aiter_tensor_t* w2,
+                  aiter_tensor_t* sorted_token_ids, aiter_tensor_t* sorted_expert_ids,
+                  aiter_tensor_t* num_valid_ids, aiter_tensor_t* out, int64_t topk,
+                  const char* kernelName, aiter_tensor_t* w1_scale, aiter_tensor_t* a1_scale,
+                  int64_t block_m, aiter_tensor_t* sorted_weights, int64_t quant_type,
+                  int64_t activation, int64_t splitk, int use_non_temporal_load,
+                  const char* dst_type, int is_shuffled, void* stream) {
+    (void)w2;
+    (void)kernelName;
+    (void)use_non_temporal_load;
+    (void)dst_type;
+    return safe_call([&] {
+        const int dev = need(hidden_states, "hidden_states").device_id;
+        const auto& a = tensor(hidden_states, "hidden_states", dev, {DT_FP8});
+        AMD_CHECK(a.ndim == 2, "hidden_states must be [tokens, model_dim]");
+        const int64_t T = a.shape[0], H = a.shape[1];
+        const auto& w = tensor(w1, "w1", dev, {DT_FP8, DT_FP4X2, DT_U8});
+        AMD_CHECK(w.ndim == 3 && w.shape[1] % 2 == 0, "w1 must be [E, 2*inter_dim, model_dim]");
+        const bool w4 = w.dtype_ != DT_FP8;
+        const int64_t E = w.shape[0], I = w.shape[1] / 2;
+        AMD_CHECK(w.shape[2] == (w4 ? H / 2 : H), "w1's last dimension does not match model_dim");
+        AMD_CHECK(quant_type == (w4 ? kQuantPer1x32 : kQuantPer1x128),
+                  w4 ? "fp4x2 w1 needs QuantType.per_1x32 (fp8 1x128 activations)"
+                     : "fp8 w1 needs QuantType.per_1x128");
+        const auto& ws = tensor(w1_scale, "w1_scale", dev,
+                                w4 ? std::initializer_list<int>{DT_FP8_E8M0, DT_U8}
+                                   : std::initializer_list<int>{DT_FP32});
+        if (w4)
+            check_shape(ws, "w1_scale", {E, 2 * I, H / 32});
+        else
+            check_shape(ws, "w1_scale", {E, 2 * I / 128, H / 128});
+        const auto& as = tensor(a1_scale, "a1_scale", dev, {DT_FP32});
+        check_numel(as, "a1_scale", T * (H / 128));
+        const bool split = splitk > 1;
+        const auto& o = tensor(out, "out", dev,
+                               split ? std::initializer_list<int>{DT_FP32}
+                                     : std::initializer_list<int>{DT_BF16, DT_FP16});
+        if (split) {
+            AMD_CHECK(o.ndim == 2 && o.shape[1] == 2 * I && o.shape[0] >= T * topk,
+                      "with splitk > 1, out must be fp32 [>= tokens*topk, 2*inter_dim]");
+        } else {
+            AMD_CHECK(o.ndim >= 1 && dim(o, -1) == I && (int64_t)o.numel_ == T * topk * I,
+                      "out must be [tokens, topk, inter_dim] (or [tokens*topk, inter_dim])");
+        }
+        const auto& sid = tensor(sorted_token_ids, "sorted_token_ids", dev, {DT_I32});
+        const auto& se = tensor(sorted_expert_ids, "sorted_expert_ids", dev, {DT_I32});
+        const auto& nv = tensor(num_valid_ids, "num_valid_ids", dev, {DT_I32});
+        check_numel(nv, "num_valid_ids", 2);
+        const auto* sw = optional(sorted_weights, "sorted_weights", dev, {DT_FP32});
+        AMD_CHECK(block_m == 16 || block_m == 32 || block_m == 64 || block_m == 128,
+                  "block_m must be 16, 32, 64 or 128, got " + std::to_string(block_m));
+        AMD_CHECK(activation == kActSilu || activation == kActGelu,
+                  "only ActivationType.Silu (0) and Gelu (1) are supported, got " +
+                      std::to_string(activation));
+        AMD_CHECK(H % 128 == 0 && (!split || (H / 128) % splitk == 0),
+                  "ksplit must divide model_dim / 128 = " + std::to_string(H / 128) + ", got " +
+                      std::to_string(splitk));
+        DeviceGuard guard(dev);
+        run(aiter_amd_moe_stage1_rows(
+            a.ptr, (const float*)as.ptr, 0, w.ptr, w4 ? nullptr : (const float*)ws.ptr,
+            w4 ? (const uint8_t*)ws.ptr : nullptr, (const int32_t*)sid.ptr,
+            (const float*)ptr(sw), (const int32_t*)se.ptr, (const int32_t*)nv.ptr, o.ptr,
+            split ? kOutGateUp : kOutAct, o.dtype_, T, H, I, E, topk, block_m, se.numel_,
+            activation, split ? splitk : 0, is_shuffled != 0, stream));
+    });
+}
+
+static int act_and_mul(aiter_tensor_t* out, aiter_tensor_t* input, int act, void* stream) {
+    return safe_call([&] {
+        const int dev = need(input, "input").device_id;
+        const auto& x = tensor(input, "input", dev, {DT_FP32, DT_BF16, DT_FP16});
+        const auto& y = tensor(out, "out", dev, {DT_FP32, DT_BF16, DT_FP16});
+        AMD_CHECK(x.ndim >= 1 && y.ndim >= 1, "input and out need a last dimension");
+        const int64_t d = dim(y, -1);
+        AMD_CHECK(dim(x, -1) == 2 * d, "input's last dimension must be twice out's");
+        AMD_CHECK((int64_t)x.numel_ == 2 * (int64_t)y.numel_,
+                  "input and out must hold the same rows");
+        const int64_t rows = d ? (int64_t)y.numel_ / d : 0;
+        DeviceGuard guard(dev);
+        run(aiter_amd_act_and_mul(x.ptr, x.dtype_, y.ptr, y.dtype_, rows, d, act, stream));
+    });
+}
+
+int silu_and_mul(aiter_tensor_t* out, aiter_tensor_t* input, void* stream) {
+    return act_and_mul(out, input, kActSilu, stream);
+}
+
+int gelu_and_mul(aiter_tensor_t* out, aiter_tensor_t* input, void* stream) {
+    return act_and_mul(out, input, kActGelu, stream);
+}
+
+int fmoe_fp8_blockscale_g1u1(aiter_tensor_t* out, aiter_tensor_t* input, aiter_tensor_t* gate,
+                             aiter_tensor_t* down, aiter_tensor_t* sorted_token_ids,
+                             aiter_tensor_t* sorted_weights, aiter_tensor_t* sorted_expert_ids,
+                             aiter_tensor_t* num_valid_ids, int64_t topk,
+                             aiter_tensor_t* input_scale, aiter_tensor_t* fc1_scale,
+                             aiter_tensor_t* fc2_scale, const char* kernel_name,
+                             int64_t fc_scale_blkn, int64_t fc_scale_blkk,
+                             aiter_tensor_t* fc2_smooth_scale, int64_t activation,
+                             int64_t block_size_M, void* stream) {
+    (void)kernel_name;
+    return safe_call([&] {
+        AMD_CHECK(fc_scale_blkn == 128 && fc_scale_blkk == 128,
+                  "fmoe_fp8_blockscale_g1u1: only 128x128 weight scale blocks are supported");
+        AMD_CHECK(fc2_smooth_scale == nullptr, "fc2_smooth_scale is not supported");
+        const int dev = need(input, "input").device_id;
+        const auto& a = tensor(input, "input", dev, {DT_FP8});
+        AMD_CHECK(a.ndim == 2, "input must be [tokens, model_dim]");
+        const int64_t T = a.shape[0], H = a.shape[1];
+        const auto& w1 = tensor(gate, "gate", dev, {DT_FP8});
+        AMD_CHECK(w1.ndim == 3 && w1.shape[2] == H && w1.shape[1] % 2 == 0,
+                  "gate must be [E, 2*inter_dim, model_dim] fp8");
+        const int64_t E = w1.shape[0], I = w1.shape[1] / 2;
+        const auto& w2 = tensor(down, "down", dev, {DT_FP8});
+        check_shape(w2, "down", {E, H, I});
+        const auto& s1 = tensor(fc1_scale, "fc1_scale", dev, {DT_FP32});
+        check_numel(s1, "fc1_scale", E * (2 * I / 128) * (H / 128));
+        const auto& s2 = tensor(fc2_scale, "fc2_scale", dev, {DT_FP32});
+        check_numel(s2, "fc2_scale", E * (H / 128) * (I / 128));
+        const auto& as = tensor(input_scale, "input_scale", dev, {DT_FP32});
+        check_numel(as, "input_scale", T * (H / 128));
+        const auto& o = tensor(out, "out", dev, {DT_BF16, DT_FP16});
+        check_shape(o, "out", {T, H});
+        const auto& sid = tensor(sorted_token_ids, "sorted_token_ids", dev, {DT_I32});
+        const auto& sw = tensor(sorted_weights, "sorted_weights", dev, {DT_FP32});
+        const auto& se = tensor(sorted_expert_ids, "sorted_expert_ids", dev, {DT_I32});
+        const auto& nv = tensor(num_valid_ids, "num_valid_ids", dev, {DT_I32});
+        check_numel(nv, "num_valid_ids", 2);
+        AMD_CHECK(block_size_M >= 1 && block_size_M <= 256,
+                  "block_size_M must be the sorting's block size, in [1, 256]");
+        AMD_CHECK(topk >= 1 && topk <= 32, "topk must be in [1, 32]");
+        AMD_CHECK(activation == kActSilu || activation == kActGelu,
+                  "only ActivationType.Silu (0) and Gelu (1) are supported, got " +
+                      std::to_string(activation));
+        const int64_t cap = std::min<int64_t>(sid.numel_, sw.numel_);
+        AMD_CHECK((int64_t)se.numel_ >= ceil_div(cap, block_size_M),
+                  "sorted_expert_ids holds fewer blocks than sorted_token_ids needs");
+        // the router's expert count, from moe_sorting's capacity
+        // tokens*topk + experts*block - topk (a block-size hint only)
+        const int64_t G = std::min<int64_t>(
+            std::max<int64_t>((cap - T * topk + topk) / block_size_M, E), 4096);
+        DeviceGuard guard(dev);
+        const int64_t need_bytes =
+            aiter_amd_fused_moe_sorted_workspace_bytes(T, H, I, E, G, topk);
+        AMD_CHECK(need_bytes >= 0, "invalid layer dimensions");
+        void* ws = T ? pooled_workspace(dev, stream, need_bytes, "fmoe_fp8_blockscale_g1u1")
+                     : nullptr;
+        // the asm kernel this replaces reads (16,16)-shuffled weights and the
+        // transposed [model_dim/128, tokens] activation scales
+        run(aiter_amd_fused_moe_sorted_fp8_blockscale(
+            a.ptr, (const float*)as.ptr, 1, w1.ptr, (const float*)s1.ptr, w2.ptr,
+            (const float*)s2.ptr, (const int32_t*)sid.ptr, (const float*)sw.ptr,
+            (const int32_t*)se.ptr, (const int32_t*)nv.ptr, cap, block_size_M, o.ptr, o.dtype_, T,
+            H, I, E, G, topk, activation, 1, ws, need_bytes, stream));
     });
 }
 

@@ -87,6 +87,15 @@ struct Args {
     // stage 1 / fused: start each workgroup's K walk (and the fused down
     // GEMM's column walk) at a staggered offset
     int krot;
+    // stage 1 output form (kOutA2 / kOutAct / kOutGateUp); the last two write
+    // rows t * topk + slot of out (kOutAct in out_dtype; kOutGateUp fp32,
+    // added atomically into rows the caller zeroed when ksplit > 1)
+    int out_mode;
+    void* out;
+    int out_dtype;
+    // sorted_eids holds one expert per BM << eid_shift sorted rows: a caller's
+    // 64- or 128-row M-blocks are walked as 32-row ones
+    int eid_shift;
 };
 
 // One K step of one wave's operands.
@@ -129,7 +138,7 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
     const int nvalid = g.num_valid[0];
     if (mb * BM >= nvalid) return;
     const int tokens = g.num_valid[1];
-    const int e = g.sorted_eids[mb];
+    const int e = g.sorted_eids[mb >> g.eid_shift];
     if (e < 0 || e >= g.E) return;
     // stage 2 may walk ntw consecutive 256-column groups in one K loop (steps
     // s = jt * KB + kb); stage 1 always has one tile, whose K range the S
@@ -357,6 +366,37 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
         }
 #pragma unroll
         for (int d = 0; d < D; ++d) compute(buf[d], km(kend - D + d), 0, sgc, d);
+        if constexpr (!FUSED) {
+            if (g.out_mode == kOutGateUp) {
+                // ---- fp32 gate | up rows before the activation; a K range of
+                // a split tile adds its partial sums (the rows start at zero) ----
+                float* out = reinterpret_cast<float*>(g.out);
+#pragma unroll
+                for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        const int row = rt * 16 + 4 * lq + v;
+                        const int64_t orow = s_orow[row];
+                        if (orow < 0) continue;
+                        // doweight_stage1 scales gate and up (linear in the partials)
+                        const float wg = g.sorted_w ? s_w[row] : 1.0f;
+                        float* dst = out + orow * 2 * g.inter + n0 + 32 * wv + lr;
+#pragma unroll
+                        for (int j = 0; j < 2; ++j) {
+                            const float gate = acc[rt][j][v] * wg;
+                            const float up = acc[rt][2 + j][v] * wg;
+                            if (S > 1) {
+                                unsafeAtomicAdd(dst + 16 * j, gate);
+                                unsafeAtomicAdd(dst + g.inter + 16 * j, up);
+                            } else {
+                                dst[16 * j] = gate;
+                                dst[g.inter + 16 * j] = up;
+                            }
+                        }
+                    }
+                return;
+            }
+        }
         if (S > 1) {
             // ---- split-K: publish this K range's partial sums; the last
             // workgroup of the tile to arrive adds all S in split order (the
@@ -488,6 +528,34 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
 
     // ---- stage 1 epilogue: silu(gate)*up -> bf16 -> 1x128 fp8 requant ----
     // wave wv holds output columns 32*wv + 16*j + lr (j = 0, 1) of the tile's 128
+    if constexpr (!FUSED) {
+        if (g.out_mode == kOutAct) {
+            // ---- act(gate) * up rows, rounded once to the output dtype ----
+#pragma unroll
+            for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int row = rt * 16 + 4 * lq + v;
+                    const int64_t orow = s_orow[row];
+                    if (orow < 0) continue;
+                    const float wg = g.sorted_w ? s_w[row] : 1.0f;
+                    const int64_t base = orow * g.inter + n0 + 32 * wv + lr;
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        const float x = acc[rt][j][v] * wg;
+                        const float y = (g.act == kActGelu ? gelu_f32(x) : silu_f32(x)) *
+                                        (acc[rt][2 + j][v] * wg);
+                        const int64_t i = base + 16 * j;
+                        if (g.out_dtype == DT_FP32)
+                            reinterpret_cast<float*>(g.out)[i] = y;
+                        else
+                            reinterpret_cast<uint16_t*>(g.out)[i] =
+                                g.out_dtype == DT_BF16 ? f32_to_bf16_bits(y) : f32_to_fp16_bits(y);
+                    }
+                }
+            return;
+        }
+    }
     float h[NRT][2][4];
     // act(gate) * up; the activation is chosen once per workgroup
     auto act_up = [&](auto act) {
@@ -780,6 +848,64 @@ void launch_moe_stage1_stream(const uint8_t* a, const float* a_scale, int64_t sa
     const int64_t mblocks = g.ksplit > 1 ? g.kmb : max_m_blocks;
     const dim3 grid((unsigned)(inter / 128 * g.ksplit), (unsigned)mblocks);
     stream::launch<1>((int)block_m, (int)(K / 128 / g.ksplit), grid, g, shuffled, stream);
+    AMD_HIP_CHECK(hipGetLastError());
+}
+
+// Stage 1 writing rows t * topk + slot of `out` instead of the fp8 a2:
+// act(gate) * up [pairs, inter] in out_dtype (kOutAct) or fp32 gate | up
+// [pairs, 2 * inter] (kOutGateUp). M-blocks of block_m 16, 32, 64 or 128
+// sorted rows (64 and 128 are walked as 32-row blocks of the same expert).
+// ksplit > 1 (kOutGateUp only): the K range of a tile is split ksplit ways,
+// each adding its partial sums into out, whose rows must be zero on entry.
+void launch_moe_stage1_stream_rows(const uint8_t* a, const float* a_scale, int64_t sa_row,
+                                   int64_t sa_kb, const uint8_t* w1, const float* w1_scale,
+                                   const uint8_t* w1_scale_e8m0, const int32_t* sorted_ids,
+                                   const int32_t* sorted_eids, const int32_t* num_valid,
+                                   void* out, int out_mode, int out_dtype, int64_t a_rows,
+                                   int64_t K, int64_t inter, int64_t E, int64_t topk,
+                                   int64_t block_m, int64_t max_m_blocks, int shuffled,
+                                   hipStream_t stream, const float* sorted_w, int act,
+                                   int ksplit) {
+    AMD_CHECK(out_mode == kOutAct || out_mode == kOutGateUp, "unknown stage-1 output form");
+    AMD_CHECK(block_m == 16 || block_m == 32 || block_m == 64 || block_m == 128,
+              "block_m must be 16, 32, 64 or 128");
+    AMD_CHECK(K > 0 && K % 128 == 0 && K / 128 <= stream::kMaxKB,
+              "model_dim must be a multiple of 128 up to 8192");
+    const int KB = (int)(K / 128);
+    const int S = ksplit > 1 ? ksplit : 1;
+    AMD_CHECK(S == 1 || (out_mode == kOutGateUp && KB % S == 0),
+              "split-K needs the fp32 gate|up output and K / 128 divisible by the split");
+    const int bmk = block_m <= 32 ? (int)block_m : 32;
+    const int shift = block_m == 128 ? 2 : block_m == 64 ? 1 : 0;
+    stream::Args g{};
+    g.ksplit = S;
+    g.kmb = (int)(max_m_blocks << shift);
+    g.krot = stream::k_rotation();
+    g.sorted_w = sorted_w;
+    g.act = act;
+    g.a = a;
+    g.a_scale = a_scale;
+    g.sa_row = sa_row;
+    g.sa_kb = sa_kb;
+    g.w = w1;
+    g.w_scale = w1_scale;
+    g.w_scale8 = w1_scale_e8m0;
+    g.sorted_ids = sorted_ids;
+    g.sorted_eids = sorted_eids;
+    g.num_valid = num_valid;
+    g.out_mode = out_mode;
+    g.out = out;
+    g.out_dtype = out_dtype;
+    g.eid_shift = shift;
+    g.K = (int)K;
+    g.N = (int)(2 * inter);
+    g.inter = (int)inter;
+    g.topk = (int)topk;
+    g.E = (int)E;
+    g.a_rows = a_rows;
+    if (max_m_blocks == 0) return;
+    const dim3 grid((unsigned)(inter / 128 * S), (unsigned)(max_m_blocks << shift));
+    stream::launch<1>(bmk, KB / S, grid, g, shuffled, stream);
     AMD_HIP_CHECK(hipGetLastError());
 }
 

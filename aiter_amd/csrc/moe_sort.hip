@@ -34,6 +34,7 @@
 // chunk that sums the counts of the chunks before it (and of all chunks,
 // for the segment layout) and writes its pairs -- the prefix is recomputed
 // by every block in parallel instead of by a serial scan launch.
+#include <algorithm>
 #include <cstdlib>
 
 #include "common.h"
@@ -628,6 +629,60 @@ bool launch_moe_sort(const int32_t* topk_ids, const float* topk_w, const int32_t
     }
     AMD_HIP_CHECK(hipGetLastError());
     return quant_done;
+}
+
+// ------------------------------------------ sorted metadata -> routing ---
+// The inverse of sorting for one layer's sorted metadata: topk_ids[t, j] =
+// the expert of the M-block holding entry (j << 24) | t, topk_w[t, j] its
+// weight, for the entries below num_valid[0] with t < num_valid[1]; pairs
+// with no entry (routed to experts another GPU holds) get id -1, which
+// sorting and the slot sum ignore. Two launches: fill, then scatter.
+__global__ __launch_bounds__(256) void unsort_fill_kernel(int32_t* __restrict__ ids,
+                                                          float* __restrict__ w, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * 256) {
+        ids[i] = -1;
+        w[i] = 0.0f;
+    }
+}
+
+__global__ __launch_bounds__(256) void unsort_scatter_kernel(
+    const int32_t* __restrict__ sorted_ids, const float* __restrict__ sorted_w,
+    const int32_t* __restrict__ sorted_eids, const int32_t* __restrict__ num_valid,
+    int64_t capacity, int block_m, int32_t* __restrict__ ids, float* __restrict__ w,
+    int64_t tokens, int topk, int E) {
+    int64_t n = (int64_t)num_valid[0];
+    n = n < capacity ? n : capacity;
+    int64_t nt = (int64_t)num_valid[1];
+    nt = nt < tokens ? nt : tokens;
+    for (int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x; r < n;
+         r += (int64_t)gridDim.x * 256) {
+        const uint32_t id = (uint32_t)sorted_ids[r];
+        const int64_t t = (int64_t)(id & 0xFFFFFFu);
+        const int s = (int)(id >> 24);
+        if (t >= nt || s >= topk) continue;                 // padding entry
+        const int e = sorted_eids[r / block_m];
+        if (e < 0 || e >= E) continue;
+        ids[t * topk + s] = e;
+        w[t * topk + s] = sorted_w[r];
+    }
+}
+
+void launch_unsort(const int32_t* sorted_ids, const float* sorted_w, const int32_t* sorted_eids,
+                   const int32_t* num_valid, int64_t sorted_capacity, int64_t block_m,
+                   int32_t* topk_ids, float* topk_w, int64_t tokens, int64_t topk, int64_t E,
+                   hipStream_t stream) {
+    const int64_t n = tokens * topk;
+    if (n == 0) return;
+    hipLaunchKernelGGL(unsort_fill_kernel, dim3((unsigned)std::min<int64_t>(ceil_div(n, 256), 4096)),
+                       dim3(256), 0, stream, topk_ids, topk_w, n);
+    if (sorted_capacity > 0)
+        hipLaunchKernelGGL(unsort_scatter_kernel,
+                           dim3((unsigned)std::min<int64_t>(ceil_div(sorted_capacity, 256), 4096)),
+                           dim3(256), 0, stream, sorted_ids, sorted_w, sorted_eids, num_valid,
+                           sorted_capacity, (int)block_m, topk_ids, topk_w, tokens, (int)topk,
+                           (int)E);
+    AMD_HIP_CHECK(hipGetLastError());
 }
 
 }  // namespace aiter_amd

@@ -14,6 +14,9 @@
 // MI355X layout: 16 lanes x 8 elements (one 16-byte load each) cover a
 // group; a 256-thread block quantises 16 groups; the group amax is a 4-step
 // xor-shuffle inside the 16-lane quarter of the wave.
+#include <algorithm>
+#include <type_traits>
+
 #include "common.h"
 #include "quant_dev.h"
 
@@ -47,20 +50,48 @@ void launch_per_group_quant_fp8(const void* x, int x_dtype, void* q, float* scal
 }
 
 // ------------------------------------------- fp32 accumulator -> output ---
-// out[r, :] = round(acc[r, :]) for r < tokens (tokens = *num_valid[1]);
-// 8 elements per thread.
+template <bool kBf16>
+__device__ __forceinline__ float to_f32(uint16_t b) {
+    return kBf16 ? bf16_bits_to_f32(b) : fp16_bits_to_f32(b);
+}
+
+// a[0..7] += the 8 bf16 / fp16 values at p (16-byte aligned)
+template <bool kBf16>
+__device__ __forceinline__ void add_row8(float (&a)[8], const uint16_t* p) {
+    const v4i o = *reinterpret_cast<const v4i*>(p);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        a[2 * e] += to_f32<kBf16>((uint16_t)((uint32_t)o[e] & 0xFFFFu));
+        a[2 * e + 1] += to_f32<kBf16>((uint16_t)((uint32_t)o[e] >> 16));
+    }
+}
+
+// out[r, :] = round(acc[r, :] (+ addend[r, :])) for r < tokens (tokens =
+// *num_valid[1]); 8 elements per thread. addend may alias out: each thread
+// reads its own 8 elements before writing them.
 template <bool kBf16>
 __global__ __launch_bounds__(256) void acc_to_out_kernel(const float* __restrict__ acc,
-                                                         uint16_t* __restrict__ out,
+                                                         uint16_t* out,
                                                          const int32_t* __restrict__ num_valid,
-                                                         int64_t rows, int cols) {
+                                                         int64_t rows, int cols,
+                                                         const uint16_t* addend) {
     int64_t tokens = num_valid ? (int64_t)num_valid[1] : rows;
     tokens = tokens < rows ? tokens : rows;
     const int64_t n8 = tokens * cols / 8;
     for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n8;
          i += (int64_t)gridDim.x * 256) {
-        const v4f a = *reinterpret_cast<const v4f*>(acc + i * 8);
-        const v4f b = *reinterpret_cast<const v4f*>(acc + i * 8 + 4);
+        v4f a = *reinterpret_cast<const v4f*>(acc + i * 8);
+        v4f b = *reinterpret_cast<const v4f*>(acc + i * 8 + 4);
+        if (addend) {
+            const v4i o = *reinterpret_cast<const v4i*>(addend + i * 8);
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                a[2 * e] += to_f32<kBf16>((uint16_t)((uint32_t)o[e] & 0xFFFFu));
+                a[2 * e + 1] += to_f32<kBf16>((uint16_t)((uint32_t)o[e] >> 16));
+                b[2 * e] += to_f32<kBf16>((uint16_t)((uint32_t)o[2 + e] & 0xFFFFu));
+                b[2 * e + 1] += to_f32<kBf16>((uint16_t)((uint32_t)o[2 + e] >> 16));
+            }
+        }
         uint32_t w[4];
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
@@ -80,16 +111,16 @@ __global__ __launch_bounds__(256) void acc_to_out_kernel(const float* __restrict
 }
 
 void launch_acc_to_out(const float* acc, void* out, int out_dtype, const int32_t* num_valid,
-                       int64_t rows, int64_t cols, hipStream_t stream) {
+                       int64_t rows, int64_t cols, hipStream_t stream, const void* addend) {
     const int64_t n8 = rows * cols / 8;
     if (n8 == 0) return;
     const int blocks = (int)std::min<int64_t>(ceil_div(n8, 256), 8192);
     if (out_dtype == DT_BF16)
         hipLaunchKernelGGL(acc_to_out_kernel<true>, dim3(blocks), dim3(256), 0, stream, acc,
-                           (uint16_t*)out, num_valid, rows, (int)cols);
+                           (uint16_t*)out, num_valid, rows, (int)cols, (const uint16_t*)addend);
     else
         hipLaunchKernelGGL(acc_to_out_kernel<false>, dim3(blocks), dim3(256), 0, stream, acc,
-                           (uint16_t*)out, num_valid, rows, (int)cols);
+                           (uint16_t*)out, num_valid, rows, (int)cols, (const uint16_t*)addend);
     AMD_HIP_CHECK(hipGetLastError());
 }
 
@@ -109,8 +140,9 @@ __global__ __launch_bounds__(256) void slot_sum_kernel(const uint16_t* __restric
                                                        const int32_t* __restrict__ mask,
                                                        int num_experts,
                                                        const int32_t* __restrict__ num_valid,
-                                                       uint16_t* __restrict__ out, int64_t rows,
-                                                       int topk, int cols) {
+                                                       uint16_t* out, int64_t rows,
+                                                       int topk, int cols,
+                                                       const uint16_t* addend) {
     int64_t tokens = (int64_t)num_valid[1];
     tokens = tokens < rows ? tokens : rows;
     const int c8 = cols / 8;
@@ -156,6 +188,7 @@ __global__ __launch_bounds__(256) void slot_sum_kernel(const uint16_t* __restric
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 if (cc[h] >= c8) continue;
+                if (addend) add_row8<kBf16>(a[h], addend + t * cols + cc[h] * 8);
                 uint32_t w[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
@@ -182,7 +215,7 @@ template <bool kBf16>
 __global__ __launch_bounds__(256) void slot_sum_wave_kernel(
     const uint16_t* __restrict__ part, const int32_t* __restrict__ topk_ids,
     const int32_t* __restrict__ mask, int num_experts, const int32_t* __restrict__ num_valid,
-    uint16_t* __restrict__ out, int64_t rows, int topk, int cols) {
+    uint16_t* out, int64_t rows, int topk, int cols, const uint16_t* addend) {
     constexpr int kPieces = 8;
     int64_t tokens = (int64_t)num_valid[1];
     tokens = tokens < rows ? tokens : rows;
@@ -224,6 +257,7 @@ __global__ __launch_bounds__(256) void slot_sum_wave_kernel(
             for (int i = 0; i < kPieces; ++i) {
                 const int cc = base + 64 * i;
                 if (cc >= c8) continue;
+                if (addend) add_row8<kBf16>(a[i], addend + t * cols + cc * 8);
                 uint32_t w[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
@@ -240,7 +274,8 @@ __global__ __launch_bounds__(256) void slot_sum_wave_kernel(
 
 void launch_slot_sum(const uint16_t* part, const int32_t* topk_ids, const int32_t* mask,
                      int64_t num_experts, const int32_t* num_valid, void* out, int out_dtype,
-                     int64_t rows, int64_t topk, int64_t cols, hipStream_t stream) {
+                     int64_t rows, int64_t topk, int64_t cols, hipStream_t stream,
+                     const void* addend) {
     if (rows == 0 || cols == 0) return;
     // an expert mask means an expert-parallel share: most slots are not routed here
     const bool per_wave = mask != nullptr;
@@ -248,12 +283,109 @@ void launch_slot_sum(const uint16_t* part, const int32_t* topk_ids, const int32_
     auto go = [&](auto kern) {
         hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), 0, stream, part, topk_ids, mask,
                            (int)num_experts, num_valid, (uint16_t*)out, rows, (int)topk,
-                           (int)cols);
+                           (int)cols, (const uint16_t*)addend);
     };
     if (out_dtype == DT_BF16)
         per_wave ? go(slot_sum_wave_kernel<true>) : go(slot_sum_kernel<true>);
     else
         per_wave ? go(slot_sum_wave_kernel<false>) : go(slot_sum_kernel<false>);
+    AMD_HIP_CHECK(hipGetLastError());
+}
+
+// ------------------------------------------- act(gate) * up of fp32 rows ---
+// out[r, c] = act(x[r, c]) * x[r, d + c] for c < d: the gate | up rows of a
+// split-K stage 1 finished into the activation's output (the reference's
+// silu_and_mul / gelu_and_mul, csrc/kernels/activation_kernels.cu:24-90,
+// 337-354). Computed in fp32, rounded once to the output dtype. Rows of x
+// are 2d wide, rows of out d wide; 4 elements per thread when d % 4 == 0.
+template <typename TI>
+__device__ __forceinline__ float load_f32(const TI* p, int64_t i) {
+    if constexpr (sizeof(TI) == 4)
+        return p[i];
+    else if constexpr (std::is_same_v<TI, __bf16>)
+        return bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
+    else
+        return fp16_bits_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
+}
+
+template <typename TO>
+__device__ __forceinline__ void store_f32(TO* p, int64_t i, float v) {
+    if constexpr (sizeof(TO) == 4)
+        p[i] = v;
+    else if constexpr (std::is_same_v<TO, __bf16>)
+        reinterpret_cast<uint16_t*>(p)[i] = f32_to_bf16_bits(v);
+    else
+        reinterpret_cast<uint16_t*>(p)[i] = f32_to_fp16_bits(v);
+}
+
+template <typename TI, typename TO, int ACT>
+__global__ __launch_bounds__(256) void act_and_mul_kernel(const TI* __restrict__ x,
+                                                          TO* __restrict__ out, int64_t rows,
+                                                          int d) {
+    const int64_t n = rows * d;
+    for (int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4; i < n;
+         i += (int64_t)gridDim.x * 256 * 4) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int64_t j = i + u;
+            if (j >= n) break;
+            const int64_t r = j / d;
+            const int64_t c = j - r * d;
+            const float g = load_f32(x, r * 2 * d + c);
+            const float up = load_f32(x, r * 2 * d + d + c);
+            store_f32(out, j, (ACT == kActGelu ? gelu_f32(g) : silu_f32(g)) * up);
+        }
+    }
+}
+
+void launch_act_and_mul(const void* in, int in_dtype, void* out, int out_dtype, int64_t rows,
+                        int64_t d, int act, hipStream_t stream) {
+    const int64_t n = rows * d;
+    if (n == 0) return;
+    const int blocks = (int)std::min<int64_t>(ceil_div(n, 1024), 16384);
+    auto go = [&](auto ti, auto to) {
+        using TI = decltype(ti);
+        using TO = decltype(to);
+        if (act == kActGelu)
+            hipLaunchKernelGGL((act_and_mul_kernel<TI, TO, kActGelu>), dim3(blocks), dim3(256),
+                               0, stream, (const TI*)in, (TO*)out, rows, (int)d);
+        else
+            hipLaunchKernelGGL((act_and_mul_kernel<TI, TO, kActSilu>), dim3(blocks), dim3(256),
+                               0, stream, (const TI*)in, (TO*)out, rows, (int)d);
+    };
+    auto with_out = [&](auto ti) {
+        if (out_dtype == DT_FP32)
+            go(ti, float{});
+        else if (out_dtype == DT_BF16)
+            go(ti, __bf16{});
+        else
+            go(ti, _Float16{});
+    };
+    if (in_dtype == DT_FP32)
+        with_out(float{});
+    else if (in_dtype == DT_BF16)
+        with_out(__bf16{});
+    else
+        with_out(_Float16{});
+    AMD_HIP_CHECK(hipGetLastError());
+}
+
+// ------------------------------------------------------------- zero fill ---
+// A kernel, not hipMemsetAsync: the memory may be cleared inside a captured
+// HIP graph.
+__global__ __launch_bounds__(256) void zero_kernel(v4i* __restrict__ p, int64_t n16) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n16;
+         i += (int64_t)gridDim.x * 256)
+        p[i] = v4i{0, 0, 0, 0};
+}
+
+void launch_zero(void* p, int64_t bytes, hipStream_t stream) {
+    AMD_CHECK(bytes % 16 == 0 && (reinterpret_cast<uintptr_t>(p) & 15u) == 0,
+              "zero fill needs 16-byte aligned memory and size");
+    const int64_t n16 = bytes / 16;
+    if (n16 == 0) return;
+    const int blocks = (int)std::min<int64_t>(ceil_div(n16, 256), 8192);
+    hipLaunchKernelGGL(zero_kernel, dim3(blocks), dim3(256), 0, stream, (v4i*)p, n16);
     AMD_HIP_CHECK(hipGetLastError());
 }
 

@@ -13,7 +13,8 @@ A call clears the library's last error, calls, and raises RuntimeError with
 `aiter_get_last_error()` when the status is non-zero or an error was left.
 The stubs below carry the reference's names and signatures
 (aiter/ops/moe_sorting.py:11-25, aiter/ops/quant.py:472-481,
-aiter/ops/moe_op.py:15-42, 196-213, 319-340, aiter/ops/topk.py:15-38), so
+aiter/ops/moe_op.py:15-42, 172-213, 295-340, aiter/ops/activation.py:10-19,
+aiter/ops/topk.py:15-38), so
 a maintainer's own `compile_ops` stubs bind the same symbols unchanged.
 """
 from __future__ import annotations
@@ -226,6 +227,61 @@ def ck_moe_stage2(
 
 
 @ctypes_op
+def ck_moe_stage1(
+    hidden_states: Tensor,
+    w1: Tensor,
+    w2: Tensor,
+    sorted_token_ids: Tensor,
+    sorted_expert_ids: Tensor,
+    num_valid_ids: Tensor,
+    out: Tensor,
+    topk: int,
+    kernelName: Optional[str] = None,
+    w1_scale: Optional[Tensor] = None,
+    a1_scale: Optional[Tensor] = None,
+    block_m: Optional[int] = 32,
+    sorted_weights: Optional[Tensor] = None,
+    quant_type: int = 0,
+    activation: int = 0,
+    splitk: Optional[int] = 1,
+    use_non_temporal_load: bool = False,
+    dst_type: Optional[str] = None,
+    is_shuffled: bool = True,
+) -> None: ...
+
+
+@ctypes_op
+def silu_and_mul(out: Tensor, input: Tensor) -> None: ...
+
+
+@ctypes_op
+def gelu_and_mul(out: Tensor, input: Tensor) -> None: ...
+
+
+@ctypes_op
+def fmoe_fp8_blockscale_g1u1(
+    out: Tensor,
+    input: Tensor,
+    gate: Tensor,
+    down: Tensor,
+    sorted_token_ids: Tensor,
+    sorted_weights: Tensor,
+    sorted_expert_ids: Tensor,
+    num_valid_ids: Tensor,
+    topk: int,
+    input_scale: Tensor,
+    fc1_scale: Tensor,
+    fc2_scale: Tensor,
+    kernelName: Optional[str] = "",
+    fc_scale_blkn: int = 128,
+    fc_scale_blkk: int = 128,
+    fc2_smooth_scale: Optional[Tensor] = None,
+    activation: Optional[int] = ActivationType.Silu.value,
+    block_size_M: int = 32,
+) -> None: ...
+
+
+@ctypes_op
 def topk_softmax(
     topk_weights: Tensor,
     topk_indices: Tensor,
@@ -268,5 +324,6 @@ def biased_grouped_topk(
 
 
 ENTRIES = ("moe_sorting_fwd", "dynamic_per_token_scaled_quant", "moe_stage1_g1u1",
-           "ck_moe_stage2", "topk_softmax", "topk_sigmoid", "grouped_topk",
+           "ck_moe_stage1", "ck_moe_stage2", "silu_and_mul", "gelu_and_mul",
+           "fmoe_fp8_blockscale_g1u1", "topk_softmax", "topk_sigmoid", "grouped_topk",
            "biased_grouped_topk")

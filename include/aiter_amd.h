@@ -152,6 +152,77 @@ int aiter_amd_moe_stage2_a8w4(const void* a2, const float* a2_scale, const void*
                               int64_t topk, int64_t block_m, int64_t max_m_blocks,
                               int64_t w_shuffled, void* stream);
 
+/* Replaces ck_moe_stage1 (aiter/ops/moe_op.py:295-316 ->
+ * csrc/ck_gemm_moe_2stages_codegen/gemm_moe_ck2stages.cu:46-116) as the
+ * reference's ck_moe_stage1 wrapper calls it (aiter/fused_moe.py:1669-1725):
+ * stage 1 without the fused requant.
+ *   a1 [tokens, model_dim] fp8 with 1x128 scales (row-major [tokens,
+ *   model_dim/128], or [model_dim/128, tokens] when a1_scale_transposed);
+ *   w1 fp8 [E, 2*inter_dim, model_dim] with w1_scale f32 [E, 2*inter_dim/128,
+ *   model_dim/128], or MXFP4 as aiter_amd_moe_stage1_a8w4 with
+ *   w1_scale_e8m0 [E, 2*inter_dim, model_dim/32] (exactly one scale given).
+ *   out_form 1: out [tokens*topk, inter_dim] rows t*topk+slot of
+ *   act(gate) * up in out_dtype (bf16, fp16 or fp32), rounded once;
+ *   out_form 2: out [>= tokens*topk, 2*inter_dim] fp32 rows of gate | up
+ *   before the activation (the reference's splitk > 1 output, which
+ *   silu_and_mul / gelu_and_mul finish); ksplit > 1 (out_form 2 only, a
+ *   divisor of model_dim/128) splits each tile's K range that many ways,
+ *   whose partial sums are added into the rows, which the call zeroes first.
+ *   Pairs not routed here leave their rows unwritten (out_form 1; out_form 2
+ *   with ksplit > 1 leaves them zero).
+ *   block_m in {16, 32, 64, 128}; sorted_weights, activation, w_shuffled,
+ *   max_m_blocks as aiter_amd_moe_stage1_fp8_blockscale; model_dim <= 8192. */
+int aiter_amd_moe_stage1_rows(const void* a1, const float* a1_scale, int64_t a1_scale_transposed,
+                              const void* w1, const float* w1_scale,
+                              const uint8_t* w1_scale_e8m0, const int32_t* sorted_ids,
+                              const float* sorted_weights, const int32_t* sorted_expert_ids,
+                              const int32_t* num_valid_ids, void* out, int out_form,
+                              int out_dtype, int64_t tokens, int64_t model_dim,
+                              int64_t inter_dim, int64_t num_experts, int64_t topk,
+                              int64_t block_m, int64_t max_m_blocks, int64_t activation,
+                              int64_t ksplit, int64_t w_shuffled, void* stream);
+
+/* Replaces silu_and_mul / gelu_and_mul (aiter/ops/activation.py:10-19,
+ * csrc/kernels/activation_kernels.cu:24-90, 337-354):
+ * out[r, c] = act(input[r, c]) * input[r, d + c] for rows r < rows and
+ * c < d, input rows 2*d wide (fp32, bf16 or fp16), out rows d wide (fp32,
+ * bf16 or fp16), both contiguous; computed in fp32, rounded once.
+ * activation 0 Silu, 1 Gelu (exact erf). */
+int aiter_amd_act_and_mul(const void* input, int input_dtype, void* out, int out_dtype,
+                          int64_t rows, int64_t d, int64_t activation, void* stream);
+
+/* Bytes of workspace for aiter_amd_fused_moe_sorted_fp8_blockscale. */
+int64_t aiter_amd_fused_moe_sorted_workspace_bytes(int64_t tokens, int64_t model_dim,
+                                                   int64_t inter_dim, int64_t num_experts,
+                                                   int64_t global_experts, int64_t topk);
+
+/* The whole FP8 blockscale layer from a caller's sorted metadata and
+ * quantised activations, added into out: the work of fmoe_fp8_blockscale_g1u1
+ * (aiter/ops/moe_op.py:172-192, csrc/py_itfs_cu/asm_fmoe.cu:858-922) as
+ * fused_moe_1stage calls it (aiter/fused_moe.py:367-511).
+ *   a1 [tokens, model_dim] fp8, a1_scale as aiter_amd_moe_stage1_rows
+ *   (fused_moe_1stage passes them transposed); w1/w1_scale/w2/w2_scale as
+ *   the stage calls; sorted_ids / sorted_weights (sorted_capacity entries),
+ *   sorted_expert_ids and num_valid_ids as moe_sorting made them at
+ *   sorted_block_m, for num_experts experts (local ids under an expert mask);
+ *   global_experts: the experts the router spread the tokens over (a
+ *   block-size hint; num_experts when unknown).
+ *   out [tokens, model_dim] bf16/fp16: the layer is added to it (once, in
+ *   fp32, then rounded) for the first num_valid_ids[1] rows; the reference's
+ *   moe_buf arrives zeroed by moe_sorting.
+ *   The pairs are read back from the sorted entries and sorted again at the
+ *   block size this library picks for the shape, so the layer runs on the
+ *   same kernels as aiter_amd_fused_moe_fp8_blockscale (two GEMM launches),
+ *   whatever block size the caller sorted at. */
+int aiter_amd_fused_moe_sorted_fp8_blockscale(
+    const void* a1, const float* a1_scale, int64_t a1_scale_transposed, const void* w1,
+    const float* w1_scale, const void* w2, const float* w2_scale, const int32_t* sorted_ids,
+    const float* sorted_weights, const int32_t* sorted_expert_ids, const int32_t* num_valid_ids,
+    int64_t sorted_capacity, int64_t sorted_block_m, void* out, int out_dtype, int64_t tokens,
+    int64_t model_dim, int64_t inter_dim, int64_t num_experts, int64_t global_experts,
+    int64_t topk, int64_t activation, int64_t w_shuffled, void* workspace,
+    int64_t workspace_bytes, void* stream);
+
 /* Converts the stage-2 f32 accumulator into moe_buf (bf16 or fp16) for the
  * first num_valid_ids[1] rows.  The reference accumulates into moe_buf
  * directly (gemm_moe_ck2stages.cu:118-181); this is the finishing pass of the

@@ -13,7 +13,9 @@
  *   - tensor metadata (dtype, shape, strides, device) is validated before
  *     any device work, and the device is set from device_id for the call;
  *   - every buffer is owned by the caller; nothing here allocates device
- *     memory.
+ *     memory, except the workspace fmoe_fp8_blockscale_g1u1 needs and its
+ *     signature does not carry (held by the library per device and stream,
+ *     described there).
  * The error state is shared with the aiter_amd_* entry points of
  * include/aiter_amd.h, which these entries call after unpacking tensors.
  */
@@ -59,10 +61,13 @@ void aiter_clear_last_error(void);
  *   one chunk of tokens; here the chunk counts are kept in moe_buf, which a
  *   last launch clears, so nothing is allocated.  moe_buf must then hold
  *   them: aiter_amd_moe_sorting_workspace_bytes(M, topk, num_experts) <=
- *   M * row bytes (any row of 16 bytes or more at 256 experts and topk <= 8;
- *   about num_experts^2 / 8192 bytes per row for more experts); otherwise the
- *   call fails with an error and the caller uses aiter_amd_moe_sorting_fwd
- *   with a workspace. */
+ *   M * row bytes.  That is ceil(M / c) * num_experts * 4 bytes for the
+ *   chunk size c sorting picks (0 when M fits one chunk); c is 16 tokens for
+ *   129 to 2047 tokens at 256 experts, so rows need at least 4 * 256 / 16 =
+ *   64 bytes there, plus one chunk's counts (80-byte rows suffice from 129
+ *   tokens on; MiMo's 8192-byte rows always do); otherwise the call fails
+ *   with an error and the caller uses aiter_amd_moe_sorting_fwd with a
+ *   workspace. */
 int moe_sorting_fwd(aiter_tensor_t* topk_ids, aiter_tensor_t* topk_weights,
                     aiter_tensor_t* sorted_token_ids, aiter_tensor_t* sorted_weights,
                     aiter_tensor_t* sorted_expert_ids, aiter_tensor_t* num_valid_ids,
@@ -124,6 +129,75 @@ int ck_moe_stage2(aiter_tensor_t* inter_states, aiter_tensor_t* w1, aiter_tensor
                   int64_t block_m, aiter_tensor_t* sorted_weights, int64_t quant_type,
                   int64_t activation, int64_t splitk, int use_non_temporal_load,
                   const char* dst_type, int is_shuffled, void* stream);
+
+/* Replaces ck_moe_stage1 (aiter/ops/moe_op.py:295-316, host
+ * csrc/ck_gemm_moe_2stages_codegen/gemm_moe_ck2stages.cu:46-116), as the
+ * ck_moe_stage1 wrapper of aiter/fused_moe.py:1669-1725 calls it through
+ * ck_moe_stage1_fwd (aiter/ops/moe_op.py:534-575):
+ *   hidden_states fp8 [T, model_dim] with a1_scale f32 [T, model_dim/128]
+ *   (row-major: fused_moe_2stages quantises without transpose_scale for
+ *   this kernel); w1 fp8 [E, 2*inter_dim, model_dim] with w1_scale f32
+ *   [E, 2*inter_dim/128, model_dim/128] and quant_type per_1x128 (4), or
+ *   fp4x2 / u8 [E, 2*inter_dim, model_dim/2] with e8m0 / u8 w1_scale
+ *   [E, 2*inter_dim, model_dim/32] and quant_type per_1x32 (3);
+ *   splitk 0 or 1: out bf16 / fp16 [T, topk, inter_dim] receives
+ *   act(gate) * up (activation 0 Silu, 1 Gelu) rounded once;
+ *   splitk > 1 (a divisor of model_dim/128): out fp32 [>= T*topk,
+ *   2*inter_dim] receives the gate | up sums before the activation in rows
+ *   t*topk + slot (zeroed first, as the reference's KBatch > 1 kernel
+ *   does), which silu_and_mul / gelu_and_mul then finish;
+ *   sorted_weights f32 or NULL (doweight_stage1: gate and up scaled before
+ *   the activation); block_m 16, 32, 64 or 128; is_shuffled: the (16,16)
+ *   weight layout; kernelName, use_non_temporal_load and dst_type are
+ *   accepted and ignored; w2 is unused. */
+int ck_moe_stage1(aiter_tensor_t* hidden_states, aiter_tensor_t* w1, aiter_tensor_t* w2,
+                  aiter_tensor_t* sorted_token_ids, aiter_tensor_t* sorted_expert_ids,
+                  aiter_tensor_t* num_valid_ids, aiter_tensor_t* out, int64_t topk,
+                  const char* kernelName, aiter_tensor_t* w1_scale, aiter_tensor_t* a1_scale,
+                  int64_t block_m, aiter_tensor_t* sorted_weights, int64_t quant_type,
+                  int64_t activation, int64_t splitk, int use_non_temporal_load,
+                  const char* dst_type, int is_shuffled, void* stream);
+
+/* Replace silu_and_mul / gelu_and_mul (aiter/ops/activation.py:10-19,
+ * csrc/kernels/activation_kernels.cu:24-90, 337-354): input [..., 2*d]
+ * fp32 / bf16 / fp16, out [..., d] fp32 / bf16 / fp16 (same rows, both
+ * contiguous), out = act(input[..., :d]) * input[..., d:], computed in fp32
+ * and rounded once. */
+int silu_and_mul(aiter_tensor_t* out, aiter_tensor_t* input, void* stream);
+int gelu_and_mul(aiter_tensor_t* out, aiter_tensor_t* input, void* stream);
+
+/* Replaces fmoe_fp8_blockscale_g1u1 (aiter/ops/moe_op.py:172-192,
+ * csrc/py_itfs_cu/asm_fmoe.cu:858-922), as fused_moe_1stage calls it
+ * (aiter/fused_moe.py:367-511), the reference's default for FP8 blockscale
+ * above 32 tokens:
+ *   out bf16 / fp16 [T, model_dim] = moe_buf, which moe_sorting_fwd zeroed:
+ *   the layer is added to it (in fp32, rounded once) for the first
+ *   num_valid_ids[1] rows; input fp8 [T, model_dim] with input_scale f32 in
+ *   the transposed layout [model_dim/128, T] (per_group_quant_hip with
+ *   transpose_scale); gate fp8 [E, 2*inter_dim, model_dim] and down fp8
+ *   [E, model_dim, inter_dim] in the (16,16) shuffled layout (the layout
+ *   the replaced kernel reads; the signature carries no flag); fc1_scale f32
+ *   [E, 2*inter_dim/128, model_dim/128], fc2_scale f32 [E, model_dim/128,
+ *   inter_dim/128]; sorted_* and num_valid_ids from moe_sorting at
+ *   block_size_M; fc_scale_blkn = fc_scale_blkk = 128; fc2_smooth_scale
+ *   NULL; activation 0 Silu, 1 Gelu; kernel_name accepted and ignored.
+ * The pairs are recovered from the sorted entries and the layer runs as
+ * aiter_amd_fused_moe_sorted_fp8_blockscale (include/aiter_amd.h): two GEMM
+ * launches at this library's block size for the shape. Its intermediates
+ * live in a device workspace the library holds per (device, stream) and
+ * grows with hipMalloc when a larger layer arrives; growing is refused
+ * during HIP graph capture (one call of that size before capturing avoids
+ * it). About 0.7 GB at T = 8192 for MiMo dims (hidden 4096, inter 2048,
+ * top-8). */
+int fmoe_fp8_blockscale_g1u1(aiter_tensor_t* out, aiter_tensor_t* input, aiter_tensor_t* gate,
+                             aiter_tensor_t* down, aiter_tensor_t* sorted_token_ids,
+                             aiter_tensor_t* sorted_weights, aiter_tensor_t* sorted_expert_ids,
+                             aiter_tensor_t* num_valid_ids, int64_t topk,
+                             aiter_tensor_t* input_scale, aiter_tensor_t* fc1_scale,
+                             aiter_tensor_t* fc2_scale, const char* kernel_name,
+                             int64_t fc_scale_blkn, int64_t fc_scale_blkk,
+                             aiter_tensor_t* fc2_smooth_scale, int64_t activation,
+                             int64_t block_size_M, void* stream);
 
 /* Replaces topk_softmax (aiter/ops/moe_op.py:15-24): gating_output
  * [M, E] f32/bf16/fp16 -> topk_weights f32 [M, k], topk_indices i32 [M, k]

@@ -177,3 +177,78 @@ def test_python_binder_raises_with_the_library_message():
                             torch.zeros(2, dtype=torch.int32),
                             torch.zeros(4, 128, dtype=torch.bfloat16), 4, 4)
     assert AITER_DTYPE[torch.uint8] == 11
+
+
+def test_reference_sequence_entries_reject_bad_descriptors(lib):
+    """ck_moe_stage1, silu_and_mul / gelu_and_mul and fmoe_fp8_blockscale_g1u1
+    check their descriptors the way the other entries do (before any device
+    work or workspace allocation)."""
+    T, H, I, E, k, bm = 16, 512, 256, 8, 2, 16
+    cap = T * k + E * bm - k
+    sid = torch.zeros(cap, dtype=torch.int32)
+    sw = torch.zeros(cap)
+    se = torch.zeros((cap + bm - 1) // bm, dtype=torch.int32)
+    nv = torch.zeros(2, dtype=torch.int32)
+    a1 = torch.zeros(T, H, dtype=torch.float8_e4m3fn)
+    a1s = torch.ones(T, H // 128)
+    w1 = torch.zeros(E, 2 * I, H, dtype=torch.float8_e4m3fn)
+    w2 = torch.zeros(E, H, I, dtype=torch.float8_e4m3fn)
+    s1 = torch.ones(E, 2 * I // 128, H // 128)
+    s2 = torch.ones(E, H // 128, I // 128)
+    a2 = torch.zeros(T, k, I, dtype=torch.bfloat16)
+    base = [a1, w1, w2, sid, se, nv, a2, k, "", s1, a1s, bm, None, 4, 0, 0, False, "", True]
+
+    def stage1(**over):
+        args = list(base)
+        names = ["hidden_states", "w1", "w2", "sid", "se", "nv", "out", "topk", "kernelName",
+                 "w1_scale", "a1_scale", "block_m", "sorted_weights", "quant_type",
+                 "activation", "splitk", "nt", "dst_type", "is_shuffled"]
+        for key, v in over.items():
+            args[names.index(key)] = v
+        return _call_like_the_reference(lib, "ck_moe_stage1", *args)
+
+    rc, err = stage1(quant_type=3)
+    assert rc == -1 and "fp8 w1 needs QuantType.per_1x128" in err
+    rc, err = stage1(out=torch.zeros(T, k, I))
+    assert rc == -1 and "out must be bf16 or fp16" in err
+    rc, err = stage1(splitk=2)          # split K writes fp32 gate|up rows
+    assert rc == -1 and "out must be fp32" in err
+    rc, err = stage1(splitk=2, out=torch.zeros(T * k, I))
+    assert rc == -1 and "with splitk > 1, out must be fp32" in err
+    rc, err = stage1(splitk=3, out=torch.zeros(T * k, 2 * I))
+    assert rc == -1 and "ksplit must divide model_dim / 128" in err
+    rc, err = stage1(block_m=48)
+    assert rc == -1 and "block_m must be 16, 32, 64 or 128" in err
+    rc, err = stage1(activation=2)
+    assert rc == -1 and "ActivationType.Silu (0) and Gelu (1)" in err
+    rc, err = stage1(w1_scale=torch.ones(E, 2 * I // 128, 1))
+    assert rc == -1 and "w1_scale must be [8, 4, 4]" in err
+
+    rc, err = _call_like_the_reference(lib, "silu_and_mul", torch.zeros(4, 10),
+                                       torch.zeros(4, 21))
+    assert rc == -1 and "twice out's" in err
+    rc, err = _call_like_the_reference(lib, "gelu_and_mul", torch.zeros(4, 10, dtype=torch.int32),
+                                       torch.zeros(4, 20))
+    assert rc == -1 and "out must be fp32 or bf16 or fp16" in err
+    rc, err = _call_like_the_reference(lib, "silu_and_mul", torch.zeros(4, 10),
+                                       torch.zeros(8, 20)[::2])
+    assert rc == -1 and "input must be contiguous" in err
+
+    out = torch.zeros(T, H, dtype=torch.bfloat16)
+    fm = [out, a1, w1, w2, sid, sw, se, nv, k, a1s.t().contiguous(), s1, s2, "", 128, 128, None,
+          0, bm]
+    rc, err = _call_like_the_reference(lib, "fmoe_fp8_blockscale_g1u1", *fm[:13], 64, *fm[14:])
+    assert rc == -1 and "only 128x128 weight scale blocks" in err
+    rc, err = _call_like_the_reference(lib, "fmoe_fp8_blockscale_g1u1", *fm[:15], s2, *fm[16:])
+    assert rc == -1 and "fc2_smooth_scale is not supported" in err
+    rc, err = _call_like_the_reference(lib, "fmoe_fp8_blockscale_g1u1", *fm[:3],
+                                       torch.zeros(E, H, I + 128, dtype=torch.float8_e4m3fn),
+                                       *fm[4:])
+    assert rc == -1 and "down must be [8, 512, 256]" in err
+    rc, err = _call_like_the_reference(lib, "fmoe_fp8_blockscale_g1u1",
+                                       torch.zeros(T, H), *fm[1:])
+    assert rc == -1 and "out must be bf16 or fp16" in err
+    rc, err = _call_like_the_reference(lib, "fmoe_fp8_blockscale_g1u1", *fm[:6], se[:2], *fm[7:])
+    assert rc == -1 and "sorted_expert_ids holds fewer blocks" in err
+    rc, err = _call_like_the_reference(lib, "fmoe_fp8_blockscale_g1u1", *fm[:16], 2, bm)
+    assert rc == -1 and "Silu (0) and Gelu (1)" in err
