@@ -82,6 +82,8 @@ _SIGNATURES = {
     ),
     "aiter_amd_moe_acc_to_out": (c_int, [c_vp, c_vp, c_int, c_vp, c_i64, c_i64, c_vp]),
     "aiter_amd_fused_moe_workspace_bytes": (c_i64, [c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64]),
+    "aiter_amd_fused_moe_workspace_a2_offsets": (
+        c_int, [c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_vp]),
     "aiter_amd_fused_moe_fp8_blockscale": (
         c_int,
         [c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_i64, c_i64,

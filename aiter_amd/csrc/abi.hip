@@ -844,6 +844,25 @@ int64_t aiter_amd_fused_moe_workspace_bytes(int64_t tokens, int64_t model_dim, i
         .total;
 }
 
+int aiter_amd_fused_moe_workspace_a2_offsets(int64_t tokens, int64_t model_dim,
+                                             int64_t inter_dim, int64_t num_experts,
+                                             int64_t global_experts, int64_t topk,
+                                             int64_t block_m, int64_t* offsets) {
+    return safe_call([&] {
+        AMD_CHECK(offsets != nullptr, "offsets is NULL");
+        AMD_CHECK(tokens >= 0 && model_dim > 0 && inter_dim > 0 && num_experts >= 1 &&
+                      topk >= 1 && global_experts >= num_experts,
+                  "invalid layer dimensions");
+        if (block_m <= 0)
+            block_m = default_block_m(tokens, topk, num_experts, global_experts, model_dim,
+                                      inter_dim);
+        const FusedLayout L =
+            fused_layout(tokens, model_dim, inter_dim, global_experts, num_experts, topk, block_m);
+        offsets[0] = L.off_a2;
+        offsets[1] = L.off_a2_scale;
+    });
+}
+
 int aiter_amd_fused_moe_fp8_blockscale(const void* hidden_states, int hidden_dtype,
                                        const void* w1, const float* w1_scale, const void* w2,
                                        const float* w2_scale, const float* topk_weights,

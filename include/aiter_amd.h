@@ -241,6 +241,20 @@ int64_t aiter_amd_fused_moe_workspace_bytes(int64_t tokens, int64_t model_dim,
                                             int64_t global_experts, int64_t topk,
                                             int64_t block_m);
 
+/* No counterpart in the reference.  Where the two-launch one-call layer
+ * (aiter_amd_fused_moe_fp8_blockscale / aiter_amd_fused_moe_a8w4, not the
+ * _1stage entries) keeps its stage-1 output in the caller's workspace, for
+ * callers that inspect the intermediate (parity tests, debugging): after a
+ * call with these sizes, the fp8 a2 [tokens*topk, inter_dim] (row
+ * t*topk + slot) starts offsets[0] bytes into the workspace and its f32
+ * 1x128 scales [tokens*topk, inter_dim/128] offsets[1] bytes in.  Rows of
+ * pairs not routed to a local expert hold no data.  Arguments as
+ * aiter_amd_fused_moe_workspace_bytes. */
+int aiter_amd_fused_moe_workspace_a2_offsets(int64_t tokens, int64_t model_dim,
+                                             int64_t inter_dim, int64_t num_experts,
+                                             int64_t global_experts, int64_t topk,
+                                             int64_t block_m, int64_t* offsets);
+
 /* The whole 2-stage FP8 blockscale MoE in one call; replaces the sequence
  * of fused_moe_ -> moe_sorting -> fused_moe_2stages (aiter/fused_moe.py:
  * 205-364, 27-103, 1103-1334) for quant_type per_1x128 / per_128x128.

@@ -127,6 +127,30 @@ def test_fused_validation_errors(lib):
     assert lib.aiter_amd_fused_moe_workspace_bytes(64, 4096, 2048, 32, 16, 8, 0) == -1
 
 
+def test_workspace_a2_offsets_lie_inside_the_workspace():
+    """The a2 section the one-call layer exposes: 256-byte aligned, the
+    fp8 rows [T*k, I] before their f32 scales [T*k, I/128], both inside the
+    workspace the size query reports, at every block size and for an EP
+    share; invalid sizes are rejected."""
+    import ctypes
+    for T, H, I, E, G, k in ((8192, 4096, 2048, 256, 256, 8), (4096, 4096, 2048, 32, 256, 8),
+                             (1, 1024, 512, 8, 8, 2), (0, 4096, 2048, 256, 256, 8)):
+        for bm in (0, 16, 32, 64, 128):
+            off = (ctypes.c_int64 * 2)()
+            _abi.call("aiter_amd_fused_moe_workspace_a2_offsets", T, H, I, E, G, k, bm,
+                      ctypes.addressof(off))
+            ws = _abi.query("aiter_amd_fused_moe_workspace_bytes", T, H, I, E, G, k, bm)
+            a2, a2s = off[0], off[1]
+            assert a2 % 256 == 0 and a2s % 256 == 0
+            assert a2 + T * k * I <= a2s
+            assert a2s + T * k * (I // 128) * 4 <= ws
+    off = (ctypes.c_int64 * 2)()
+    _expect_error("aiter_amd_fused_moe_workspace_a2_offsets", 64, 4096, 2048, 32, 16, 8, 0,
+                  ctypes.addressof(off), match="invalid layer dimensions")
+    _expect_error("aiter_amd_fused_moe_workspace_a2_offsets", 64, 4096, 2048, 32, 32, 8, 0,
+                  None, match="offsets is NULL")
+
+
 def test_workspace_query_resolves_block_m_like_the_layer(lib):
     """block_m = 0 resolves the same way in the workspace query and the
     one-call entries, from the routed rows per expert over all the router's
