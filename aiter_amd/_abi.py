@@ -34,6 +34,9 @@ _SIGNATURES = {
     "aiter_amd_layer_timing_end": (c_i64, [c_vp, c_i64]),
     "aiter_amd_topk_softmax": (
         c_int, [c_vp, c_int, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_int, c_vp]),
+    "aiter_amd_topk_softmax_shared": (
+        c_int, [c_vp, c_int, c_i64, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_int,
+                c_vp]),
     "aiter_amd_topk_sigmoid": (
         c_int, [c_vp, c_int, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp]),
     "aiter_amd_grouped_topk": (

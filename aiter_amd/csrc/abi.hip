@@ -109,7 +109,8 @@ bool route_supported(int64_t E, int64_t k);
 void launch_moe_route(const void* gating, int dtype, int64_t M, int64_t E, int64_t k, int mode,
                       int need_renorm, int softmax_scores, int64_t n_group, int64_t topk_group,
                       float scaling, const float* bias, float* w, int64_t ws, int32_t* ids,
-                      int64_t is, int32_t* tei, hipStream_t stream);
+                      int64_t is, int32_t* tei, hipStream_t stream, int64_t gating_stride = 0,
+                      int64_t num_shared = 0);
 
 // moe_gemm_prefill.hip (64/128-row M-blocks, weight fragments in registers)
 bool prefill_supported(int64_t block_m, int64_t K);
@@ -1142,6 +1143,27 @@ int aiter_amd_topk_softmax(const void* gating, int gating_dtype, int64_t tokens,
         launch_moe_route(gating, gating_dtype, tokens, num_experts, topk, 0, need_renorm != 0, 0,
                          1, 1, 1.0f, nullptr, topk_weights, weights_stride, topk_ids, ids_stride,
                          token_expert_indices, (hipStream_t)stream);
+    });
+}
+
+int aiter_amd_topk_softmax_shared(const void* gating, int gating_dtype, int64_t tokens,
+                                  int64_t num_experts, int64_t num_shared_experts,
+                                  int64_t topk, float* topk_weights, int64_t weights_stride,
+                                  int32_t* topk_ids, int64_t ids_stride,
+                                  int32_t* token_expert_indices, int need_renorm,
+                                  void* stream) {
+    return safe_call([&] {
+        AMD_CHECK(num_shared_experts >= 0 && num_shared_experts <= kMaxExperts,
+                  "num_shared_experts must be in [0, " + std::to_string(kMaxExperts) + "]");
+        check_route(gating, gating_dtype, tokens, num_experts, topk, topk_weights,
+                    weights_stride, topk_ids, ids_stride);
+        AMD_CHECK(weights_stride >= topk + num_shared_experts,
+                  "topk_weights rows must hold topk + num_shared_experts weights");
+        if (tokens == 0) return;
+        launch_moe_route(gating, gating_dtype, tokens, num_experts, topk, 0, need_renorm != 0, 0,
+                         1, 1, 1.0f, nullptr, topk_weights, weights_stride, topk_ids, ids_stride,
+                         token_expert_indices, (hipStream_t)stream,
+                         num_experts + num_shared_experts, num_shared_experts);
     });
 }
 

@@ -544,20 +544,38 @@ int topk_softmax(aiter_tensor_t* topk_weights, aiter_tensor_t* topk_indices,
                  int need_renorm, int64_t num_shared_experts,
                  const char* shared_expert_scoring_func, void* stream) {
     return safe_call([&] {
-        AMD_CHECK(num_shared_experts == 0 &&
-                      (!shared_expert_scoring_func || !shared_expert_scoring_func[0]),
-                  "the shared-expert fusion of topk_softmax is not provided");
+        const bool func = shared_expert_scoring_func && shared_expert_scoring_func[0];
+        AMD_CHECK(num_shared_experts >= 0, "num_shared_experts must be >= 0");
+        AMD_CHECK(!func || std::string(shared_expert_scoring_func) == "sigmoid",
+                  std::string("Only 'sigmoid' scoring function is supported for shared experts, "
+                              "got: ") + (func ? shared_expert_scoring_func : ""));
+        AMD_CHECK(num_shared_experts == 0 || func,
+                  "num_shared_experts > 0 needs shared_expert_scoring_func 'sigmoid'");
         const int dev = need(gating_output, "gating_output").device_id;
-        int64_t M, k;
-        route_outputs(topk_weights, topk_indices, dev, M, k);
+        const auto& tiw = need(topk_weights, "topk_weights");
+        const auto& tii = need(topk_indices, "topk_indices");
+        check_dtype(tiw, "topk_weights", {DT_FP32});
+        check_dtype(tii, "topk_indices", {DT_I32});
+        check_device(tiw, dev, "topk_weights");
+        check_device(tii, dev, "topk_indices");
+        // topk_weights [M, topk + shared], topk_indices [M, topk]
+        AMD_CHECK(tiw.ndim == 2 && tii.ndim == 2 && tiw.shape[0] == tii.shape[0] &&
+                      tiw.shape[1] == tii.shape[1] + num_shared_experts,
+                  "topk_weights must be [M, topk + num_shared_experts] and topk_indices "
+                  "[M, topk]");
+        AMD_CHECK(tiw.strides[1] == 1 && tii.strides[1] == 1,
+                  "topk_weights / topk_indices rows must be contiguous");
+        const int64_t M = tii.shape[0], k = tii.shape[1];
         const auto& x = gating(gating_output, M);
+        AMD_CHECK(x.shape[1] > num_shared_experts,
+                  "gating_output must hold the routed experts, then the shared ones");
         const auto* tei = optional(token_expert_indices, "token_expert_indices", dev, {DT_I32});
         if (tei) check_shape(*tei, "token_expert_indices", {M, k});
         DeviceGuard guard(dev);
-        run(aiter_amd_topk_softmax(x.ptr, x.dtype_, M, x.shape[1], k, (float*)topk_weights->ptr,
-                                   topk_weights->strides[0], (int32_t*)topk_indices->ptr,
-                                   topk_indices->strides[0], (int32_t*)(tei ? tei->ptr : nullptr),
-                                   need_renorm, stream));
+        run(aiter_amd_topk_softmax_shared(
+            x.ptr, x.dtype_, M, x.shape[1] - num_shared_experts, num_shared_experts, k,
+            (float*)tiw.ptr, tiw.strides[0], (int32_t*)tii.ptr, tii.strides[0],
+            (int32_t*)(tei ? tei->ptr : nullptr), need_renorm, stream));
     });
 }
 

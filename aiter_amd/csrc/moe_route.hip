@@ -5,7 +5,9 @@
 //   * softmax top-k (topk_softmax, csrc/kernels/topk_softmax_kernels.cu:
 //     380-500; fused_topk, aiter/fused_moe.py:1853-1923): experts ranked by
 //     logit; weight exp(x - rowmax), divided by the sum over the k chosen
-//     (renormalise) or over the whole row (plain softmax);
+//     (renormalise) or over the whole row (plain softmax); optionally with
+//     shared experts after the routed ones in each gating row, whose sigmoid
+//     scores follow the k weights (topk_softmax_kernels.cu:326-353, 760-810);
 //   * sigmoid top-k (topk_sigmoid, op_tests/test_moe_topk_sigmoid.py:28-32):
 //     ranked by logit, weight sigmoid(x);
 //   * grouped top-k (grouped_topk, aiter/ops/topk.py:163-197): softmax or
@@ -52,6 +54,8 @@ struct Args {
     int32_t* ids;
     int64_t is;
     int32_t* tei;                 // optional token_expert_indices [M, k]
+    int64_t gs;                   // gating row stride (elements, >= E + ns)
+    int ns;                       // shared experts: gating columns E .. E+ns-1
 };
 
 __device__ __forceinline__ float load_logit(const void* p, int dtype, int64_t i) {
@@ -147,7 +151,7 @@ __global__ __launch_bounds__(64 * kWaves) void moe_route_kernel(Args g) {
 #pragma unroll
     for (int j = 0; j < V; ++j) {
         const int e = lane * V + j;
-        x[j] = e < E ? load_logit(g.gating, g.dtype, lrow * E + e) : NEG;
+        x[j] = e < E ? load_logit(g.gating, g.dtype, lrow * g.gs + e) : NEG;
     }
 
     // score s (what the weight is taken from) and ranking key per expert
@@ -293,6 +297,13 @@ __global__ __launch_bounds__(64 * kWaves) void moe_route_kernel(Args g) {
             if (g.tei) g.tei[row * k + t] = (int32_t)((int64_t)t * g.M + row);
         }
     }
+    // shared experts (topk_softmax's fusion, topk_softmax_kernels.cu:326-353):
+    // weight column k + j is sigmoid of gating column E + j, outside the
+    // ranking and the renormalisation
+    for (int j = lane; j < g.ns; j += LPR)
+        if (live)
+            g.w[row * g.ws + k + j] =
+                sigmoid_f32(load_logit(g.gating, g.dtype, row * g.gs + E + j));
 }
 
 }  // namespace route
@@ -304,8 +315,11 @@ bool route_supported(int64_t E, int64_t k) {
 void launch_moe_route(const void* gating, int dtype, int64_t M, int64_t E, int64_t k, int mode,
                       int need_renorm, int softmax_scores, int64_t n_group, int64_t topk_group,
                       float scaling, const float* bias, float* w, int64_t ws, int32_t* ids,
-                      int64_t is, int32_t* tei, hipStream_t stream) {
+                      int64_t is, int32_t* tei, hipStream_t stream, int64_t gating_stride,
+                      int64_t num_shared) {
     route::Args g{};
+    g.gs = gating_stride > 0 ? gating_stride : E;
+    g.ns = (int)num_shared;
     g.gating = gating;
     g.dtype = dtype;
     g.M = M;

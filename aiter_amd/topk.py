@@ -5,7 +5,8 @@ Mirrors aiter's routing surface, with the same argument names, in-place
 outputs and return values:
 
 * ``topk_softmax(topk_weights, topk_indices, token_expert_indices,
-  gating_output, need_renorm)`` -- aiter/ops/moe_op.py:15-36;
+  gating_output, need_renorm, num_shared_experts=0,
+  shared_expert_scoring_func="")`` -- aiter/ops/moe_op.py:15-36;
 * ``topk_sigmoid(topk_weights, topk_indices, gating_output)`` --
   aiter/ops/moe_op.py:39-42;
 * ``grouped_topk(gating_output, topk_weights, topk_ids, num_expert_group,
@@ -52,18 +53,34 @@ def _check(gating_output: torch.Tensor, topk_weights: torch.Tensor, topk_ids: to
 
 def topk_softmax(topk_weights: torch.Tensor, topk_indices: torch.Tensor,
                  token_expert_indices: Optional[torch.Tensor], gating_output: torch.Tensor,
-                 need_renorm: bool) -> None:
+                 need_renorm: bool, num_shared_experts: int = 0,
+                 shared_expert_scoring_func: str = "") -> None:
     """Experts ranked by logit (ties: lower index first); weight
     exp(x - rowmax) divided by the sum over the topk (need_renorm) or over
     the whole row; token_expert_indices[t, j] = j * tokens + t
-    (csrc/kernels/topk_softmax_kernels.cu:380-500)."""
-    M, E, k = _check(gating_output, topk_weights, topk_indices)
+    (csrc/kernels/topk_softmax_kernels.cu:380-500).
+
+    With num_shared_experts = S > 0 and shared_expert_scoring_func
+    "sigmoid" (the only one the reference supports), gating_output is
+    [tokens, E + S]: the first E columns are routed as above and
+    topk_weights [tokens, topk + S] receives sigmoid(gating_output[:, E + j])
+    in column topk + j (topk_softmax_kernels.cu:326-353, 760-810)."""
+    S = int(num_shared_experts)
+    if S == 0:
+        M, E, k = _check(gating_output, topk_weights, topk_indices)
+    else:
+        if shared_expert_scoring_func != "sigmoid":
+            raise ValueError("Only 'sigmoid' scoring function is supported for shared experts, "
+                             f"got: {shared_expert_scoring_func!r}")
+        if topk_weights.dim() != 2 or topk_weights.shape[1] != topk_indices.shape[-1] + S:
+            raise ValueError("topk_weights must be [tokens, topk + num_shared_experts]")
+        M, _, k = _check(gating_output, topk_weights[:, :topk_indices.shape[-1]], topk_indices)
     if token_expert_indices is not None:
         if (token_expert_indices.dtype != dtypes.i32 or not token_expert_indices.is_contiguous()
                 or tuple(token_expert_indices.shape) != (M, k)):
             raise ValueError("token_expert_indices must be a contiguous [tokens, topk] i32 tensor")
     ffi.topk_softmax(topk_weights, topk_indices, token_expert_indices, gating_output,
-                     bool(need_renorm))
+                     bool(need_renorm), S, shared_expert_scoring_func)
 
 
 def topk_sigmoid(topk_weights: torch.Tensor, topk_indices: torch.Tensor,

@@ -366,6 +366,22 @@ int aiter_amd_topk_softmax(const void* gating, int gating_dtype, int64_t tokens,
                            int64_t weights_stride, int32_t* topk_ids, int64_t ids_stride,
                            int32_t* token_expert_indices, int need_renorm, void* stream);
 
+/* Replaces topk_softmax with its shared-expert fusion (num_shared_experts > 0,
+ * shared_expert_scoring_func "sigmoid"; aiter/ops/moe_op.py:15-24,
+ * csrc/kernels/topk_softmax_kernels.cu:326-353, 760-810): gating rows hold
+ * num_experts routed logits then num_shared_experts shared ones (row stride
+ * num_experts + num_shared_experts, contiguous); the routed experts are
+ * ranked and weighted as aiter_amd_topk_softmax over the first num_experts
+ * columns, and topk_weights[t, topk + j] = sigmoid(gating[t, num_experts +
+ * j]) for j < num_shared_experts (weights_stride >= topk +
+ * num_shared_experts); topk_ids holds the routed experts only. */
+int aiter_amd_topk_softmax_shared(const void* gating, int gating_dtype, int64_t tokens,
+                                  int64_t num_experts, int64_t num_shared_experts,
+                                  int64_t topk, float* topk_weights, int64_t weights_stride,
+                                  int32_t* topk_ids, int64_t ids_stride,
+                                  int32_t* token_expert_indices, int need_renorm,
+                                  void* stream);
+
 /* Replaces topk_sigmoid (aiter/ops/moe_op.py:39-42; semantics
  * op_tests/test_moe_topk_sigmoid.py:28-32): experts ranked by logit, weight
  * sigmoid(logit). */

@@ -199,11 +199,15 @@ int fmoe_fp8_blockscale_g1u1(aiter_tensor_t* out, aiter_tensor_t* input, aiter_t
                              aiter_tensor_t* fc2_smooth_scale, int64_t activation,
                              int64_t block_size_M, void* stream);
 
-/* Replaces topk_softmax (aiter/ops/moe_op.py:15-24): gating_output
- * [M, E] f32/bf16/fp16 -> topk_weights f32 [M, k], topk_indices i32 [M, k]
- * (row strides taken from the tensors), token_expert_indices i32 [M, k] or
- * NULL; num_shared_experts must be 0 and shared_expert_scoring_func empty
- * or NULL (the shared-expert fusion is not provided). */
+/* Replaces topk_softmax (aiter/ops/moe_op.py:15-24,
+ * csrc/kernels/topk_softmax_kernels.cu:760-810): gating_output
+ * [M, E + S] f32/bf16/fp16 (contiguous) -> topk_weights f32 [M, k + S],
+ * topk_indices i32 [M, k] (row strides taken from the tensors),
+ * token_expert_indices i32 [M, k] or NULL. The first E columns are ranked
+ * by softmax top-k; with S = num_shared_experts > 0 and
+ * shared_expert_scoring_func "sigmoid" (the only function the reference
+ * supports), topk_weights[:, k + j] = sigmoid(gating_output[:, E + j]).
+ * S > 0 with an empty function is an error, as is another function. */
 int topk_softmax(aiter_tensor_t* topk_weights, aiter_tensor_t* topk_indices,
                  aiter_tensor_t* token_expert_indices, aiter_tensor_t* gating_output,
                  int need_renorm, int64_t num_shared_experts,

@@ -11,6 +11,8 @@ the kernels do it:
   exp(x - rowmax) times 1/(sum of the k chosen) when renormalising, else
   times 1/(that sum + the sum over the other experts));
   token_expert_indices = rank * tokens + row (same file, 436-451);
+* topk_softmax_shared_ref -- the shared-expert fusion of topk_softmax
+  (same file, 326-353, 760-810);
 * topk_sigmoid_ref -- op_tests/test_moe_topk_sigmoid.py:28-32;
 * grouped_topk_ref -- aiter/ops/topk.py:163-197 (grouped, max per group)
   and 127-160 (biased: group score = sum of the two best choices), with the
@@ -48,6 +50,18 @@ def topk_softmax_ref(logits: np.ndarray, k: int, renorm: bool):
     w = (numer * scale).astype(F32)
     tei = (np.arange(k, dtype=np.int64)[None, :] * M + np.arange(M)[:, None]).astype(np.int32)
     return w, ids.astype(np.int32), tei
+
+
+def topk_softmax_shared_ref(logits: np.ndarray, k: int, renorm: bool, num_shared: int):
+    """topk_softmax with its shared-expert fusion (topk_softmax_kernels.cu:
+    326-353, 760-810): the first E = columns - num_shared logits are routed
+    by topk_softmax_ref; the weights gain num_shared columns
+    sigmoid(logit) of the last num_shared logits, 1 / (1 + exp(-x)) in fp32."""
+    x = np.asarray(logits, dtype=F32)
+    E = x.shape[1] - num_shared
+    w, ids, tei = topk_softmax_ref(x[:, :E], k, renorm)
+    sh = (F32(1) / (F32(1) + np.exp(-x[:, E:]).astype(F32))).astype(F32)
+    return np.concatenate([w, sh], axis=1), ids, tei
 
 
 def topk_sigmoid_ref(logits: np.ndarray, k: int):

@@ -164,10 +164,16 @@ def test_entries_reject_bad_descriptors_before_device_work(lib):
                                        torch.zeros(4, 256, dtype=torch.bfloat16),
                                        torch.zeros(8), None, False, None, 1)
     assert rc == -1 and "viewed as [groups, 128]" in err
-    rc, err = _call_like_the_reference(lib, "topk_softmax", torch.zeros(4, 2),
+    # shared experts: the reference's only scoring function is sigmoid, and
+    # num_shared_experts > 0 with no function is an error
+    rc, err = _call_like_the_reference(lib, "topk_softmax", torch.zeros(4, 3),
                                        torch.zeros(4, 2, dtype=torch.int32), None,
-                                       torch.zeros(4, 8), True, 1, "")
-    assert rc == -1 and "shared-expert fusion" in err
+                                       torch.zeros(4, 9), True, 1, "")
+    assert rc == -1 and "needs shared_expert_scoring_func 'sigmoid'" in err
+    rc, err = _call_like_the_reference(lib, "topk_softmax", torch.zeros(4, 3),
+                                       torch.zeros(4, 2, dtype=torch.int32), None,
+                                       torch.zeros(4, 9), True, 1, "softmax")
+    assert rc == -1 and "Only 'sigmoid' scoring function" in err
 
 
 def test_python_binder_raises_with_the_library_message():

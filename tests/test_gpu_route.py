@@ -52,6 +52,36 @@ def test_topk_softmax_parity(cuda_device, E, k, dtype, renorm):
     assert (_np(wbuf[:, k:]) == -7).all() and (_np(ibuf[:, k:]) == -7).all()
 
 
+@pytest.mark.parametrize("E,S,k", [(256, 1, 8), (256, 2, 8), (128, 8, 6), (60, 4, 4),
+                                   (512, 1, 8)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("renorm", [True, False])
+def test_topk_softmax_shared_experts(cuda_device, E, S, k, dtype, renorm):
+    """topk_softmax's shared-expert fusion against the oracle: routed ids and
+    token_expert_indices bit-exact, weights (routed and shared sigmoid)
+    within rtol 2e-6, through the Python op and the reference-shaped ctypes
+    entry; the shared logits are raised so they would win if they were
+    ranked; the padding columns of strided outputs stay untouched."""
+    M = 700
+    x = _logits(M, E + S, dtype, E * 5 + S, cuda_device)
+    x[:, E:] += 8.0
+    wbuf = torch.full((M, k + S + 3), -7.0, device=cuda_device)
+    w = wbuf[:, :k + S]
+    ids, ibuf = _strided(M, k, torch.int32, cuda_device, 5)
+    tei = torch.empty(M, k, dtype=torch.int32, device=cuda_device)
+    A.topk_softmax(w, ids, tei, x, renorm, S, "sigmoid")
+    rw, rids, rtei = RR.topk_softmax_shared_ref(_np(x.float()), k, renorm, S)
+    assert np.array_equal(_np(ids), rids)
+    assert np.array_equal(_np(tei), rtei)
+    np.testing.assert_allclose(_np(w), rw, rtol=2e-6, atol=1e-9)
+    assert (_np(wbuf[:, k + S:]) == -7).all() and (_np(ibuf[:, k:]) == -7).all()
+    from aiter_amd import ffi
+    w2 = torch.empty(M, k + S, device=cuda_device)
+    ids2 = torch.empty(M, k, dtype=torch.int32, device=cuda_device)
+    ffi.topk_softmax(w2, ids2, None, x, renorm, S, "sigmoid")
+    assert torch.equal(ids2, ids) and torch.equal(w2, w)
+
+
 def test_topk_softmax_ties_and_fused_topk(cuda_device):
     M, E, k = 64, 256, 8
     x = torch.zeros(M, E, device=cuda_device)

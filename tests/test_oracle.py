@@ -483,6 +483,32 @@ def test_route_topk_sigmoid_oracle():
         np.testing.assert_allclose(w[r], special.expit(x[r, ref].astype(np.float64)), rtol=2e-6)
 
 
+@pytest.mark.parametrize("S", [1, 2, 8])
+def test_route_topk_softmax_shared_oracle(S):
+    """The shared-expert fusion: routing over the first E columns only (a
+    large shared logit must not be picked, nor enter the softmax sum), and
+    sigmoid scores of the shared columns against scipy's expit in fp64."""
+    rng = np.random.default_rng(20 + S)
+    E, k = 64, 6
+    x = rng.standard_normal((25, E + S)).astype(np.float32) * 3
+    x[:, E:] += 10.0                             # would win every rank if routed
+    for renorm in (True, False):
+        w, ids, tei = RR.topk_softmax_shared_ref(x, k, renorm, S)
+        assert w.shape == (25, k + S) and ids.shape == (25, k)
+        assert (ids < E).all()
+        for r in range(25):
+            ref = _brute_rank(x[r, :E], k)
+            assert ids[r].tolist() == ref
+            p = special.softmax(x[r, :E].astype(np.float64))[ref]
+            if renorm:
+                p = p / p.sum()
+            np.testing.assert_allclose(w[r, :k], p, rtol=2e-6, atol=0)
+            np.testing.assert_allclose(w[r, k:], special.expit(x[r, E:].astype(np.float64)),
+                                       rtol=2e-6)
+    np.testing.assert_allclose(RR.topk_softmax_shared_ref(np.zeros((1, 9), np.float32), 2, True,
+                                                          1)[0][0, 2], 0.5)
+
+
 def _grouped_brute(x, k, n_group, topk_group, renorm, softmax, scaling, bias):
     """Per-row python loops in fp64 (the structure of aiter/ops/topk.py:127-197)."""
     xs = x.astype(np.float64)
