@@ -242,7 +242,10 @@ def select_run_1stage(tokens: int, topk: int, num_experts: int, model_dim: int,
     the role of the reference's fused_moe_1stage): AITER_AMD_FUSED=0/1 when
     set, else the tuned table's run_1stage for this shape (the reference's
     cfg["run_1stage"], aiter/fused_moe.py:903-911). The one-launch kernel
-    runs 16/32-row M-blocks with model_dim a multiple of 256 up to 8192."""
+    runs 16/32-row M-blocks with model_dim a multiple of 256 up to 8192.
+    The table's run_1stage was measured at the row's own block_m, so it is
+    honoured only when the layer runs at that block_m (a caller's
+    block_size_M may differ)."""
     if block_m not in (16, 32) or model_dim % 256 or model_dim > 8192:
         return False
     env = os.environ.get("AITER_AMD_FUSED")
@@ -250,7 +253,7 @@ def select_run_1stage(tokens: int, topk: int, num_experts: int, model_dim: int,
         return int(env) != 0
     cfg = tuned_config(_cu_num(device), tokens, model_dim, inter_dim, num_experts, topk,
                        "per_1x32" if a8w4 else "per_1x128", "fp4x2" if a8w4 else "fp8")
-    return bool(cfg and cfg[1])
+    return bool(cfg and cfg[1] and cfg[0] == block_m)
 
 
 def e8m0_rowmajor(scale: torch.Tensor, E: int, N: int, KS: int) -> torch.Tensor:

@@ -512,7 +512,8 @@ def test_tuned_table_run_1stage(tmp_path, monkeypatch):
     """The tuned table's run_1stage column picks the one-launch layer per shape
     (the reference's cfg["run_1stage"], aiter/fused_moe.py:903-911);
     AITER_AMD_FUSED overrides it; rows without the column, shapes without a
-    row and block sizes the one-launch kernel does not run keep two launches."""
+    row, block sizes the one-launch kernel does not run and block sizes other
+    than the row's keep two launches."""
     import importlib
 
     from aiter_amd import tune
@@ -535,6 +536,9 @@ def test_tuned_table_run_1stage(tmp_path, monkeypatch):
         assert not F.select_run_1stage(4, 8, 256, *args)
         assert not F.select_run_1stage(8, 8, 256, *args)                 # no row
         assert not F.select_run_1stage(2, 8, 256, 4096, 2048, False, 64, torch.device("cpu"))
+        # the row's run_1stage was measured at its own block_m (16): a caller's
+        # block_size_M of 32 keeps two launches
+        assert not F.select_run_1stage(2, 8, 256, 4096, 2048, False, 32, torch.device("cpu"))
         assert tune.tuned_block_m(256, 2, 4096, 2048, 256, 8, "per_1x128", "fp8") == 16
         monkeypatch.setenv("AITER_AMD_FUSED", "0")
         assert not F.select_run_1stage(2, 8, 256, *args)

@@ -29,19 +29,28 @@ def _inputs(cfg, dev):
     return dict(x=x, tw=tw, ids=ids, **wts)
 
 
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
 def _args(d, cfg, out, bm):
+    """The one-call layer's arguments; an expert-parallel share passes its
+    mask (global expert count cfg.experts, local weights only) and, when the
+    inputs carry one, num_local_tokens."""
+    local = cfg.local_experts or cfg.experts
     return (d["x"].data_ptr(), AITER_DTYPE[d["x"].dtype], d["w1"].data_ptr(),
             d["w1_scale"].data_ptr(), d["w2"].data_ptr(), d["w2_scale"].data_ptr(),
-            d["tw"].data_ptr(), d["ids"].data_ptr(), None, None, out.data_ptr(),
-            AITER_DTYPE[out.dtype], cfg.tokens, cfg.model_dim, cfg.inter_dim, cfg.experts,
-            cfg.experts, cfg.topk, bm, 0, 0, 1)
+            d["tw"].data_ptr(), d["ids"].data_ptr(), _ptr(d.get("mask")), _ptr(d.get("nlt")),
+            out.data_ptr(), AITER_DTYPE[out.dtype], cfg.tokens, cfg.model_dim, cfg.inter_dim,
+            local, cfg.experts, cfg.topk, bm, 0, 0, 1)
 
 
 def _with_workspace(d, cfg, bm):
     dev = d["x"].device
     out = torch.empty(cfg.tokens, cfg.model_dim, dtype=torch.bfloat16, device=dev)
     nbytes = _abi.query("aiter_amd_fused_moe_workspace_bytes", cfg.tokens, cfg.model_dim,
-                        cfg.inter_dim, cfg.experts, cfg.experts, cfg.topk, bm)
+                        cfg.inter_dim, cfg.local_experts or cfg.experts, cfg.experts, cfg.topk,
+                        bm)
     ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
     _abi.call("aiter_amd_fused_moe_fp8_blockscale", *_args(d, cfg, out, bm), ws.data_ptr(),
               nbytes, torch.cuda.current_stream(dev).cuda_stream)
@@ -78,3 +87,57 @@ def test_no_alloc_matches_workspace_entry(cuda_device, big, small, bm):
             print(f"[no-alloc] {cfg.name}: max-rel {mx:.2e} rms-rel {rms:.2e}", flush=True)
             assert mx <= 1e-2 and rms <= 1e-3, (mx, rms)
         del d
+
+
+def _check(want, got, rows, atomics, name):
+    want, got = want[:rows], got[:rows]
+    assert torch.count_nonzero(got).item() > 0
+    if not atomics:
+        assert torch.equal(got, want), name
+        return
+    mx, rms = R.normalized_errors(want.float().cpu().numpy(), got.float().cpu().numpy())
+    print(f"[no-alloc] {name}: max-rel {mx:.2e} rms-rel {rms:.2e}", flush=True)
+    assert mx <= 1e-2 and rms <= 1e-3, (mx, rms)
+
+
+def test_no_alloc_split_k_after_a_larger_call(cuda_device):
+    """Stage-1 split-K on the shared scratch after a larger per-pair layer
+    left it dirty: MiMo-like dims at 5 tokens expect 8 M-blocks x 4 column
+    tiles, below the 128 tiles under which stage 1 splits K in two, so its
+    arrival counters and partial sums live in scratch that the larger call
+    overwrote (the sorting launch must clear the counters again). Two
+    split-K calls in a row, each against the workspace entry."""
+    big = W.MoEConfig("na_dirty", 600, 2048, 512, 8, 4, seed=45)
+    d = _inputs(big, cuda_device)
+    _no_alloc(d, big, 128)
+    torch.cuda.synchronize()
+    del d
+    for T, seed in ((5, 46), (3, 47)):
+        cfg = W.MoEConfig(f"na_splitk_{T}", T, 2048, 512, 8, 4, seed=seed)
+        print(f"[no-alloc] {cfg.name} bm=16 (split K)", flush=True)
+        d = _inputs(cfg, cuda_device)
+        want = _with_workspace(d, cfg, 16)
+        got = _no_alloc(d, cfg, 16)
+        torch.cuda.synchronize()
+        _check(want, got, T, True, cfg.name)
+
+
+def test_no_alloc_expert_parallel_share(cuda_device):
+    """An expert-parallel share (expert mask, 8 of 32 experts local, sigmoid
+    routing) with num_local_tokens below the batch, at 64-row blocks (the
+    per-pair rows and the per-wave slot sum), a larger call then a smaller
+    one: the slot sum must not read part rows a previous call left in
+    scratch for pairs that are not routed here. Rows past num_local_tokens
+    are not written and are not compared."""
+    for T, nl, seed in ((400, 390, 48), (120, 100, 49)):
+        cfg = W.MoEConfig(f"na_ep_{T}", T, 1024, 512, 32, 4, routing="sigmoid", local_experts=8,
+                          seed=seed)
+        print(f"[no-alloc] {cfg.name} local tokens {nl} bm=64", flush=True)
+        d = _inputs(cfg, cuda_device)
+        d["mask"] = W.make_expert_mask(cfg, device=cuda_device)
+        d["nlt"] = torch.tensor([nl], dtype=torch.int32, device=cuda_device)
+        want = _with_workspace(d, cfg, 64)
+        got = _no_alloc(d, cfg, 64)
+        torch.cuda.synchronize()
+        _check(want, got, nl, False, cfg.name)
+
