@@ -48,8 +48,9 @@ def parse():
                    help="prefill<T> | decode<T> | a8w4_<T> | ep<T> (e.g. prefill8192, "
                         "decode32, a8w4_1024, ep4096)")
     p.add_argument("--legs",
-                   default="a8w4_32,a8w4_1024,a8w4_8192,ep4096,route_32,route_8192,"
-                           "one_launch_1,one_launch_4,one_launch_32,dense_fp8_ceiling,hbm_ceiling",
+                   default="decode1,decode8,decode128,prefill2048,a8w4_32,a8w4_1024,a8w4_8192,"
+                           "ep4096,route_32,route_8192,one_launch_1,one_launch_4,one_launch_32,"
+                           "dense_fp8_ceiling,hbm_ceiling",
                    help="comma-separated extra workloads reported under 'legs' ('none': "
                         "skip); route_<T> times the router top-k kernels at T tokens; "
                         "one_launch_<T> the one-launch layer against the two-launch one; "
@@ -58,9 +59,10 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-decode", action="store_true")
     p.add_argument("--block-m", type=int, default=0, help="override the M-block (0 = default)")
-    p.add_argument("--kernel-only", choices=["stage1", "stage2"], default=None,
+    p.add_argument("--kernel-only", choices=["stage1", "stage2", "layer"], default=None,
                    help="profiling mode: run a 256 MiB device copy (counter calibration) "
-                        "then only this kernel --steps times")
+                        "then only this kernel --steps times ('layer': the one-call layer "
+                        "the bench times, every kernel of it)")
     return p.parse_args()
 
 
@@ -191,7 +193,8 @@ def layer_step_times(layer, steps):
 def kernel_only(layer, which, steps):
     """Profiling mode for rocprofv3 counter runs: a plain 256 MiB copy
     (known bytes, for scaling FETCH_SIZE / WRITE_SIZE) and then one stage
-    kernel alone."""
+    kernel alone, or the whole one-call layer (each of its kernels is a
+    dispatch of its own in the counter output)."""
     import torch
 
     import aiter_amd as A
@@ -200,6 +203,12 @@ def kernel_only(layer, which, steps):
     dst = torch.empty_like(src)
     for _ in range(3):
         dst.copy_(src)
+    if which == "layer":
+        for _ in range(steps):
+            layer.run()
+        torch.cuda.synchronize()
+        log(f"kernel-only layer: {steps} layers done")
+        return
     cfg = layer.cfg
     bm = layer.block_m_used()
     st1, st2 = layer.stages()
@@ -541,7 +550,8 @@ def leg(name, args, dev):
            "routed_pairs": lay.pairs, "distinct_experts": lay.distinct,
            "block_m": lay.block_m_used(),
            "kernels_us": {k: round(v * 1e6, 1) for k, v in kt.items()},
-           "stage1_roofline": roofline(f1, b1, kt["stage1"])}
+           "stage1_roofline": dict(roofline(f1, b1, kt["stage1"]),
+                                   traffic=measured_traffic(name), alg_bytes=round(b1))}
     del lay
     torch.cuda.empty_cache()
     return out
@@ -620,11 +630,17 @@ def main():
         dl = Layer(dcfg, dev)
         dms, _ = time_steps(dl.run, max(args.steps, 20), args.warmup)
         db = W.layer_bytes(dcfg, dl.distinct)
+        dkt, _ = layer_step_times(dl, max(args.steps, 20))
+        df1, db1 = stage1_work(dl)
         line["decode"] = {"workload": dcfg.name, "ms_per_step": round(dms, 4),
                           "tokens_per_s": round(dcfg.tokens / (dms * 1e-3), 1),
                           "hbm_gbps": round(db / (dms * 1e-3) / 1e9, 1),
                           "hbm_peak_frac": round(db / (dms * 1e-3) / PEAK_HBM_BPS, 4),
-                          "distinct_experts": dl.distinct}
+                          "distinct_experts": dl.distinct, "block_m": dl.block_m_used(),
+                          "kernels_us": {k: round(v * 1e6, 1) for k, v in dkt.items()},
+                          "stage1_roofline": dict(roofline(df1, db1, dkt["stage1"]),
+                                                  traffic=measured_traffic("decode32"),
+                                                  alg_bytes=round(db1))}
         del dl
         torch.cuda.empty_cache()
     if legs:
