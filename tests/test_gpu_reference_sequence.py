@@ -266,6 +266,49 @@ def test_ck_moe_stage1_gate_up_rows(cuda_device, ksplit):
     assert ((act.double().cpu() - h).abs() <= bound).all()
 
 
+@pytest.mark.parametrize("shuffle", [True, False])
+@pytest.mark.parametrize("bm,splitk", [(16, 0), (64, 0), (16, 4)])
+def test_ck_moe_stage1_mxfp4_weights(cuda_device, shuffle, bm, splitk):
+    """ck_moe_stage1 with packed fp4x2 w1 and e8m0 1x32 scales (quant_type
+    per_1x32): the bf16 act rows, and with a K split the fp32 gate|up rows,
+    against an fp64 product of the dequantised operands (the fp8 activations
+    dequantised with their 1x128 scales, the weights with the mxfp4 decode),
+    element by element within the fp32 accumulation bound."""
+    cfg = W.MoEConfig("ck_w4", 40, 1024, 512, 8, 2, seed=64, weights="mxfp4")
+    T, k, I, H, E = cfg.tokens, cfg.topk, cfg.inter_dim, cfg.model_dim, cfg.experts
+    print(f"[ck stage1 mxfp4] T={T} bm={bm} splitk={splitk} shuffle={shuffle}", flush=True)
+    wts = W.make_weights(cfg, device="cpu", shuffle=False)
+    x = W.make_hidden(cfg)
+    tw, ids = W.make_routing(cfg)
+    dev = cuda_device
+    w1 = A.shuffle_weight(wts["w1"]) if shuffle else wts["w1"]
+    w1, s1 = w1.to(dev), wts["w1_scale"].to(dev)
+    sid, sw, se, nv, _ = S.moe_sorting(ids.to(dev), tw.to(dev), E, H, torch.bfloat16, bm)
+    a1, a1s = S.per_group_quant_hip(x.to(dev))
+    a1d = torch.from_numpy(R.dequant_1x128(a1.view(torch.uint8).cpu().numpy(),
+                                           a1s.cpu().numpy())).double()
+    w1d = torch.from_numpy(R.dequant_weight_mxfp4(wts["w1"].numpy(),
+                                                  wts["w1_scale"].numpy())).double()
+    y, sabs = _gate_up64(a1d, lambda e: w1d[e], ids, T, k)
+    if splitk:
+        tmp = torch.full((T * k, 2 * I), 5.0, device=dev)
+        ffi.ck_moe_stage1(a1, w1, w1, sid, se, nv, tmp, k, "", s1, a1s, bm, None,
+                          int(A.QuantType.per_1x32), 0, splitk, False, None, shuffle)
+        torch.cuda.synchronize()
+        err = (tmp.double().cpu() - y).abs()
+        print(f"[ck stage1 mxfp4] gate|up: bound used {(err / (_gamma(H) * sabs)).max():.3f}")
+        assert (err <= _gamma(H) * sabs).all()
+        return
+    out = torch.empty(T, k, I, dtype=torch.bfloat16, device=dev)
+    ffi.ck_moe_stage1(a1, w1, w1, sid, se, nv, out, k, "", s1, a1s, bm, None,
+                      int(A.QuantType.per_1x32), 0, 0, False, None, shuffle)
+    torch.cuda.synchronize()
+    h, bound = _act_rows_bound(y, sabs, H, ActivationType.Silu, 2.0 ** -8)
+    err = (out.double().cpu().view(T * k, I) - h).abs()
+    print(f"[ck stage1 mxfp4] act rows: bound used {(err / bound).max():.3f}")
+    assert (err <= bound).all()
+
+
 @pytest.mark.parametrize("in_dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("name", ["silu_and_mul", "gelu_and_mul"])
