@@ -345,109 +345,122 @@ def _blas_threads():
 
 
 def cpu_baseline_config_a(warmup=2, runs=10):
-    """The oracle ('port': the numpy restatement of the reference's torch MoE
-    path, aiter/fused_moe.py:1483-1666 with pertoken_quant activations) timed
-    on this host at BASELINE.json's CPU configuration (config A: E=8, top-2,
-    hidden 1024, inter 512, T=64, the seeded inputs of the GPU tests): the
-    whole layer -- weight dequant, activation quant, both GEMM stages, the
-    requant and the weighted sum -- 2 warm-ups, then the median of 10
-    wall-clock runs."""
+    """The reference's CPU torch MoE path at BASELINE.json's CPU configuration
+    (config A: E=8, top-2, hidden 1024, inter 512, T=64, the seeded inputs of
+    the GPU tests), restated in PyTorch (oracle/torch_ref.py, the op sequence
+    of aiter/fused_moe.py:1483-1666 with pertoken_quant activations) and run
+    on this host's CPU with torch's thread count: the whole layer -- weight
+    dequant, activation quant, both GEMM stages, the requant and the weighted
+    sum -- 2 warm-ups, then the median of 10 wall-clock runs. The numpy
+    oracle's time on the same layer is reported beside it."""
     import statistics
 
     import torch
 
     from aiter_amd import workloads as W
     from oracle import moe_ref as R
+    from oracle import torch_ref as TR
 
     cfg = W.CONFIG_A
     wts = W.make_weights(cfg, device="cpu", shuffle=False)
-    x = W.make_hidden(cfg).float().numpy()
+    xb = W.make_hidden(cfg)
     tw, ids = W.make_routing(cfg)
-    args = (x, wts["w1"].view(torch.uint8).numpy(), wts["w1_scale"].numpy(),
+
+    def median_time(fn):
+        for _ in range(warmup):
+            fn()
+        times = []
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+        return statistics.median(times)
+
+    t = median_time(lambda: TR.fused_moe_torch(xb, wts["w1"], wts["w1_scale"], wts["w2"],
+                                               wts["w2_scale"], ids, tw))
+    args = (xb.float().numpy(), wts["w1"].view(torch.uint8).numpy(), wts["w1_scale"].numpy(),
             wts["w2"].view(torch.uint8).numpy(), wts["w2_scale"].numpy(), ids.numpy(),
             tw.numpy())
-    for _ in range(warmup):
-        R.fused_moe_ref(*args, act_quant="torch")
-    times = []
-    for _ in range(runs):
-        t0 = time.perf_counter()
-        R.fused_moe_ref(*args, act_quant="torch")
-        times.append(time.perf_counter() - t0)
-    t = statistics.median(times)
+    t_np = median_time(lambda: R.fused_moe_ref(*args, act_quant="torch"))
     flops = 2.0 * cfg.tokens * cfg.topk * 3 * cfg.inter_dim * cfg.model_dim
-    threads = _blas_threads()
+    threads = torch.get_num_threads()
     return {
         "value": round(cfg.tokens / t, 1), "unit": "tokens/s", "cores": threads,
         "kind": "port", "measured": True,
         "sample": (f"config A full layer (T={cfg.tokens}, E={cfg.experts}, top-{cfg.topk}, "
-                   f"hidden {cfg.model_dim}, inter {cfg.inter_dim}) through the numpy oracle: "
+                   f"hidden {cfg.model_dim}, inter {cfg.inter_dim}) through the PyTorch-CPU "
+                   f"restatement of the reference's torch MoE path ({threads} threads): "
                    f"{warmup} warm-ups, median of {runs} runs"),
         "latency_ms": round(t * 1e3, 3), "gflops": round(flops / t / 1e9, 2),
-        "cpu_model": _cpu_model(), "os_cpu_count": os.cpu_count(), "blas_threads": threads,
+        "numpy_oracle": {"value": round(cfg.tokens / t_np, 1), "unit": "tokens/s",
+                         "latency_ms": round(t_np * 1e3, 3), "blas_threads": _blas_threads()},
+        "cpu_model": _cpu_model(), "os_cpu_count": os.cpu_count(), "torch_threads": threads,
     }
 
 
 def cpu_extrapolated_mimo(layer, budget_s=8.0):
     """A bounded sample of the headline workload itself, extrapolated (second,
-    labelled figure): the oracle on a seeded sample of the touched experts,
-    each for all of its routed pairs (dequant of its weights, stage-1 GEMM,
-    SiLU*up, requant, stage-2 GEMM); full layer time = D * (mean dequant time
-    per expert) + P * (mean GEMM time per pair)."""
+    labelled figure): the PyTorch-CPU restatement on a seeded sample of the
+    touched experts, each for all of its routed pairs (dequant of its
+    weights, stage-1 GEMM, act(gate)*up, requant, stage-2 GEMM); full layer
+    time = quant + D * (mean dequant time per expert) + P * (mean GEMM time
+    per pair)."""
     import numpy as np
     import torch
 
-    from oracle import moe_ref as R
+    from aiter_amd.shuffle import unshuffle_weight
+    from oracle import torch_ref as TR
 
+    if layer.a8w4:
+        return {"measured": False, "note": "the CPU restatement covers the FP8 layer only"}
     cfg = layer.cfg
-    ids = layer.ids.cpu().numpy()
-    tw = layer.tw.cpu().numpy()
-    x = layer.x.float().cpu().numpy()
+    ids = layer.ids.cpu()
+    tw = layer.tw.cpu()
+    x = layer.x.cpu()
     if layer.mask is not None:
-        ids = R.local_expert_ids(ids, layer.mask.cpu().numpy())
-    experts = np.unique(ids[ids >= 0])
+        m = layer.mask.cpu().bool()
+        ids = torch.where(m[ids.long()], torch.cumsum(m.int(), 0)[ids.long()] - 1, -1)
+    experts = torch.unique(ids[ids >= 0]).numpy()
     rng = np.random.default_rng(0)
     rng.shuffle(experts)
-    from aiter_amd.shuffle import unshuffle_weight
-
-    def deq(w, s):
-        if layer.a8w4:
-            return R.dequant_weight_mxfp4(w, s)[0]
-        return R.dequant_weight_128x128(w, s)[0]
-
+    I = cfg.inter_dim
     t_deq = t_gemm = 0.0
     n_exp = n_pairs = 0
     t_start = time.perf_counter()
-    a1q, a1s = R.quant_1x128_kernel(x)
-    a1 = R.dequant_1x128(a1q, a1s)
+    a1q, a1s = TR.pertoken_quant_1x128(x)
+    a1 = TR.dequant_1x128(a1q, a1s)
     t_quant = time.perf_counter() - t_start
-    I = cfg.inter_dim
-    for e in experts:
-        w1q = unshuffle_weight(layer.w["w1"][e:e + 1]).view(torch.uint8).cpu().numpy()
-        w2q = unshuffle_weight(layer.w["w2"][e:e + 1]).view(torch.uint8).cpu().numpy()
-        s1 = layer.w["w1_scale"][e:e + 1].cpu().numpy()
-        s2 = layer.w["w2_scale"][e:e + 1].cpu().numpy()
+    for e in experts.tolist():
+        w1q = unshuffle_weight(layer.w["w1"][e:e + 1]).cpu()
+        w2q = unshuffle_weight(layer.w["w2"][e:e + 1]).cpu()
+        s1 = layer.w["w1_scale"][e:e + 1].cpu()
+        s2 = layer.w["w2_scale"][e:e + 1].cpu()
         t0 = time.perf_counter()
-        w1 = deq(w1q, s1)
-        w2 = deq(w2q, s2)
+        w1 = TR.dequant_weight_128x128(w1q, s1)[0]
+        w2 = TR.dequant_weight_128x128(w2q, s2)[0]
         t1 = time.perf_counter()
-        tok, slot = np.nonzero(ids == e)
+        tok, slot = torch.nonzero(ids == e, as_tuple=True)
         y = a1[tok] @ w1.T
-        h = R.bf16_round(R.silu(y[:, :I]) * y[:, I:])
-        hq, hs = R.quant_1x128_kernel(h)
-        (R.dequant_1x128(hq, hs) @ w2.T) * tw[tok, slot][:, None]
+        h = (torch.nn.functional.silu(y[:, :I]) * y[:, I:]).to(torch.bfloat16).float()
+        hq, hs = TR.pertoken_quant_1x128(h)
+        (TR.dequant_1x128(hq, hs) @ w2.T) * tw[tok, slot][:, None]
         t2 = time.perf_counter()
         t_deq += t1 - t0
         t_gemm += t2 - t1
         n_exp += 1
-        n_pairs += tok.size
+        n_pairs += tok.numel()
         if time.perf_counter() - t_start > budget_s and n_exp >= 2:
             break
-    full = t_quant + len(experts) * (t_deq / n_exp) + layer.pairs * (t_gemm / max(n_pairs, 1))
-    return {"value": round(cfg.tokens / full, 2), "unit": "tokens/s", "measured": False,
-            "cores": _blas_threads(),
-            "sample": (f"numpy oracle on {n_exp} of {len(experts)} touched experts "
+    whole = n_exp == len(experts)
+    full = (t_quant + t_deq + t_gemm if whole else
+            t_quant + len(experts) * (t_deq / n_exp) + layer.pairs * (t_gemm / max(n_pairs, 1)))
+    how = ("the whole layer ran (no extrapolation)" if whole else
+           "extrapolated as quant + D*dequant/expert + P*gemm/pair")
+    return {"value": round(cfg.tokens / full, 2), "unit": "tokens/s", "measured": whole,
+            "cores": torch.get_num_threads(),
+            "sample": (f"PyTorch-CPU restatement on {n_exp} of {len(experts)} touched experts "
                        f"({n_pairs} of {layer.pairs} routed pairs) of the T={cfg.tokens} layer; "
-                       f"extrapolated as D*dequant/expert + P*gemm/pair = {full:.2f} s")}
+                       f"{how}: {full:.2f} s")}
 
 
 def route_leg(name, args, dev):
@@ -670,7 +683,7 @@ def main():
     }
     legs = [] if args.legs in ("", "none") else [x for x in args.legs.split(",") if x]
     if not args.no_cpu_baseline:
-        log("cpu baseline: the oracle at config A, then a sample of this workload")
+        log("cpu baseline: the PyTorch-CPU restatement at config A, then this workload")
         line["cpu_baseline"] = cpu_baseline_config_a()
         line["cpu_baseline"]["extrapolated_" + cfg.name] = cpu_extrapolated_mimo(layer)
     if not args.no_decode and not args.workload.startswith("decode"):

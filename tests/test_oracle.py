@@ -560,3 +560,32 @@ def test_route_grouped_reduces_to_plain_topk():
     w3, ids3 = RR.topk_sigmoid_ref(x, 6)
     assert np.array_equal(ids2, ids3)
     np.testing.assert_allclose(w2, w3, rtol=1e-6)
+
+
+def test_torch_cpu_restatement_matches_the_oracle():
+    """oracle/torch_ref.fused_moe_torch (the PyTorch-CPU restatement the CPU
+    baseline times) against the numpy oracle with the same pertoken_quant
+    semantics, at config A: the same layer to the strict normalised bar, and
+    its activation quant bit-exact with the numpy one (codes and scales)."""
+    import torch
+
+    from aiter_amd import workloads as W
+    from oracle import torch_ref as TR
+
+    cfg = W.CONFIG_A
+    wts = W.make_weights(cfg, device="cpu", shuffle=False)
+    x = W.make_hidden(cfg)
+    tw, ids = W.make_routing(cfg)
+    ref = R.fused_moe_ref(x.float().numpy(), wts["w1"].view(torch.uint8).numpy(),
+                          wts["w1_scale"].numpy(), wts["w2"].view(torch.uint8).numpy(),
+                          wts["w2_scale"].numpy(), ids.numpy(), tw.numpy(), act_quant="torch")
+    got = TR.fused_moe_torch(x, wts["w1"], wts["w1_scale"], wts["w2"], wts["w2_scale"], ids, tw)
+    mx, rms = R.normalized_errors(ref["out"], got.float().numpy())
+    assert mx <= R.MAXTOL and rms <= R.RMSTOL, (mx, rms)
+    q, sc = TR.pertoken_quant_1x128(x)
+    nq, nsc = R.pertoken_quant_torch_semantics(x.float().numpy())
+    assert np.array_equal(q.view(torch.uint8).numpy(), nq) and np.array_equal(sc.numpy(), nsc)
+    z = torch.zeros(2, 256)                          # all-zero groups: scale 1, codes 0
+    qz, sz = TR.pertoken_quant_1x128(z)
+    assert (sz == 1).all() and (qz.float() == 0).all()
+
