@@ -186,7 +186,8 @@ int gelu_and_mul(aiter_tensor_t* out, aiter_tensor_t* input, void* stream);
  * launches at this library's block size for the shape. Its intermediates
  * live in a device workspace the library holds per (device, stream) and
  * grows with hipMalloc when a larger layer arrives; growing is refused
- * during HIP graph capture (one call of that size before capturing avoids
+ * during HIP graph capture (one call of that size on the same stream before
+ * capturing avoids
  * it). About 0.7 GB at T = 8192 for MiMo dims (hidden 4096, inter 2048,
  * top-8). */
 int fmoe_fp8_blockscale_g1u1(aiter_tensor_t* out, aiter_tensor_t* input, aiter_tensor_t* gate,

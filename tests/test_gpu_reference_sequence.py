@@ -495,3 +495,53 @@ def test_fmoe_adds_into_moe_buf(cuda_device):
     diff = (buf2.float() - (base.float() + buf.float())).abs()
     tol = 2.0 ** -8 * (base.float() + buf.float()).abs() + 2.0 ** -8 * buf.float().abs()
     assert (diff <= tol).all()
+
+
+@pytest.mark.filterwarnings("ignore:The CUDA Graph is empty")
+def test_fmoe_workspace_under_graph_capture(cuda_device):
+    """fmoe_fp8_blockscale_g1u1 keeps its workspace per (device, stream): after
+    one call on a stream, the same call captures into a HIP graph on that
+    stream (torch.cuda.graph(..., stream=s)) and each of three replays on new
+    inputs matches an eager call; a capture that would need a larger
+    workspace on a fresh stream is refused with an error (the check runs on
+    the host before any allocation)."""
+    cfg = W.CONFIG_A
+    d, _ = _layer(cfg, cuda_device)
+    T, H, k = cfg.tokens, cfg.model_dim, cfg.topk
+    xs = [d["x"]] + [torch.randn_like(d["x"].float()).to(torch.bfloat16) for _ in range(2)]
+    static_x = d["x"].clone()
+    run = lambda x: S.fused_moe(x, d["w1"], d["w2"], d["tw"], d["ids"], d["s1"], d["s2"],
+                                force_path="1stage")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        run(static_x)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        static_out = run(static_x)
+    for i, x in enumerate(xs):
+        static_x.copy_(x)
+        graph.replay()
+        torch.cuda.synchronize()
+        got = static_out.float().clone()
+        eager = run(x).float()
+        torch.cuda.synchronize()
+        mx, rms = R.normalized_errors(eager.cpu().numpy(), got.cpu().numpy())
+        print(f"[fmoe graph] replay {i}: max-rel {mx:.2e} rms-rel {rms:.2e}", flush=True)
+        assert mx <= 2.0 ** -7 and rms <= 1e-3, (i, mx, rms)
+    del graph
+    torch.cuda.synchronize()
+    # a fresh stream holds no workspace yet: growing it inside capture is refused
+    s2 = torch.cuda.Stream()
+    sid, sw, se, nv, buf = S.moe_sorting(d["ids"], d["tw"], cfg.experts, H, torch.bfloat16, 32)
+    a1, a1s = S.per_group_quant_hip(d["x"], transpose_scale=True)
+    torch.cuda.synchronize()
+    g2 = torch.cuda.CUDAGraph()
+    with pytest.raises(RuntimeError, match="cannot be allocated during graph capture"):
+        with torch.cuda.graph(g2, stream=s2):
+            ffi.fmoe_fp8_blockscale_g1u1(buf, a1, d["w1"], d["w2"], sid, sw, se, nv, k, a1s,
+                                         d["s1"], d["s2"])
+    del g2
+    torch.cuda.synchronize()
+
