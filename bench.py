@@ -626,7 +626,8 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on exactly one GPU; --gpus N>1 is not "
-                                   "supported (see DESIGN.md: how the path would shard)"}))
+                                   "supported (across GPUs the layer would shard by expert: "
+                                   "each GPU runs its experts' share under an expert_mask)"}))
         sys.exit(2)
     import torch
 
