@@ -80,7 +80,8 @@ void launch_moe_stage1_stream(const uint8_t*, const float*, int64_t, int64_t, co
                               const int32_t*, uint8_t*, float*, int64_t, int64_t, int64_t,
                               int64_t, int64_t, int64_t, int64_t, int, hipStream_t,
                               const float*, int, int ksplit = 1, void* kpart = nullptr,
-                              int32_t* kcnt = nullptr, int64_t kmb = 0);
+                              int32_t* kcnt = nullptr, int64_t kmb = 0,
+                              StreamDirect direct = StreamDirect{});
 // the fused layer (both GEMMs in one launch) on the stream kernel
 bool stream_fused_supported(int64_t block_m, int64_t hidden, int64_t inter);
 void launch_moe_fused_stream(const uint8_t*, const float*, int64_t, int64_t, const uint8_t*,
@@ -96,7 +97,8 @@ int64_t stream_ksplit_part_bytes(int64_t block_m, int64_t mblocks, int64_t inter
 void launch_moe_stage2_stream(const uint8_t*, const float*, const uint8_t*, const float*,
                               const uint8_t*, const int32_t*, const float*, const int32_t*,
                               const int32_t*, void*, int, int64_t, int64_t, int64_t, int64_t,
-                              int64_t, int64_t, int64_t, int, hipStream_t);
+                              int64_t, int64_t, int64_t, int, hipStream_t,
+                              StreamDirect direct = StreamDirect{});
 
 // quant.hip: per-pair bf16 rows -> output
 void launch_slot_sum(const uint16_t* part, const int32_t* topk_ids, const int32_t* mask,
@@ -470,6 +472,24 @@ static void timing_mark(int step, hipStream_t s) {
 // Activations already quantised by the caller (fp8 [tokens, model_dim] and
 // their 1x128 scales at a1_scale[row * sa_row + kb * sa_kb]) instead of
 // bf16 / fp16 hidden states.
+// Whether a layer runs on direct M-blocks (no sorting launch): one token
+// (each routed pair then fills its own 16-row M-block, as sorting would lay
+// it out), every expert local, both GEMMs on the decode kernel with one K
+// range per stage-1 tile. AITER_AMD_DIRECT=0 sorts anyway (tests compare the
+// two). Measured on MI355X at MiMo dims, T=1, alternating on one box: FP8
+// 50.2-50.3 -> 44.8-45.1 us, A8W4 36.9-37.1 -> 30.8-30.9 us. Two or more
+// tokens can route two pairs to one expert, whose weights two direct
+// M-blocks would then stream twice; they keep the sorting launch.
+bool direct_layer(int64_t tokens, int64_t block_m, int64_t H, int64_t I,
+                  const int32_t* expert_mask, const int32_t* num_local_tokens, const void* part,
+                  bool one_launch, int ksplit) {
+    if (const char* env = getenv("AITER_AMD_DIRECT"))
+        if (atoi(env) == 0) return false;
+    return tokens == 1 && block_m == 16 && !expert_mask && !num_local_tokens && !part &&
+           !one_launch && ksplit == 1 && stream_supported(16, H) && stream_supported(16, I) &&
+           H % 256 == 0;
+}
+
 struct PreQuant {
     const uint8_t* a1 = nullptr;
     const float* a1_scale = nullptr;
@@ -544,6 +564,43 @@ void fused_entry(const void* hidden_states, int hidden_dtype, const void* w1, WS
                          ? reinterpret_cast<uint16_t*>(ws + L.off_acc) : nullptr;
     hipStream_t s = (hipStream_t)stream;
     timing_mark(0, s);
+    const int sh = (int)(w_shuffled != 0);
+    // doweight_stage1: the routing weights scale stage 1's gate and up, stage 2 sums unweighted
+    const bool dw = doweight_stage1 != 0;
+    const void* addend = accumulate ? out : nullptr;
+    if (direct_layer(tokens, block_m, model_dim, inter_dim, expert_mask, num_local_tokens, part,
+                     one_launch || use_fused_layer(tokens, topk, block_m, model_dim, inter_dim),
+                     L.ksplit)) {
+        // one token: each routed pair is its own 16-row M-block, so the GEMMs
+        // read the routing directly and stage 1 quantises the token and clears
+        // stage 2's accumulator -- no sorting launch
+        StreamDirect d1;
+        d1.ids = topk_ids;
+        d1.tokens = (int)tokens;
+        d1.xq = pre.a1 ? nullptr : hidden_states;
+        d1.xq_dtype = (int)hidden_dtype;
+        d1.zero = acc;
+        d1.zero_bytes = tokens * model_dim * 4;
+        timing_mark(1, s);
+        timing_mark(2, s);
+        launch_moe_stage1_stream(a1, a1_scale, sa_row, sa_kb, (const uint8_t*)w1, w1s.f32,
+                                 w1s.e8m0, nullptr, nullptr, nullptr, a2, a2_scale, tokens,
+                                 model_dim, inter_dim, num_experts, topk, block_m, tokens * topk,
+                                 sh, s, dw ? topk_weights : nullptr, (int)activation, 1, nullptr,
+                                 nullptr, 0, d1);
+        timing_mark(3, s);
+        StreamDirect d2;
+        d2.ids = topk_ids;
+        d2.tokens = (int)tokens;
+        launch_moe_stage2_stream(a2, a2_scale, (const uint8_t*)w2, w2s.f32, w2s.e8m0, nullptr,
+                                 dw ? nullptr : topk_weights, nullptr, nullptr, acc, DT_FP32,
+                                 tokens * topk, inter_dim, model_dim, num_experts, topk, block_m,
+                                 tokens * topk, sh, s, d2);
+        timing_mark(4, s);
+        launch_acc_to_out(acc, out, out_dtype, nullptr, tokens, model_dim, s, addend);
+        timing_mark(5, s);
+        return;
+    }
     // decode-sized batches: the sorting launch also quantises the activations
     const bool quantised = launch_moe_sort(
         topk_ids, topk_weights, expert_mask, num_local_tokens, sorted_ids, sorted_w, sorted_eids,
@@ -555,10 +612,6 @@ void fused_entry(const void* hidden_states, int hidden_dtype, const void* w1, WS
         launch_per_group_quant_fp8(hidden_states, hidden_dtype, a1, a1_scale, tokens, model_dim,
                                    0, num_local_tokens, 1, s);
     timing_mark(2, s);
-    const int sh = (int)(w_shuffled != 0);
-    // doweight_stage1: the routing weights scale stage 1's gate and up, stage 2 sums unweighted
-    const bool dw = doweight_stage1 != 0;
-    const void* addend = accumulate ? out : nullptr;
     if (!part && (one_launch || use_fused_layer(tokens, topk, block_m, model_dim, inter_dim))) {
         // decode sizes: both GEMMs in one launch, a2 kept per workgroup in LDS
         launch_moe_fused_stream(a1, a1_scale, sa_row, sa_kb, (const uint8_t*)w1, w1s.f32,

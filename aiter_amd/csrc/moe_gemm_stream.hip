@@ -30,6 +30,7 @@
 #include <cstdlib>
 
 #include "common.h"
+#include "quant_dev.h"
 
 namespace aiter_amd {
 
@@ -96,6 +97,23 @@ struct Args {
     // sorted_eids holds one expert per BM << eid_shift sorted rows: a caller's
     // 64- or 128-row M-blocks are walked as 32-row ones
     int eid_shift;
+    // direct M-blocks, for a layer too small to be worth a sorting launch:
+    // with dir_ids set, M-block p holds routing pair p = token * topk + slot
+    // of dir_tokens tokens in its first row (the rest is padding), its expert
+    // is dir_ids[p] and its routing weight sorted_w[p] (sorted_w is then the
+    // caller's [tokens, topk] weights); sorted_ids, sorted_eids and num_valid
+    // are not read
+    const int32_t* dir_ids;
+    int dir_tokens;
+    // stage 1 with direct M-blocks: the activations bf16 / fp16 [tokens, K],
+    // quantised 1x128 to fp8 by each workgroup into LDS with the quant
+    // kernel's arithmetic (a and a_scale are not read)
+    const uint16_t* xq;
+    int xq_bf16;
+    // zero_n16 16-byte words cleared by the launch's workgroups before their
+    // tiles (stage 1 with direct M-blocks: stage 2's fp32 accumulator)
+    v4i* zero;
+    int64_t zero_n16;
 };
 
 // One K step of one wave's operands.
@@ -108,7 +126,7 @@ struct Step {
 // STAGE 1: gate+up GEMM -> SiLU*up -> a2 (fp8 + 1x128 scales); STAGE 2:
 // down GEMM accumulated into acc; STAGE 3: both for one 128-wide slice of
 // the intermediate dim per workgroup (the fused layer).
-template <int BM, int STAGE, bool SHUFFLED, bool W4, int D>
+template <int BM, int STAGE, bool SHUFFLED, bool W4, int D, bool XQ = false>
 __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
     constexpr int NRT = BM / 16;
     constexpr bool G1 = STAGE != 2;                      // runs the gate+up GEMM
@@ -127,6 +145,10 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
     __shared__ float s_rs[FUSED ? BM : 1];               // fused: a2 scale x routing weight
     __shared__ __attribute__((aligned(16))) uint8_t s_q[G1 ? BM * 144 : 16];
     __shared__ int s_last;
+    // XQ: the routed row's fp8 codes [K] and 1x128 scales [K / 128]
+    __shared__ __attribute__((aligned(16))) uint8_t s_xq[XQ ? kMaxKB * 128 : 16];
+    __shared__ float s_xs[XQ ? kMaxKB : 1];
+    static_assert(!XQ || (BM == 16 && STAGE == 1), "in-kernel quant: direct 16-row stage 1");
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -134,11 +156,19 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
     const int lr = lane & 15;
     const int lq = lane >> 4;
 
+    if (g.zero) {
+        const int64_t nwg = (int64_t)gridDim.x * gridDim.y;
+        const int64_t wg = (int64_t)blockIdx.y * gridDim.x + blockIdx.x;
+        for (int64_t i = wg * kThreads + tid; i < g.zero_n16; i += nwg * kThreads)
+            g.zero[i] = v4i{0, 0, 0, 0};
+    }
+
     const int mb = blockIdx.y;
-    const int nvalid = g.num_valid[0];
+    const bool direct = g.dir_ids != nullptr;
+    const int nvalid = direct ? g.dir_tokens * g.topk * BM : g.num_valid[0];
     if (mb * BM >= nvalid) return;
-    const int tokens = g.num_valid[1];
-    const int e = g.sorted_eids[mb >> g.eid_shift];
+    const int tokens = direct ? g.dir_tokens : g.num_valid[1];
+    const int e = direct ? g.dir_ids[mb] : g.sorted_eids[mb >> g.eid_shift];
     if (e < 0 || e >= g.E) return;
     // stage 2 may walk ntw consecutive 256-column groups in one K loop (steps
     // s = jt * KB + kb); stage 1 always has one tile, whose K range the S
@@ -151,7 +181,11 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
     const int n0 = nt * (G1 ? 128 : 256 * ntw);
 
     for (int r = tid; r < BM; r += kThreads) {
-        const uint32_t id = (uint32_t)g.sorted_ids[mb * BM + r];
+        // a direct M-block's first row is pair mb, the rest padding
+        const uint32_t id =
+            !direct ? (uint32_t)g.sorted_ids[mb * BM + r]
+            : r == 0 ? ((uint32_t)(mb % g.topk) << 24) | (uint32_t)(mb / g.topk)
+                     : ((uint32_t)g.topk << 24) | (uint32_t)tokens;
         const int t = (int)(id & 0xFFFFFFu);
         const int s = (int)(id >> 24);
         const bool valid = t < tokens && s < g.topk;
@@ -170,9 +204,29 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
         }
         // routing weight of the pair (1 when none is passed: stage 2 without
         // weights, or stage 1 without doweight); stage 1 applies it only when given
-        s_w[r] = valid ? (g.sorted_w ? g.sorted_w[mb * BM + r] : 1.0f) : 0.0f;
+        s_w[r] = valid ? (g.sorted_w ? g.sorted_w[direct ? mb : mb * BM + r] : 1.0f) : 0.0f;
     }
     __syncthreads();
+    if constexpr (XQ) {
+        // the block's routed row (row 0) quantised 1x128: 16 lanes per group,
+        // 8 elements each, as the quant kernel does
+        const int t = s_arow[0];
+        const uint16_t* xr = g.xq + (int64_t)(t < 0 ? 0 : t) * g.K;
+        for (int c = tid; c < g.K / 8; c += kThreads) {
+            float v[8] = {};
+            if (t >= 0) {
+                if (g.xq_bf16)
+                    load8_f32<true>(xr + c * 8, v);
+                else
+                    load8_f32<false>(xr + c * 8, v);
+            }
+            uint2 q;
+            const float sc = quant8(v, t >= 0, &q);
+            *reinterpret_cast<uint2*>(&s_xq[c * 8]) = q;
+            if ((c & 15) == 0) s_xs[c >> 4] = sc;
+        }
+        __syncthreads();
+    }
 
     const int K = g.K;
     const int KB = K / 128;
@@ -186,7 +240,9 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
     for (int i = tid; i < BM * KBS; i += kThreads) {
         const int r = i % BM, kb = kbeg + i / BM;
         const int arow = s_arow[r];
-        s_sa[kb * BM + r] = arow >= 0 ? g.a_scale[arow * g.sa_row + kb * g.sa_kb] : 0.0f;
+        s_sa[kb * BM + r] = arow < 0 ? 0.0f
+                            : XQ   ? s_xs[kb]
+                                   : g.a_scale[arow * g.sa_row + kb * g.sa_kb];
     }
     if (!W4) {
         // stage 1: blocks gate, up; stage 2: the 2 * ntw 128-column blocks
@@ -250,9 +306,17 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
         }
 #pragma unroll
         for (int rt = 0; rt < NRT; ++rt) {
-            const uint8_t* p = asrc[rt] + kb * 128;
-            s.a[rt][0] = *reinterpret_cast<const v4i*>(p);
-            s.a[rt][1] = *reinterpret_cast<const v4i*>(p + AHI);
+            if constexpr (XQ) {
+                // every row of the tile reads the routed row (row 0); the
+                // padding rows' results are not stored
+                const int o = kb * 128 + (W4 ? lq * 16 : lq * 32);
+                s.a[rt][0] = *reinterpret_cast<const v4i*>(&s_xq[o]);
+                s.a[rt][1] = *reinterpret_cast<const v4i*>(&s_xq[o + AHI]);
+            } else {
+                const uint8_t* p = asrc[rt] + kb * 128;
+                s.a[rt][0] = *reinterpret_cast<const v4i*>(p);
+                s.a[rt][1] = *reinterpret_cast<const v4i*>(p + AHI);
+            }
         }
     };
 
@@ -678,22 +742,30 @@ template <int BM>
 constexpr int max_depth() { return BM == 16 ? 4 : 2; }
 
 // KB: the K steps of one workgroup (split-K: KB / ksplit).
-template <int BM, int STAGE, bool SHUFFLED, bool W4>
+template <int BM, int STAGE, bool SHUFFLED, bool W4, bool XQ = false>
 static void launch_depth(int KB, dim3 grid, const Args& a, hipStream_t s) {
     constexpr int DM = max_depth<BM>();
     if (DM >= 4 && KB % 4 == 0)
-        hipLaunchKernelGGL((moe_gemm_stream_kernel<BM, STAGE, SHUFFLED, W4, DM >= 4 ? 4 : 2>),
+        hipLaunchKernelGGL((moe_gemm_stream_kernel<BM, STAGE, SHUFFLED, W4, DM >= 4 ? 4 : 2, XQ>),
                            grid, dim3(kThreads), 0, s, a);
     else if (KB % 2 == 0)
-        hipLaunchKernelGGL((moe_gemm_stream_kernel<BM, STAGE, SHUFFLED, W4, 2>), grid,
+        hipLaunchKernelGGL((moe_gemm_stream_kernel<BM, STAGE, SHUFFLED, W4, 2, XQ>), grid,
                            dim3(kThreads), 0, s, a);
     else
-        hipLaunchKernelGGL((moe_gemm_stream_kernel<BM, STAGE, SHUFFLED, W4, 1>), grid,
+        hipLaunchKernelGGL((moe_gemm_stream_kernel<BM, STAGE, SHUFFLED, W4, 1, XQ>), grid,
                            dim3(kThreads), 0, s, a);
 }
 
 template <int STAGE, bool SHUFFLED, bool W4>
 static void launch_bm(int bm, int KB, dim3 grid, const Args& a, hipStream_t s) {
+    if constexpr (STAGE == 1) {
+        if (a.xq) {
+            AMD_CHECK(bm == 16 && a.dir_ids && a.ksplit == 1,
+                      "in-kernel activation quant needs direct 16-row M-blocks, one K range");
+            launch_depth<16, STAGE, SHUFFLED, W4, true>(KB, grid, a, s);
+            return;
+        }
+    }
     if (bm == 16)
         launch_depth<16, STAGE, SHUFFLED, W4>(KB, grid, a, s);
     else if (bm == 32)
@@ -814,9 +886,21 @@ void launch_moe_stage1_stream(const uint8_t* a, const float* a_scale, int64_t sa
                               float* a2_scale, int64_t a_rows, int64_t K, int64_t inter,
                               int64_t E, int64_t topk, int64_t block_m, int64_t max_m_blocks,
                               int shuffled, hipStream_t stream, const float* sorted_w, int act,
-                              int ksplit, void* kpart, int32_t* kcnt, int64_t kmb) {
+                              int ksplit, void* kpart, int32_t* kcnt, int64_t kmb,
+                              StreamDirect direct) {
     stream::Args g{};
     g.ksplit = ksplit > 1 ? ksplit : 1;
+    AMD_CHECK(!direct.ids || (block_m == 16 && g.ksplit == 1 && direct.zero_bytes % 16 == 0 &&
+                              max_m_blocks == direct.tokens * topk),
+              "direct M-blocks need block_m 16, one K range and one M-block per pair");
+    AMD_CHECK(!direct.xq || direct.xq_dtype == DT_BF16 || direct.xq_dtype == DT_FP16,
+              "activations to quantise must be bf16 or fp16");
+    g.dir_ids = direct.ids;
+    g.dir_tokens = direct.tokens;
+    g.xq = reinterpret_cast<const uint16_t*>(direct.xq);
+    g.xq_bf16 = direct.xq_dtype == DT_BF16;
+    g.zero = reinterpret_cast<v4i*>(direct.zero);
+    g.zero_n16 = direct.zero ? direct.zero_bytes / 16 : 0;
     AMD_CHECK(g.ksplit == 1 || (kpart && kcnt && kmb > 0 && (K / 128) % g.ksplit == 0),
               "split-K needs partial and counter buffers and K steps divisible by the split");
     g.kpart = reinterpret_cast<v4f*>(kpart);
@@ -915,8 +999,13 @@ void launch_moe_stage2_stream(const uint8_t* a2, const float* a2_scale, const ui
                               const int32_t* sorted_eids, const int32_t* num_valid, void* acc, int acc_dtype,
                               int64_t a_rows, int64_t inter, int64_t hidden, int64_t E,
                               int64_t topk, int64_t block_m, int64_t max_m_blocks, int shuffled,
-                              hipStream_t stream) {
+                              hipStream_t stream, StreamDirect direct) {
+    AMD_CHECK(!direct.ids || (block_m == 16 && max_m_blocks == direct.tokens * topk && !direct.xq &&
+                              !direct.zero),
+              "direct M-blocks need block_m 16 and one M-block per pair");
     stream::Args g{};
+    g.dir_ids = direct.ids;
+    g.dir_tokens = direct.tokens;
     g.a = a2;
     g.a_scale = a2_scale;
     g.sa_row = inter / 128;

@@ -819,3 +819,89 @@ def test_fused_moe_hip_graph_replay(cuda_device, T, bm):
             assert mx <= 1e-2 and rms <= 1e-3, (i, mx, rms)
         if i == 0:   # per stage: one fp8 requant tie moves a small output past max-rel here
             _fullshape.stagewise_vs_oracle(cfg, dev, ref, got, bm, A.ActivationType.Silu)
+
+
+# ------------------------------------------- one token: direct M-blocks ---
+def _bf16_close(a, b):
+    """Within one bf16 rounding of each other: the two layers sum the same
+    fp32 terms into the accumulator with atomics, in different orders."""
+    a, b = a.float(), b.float()
+    return bool(((a - b).abs() <= 2.0 ** -7 * torch.maximum(a.abs(), b.abs()) + 1e-30).all())
+
+
+def test_fused_moe_direct_t1_stagewise(cuda_device):
+    """MiMo decode T=1 on direct M-blocks (no sorting launch: the GEMMs read
+    the routing, stage 1 quantises the token and clears the accumulator),
+    checked per stage against the oracle."""
+    _fullshape.stagewise_check(W.mimo_decode(1), cuda_device, (16,))
+
+
+@pytest.mark.parametrize("weights", ["fp8", "mxfp4"])
+def test_fused_moe_direct_matches_sorted(cuda_device, monkeypatch, weights):
+    """At MiMo T=1 the direct layer's stage-1 output (fp8 a2 and its scales,
+    read back from the layer's workspace) equals the sorted layer's bitwise:
+    the in-kernel quant runs the quant kernel's arithmetic and each pair's
+    M-block holds the same rows; the outputs agree to one bf16 rounding. The
+    staggered K walk is off here (AITER_AMD_ST_ROT=0): its rotation follows
+    the M-block index, which differs between the two layouts, and with it the
+    order of stage 1's fp32 K sum."""
+    monkeypatch.setenv("AITER_AMD_ST_ROT", "0")
+    cfg = W.mimo_decode(1) if weights == "fp8" else W.mimo_a8w4(1)
+    wts = W.make_weights(cfg, device=cuda_device, shuffle=False)
+    x = W.make_hidden(cfg, device=cuda_device)
+    tw, ids = W.make_routing(cfg, device=cuda_device)
+    w1s, w2s = A.shuffle_weight(wts["w1"]), A.shuffle_weight(wts["w2"])
+    res = {}
+    for direct in (1, 0):
+        monkeypatch.setenv("AITER_AMD_DIRECT", str(direct))
+        res[direct] = _fullshape.run_layer_keep_a2(cfg, x, w1s, w2s, wts["w1_scale"],
+                                                   wts["w2_scale"], tw, ids, None, 16)
+    torch.cuda.synchronize()
+    (o1, a21, s21), (o0, a20, s20) = res[1], res[0]
+    assert torch.equal(a21.view(torch.uint8), a20.view(torch.uint8))
+    assert torch.equal(s21, s20)
+    assert torch.count_nonzero(o1).item() > 0 and _bf16_close(o1, o0)
+
+
+def _one_token_ref(cfg, x, ids, tw, doweight, activation):
+    """The oracle layer for activations x and routing (ids, tw) on cfg's weights."""
+    wts = W.make_weights(cfg, device="cpu", shuffle=False)
+    return R.fused_moe_ref(x.float().cpu().numpy(), wts["w1"].view(torch.uint8).numpy(),
+                           wts["w1_scale"].numpy(), wts["w2"].view(torch.uint8).numpy(),
+                           wts["w2_scale"].numpy(), ids.cpu().numpy(), tw.cpu().numpy(),
+                           None, doweight_stage1=doweight, activation=activation)
+
+
+@pytest.mark.parametrize("case", ["plain", "fp16", "doweight", "gelu", "fp8_input", "dup_ids"])
+def test_fused_moe_direct_small(cuda_device, monkeypatch, case):
+    """One token at a small shape (stage 1 kept to one K range, so the layer
+    runs on direct M-blocks) against the oracle and against the sorted layer:
+    fp16 activations, doweight_stage1, GeLU, a pre-quantised fp8 input, and
+    both of the token's slots routed to one expert (two direct M-blocks of
+    the same expert, where sorting puts both pairs in one)."""
+    monkeypatch.setenv("AITER_AMD_ST_KSPLIT1", "1")
+    cfg = W.MoEConfig("one_token", 1, 1024, 512, 8, 2, seed=31)
+    dw = case == "doweight"
+    act = "gelu" if case == "gelu" else "silu"
+    dev, _ = _make_layer(cfg, cuda_device, True, doweight=dw, activation=act)
+    if case == "dup_ids":
+        dev["ids"] = torch.full_like(dev["ids"], 3)
+    if case == "fp16":
+        dev["x"] = dev["x"].to(torch.float16)
+    ref = _one_token_ref(cfg, dev["x"], dev["ids"], dev["tw"], dw, act)
+    kw = dict(doweight_stage1=dw,
+              activation=A.ActivationType.Gelu if act == "gelu" else A.ActivationType.Silu)
+    outs = {}
+    for direct in (1, 0):
+        monkeypatch.setenv("AITER_AMD_DIRECT", str(direct))
+        if case == "fp8_input":
+            a1, a1s = A.per_group_quant_hip(dev["x"])
+            outs[direct] = A.fused_moe(a1, dev["w1"], dev["w2"], dev["tw"], dev["ids"],
+                                       quant_type=A.QuantType.per_128x128, w1_scale=dev["s1"],
+                                       w2_scale=dev["s2"], a1_scale=a1s, dtype=torch.bfloat16,
+                                       **kw)
+        else:
+            outs[direct] = _run(dev, block_size_M=16, **kw)
+    torch.cuda.synchronize()
+    _check(ref["out"], _np(outs[1].float()), f"direct one token {case}")
+    assert _bf16_close(outs[1], outs[0]), case
