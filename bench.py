@@ -154,6 +154,26 @@ def time_steps(fn, steps, warmup):
     return s.elapsed_time(e) / steps, wall
 
 
+def time_steady(fn, args, min_ms=50.0, warm_ms=20.0):
+    """(ms per step, steps timed) for a workload reported beside the headline:
+    at least max(--steps, 20) steps and at least min_ms of device time, after
+    at least warm_ms of warm-up. A timed region of about a millisecond
+    measures the GPU leaving its idle clocks rather than the kernels
+    (measured on MI355X, the decode T=1 layer: 47-55 us over 20 steps after
+    3 warm-up steps, 45.4 us over 200 after 20)."""
+    import math
+
+    wait = _SETTLE_AFTER - time.monotonic()
+    if wait > 0:
+        time.sleep(wait)
+    est, _ = time_steps(fn, 5, max(args.warmup, 1))
+    est = max(est, 1e-3)
+    steps = max(args.steps, 20, math.ceil(min_ms / est))
+    warm = max(args.warmup, math.ceil(warm_ms / est))
+    ms, _ = time_steps(fn, steps, warm)
+    return ms, steps
+
+
 STEP_NAMES = ("sorting", "act_quant", "stage1", "stage2", "finish")
 
 
@@ -240,6 +260,33 @@ def stage_inputs(layer):
     return sid, sw, se, nv, acc, a1, a1s
 
 
+_SETTLE_AFTER = 0.0
+
+
+def graph_seconds(fn, reps, replays):
+    """Device seconds per call of fn: reps calls captured back to back in a
+    HIP graph, the graph replayed `replays` times between two events."""
+    import torch
+
+    global _SETTLE_AFTER
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        for _ in range(reps):
+            fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    ms, _ = time_steps(graph.replay, replays, 0)
+    del graph
+    torch.cuda.synchronize()
+    _SETTLE_AFTER = time.monotonic() + 3.0       # see stage1_b2b_seconds
+    return ms * 1e-3 / reps
+
+
 def stage1_b2b_seconds(layer, reps, warmup, replays=3):
     """Device time of one stage-1 launch: `reps` launches on the layer's own
     inputs captured back to back in a HIP graph, replayed between two events.
@@ -266,6 +313,12 @@ def stage1_b2b_seconds(layer, reps, warmup, replays=3):
     ms, _ = time_steps(graph.replay, replays, 0)
     del graph
     torch.cuda.synchronize()
+    # short launches issued in the next few seconds run slower (measured on
+    # MI355X: the decode T=1 layer timed right after this function ran on
+    # decode T=32 took 48.9 us, 3 s later 45.0 us, with or without the graph
+    # destroyed): the next timing waits that long
+    global _SETTLE_AFTER
+    _SETTLE_AFTER = time.monotonic() + 3.0
     return ms * 1e-3 / reps
 
 
@@ -479,13 +532,16 @@ def route_leg(name, args, dev):
     bias = (torch.randn(E, generator=g) * 0.3).to(dev)
     w = torch.empty(T, k, dtype=torch.float32, device=dev)
     ids = torch.empty(T, k, dtype=torch.int32, device=dev)
-    iters = max(args.steps, 50)
     byts = T * E * 2 + T * k * 8
     out = {"workload": name, "tokens": T, "experts": E, "topk": k, "alg_bytes": byts}
     for tag, fn in (("softmax_topk", lambda: A.topk_softmax(w, ids, None, x, True)),
                     ("biased_grouped_topk",
                      lambda: A.biased_grouped_topk(x, bias, w, ids, 8, 4, True, 2.5))):
-        ms, _ = time_steps(fn, iters, args.warmup)
+        # the router kernel alone: a call's host side (~15 us of Python and
+        # ctypes) is longer than the kernel, so eager calls would time the
+        # host; 100 calls back to back in a HIP graph time the kernel
+        time_steady(fn, args)                       # warm the clocks
+        ms = graph_seconds(fn, 100, 5) * 1e3
         sec = ms * 1e-3
         out[tag] = {"us": round(ms * 1e3, 2), "hbm_gbps": round(byts / sec / 1e9, 1),
                     "hbm_peak_frac": round(byts / sec / PEAK_HBM_BPS, 4)}
@@ -514,12 +570,11 @@ def dense_ceiling_leg(name, args, dev):
                 sa = torch.rand(M, 1, device=dev) + 0.5
                 sb = torch.rand(1, N, device=dev) + 0.5
             fn = lambda: torch._scaled_mm(a, b, scale_a=sa, scale_b=sb, out_dtype=torch.bfloat16)
-            ms, _ = time_steps(fn, max(args.steps, 20), args.warmup)
+            ms, _ = time_steady(fn, args)
             tf = 2.0 * M * N * K / (ms * 1e-3)
             out[f"M{M}_{scales}"] = {"us": round(ms * 1e3, 1), "tflops": round(tf / 1e12, 1),
                                      "fp8_peak_frac": round(tf / PEAK_FP8_FLOPS, 4)}
         del a, b
-    torch.cuda.empty_cache()
     return out
 
 
@@ -535,12 +590,11 @@ def hbm_ceiling_leg(name, args, dev):
     out = {"workload": name, "bytes": n}
     for tag, fn, byts in (("sum_read", lambda: torch.sum(x.view(torch.int64)), n),
                           ("copy", lambda: y.copy_(x), 2 * n)):
-        ms, _ = time_steps(fn, max(args.steps, 20), args.warmup)
+        ms, _ = time_steady(fn, args)
         bw = byts / (ms * 1e-3)
         out[tag] = {"us": round(ms * 1e3, 1), "tbps": round(bw / 1e12, 3),
                     "hbm_peak_frac": round(bw / PEAK_HBM_BPS, 4)}
     del x, y
-    torch.cuda.empty_cache()
     return out
 
 
@@ -551,8 +605,6 @@ def one_launch_leg(name, args, dev):
     =0, and the tuned table's choice."""
     import importlib
     import os
-
-    import torch
 
     from aiter_amd import workloads as W
 
@@ -569,7 +621,7 @@ def one_launch_leg(name, args, dev):
     try:
         for tag, v in (("one_launch", "1"), ("two_launch", "0")):
             os.environ["AITER_AMD_FUSED"] = v
-            ms, _ = time_steps(lay.run, max(args.steps, 20), args.warmup)
+            ms, _ = time_steady(lay.run, args)
             out[f"{tag}_ms"] = round(ms, 4)
     finally:
         if old is None:
@@ -578,7 +630,6 @@ def one_launch_leg(name, args, dev):
             os.environ["AITER_AMD_FUSED"] = old
     out["one_launch_speedup"] = round(out["two_launch_ms"] / out["one_launch_ms"], 3)
     del lay
-    torch.cuda.empty_cache()
     return out
 
 
@@ -593,21 +644,20 @@ def leg(name, args, dev):
         return dense_ceiling_leg(name, args, dev)
     if name == "hbm_ceiling":
         return hbm_ceiling_leg(name, args, dev)
-    import torch
-
     from aiter_amd import workloads as W
 
     cfg = make_cfg(name)
     log(f"leg {cfg.name}")
     lay = Layer(cfg, dev)
-    ms, _ = time_steps(lay.run, max(args.steps, 20), args.warmup)
+    ms, steps = time_steady(lay.run, args)
     sec = ms * 1e-3
     flops = 2.0 * lay.pairs * 3 * cfg.inter_dim * cfg.model_dim
     byts = W.layer_bytes(cfg, lay.distinct)
-    kt, _ = layer_step_times(lay, max(args.steps, 20))
+    kt, _ = layer_step_times(lay, steps)
     f1, b1 = stage1_work(lay)
     out = {"workload": cfg.name, "weights": cfg.weights, "tokens": cfg.tokens,
-           "ms_per_step": round(ms, 4), "tokens_per_s": round(cfg.tokens / sec, 1),
+           "ms_per_step": round(ms, 4), "steps_timed": steps,
+           "tokens_per_s": round(cfg.tokens / sec, 1),
            "tflops": round(flops / sec / 1e12, 2),
            "fp8_peak_frac": round(flops / sec / PEAK_FP8_FLOPS, 4),
            "hbm_gbps": round(byts / sec / 1e9, 1),
@@ -617,8 +667,12 @@ def leg(name, args, dev):
            "kernels_us": {k: round(v * 1e6, 1) for k, v in kt.items()},
            "stage1_roofline": stage1_roofline(lay, f1, b1, name, max(args.steps, 20),
                                               args.warmup)}
+    # the leg's tensors go back to torch's cache, not to the driver: the next
+    # workload reuses those blocks. Returning several GiB to the driver slows
+    # the GPU for a few seconds (measured on MI355X, decode T=1 layer: 45.0 us,
+    # 48.8 us right after an empty_cache of 6 GiB, 45.3 us 5 s later), and
+    # the next workload's timing would fall inside that window.
     del lay
-    torch.cuda.empty_cache()
     return out
 
 
@@ -689,15 +743,15 @@ def main():
         line["cpu_baseline"]["extrapolated_" + cfg.name] = cpu_extrapolated_mimo(layer)
     if not args.no_decode and not args.workload.startswith("decode"):
         dcfg = make_cfg("decode32")
-        del layer
-        torch.cuda.empty_cache()
+        del layer                      # kept in torch's cache (see leg())
         log(f"decode leg {dcfg.name}")
         dl = Layer(dcfg, dev)
-        dms, _ = time_steps(dl.run, max(args.steps, 20), args.warmup)
+        dms, dsteps = time_steady(dl.run, args)
         db = W.layer_bytes(dcfg, dl.distinct)
-        dkt, _ = layer_step_times(dl, max(args.steps, 20))
+        dkt, _ = layer_step_times(dl, dsteps)
         df1, db1 = stage1_work(dl)
         line["decode"] = {"workload": dcfg.name, "ms_per_step": round(dms, 4),
+                          "steps_timed": dsteps,
                           "tokens_per_s": round(dcfg.tokens / (dms * 1e-3), 1),
                           "hbm_gbps": round(db / (dms * 1e-3) / 1e9, 1),
                           "hbm_peak_frac": round(db / (dms * 1e-3) / PEAK_HBM_BPS, 4),
@@ -706,11 +760,9 @@ def main():
                           "stage1_roofline": stage1_roofline(dl, df1, db1, "decode32",
                                                              max(args.steps, 20), args.warmup)}
         del dl
-        torch.cuda.empty_cache()
     if legs:
         if "layer" in locals():
             del layer
-            torch.cuda.empty_cache()
         line["legs"] = {}
         for name in legs:
             try:
