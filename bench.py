@@ -292,7 +292,12 @@ def stage1_b2b_seconds(layer, reps, warmup, replays=3):
     inputs captured back to back in a HIP graph, replayed between two events.
     The launches queue behind one another with no host work in between, so
     the dispatch latency that an event pair around a single short launch
-    includes is paid once (the kernel duration a profiler reports)."""
+    includes is paid once (the kernel duration a profiler reports). Before
+    the timed replays the graph is replayed for at least 20 ms, so the time
+    does not depend on how busy the GPU was before. Returns (seconds per
+    launch, stage-1 launches issued here)."""
+    import math
+
     import torch
 
     cfg = layer.cfg
@@ -310,7 +315,12 @@ def stage1_b2b_seconds(layer, reps, warmup, replays=3):
             fn()
     graph.replay()
     torch.cuda.synchronize()
+    one, _ = time_steps(graph.replay, 1, 0)
+    warm = max(0, math.ceil(20.0 / max(one, 1e-3)) - 2)
+    for _ in range(warm):
+        graph.replay()
     ms, _ = time_steps(graph.replay, replays, 0)
+    launches = max(warmup, 1) + reps * (2 + warm + replays)
     del graph
     torch.cuda.synchronize()
     # short launches issued in the next few seconds run slower (measured on
@@ -319,16 +329,16 @@ def stage1_b2b_seconds(layer, reps, warmup, replays=3):
     # destroyed): the next timing waits that long
     global _SETTLE_AFTER
     _SETTLE_AFTER = time.monotonic() + 3.0
-    return ms * 1e-3 / reps
+    return ms * 1e-3 / reps, launches
 
 
 def stage1_roofline(layer, flops, byts, workload, reps, warmup):
     """The roofline object of the stage-1 kernel: algorithmic work over its
     back-to-back launch time, the committed traffic summary of this
     workload, and the launch time itself (kernel_us)."""
-    sec = stage1_b2b_seconds(layer, reps, warmup)
+    sec, launches = stage1_b2b_seconds(layer, reps, warmup)
     return dict(roofline(flops, byts, sec), traffic=measured_traffic(workload),
-                alg_bytes=round(byts), kernel_us=round(sec * 1e6, 1))
+                alg_bytes=round(byts), kernel_us=round(sec * 1e6, 1), launches=launches)
 
 
 def stage1_work(layer):
