@@ -905,3 +905,44 @@ def test_fused_moe_direct_small(cuda_device, monkeypatch, case):
     torch.cuda.synchronize()
     _check(ref["out"], _np(outs[1].float()), f"direct one token {case}")
     assert _bf16_close(outs[1], outs[0]), case
+
+
+@pytest.mark.parametrize("shape", ["small", "mimo"])
+def test_fused_moe_direct_hip_graph_replay(cuda_device, monkeypatch, shape):
+    """One token on direct M-blocks captured in a HIP graph: stage 1 quantises
+    the token and clears stage 2's accumulator with its own stores (nothing
+    to record but kernels), so each of three replays on new inputs, with
+    eager layers and synchronisation in between, matches an eager call to
+    one bf16 rounding (fp32 atomics in another order)."""
+    if shape == "small":
+        monkeypatch.setenv("AITER_AMD_ST_KSPLIT1", "1")   # one K range: direct M-blocks
+        cfg = W.MoEConfig("graph_one_token", 1, 1024, 512, 8, 2, seed=37)
+        dev, _ = _make_layer(cfg, cuda_device, True)
+        run = lambda x: _run(dict(dev, x=x), block_size_M=16)
+    else:
+        cfg = W.mimo_decode(1)
+        wts = W.make_weights(cfg, device=cuda_device, shuffle=True)
+        tw, ids = W.make_routing(cfg, device=cuda_device)
+        dev = dict(x=W.make_hidden(cfg, device=cuda_device))
+        run = lambda x: A.fused_moe(x, wts["w1"], wts["w2"], tw, ids,
+                                    quant_type=A.QuantType.per_128x128,
+                                    w1_scale=wts["w1_scale"], w2_scale=wts["w2_scale"])
+    xs = [dev["x"]] + [torch.randn_like(dev["x"].float()).to(torch.bfloat16) for _ in range(2)]
+    static_x = dev["x"].clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            run(static_x)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        static_out = run(static_x)
+    for i, x in enumerate(xs):
+        static_x.copy_(x)
+        graph.replay()
+        torch.cuda.synchronize()
+        got = static_out.float().clone()
+        eager = run(x).float()
+        torch.cuda.synchronize()
+        assert torch.count_nonzero(got).item() > 0 and _bf16_close(got, eager), f"replay {i}"
