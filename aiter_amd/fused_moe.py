@@ -31,8 +31,22 @@ from .tune import tuned_block_m, tuned_config
 BLOCK_SIZE_M = 32
 
 
+# torch's current stream as a raw hipStream_t without building a Stream
+# object (a few microseconds of host time per layer call at decode sizes)
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(dev: torch.device) -> int:
+    if _RAW_STREAM is not None and dev.index is not None:
+        return _RAW_STREAM(dev.index)
     return torch.cuda.current_stream(dev).cuda_stream
+
+
+@functools.lru_cache(maxsize=1024)
+def _layer_workspace_bytes(M: int, model_dim: int, inter_dim: int, E: int, global_E: int,
+                           topk: int, block_m: int) -> int:
+    return _abi.query("aiter_amd_fused_moe_workspace_bytes", M, model_dim, inter_dim, E,
+                      global_E, topk, block_m)
 
 
 @functools.lru_cache(maxsize=16)
@@ -446,8 +460,7 @@ def _fused_moe_impl(hidden_states, w1, w2, topk_weight, topk_ids, expert_mask, a
     if hidden_states.dtype != dtypes.fp8:
         # one C-ABI call runs the whole layer
         x = hidden_states.contiguous()
-        ws_bytes = _abi.query("aiter_amd_fused_moe_workspace_bytes", M, model_dim, inter_dim,
-                              E, global_E, topk, block_m)
+        ws_bytes = _layer_workspace_bytes(M, model_dim, inter_dim, E, global_E, topk, block_m)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
         one = select_run_1stage(M, topk, E, model_dim, inter_dim, a8w4, block_m, device)
         _abi.call(

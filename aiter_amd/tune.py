@@ -69,8 +69,21 @@ def tuned_block_m(cu_num: int, token: int, model_dim: int, inter_dim: int, exper
 def tuned_config(cu_num: int, token: int, model_dim: int, inter_dim: int, expert: int,
                  topk: int, q_type: str, q_dtype_w: str):
     """(block_m, run_1stage) for this shape, or None when the table has no row."""
-    table = _load(os.environ.get("AITER_AMD_TUNED_FMOE", str(TABLE)))
-    return table.get(_key(cu_num, token, model_dim, inter_dim, expert, topk, q_type, q_dtype_w))
+    return _config(os.environ.get("AITER_AMD_TUNED_FMOE", str(TABLE)), cu_num,
+                   padded_tokens(token), model_dim, inter_dim, expert, topk, q_type, q_dtype_w)
+
+
+def clear_cache() -> None:
+    """Forget the loaded tables and their lookups (after a table file changed)."""
+    _load.cache_clear()
+    _config.cache_clear()
+
+
+@functools.lru_cache(maxsize=4096)
+def _config(path, cu_num, token, model_dim, inter_dim, expert, topk, q_type, q_dtype_w):
+    # one lookup per shape and table: fused_moe asks twice per call
+    return _load(path).get(_key(cu_num, token, model_dim, inter_dim, expert, topk, q_type,
+                                q_dtype_w))
 
 
 def _candidates(model_dim: int, inter_dim: int):
@@ -172,7 +185,7 @@ def main(argv=None):
                            int(r["expert"]), int(r["topk"]), int(r["token"]))
         for r in sorted(keep + rows, key=order):
             w.writerow({c: r.get(c, "") for c in COLUMNS})
-    _load.cache_clear()
+    clear_cache()
     print(f"wrote {len(keep) + len(rows)} rows to {a.out}", file=sys.stderr)
 
 

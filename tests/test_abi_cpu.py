@@ -529,7 +529,7 @@ def test_tuned_table_run_1stage(tmp_path, monkeypatch):
     monkeypatch.setenv("AITER_AMD_TUNED_FMOE", str(table))
     monkeypatch.delenv("AITER_AMD_FUSED", raising=False)
     monkeypatch.setattr(F, "_cu_num", lambda dev: 256)
-    tune._load.cache_clear()
+    tune.clear_cache()
     try:
         args = (4096, 2048, False, 16, torch.device("cpu"))
         assert F.select_run_1stage(2, 8, 256, *args)
@@ -545,4 +545,4 @@ def test_tuned_table_run_1stage(tmp_path, monkeypatch):
         monkeypatch.setenv("AITER_AMD_FUSED", "1")
         assert F.select_run_1stage(8, 8, 256, *args)
     finally:
-        tune._load.cache_clear()
+        tune.clear_cache()
