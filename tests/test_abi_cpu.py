@@ -5,6 +5,7 @@ the reference's ctypes error bridge (csrc/include/aiter_ctypes_error.h:
 60-147).  Also host-side logic of the Python layer.
 """
 import ctypes
+import importlib
 import re
 from pathlib import Path
 
@@ -125,6 +126,22 @@ def test_fused_validation_errors(lib):
     # sorted ids/weights + a1 + a2 + f32 accumulator dominate
     assert ws > 8192 * 4096 * (1 + 4) + 8192 * 8 * 2048
     assert lib.aiter_amd_fused_moe_workspace_bytes(64, 4096, 2048, 32, 16, 8, 0) == -1
+
+
+def test_cached_workspace_size_follows_the_ksplit_override(lib, monkeypatch):
+    """The host path caches the layer's workspace size per shape; the
+    stage-1 K-split override (AITER_AMD_ST_KSPLIT1) sizes the split's partial
+    sums, so a new value must give the new size, not the cached one."""
+    F = importlib.import_module("aiter_amd.fused_moe")   # the module, not the function
+    shape = (5, 2048, 512, 8, 8, 4, 16)
+    monkeypatch.setenv("AITER_AMD_ST_KSPLIT1", "1")
+    one = F._layer_workspace_bytes(*shape)
+    monkeypatch.setenv("AITER_AMD_ST_KSPLIT1", "4")
+    four = F._layer_workspace_bytes(*shape)
+    assert four > one
+    assert four == lib.aiter_amd_fused_moe_workspace_bytes(*shape)
+    monkeypatch.setenv("AITER_AMD_ST_KSPLIT1", "1")
+    assert F._layer_workspace_bytes(*shape) == one
 
 
 def test_workspace_a2_offsets_lie_inside_the_workspace():
