@@ -856,6 +856,180 @@ static int k_rotation() {
     return !env || atoi(env) != 0;
 }
 
+// ---- one token: stage 2 with the token's routed slots summed in a workgroup ----
+// With one token every routed pair adds into the same output row, so a
+// workgroup can own 32 output columns and run the down GEMM of all the
+// token's pairs for them: wave w takes slots w, w + 4, ... Each slot's K
+// blocks fold into a per-slot fp32 sum (a2 scale x w2 scale per 128-K block,
+// as in the streaming kernel), which is weighted and added to the wave's
+// row; the four waves' rows meet in LDS and are added in wave order, rounded
+// once and stored (plus the addend when one is given). No atomics, no
+// accumulator and no finishing pass, and the summation order is fixed. FP8
+// weights only: measured on MI355X at MiMo T=1, FP8 45.0 -> 43.6 us, but
+// MXFP4 30.8 -> 33.7 us (its per-step e8m0 loads each touch 16 rows' cache
+// lines), so an MXFP4 layer keeps the streaming stage 2.
+struct TokArgs {
+    const uint8_t* a2;          // fp8 [topk, I]: the token's pairs
+    const float* a2_scale;      // [topk, I / 128]
+    const uint8_t* w2;          // fp8 [E, H, I]
+    const float* w2_scale;      // [E, H / 128, I / 128]
+    const int32_t* ids;         // [topk] experts of the token's slots
+    const float* route_w;       // [topk] routing weights, or NULL (weights applied in stage 1)
+    void* out;                  // [H] bf16 / fp16
+    int out_dtype;
+    const void* addend;         // [H] added before the rounding, or NULL (may alias out)
+    int topk;
+    int H;
+    int I;
+    int E;
+};
+
+struct TokStep {
+    v4i a[2];
+    v4i b[2][2];
+    float sc;                   // a2 scale x w2 scale
+};
+
+template <bool SHUFFLED, int D>
+__global__ __launch_bounds__(kThreads) void moe_token_stage2_kernel(TokArgs g) {
+    __shared__ float s_row[kWaves][32];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wv = tid >> 6;
+    const int lr = lane & 15;
+    const int lq = lane >> 4;
+    const int c0 = blockIdx.x * 32;
+    const int I = g.I;
+    const int KB = I / 128;
+    constexpr int BSTEP = SHUFFLED ? 2048 : 128;
+    constexpr int BHI = SHUFFLED ? 256 : 16;
+    const int nsl = wv < g.topk ? (g.topk - wv + kWaves - 1) / kWaves : 0;
+    const int nsteps = nsl * KB;          // a multiple of D (D divides KB)
+
+    // step q: slot wv + 4 (q / KB), K block q % KB; eraw is that slot's expert
+    // id, fetched a slot ahead so that no weight load waits on it
+    auto load = [&](TokStep& st, int q, int eraw) __attribute__((always_inline)) {
+        const int sl = wv + kWaves * (q / KB);
+        const int kb = q - (q / KB) * KB;
+        const bool ok = eraw >= 0 && eraw < g.E;
+        const int e = ok ? eraw : 0;
+        const uint8_t* ap = g.a2 + (int64_t)sl * I + kb * 128 + lq * 32;
+        const v4i a0 = *reinterpret_cast<const v4i*>(ap);
+        const v4i a1 = *reinterpret_cast<const v4i*>(ap + 16);
+        // a slot routed outside [0, E) contributes nothing: zero operands
+        st.a[0] = ok ? a0 : v4i{0, 0, 0, 0};
+        st.a[1] = ok ? a1 : v4i{0, 0, 0, 0};
+        const uint8_t* we = g.w2 + (int64_t)e * g.H * I;
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+            const int row0 = c0 + 16 * ct;
+            const uint8_t* bp = SHUFFLED ? we + (int64_t)row0 * I + lq * 512 + lr * 16
+                                         : we + (int64_t)(row0 + lr) * I + lq * 32;
+            bp += (int64_t)kb * BSTEP;
+            st.b[ct][0] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(bp));
+            st.b[ct][1] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(bp + BHI));
+        }
+        const float sa = g.a2_scale[(int64_t)sl * KB + kb];
+        const float sw = g.w2_scale[((int64_t)e * (g.H / 128) + c0 / 128) * KB + kb];
+        st.sc = sa * sw;
+    };
+    v4f pacc[2] = {v4f{0.f, 0.f, 0.f, 0.f}, v4f{0.f, 0.f, 0.f, 0.f}};
+    v4f row[2] = {v4f{0.f, 0.f, 0.f, 0.f}, v4f{0.f, 0.f, 0.f, 0.f}};
+    auto compute = [&](const TokStep& st) __attribute__((always_inline)) {
+        const v8i af = v8i{st.a[0][0], st.a[0][1], st.a[0][2], st.a[0][3],
+                           st.a[1][0], st.a[1][1], st.a[1][2], st.a[1][3]};
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+            const v8i bf = v8i{st.b[ct][0][0], st.b[ct][0][1], st.b[ct][0][2], st.b[ct][0][3],
+                               st.b[ct][1][0], st.b[ct][1][1], st.b[ct][1][2], st.b[ct][1][3]};
+            const v4f blk = mfma16x16x128_fp8(af, bf);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) pacc[ct][v] += blk[v] * st.sc;
+        }
+    };
+    // a slot's K blocks are done: weight its sum into the row
+    auto fold_slot = [&](float rw) __attribute__((always_inline)) {
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) row[ct][v] += pacc[ct][v] * rw;
+            pacc[ct] = v4f{0.f, 0.f, 0.f, 0.f};
+        }
+    };
+    auto slot_id = [&](int j) { return j < nsl ? g.ids[wv + kWaves * j] : 0; };
+    auto slot_w = [&](int j) { return g.route_w ? g.route_w[wv + kWaves * j] : 1.0f; };
+    TokStep buf[D];
+    if (nsteps > 0) {
+        // D divides KB, so a group of D steps lies in one slot and slots
+        // change only between groups
+        int jl = 0;                         // slot of the steps being loaded
+        int el = slot_id(0), en = slot_id(1);
+        float rw = slot_w(0);               // weight of the slot being computed
+#pragma unroll
+        for (int d = 0; d < D; ++d) load(buf[d], d, el);
+        int q0 = 0;
+        for (; q0 < nsteps - D; q0 += D) {
+            const bool slot_end = (q0 + D) % KB == 0;
+            if (slot_end) {                 // this group's loads start slot jl + 1
+                ++jl;
+                el = en;
+                en = slot_id(jl + 1);
+            }
+#pragma unroll
+            for (int d = 0; d < D; ++d) {
+                compute(buf[d]);
+                load(buf[d], q0 + D + d, el);
+            }
+            if (slot_end) {
+                fold_slot(rw);
+                rw = slot_w(jl);
+            }
+        }
+#pragma unroll
+        for (int d = 0; d < D; ++d) compute(buf[d]);
+        fold_slot(rw);
+    }
+    // output row 0 sits in lanes lq == 0, element 0: column lr of each tile
+    if (lq == 0) {
+        s_row[wv][lr] = row[0][0];
+        s_row[wv][16 + lr] = row[1][0];
+    }
+    __syncthreads();
+    if (tid < 32) {
+        float v = s_row[0][tid];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) v += s_row[w][tid];
+        uint16_t* o = reinterpret_cast<uint16_t*>(g.out) + c0 + tid;
+        const uint16_t* ad = reinterpret_cast<const uint16_t*>(g.addend);
+        if (g.out_dtype == DT_BF16) {
+            if (ad) v += bf16_bits_to_f32(ad[c0 + tid]);
+            *o = f32_to_bf16_bits(v);
+        } else {
+            if (ad) v += fp16_bits_to_f32(ad[c0 + tid]);
+            *o = f32_to_fp16_bits(v);
+        }
+    }
+}
+
+// D K steps in flight per wave (D divides the K steps): 8 where it can, as
+// many weight bytes in flight as the streaming stage 2 (measured on MI355X
+// at MiMo T=1: the layer 43.6 us at 8, 44.8 us at 4).
+template <bool SHUFFLED>
+static void launch_token_stage2(int KB, int grid, const TokArgs& a, hipStream_t s) {
+    if (KB % 8 == 0)
+        hipLaunchKernelGGL((moe_token_stage2_kernel<SHUFFLED, 8>), dim3(grid), dim3(kThreads), 0,
+                           s, a);
+    else if (KB % 4 == 0)
+        hipLaunchKernelGGL((moe_token_stage2_kernel<SHUFFLED, 4>), dim3(grid), dim3(kThreads), 0,
+                           s, a);
+    else if (KB % 2 == 0)
+        hipLaunchKernelGGL((moe_token_stage2_kernel<SHUFFLED, 2>), dim3(grid), dim3(kThreads), 0,
+                           s, a);
+    else
+        hipLaunchKernelGGL((moe_token_stage2_kernel<SHUFFLED, 1>), dim3(grid), dim3(kThreads), 0,
+                           s, a);
+}
+
 }  // namespace stream
 
 bool stream_supported(int64_t block_m, int64_t K);
@@ -870,6 +1044,44 @@ int stream_stage1_ksplit(int64_t block_m, int64_t K, int64_t inter, int64_t est_
 int64_t stream_ksplit_part_bytes(int64_t block_m, int64_t mblocks, int64_t inter, int64_t ksplit) {
     if (ksplit <= 1) return 0;
     return mblocks * (inter / 128) * ksplit * stream::kThreads * (block_m / 16) * stream::kNCT * 16;
+}
+
+// Stage 2 of a one-token FP8 layer straight into its bf16 / fp16 output row
+// (see moe_token_stage2_kernel): a2 [topk, inter] fp8 with its 1x128 scales,
+// fp8 w2 with 128x128 scales, the token's expert ids and routing weights
+// (NULL: applied in stage 1), out and an optional addend [hidden]. hidden a
+// multiple of 32, inter of 128.
+void launch_moe_token_stage2(const uint8_t* a2, const float* a2_scale, const uint8_t* w2,
+                             const float* w2_scale, const int32_t* ids, const float* route_w,
+                             void* out, int out_dtype, const void* addend, int64_t topk,
+                             int64_t hidden, int64_t inter, int64_t E, int shuffled,
+                             hipStream_t stream) {
+    AMD_CHECK(hidden % 32 == 0 && hidden > 0, "model_dim must be a multiple of 32");
+    AMD_CHECK(inter % 128 == 0 && inter > 0 && inter / 128 <= stream::kMaxKB,
+              "inter_dim must be a multiple of 128 up to 8192");
+    AMD_CHECK(topk >= 1 && topk <= 32, "topk must be in [1, 32]");
+    AMD_CHECK(out_dtype == DT_BF16 || out_dtype == DT_FP16, "out dtype must be bf16 or fp16");
+    AMD_CHECK(w2_scale != nullptr, "w2 scales are NULL");
+    stream::TokArgs g{};
+    g.a2 = a2;
+    g.a2_scale = a2_scale;
+    g.w2 = w2;
+    g.w2_scale = w2_scale;
+    g.ids = ids;
+    g.route_w = route_w;
+    g.out = out;
+    g.out_dtype = out_dtype;
+    g.addend = addend;
+    g.topk = (int)topk;
+    g.H = (int)hidden;
+    g.I = (int)inter;
+    g.E = (int)E;
+    const int KB = (int)(inter / 128), grid = (int)(hidden / 32);
+    if (shuffled)
+        stream::launch_token_stage2<true>(KB, grid, g, stream);
+    else
+        stream::launch_token_stage2<false>(KB, grid, g, stream);
+    AMD_HIP_CHECK(hipGetLastError());
 }
 
 // 16/32-row M-blocks, K a multiple of 128 up to 8192; stage 2 also needs

@@ -824,15 +824,16 @@ def test_fused_moe_hip_graph_replay(cuda_device, T, bm):
 # ------------------------------------------- one token: direct M-blocks ---
 def _bf16_close(a, b):
     """Within one bf16 rounding of each other: the two layers sum the same
-    fp32 terms into the accumulator with atomics, in different orders."""
+    fp32 terms in different orders (the sorted layer with fp32 atomics, the
+    direct FP8 layer per token in slot order)."""
     a, b = a.float(), b.float()
     return bool(((a - b).abs() <= 2.0 ** -7 * torch.maximum(a.abs(), b.abs()) + 1e-30).all())
 
 
 def test_fused_moe_direct_t1_stagewise(cuda_device):
     """MiMo decode T=1 on direct M-blocks (no sorting launch: the GEMMs read
-    the routing, stage 1 quantises the token and clears the accumulator),
-    checked per stage against the oracle."""
+    the routing, stage 1 quantises the token, stage 2 sums the token's slots
+    straight into the output row), checked per stage against the oracle."""
     _fullshape.stagewise_check(W.mimo_decode(1), cuda_device, (16,))
 
 
@@ -907,26 +908,32 @@ def test_fused_moe_direct_small(cuda_device, monkeypatch, case):
     assert _bf16_close(outs[1], outs[0]), case
 
 
-@pytest.mark.parametrize("shape", ["small", "mimo"])
+@pytest.mark.parametrize("shape", ["small", "mimo", "mimo_a8w4"])
 def test_fused_moe_direct_hip_graph_replay(cuda_device, monkeypatch, shape):
-    """One token on direct M-blocks captured in a HIP graph: stage 1 quantises
-    the token and clears stage 2's accumulator with its own stores (nothing
-    to record but kernels), so each of three replays on new inputs, with
-    eager layers and synchronisation in between, matches an eager call to
-    one bf16 rounding (fp32 atomics in another order)."""
+    """One token on direct M-blocks captured in a HIP graph (nothing to
+    record but kernels): each of three replays on new inputs, with eager
+    layers and synchronisation in between, matches an eager call. FP8: bit
+    for bit (stage 2 sums each output in a fixed order, no atomics). MXFP4:
+    stage 1 clears stage 2's accumulator with its own stores and stage 2
+    adds with fp32 atomics, so to one bf16 rounding."""
     if shape == "small":
         monkeypatch.setenv("AITER_AMD_ST_KSPLIT1", "1")   # one K range: direct M-blocks
         cfg = W.MoEConfig("graph_one_token", 1, 1024, 512, 8, 2, seed=37)
         dev, _ = _make_layer(cfg, cuda_device, True)
         run = lambda x: _run(dict(dev, x=x), block_size_M=16)
     else:
-        cfg = W.mimo_decode(1)
+        w4 = shape == "mimo_a8w4"
+        cfg = W.mimo_a8w4(1) if w4 else W.mimo_decode(1)
         wts = W.make_weights(cfg, device=cuda_device, shuffle=True)
         tw, ids = W.make_routing(cfg, device=cuda_device)
         dev = dict(x=W.make_hidden(cfg, device=cuda_device))
-        run = lambda x: A.fused_moe(x, wts["w1"], wts["w2"], tw, ids,
-                                    quant_type=A.QuantType.per_128x128,
-                                    w1_scale=wts["w1_scale"], w2_scale=wts["w2_scale"])
+        if w4:
+            run = lambda x: A.fused_moe_a8w4(x, wts["w1"], wts["w2"], tw, ids,
+                                             w1_scale=wts["w1_scale"], w2_scale=wts["w2_scale"])
+        else:
+            run = lambda x: A.fused_moe(x, wts["w1"], wts["w2"], tw, ids,
+                                        quant_type=A.QuantType.per_128x128,
+                                        w1_scale=wts["w1_scale"], w2_scale=wts["w2_scale"])
     xs = [dev["x"]] + [torch.randn_like(dev["x"].float()).to(torch.bfloat16) for _ in range(2)]
     static_x = dev["x"].clone()
     side = torch.cuda.Stream()
@@ -945,4 +952,8 @@ def test_fused_moe_direct_hip_graph_replay(cuda_device, monkeypatch, shape):
         got = static_out.float().clone()
         eager = run(x).float()
         torch.cuda.synchronize()
-        assert torch.count_nonzero(got).item() > 0 and _bf16_close(got, eager), f"replay {i}"
+        assert torch.count_nonzero(got).item() > 0, f"replay {i}"
+        if shape == "mimo_a8w4":
+            assert _bf16_close(got, eager), f"replay {i}"
+        else:
+            assert torch.equal(got, eager), f"replay {i}"
