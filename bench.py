@@ -287,15 +287,18 @@ def graph_seconds(fn, reps, replays):
     return ms * 1e-3 / reps
 
 
-def stage1_b2b_seconds(layer, reps, warmup, replays=3):
-    """Device time of one stage-1 launch: `reps` launches on the layer's own
-    inputs captured back to back in a HIP graph, replayed between two events.
-    The launches queue behind one another with no host work in between, so
-    the dispatch latency that an event pair around a single short launch
-    includes is paid once (the kernel duration a profiler reports). Before
-    the timed replays the graph is replayed for at least 20 ms, so the time
-    does not depend on how busy the GPU was before. Returns (seconds per
-    launch, stage-1 launches issued here)."""
+def stage1_b2b_seconds(layer, reps, warmup, replays=3, min_replay_ms=4.0):
+    """Device time of one stage-1 launch: launches on the layer's own inputs
+    captured back to back in a HIP graph, replayed between two events. The
+    launches queue behind one another with no host work in between, so no
+    per-launch dispatch latency is counted. A replay itself adds a fixed
+    15-21 us to the event interval (measured on MI355X against rocprofv3's
+    dispatch timestamps, from a 30 us to a 1.5 ms kernel), so the graph holds
+    at least `reps` launches and at least min_replay_ms of them, which keeps
+    that cost under 0.5% of a launch. Before the timed replays the graph is
+    replayed for at least 20 ms, so the time does not depend on how busy the
+    GPU was before. Returns (seconds per launch, stage-1 launches issued
+    here, launches per timed replay)."""
     import math
 
     import torch
@@ -306,21 +309,31 @@ def stage1_b2b_seconds(layer, reps, warmup, replays=3):
     bm = layer.block_m_used()
     fn = lambda: st1(a1, a1s, layer.w["w1"], layer.w["w1_scale"], sid, se, nv, cfg.topk, bm,
                      True)
+
+    def capture(n):
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(n):
+                fn()
+        return graph
+
     for _ in range(max(warmup, 1)):
         fn()
     torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for _ in range(reps):
-            fn()
+    graph = capture(reps)
     graph.replay()
     torch.cuda.synchronize()
     one, _ = time_steps(graph.replay, 1, 0)
-    warm = max(0, math.ceil(20.0 / max(one, 1e-3)) - 2)
+    launches = max(warmup, 1) + 2 * reps
+    n = max(reps, math.ceil(min_replay_ms * reps / max(one, 1e-3)))
+    if n > reps:
+        del graph
+        graph = capture(n)
+    warm = max(1, math.ceil(20.0 * reps / (max(one, 1e-3) * n)))
     for _ in range(warm):
         graph.replay()
     ms, _ = time_steps(graph.replay, replays, 0)
-    launches = max(warmup, 1) + reps * (2 + warm + replays)
+    launches += n * (warm + replays)
     del graph
     torch.cuda.synchronize()
     # short launches issued in the next few seconds run slower (measured on
@@ -329,16 +342,17 @@ def stage1_b2b_seconds(layer, reps, warmup, replays=3):
     # destroyed): the next timing waits that long
     global _SETTLE_AFTER
     _SETTLE_AFTER = time.monotonic() + 3.0
-    return ms * 1e-3 / reps, launches
+    return ms * 1e-3 / n, launches, n
 
 
 def stage1_roofline(layer, flops, byts, workload, reps, warmup):
     """The roofline object of the stage-1 kernel: algorithmic work over its
     back-to-back launch time, the committed traffic summary of this
     workload, and the launch time itself (kernel_us)."""
-    sec, launches = stage1_b2b_seconds(layer, reps, warmup)
+    sec, launches, per_replay = stage1_b2b_seconds(layer, reps, warmup)
     return dict(roofline(flops, byts, sec), traffic=measured_traffic(workload),
-                alg_bytes=round(byts), kernel_us=round(sec * 1e6, 1), launches=launches)
+                alg_bytes=round(byts), kernel_us=round(sec * 1e6, 1), launches=launches,
+                launches_per_replay=per_replay)
 
 
 def stage1_work(layer):
