@@ -229,8 +229,9 @@ def stagewise_check(cfg, device, block_ms, log=print):
 def stagewise_vs_oracle(cfg, dev, ref, out, bm, activation, doweight=False, log=print,
                         e2e_rms=True):
     """The same split for a small layer, against the CPU oracle: stage 1's
-    fp8 codes against the oracle's a2 (at most 0.5% different, each element
-    within one top-binade e4m3 step of its group), the layer's output against the oracle's stage 2 applied to
+    fp8 codes against the oracle's a2 (each group scale within one bf16 ulp,
+    at most 0.5% of the codes different in the groups whose scales agree,
+    each element within one top-binade e4m3 step of its group), the layer's output against the oracle's stage 2 applied to
     the kernel's own a2 (the strict normalised bar), and RMS-rel against the
     whole oracle chain. For layers whose smallest outputs sit next to a
     one-step requant flip (GELU(gate)·up makes such ties common), where the
@@ -262,9 +263,19 @@ def stagewise_vs_oracle(cfg, dev, ref, out, bm, activation, doweight=False, log=
     sc = np.repeat(ref["a2s"], 128, axis=-1)
     with np.errstate(divide="ignore", over="ignore", invalid="ignore"):   # unrouted pairs
         err = (np.abs(a2d - ref_d) / (sc * 448))[loc]
-    differ = (codes != ref["a2q"])[loc].mean()
-    log(f"[{cfg.name} bm={bm}] stage 1 codes differing {differ:.3%}, element err/amax "
+    # a group whose largest element sits on a bf16 rounding tie gets a scale
+    # one bf16 ulp away, which moves every code of the group: the scales are
+    # held to that ulp, and the codes are compared in the groups whose scales
+    # agree (with one token such a group alone is 1/8 of a pair's codes)
+    gs = a2s.cpu().numpy().reshape(T, k, -1)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        srel = (np.abs(gs - ref["a2s"]) / ref["a2s"])[loc]
+    same = np.repeat(gs == ref["a2s"], 128, axis=-1)
+    differ = (codes != ref["a2q"])[same & loc[..., None]].mean()
+    log(f"[{cfg.name} bm={bm}] stage 1 codes differing {differ:.3%} (groups with equal scales; "
+        f"{int((srel > 0).sum())} of {srel.size} scales one bf16 ulp off), element err/amax "
         f"{err.max():.4f}")
+    assert srel.max() <= BF16_ULP * (1 + 1e-6), srel.max()
     assert differ <= 0.005 and err.max() <= E4M3_TOP_ULP * (1 + 2 * BF16_ULP), (differ, err.max())
     a2d[~loc] = 0
     wts = W.make_weights(cfg, device="cpu", shuffle=False)

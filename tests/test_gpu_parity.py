@@ -873,15 +873,25 @@ def _one_token_ref(cfg, x, ids, tw, doweight, activation):
                            None, doweight_stage1=doweight, activation=activation)
 
 
-@pytest.mark.parametrize("case", ["plain", "fp16", "doweight", "gelu", "fp8_input", "dup_ids"])
+@pytest.mark.parametrize("case", ["plain", "fp16", "doweight", "gelu", "fp8_input", "dup_ids",
+                                  "topk6", "topk8", "topk12"])
 def test_fused_moe_direct_small(cuda_device, monkeypatch, case):
     """One token at a small shape (stage 1 kept to one K range, so the layer
     runs on direct M-blocks) against the oracle and against the sorted layer:
     fp16 activations, doweight_stage1, GeLU, a pre-quantised fp8 input, and
     both of the token's slots routed to one expert (two direct M-blocks of
-    the same expert, where sorting puts both pairs in one)."""
+    the same expert, where sorting puts both pairs in one). Stage 2's four
+    waves take every fourth slot: top-2 leaves two waves without a slot,
+    top-6 and top-12 give the waves unequal counts, top-8 two each. The
+    oracle check is the stage-wise one of the other small layers: with one
+    token a single one-step requant flip on a dominant a2 element moves the
+    RMS of the whole output, so the output is held to the strict bar against
+    the oracle's stage 2 on the kernel's own a2 (the staggered K walk off, so
+    that the sorted stage 1 the check runs gives the layer's a2 bit for bit)."""
     monkeypatch.setenv("AITER_AMD_ST_KSPLIT1", "1")
-    cfg = W.MoEConfig("one_token", 1, 1024, 512, 8, 2, seed=31)
+    monkeypatch.setenv("AITER_AMD_ST_ROT", "0")
+    k = int(case[4:]) if case.startswith("topk") else 2
+    cfg = W.MoEConfig("one_token", 1, 1024, 512, 16, k, seed=31 + k)
     dw = case == "doweight"
     act = "gelu" if case == "gelu" else "silu"
     dev, _ = _make_layer(cfg, cuda_device, True, doweight=dw, activation=act)
@@ -904,7 +914,8 @@ def test_fused_moe_direct_small(cuda_device, monkeypatch, case):
         else:
             outs[direct] = _run(dev, block_size_M=16, **kw)
     torch.cuda.synchronize()
-    _check(ref["out"], _np(outs[1].float()), f"direct one token {case}")
+    _fullshape.stagewise_vs_oracle(cfg, dev, ref, _np(outs[1].float()), 16, kw["activation"],
+                                   doweight=dw, e2e_rms=False)
     assert _bf16_close(outs[1], outs[0]), case
 
 
