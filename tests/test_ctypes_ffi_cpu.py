@@ -75,6 +75,20 @@ def test_descriptor_layout():
     assert d.dtype_ == 3 and d.device_id == -1
 
 
+def test_packed_descriptor_matches_the_structure():
+    """The binder packs descriptors with struct; each must be the bytes of
+    the ctypes aiter_tensor_t of the same tensor (views, 8 dims, empty, 0-d)."""
+    cases = [torch.zeros(3, 5, dtype=torch.bfloat16)[:, 1:4],
+             torch.zeros(2, 1, 3, 1, 2, 1, 2, 3, dtype=torch.int32).transpose(0, 7),
+             torch.zeros(0, 4, dtype=torch.float32), torch.tensor(1.5), torch.zeros(7, dtype=torch.uint8)]
+    for t in cases:
+        buf = bytearray(ctypes.sizeof(ffi.aiter_tensor_t))
+        ffi._pack_desc(buf, 0, t, t.get_device())
+        assert bytes(buf) == bytes(ffi.to_aiter_tensor(t)), t.shape
+    with pytest.raises(ValueError, match="at most 8 dims"):
+        ffi._pack_desc(bytearray(160), 0, torch.zeros([1] * 9), -1)
+
+
 def _call_like_the_reference(lib, name, *args):
     """What aiter/jit/core.py's caller does: clear, call with tensors by
     reference and ints as int64, then read the error."""
