@@ -304,15 +304,10 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
                 s.b[ct][W4 ? 0 : 1] =
                     __builtin_nontemporal_load(reinterpret_cast<const v4i*>(p + BHI));
         }
+        // XQ: A comes from LDS when the step is computed (no registers held)
+        if constexpr (!XQ) {
 #pragma unroll
-        for (int rt = 0; rt < NRT; ++rt) {
-            if constexpr (XQ) {
-                // every row of the tile reads the routed row (row 0); the
-                // padding rows' results are not stored
-                const int o = kb * 128 + (W4 ? lq * 16 : lq * 32);
-                s.a[rt][0] = *reinterpret_cast<const v4i*>(&s_xq[o]);
-                s.a[rt][1] = *reinterpret_cast<const v4i*>(&s_xq[o + AHI]);
-            } else {
+            for (int rt = 0; rt < NRT; ++rt) {
                 const uint8_t* p = asrc[rt] + kb * 128;
                 s.a[rt][0] = *reinterpret_cast<const v4i*>(p);
                 s.a[rt][1] = *reinterpret_cast<const v4i*>(p + AHI);
@@ -333,7 +328,12 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
 #pragma unroll
         for (int ct = 0; ct < kNCT; ++ct) {
             const uint8_t* p = bssrc[ct] + kb * 4 + (int64_t)jt * 256 * (K / 32);
-            if constexpr (D == 4) {
+            if constexpr (D == 8) {
+                const v4i v = *reinterpret_cast<const v4i*>(p);
+                const v4i u = *reinterpret_cast<const v4i*>(p + 16);
+                dst[ct][0] = v[0], dst[ct][1] = v[1], dst[ct][2] = v[2], dst[ct][3] = v[3];
+                dst[ct][4] = u[0], dst[ct][5] = u[1], dst[ct][6] = u[2], dst[ct][7] = u[3];
+            } else if constexpr (D == 4) {
                 const v4i v = *reinterpret_cast<const v4i*>(p);
                 dst[ct][0] = v[0], dst[ct][1] = v[1], dst[ct][2] = v[2], dst[ct][3] = v[3];
             } else if constexpr (D == 2) {
@@ -354,8 +354,15 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
 #pragma unroll
         for (int rt = 0; rt < NRT; ++rt) {
             const v4f sa = *reinterpret_cast<const v4f*>(&s_sa[kb * BM + rt * 16 + 4 * lq]);
-            const v8i af = v8i{s.a[rt][0][0], s.a[rt][0][1], s.a[rt][0][2], s.a[rt][0][3],
-                               s.a[rt][1][0], s.a[rt][1][1], s.a[rt][1][2], s.a[rt][1][3]};
+            v4i a0 = s.a[rt][0], a1 = s.a[rt][1];
+            if constexpr (XQ) {
+                // every row of the tile reads the routed row (row 0); the
+                // padding rows' results are not stored
+                const int o = kb * 128 + (W4 ? lq * 16 : lq * 32);
+                a0 = *reinterpret_cast<const v4i*>(&s_xq[o]);
+                a1 = *reinterpret_cast<const v4i*>(&s_xq[o + AHI]);
+            }
+            const v8i af = v8i{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
 #pragma unroll
             for (int ct = 0; ct < kNCT; ++ct) {
                 v4f blk;
@@ -745,6 +752,18 @@ constexpr int max_depth() { return BM == 16 ? 4 : 2; }
 template <int BM, int STAGE, bool SHUFFLED, bool W4, bool XQ = false>
 static void launch_depth(int KB, dim3 grid, const Args& a, hipStream_t s) {
     constexpr int DM = max_depth<BM>();
+    // One-token MXFP4 stage 1 (XQ: A from LDS, so a step holds only weight
+    // fragments, 16 bytes per lane and column tile) keeps 8 steps in flight.
+    // Measured on MI355X at MiMo T=1, alternating: A8W4 layer 30.6-30.8 ->
+    // 30.0-30.1 us; FP8 at 8 steps (256 VGPRs + 60 AGPRs, one workgroup per
+    // CU) was slower, 43.4-43.5 -> 43.9-44.0 us, so FP8 keeps 4.
+    if constexpr (XQ && W4) {
+        if (KB % 8 == 0) {
+            hipLaunchKernelGGL((moe_gemm_stream_kernel<BM, STAGE, SHUFFLED, W4, 8, XQ>), grid,
+                               dim3(kThreads), 0, s, a);
+            return;
+        }
+    }
     if (DM >= 4 && KB % 4 == 0)
         hipLaunchKernelGGL((moe_gemm_stream_kernel<BM, STAGE, SHUFFLED, W4, DM >= 4 ? 4 : 2, XQ>),
                            grid, dim3(kThreads), 0, s, a);
