@@ -97,13 +97,12 @@ int64_t stream_ksplit_part_bytes(int64_t block_m, int64_t mblocks, int64_t inter
 void launch_moe_stage2_stream(const uint8_t*, const float*, const uint8_t*, const float*,
                               const uint8_t*, const int32_t*, const float*, const int32_t*,
                               const int32_t*, void*, int, int64_t, int64_t, int64_t, int64_t,
-                              int64_t, int64_t, int64_t, int, hipStream_t,
-                              StreamDirect direct = StreamDirect{});
+                              int64_t, int64_t, int64_t, int, hipStream_t);
 
 // one token: stage 2 with the token's slots summed per workgroup, into out
 void launch_moe_token_stage2(const uint8_t*, const float*, const uint8_t*, const float*,
-                             const int32_t*, const float*, void*, int, const void*, int64_t,
-                             int64_t, int64_t, int64_t, int, hipStream_t);
+                             const uint8_t*, const int32_t*, const float*, void*, int, const void*,
+                             int64_t, int64_t, int64_t, int64_t, int, hipStream_t);
 
 // quant.hip: per-pair bf16 rows -> output
 void launch_slot_sum(const uint16_t* part, const int32_t* topk_ids, const int32_t* mask,
@@ -578,17 +577,13 @@ void fused_entry(const void* hidden_states, int hidden_dtype, const void* w1, WS
                      L.ksplit)) {
         // one token: each routed pair is its own 16-row M-block, so stage 1
         // reads the routing directly and quantises the token itself (no
-        // sorting launch). FP8: stage 2 sums the token's slots per workgroup
-        // straight into out (no atomics, no finishing pass); MXFP4 keeps the
-        // streaming stage 2, whose accumulator stage 1 clears.
-        const bool token_sum = w2s.e8m0 == nullptr;
+        // sorting launch), and stage 2 sums the token's slots per workgroup
+        // straight into out (no atomics, no finishing pass)
         StreamDirect d1;
         d1.ids = topk_ids;
         d1.tokens = (int)tokens;
         d1.xq = pre.a1 ? nullptr : hidden_states;
         d1.xq_dtype = (int)hidden_dtype;
-        d1.zero = token_sum ? nullptr : acc;
-        d1.zero_bytes = token_sum ? 0 : tokens * model_dim * 4;
         timing_mark(1, s);
         timing_mark(2, s);
         launch_moe_stage1_stream(a1, a1_scale, sa_row, sa_kb, (const uint8_t*)w1, w1s.f32,
@@ -597,23 +592,10 @@ void fused_entry(const void* hidden_states, int hidden_dtype, const void* w1, WS
                                  sh, s, dw ? topk_weights : nullptr, (int)activation, 1, nullptr,
                                  nullptr, 0, d1);
         timing_mark(3, s);
-        if (token_sum) {
-            launch_moe_token_stage2(a2, a2_scale, (const uint8_t*)w2, w2s.f32, topk_ids,
-                                    dw ? nullptr : topk_weights, out, out_dtype, addend, topk,
-                                    model_dim, inter_dim, num_experts, sh, s);
-            timing_mark(4, s);
-            timing_mark(5, s);
-            return;
-        }
-        StreamDirect d2;
-        d2.ids = topk_ids;
-        d2.tokens = (int)tokens;
-        launch_moe_stage2_stream(a2, a2_scale, (const uint8_t*)w2, w2s.f32, w2s.e8m0, nullptr,
-                                 dw ? nullptr : topk_weights, nullptr, nullptr, acc, DT_FP32,
-                                 tokens * topk, inter_dim, model_dim, num_experts, topk, block_m,
-                                 tokens * topk, sh, s, d2);
+        launch_moe_token_stage2(a2, a2_scale, (const uint8_t*)w2, w2s.f32, w2s.e8m0, topk_ids,
+                                dw ? nullptr : topk_weights, out, out_dtype, addend, topk,
+                                model_dim, inter_dim, num_experts, sh, s);
         timing_mark(4, s);
-        launch_acc_to_out(acc, out, out_dtype, nullptr, tokens, model_dim, s, addend);
         timing_mark(5, s);
         return;
     }

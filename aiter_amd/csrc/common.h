@@ -199,17 +199,15 @@ constexpr int kOutA2 = 0;
 constexpr int kOutAct = 1;
 constexpr int kOutGateUp = 2;
 
-// Direct M-blocks for the decode kernel (a layer too small to be worth a
-// sorting launch): M-block p holds routing pair p of `tokens` tokens, its
-// expert ids[p]. Stage 1 may also quantise the activations xq (bf16 / fp16
-// [tokens, K]) itself and clear zero_bytes at zero (stage 2's accumulator).
+// Direct M-blocks for the decode kernel's stage 1 (a one-token layer, too
+// small to be worth a sorting launch): M-block p holds routing pair p of
+// `tokens` tokens, its expert ids[p]. Stage 1 may also quantise the
+// activations xq (bf16 / fp16 [tokens, K]) itself.
 struct StreamDirect {
     const int32_t* ids = nullptr;
     int tokens = 0;
     const void* xq = nullptr;
     int xq_dtype = 0;
-    void* zero = nullptr;
-    int64_t zero_bytes = 0;
 };
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }

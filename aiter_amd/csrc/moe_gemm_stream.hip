@@ -110,10 +110,6 @@ struct Args {
     // kernel's arithmetic (a and a_scale are not read)
     const uint16_t* xq;
     int xq_bf16;
-    // zero_n16 16-byte words cleared by the launch's workgroups before their
-    // tiles (stage 1 with direct M-blocks: stage 2's fp32 accumulator)
-    v4i* zero;
-    int64_t zero_n16;
 };
 
 // One K step of one wave's operands.
@@ -155,13 +151,6 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_stream_kernel(Args g) {
     const int wv = tid >> 6;
     const int lr = lane & 15;
     const int lq = lane >> 4;
-
-    if (g.zero) {
-        const int64_t nwg = (int64_t)gridDim.x * gridDim.y;
-        const int64_t wg = (int64_t)blockIdx.y * gridDim.x + blockIdx.x;
-        for (int64_t i = wg * kThreads + tid; i < g.zero_n16; i += nwg * kThreads)
-            g.zero[i] = v4i{0, 0, 0, 0};
-    }
 
     const int mb = blockIdx.y;
     const bool direct = g.dir_ids != nullptr;
@@ -883,15 +872,18 @@ static int k_rotation() {
 // as in the streaming kernel), which is weighted and added to the wave's
 // row; the four waves' rows meet in LDS and are added in wave order, rounded
 // once and stored (plus the addend when one is given). No atomics, no
-// accumulator and no finishing pass, and the summation order is fixed. FP8
-// weights only: measured on MI355X at MiMo T=1, FP8 45.0 -> 43.6 us, but
-// MXFP4 30.8 -> 33.7 us (its per-step e8m0 loads each touch 16 rows' cache
-// lines), so an MXFP4 layer keeps the streaming stage 2.
+// accumulator and no finishing pass, and the summation order is fixed.
+// Measured on MI355X at MiMo T=1 against the streaming stage 2 with its fp32
+// atomics and finishing pass: FP8 45.0 -> 43.6 us; MXFP4 29.9-30.0 -> 29.5
+// us with each lane loading its rows' e8m0 bytes of the D steps in flight at
+// once (4 D bytes, as the streaming kernel does), where a load per step had
+// made it slower (33.7 us).
 struct TokArgs {
     const uint8_t* a2;          // fp8 [topk, I]: the token's pairs
     const float* a2_scale;      // [topk, I / 128]
-    const uint8_t* w2;          // fp8 [E, H, I]
-    const float* w2_scale;      // [E, H / 128, I / 128]
+    const uint8_t* w2;          // fp8 [E, H, I] or packed e2m1 [E, H, I / 2]
+    const float* w2_scale;      // [E, H / 128, I / 128] (fp8 weights)
+    const uint8_t* w2_scale8;   // [E, H, I / 32] e8m0 (MXFP4 weights)
     const int32_t* ids;         // [topk] experts of the token's slots
     const float* route_w;       // [topk] routing weights, or NULL (weights applied in stage 1)
     void* out;                  // [H] bf16 / fp16
@@ -903,13 +895,14 @@ struct TokArgs {
     int E;
 };
 
+template <bool W4>
 struct TokStep {
     v4i a[2];
-    v4i b[2][2];
-    float sc;                   // a2 scale x w2 scale
+    v4i b[2][W4 ? 1 : 2];
+    float sc;                   // a2 scale (x w2 scale for fp8 weights)
 };
 
-template <bool SHUFFLED, int D>
+template <bool SHUFFLED, bool W4, int D>
 __global__ __launch_bounds__(kThreads) void moe_token_stage2_kernel(TokArgs g) {
     __shared__ float s_row[kWaves][32];
     const int tid = threadIdx.x;
@@ -920,48 +913,93 @@ __global__ __launch_bounds__(kThreads) void moe_token_stage2_kernel(TokArgs g) {
     const int c0 = blockIdx.x * 32;
     const int I = g.I;
     const int KB = I / 128;
-    constexpr int BSTEP = SHUFFLED ? 2048 : 128;
+    const int KBY = W4 ? I / 2 : I;
+    constexpr int BSTEP = W4 ? (SHUFFLED ? 1024 : 64) : (SHUFFLED ? 2048 : 128);
     constexpr int BHI = SHUFFLED ? 256 : 16;
+    constexpr int AHI = W4 ? 64 : 16;
     const int nsl = wv < g.topk ? (g.topk - wv + kWaves - 1) / kWaves : 0;
     const int nsteps = nsl * KB;          // a multiple of D (D divides KB)
 
     // step q: slot wv + 4 (q / KB), K block q % KB; eraw is that slot's expert
     // id, fetched a slot ahead so that no weight load waits on it
-    auto load = [&](TokStep& st, int q, int eraw) __attribute__((always_inline)) {
+    auto load = [&](TokStep<W4>& st, int q, int eraw) __attribute__((always_inline)) {
         const int sl = wv + kWaves * (q / KB);
         const int kb = q - (q / KB) * KB;
         const bool ok = eraw >= 0 && eraw < g.E;
         const int e = ok ? eraw : 0;
-        const uint8_t* ap = g.a2 + (int64_t)sl * I + kb * 128 + lq * 32;
+        const uint8_t* ap = g.a2 + (int64_t)sl * I + kb * 128 + (W4 ? lq * 16 : lq * 32);
         const v4i a0 = *reinterpret_cast<const v4i*>(ap);
-        const v4i a1 = *reinterpret_cast<const v4i*>(ap + 16);
+        const v4i a1 = *reinterpret_cast<const v4i*>(ap + AHI);
         // a slot routed outside [0, E) contributes nothing: zero operands
         st.a[0] = ok ? a0 : v4i{0, 0, 0, 0};
         st.a[1] = ok ? a1 : v4i{0, 0, 0, 0};
-        const uint8_t* we = g.w2 + (int64_t)e * g.H * I;
+        const uint8_t* we = g.w2 + (int64_t)e * g.H * KBY;
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct) {
             const int row0 = c0 + 16 * ct;
-            const uint8_t* bp = SHUFFLED ? we + (int64_t)row0 * I + lq * 512 + lr * 16
-                                         : we + (int64_t)(row0 + lr) * I + lq * 32;
+            const uint8_t* bp;
+            if (W4)
+                bp = SHUFFLED ? we + (int64_t)row0 * KBY + lane * 16
+                              : we + (int64_t)(row0 + lr) * KBY + lq * 16;
+            else
+                bp = SHUFFLED ? we + (int64_t)row0 * I + lq * 512 + lr * 16
+                              : we + (int64_t)(row0 + lr) * I + lq * 32;
             bp += (int64_t)kb * BSTEP;
             st.b[ct][0] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(bp));
-            st.b[ct][1] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(bp + BHI));
+            if (!W4)
+                st.b[ct][W4 ? 0 : 1] =
+                    __builtin_nontemporal_load(reinterpret_cast<const v4i*>(bp + BHI));
         }
         const float sa = g.a2_scale[(int64_t)sl * KB + kb];
-        const float sw = g.w2_scale[((int64_t)e * (g.H / 128) + c0 / 128) * KB + kb];
-        st.sc = sa * sw;
+        st.sc = W4 ? sa : sa * g.w2_scale[((int64_t)e * (g.H / 128) + c0 / 128) * KB + kb];
+    };
+    // MXFP4: the e8m0 dwords of the D steps from q (one slot, kb a multiple
+    // of D) of the lane's two weight rows; step d's byte for this lane is
+    // byte lq of dword d
+    auto load_e8 = [&](int (&dst)[2][D], int q, int eraw) __attribute__((always_inline)) {
+        if constexpr (W4) {
+            const int kb = q - (q / KB) * KB;
+            const int e = eraw >= 0 && eraw < g.E ? eraw : 0;
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct) {
+                const uint8_t* p =
+                    g.w2_scale8 + ((int64_t)e * g.H + c0 + 16 * ct + lr) * (I / 32) + kb * 4;
+#pragma unroll
+                for (int h = 0; h < (D + 3) / 4; ++h) {
+                    if constexpr (D >= 4) {
+                        const v4i v = *reinterpret_cast<const v4i*>(p + 16 * h);
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) dst[ct][4 * h + i] = v[i];
+                    } else if constexpr (D == 2) {
+                        const v2i v = *reinterpret_cast<const v2i*>(p);
+                        dst[ct][0] = v[0], dst[ct][1] = v[1];
+                    } else {
+                        dst[ct][0] = *reinterpret_cast<const int*>(p);
+                    }
+                }
+            }
+        }
     };
     v4f pacc[2] = {v4f{0.f, 0.f, 0.f, 0.f}, v4f{0.f, 0.f, 0.f, 0.f}};
     v4f row[2] = {v4f{0.f, 0.f, 0.f, 0.f}, v4f{0.f, 0.f, 0.f, 0.f}};
-    auto compute = [&](const TokStep& st) __attribute__((always_inline)) {
+    int e8c[2][D], e8n[2][D];               // MXFP4: the steps computed / loaded
+    auto compute = [&](const TokStep<W4>& st, int d) __attribute__((always_inline)) {
         const v8i af = v8i{st.a[0][0], st.a[0][1], st.a[0][2], st.a[0][3],
                            st.a[1][0], st.a[1][1], st.a[1][2], st.a[1][3]};
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct) {
-            const v8i bf = v8i{st.b[ct][0][0], st.b[ct][0][1], st.b[ct][0][2], st.b[ct][0][3],
-                               st.b[ct][1][0], st.b[ct][1][1], st.b[ct][1][2], st.b[ct][1][3]};
-            const v4f blk = mfma16x16x128_fp8(af, bf);
+            v4f blk;
+            if constexpr (W4) {
+                const v8i bf = v8i{st.b[ct][0][0], st.b[ct][0][1], st.b[ct][0][2],
+                                   st.b[ct][0][3], 0, 0, 0, 0};
+                blk = mfma16x16x128_fp8_fp4(af, bf, e8c[ct][d] >> (8 * lq));
+            } else {
+                const v8i bf = v8i{st.b[ct][0][0], st.b[ct][0][1], st.b[ct][0][2],
+                                   st.b[ct][0][3], st.b[ct][W4 ? 0 : 1][0],
+                                   st.b[ct][W4 ? 0 : 1][1], st.b[ct][W4 ? 0 : 1][2],
+                                   st.b[ct][W4 ? 0 : 1][3]};
+                blk = mfma16x16x128_fp8(af, bf);
+            }
 #pragma unroll
             for (int v = 0; v < 4; ++v) pacc[ct][v] += blk[v] * st.sc;
         }
@@ -977,13 +1015,14 @@ __global__ __launch_bounds__(kThreads) void moe_token_stage2_kernel(TokArgs g) {
     };
     auto slot_id = [&](int j) { return j < nsl ? g.ids[wv + kWaves * j] : 0; };
     auto slot_w = [&](int j) { return g.route_w ? g.route_w[wv + kWaves * j] : 1.0f; };
-    TokStep buf[D];
+    TokStep<W4> buf[D];
     if (nsteps > 0) {
         // D divides KB, so a group of D steps lies in one slot and slots
         // change only between groups
         int jl = 0;                         // slot of the steps being loaded
         int el = slot_id(0), en = slot_id(1);
         float rw = slot_w(0);               // weight of the slot being computed
+        load_e8(e8c, 0, el);
 #pragma unroll
         for (int d = 0; d < D; ++d) load(buf[d], d, el);
         int q0 = 0;
@@ -994,10 +1033,17 @@ __global__ __launch_bounds__(kThreads) void moe_token_stage2_kernel(TokArgs g) {
                 el = en;
                 en = slot_id(jl + 1);
             }
+            load_e8(e8n, q0 + D, el);
 #pragma unroll
             for (int d = 0; d < D; ++d) {
-                compute(buf[d]);
+                compute(buf[d], d);
                 load(buf[d], q0 + D + d, el);
+            }
+            if constexpr (W4) {
+#pragma unroll
+                for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+                    for (int d = 0; d < D; ++d) e8c[ct][d] = e8n[ct][d];
             }
             if (slot_end) {
                 fold_slot(rw);
@@ -1005,7 +1051,7 @@ __global__ __launch_bounds__(kThreads) void moe_token_stage2_kernel(TokArgs g) {
             }
         }
 #pragma unroll
-        for (int d = 0; d < D; ++d) compute(buf[d]);
+        for (int d = 0; d < D; ++d) compute(buf[d], d);
         fold_slot(rw);
     }
     // output row 0 sits in lanes lq == 0, element 0: column lr of each tile
@@ -1033,20 +1079,20 @@ __global__ __launch_bounds__(kThreads) void moe_token_stage2_kernel(TokArgs g) {
 // D K steps in flight per wave (D divides the K steps): 8 where it can, as
 // many weight bytes in flight as the streaming stage 2 (measured on MI355X
 // at MiMo T=1: the layer 43.6 us at 8, 44.8 us at 4).
-template <bool SHUFFLED>
+template <bool SHUFFLED, bool W4>
 static void launch_token_stage2(int KB, int grid, const TokArgs& a, hipStream_t s) {
     if (KB % 8 == 0)
-        hipLaunchKernelGGL((moe_token_stage2_kernel<SHUFFLED, 8>), dim3(grid), dim3(kThreads), 0,
-                           s, a);
+        hipLaunchKernelGGL((moe_token_stage2_kernel<SHUFFLED, W4, 8>), dim3(grid), dim3(kThreads),
+                           0, s, a);
     else if (KB % 4 == 0)
-        hipLaunchKernelGGL((moe_token_stage2_kernel<SHUFFLED, 4>), dim3(grid), dim3(kThreads), 0,
-                           s, a);
+        hipLaunchKernelGGL((moe_token_stage2_kernel<SHUFFLED, W4, 4>), dim3(grid), dim3(kThreads),
+                           0, s, a);
     else if (KB % 2 == 0)
-        hipLaunchKernelGGL((moe_token_stage2_kernel<SHUFFLED, 2>), dim3(grid), dim3(kThreads), 0,
-                           s, a);
+        hipLaunchKernelGGL((moe_token_stage2_kernel<SHUFFLED, W4, 2>), dim3(grid), dim3(kThreads),
+                           0, s, a);
     else
-        hipLaunchKernelGGL((moe_token_stage2_kernel<SHUFFLED, 1>), dim3(grid), dim3(kThreads), 0,
-                           s, a);
+        hipLaunchKernelGGL((moe_token_stage2_kernel<SHUFFLED, W4, 1>), dim3(grid), dim3(kThreads),
+                           0, s, a);
 }
 
 }  // namespace stream
@@ -1065,27 +1111,28 @@ int64_t stream_ksplit_part_bytes(int64_t block_m, int64_t mblocks, int64_t inter
     return mblocks * (inter / 128) * ksplit * stream::kThreads * (block_m / 16) * stream::kNCT * 16;
 }
 
-// Stage 2 of a one-token FP8 layer straight into its bf16 / fp16 output row
-// (see moe_token_stage2_kernel): a2 [topk, inter] fp8 with its 1x128 scales,
-// fp8 w2 with 128x128 scales, the token's expert ids and routing weights
-// (NULL: applied in stage 1), out and an optional addend [hidden]. hidden a
-// multiple of 32, inter of 128.
+// Stage 2 of a one-token layer straight into its bf16 / fp16 output row (see
+// moe_token_stage2_kernel): a2 [topk, inter] fp8 with its 1x128 scales, w2
+// fp8 with 128x128 scales or MXFP4 with e8m0 bytes (w2_scale_e8m0 given), the
+// token's expert ids and routing weights (NULL: applied in stage 1), out and
+// an optional addend [hidden]. hidden a multiple of 32, inter of 128.
 void launch_moe_token_stage2(const uint8_t* a2, const float* a2_scale, const uint8_t* w2,
-                             const float* w2_scale, const int32_t* ids, const float* route_w,
-                             void* out, int out_dtype, const void* addend, int64_t topk,
-                             int64_t hidden, int64_t inter, int64_t E, int shuffled,
-                             hipStream_t stream) {
+                             const float* w2_scale, const uint8_t* w2_scale_e8m0,
+                             const int32_t* ids, const float* route_w, void* out, int out_dtype,
+                             const void* addend, int64_t topk, int64_t hidden, int64_t inter,
+                             int64_t E, int shuffled, hipStream_t stream) {
     AMD_CHECK(hidden % 32 == 0 && hidden > 0, "model_dim must be a multiple of 32");
     AMD_CHECK(inter % 128 == 0 && inter > 0 && inter / 128 <= stream::kMaxKB,
               "inter_dim must be a multiple of 128 up to 8192");
     AMD_CHECK(topk >= 1 && topk <= 32, "topk must be in [1, 32]");
     AMD_CHECK(out_dtype == DT_BF16 || out_dtype == DT_FP16, "out dtype must be bf16 or fp16");
-    AMD_CHECK(w2_scale != nullptr, "w2 scales are NULL");
+    AMD_CHECK(w2_scale_e8m0 ? true : w2_scale != nullptr, "w2 scales are NULL");
     stream::TokArgs g{};
     g.a2 = a2;
     g.a2_scale = a2_scale;
     g.w2 = w2;
     g.w2_scale = w2_scale;
+    g.w2_scale8 = w2_scale_e8m0;
     g.ids = ids;
     g.route_w = route_w;
     g.out = out;
@@ -1096,10 +1143,13 @@ void launch_moe_token_stage2(const uint8_t* a2, const float* a2_scale, const uin
     g.I = (int)inter;
     g.E = (int)E;
     const int KB = (int)(inter / 128), grid = (int)(hidden / 32);
-    if (shuffled)
-        stream::launch_token_stage2<true>(KB, grid, g, stream);
+    const bool w4 = w2_scale_e8m0 != nullptr;
+    if (w4)
+        shuffled ? stream::launch_token_stage2<true, true>(KB, grid, g, stream)
+                 : stream::launch_token_stage2<false, true>(KB, grid, g, stream);
     else
-        stream::launch_token_stage2<false>(KB, grid, g, stream);
+        shuffled ? stream::launch_token_stage2<true, false>(KB, grid, g, stream)
+                 : stream::launch_token_stage2<false, false>(KB, grid, g, stream);
     AMD_HIP_CHECK(hipGetLastError());
 }
 
@@ -1121,8 +1171,7 @@ void launch_moe_stage1_stream(const uint8_t* a, const float* a_scale, int64_t sa
                               StreamDirect direct) {
     stream::Args g{};
     g.ksplit = ksplit > 1 ? ksplit : 1;
-    AMD_CHECK(!direct.ids || (block_m == 16 && g.ksplit == 1 && direct.zero_bytes % 16 == 0 &&
-                              max_m_blocks == direct.tokens * topk),
+    AMD_CHECK(!direct.ids || (block_m == 16 && g.ksplit == 1 && max_m_blocks == direct.tokens * topk),
               "direct M-blocks need block_m 16, one K range and one M-block per pair");
     AMD_CHECK(!direct.xq || direct.xq_dtype == DT_BF16 || direct.xq_dtype == DT_FP16,
               "activations to quantise must be bf16 or fp16");
@@ -1130,8 +1179,6 @@ void launch_moe_stage1_stream(const uint8_t* a, const float* a_scale, int64_t sa
     g.dir_tokens = direct.tokens;
     g.xq = reinterpret_cast<const uint16_t*>(direct.xq);
     g.xq_bf16 = direct.xq_dtype == DT_BF16;
-    g.zero = reinterpret_cast<v4i*>(direct.zero);
-    g.zero_n16 = direct.zero ? direct.zero_bytes / 16 : 0;
     AMD_CHECK(g.ksplit == 1 || (kpart && kcnt && kmb > 0 && (K / 128) % g.ksplit == 0),
               "split-K needs partial and counter buffers and K steps divisible by the split");
     g.kpart = reinterpret_cast<v4f*>(kpart);
@@ -1230,13 +1277,8 @@ void launch_moe_stage2_stream(const uint8_t* a2, const float* a2_scale, const ui
                               const int32_t* sorted_eids, const int32_t* num_valid, void* acc, int acc_dtype,
                               int64_t a_rows, int64_t inter, int64_t hidden, int64_t E,
                               int64_t topk, int64_t block_m, int64_t max_m_blocks, int shuffled,
-                              hipStream_t stream, StreamDirect direct) {
-    AMD_CHECK(!direct.ids || (block_m == 16 && max_m_blocks == direct.tokens * topk && !direct.xq &&
-                              !direct.zero),
-              "direct M-blocks need block_m 16 and one M-block per pair");
+                              hipStream_t stream) {
     stream::Args g{};
-    g.dir_ids = direct.ids;
-    g.dir_tokens = direct.tokens;
     g.a = a2;
     g.a_scale = a2_scale;
     g.sa_row = inter / 128;

@@ -825,7 +825,7 @@ def test_fused_moe_hip_graph_replay(cuda_device, T, bm):
 def _bf16_close(a, b):
     """Within one bf16 rounding of each other: the two layers sum the same
     fp32 terms in different orders (the sorted layer with fp32 atomics, the
-    direct FP8 layer per token in slot order)."""
+    direct layer per token in slot order)."""
     a, b = a.float(), b.float()
     return bool(((a - b).abs() <= 2.0 ** -7 * torch.maximum(a.abs(), b.abs()) + 1e-30).all())
 
@@ -921,12 +921,10 @@ def test_fused_moe_direct_small(cuda_device, monkeypatch, case):
 
 @pytest.mark.parametrize("shape", ["small", "mimo", "mimo_a8w4"])
 def test_fused_moe_direct_hip_graph_replay(cuda_device, monkeypatch, shape):
-    """One token on direct M-blocks captured in a HIP graph (nothing to
-    record but kernels): each of three replays on new inputs, with eager
-    layers and synchronisation in between, matches an eager call. FP8: bit
-    for bit (stage 2 sums each output in a fixed order, no atomics). MXFP4:
-    stage 1 clears stage 2's accumulator with its own stores and stage 2
-    adds with fp32 atomics, so to one bf16 rounding."""
+    """One token on direct M-blocks captured in a HIP graph (two kernels,
+    nothing else to record): each of three replays on new inputs, with eager
+    layers and synchronisation in between, matches an eager call bit for bit
+    (stage 2 sums each output in a fixed order, no atomics), FP8 and MXFP4."""
     if shape == "small":
         monkeypatch.setenv("AITER_AMD_ST_KSPLIT1", "1")   # one K range: direct M-blocks
         cfg = W.MoEConfig("graph_one_token", 1, 1024, 512, 8, 2, seed=37)
@@ -963,8 +961,4 @@ def test_fused_moe_direct_hip_graph_replay(cuda_device, monkeypatch, shape):
         got = static_out.float().clone()
         eager = run(x).float()
         torch.cuda.synchronize()
-        assert torch.count_nonzero(got).item() > 0, f"replay {i}"
-        if shape == "mimo_a8w4":
-            assert _bf16_close(got, eager), f"replay {i}"
-        else:
-            assert torch.equal(got, eager), f"replay {i}"
+        assert torch.count_nonzero(got).item() > 0 and torch.equal(got, eager), f"replay {i}"
