@@ -89,6 +89,22 @@ def test_no_alloc_matches_workspace_entry(cuda_device, big, small, bm):
         del d
 
 
+def test_no_alloc_one_token_after_a_larger_call(cuda_device):
+    """A one-token layer (direct M-blocks: no sorting launch, stage 2 sums the
+    token's slots in a fixed order) right after a MiMo T=32 call has filled
+    the scratch buffer: bit for bit the workspace entry's output."""
+    big, one = W.mimo_decode(32), W.mimo_decode(1)
+    d = _inputs(big, cuda_device)
+    _no_alloc(d, big, 16)
+    del d
+    d = _inputs(one, cuda_device)
+    print(f"[no-alloc] {one.name} T=1 after T=32", flush=True)
+    want = _with_workspace(d, one, 16)
+    got = _no_alloc(d, one, 16)
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(got).item() > 0 and torch.equal(got, want)
+
+
 def _check(want, got, rows, atomics, name):
     want, got = want[:rows], got[:rows]
     assert torch.count_nonzero(got).item() > 0
