@@ -268,8 +268,7 @@ def stagewise_vs_oracle(cfg, dev, ref, out, bm, activation, doweight=False, log=
     # held to that ulp, and the codes are compared in the groups whose scales
     # agree (with one token such a group alone is 1/8 of a pair's codes)
     gs = a2s.cpu().numpy().reshape(T, k, -1)
-    with np.errstate(divide="ignore", invalid="ignore"):
-        srel = (np.abs(gs - ref["a2s"]) / ref["a2s"])[loc]
+    srel = np.abs(gs[loc] - ref["a2s"][loc]) / ref["a2s"][loc]   # routed pairs only
     same = np.repeat(gs == ref["a2s"], 128, axis=-1)
     differ = (codes != ref["a2q"])[same & loc[..., None]].mean()
     log(f"[{cfg.name} bm={bm}] stage 1 codes differing {differ:.3%} (groups with equal scales; "
