@@ -919,6 +919,47 @@ def test_fused_moe_direct_small(cuda_device, monkeypatch, case):
     assert _bf16_close(outs[1], outs[0]), case
 
 
+@pytest.mark.parametrize("weights", ["fp8", "mxfp4"])
+@pytest.mark.parametrize("inter", [384, 768, 1536])
+def test_fused_moe_direct_inter_sizes(cuda_device, monkeypatch, weights, inter):
+    """One token at K-step counts of 3, 6 and 12 per slot (inter 384, 768,
+    1536): the one-token stage 2 then keeps 1, 2 or 4 steps in flight per
+    wave (8 at MiMo), with fp8 or MXFP4 weights (e8m0 dwords loaded per
+    group of steps); stage-wise against the oracle and against the sorted
+    layer."""
+    monkeypatch.setenv("AITER_AMD_ST_KSPLIT1", "1")
+    monkeypatch.setenv("AITER_AMD_ST_ROT", "0")
+    mx4 = weights == "mxfp4"
+    cfg = W.MoEConfig("one_token_k", 1, 1024, inter, 16, 6, seed=inter,
+                      weights="mxfp4" if mx4 else "fp8")
+    wts = W.make_weights(cfg, device="cpu", shuffle=False)
+    x = W.make_hidden(cfg)
+    tw, ids = W.make_routing(cfg)
+    w1u = wts["w1"] if mx4 else wts["w1"].view(torch.uint8)
+    w2u = wts["w2"] if mx4 else wts["w2"].view(torch.uint8)
+    ref = R.fused_moe_ref(x.float().numpy(), w1u.numpy(), wts["w1_scale"].numpy(), w2u.numpy(),
+                          wts["w2_scale"].numpy(), ids.numpy(), tw.numpy(), None,
+                          weight_format="mxfp4" if mx4 else "fp8_128x128")
+    dev = dict(x=x.to(cuda_device), w1=A.shuffle_weight(wts["w1"]).to(cuda_device),
+               w2=A.shuffle_weight(wts["w2"]).to(cuda_device), s1=wts["w1_scale"].to(cuda_device),
+               s2=wts["w2_scale"].to(cuda_device), tw=tw.to(cuda_device), ids=ids.to(cuda_device),
+               mask=None)
+    dev["w1"].is_shuffled = dev["w2"].is_shuffled = True
+    outs = {}
+    for direct in (1, 0):
+        monkeypatch.setenv("AITER_AMD_DIRECT", str(direct))
+        if mx4:
+            outs[direct] = A.fused_moe_a8w4(dev["x"], dev["w1"], dev["w2"], dev["tw"], dev["ids"],
+                                            w1_scale=dev["s1"], w2_scale=dev["s2"],
+                                            block_size_M=16)
+        else:
+            outs[direct] = _run(dev, block_size_M=16)
+    torch.cuda.synchronize()
+    _fullshape.stagewise_vs_oracle(cfg, dev, ref, _np(outs[1].float()), 16, A.ActivationType.Silu,
+                                   e2e_rms=False)
+    assert _bf16_close(outs[1], outs[0]), (weights, inter)
+
+
 @pytest.mark.parametrize("shape", ["small", "mimo", "mimo_a8w4"])
 def test_fused_moe_direct_hip_graph_replay(cuda_device, monkeypatch, shape):
     """One token on direct M-blocks captured in a HIP graph (two kernels,
