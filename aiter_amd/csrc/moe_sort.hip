@@ -80,6 +80,7 @@ struct SortParams {
     int q_cols;
     int q_bf16;
     int q_blocks;
+    int q_first;               // the scatter launch's quant blocks start at block q_first of the quant
 };
 
 __host__ __device__ inline int table_words(int ct, int E, int cell_bytes) {
@@ -451,7 +452,7 @@ constexpr int kChunkBatch = 16;   // per-chunk counts loaded per round trip
 __global__ __launch_bounds__(kSortThreads) void moe_sort_scatter_kernel(SortParams p) {
     extern __shared__ uint32_t smem[];
     if ((int)blockIdx.x >= p.num_chunks) {   // the activation quant, beside the chunks
-        const int b = (int)blockIdx.x - p.num_chunks;
+        const int b = (int)blockIdx.x - p.num_chunks + p.q_first;
         if (p.q_bf16)
             quant_groups_block<true>(p.qx, p.qq, p.qs, p.q_rows, p.q_cols, 0, p.q_num_rows, 1, b);
         else
@@ -565,6 +566,7 @@ bool launch_moe_sort(const int32_t* topk_ids, const float* topk_w, const int32_t
     p.q_cols = 0;
     p.q_bf16 = 0;
     p.q_blocks = 0;
+    p.q_first = 0;
 
     // zero blocks: about one 16-byte store per thread per 4 iterations
     int zero_blocks = 0;
@@ -609,17 +611,22 @@ bool launch_moe_sort(const int32_t* topk_ids, const float* topk_w, const int32_t
         }
         p.sort_blocks = p.num_chunks;
         // Up to 4096 rows the activation quant rides in the scatter launch,
-        // whose few sorting blocks leave most CUs free; larger quants go in
-        // the counting launch, where they do not slow the latency-bound
-        // scatter. Measured on MI355X at MiMo dims (sort launches' time in the
-        // layer): EP share T=4096 28.7 -> 23.0 us (layer 0.304 -> 0.298 ms),
-        // T=2048 20.6 -> 18.8 us, T=8192 42.7 -> 45.0 us with the quant moved.
-        const bool q_in_scatter = rows <= 4096;
+        // whose few sorting blocks leave most CUs free; larger quants are
+        // split, half in the counting launch and half in the scatter launch,
+        // so that neither the latency-bound scatter nor the counting launch
+        // waits on all of it. Measured on MI355X at MiMo dims (sort launches'
+        // time in the layer, HIP events): EP share T=4096 all in the counting
+        // launch 28.7 -> 23.0 us in the scatter launch; T=8192 42.4 us all in
+        // the counting launch, 45.0 all in the scatter launch, 37.0 split in
+        // half (39.6 at three quarters, 40.1 at one quarter); T=2048 and the
+        // EP share are best with all of it in the scatter launch.
+        const int q_count = rows <= 4096 ? 0 : p.q_blocks / 2;   // quant blocks [0, q_count)
+        p.q_first = q_count;
         hipLaunchKernelGGL(moe_sort_count_kernel,
-                           dim3(p.num_chunks + zero_blocks + (q_in_scatter ? 0 : p.q_blocks)),
+                           dim3(p.num_chunks + zero_blocks + q_count),
                            dim3(kSortThreads), (size_t)E * 4, stream, p);
         hipLaunchKernelGGL(moe_sort_scatter_kernel,
-                           dim3(p.num_chunks + (q_in_scatter ? p.q_blocks : 0)),
+                           dim3(p.num_chunks + (p.q_blocks - q_count)),
                            dim3(kSortThreads), full_lds, stream, p);
         if (ws_in_buf) {
             const int64_t nb = std::min<int64_t>(ceil_div(p.zero_skip16, kSortThreads), 1024);
