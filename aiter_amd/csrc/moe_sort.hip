@@ -497,11 +497,12 @@ __global__ __launch_bounds__(kSortThreads) void moe_sort_scatter_kernel(SortPara
 // row-group prefix (at most 16 KB) a block's LDS stays under gfx950's 160 KB.
 // With several chunks, smaller ones spread the per-chunk walks over more
 // blocks: about 64 chunks (ct = rows / 64 rounded down to a power of two, at
-// least 16). Measured on MI355X at MiMo dims (E = 256, top-8; sort launches'
-// time in the layer): T=512 30.2 -> 17.7 us (ct 16), T=1024 29.2 -> 20.2 us
-// (16), T=2048 28.6 -> 21.6 us (32), EP share T=4096 33.2 -> 29.3 us (64),
-// T=8192 43.3 us (128; 41.1 at 64, 45.2 at 32). AITER_AMD_SORT_CT forces a
-// power of two up to the table limit.
+// least 16), about 128 above 4096 rows. Measured on MI355X at MiMo dims (E =
+// 256, top-8; sort launches' time in the layer): T=512 30.2 -> 17.7 us (ct
+// 16), T=1024 29.2 -> 20.2 us (16), T=2048 28.6 -> 21.6 us (32), EP share
+// T=4096 33.2 -> 29.3 us (64), T=8192 with the activation quant split 37.6
+// us at ct 128, 35.1 at 64, 38.0 at 32. AITER_AMD_SORT_CT forces a power of
+// two up to the table limit.
 static int sort_chunk_tokens(int E, int topk, int64_t rows) {
     const int cell = topk <= 8 ? 1 : 4;
     int ct = 256;
@@ -511,8 +512,11 @@ static int sort_chunk_tokens(int E, int topk, int64_t rows) {
             const int c = atoi(env);
             if (c >= 1 && c <= ct && (c & (c - 1)) == 0) return c;
         }
+        // T=2048, 4096 and the EP share measured level or slower with twice
+        // the chunks
+        const int64_t per_chunk = rows > 4096 ? 128 : 64;
         int c = 16;
-        while (c * 2 <= ct && (int64_t)c * 2 * 64 <= rows) c *= 2;
+        while (c * 2 <= ct && (int64_t)c * 2 * per_chunk <= rows) c *= 2;
         ct = c < ct ? c : ct;
     }
     return ct;

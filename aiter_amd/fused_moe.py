@@ -45,13 +45,15 @@ def _stream(dev: torch.device) -> int:
 def _layer_workspace_bytes(M: int, model_dim: int, inter_dim: int, E: int, global_E: int,
                            topk: int, block_m: int) -> int:
     # AITER_AMD_ST_KSPLIT1 (the stage-1 K-split override) sizes the split's
-    # partial sums, so its value is part of the cached query's key
+    # partial sums and AITER_AMD_SORT_CT (the sorting chunk override) the
+    # sorting's chunk counts, so their values are part of the cached query's key
     return _workspace_query(M, model_dim, inter_dim, E, global_E, topk, block_m,
-                            os.environ.get("AITER_AMD_ST_KSPLIT1"))
+                            os.environ.get("AITER_AMD_ST_KSPLIT1"),
+                            os.environ.get("AITER_AMD_SORT_CT"))
 
 
 @functools.lru_cache(maxsize=1024)
-def _workspace_query(M, model_dim, inter_dim, E, global_E, topk, block_m, ksplit_env):
+def _workspace_query(M, model_dim, inter_dim, E, global_E, topk, block_m, ksplit_env, ct_env):
     return _abi.query("aiter_amd_fused_moe_workspace_bytes", M, model_dim, inter_dim, E,
                       global_E, topk, block_m)
 
