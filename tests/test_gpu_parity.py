@@ -920,13 +920,14 @@ def test_fused_moe_direct_small(cuda_device, monkeypatch, case):
 
 
 @pytest.mark.parametrize("weights", ["fp8", "mxfp4"])
-@pytest.mark.parametrize("inter", [384, 768, 1536])
-def test_fused_moe_direct_inter_sizes(cuda_device, monkeypatch, weights, inter):
+@pytest.mark.parametrize("inter,variant", [(384, "plain"), (768, "plain"), (1536, "plain"),
+                                           (768, "doweight_gelu")])
+def test_fused_moe_direct_inter_sizes(cuda_device, monkeypatch, weights, inter, variant):
     """One token at K-step counts of 3, 6 and 12 per slot (inter 384, 768,
     1536): the one-token stage 2 then keeps 1, 2 or 4 steps in flight per
     wave (8 at MiMo), with fp8 or MXFP4 weights (e8m0 dwords loaded per
-    group of steps); stage-wise against the oracle and against the sorted
-    layer."""
+    group of steps), and once with doweight_stage1 and GeLU; stage-wise
+    against the oracle and against the sorted layer."""
     monkeypatch.setenv("AITER_AMD_ST_KSPLIT1", "1")
     monkeypatch.setenv("AITER_AMD_ST_ROT", "0")
     mx4 = weights == "mxfp4"
@@ -937,9 +938,12 @@ def test_fused_moe_direct_inter_sizes(cuda_device, monkeypatch, weights, inter):
     tw, ids = W.make_routing(cfg)
     w1u = wts["w1"] if mx4 else wts["w1"].view(torch.uint8)
     w2u = wts["w2"] if mx4 else wts["w2"].view(torch.uint8)
+    dw = variant == "doweight_gelu"
+    act = A.ActivationType.Gelu if dw else A.ActivationType.Silu
     ref = R.fused_moe_ref(x.float().numpy(), w1u.numpy(), wts["w1_scale"].numpy(), w2u.numpy(),
                           wts["w2_scale"].numpy(), ids.numpy(), tw.numpy(), None,
-                          weight_format="mxfp4" if mx4 else "fp8_128x128")
+                          weight_format="mxfp4" if mx4 else "fp8_128x128", doweight_stage1=dw,
+                          activation="gelu" if dw else "silu")
     dev = dict(x=x.to(cuda_device), w1=A.shuffle_weight(wts["w1"]).to(cuda_device),
                w2=A.shuffle_weight(wts["w2"]).to(cuda_device), s1=wts["w1_scale"].to(cuda_device),
                s2=wts["w2_scale"].to(cuda_device), tw=tw.to(cuda_device), ids=ids.to(cuda_device),
@@ -951,13 +955,13 @@ def test_fused_moe_direct_inter_sizes(cuda_device, monkeypatch, weights, inter):
         if mx4:
             outs[direct] = A.fused_moe_a8w4(dev["x"], dev["w1"], dev["w2"], dev["tw"], dev["ids"],
                                             w1_scale=dev["s1"], w2_scale=dev["s2"],
-                                            block_size_M=16)
+                                            block_size_M=16, doweight_stage1=dw, activation=act)
         else:
-            outs[direct] = _run(dev, block_size_M=16)
+            outs[direct] = _run(dev, block_size_M=16, doweight_stage1=dw, activation=act)
     torch.cuda.synchronize()
-    _fullshape.stagewise_vs_oracle(cfg, dev, ref, _np(outs[1].float()), 16, A.ActivationType.Silu,
+    _fullshape.stagewise_vs_oracle(cfg, dev, ref, _np(outs[1].float()), 16, act, doweight=dw,
                                    e2e_rms=False)
-    assert _bf16_close(outs[1], outs[0]), (weights, inter)
+    assert _bf16_close(outs[1], outs[0]), (weights, inter, variant)
 
 
 @pytest.mark.parametrize("shape", ["small", "mimo", "mimo_a8w4"])
