@@ -473,17 +473,17 @@ static void timing_mark(int step, hipStream_t s) {
     if (step == kTimedSteps) ++t.calls;
 }
 
-// Activations already quantised by the caller (fp8 [tokens, model_dim] and
-// their 1x128 scales at a1_scale[row * sa_row + kb * sa_kb]) instead of
-// bf16 / fp16 hidden states.
 // Whether a layer runs on direct M-blocks (no sorting launch): one token
 // (each routed pair then fills its own 16-row M-block, as sorting would lay
-// it out), every expert local, both GEMMs on the decode kernel with one K
-// range per stage-1 tile. AITER_AMD_DIRECT=0 sorts anyway (tests compare the
-// two). Measured on MI355X at MiMo dims, T=1, alternating on one box: FP8
-// 50.2-50.3 -> 44.8-45.1 us, A8W4 36.9-37.1 -> 30.8-30.9 us. Two or more
-// tokens can route two pairs to one expert, whose weights two direct
-// M-blocks would then stream twice; they keep the sorting launch.
+// it out), every expert local, stage 1 on the decode kernel with one K range
+// per tile and stage 2 on the one-token kernel. AITER_AMD_DIRECT=0 sorts
+// anyway (tests compare the two). Measured on MI355X at MiMo dims, T=1,
+// alternating on one box: FP8 50.2-50.3 -> 44.8-45.1 us, A8W4 36.9-37.1 ->
+// 30.8-30.9 us with the streaming stage 2 (43.2-43.6 and 29.5-29.8 us with
+// the one-token stage 2). Two or more tokens can route two pairs to one
+// expert, whose weights two direct M-blocks would then stream twice; at
+// T=2..8 direct M-blocks measured level or slower, so they keep the sorting
+// launch.
 bool direct_layer(int64_t tokens, int64_t block_m, int64_t H, int64_t I,
                   const int32_t* expert_mask, const int32_t* num_local_tokens, const void* part,
                   bool one_launch, int ksplit) {
@@ -494,6 +494,9 @@ bool direct_layer(int64_t tokens, int64_t block_m, int64_t H, int64_t I,
            H % 256 == 0;
 }
 
+// Activations already quantised by the caller (fp8 [tokens, model_dim] and
+// their 1x128 scales at a1_scale[row * sa_row + kb * sa_kb]) instead of
+// bf16 / fp16 hidden states.
 struct PreQuant {
     const uint8_t* a1 = nullptr;
     const float* a1_scale = nullptr;
