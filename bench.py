@@ -7,7 +7,7 @@ scales, bf16 in/out.  A step is one aiter_amd.fused_moe call (sorting,
 activation quant, stage 1, stage 2, output conversion) on inputs resident
 in HBM.  The decode leg (T=32, uniform softmax routing) is reported under
 "decode"; the other single-GPU configurations -- A8W4 (fp8 activations x
-MXFP4 weights) at T=32/1024/8192 and the expert-parallel share (32 of 256
+MXFP4 weights) at T=32/1024/2048/8192 and the expert-parallel share (32 of 256
 experts, T=4096), the router, and two references for the roofline
 fractions (the library's plain dense FP8 GEMM at the stage-1 shape, torch's
 streaming read and copy) -- under "legs".  Prints
@@ -48,7 +48,8 @@ def parse():
                    help="prefill<T> | decode<T> | a8w4_<T> | ep<T> (e.g. prefill8192, "
                         "decode32, a8w4_1024, ep4096)")
     p.add_argument("--legs",
-                   default="decode1,decode8,decode128,prefill2048,a8w4_32,a8w4_1024,a8w4_8192,"
+                   default="decode1,decode8,decode128,prefill2048,a8w4_32,a8w4_1024,a8w4_2048,"
+                           "a8w4_8192,"
                            "ep4096,route_32,route_8192,one_launch_1,one_launch_4,one_launch_32,"
                            "dense_fp8_ceiling,hbm_ceiling",
                    help="comma-separated extra workloads reported under 'legs' ('none': "
